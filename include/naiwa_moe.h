@@ -1,0 +1,214 @@
+/*
+ * naiwa_moe.h -- C ABI of the MI355X (gfx950) MoE expert hot path.
+ *
+ * Every entry point is `extern "C"`, takes plain pointers and sizes, returns
+ * an int (0 = ok, > 0 a hipError_t, < 0 a NAIWA_E_* code) unless it keeps the
+ * reference's own `void` signature, and never throws.  Device pointers are
+ * caller-owned.  `stream` is a hipStream_t passed as int64_t (0 = the null
+ * stream), as in the reference's doorbell FFI.  Launches are asynchronous and
+ * stream-ordered.  One thread submits GPU work per device; the upload entry
+ * points may be called from one other thread.
+ *
+ * Reference interfaces each group replaces (naiwa-rs paths):
+ *   doorbell_*            src/doorbell/mod.rs:31-69, src/doorbell/doorbell.cu:15-149
+ *   naiwa_moe_decode      mistralrs_quant::indexed_moe_fused_decode, called at
+ *                         src/moe/stages/gpu.rs:27-66
+ *   naiwa_router_topk     the model-side router softmax/top-k consumed at
+ *                         src/moe/decode.rs:33-39 (tie rule of
+ *                         src/moe/cached_layer.rs:357-363)
+ *   naiwa_moe_gather      the per-bank grouping of src/moe/stages/gpu.rs:100-133
+ *   naiwa_upload_expert   CopyStream::queue_async, src/copy_stream.rs:387-409
+ *   naiwa_policy_*        the slot policy of src/moe/cached_layer.rs and
+ *                         src/moe/stages/{route,dma_miss}.rs, src/moe/staging.rs
+ */
+#ifndef NAIWA_MOE_H
+#define NAIWA_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes -------------------------------------------------------- */
+#define NAIWA_OK             0
+#define NAIWA_E_INVALID     -1  /* bad argument, shape or alignment          */
+#define NAIWA_E_UNSUPPORTED -2  /* dtype / activation / mode not served      */
+#define NAIWA_E_TIMEOUT     -3  /* a bounded wait expired                    */
+#define NAIWA_E_NOMEM       -4  /* allocation failed                         */
+#define NAIWA_E_BAD_ID      -5  /* expert or slot id out of range            */
+#define NAIWA_E_NOT_FOUND   -6  /* no such expert / slot / entry             */
+#define NAIWA_E_DEVICE      -7  /* the device reported a failed condition    */
+
+/* ---- GGML type ids --------------------------------------------------------- */
+#define NAIWA_F32  0
+#define NAIWA_F16  1
+#define NAIWA_Q8_0 8
+#define NAIWA_Q4_K 12
+#define NAIWA_BF16 30
+
+/* ---- activations (src/moe/stages/gpu.rs:15-21) ------------------------------- */
+#define NAIWA_ACT_SILU           0
+#define NAIWA_ACT_GELU_PYTORCH_TANH 1
+
+/* ---- router weight modes (public model configs) ------------------------------ */
+#define NAIWA_ROUTE_SOFTMAX_TOPK_RENORM 0 /* Qwen3: softmax, top-k, renormalize  */
+#define NAIWA_ROUTE_TOPK_SOFTMAX        1 /* Mixtral: softmax over the top-k     */
+#define NAIWA_ROUTE_SOFTMAX_TOPK        2 /* DeepSeek-V2-Lite: no renormalize    */
+
+const char* naiwa_status_string(int rc);
+
+/* ======================================================================== */
+/* Runtime plumbing (device memory, streams, events) so a host binding      */
+/* needs nothing but this library.                                          */
+/* ======================================================================== */
+int naiwa_device_count(int* n);
+int naiwa_set_device(int dev);
+int naiwa_device_info(int dev, int* cu_count, int* wall_clock_khz, int64_t* hbm_bytes, char* name, int name_len);
+int naiwa_malloc(void** p, size_t bytes);          /* 256-B aligned device memory */
+int naiwa_free(void* p);
+int naiwa_host_alloc(void** p, size_t bytes);      /* pinned, portable host memory */
+int naiwa_host_free(void* p);
+int naiwa_memcpy_h2d(void* dst, const void* src, size_t bytes, int64_t stream);
+int naiwa_memcpy_d2h(void* dst, const void* src, size_t bytes, int64_t stream);
+int naiwa_memcpy_d2d(void* dst, const void* src, size_t bytes, int64_t stream);
+int naiwa_memset(void* p, int value, size_t bytes, int64_t stream);
+int naiwa_stream_create(int64_t* stream);
+int naiwa_stream_destroy(int64_t stream);
+int naiwa_stream_sync(int64_t stream);
+int naiwa_stream_wait_event(int64_t stream, int64_t event);
+int naiwa_event_create(int64_t* event, int timing);
+int naiwa_event_destroy(int64_t event);
+int naiwa_event_record(int64_t event, int64_t stream);
+int naiwa_event_sync(int64_t event);
+int naiwa_event_query(int64_t event);              /* 0 done, 1 pending, else error */
+int naiwa_event_elapsed_ms(float* ms, int64_t start, int64_t end);
+int naiwa_device_sync(void);
+int naiwa_last_error(void);                        /* hipGetLastError as int */
+
+/* ======================================================================== */
+/* Doorbells -- same names and signatures as the reference FFI             */
+/* (src/doorbell/mod.rs:31-69).  Mapped memory is fine-grained and host-    */
+/* coherent (hipHostMallocMapped | hipHostMallocCoherent), zeroed here.     */
+/* ======================================================================== */
+/* cudaHostAlloc(Mapped) counterpart, src/doorbell/doorbell.cu:35-38. */
+int  doorbell_alloc_mapped(void** out, size_t bytes);
+/* src/doorbell/doorbell.cu:40-42. */
+int  doorbell_free_host(void* p);
+/* src/doorbell/doorbell.cu:44-46.  *dev = NULL on failure. */
+void doorbell_get_device_ptr(void* host, void** dev);
+/* Publish n u32 ids + n f32 weights, system fence, then *d_seq += 1
+ * (src/doorbell/doorbell.cu:15-33, :48-61). */
+void doorbell_ring(void* d_seq, void* d_ids, void* d_weights, const void* src_ids,
+                   const void* src_weights, int n, int64_t stream);
+/* Copy n f32 to a mapped slot, fence, *d_seq += 1 (doorbell.cu:70-96). */
+void doorbell_copy_f32(void* d_seq, void* d_dst, const void* src, int n, int64_t stream);
+/* Wait until *d_seq >= target, copy n f32 from d_payload + slot_off to dst,
+ * fence, *d_consumed = target (doorbell.cu:105-149).  Unlike the reference the
+ * wait is bounded (naiwa_doorbell_set_wait_limit_us): an expired wait copies
+ * nothing, leaves d_consumed alone and counts a timeout. */
+void doorbell_wait_copy_f32(void* d_seq, uint32_t target, void* d_payload, int64_t slot_off,
+                            void* d_consumed, void* dst, int n, int64_t stream);
+/* Bound of every device-side doorbell wait (default 10 s; 0 restores it). */
+int  naiwa_doorbell_set_wait_limit_us(uint64_t us);
+/* Device waits that expired since the library was loaded. */
+int  naiwa_doorbell_timeouts(uint32_t* count);
+/* Host-side helpers of the doorbell protocol (src/doorbell/mapped.rs:99-141):
+ * release-store a u32, acquire-load a u32, and wait (spin then sleep-poll)
+ * for *word >= target with an optional timeout (timeout_us < 0: never).
+ * naiwa_host_wait_ge returns 0 when reached, NAIWA_E_TIMEOUT otherwise. */
+void naiwa_host_store_release_u32(void* word, uint32_t value);
+uint32_t naiwa_host_load_acquire_u32(const void* word);
+int  naiwa_host_wait_ge(const void* word, uint32_t target, int64_t timeout_us, int64_t poll_us);
+
+/* ======================================================================== */
+/* Expert banks: the slot-indexed GPU expert cache                           */
+/* (src/moe/slot.rs:46-66).  One bank per projection: slot s of the bank    */
+/* starts at base + s * slot_stride and holds one expert's [n, k] GGML       */
+/* blocks verbatim.  base and slot_stride are 256-B aligned.                  */
+/* ======================================================================== */
+typedef struct naiwa_bank {
+    const void* base;
+    int64_t slot_stride;   /* bytes between slots (>= n * row_bytes(k))      */
+    int32_t slots;         /* slots in the bank                                */
+    int32_t n;             /* output rows                                      */
+    int32_t k;             /* input features                                   */
+    int32_t dtype;         /* NAIWA_Q4_K or NAIWA_Q8_0                         */
+} naiwa_bank;
+
+/* Bytes of one [n, k] projection in `dtype` (src/moe/slot.rs:84-95); -1 when
+ * k is not a multiple of the block size. */
+int64_t naiwa_projection_bytes(int dtype, int64_t n, int64_t k);
+
+/* The replacement of indexed_moe_fused_decode (src/moe/stages/gpu.rs:27-66):
+ *   out[t] = sum_j w[t,j] * down_s( act(gate_s x_t) * up_s x_t ),  s = slot_ids[t,j]
+ * x [rows, H] bf16 or f32 (x_dtype), slot_ids/w [rows, width] device arrays,
+ * out [rows, H] f32.  Weight-0 entries (the reference's padding) are skipped.
+ * The combine is atomics-free: per output row, slots are added in ascending
+ * slot order, the same on every run. */
+int naiwa_moe_decode(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down,
+                     const void* x, int x_dtype, const uint32_t* slot_ids, const float* w,
+                     int rows, int width, int act, float* out, int64_t stream);
+
+/* Router: logits = W . x with the chunked fixed-point accumulation (chunks of 8
+ * features summed as an f32 fma chain, each rounded to int64 with 32
+ * fractional bits, chunk partials added exactly), top-k by (logit desc, id
+ * asc), weights per mode.  x [rows, H] bf16/f32, W [E, H] f32; ids_out/w_out
+ * [rows, k]; logits_out [rows, E] f32 or NULL.  H % 8 == 0, E <= 1024, k <= 32. */
+int naiwa_router_topk(const void* x, int x_dtype, const float* W, int rows, int H, int E, int k,
+                      int mode, uint32_t* ids_out, float* w_out, float* logits_out, int64_t stream);
+
+/* Gather: stable counting sort of the n flattened ids by value.
+ * perm_out[n] = flat (t*k + j) indices grouped by id, offsets_out[E+1] =
+ * segment starts.  n <= 65536, E <= 4096.  Ids >= E are counted in
+ * *bad_out (device int, may be NULL) and left out of every segment. */
+int naiwa_moe_gather(const uint32_t* ids, int n, int E, uint32_t* perm_out, uint32_t* offsets_out,
+                     int* bad_out, int64_t stream);
+
+/* ======================================================================== */
+/* A decode stack: per layer, x <- bf16(x + MoE_l(x)) with the router,      */
+/* top-k, expert decode and combine all on the device.  The reference runs  */
+/* one CachedExperts::forward per MoE layer (src/moe/cached_layer.rs:524)   */
+/* after the model's router; this entry chains those calls for a whole      */
+/* decode step so no routing decision leaves the GPU.                       */
+/* ======================================================================== */
+typedef struct naiwa_layer {
+    const float* router;            /* [E, H] f32                                */
+    naiwa_bank gate, up, down;      /* slot banks of this layer                  */
+    const int32_t* slot_of_expert;  /* [E] device table (-1: not resident), or
+                                       NULL when slot == expert id               */
+} naiwa_layer;
+
+#define NAIWA_STACK_LAYERED 0  /* router, decode and residual as separate launches */
+#define NAIWA_STACK_FUSED   1  /* one persistent kernel for the whole stack        */
+
+/* x: [rows, H] bf16 device buffer, updated in place.  ids_out / w_out:
+ * [n_layers, rows, k] device buffers receiving the routing, or NULL. */
+int naiwa_stack_decode(const naiwa_layer* layers, int n_layers, void* x, int rows, int H, int E,
+                       int k, int mode, int act, uint32_t* ids_out, float* w_out, int flags,
+                       int64_t stream);
+
+/* Blocks per CU of the fused kernel (1..8, capped by occupancy; default 2). */
+int naiwa_stack_set_blocks_per_cu(int n);
+/* Counters of the last fused launch: grid-barrier waits that gave up after
+ * their 2 s bound, and routed experts with no resident slot (weight dropped).
+ * Synchronizes the device. */
+int naiwa_stack_status(int* barrier_timeouts, int* missing_experts);
+
+/* x[i] <- bf16(f32(x[i]) + y[i]) for i < n (the residual of the stack). */
+int naiwa_residual_add_bf16(void* x, const float* y, int64_t n, int64_t stream);
+
+/* ======================================================================== */
+/* Synthetic data (benchmarks and tests): n values of the N(mean, std)       */
+/* stream (seed, offset) -- value i depends only on (seed, offset + i) --    */
+/* written as f32, bf16, Q8_0 or Q4_K bytes with the library's quantizers.   */
+/* No counterpart in the reference, whose weights come from GGUF files.      */
+/* ======================================================================== */
+int naiwa_synth(int dtype, uint64_t seed, uint64_t offset, int64_t n, float mean, float stdv,
+                void* out, int64_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

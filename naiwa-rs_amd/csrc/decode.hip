@@ -1,0 +1,269 @@
+// naiwa_moe_decode: the dequant-fused SwiGLU expert decode over a slot-indexed
+// bank, replacing mistralrs_quant::indexed_moe_fused_decode as called at
+// src/moe/stages/gpu.rs:27-66.
+//
+// Three launches, all stream-ordered:
+//   1. segments: stable counting sort of the (token, slot) pairs by slot,
+//      weight-0 pairs (the reference's padding, gpu.rs:117-129) left out;
+//   2. gate+up: one block per (slot segment, 16-row tile of the intermediate);
+//      each 16-lane group owns one row of gate and the same row of up, streams
+//      their codes once with 16-byte loads and dots them against every token
+//      of the segment staged in LDS; h = act(g) * u in f32;
+//   3. down+combine: one block per 16-row tile of the output; walks the
+//      segments in ascending slot order, stages the segment's h vectors,
+//      streams each down row once per 4 tokens and accumulates w * (down . h)
+//      per (token, row) in LDS.  No atomics, so every run adds the same terms
+//      in the same order.
+#include "rowdot.h"
+#include "segments.h"
+#include "workspace.h"
+
+namespace {
+
+constexpr int kRowsPerBlock = 16;                    // 16 groups of 16 lanes
+constexpr int kThreads = kRowsPerBlock * NAIWA_GROUP; // 256
+constexpr int kTokMax = 4;                            // tokens staged per pass
+
+struct BankArg {
+    const uint8_t* base;
+    int64_t stride;
+    int64_t row_bytes;
+};
+
+__global__ void __launch_bounds__(NAIWA_SEG_THREADS)
+segments_kernel(const uint32_t* slot_ids, const float* w, int n, int nslots, uint32_t* perm,
+                int* seg_count, uint32_t* seg_key, uint32_t* seg_begin, int* bad) {
+    __shared__ NaiwaSegSmem sm;
+    naiwa_segment(sm, slot_ids, w, n, nslots, perm, nullptr, seg_count, seg_key, seg_begin, bad);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads)
+gate_up_kernel(BankArg gate, BankArg up, const void* x, int x_bf16, int H, int I, int width,
+               int tok_max, const int* seg_count, const uint32_t* seg_key,
+               const uint32_t* seg_begin, const uint32_t* perm, int act, float* hbuf) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int s = blockIdx.x;
+    if (s >= *seg_count) return;
+    const int tid = threadIdx.x, grp = tid / NAIWA_GROUP, lr = tid % NAIWA_GROUP;
+    const int r = blockIdx.y * kRowsPerBlock + grp;
+    const uint32_t slot = seg_key[s];
+    const int b = (int)seg_begin[s], e = (int)seg_begin[s + 1];
+    const int stage = naiwa_stage_bytes(DT, H);
+    const uint8_t* grow = gate.base + (int64_t)slot * gate.stride + (int64_t)r * gate.row_bytes;
+    const uint8_t* urow = up.base + (int64_t)slot * up.stride + (int64_t)r * up.row_bytes;
+    const int nu = Fmt<DT>::units(H);
+    constexpr int UM = Umax<DT>::v;
+
+    for (int c0 = b; c0 < e; c0 += tok_max) {
+        const int nt = min(tok_max, e - c0);
+        __syncthreads();
+        for (int tt = 0; tt < nt; ++tt) {
+            const int t = (int)perm[c0 + tt] / width;
+            const void* src = x_bf16 ? (const void*)((const uint16_t*)x + (int64_t)t * H)
+                                     : (const void*)((const float*)x + (int64_t)t * H);
+            uint32_t* words = (uint32_t*)(smem + tt * stage);
+            naiwa_stage<DT>(src, x_bf16 != 0, H, words, (float*)(words + H / 2), tid, kThreads);
+        }
+        __syncthreads();
+        if (r >= I) continue;
+        float ag[kTokMax], au[kTokMax];
+#pragma unroll
+        for (int tt = 0; tt < kTokMax; ++tt) ag[tt] = au[tt] = 0.0f;
+        for (int base = lr; base < nu; base += NAIWA_GROUP * UM) {
+            typename Fmt<DT>::Frag fg[UM], fu[UM];
+#pragma unroll
+            for (int i = 0; i < UM; ++i) {
+                const int u = base + NAIWA_GROUP * i;
+                if (u < nu) {
+                    fg[i] = Fmt<DT>::load(grow, u);
+                    fu[i] = Fmt<DT>::load(urow, u);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < UM; ++i) {
+                const int u = base + NAIWA_GROUP * i;
+                if (u >= nu) continue;
+#pragma unroll
+                for (int tt = 0; tt < kTokMax; ++tt) {
+                    if (tt >= nt) break;
+                    const uint32_t* words = (const uint32_t*)(smem + tt * stage);
+                    const float* sums = (const float*)(words + H / 2);
+                    ag[tt] += Fmt<DT>::dot(fg[i], u, words, sums);
+                    au[tt] += Fmt<DT>::dot(fu[i], u, words, sums);
+                }
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < kTokMax; ++tt) {
+            const float g = naiwa_group_sum<NAIWA_GROUP>(ag[tt]);
+            const float u = naiwa_group_sum<NAIWA_GROUP>(au[tt]);
+            if (tt < nt && lr == 0) hbuf[(int64_t)perm[c0 + tt] * I + r] = naiwa_act(act, g) * u;
+        }
+    }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads)
+down_kernel(BankArg down, int H, int I, int rows, int width, int tok_max, const int* seg_count,
+            const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm,
+            const float* w, const float* hbuf, float* out) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, grp = tid / NAIWA_GROUP, lr = tid % NAIWA_GROUP;
+    const int r = blockIdx.x * kRowsPerBlock + grp;
+    float* acc = (float*)smem; // [rows][kRowsPerBlock]
+    const int acc_bytes = ((rows * kRowsPerBlock * 4) + 15) & ~15;
+    uint8_t* stage_base = smem + acc_bytes;
+    const int stage = naiwa_stage_bytes(DT, I);
+    for (int i = tid; i < rows * kRowsPerBlock; i += kThreads) acc[i] = 0.0f;
+    const int nseg = *seg_count;
+    const int nu = Fmt<DT>::units(I);
+    constexpr int UM = Umax<DT>::v;
+    for (int s = 0; s < nseg; ++s) {
+        const uint32_t slot = seg_key[s];
+        const int b = (int)seg_begin[s], e = (int)seg_begin[s + 1];
+        const uint8_t* drow = down.base + (int64_t)slot * down.stride + (int64_t)r * down.row_bytes;
+        for (int c0 = b; c0 < e; c0 += tok_max) {
+            const int nt = min(tok_max, e - c0);
+            __syncthreads();
+            for (int tt = 0; tt < nt; ++tt) {
+                const float* src = hbuf + (int64_t)perm[c0 + tt] * I;
+                uint32_t* words = (uint32_t*)(stage_base + tt * stage);
+                naiwa_stage<DT>(src, false, I, words, (float*)(words + I / 2), tid, kThreads);
+            }
+            __syncthreads();
+            if (r >= H) continue;
+            float a[kTokMax];
+#pragma unroll
+            for (int tt = 0; tt < kTokMax; ++tt) a[tt] = 0.0f;
+            for (int base = lr; base < nu; base += NAIWA_GROUP * UM) {
+                typename Fmt<DT>::Frag f[UM];
+#pragma unroll
+                for (int i = 0; i < UM; ++i) {
+                    const int u = base + NAIWA_GROUP * i;
+                    if (u < nu) f[i] = Fmt<DT>::load(drow, u);
+                }
+#pragma unroll
+                for (int i = 0; i < UM; ++i) {
+                    const int u = base + NAIWA_GROUP * i;
+                    if (u >= nu) continue;
+#pragma unroll
+                    for (int tt = 0; tt < kTokMax; ++tt) {
+                        if (tt >= nt) break;
+                        const uint32_t* words = (const uint32_t*)(stage_base + tt * stage);
+                        a[tt] += Fmt<DT>::dot(f[i], u, words, (const float*)(words + I / 2));
+                    }
+                }
+            }
+#pragma unroll
+            for (int tt = 0; tt < kTokMax; ++tt) {
+                const float v = naiwa_group_sum<NAIWA_GROUP>(a[tt]);
+                if (tt < nt && lr == 0) {
+                    const uint32_t p = perm[c0 + tt];
+                    acc[(p / width) * kRowsPerBlock + grp] += w[p] * v;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    if (r < H && lr == 0)
+        for (int t = 0; t < rows; ++t) out[(int64_t)t * H + r] = acc[t * kRowsPerBlock + grp];
+}
+
+bool bank_ok(const naiwa_bank* b) {
+    if (!b || !b->base || b->slots <= 0 || b->n <= 0 || b->k <= 0) return false;
+    if (b->dtype != NAIWA_Q4_K && b->dtype != NAIWA_Q8_0) return false;
+    const int64_t rb = naiwa_row_bytes(b->dtype, b->k);
+    if (rb < 0 || b->slot_stride < rb * b->n) return false;
+    if (((uintptr_t)b->base & 15) != 0 || (b->slot_stride & 15) != 0) return false;
+    return true;
+}
+
+int tok_cap(int dtype, int k) {
+    const int per = naiwa_stage_bytes(dtype, k);
+    int cap = (48 * 1024) / per;
+    return cap < 1 ? 0 : (cap > kTokMax ? kTokMax : cap);
+}
+
+} // namespace
+
+extern "C" int naiwa_moe_decode(const naiwa_bank* gate, const naiwa_bank* up,
+                                const naiwa_bank* down, const void* x, int x_dtype,
+                                const uint32_t* slot_ids, const float* w, int rows, int width,
+                                int act, float* out, int64_t stream) {
+    if (!bank_ok(gate) || !bank_ok(up) || !bank_ok(down)) return NAIWA_E_INVALID;
+    if (gate->dtype != up->dtype) return NAIWA_E_UNSUPPORTED;
+    const int H = gate->k, I = gate->n;
+    if (up->k != H || up->n != I || down->k != I || down->n != H) return NAIWA_E_INVALID;
+    if (gate->slots != up->slots || gate->slots != down->slots) return NAIWA_E_INVALID;
+    if (gate->slots > NAIWA_SEG_MAX_KEYS) return NAIWA_E_UNSUPPORTED;
+    if (x_dtype != NAIWA_BF16 && x_dtype != NAIWA_F32) return NAIWA_E_UNSUPPORTED;
+    if (act != NAIWA_ACT_SILU && act != NAIWA_ACT_GELU_PYTORCH_TANH) return NAIWA_E_UNSUPPORTED;
+    if (rows < 0 || width < 0 || (int64_t)rows * width > 65536) return NAIWA_E_INVALID;
+    if (H % 32 || I % 32) return NAIWA_E_INVALID;
+    if (rows > 4096) return NAIWA_E_INVALID;
+    hipStream_t st = (hipStream_t)stream;
+    if (rows == 0) return NAIWA_OK;
+    if (!x || !out || (width > 0 && (!slot_ids || !w))) return NAIWA_E_INVALID;
+    if (width == 0) return naiwa_hip_rc(hipMemsetAsync(out, 0, (size_t)rows * H * 4, st));
+    const int tok_g = tok_cap(gate->dtype, H), tok_d = tok_cap(down->dtype, I);
+    if (!tok_g || !tok_d) return NAIWA_E_UNSUPPORTED;
+    const int acc_bytes = ((rows * kRowsPerBlock * 4) + 15) & ~15;
+    const size_t lds_down = (size_t)acc_bytes + (size_t)tok_d * naiwa_stage_bytes(down->dtype, I);
+    if (lds_down > 64 * 1024) return NAIWA_E_UNSUPPORTED;
+
+    // scratch: seg_count, bad | seg_key[n] | seg_begin[n+1] | perm[n] | h[n*I]
+    const int n = rows * width;
+    const size_t off_key = 256, off_begin = off_key + (((size_t)n * 4 + 255) & ~size_t(255));
+    const size_t off_perm = off_begin + (((size_t)(n + 1) * 4 + 255) & ~size_t(255));
+    const size_t off_h = off_perm + (((size_t)n * 4 + 255) & ~size_t(255));
+    const size_t total = off_h + (size_t)n * I * 4;
+    int rc = 0;
+    uint8_t* ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_DECODE, total, &rc);
+    if (!ws) return rc;
+    int* seg_count = (int*)ws;
+    int* bad = (int*)(ws + 4);
+    uint32_t* seg_key = (uint32_t*)(ws + off_key);
+    uint32_t* seg_begin = (uint32_t*)(ws + off_begin);
+    uint32_t* perm = (uint32_t*)(ws + off_perm);
+    float* hbuf = (float*)(ws + off_h);
+
+    segments_kernel<<<1, NAIWA_SEG_THREADS, 0, st>>>(slot_ids, w, n, gate->slots, perm, seg_count,
+                                                     seg_key, seg_begin, bad);
+    BankArg g{(const uint8_t*)gate->base, gate->slot_stride, naiwa_row_bytes(gate->dtype, H)};
+    BankArg u{(const uint8_t*)up->base, up->slot_stride, naiwa_row_bytes(up->dtype, H)};
+    BankArg d{(const uint8_t*)down->base, down->slot_stride, naiwa_row_bytes(down->dtype, I)};
+    const dim3 ggrid(n, (I + kRowsPerBlock - 1) / kRowsPerBlock);
+    const size_t lds_g = (size_t)tok_g * naiwa_stage_bytes(gate->dtype, H);
+    const int xb = x_dtype == NAIWA_BF16;
+    switch (naiwa_kernel_fmt(gate->dtype, H)) {
+    case NAIWA_Q4_K:
+        gate_up_kernel<NAIWA_Q4_K><<<ggrid, kThreads, lds_g, st>>>(
+            g, u, x, xb, H, I, width, tok_g, seg_count, seg_key, seg_begin, perm, act, hbuf);
+        break;
+    case NAIWA_Q8_0:
+        gate_up_kernel<NAIWA_Q8_0><<<ggrid, kThreads, lds_g, st>>>(
+            g, u, x, xb, H, I, width, tok_g, seg_count, seg_key, seg_begin, perm, act, hbuf);
+        break;
+    default:
+        gate_up_kernel<NAIWA_Q8_0_ODD><<<ggrid, kThreads, lds_g, st>>>(
+            g, u, x, xb, H, I, width, tok_g, seg_count, seg_key, seg_begin, perm, act, hbuf);
+        break;
+    }
+    const dim3 dgrid((H + kRowsPerBlock - 1) / kRowsPerBlock);
+    switch (naiwa_kernel_fmt(down->dtype, I)) {
+    case NAIWA_Q4_K:
+        down_kernel<NAIWA_Q4_K><<<dgrid, kThreads, lds_down, st>>>(
+            d, H, I, rows, width, tok_d, seg_count, seg_key, seg_begin, perm, w, hbuf, out);
+        break;
+    case NAIWA_Q8_0:
+        down_kernel<NAIWA_Q8_0><<<dgrid, kThreads, lds_down, st>>>(
+            d, H, I, rows, width, tok_d, seg_count, seg_key, seg_begin, perm, w, hbuf, out);
+        break;
+    default:
+        down_kernel<NAIWA_Q8_0_ODD><<<dgrid, kThreads, lds_down, st>>>(
+            d, H, I, rows, width, tok_d, seg_count, seg_key, seg_begin, perm, w, hbuf, out);
+        break;
+    }
+    return naiwa_hip_rc(hipGetLastError());
+}

@@ -1,0 +1,120 @@
+// Router device functions shared by naiwa_router_topk and the fused stack
+// kernel: the chunked fixed-point logit rule and the one-wave top-k.
+#pragma once
+
+#include "common.h"
+#include "workspace.h"
+
+#define NAIWA_ROUTER_CHUNK 8
+#define NAIWA_ROUTER_MAX_E 1024
+#define NAIWA_ROUTER_MAX_K 32
+
+// 8 activations starting at element `off` (bf16 or f32 source).
+__device__ __forceinline__ void naiwa_load_x8(const void* x, int x_bf16, int64_t off, float* xv) {
+    if (x_bf16) {
+        const uint4 r = *reinterpret_cast<const uint4*>((const uint16_t*)x + off);
+        const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xv[2 * i] = naiwa_bf16_to_f32(w[i] & 0xffffu);
+            xv[2 * i + 1] = naiwa_bf16_to_f32(w[i] >> 16);
+        }
+    } else {
+        const float4 a = *reinterpret_cast<const float4*>((const float*)x + off);
+        const float4 b = *reinterpret_cast<const float4*>((const float*)x + off + 4);
+        xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
+        xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+    }
+}
+
+// One chunk: f32 fma chain over 8 features, rounded half-to-even to int64
+// with 32 fractional bits (scaling by 2^32 is exact).
+__device__ __forceinline__ long long naiwa_router_chunk(const float* w8, const float* xv) {
+    const float4 a = *reinterpret_cast<const float4*>(w8);
+    const float4 b = *reinterpret_cast<const float4*>(w8 + 4);
+    const float wv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float p = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p = __builtin_fmaf(wv[i], xv[i], p);
+    return (long long)__builtin_rintf(p * 4294967296.0f);
+}
+
+__device__ __forceinline__ float naiwa_router_fix_to_f32(long long s) {
+    return (float)s * 0x1p-32f;
+}
+
+__device__ __forceinline__ long long naiwa_wave_sum_i64(long long v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+// (value desc, id asc): is (va, ia) ranked before (vb, ib)?
+__device__ __forceinline__ bool naiwa_rank_before(float va, int ia, float vb, int ib) {
+    return va > vb || (va == vb && ia < ib);
+}
+
+// One wave (64 lanes) selects the top k of E <= 1024 logits and writes ids
+// (rank order) and weights (mode).  Every lane must call it.
+__device__ inline void naiwa_wave_topk(const float* l, int E, int k, int mode, uint32_t* ids,
+                                       float* w) {
+    const int lane = threadIdx.x & 63;
+    constexpr int PER = NAIWA_ROUTER_MAX_E / 64;
+    float v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int e = lane + 64 * i;
+        v[i] = e < E ? l[e] : -__builtin_inff();
+    }
+    uint32_t taken = 0; // bit i: element lane + 64 i already selected
+    float my_v = 0.0f;  // lane j < k keeps the rank-j selection
+    int my_i = 0;
+    float mx = 0.0f;
+    for (int j = 0; j < k; ++j) {
+        float bv = -__builtin_inff();
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int e = lane + 64 * i;
+            if (e < E && !((taken >> i) & 1u) && naiwa_rank_before(v[i], e, bv, bi)) {
+                bv = v[i];
+                bi = e;
+            }
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            const float ov = __shfl_xor(bv, m, 64);
+            const int oi = __shfl_xor(bi, m, 64);
+            if (naiwa_rank_before(ov, oi, bv, bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (lane == j) {
+            my_v = bv;
+            my_i = bi;
+        }
+        if (j == 0) mx = bv;
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+    }
+    // weights: exp(l - max) over the k, normalized by the k or by all E.  The
+    // k-term sum runs in rank order in every lane (the oracle's order).
+    float denom = 0.0f;
+    if (mode == NAIWA_ROUTE_SOFTMAX_TOPK) {
+        float part = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int e = lane + 64 * i;
+            if (e < E) part += expf(v[i] - mx);
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) part += __shfl_xor(part, m, 64);
+        denom = part;
+    } else {
+        for (int j = 0; j < k; ++j) denom += expf(__shfl(my_v, j, 64) - mx);
+    }
+    if (lane < k) {
+        ids[lane] = (uint32_t)my_i;
+        w[lane] = expf(my_v - mx) / denom;
+    }
+}

@@ -1,0 +1,74 @@
+// naiwa_router_topk: router logits, top-k and routing weights on the device,
+// so the decode path never round-trips the routing through the host (the
+// reference's host read costs 0.72-0.93 ms per layer,
+// docs/worklogs/m28-routing-round-trip.md:225-235).
+//
+// Logits use the chunked fixed-point rule: each chunk of 8 features is an
+// f32 fma chain, rounded to int64 with 32 fractional bits; chunk partials are
+// added as integers.  Integer addition is associative, so any split of the
+// chunks over threads (or over the blocks of the fused stack kernel) yields
+// the same bits as the CPU oracle.  Top-k orders by (logit desc, id asc), the
+// tie rule of top_k_ids (src/moe/cached_layer.rs:357-363).
+#include "common.h"
+#include "router.h"
+
+namespace {
+
+constexpr int kLogitThreads = 256;
+
+__global__ void __launch_bounds__(kLogitThreads)
+router_logits_kernel(const void* x, int x_bf16, const float* W, int rows, int H, int E,
+                     float* logits) {
+    __shared__ long long part[kLogitThreads / 64];
+    const int e = blockIdx.x, tid = threadIdx.x;
+    const int nchunks = H / NAIWA_ROUTER_CHUNK;
+    const float* wr = W + (int64_t)e * H;
+    for (int t = 0; t < rows; ++t) {
+        long long acc = 0;
+        for (int c = tid; c < nchunks; c += kLogitThreads) {
+            float xv[8];
+            naiwa_load_x8(x, x_bf16, (int64_t)t * H + 8 * c, xv);
+            acc += naiwa_router_chunk(wr + 8 * c, xv);
+        }
+        acc = naiwa_wave_sum_i64(acc);
+        if ((tid & 63) == 0) part[tid >> 6] = acc;
+        __syncthreads();
+        if (tid == 0) {
+            long long s = 0;
+            for (int i = 0; i < kLogitThreads / 64; ++i) s += part[i];
+            logits[(int64_t)t * E + e] = naiwa_router_fix_to_f32(s);
+        }
+        __syncthreads();
+    }
+}
+
+__global__ void __launch_bounds__(64)
+router_topk_kernel(const float* logits, int E, int k, int mode, uint32_t* ids, float* w) {
+    const int t = blockIdx.x;
+    naiwa_wave_topk(logits + (int64_t)t * E, E, k, mode, ids + (int64_t)t * k, w + (int64_t)t * k);
+}
+
+} // namespace
+
+extern "C" int naiwa_router_topk(const void* x, int x_dtype, const float* W, int rows, int H,
+                                 int E, int k, int mode, uint32_t* ids_out, float* w_out,
+                                 float* logits_out, int64_t stream) {
+    if (x_dtype != NAIWA_BF16 && x_dtype != NAIWA_F32) return NAIWA_E_UNSUPPORTED;
+    if (mode < NAIWA_ROUTE_SOFTMAX_TOPK_RENORM || mode > NAIWA_ROUTE_SOFTMAX_TOPK)
+        return NAIWA_E_UNSUPPORTED;
+    if (rows < 0 || H <= 0 || H % NAIWA_ROUTER_CHUNK || E <= 0 || E > NAIWA_ROUTER_MAX_E || k <= 0 ||
+        k > E || k > NAIWA_ROUTER_MAX_K)
+        return NAIWA_E_INVALID;
+    if (rows == 0) return NAIWA_OK;
+    if (!x || !W || !ids_out || !w_out) return NAIWA_E_INVALID;
+    hipStream_t st = (hipStream_t)stream;
+    float* logits = logits_out;
+    if (!logits) {
+        int rc = 0;
+        logits = (float*)naiwa_scratch(NAIWA_SCRATCH_ROUTER, (size_t)rows * E * 4, &rc);
+        if (!logits) return rc;
+    }
+    router_logits_kernel<<<E, kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, W, rows, H, E, logits);
+    router_topk_kernel<<<rows, 64, 0, st>>>(logits, E, k, mode, ids_out, w_out);
+    return naiwa_hip_rc(hipGetLastError());
+}

@@ -1,0 +1,192 @@
+// Row-dot building blocks shared by the decode kernels and the fused stack
+// kernel: per-format unit loads, activation staging into LDS, and the dot of
+// one quantized row against one staged activation vector by a group of 16
+// lanes.
+#pragma once
+
+#include "common.h"
+
+#define NAIWA_GROUP 16 // lanes cooperating on one weight row
+
+// A staged activation vector in LDS: perm words [K/2] followed by sums.
+// Q4_K: bf16 words, one sum per 16 values.  Q8_0: fp16 words, one per 32.
+template <int DT> struct Fmt;
+
+template <> struct Fmt<NAIWA_Q4_K> {
+    static constexpr int kSumSpan = 16;
+    struct Frag {
+        uint4 q, hd;
+    };
+    __device__ static int units(int k) { return (k / NAIWA_QK_K) * 8; }
+    __device__ static Frag load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (u >> 3) * NAIWA_Q4_K_BYTES;
+        Frag f;
+        f.hd = *reinterpret_cast<const uint4*>(blk);
+        f.q = *reinterpret_cast<const uint4*>(blk + 16 + 16 * (u & 7));
+        return f;
+    }
+    // words: perm words of the vector (K/2), sums: K/16 sums
+    __device__ static float dot(const Frag& f, int u, const uint32_t* words, const float* sums) {
+        const int j = u & 7, c = j >> 1;
+        const int elo = (u >> 3) * NAIWA_QK_K + 64 * c + 16 * (j & 1);
+        const uint4* xl = reinterpret_cast<const uint4*>(words + elo / 2);
+        const uint4* xh = reinterpret_cast<const uint4*>(words + elo / 2 + 16);
+        uint32_t lo[8], hi[8];
+        const uint4 l0 = xl[0], l1 = xl[1], h0 = xh[0], h1 = xh[1];
+        lo[0] = l0.x; lo[1] = l0.y; lo[2] = l0.z; lo[3] = l0.w;
+        lo[4] = l1.x; lo[5] = l1.y; lo[6] = l1.z; lo[7] = l1.w;
+        hi[0] = h0.x; hi[1] = h0.y; hi[2] = h0.z; hi[3] = h0.w;
+        hi[4] = h1.x; hi[5] = h1.y; hi[6] = h1.z; hi[7] = h1.w;
+        return naiwa_q4k_unit(f.q, f.hd, c, lo, hi, sums[elo / 16], sums[elo / 16 + 2]);
+    }
+    __device__ static uint32_t to16(float v) { return naiwa_f32_to_bf16(v); }
+    __device__ static float from16(uint32_t h) { return naiwa_bf16_to_f32(h); }
+};
+
+template <> struct Fmt<NAIWA_Q8_0> {
+    static constexpr int kSumSpan = 32;
+    struct Frag {
+        uint32_t d[17];
+    };
+    __device__ static int units(int k) { return k / (2 * NAIWA_QK8_0); }
+    __device__ static Frag load(const uint8_t* row, int u) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(row + 68 * u);
+        Frag f;
+#pragma unroll
+        for (int i = 0; i < 17; ++i) f.d[i] = p[i];
+        return f;
+    }
+    __device__ static float dot(const Frag& f, int u, const uint32_t* words, const float* sums) {
+        uint32_t xw[32];
+        const uint4* xv = reinterpret_cast<const uint4*>(words + 32 * u);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint4 v = xv[i];
+            xw[4 * i] = v.x; xw[4 * i + 1] = v.y; xw[4 * i + 2] = v.z; xw[4 * i + 3] = v.w;
+        }
+        return naiwa_q8_0_pair(f.d, xw, sums[2 * u], sums[2 * u + 1]);
+    }
+    __device__ static uint32_t to16(float v) { return naiwa_f32_to_f16(v); }
+    __device__ static float from16(uint32_t h) { return naiwa_f16_to_f32(h); }
+};
+
+// Q8_0 rows with an odd number of blocks are only 2-byte aligned: one block per
+// unit, its 34 bytes read as 17 halfwords.  Internal format tag.
+#define NAIWA_Q8_0_ODD 1008
+
+template <> struct Fmt<NAIWA_Q8_0_ODD> {
+    static constexpr int kSumSpan = 32;
+    struct Frag {
+        uint32_t d;
+        uint32_t q[8];
+    };
+    __device__ static int units(int k) { return k / NAIWA_QK8_0; }
+    __device__ static Frag load(const uint8_t* row, int u) {
+        const uint16_t* p = reinterpret_cast<const uint16_t*>(row + NAIWA_Q8_0_BYTES * u);
+        Frag f;
+        f.d = p[0];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) f.q[i] = (uint32_t)p[1 + 2 * i] | ((uint32_t)p[2 + 2 * i] << 16);
+        return f;
+    }
+    __device__ static float dot(const Frag& f, int u, const uint32_t* words, const float* sums) {
+        const uint4* xv = reinterpret_cast<const uint4*>(words + 16 * u);
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint4 v = xv[i];
+            const uint32_t xw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t w = f.q[2 * i + h] ^ 0x80808080u;
+                a = naiwa_dot2_f16((w & 0x00FF00FFu) | 0x64006400u, xw[2 * h], a);
+                a = naiwa_dot2_f16(((w >> 8) & 0x00FF00FFu) | 0x64006400u, xw[2 * h + 1], a);
+            }
+        }
+        return naiwa_f16_to_f32(f.d) * (a - 1152.0f * sums[u]);
+    }
+    __device__ static uint32_t to16(float v) { return naiwa_f32_to_f16(v); }
+    __device__ static float from16(uint32_t h) { return naiwa_f16_to_f32(h); }
+};
+
+// LDS bytes of one staged vector of length k, rounded up to 16 so that
+// consecutive vectors keep 16-byte aligned words.
+__host__ __device__ inline int naiwa_stage_bytes(int dtype, int k) {
+    const int span = dtype == NAIWA_Q4_K ? 16 : 32; // Q8_0 (either variant): 32
+    return (k * 2 + (k / span) * 4 + 15) & ~15;
+}
+
+// Stage `k` activations (f32 source, or bf16 when src_bf16) into the perm
+// layout + sums of format DT.  All `nthr` threads of the block take part;
+// k % 32 == 0.  The caller synchronizes afterwards.
+template <int DT>
+__device__ inline void naiwa_stage(const void* src, bool src_bf16, int k, uint32_t* words,
+                                   float* sums, int tid, int nthr) {
+    constexpr int span = Fmt<DT>::kSumSpan;
+    constexpr int gpg = span / 4; // 4-element groups per sum
+    // Thread handles groups g = tid, tid + nthr, ...; nthr is a multiple of gpg
+    // so the lanes summing one span sit in one aligned run of the wave.
+    for (int g0 = 0; g0 < k / 4; g0 += nthr) {
+        const int g = g0 + tid;
+        float part = 0.0f;
+        if (g < k / 4) {
+            float v[4];
+            if (src_bf16) {
+                const uint2 raw = reinterpret_cast<const uint2*>(src)[g];
+                v[0] = naiwa_bf16_to_f32(raw.x & 0xffffu);
+                v[1] = naiwa_bf16_to_f32(raw.x >> 16);
+                v[2] = naiwa_bf16_to_f32(raw.y & 0xffffu);
+                v[3] = naiwa_bf16_to_f32(raw.y >> 16);
+            } else {
+                const float4 raw = reinterpret_cast<const float4*>(src)[g];
+                v[0] = raw.x; v[1] = raw.y; v[2] = raw.z; v[3] = raw.w;
+            }
+            uint32_t h[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                h[i] = Fmt<DT>::to16(v[i]);
+                v[i] = Fmt<DT>::from16(h[i]);
+            }
+            words[2 * g] = h[0] | (h[2] << 16);
+            words[2 * g + 1] = h[1] | (h[3] << 16);
+            part = (v[0] + v[1]) + (v[2] + v[3]);
+        }
+        part = naiwa_group_sum<gpg>(part);
+        if (g < k / 4 && (g % gpg) == 0) sums[g / gpg] = part;
+    }
+}
+
+// Dot of one quantized row with one staged vector, by the 16 lanes of a
+// group (lr = lane in group).  Loads of up to UMAX units are issued before
+// any of them is used.  Returns the full sum in every lane of the group.
+template <int DT, int UMAX>
+__device__ inline float naiwa_row_dot(const uint8_t* row, int k, const uint32_t* words,
+                                      const float* sums, int lr) {
+    const int nu = Fmt<DT>::units(k);
+    float acc = 0.0f;
+    for (int base = lr; base < nu; base += NAIWA_GROUP * UMAX) {
+        typename Fmt<DT>::Frag f[UMAX];
+#pragma unroll
+        for (int i = 0; i < UMAX; ++i) {
+            const int u = base + NAIWA_GROUP * i;
+            if (u < nu) f[i] = Fmt<DT>::load(row, u);
+        }
+#pragma unroll
+        for (int i = 0; i < UMAX; ++i) {
+            const int u = base + NAIWA_GROUP * i;
+            if (u < nu) acc += Fmt<DT>::dot(f[i], u, words, sums);
+        }
+    }
+    return naiwa_group_sum<NAIWA_GROUP>(acc);
+}
+
+// Loads in flight per lane per pass, by format (about 32 VGPRs of codes).
+template <int DT> struct Umax { static constexpr int v = 4; };
+template <> struct Umax<NAIWA_Q8_0> { static constexpr int v = 2; };
+template <> struct Umax<NAIWA_Q8_0_ODD> { static constexpr int v = 4; };
+
+// Kernel format tag of a bank: Q8_0 rows with an odd block count use the
+// halfword-loading variant.
+__host__ __device__ inline int naiwa_kernel_fmt(int dtype, int k) {
+    return dtype == NAIWA_Q8_0 && (k / NAIWA_QK8_0) % 2 ? NAIWA_Q8_0_ODD : dtype;
+}

@@ -1,0 +1,116 @@
+"""Loading and declaring libnaiwa_moe.so (the gfx950 C ABI of include/naiwa_moe.h).
+
+The product path has no fallback: if the shared library is missing or fails to
+load, every entry point raises.  Build it with ``python naiwa-rs_amd/build.py``
+(or ``__graft_entry__.build()``).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_ROOT, "libnaiwa_moe.so")
+
+OK = 0
+E_INVALID, E_UNSUPPORTED, E_TIMEOUT, E_NOMEM, E_BAD_ID, E_NOT_FOUND, E_DEVICE = -1, -2, -3, -4, -5, -6, -7
+
+F32, F16, Q8_0, Q4_K, BF16 = 0, 1, 8, 12, 30
+ACT_SILU, ACT_GELU_PYTORCH_TANH = 0, 1
+ROUTE_SOFTMAX_TOPK_RENORM, ROUTE_TOPK_SOFTMAX, ROUTE_SOFTMAX_TOPK = 0, 1, 2
+
+
+class NaiwaError(RuntimeError):
+    def __init__(self, rc: int, what: str):
+        self.rc = rc
+        msg = lib().naiwa_status_string(rc).decode() if _lib is not None else str(rc)
+        super().__init__(f"{what}: {msg} ({rc})")
+
+
+class Bank(C.Structure):
+    """naiwa_bank: one projection's slot bank (include/naiwa_moe.h)."""
+    _fields_ = [("base", C.c_void_p), ("slot_stride", C.c_int64), ("slots", C.c_int32),
+                ("n", C.c_int32), ("k", C.c_int32), ("dtype", C.c_int32)]
+
+
+class Layer(C.Structure):
+    """naiwa_layer: router + the three banks + the expert->slot table of one layer."""
+    _fields_ = [("router", C.c_void_p), ("gate", Bank), ("up", Bank), ("down", Bank),
+                ("slot_of_expert", C.c_void_p)]
+
+
+STACK_LAYERED, STACK_FUSED = 0, 1
+
+
+_lib: C.CDLL | None = None
+
+vp, i32, i64, u32, u64, f32 = C.c_void_p, C.c_int, C.c_int64, C.c_uint32, C.c_uint64, C.c_float
+_P = C.POINTER
+
+# name -> (restype, argtypes).  Every symbol include/naiwa_moe.h declares is listed.
+SIGNATURES: dict[str, tuple] = {
+    "naiwa_status_string": (C.c_char_p, [i32]),
+    "naiwa_device_count": (i32, [_P(i32)]),
+    "naiwa_set_device": (i32, [i32]),
+    "naiwa_device_info": (i32, [i32, _P(i32), _P(i32), _P(i64), C.c_char_p, i32]),
+    "naiwa_malloc": (i32, [_P(vp), C.c_size_t]),
+    "naiwa_free": (i32, [vp]),
+    "naiwa_host_alloc": (i32, [_P(vp), C.c_size_t]),
+    "naiwa_host_free": (i32, [vp]),
+    "naiwa_memcpy_h2d": (i32, [vp, vp, C.c_size_t, i64]),
+    "naiwa_memcpy_d2h": (i32, [vp, vp, C.c_size_t, i64]),
+    "naiwa_memcpy_d2d": (i32, [vp, vp, C.c_size_t, i64]),
+    "naiwa_memset": (i32, [vp, i32, C.c_size_t, i64]),
+    "naiwa_stream_create": (i32, [_P(i64)]),
+    "naiwa_stream_destroy": (i32, [i64]),
+    "naiwa_stream_sync": (i32, [i64]),
+    "naiwa_stream_wait_event": (i32, [i64, i64]),
+    "naiwa_event_create": (i32, [_P(i64), i32]),
+    "naiwa_event_destroy": (i32, [i64]),
+    "naiwa_event_record": (i32, [i64, i64]),
+    "naiwa_event_sync": (i32, [i64]),
+    "naiwa_event_query": (i32, [i64]),
+    "naiwa_event_elapsed_ms": (i32, [_P(f32), i64, i64]),
+    "naiwa_device_sync": (i32, []),
+    "naiwa_last_error": (i32, []),
+    "doorbell_alloc_mapped": (i32, [_P(vp), C.c_size_t]),
+    "doorbell_free_host": (i32, [vp]),
+    "doorbell_get_device_ptr": (None, [vp, _P(vp)]),
+    "doorbell_ring": (None, [vp, vp, vp, vp, vp, i32, i64]),
+    "doorbell_copy_f32": (None, [vp, vp, vp, i32, i64]),
+    "doorbell_wait_copy_f32": (None, [vp, u32, vp, i64, vp, vp, i32, i64]),
+    "naiwa_doorbell_set_wait_limit_us": (i32, [u64]),
+    "naiwa_doorbell_timeouts": (i32, [_P(u32)]),
+    "naiwa_host_store_release_u32": (None, [vp, u32]),
+    "naiwa_host_load_acquire_u32": (u32, [vp]),
+    "naiwa_host_wait_ge": (i32, [vp, u32, i64, i64]),
+    "naiwa_projection_bytes": (i64, [i32, i64, i64]),
+    "naiwa_moe_decode": (i32, [_P(Bank), _P(Bank), _P(Bank), vp, i32, vp, vp, i32, i32, i32, vp, i64]),
+    "naiwa_router_topk": (i32, [vp, i32, vp, i32, i32, i32, i32, i32, vp, vp, vp, i64]),
+    "naiwa_moe_gather": (i32, [vp, i32, i32, vp, vp, vp, i64]),
+    "naiwa_synth": (i32, [i32, u64, u64, i64, f32, f32, vp, i64]),
+    "naiwa_stack_decode": (i32, [_P(Layer), i32, vp, i32, i32, i32, i32, i32, i32, vp, vp, i32, i64]),
+    "naiwa_stack_set_blocks_per_cu": (i32, [i32]),
+    "naiwa_stack_status": (i32, [_P(i32), _P(i32)]),
+    "naiwa_residual_add_bf16": (i32, [vp, vp, i64, i64]),
+}
+
+
+def lib() -> C.CDLL:
+    """The loaded library; raises if it was never built (there is no CPU fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with naiwa-rs_amd/build.py")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != OK:
+        raise NaiwaError(rc, what)

@@ -1,0 +1,145 @@
+"""The expert hot path's operators, as the reference's call sites see them.
+
+- ``SlotBank`` / ``LayerBanks``: the slot-indexed GPU expert cache of one layer
+  (one ``[slots, N, K]`` bank per projection, src/moe/slot.rs:46-66), filled
+  from stacked ``[E, N, K]`` GGUF bytes sliced per expert like
+  ``expert_range`` (src/moe/expert.rs:123-145).
+- ``indexed_moe_fused_decode``: the call of src/moe/stages/gpu.rs:53-64 with the
+  same argument meaning (banks, activations, row-major ``[rows, topk]`` local
+  slot ids and weights, activation id); the result is ``[rows, hidden]`` f32.
+- ``router_topk`` and ``moe_gather``: routing and grouping on the device.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from ._lib import (ACT_SILU, BF16, F32, Q4_K, Q8_0, ROUTE_SOFTMAX_TOPK_RENORM, STACK_FUSED,
+                   STACK_LAYERED, Bank, Layer, check, lib)
+from .device import DeviceBuffer
+
+BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144)}
+
+
+def row_bytes(dtype: int, k: int) -> int:
+    bs, ts = BLOCK[dtype]
+    if k % bs:
+        raise ValueError(f"K={k} is not divisible by block_size={bs} for dtype {dtype}")
+    return (k // bs) * ts
+
+
+def expert_range(dtype: int, n: int, k: int, e: int) -> range:
+    """Byte range of expert e in a stacked [E, N, K] tensor (src/moe/expert.rs:123-145)."""
+    stride = n * row_bytes(dtype, k)
+    return range(e * stride, (e + 1) * stride)
+
+
+def slot_stride(dtype: int, n: int, k: int) -> int:
+    """Bytes between slots: the projection's bytes rounded up to 256."""
+    return (n * row_bytes(dtype, k) + 255) // 256 * 256
+
+
+class SlotBank:
+    """One projection's slot bank on the device."""
+
+    def __init__(self, slots: int, n: int, k: int, dtype: int, buffer: DeviceBuffer | None = None,
+                 offset: int = 0):
+        self.slots, self.n, self.k, self.dtype = slots, n, k, dtype
+        self.stride = slot_stride(dtype, n, k)
+        self.expert_bytes = n * row_bytes(dtype, k)
+        if buffer is None:
+            buffer = DeviceBuffer(self.stride * slots)
+            offset = 0
+        self.buffer, self.offset = buffer, offset
+        self.base = buffer.ptr + offset
+
+    def slot_ptr(self, slot: int) -> int:
+        if not 0 <= slot < self.slots:
+            raise IndexError(f"slot {slot} outside [0, {self.slots})")
+        return self.base + slot * self.stride
+
+    def write_slot(self, slot: int, expert_bytes: np.ndarray, stream: int = 0) -> None:
+        b = np.ascontiguousarray(expert_bytes, dtype=np.uint8).reshape(-1)
+        if b.size != self.expert_bytes:
+            raise ValueError(f"expert of {b.size} bytes into a {self.expert_bytes}-byte slot")
+        self.buffer.upload(b, stream, offset=self.offset + slot * self.stride)
+
+    def desc(self) -> Bank:
+        return Bank(self.base, self.stride, self.slots, self.n, self.k, self.dtype)
+
+
+class LayerBanks:
+    """gate/up/down banks of one layer: gate/up [I, H], down [H, I]."""
+
+    def __init__(self, slots: int, hidden: int, inter: int, dtypes: tuple[int, int, int]):
+        self.hidden, self.inter, self.slots = hidden, inter, slots
+        self.gate = SlotBank(slots, inter, hidden, dtypes[0])
+        self.up = SlotBank(slots, inter, hidden, dtypes[1])
+        self.down = SlotBank(slots, hidden, inter, dtypes[2])
+
+    def load(self, slot: int, gate: np.ndarray, up: np.ndarray, down: np.ndarray) -> None:
+        self.gate.write_slot(slot, gate)
+        self.up.write_slot(slot, up)
+        self.down.write_slot(slot, down)
+
+
+def _dev(a) -> int:
+    return a.ptr if isinstance(a, DeviceBuffer) else int(a)
+
+
+def indexed_moe_fused_decode(banks: LayerBanks, x, x_dtype: int, slot_ids, weights, rows: int,
+                             topk: int, out, act: int = ACT_SILU, stream: int = 0) -> None:
+    """out[rows, hidden] f32 = sum_j w[t,j] * expert(slot_ids[t,j])(x[t]); all device pointers."""
+    g, u, d = banks.gate.desc(), banks.up.desc(), banks.down.desc()
+    rc = lib().naiwa_moe_decode(C.byref(g), C.byref(u), C.byref(d), _dev(x), x_dtype,
+                                _dev(slot_ids), _dev(weights), rows, topk, act, _dev(out), stream)
+    check(rc, "naiwa_moe_decode")
+
+
+def router_topk(x, x_dtype: int, W, rows: int, H: int, E: int, k: int, ids_out, w_out,
+                mode: int = ROUTE_SOFTMAX_TOPK_RENORM, logits_out=None, stream: int = 0) -> None:
+    rc = lib().naiwa_router_topk(_dev(x), x_dtype, _dev(W), rows, H, E, k, mode, _dev(ids_out),
+                                 _dev(w_out), _dev(logits_out) if logits_out is not None else None,
+                                 stream)
+    check(rc, "naiwa_router_topk")
+
+
+def moe_gather(ids, n: int, E: int, perm_out, offsets_out, bad_out=None, stream: int = 0) -> None:
+    rc = lib().naiwa_moe_gather(_dev(ids), n, E, _dev(perm_out), _dev(offsets_out),
+                                _dev(bad_out) if bad_out is not None else None, stream)
+    check(rc, "naiwa_moe_gather")
+
+
+def layer_desc(router, banks: "LayerBanks", slot_of_expert=None) -> Layer:
+    return Layer(_dev(router), banks.gate.desc(), banks.up.desc(), banks.down.desc(),
+                 _dev(slot_of_expert) if slot_of_expert is not None else None)
+
+
+def stack_decode(layers: list, x, rows: int, H: int, E: int, k: int,
+                 mode: int = ROUTE_SOFTMAX_TOPK_RENORM, act: int = ACT_SILU, ids_out=None,
+                 w_out=None, fused: bool = True, stream: int = 0) -> None:
+    """One decode step through every layer: x [rows, H] bf16 (device) updated in place.
+    layers: a list of Layer descriptors (layer_desc) or a prebuilt ctypes array."""
+    arr = layers if isinstance(layers, C.Array) else (Layer * len(layers))(*layers)
+    rc = lib().naiwa_stack_decode(arr, len(arr), _dev(x), rows, H, E, k, mode, act,
+                                  _dev(ids_out) if ids_out is not None else None,
+                                  _dev(w_out) if w_out is not None else None,
+                                  STACK_FUSED if fused else STACK_LAYERED, stream)
+    check(rc, "naiwa_stack_decode")
+
+
+def stack_status() -> tuple[int, int]:
+    a, b = C.c_int(0), C.c_int(0)
+    check(lib().naiwa_stack_status(C.byref(a), C.byref(b)), "naiwa_stack_status")
+    return a.value, b.value
+
+
+def synth(dtype: int, seed: int, n: int, out, mean: float = 0.0, std: float = 1.0,
+          offset: int = 0, stream: int = 0) -> None:
+    """Fill a device buffer with the N(mean, std) stream (seed, offset) as dtype bytes."""
+    check(lib().naiwa_synth(dtype, seed, offset, n, mean, std, _dev(out), stream), "naiwa_synth")
+
+
+__all__ = ["layer_desc", "stack_decode", "stack_status", "synth","SlotBank", "LayerBanks", "indexed_moe_fused_decode", "router_topk", "moe_gather",
+           "row_bytes", "expert_range", "slot_stride", "BF16", "F32", "Q4_K", "Q8_0"]
