@@ -47,6 +47,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="budget of the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--trace", action="store_true",
+                    help="print per-phase times of one fused step (diagnostic, untimed)")
     return ap.parse_args()
 
 
@@ -112,6 +114,9 @@ def main() -> int:
     ids = ids_d.download(np.uint32).reshape(L, rows, K)
     ws = w_d.download(np.float32).reshape(L, rows, K)
     assert (ids < E).all() and np.allclose(ws.sum(-1), 1.0, atol=1e-4), "routing output invalid"
+
+    if args.trace and fused:
+        print_trace(nm, lambda: step(0, False), stream, L, info["wall_clock_khz"])
 
     # ---- timed region ----
     ev = [nm.Event() for _ in range(args.steps + 1)]
@@ -188,6 +193,39 @@ def main() -> int:
     }
     print(json.dumps(result), flush=True)
     return 0
+
+
+def print_trace(nm, run, stream, L, khz):
+    """One extra (untimed) fused step with phase timestamps: block 0 and the last block."""
+    import ctypes as C
+    lib = nm.lib()
+    lib.naiwa_stack_trace_enable(1)
+    run()
+    stream.sync()
+    lib.naiwa_stack_trace_enable(0)
+    slots = 16
+    n = 2 * (L + 1) * slots
+    buf = (C.c_uint64 * n)()
+    nl = C.c_int(0)
+    nm._lib.check(lib.naiwa_stack_trace_read(buf, n, C.byref(nl)), "trace_read")
+    t = np.frombuffer(buf, dtype=np.uint64).astype(np.float64).reshape(2, L + 1, slots) / (khz / 1000.0)
+    names = ["logits", "topk", "segments", "preload", "touch", "stage_x", "gate_up", "barrier_Y",
+             "stage_h", "down_dots", "combine", "router", "reduce_X"]
+    for who in range(2):
+        pro = t[who, L]
+        log(f"trace block {'first' if who == 0 else 'last'}: prologue partials {pro[1] - pro[0]:.2f} us, "
+            f"reduce {pro[2] - pro[1]:.2f} us")
+        per = []
+        prev = t[who, L, 2]
+        for l in range(L):
+            m = t[who, l]
+            row = [m[0] - prev] + [m[i] - m[i - 1] for i in range(1, 13)]
+            per.append(row)
+            prev = m[12]
+        per = np.array(per)
+        log("  mean us/layer: " + ", ".join(f"{nme} {v:.2f}" for nme, v in zip(names, per.mean(0)))
+            + f" | total {per.sum(1).mean():.2f}")
+    log(f"trace: kernel span {t[0, L - 1, 12] - t[0, L, 0]:.1f} us")
 
 
 def layers_host_sample(nm, keep, L, E, H, I, n_layers: int = 4):

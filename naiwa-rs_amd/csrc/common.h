@@ -74,11 +74,41 @@ __device__ __forceinline__ float naiwa_dot2_f16(uint32_t a, uint32_t b, float c)
                                   __builtin_bit_cast(naiwa_f16x2, b), c, false);
 }
 
-// Sum over groups of `width` lanes (width a power of two <= 64), result in every lane.
+// One DPP lane move (no LDS round trip): quad permutations and the 8/16-lane
+// mirrors.
+template <int CTRL>
+__device__ __forceinline__ float naiwa_dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of W lanes (a power of two <= 64), result in every
+// lane of the group.  Up to 16 lanes the steps are DPP moves within a row
+// (xor 1, xor 2, then the 8- and 16-lane mirrors); every lane ends with the
+// same bits because each step adds the same two values in either order.
 template <int W>
 __device__ __forceinline__ float naiwa_group_sum(float v) {
+    if (W >= 2) v += naiwa_dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+    if (W >= 4) v += naiwa_dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    if (W >= 8) v += naiwa_dpp<0x141>(v);  // row_half_mirror
+    if (W >= 16) v += naiwa_dpp<0x140>(v); // row_mirror
 #pragma unroll
-    for (int m = W / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, W);
+    for (int m = 16; m < W; m <<= 1) v += __shfl_xor(v, m, W);
+    return v;
+}
+
+template <int CTRL>
+__device__ __forceinline__ long long naiwa_dpp_i64(long long v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(v & 0xffffffffll), CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(v >> 32), CTRL, 0xF, 0xF, false);
+    return (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+}
+
+// Exact int64 sum over aligned groups of 16 lanes (DPP), result in every lane.
+__device__ __forceinline__ long long naiwa_group_sum16_i64(long long v) {
+    v += naiwa_dpp_i64<0xB1>(v);
+    v += naiwa_dpp_i64<0x4E>(v);
+    v += naiwa_dpp_i64<0x141>(v);
+    v += naiwa_dpp_i64<0x140>(v);
     return v;
 }
 

@@ -43,6 +43,58 @@ __device__ __forceinline__ float naiwa_router_fix_to_f32(long long s) {
     return (float)s * 0x1p-32f;
 }
 
+// Top-k of one token's logits (LDS, E <= NT * PER entries) by ranking: thread i
+// computes the rank of expert e = i % E against the logits in its share of the
+// comparison range, the shares are added in LDS, and the experts of rank < k
+// write their slot of ids/w.  No step waits on another lane's result, so the
+// cost is ~E/NT compares per thread instead of k serial wave reductions.
+// rank_tmp: LDS scratch of E ints.  All NT threads of the block must call it.
+template <int NT>
+__device__ inline void naiwa_block_topk(const float* l, int E, int k, int mode, uint32_t* ids, float* w,
+                                        int* rank_tmp, float* ex_tmp) {
+    const int tid = threadIdx.x;
+    const int shares = E > 0 && NT / E > 0 ? NT / E : 1;
+    for (int i = tid; i < E; i += NT) rank_tmp[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < E * shares; i += NT) {
+        const int e = i % E, sh = i / E;
+        const int lo = (int)((long long)E * sh / shares), hi = (int)((long long)E * (sh + 1) / shares);
+        const float me = l[e];
+        int r = 0;
+#pragma unroll 8
+        for (int o = lo; o < hi; ++o) {
+            const float v = l[o];
+            r += (v > me) | ((v == me) & (o < e));
+        }
+        atomicAdd(&rank_tmp[e], r);
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += NT) {
+        const int r = rank_tmp[e];
+        if (r < k) {
+            ids[r] = (uint32_t)e;
+            ex_tmp[r] = l[e];
+        }
+    }
+    __syncthreads();
+    if (tid < 64) {
+        // weights in rank order, the oracle's summation order
+        const float mx = ex_tmp[0];
+        float denom = 0.0f;
+        if (mode == NAIWA_ROUTE_SOFTMAX_TOPK) {
+            float part = 0.0f;
+            for (int e = tid; e < E; e += 64) part += expf(l[e] - mx);
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) part += __shfl_xor(part, m, 64);
+            denom = part;
+        } else {
+            for (int j = 0; j < k; ++j) denom += expf(ex_tmp[j] - mx);
+        }
+        if (tid < k) w[tid] = expf(ex_tmp[tid] - mx) / denom;
+    }
+    __syncthreads();
+}
+
 __device__ __forceinline__ long long naiwa_wave_sum_i64(long long v) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
@@ -54,12 +106,12 @@ __device__ __forceinline__ bool naiwa_rank_before(float va, int ia, float vb, in
     return va > vb || (va == vb && ia < ib);
 }
 
-// One wave (64 lanes) selects the top k of E <= 1024 logits and writes ids
+// One wave (64 lanes) selects the top k of E <= 64 * PER logits and writes ids
 // (rank order) and weights (mode).  Every lane must call it.
+template <int PER = NAIWA_ROUTER_MAX_E / 64>
 __device__ inline void naiwa_wave_topk(const float* l, int E, int k, int mode, uint32_t* ids,
                                        float* w) {
     const int lane = threadIdx.x & 63;
-    constexpr int PER = NAIWA_ROUTER_MAX_E / 64;
     float v[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {

@@ -42,10 +42,23 @@ router_logits_kernel(const void* x, int x_bf16, const float* W, int rows, int H,
     }
 }
 
-__global__ void __launch_bounds__(64)
+constexpr int kTopkThreads = 256;
+
+__global__ void __launch_bounds__(kTopkThreads)
 router_topk_kernel(const float* logits, int E, int k, int mode, uint32_t* ids, float* w) {
+    __shared__ float l[NAIWA_ROUTER_MAX_E];
+    __shared__ int rank_tmp[NAIWA_ROUTER_MAX_E];
+    __shared__ float ex_tmp[NAIWA_ROUTER_MAX_E];
+    __shared__ uint32_t ids_s[NAIWA_ROUTER_MAX_K];
+    __shared__ float w_s[NAIWA_ROUTER_MAX_K];
     const int t = blockIdx.x;
-    naiwa_wave_topk(logits + (int64_t)t * E, E, k, mode, ids + (int64_t)t * k, w + (int64_t)t * k);
+    for (int e = threadIdx.x; e < E; e += kTopkThreads) l[e] = logits[(int64_t)t * E + e];
+    __syncthreads();
+    naiwa_block_topk<kTopkThreads>(l, E, k, mode, ids_s, w_s, rank_tmp, ex_tmp);
+    if (threadIdx.x < k) {
+        ids[(int64_t)t * k + threadIdx.x] = ids_s[threadIdx.x];
+        w[(int64_t)t * k + threadIdx.x] = w_s[threadIdx.x];
+    }
 }
 
 } // namespace
@@ -69,6 +82,6 @@ extern "C" int naiwa_router_topk(const void* x, int x_dtype, const float* W, int
         if (!logits) return rc;
     }
     router_logits_kernel<<<E, kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, W, rows, H, E, logits);
-    router_topk_kernel<<<rows, 64, 0, st>>>(logits, E, k, mode, ids_out, w_out);
+    router_topk_kernel<<<rows, kTopkThreads, 0, st>>>(logits, E, k, mode, ids_out, w_out);
     return naiwa_hip_rc(hipGetLastError());
 }

@@ -116,10 +116,22 @@ __host__ __device__ inline int naiwa_stage_bytes(int dtype, int k) {
     return (k * 2 + (k / span) * 4 + 15) & ~15;
 }
 
+// 8 bytes of activations; device-coherent (bypassing the non-coherent caches)
+// when COH, for vectors other blocks of a persistent kernel have just written.
+template <bool COH>
+__device__ __forceinline__ uint2 naiwa_ld8(const void* p) {
+    if (COH) {
+        const unsigned long long v =
+            __hip_atomic_load((const unsigned long long*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+    }
+    return *reinterpret_cast<const uint2*>(p);
+}
+
 // Stage `k` activations (f32 source, or bf16 when src_bf16) into the perm
 // layout + sums of format DT.  All `nthr` threads of the block take part;
 // k % 32 == 0.  The caller synchronizes afterwards.
-template <int DT>
+template <int DT, bool COH = false>
 __device__ inline void naiwa_stage(const void* src, bool src_bf16, int k, uint32_t* words,
                                    float* sums, int tid, int nthr) {
     constexpr int span = Fmt<DT>::kSumSpan;
@@ -132,14 +144,16 @@ __device__ inline void naiwa_stage(const void* src, bool src_bf16, int k, uint32
         if (g < k / 4) {
             float v[4];
             if (src_bf16) {
-                const uint2 raw = reinterpret_cast<const uint2*>(src)[g];
+                const uint2 raw = naiwa_ld8<COH>((const uint16_t*)src + 4 * g);
                 v[0] = naiwa_bf16_to_f32(raw.x & 0xffffu);
                 v[1] = naiwa_bf16_to_f32(raw.x >> 16);
                 v[2] = naiwa_bf16_to_f32(raw.y & 0xffffu);
                 v[3] = naiwa_bf16_to_f32(raw.y >> 16);
             } else {
-                const float4 raw = reinterpret_cast<const float4*>(src)[g];
-                v[0] = raw.x; v[1] = raw.y; v[2] = raw.z; v[3] = raw.w;
+                const uint2 a = naiwa_ld8<COH>((const float*)src + 4 * g);
+                const uint2 b = naiwa_ld8<COH>((const float*)src + 4 * g + 2);
+                v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y);
+                v[2] = __uint_as_float(b.x); v[3] = __uint_as_float(b.y);
             }
             uint32_t h[4];
 #pragma unroll
@@ -153,6 +167,63 @@ __device__ inline void naiwa_stage(const void* src, bool src_bf16, int k, uint32
         }
         part = naiwa_group_sum<gpg>(part);
         if (g < k / 4 && (g % gpg) == 0) sums[g / gpg] = part;
+    }
+}
+
+// Stage nv (<= MAXV) vectors of k activations at once: every thread issues
+// the loads of all vectors before converting any, so the vectors cost one
+// memory round trip instead of nv.  Vector v goes to dst + v * stride_bytes.
+template <int DT, bool COH, int MAXV>
+__device__ inline void naiwa_stage_multi(const void* const* srcs, int nv, bool src_bf16, int k,
+                                         uint8_t* dst, int stride_bytes, int tid, int nthr) {
+    constexpr int span = Fmt<DT>::kSumSpan;
+    constexpr int gpg = span / 4;
+    for (int g0 = 0; g0 < k / 4; g0 += nthr) {
+        const int g = g0 + tid;
+        const bool in = g < k / 4;
+        uint2 raw[MAXV][2];
+#pragma unroll
+        for (int v = 0; v < MAXV; ++v) {
+            if (v < nv && in) {
+                if (src_bf16) {
+                    raw[v][0] = naiwa_ld8<COH>((const uint16_t*)srcs[v] + 4 * g);
+                } else {
+                    raw[v][0] = naiwa_ld8<COH>((const float*)srcs[v] + 4 * g);
+                    raw[v][1] = naiwa_ld8<COH>((const float*)srcs[v] + 4 * g + 2);
+                }
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < MAXV; ++v) {
+            if (v < nv) {
+            uint32_t* words = (uint32_t*)(dst + v * stride_bytes);
+            float* sums = (float*)(words + k / 2);
+            float part = 0.0f;
+            if (in) {
+                float x[4];
+                if (src_bf16) {
+                    x[0] = naiwa_bf16_to_f32(raw[v][0].x & 0xffffu);
+                    x[1] = naiwa_bf16_to_f32(raw[v][0].x >> 16);
+                    x[2] = naiwa_bf16_to_f32(raw[v][0].y & 0xffffu);
+                    x[3] = naiwa_bf16_to_f32(raw[v][0].y >> 16);
+                } else {
+                    x[0] = __uint_as_float(raw[v][0].x); x[1] = __uint_as_float(raw[v][0].y);
+                    x[2] = __uint_as_float(raw[v][1].x); x[3] = __uint_as_float(raw[v][1].y);
+                }
+                uint32_t h[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    h[i] = Fmt<DT>::to16(x[i]);
+                    x[i] = Fmt<DT>::from16(h[i]);
+                }
+                words[2 * g] = h[0] | (h[2] << 16);
+                words[2 * g + 1] = h[1] | (h[3] << 16);
+                part = (x[0] + x[1]) + (x[2] + x[3]);
+            }
+            part = naiwa_group_sum<gpg>(part);
+            if (in && (g % gpg) == 0) sums[g / gpg] = part;
+            }
+        }
     }
 }
 

@@ -1,25 +1,36 @@
 // NAIWA_STACK_FUSED: one persistent, cooperatively launched kernel runs a
 // whole decode step through every MoE layer, x <- bf16(x + MoE_l(x)).
 //
-// Per layer, with every block resident (grid = CUs x blocks per CU):
-//   A  route   every block reads the layer's router logits (int64 fixed-point
-//              sums, see below), selects the top-k in one wave per token and
-//              groups the (token, k) pairs by cache slot -- redundantly and
-//              identically in every block, so no barrier is needed for it;
-//   B  gate/up the (segment, intermediate row) pairs are dealt out evenly to
-//              the blocks; each 16-lane group streams one gate and one up row
-//              with 16-byte loads and writes h = act(g) * u (f32) per pair;
-//   -- grid barrier --
-//   C  down    each block owns 8 consecutive output features: it stages the
-//              h vectors, dots every (feature, pair), adds the pairs of each
+// One block of 256 threads per CU (16 groups of 16 lanes; one wave per SIMD
+// leaves 512 registers per lane), every block resident.  Per layer:
+//   A  route   every block reads the layer's router logits, selects the top-k
+//              in one wave per token and groups the (token, k) pairs by cache
+//              slot -- redundantly and identically in every block;
+//   B  gate/up the (segment, intermediate row) work is dealt out evenly; each
+//              16-lane group issues the 16-byte loads of one gate row and one
+//              up row before the activations are even staged, then writes
+//              h = act(g) * u per pair.  The block also touches the down rows
+//              and next-layer router rows it will need in C, so they are in
+//              its XCD's L2 by then;
+//   -- all-gather barrier --
+//   C  down    each block owns 8-feature chunks of the output: it stages the h
+//              vectors, dots every (feature, pair), adds the pairs of each
 //              token in ascending slot order (no atomics), applies the
-//              residual, stores bf16 x, and adds the next layer's router
-//              partial sums for its 8 features;
-//   -- grid barrier --
+//              residual, stores bf16 x, and stores its int64 partial sums of
+//              the next layer's router logits;
+//   -- reduce barrier: 8 leader blocks add the partials of every block and
+//      publish the logits --
+//
+// Cross-block data (h, x, router partials, logits, flags) moves with
+// device-coherent relaxed atomic loads and stores (sc1: past the per-XCD L2s),
+// and every block waits for its own stores to complete before it raises its
+// arrival flag, so no barrier needs an L2 writeback or invalidate.  Weights are
+// read with ordinary cached loads; they never change during the kernel.
+//
 // Router logits: each chunk of 8 features is an f32 fma chain rounded to
-// int64 with 32 fractional bits; chunks are added with integer atomics.
+// int64 with 32 fractional bits, and the chunks are added as integers.
 // Integer addition is associative, so the logits (and the top-k) are bit-
-// identical to the CPU oracle's whatever order the blocks finish in.
+// identical to the CPU oracle's however the chunks are distributed.
 #include <mutex>
 #include <string.h>
 #include <vector>
@@ -30,14 +41,19 @@
 
 namespace {
 
-constexpr int kThreads = 256;           // 4 waves, 16 groups of 16 lanes
+constexpr int kThreads = 256;             // 4 waves, 16 groups of 16 lanes
 constexpr int kGroups = kThreads / NAIWA_GROUP;
-constexpr int kMaxRows = 8;             // tokens per step served by this kernel
-constexpr int kMaxK = 8;                // routed experts per token
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxRows = 8;               // tokens per step served by this kernel
+constexpr int kMaxK = 8;                  // routed experts per token
 constexpr int kMaxPairs = kMaxRows * kMaxK;
 constexpr int kMaxE = 256;
-constexpr int kChunk = NAIWA_ROUTER_CHUNK; // output features per phase-C block
-constexpr int kCPairs = 16;             // h vectors staged per phase-C pass
+constexpr int kLeaders = 8;               // blocks that reduce the router partials
+constexpr int kChunk = NAIWA_ROUTER_CHUNK; // output features per phase-C chunk
+constexpr int kCPairs = 16;               // h vectors staged per phase-C pass
+constexpr int kLine = 64;                 // u32 per 256-byte flag line
+constexpr int kPartPerThread = (kMaxRows * kMaxE + kThreads - 1) / kThreads;
+constexpr int kTraceSlots = 16;
 
 struct LayerDev {
     const float* router;
@@ -55,52 +71,219 @@ struct Params {
     int n_layers, rows, H, I, E, k, mode, act;
     uint16_t* x;                 // [rows, H] bf16, in/out
     float* h;                    // [kMaxPairs, I] f32
-    unsigned long long* logit;   // [n_layers, rows, E] int64 fixed point
-    unsigned int* bar;           // barrier counter
+    long long* part;             // [blocks, rows, E] int64 router partials
+    long long* logits;           // [rows, E] int64 fixed point
+    unsigned* arrive;            // [blocks] flag lines
+    unsigned* release;           // [kLeaders] flag lines
     int* status;                 // [0] barrier timeouts, [1] missing experts
     uint32_t* ids_out;           // [n_layers, rows, k] or null
     float* w_out;
-    uint64_t spin_limit;         // wall-clock ticks before a barrier gives up
+    uint64_t spin_limit;         // wall-clock ticks before a wait gives up
+    int never;                   // always 0: keeps the prefetch touches alive
+    unsigned long long* trace;   // optional [2][n_layers + 1][kTraceSlots] phase timestamps
 };
+
+// Phase timestamps (s_memrealtime) of the first and last block, when tracing.
+__device__ __forceinline__ void mark(const Params& p, int layer, int slot) {
+    if (!p.trace || threadIdx.x != 0) return;
+    const int who = blockIdx.x == 0 ? 0 : (blockIdx.x == gridDim.x - 1 ? 1 : -1);
+    if (who < 0) return;
+    p.trace[((size_t)who * (p.n_layers + 1) + layer) * kTraceSlots + slot] = wall_clock64();
+}
 
 struct Smem {
     uint32_t pair_slot[kMaxPairs]; // slot of pair p = t*k + j
     float pair_w[kMaxPairs];
-    uint32_t sorted[kMaxPairs];    // pairs in (slot, p) order
+    uint32_t sorted[kMaxPairs];    // valid pairs in (slot, p) order
     uint32_t seg_begin[kMaxPairs + 1];
     int nseg;
+    uint32_t seg_slot[kMaxPairs];
+    float lg[kMaxRows][kMaxE];
+    uint32_t top_ids[kMaxRows][kMaxK];
+    float top_w[kMaxRows][kMaxK];
+    int rank_tmp[kMaxE];
+    float ex_tmp[kMaxE];
     float partial[kChunk][kMaxPairs];
     float xnew[kMaxRows][kChunk];
 };
 
-__device__ __forceinline__ void grid_barrier(const Params& p, unsigned int& gen) {
-    gen += gridDim.x;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __hip_atomic_fetch_add(p.bar, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-        const uint64_t t0 = wall_clock64();
-        while (__hip_atomic_load(p.bar, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < gen) {
-            if (wall_clock64() - t0 > p.spin_limit) {
-                atomicAdd(&p.status[0], 1);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
+constexpr int kMaxLayers = 128;           // layer descriptors kept in LDS
+
+__device__ __forceinline__ unsigned ld_flag(const unsigned* f) {
+    return __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_flag(unsigned* f, unsigned v) {
+    __hip_atomic_store(f, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh(long long* p, long long v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ long long ld_coh(const long long* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_coh(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// This wave's stores have completed (reached the device-coherent level).
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ inline void spin_ge(const unsigned* f, unsigned target, const Params& p, bool sleep) {
+    const uint64_t t0 = wall_clock64();
+    while (ld_flag(f) < target) {
+        if (wall_clock64() - t0 > p.spin_limit) {
+            atomicAdd(&p.status[0], 1);
+            return;
         }
+        if (sleep) __builtin_amdgcn_s_sleep(1);
     }
-    __syncthreads();
-    __threadfence();
 }
 
-// Router partial sums of the features [f0, f0 + kChunk) for every (token, expert).
-__device__ inline void router_partials(const Params& p, const float* W, int layer, int f0,
-                                       const float (*xv)[kChunk]) {
-    unsigned long long* acc = p.logit + (size_t)layer * p.rows * p.E;
-    for (int it = threadIdx.x; it < p.rows * p.E; it += kThreads) {
-        const int t = it / p.E, e = it % p.E;
-        const long long v = naiwa_router_chunk(W + (size_t)e * p.H + f0, xv[t]);
-        if (v) atomicAdd(&acc[it], (unsigned long long)v);
-        (void)t;
+// Every block raises its flag and waits for every other block's.
+__device__ inline void barrier_all(const Params& p, unsigned epoch) {
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) st_flag(&p.arrive[blockIdx.x * kLine], epoch);
+    for (int i = threadIdx.x; i < (int)gridDim.x; i += kThreads) spin_ge(&p.arrive[i * kLine], epoch, p, true);
+    __syncthreads();
+}
+
+// Barrier that also publishes the logits: leader L waits for every block,
+// adds all blocks' partials of its experts and raises its release flag; the
+// others wait for the leaders only.
+__device__ inline void barrier_reduce(const Params& p, Smem& sm, unsigned epoch) {
+    const int tid = threadIdx.x, bid = blockIdx.x, G = gridDim.x;
+    wait_stores();
+    __syncthreads();
+    if (tid == 0) st_flag(&p.arrive[bid * kLine], epoch);
+    const int epl = (p.E + kLeaders - 1) / kLeaders;
+    if (bid < kLeaders) {
+        for (int i = tid; i < G; i += kThreads) spin_ge(&p.arrive[i * kLine], epoch, p, false);
+        __syncthreads();
+        const int e0 = bid * epl;
+        const int ne = max(0, min(epl, p.E - e0));
+        const int items = p.rows * ne;
+        const int grp = tid / NAIWA_GROUP, lr = tid % NAIWA_GROUP;
+        const size_t bstride = (size_t)p.rows * p.E;
+        // one 16-lane group per (token, expert); lane lr adds blocks lr, lr + 16, ...
+        for (int it = grp; it < items; it += kGroups) {
+            const int t = it / ne, e = e0 + it % ne;
+            const long long* src = p.part + (size_t)t * p.E + e;
+            long long s = 0;
+#pragma unroll 1
+            for (int b0 = lr; b0 < G; b0 += 8 * NAIWA_GROUP) {
+                long long v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int b = b0 + j * NAIWA_GROUP;
+                    v[j] = b < G ? ld_coh(src + (size_t)b * bstride) : 0;
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) s += v[j];
+            }
+            s = naiwa_group_sum16_i64(s);
+            if (lr == 0) st_coh(&p.logits[(size_t)t * p.E + e], s);
+        }
+        wait_stores();
+        __syncthreads();
+        if (tid == 0) st_flag(&p.release[bid * kLine], epoch);
+    }
+    if (tid < kLeaders) spin_ge(&p.release[tid * kLine], epoch, p, true);
+    __syncthreads();
+}
+
+// Router partials of this block's chunks for (token, expert) items; the
+// chunk's 8 activations come from LDS.  acc holds kPartPerThread items.
+__device__ inline void router_chunk_accumulate(const Params& p, const float* W, int f0,
+                                               const float (*xv)[kChunk], long long* acc) {
+#pragma unroll
+    for (int j = 0; j < kPartPerThread; ++j) {
+        const int it = threadIdx.x + j * kThreads;
+        if (it < p.rows * p.E) {
+            const int t = it / p.E, e = it % p.E;
+            acc[j] += naiwa_router_chunk(W + (size_t)e * p.H + f0, xv[t]);
+        }
+    }
+}
+
+__device__ inline void router_store_partials(const Params& p, const long long* acc) {
+#pragma unroll
+    for (int j = 0; j < kPartPerThread; ++j) {
+        const int it = threadIdx.x + j * kThreads;
+        if (it < p.rows * p.E) st_coh(&p.part[(size_t)blockIdx.x * p.rows * p.E + it], acc[j]);
+    }
+}
+
+// One gate/up row of a segment for every token of the segment: h = act(g) * u.
+// With `preloaded`, the first batch of codes is already in fg/fu.
+template <int DG>
+__device__ inline void gate_up_row(const Params& p, const Smem& sm, const LayerDev& L, const uint8_t* dyn,
+                                   int q, int xstage, int64_t rb, int nu, int lr,
+                                   typename Fmt<DG>::Frag* fg, typename Fmt<DG>::Frag* fu, bool preloaded) {
+    constexpr int UM = Umax<DG>::v;
+    const int I = p.I, H = p.H, k = p.k;
+    const int s = q / I, r = q % I;
+    const uint32_t slot = sm.seg_slot[s];
+    const uint8_t* grow = L.gate + (int64_t)slot * L.gate_stride + (int64_t)r * rb;
+    const uint8_t* urow = L.up + (int64_t)slot * L.up_stride + (int64_t)r * rb;
+    const int b = (int)sm.seg_begin[s], e = (int)sm.seg_begin[s + 1];
+    const int nbatch = (nu + NAIWA_GROUP * UM - 1) / (NAIWA_GROUP * UM);
+    for (int tt = b; tt < e; ++tt) {
+        const int t = (int)sm.sorted[tt] / k;
+        const uint32_t* words = (const uint32_t*)(dyn + t * xstage);
+        const float* sums = (const float*)(words + H / 2);
+        float ag = 0.0f, au = 0.0f;
+        for (int bt = 0; bt < nbatch; ++bt) {
+            const int base = lr + bt * NAIWA_GROUP * UM;
+            // batch 0 stays in registers across tokens when it is the only batch
+            const bool have = bt == 0 && ((tt == b && preloaded) || (tt > b && nbatch == 1));
+            if (!have) {
+#pragma unroll
+                for (int i = 0; i < UM; ++i) {
+                    const int u = base + NAIWA_GROUP * i;
+                    if (u < nu) {
+                        fg[i] = Fmt<DG>::load(grow, u);
+                        fu[i] = Fmt<DG>::load(urow, u);
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < UM; ++i) {
+                const int u = base + NAIWA_GROUP * i;
+                if (u < nu) {
+                    ag += Fmt<DG>::dot(fg[i], u, words, sums);
+                    au += Fmt<DG>::dot(fu[i], u, words, sums);
+                }
+            }
+        }
+        const float gv = naiwa_group_sum<NAIWA_GROUP>(ag);
+        const float uv = naiwa_group_sum<NAIWA_GROUP>(au);
+        if (lr == 0) st_coh(&p.h[(size_t)sm.sorted[tt] * I + r], naiwa_act(p.act, gv) * uv);
+    }
+}
+
+// Issue the loads of the first batch of a row's gate and up codes.
+template <int DG>
+__device__ inline void gate_up_preload(const Params& p, const Smem& sm, const LayerDev& L, int q,
+                                       int64_t rb, int nu, int lr, typename Fmt<DG>::Frag* fg,
+                                       typename Fmt<DG>::Frag* fu) {
+    constexpr int UM = Umax<DG>::v;
+    const int s = q / p.I, r = q % p.I;
+    const uint32_t slot = sm.seg_slot[s];
+    const uint8_t* grow = L.gate + (int64_t)slot * L.gate_stride + (int64_t)r * rb;
+    const uint8_t* urow = L.up + (int64_t)slot * L.up_stride + (int64_t)r * rb;
+#pragma unroll
+    for (int i = 0; i < UM; ++i) {
+        const int u = lr + NAIWA_GROUP * i;
+        if (u < nu) {
+            fg[i] = Fmt<DG>::load(grow, u);
+            fu[i] = Fmt<DG>::load(urow, u);
+        }
     }
 }
 
@@ -109,6 +292,7 @@ __global__ void __launch_bounds__(kThreads)
 stack_kernel(Params p) {
     extern __shared__ __align__(16) uint8_t dyn[];
     __shared__ Smem sm;
+    __shared__ LayerDev layers_lds[kMaxLayers];
     const int tid = threadIdx.x, grp = tid / NAIWA_GROUP, lr = tid % NAIWA_GROUP;
     const int lane = tid & 63, wave = tid >> 6;
     const int G = gridDim.x, bid = blockIdx.x;
@@ -116,168 +300,246 @@ stack_kernel(Params p) {
     const int npairs = rows * k;
     const int xstage = naiwa_stage_bytes(DG, H);
     const int hstage = naiwa_stage_bytes(DD, I);
-    unsigned int gen = 0;
+    const int nchunks = H / kChunk;
+    const int64_t rb = naiwa_row_bytes(DG == NAIWA_Q8_0_ODD ? NAIWA_Q8_0 : DG, H);
+    const int64_t drb = naiwa_row_bytes(DD == NAIWA_Q8_0_ODD ? NAIWA_Q8_0 : DD, I);
+    const int nu = Fmt<DG>::units(H);
+    constexpr int UM = Umax<DG>::v;
+    unsigned epoch = 0;
+    uint32_t touch = 0;
 
-    // ---- prologue: zero the logit accumulators, then layer 0's partials ----
+    // ---- prologue: layer descriptors into LDS, layer 0's router logits ----
+    mark(p, p.n_layers, 0);
+    for (int i = tid; i < p.n_layers * (int)(sizeof(LayerDev) / 8); i += kThreads)
+        reinterpret_cast<unsigned long long*>(layers_lds)[i] =
+            reinterpret_cast<const unsigned long long*>(p.layers)[i];
+    __syncthreads();
     {
-        const size_t n = (size_t)p.n_layers * rows * E;
-        for (size_t i = (size_t)bid * kThreads + tid; i < n; i += (size_t)G * kThreads) p.logit[i] = 0ull;
-    }
-    grid_barrier(p, gen);
-    for (int c = bid; c < H / kChunk; c += G) {
-        __shared__ float x0[kMaxRows][kChunk];
-        if (tid < rows * kChunk) {
-            const int t = tid / kChunk, i = tid % kChunk;
-            x0[t][i] = naiwa_bf16_to_f32(p.x[(size_t)t * H + c * kChunk + i]);
+        long long acc[kPartPerThread];
+#pragma unroll
+        for (int j = 0; j < kPartPerThread; ++j) acc[j] = 0;
+        for (int c = bid; c < nchunks; c += G) {
+            __syncthreads();
+            if (tid < rows * kChunk) {
+                const int t = tid / kChunk, i = tid % kChunk;
+                sm.xnew[t][i] = naiwa_bf16_to_f32(p.x[(size_t)t * H + c * kChunk + i]);
+            }
+            __syncthreads();
+            router_chunk_accumulate(p, layers_lds[0].router, c * kChunk, sm.xnew, acc);
         }
-        __syncthreads();
-        router_partials(p, p.layers[0].router, 0, c * kChunk, x0);
-        __syncthreads();
+        router_store_partials(p, acc);
+        mark(p, p.n_layers, 1);
+        barrier_reduce(p, sm, ++epoch);
+        mark(p, p.n_layers, 2);
     }
-    grid_barrier(p, gen);
 
     for (int l = 0; l < p.n_layers; ++l) {
-        const LayerDev L = p.layers[l];
+        const LayerDev L = layers_lds[l];
         // ---- A: route (every block, identically) ----
-        unsigned long long* acc = p.logit + (size_t)l * rows * E;
-        for (int t = wave; t < rows; t += kThreads / 64) {
-            __shared__ float lg[kThreads / 64][kMaxE];
-            for (int e = lane; e < E; e += 64)
-                lg[wave][e] = naiwa_router_fix_to_f32((long long)__hip_atomic_load(
-                    &acc[(size_t)t * E + e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-            __builtin_amdgcn_wave_barrier();
-            __shared__ uint32_t tid_ids[kMaxRows][kMaxK];
-            __shared__ float tid_w[kMaxRows][kMaxK];
-            naiwa_wave_topk(lg[wave], E, k, p.mode, tid_ids[t], tid_w[t]);
-            __builtin_amdgcn_wave_barrier();
-            if (lane < k) {
-                const uint32_t e = tid_ids[t][lane];
-                const int32_t s = L.slot_of ? L.slot_of[e] : (int32_t)e;
-                const bool ok = s >= 0 && s < L.slots;
-                sm.pair_slot[t * k + lane] = ok ? (uint32_t)s : 0u;
-                sm.pair_w[t * k + lane] = ok ? tid_w[t][lane] : 0.0f;
-                if (!ok && bid == 0) atomicAdd(&p.status[1], 1);
-                if (bid == 0 && p.ids_out) {
-                    p.ids_out[((size_t)l * rows + t) * k + lane] = e;
-                    p.w_out[((size_t)l * rows + t) * k + lane] = tid_w[t][lane];
-                }
-            }
-        }
-        __syncthreads();
-        // rank of pair q in (slot, q) order; zero-weight pairs are dropped
-        if (wave == 0) {
-            for (int q = lane; q < npairs; q += 64) {
-                if (sm.pair_w[q] == 0.0f) continue;
-                const uint32_t sq = sm.pair_slot[q];
-                int rank = 0;
-                for (int o = 0; o < npairs; ++o) {
-                    if (sm.pair_w[o] == 0.0f) continue;
-                    const uint32_t so = sm.pair_slot[o];
-                    rank += so < sq || (so == sq && o < q);
-                }
-                sm.sorted[rank] = (uint32_t)q;
-            }
-        }
-        __syncthreads();
-        if (tid == 0) {
-            int nvalid = 0;
-            for (int q = 0; q < npairs; ++q) nvalid += sm.pair_w[q] != 0.0f;
-            int ns = 0;
-            for (int i = 0; i < nvalid; ++i) {
-                if (i == 0 || sm.pair_slot[sm.sorted[i]] != sm.pair_slot[sm.sorted[i - 1]])
-                    sm.seg_begin[ns++] = (uint32_t)i;
-            }
-            sm.seg_begin[ns] = (uint32_t)nvalid;
-            sm.nseg = ns;
-        }
-        // stage x of every token (bf16 source)
-        for (int t = 0; t < rows; ++t) {
-            uint32_t* words = (uint32_t*)(dyn + t * xstage);
-            naiwa_stage<DG>(p.x + (size_t)t * H, true, H, words, (float*)(words + H / 2), tid, kThreads);
-        }
-        __syncthreads();
-
-        // ---- B: gate/up, rows dealt out evenly ----
         {
-            const int nseg = sm.nseg;
-            const int total = nseg * I;
-            const int per = (total + G - 1) / G;
-            const int q0 = bid * per, q1 = min(total, q0 + per);
-            const int64_t rb = naiwa_row_bytes(DG == NAIWA_Q8_0_ODD ? NAIWA_Q8_0 : DG, H);
-            const int nu = Fmt<DG>::units(H);
-            constexpr int UM = Umax<DG>::v;
-            for (int q = q0 + grp; q < q1; q += kGroups) {
-                const int s = q / I, r = q % I;
-                const uint32_t slot = sm.pair_slot[sm.sorted[sm.seg_begin[s]]];
-                const uint8_t* grow = L.gate + (int64_t)slot * L.gate_stride + (int64_t)r * rb;
-                const uint8_t* urow = L.up + (int64_t)slot * L.up_stride + (int64_t)r * rb;
-                const int b = (int)sm.seg_begin[s], e = (int)sm.seg_begin[s + 1];
-                float ag[kMaxRows], au[kMaxRows];
+            const int n = rows * E;
+#pragma unroll 1
+            for (int i0 = tid; i0 < n; i0 += 8 * kThreads) {
+                long long v[8];
 #pragma unroll
-                for (int i = 0; i < kMaxRows; ++i) ag[i] = au[i] = 0.0f;
-                for (int base = lr; base < nu; base += NAIWA_GROUP * UM) {
-                    typename Fmt<DG>::Frag fg[UM], fu[UM];
-#pragma unroll
-                    for (int i = 0; i < UM; ++i) {
-                        const int u = base + NAIWA_GROUP * i;
-                        if (u < nu) {
-                            fg[i] = Fmt<DG>::load(grow, u);
-                            fu[i] = Fmt<DG>::load(urow, u);
-                        }
-                    }
-#pragma unroll
-                    for (int i = 0; i < UM; ++i) {
-                        const int u = base + NAIWA_GROUP * i;
-                        if (u >= nu) continue;
-#pragma unroll
-                        for (int tt = 0; tt < kMaxRows; ++tt) {
-                            if (b + tt >= e) break;
-                            const int t = (int)sm.sorted[b + tt] / k;
-                            const uint32_t* words = (const uint32_t*)(dyn + t * xstage);
-                            const float* sums = (const float*)(words + H / 2);
-                            ag[tt] += Fmt<DG>::dot(fg[i], u, words, sums);
-                            au[tt] += Fmt<DG>::dot(fu[i], u, words, sums);
-                        }
-                    }
+                for (int j = 0; j < 8; ++j) {
+                    const int i = i0 + j * kThreads;
+                    v[j] = i < n ? ld_coh(&p.logits[i]) : 0;
                 }
 #pragma unroll
-                for (int tt = 0; tt < kMaxRows; ++tt) {
-                    if (b + tt >= e) break;
-                    const float gv = naiwa_group_sum<NAIWA_GROUP>(ag[tt]);
-                    const float uv = naiwa_group_sum<NAIWA_GROUP>(au[tt]);
-                    if (lr == 0) p.h[(size_t)sm.sorted[b + tt] * I + r] = naiwa_act(p.act, gv) * uv;
+                for (int j = 0; j < 8; ++j) {
+                    const int i = i0 + j * kThreads;
+                    if (i < n) sm.lg[i / E][i % E] = naiwa_router_fix_to_f32(v[j]);
                 }
             }
         }
-        grid_barrier(p, gen);
+        __syncthreads();
+        mark(p, l, 0);
+        for (int t = 0; t < rows; ++t)
+            naiwa_block_topk<kThreads>(sm.lg[t], E, k, p.mode, sm.top_ids[t], sm.top_w[t], sm.rank_tmp, sm.ex_tmp);
+        if (tid < npairs) {
+            const int t = tid / k, j = tid % k;
+            const uint32_t e = sm.top_ids[t][j];
+            const int32_t s = L.slot_of ? L.slot_of[e] : (int32_t)e;
+            const bool ok = s >= 0 && s < L.slots;
+            sm.pair_slot[tid] = ok ? (uint32_t)s : 0u;
+            sm.pair_w[tid] = ok ? sm.top_w[t][j] : 0.0f;
+            if (!ok && bid == 0) atomicAdd(&p.status[1], 1);
+            if (bid == 0 && p.ids_out) {
+                p.ids_out[(size_t)l * npairs + tid] = e;
+                p.w_out[(size_t)l * npairs + tid] = sm.top_w[t][j];
+            }
+        }
+        __syncthreads();
+        mark(p, l, 1);
+        // group the valid pairs by slot (ascending slot, then pair index):
+        // one wave, one pair per lane, ranks and segment starts by counting
+        if (wave == 0) {
+            const int q = lane;
+            const bool valid = q < npairs && sm.pair_w[q] != 0.0f;
+            const uint32_t sq = valid ? sm.pair_slot[q] : 0u;
+            int rank = 0;
+            bool start = valid;
+            for (int o = 0; o < npairs; ++o) {
+                const bool vo = sm.pair_w[o] != 0.0f;
+                const uint32_t so = sm.pair_slot[o];
+                if (vo) {
+                    rank += so < sq || (so == sq && o < q);
+                    if (so == sq && o < q) start = false;
+                }
+            }
+            const unsigned long long starts = __ballot(start);
+            const unsigned long long valids = __ballot(valid);
+            int segidx = 0;
+            for (int o = 0; o < npairs; ++o)
+                segidx += ((starts >> o) & 1ull) && sm.pair_slot[o] < sq;
+            if (valid) sm.sorted[rank] = (uint32_t)q;
+            if (start) {
+                sm.seg_begin[segidx] = (uint32_t)rank;
+                sm.seg_slot[segidx] = sq;
+            }
+            if (lane == 0) {
+                const int ns = __popcll(starts);
+                sm.seg_begin[ns] = (uint32_t)__popcll(valids);
+                sm.nseg = ns;
+            }
+        }
+        __syncthreads();
+        const int nseg = sm.nseg;
+        const int nvalid = (int)sm.seg_begin[nseg];
+        mark(p, l, 2);
+
+        // ---- B: gate/up ----
+        const int total = nseg * I;
+        const int per = (total + G - 1) / G;
+        const int q0 = bid * per, q1 = min(total, q0 + per);
+        // this group's first two rows: issue their loads before staging anything
+        typename Fmt<DG>::Frag fg0[UM], fu0[UM], fg1[UM], fu1[UM];
+        const int qa = q0 + grp, qb = q0 + grp + kGroups;
+        if (qa < q1) gate_up_preload<DG>(p, sm, L, qa, rb, nu, lr, fg0, fu0);
+        if (qb < q1) gate_up_preload<DG>(p, sm, L, qb, rb, nu, lr, fg1, fu1);
+        mark(p, l, 3);
+        // touch the down rows of this block's C chunks (the 16-byte pieces that
+        // cover them; each slot is 16-byte aligned and padded to 16) and the next
+        // router's columns, so C finds them in this XCD's L2.  Eight loads are
+        // in flight per thread before any result is used.
+        {
+            const float* Wn = l + 1 < p.n_layers ? layers_lds[l + 1].router : nullptr;
+            for (int c = bid; c < nchunks; c += G) {
+                const int64_t lo = (int64_t)c * kChunk * drb, hi = lo + kChunk * drb;
+                const int64_t a0 = lo & ~int64_t(15);
+                const int per_seg = (int)((hi - a0 + 15) / 16);
+                const int npieces = nseg * per_seg;
+#pragma unroll 1
+                for (int i0 = tid; i0 < npieces; i0 += 8 * kThreads) {
+                    uint32_t v[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int i = min(i0 + j * kThreads, npieces - 1);
+                        const int s = i / per_seg, piece = i % per_seg;
+                        const uint32_t slot = sm.seg_slot[s];
+                        v[j] = reinterpret_cast<const uint4*>(L.down + (int64_t)slot * L.down_stride + a0 + 16 * piece)->x;
+                    }
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) touch ^= v[j];
+                }
+                if (Wn)
+                    for (int e = tid; e < E; e += kThreads) touch ^= __float_as_uint(Wn[(size_t)e * H + c * kChunk]);
+            }
+        }
+        mark(p, l, 4);
+        // stage every token's activations
+        {
+            const void* srcs[kMaxRows];
+#pragma unroll
+            for (int t = 0; t < kMaxRows; ++t) srcs[t] = p.x + (size_t)min(t, rows - 1) * H;
+            naiwa_stage_multi<DG, true, kMaxRows>(srcs, rows, true, H, dyn, xstage, tid, kThreads);
+        }
+        __syncthreads();
+        mark(p, l, 5);
+#pragma unroll 1
+        for (int q = qa, j = 0; q < q1; q += kGroups, ++j) {
+            if (j == 1) {
+#pragma unroll
+                for (int i = 0; i < UM; ++i) {
+                    fg0[i] = fg1[i];
+                    fu0[i] = fu1[i];
+                }
+            }
+            gate_up_row<DG>(p, sm, L, dyn, q, xstage, rb, nu, lr, fg0, fu0, j < 2);
+        }
+        mark(p, l, 6);
+        barrier_all(p, ++epoch);
+        mark(p, l, 7);
 
         // ---- C: down + ordered combine + residual + next router partials ----
-        const int64_t drb = naiwa_row_bytes(DD == NAIWA_Q8_0_ODD ? NAIWA_Q8_0 : DD, I);
-        const int nvalid = (int)sm.seg_begin[sm.nseg];
-        for (int c = bid; c < H / kChunk; c += G) {
+        long long racc[kPartPerThread];
+#pragma unroll
+        for (int j = 0; j < kPartPerThread; ++j) racc[j] = 0;
+        for (int c = bid; c < nchunks; c += G) {
             const int f0 = c * kChunk;
             for (int b0 = 0; b0 < nvalid; b0 += kCPairs) {
                 const int nb = min(kCPairs, nvalid - b0);
                 __syncthreads();
-                for (int i = 0; i < nb; ++i) {
-                    uint32_t* words = (uint32_t*)(dyn + i * hstage);
-                    naiwa_stage<DD>(p.h + (size_t)sm.sorted[b0 + i] * I, false, I, words,
-                                    (float*)(words + I / 2), tid, kThreads);
+                {
+#pragma unroll 1
+                    for (int v0 = 0; v0 < nb; v0 += 8) {
+                        const void* srcs[8];
+#pragma unroll
+                        for (int i = 0; i < 8; ++i)
+                            srcs[i] = p.h + (size_t)sm.sorted[b0 + min(v0 + i, nb - 1)] * I;
+                        naiwa_stage_multi<DD, true, 8>(srcs, min(8, nb - v0), false, I, dyn + v0 * hstage,
+                                                       hstage, tid, kThreads);
+                    }
                 }
                 __syncthreads();
-                // (feature, staged pair) items over the 16 groups
-                for (int it = grp; it < kChunk * nb; it += kGroups) {
-                    const int fi = it % kChunk, pi = it / kChunk;
-                    const uint32_t pr = sm.sorted[b0 + pi];
-                    const uint8_t* drow = L.down + (int64_t)sm.pair_slot[pr] * L.down_stride +
-                                          (int64_t)(f0 + fi) * drb;
-                    const uint32_t* words = (const uint32_t*)(dyn + pi * hstage);
-                    const float v = naiwa_row_dot<DD, Umax<DD>::v>(drow, I, words,
-                                                                  (const float*)(words + I / 2), lr);
-                    if (lr == 0) sm.partial[fi][b0 + pi] = v;
+                mark(p, l, 8);
+                // (feature, staged pair) items, kCB per group at a time: all
+                // their loads are issued before the first dot
+                constexpr int kCB = 4;
+                constexpr int DUM = 2;
+                const int dnu = Fmt<DD>::units(I);
+                const int nitems = kChunk * nb;
+                for (int it0 = grp; it0 < nitems; it0 += kGroups * kCB) {
+                    typename Fmt<DD>::Frag fr[kCB][DUM];
+                    float acc[kCB];
+#pragma unroll
+                    for (int j = 0; j < kCB; ++j) acc[j] = 0.0f;
+                    for (int base = lr; base < dnu; base += NAIWA_GROUP * DUM) {
+#pragma unroll
+                        for (int j = 0; j < kCB; ++j) {
+                            const int it = min(it0 + j * kGroups, nitems - 1);
+                            const int fi = it % kChunk, pi = it / kChunk;
+                            const uint8_t* drow = L.down + (int64_t)sm.pair_slot[sm.sorted[b0 + pi]] * L.down_stride +
+                                                  (int64_t)(f0 + fi) * drb;
+#pragma unroll
+                            for (int i = 0; i < DUM; ++i) {
+                                const int u = base + NAIWA_GROUP * i;
+                                if (u < dnu) fr[j][i] = Fmt<DD>::load(drow, u);
+                            }
+                        }
+#pragma unroll
+                        for (int j = 0; j < kCB; ++j) {
+                            const int it = min(it0 + j * kGroups, nitems - 1);
+                            const int pi = it / kChunk;
+                            const uint32_t* words = (const uint32_t*)(dyn + pi * hstage);
+#pragma unroll
+                            for (int i = 0; i < DUM; ++i) {
+                                const int u = base + NAIWA_GROUP * i;
+                                if (u < dnu) acc[j] += Fmt<DD>::dot(fr[j][i], u, words, (const float*)(words + I / 2));
+                            }
+                        }
+                    }
+#pragma unroll
+                    for (int j = 0; j < kCB; ++j) {
+                        const int it = it0 + j * kGroups;
+                        const float v = naiwa_group_sum<NAIWA_GROUP>(acc[j]);
+                        if (it < nitems && lr == 0) sm.partial[it % kChunk][b0 + it / kChunk] = v;
+                    }
                 }
             }
             __syncthreads();
+            mark(p, l, 9);
             if (tid < rows * kChunk) {
                 const int t = tid / kChunk, fi = tid % kChunk;
                 float y = 0.0f;
@@ -285,16 +547,32 @@ stack_kernel(Params p) {
                     const uint32_t pr = sm.sorted[i];
                     if ((int)pr / k == t) y += sm.pair_w[pr] * sm.partial[fi][i];
                 }
-                uint16_t* xp = p.x + (size_t)t * H + f0 + fi;
-                const float xn = naiwa_bf16_to_f32(naiwa_f32_to_bf16(naiwa_bf16_to_f32(*xp) + y));
-                *xp = (uint16_t)naiwa_f32_to_bf16(xn);
-                sm.xnew[t][fi] = xn;
+                const uint32_t pair = ld_coh((const uint32_t*)(p.x + (size_t)t * H + f0 + (fi & ~1)));
+                const float xo = naiwa_bf16_to_f32((fi & 1) ? pair >> 16 : pair & 0xffffu);
+                sm.xnew[t][fi] = naiwa_bf16_to_f32(naiwa_f32_to_bf16(xo + y));
             }
             __syncthreads();
-            if (l + 1 < p.n_layers) router_partials(p, p.layers[l + 1].router, l + 1, f0, sm.xnew);
+            if (tid < rows * kChunk / 2) {
+                const int t = tid / (kChunk / 2), fi = 2 * (tid % (kChunk / 2));
+                const uint32_t packed = naiwa_f32_to_bf16(sm.xnew[t][fi]) |
+                                        (naiwa_f32_to_bf16(sm.xnew[t][fi + 1]) << 16);
+                st_coh((uint32_t*)(p.x + (size_t)t * H + f0 + fi), packed);
+            }
+            mark(p, l, 10);
+            if (l + 1 < p.n_layers) router_chunk_accumulate(p, layers_lds[l + 1].router, f0, sm.xnew, racc);
         }
-        grid_barrier(p, gen);
+        mark(p, l, 11);
+        if (l + 1 < p.n_layers) {
+            router_store_partials(p, racc);
+            barrier_reduce(p, sm, ++epoch);
+        }
+        mark(p, l, 12);
     }
+    if (touch == 0x9E3779B9u && p.never) p.status[2] = (int)touch;
+}
+
+__global__ void zero_u32(unsigned int* ptr, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) ptr[i] = 0u;
 }
 
 struct FusedCache {
@@ -322,14 +600,31 @@ int occupancy(size_t lds, int* per_cu) {
                                                                      kThreads, lds));
 }
 
-__global__ void zero_u32(unsigned int* p, int n) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0u;
-}
-
 } // namespace
 
-static int g_fused_blocks_per_cu = 2;
+static int g_fused_blocks_per_cu = 1;
+static bool g_trace_enabled = false;
+static int g_trace_layers = 0;
+
+// Phase timestamps of the fused kernel (diagnostic): when on, the first and
+// last block record s_memrealtime ticks at each phase boundary of every layer.
+extern "C" int naiwa_stack_trace_enable(int on) {
+    g_trace_enabled = on != 0;
+    return NAIWA_OK;
+}
+
+// Copies the last traced launch's timestamps: [2][n_layers + 1][8] u64 ticks
+// (the extra layer row is the prologue).  Synchronizes the device.
+extern "C" int naiwa_stack_trace_read(uint64_t* out, int capacity, int* n_layers) {
+    int rc = 0;
+    if (!g_trace_layers) return NAIWA_E_NOT_FOUND;
+    const size_t n = (size_t)2 * (g_trace_layers + 1) * kTraceSlots;
+    if (!out || capacity < (int)n) return NAIWA_E_INVALID;
+    void* t = naiwa_scratch(NAIWA_SCRATCH_STACK + 2, n * 8, &rc);
+    if (!t) return rc;
+    if (n_layers) *n_layers = g_trace_layers;
+    return naiwa_hip_rc(hipMemcpy(out, t, n * 8, hipMemcpyDeviceToHost));
+}
 
 extern "C" int naiwa_stack_set_blocks_per_cu(int n) {
     if (n < 1 || n > 8) return NAIWA_E_INVALID;
@@ -337,14 +632,19 @@ extern "C" int naiwa_stack_set_blocks_per_cu(int n) {
     return NAIWA_OK;
 }
 
-// Status of the last fused launches: barrier timeouts and routed experts that
-// had no resident slot.  Synchronizes the device.
+namespace {
+// status words live after the flag lines in the sync scratch
+constexpr size_t kStatusOff = 0;
+}
+
+// Status of the last fused launches: barrier waits that gave up after their
+// 2 s bound, and routed experts that had no resident slot.  Synchronizes.
 extern "C" int naiwa_stack_status(int* barrier_timeouts, int* missing_experts) {
     int rc = 0;
-    int* status = (int*)naiwa_scratch(NAIWA_SCRATCH_STACK + 1, 4096, &rc);
-    if (!status) return rc;
+    uint8_t* sync = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK + 1, 4096, &rc);
+    if (!sync) return rc;
     int h[2] = {0, 0};
-    hipError_t e = hipMemcpy(h, status, sizeof(h), hipMemcpyDeviceToHost);
+    hipError_t e = hipMemcpy(h, sync + kStatusOff, sizeof(h), hipMemcpyDeviceToHost);
     if (e != hipSuccess) return (int)e;
     if (barrier_timeouts) *barrier_timeouts = h[0];
     if (missing_experts) *missing_experts = h[1];
@@ -353,10 +653,11 @@ extern "C" int naiwa_stack_status(int* barrier_timeouts, int* missing_experts) {
 
 int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows, int H, int E, int k,
                       int mode, int act, uint32_t* ids_out, float* w_out, int64_t stream) {
-    if (rows > kMaxRows || k > kMaxK || E > kMaxE) return NAIWA_E_UNSUPPORTED;
+    if (rows > kMaxRows || k > kMaxK || E > kMaxE || n_layers > kMaxLayers) return NAIWA_E_UNSUPPORTED;
     if (H % kChunk || (ids_out == nullptr) != (w_out == nullptr)) return NAIWA_E_INVALID;
     if (mode < 0 || mode > 2 || (act != NAIWA_ACT_SILU && act != NAIWA_ACT_GELU_PYTORCH_TANH))
         return NAIWA_E_UNSUPPORTED;
+    if (((uintptr_t)x & 15) != 0) return NAIWA_E_INVALID;
     const naiwa_layer& L0 = layers[0];
     const int I = L0.gate.n;
     for (int l = 0; l < n_layers; ++l) {
@@ -385,14 +686,33 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     if (lds > 96 * 1024) return NAIWA_E_UNSUPPORTED;
 
     hipStream_t st = (hipStream_t)stream;
-    int rc = 0;
-    // scratch: h [kMaxPairs * I] f32 | logits [n_layers * rows * E] int64
+    int rc = 0, dev = 0, cus = 0, khz = 0;
+    if ((rc = naiwa_hip_rc(hipGetDevice(&dev)))) return rc;
+    if ((rc = naiwa_hip_rc(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)))) return rc;
+    if ((rc = naiwa_hip_rc(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev)))) return rc;
+    int per_cu = 0;
+    if (fg == NAIWA_Q4_K && fd == NAIWA_Q4_K) rc = occupancy<NAIWA_Q4_K, NAIWA_Q4_K>(lds, &per_cu);
+    else if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0) rc = occupancy<NAIWA_Q4_K, NAIWA_Q8_0>(lds, &per_cu);
+    else if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0_ODD) rc = occupancy<NAIWA_Q4_K, NAIWA_Q8_0_ODD>(lds, &per_cu);
+    else if (fg == NAIWA_Q8_0 && fd == NAIWA_Q8_0) rc = occupancy<NAIWA_Q8_0, NAIWA_Q8_0>(lds, &per_cu);
+    else if (fg == NAIWA_Q8_0 && fd == NAIWA_Q8_0_ODD) rc = occupancy<NAIWA_Q8_0, NAIWA_Q8_0_ODD>(lds, &per_cu);
+    else return NAIWA_E_UNSUPPORTED;
+    if (rc) return rc;
+    const int bpc = per_cu < g_fused_blocks_per_cu ? per_cu : g_fused_blocks_per_cu;
+    if (bpc < 1) return NAIWA_E_UNSUPPORTED;
+    const int blocks = cus * bpc;
+    if (blocks < kLeaders || blocks > 4096) return NAIWA_E_UNSUPPORTED;
+
+    // scratch: h [kMaxPairs * I] f32 | part [blocks * rows * E] i64 | logits [rows * E] i64
     const size_t h_bytes = ((size_t)kMaxPairs * I * 4 + 255) & ~size_t(255);
-    const size_t lg_bytes = (size_t)n_layers * rows * E * 8;
-    uint8_t* ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK, h_bytes + lg_bytes, &rc);
+    const size_t part_bytes = ((size_t)blocks * rows * E * 8 + 255) & ~size_t(255);
+    const size_t lg_bytes = ((size_t)rows * E * 8 + 255) & ~size_t(255);
+    uint8_t* ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK, h_bytes + part_bytes + lg_bytes, &rc);
     if (!ws) return rc;
-    int* misc = (int*)naiwa_scratch(NAIWA_SCRATCH_STACK + 1, 4096, &rc);
-    if (!misc) return rc;
+    // sync scratch: status (256 B) | release lines | arrive lines
+    const size_t sync_bytes = 256 + (size_t)(kLeaders + blocks) * kLine * 4;
+    uint8_t* sync = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK + 1, sync_bytes, &rc);
+    if (!sync) return rc;
 
     // layer descriptors on the device (re-uploaded only when they change)
     std::vector<LayerDev> desc(n_layers);
@@ -418,30 +738,13 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
             if (hipMalloc(&g_fused.dev_layers, bytes) != hipSuccess) return NAIWA_E_NOMEM;
             g_fused.cap = bytes;
         }
-        if (g_fused.last.size() != desc.size() ||
-            memcmp(g_fused.last.data(), desc.data(), bytes) != 0) {
+        if (g_fused.last.size() != desc.size() || memcmp(g_fused.last.data(), desc.data(), bytes) != 0) {
             hipError_t e = hipMemcpy(g_fused.dev_layers, desc.data(), bytes, hipMemcpyHostToDevice);
             if (e != hipSuccess) return (int)e;
             g_fused.last = desc;
         }
         dev_layers = g_fused.dev_layers;
     }
-
-    int dev = 0, cus = 0, khz = 0;
-    if ((rc = naiwa_hip_rc(hipGetDevice(&dev)))) return rc;
-    if ((rc = naiwa_hip_rc(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)))) return rc;
-    if ((rc = naiwa_hip_rc(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev)))) return rc;
-    int per_cu = 0;
-    if (fg == NAIWA_Q4_K && fd == NAIWA_Q4_K) rc = occupancy<NAIWA_Q4_K, NAIWA_Q4_K>(lds, &per_cu);
-    else if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0) rc = occupancy<NAIWA_Q4_K, NAIWA_Q8_0>(lds, &per_cu);
-    else if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0_ODD) rc = occupancy<NAIWA_Q4_K, NAIWA_Q8_0_ODD>(lds, &per_cu);
-    else if (fg == NAIWA_Q8_0 && fd == NAIWA_Q8_0) rc = occupancy<NAIWA_Q8_0, NAIWA_Q8_0>(lds, &per_cu);
-    else if (fg == NAIWA_Q8_0 && fd == NAIWA_Q8_0_ODD) rc = occupancy<NAIWA_Q8_0, NAIWA_Q8_0_ODD>(lds, &per_cu);
-    else return NAIWA_E_UNSUPPORTED;
-    if (rc) return rc;
-    const int bpc = per_cu < g_fused_blocks_per_cu ? per_cu : g_fused_blocks_per_cu;
-    if (bpc < 1) return NAIWA_E_UNSUPPORTED;
-    const int blocks = cus * bpc;
 
     Params prm;
     prm.layers = dev_layers;
@@ -455,13 +758,22 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     prm.act = act;
     prm.x = (uint16_t*)x;
     prm.h = (float*)ws;
-    prm.logit = (unsigned long long*)(ws + h_bytes);
-    prm.bar = (unsigned int*)(misc + 16);
-    prm.status = misc;
+    prm.part = (long long*)(ws + h_bytes);
+    prm.logits = (long long*)(ws + h_bytes + part_bytes);
+    prm.status = (int*)(sync + kStatusOff);
+    prm.release = (unsigned*)(sync + 256);
+    prm.arrive = (unsigned*)(sync + 256 + (size_t)kLeaders * kLine * 4);
     prm.ids_out = ids_out;
     prm.w_out = w_out;
     prm.spin_limit = (uint64_t)khz * 2000ull; // 2 s
-    zero_u32<<<1, 64, 0, st>>>((unsigned int*)misc, 32);
+    prm.never = 0;
+    prm.trace = g_trace_enabled ? (unsigned long long*)naiwa_scratch(NAIWA_SCRATCH_STACK + 2,
+                                                                     (size_t)2 * (n_layers + 1) * kTraceSlots * 8, &rc)
+                                : nullptr;
+    if (g_trace_enabled && !prm.trace) return rc;
+    g_trace_layers = n_layers;
+    const int nzero = (int)(sync_bytes / 4);
+    zero_u32<<<(nzero + 255) / 256, 256, 0, st>>>((unsigned int*)sync, nzero);
     if (fg == NAIWA_Q4_K && fd == NAIWA_Q4_K) return launch<NAIWA_Q4_K, NAIWA_Q4_K>(prm, blocks, lds, st);
     if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0) return launch<NAIWA_Q4_K, NAIWA_Q8_0>(prm, blocks, lds, st);
     if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0_ODD) return launch<NAIWA_Q4_K, NAIWA_Q8_0_ODD>(prm, blocks, lds, st);

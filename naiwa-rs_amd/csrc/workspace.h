@@ -21,4 +21,4 @@ struct NaiwaScratch {
 // buffer (with a device sync, since a kernel may still read the old one).
 void* naiwa_scratch(int tag, size_t bytes, int* rc);
 
-enum { NAIWA_SCRATCH_DECODE = 0, NAIWA_SCRATCH_ROUTER = 1, NAIWA_SCRATCH_STACK = 2, NAIWA_SCRATCH_TAGS = 4 };
+enum { NAIWA_SCRATCH_DECODE = 0, NAIWA_SCRATCH_ROUTER = 1, NAIWA_SCRATCH_STACK = 2, NAIWA_SCRATCH_TAGS = 6 };

@@ -93,6 +93,8 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_stack_set_blocks_per_cu": (i32, [i32]),
     "naiwa_stack_status": (i32, [_P(i32), _P(i32)]),
     "naiwa_residual_add_bf16": (i32, [vp, vp, i64, i64]),
+    "naiwa_stack_trace_enable": (i32, [i32]),
+    "naiwa_stack_trace_read": (i32, [_P(u64), i32, _P(i32)]),
 }
 
 

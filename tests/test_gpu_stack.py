@@ -96,7 +96,9 @@ def test_fused_multi_layer_matches_oracle_chain(gpu):
     if np.array_equal(ids, want_ids):
         delta = got - O.from_bf16(x)
         want_delta = O.from_bf16(want_x) - O.from_bf16(x)
-        assert S.max_rel_err(delta, want_delta) < 2 * TOL
+        # each layer's bf16 store may round the other way: one ulp of |x| per layer
+        slack = L * np.abs(got).max() * 2.0 ** -7 / np.abs(want_delta).max()
+        assert S.max_rel_err(delta, want_delta) < TOL + slack
 
 
 def test_fused_is_deterministic(gpu):
