@@ -47,6 +47,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="budget of the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="run one device-to-device copy of MIB MiB before timing (a known-size "
+                         "reference for HBM traffic counters)")
     ap.add_argument("--trace", action="store_true",
                     help="print per-phase times of one fused step (diagnostic, untimed)")
     return ap.parse_args()
@@ -114,6 +117,16 @@ def main() -> int:
     ids = ids_d.download(np.uint32).reshape(L, rows, K)
     ws = w_d.download(np.float32).reshape(L, rows, K)
     assert (ids < E).all() and np.allclose(ws.sum(-1), 1.0, atol=1e-4), "routing output invalid"
+
+    if args.calibrate_copy:
+        nbytes = args.calibrate_copy << 20
+        a, b = nm.DeviceBuffer(nbytes), nm.DeviceBuffer(nbytes)
+        a.zero(stream.handle)
+        stream.sync()
+        lib.naiwa_memcpy_d2d(b.ptr, a.ptr, nbytes, stream.handle)
+        stream.sync()
+        log(f"calibration copy: {nbytes} bytes device to device")
+        del a, b
 
     if args.trace and fused:
         print_trace(nm, lambda: step(0, False), stream, L, info["wall_clock_khz"])

@@ -1,25 +1,28 @@
 // NAIWA_STACK_FUSED: one persistent, cooperatively launched kernel runs a
 // whole decode step through every MoE layer, x <- bf16(x + MoE_l(x)).
 //
-// One block of 256 threads per CU (16 groups of 16 lanes; one wave per SIMD
-// leaves 512 registers per lane), every block resident.  Per layer:
-//   A  route   every block reads the layer's router logits, selects the top-k
-//              in one wave per token and groups the (token, k) pairs by cache
-//              slot -- redundantly and identically in every block;
-//   B  gate/up the (segment, intermediate row) work is dealt out evenly; each
-//              16-lane group issues the 16-byte loads of one gate row and one
-//              up row before the activations are even staged, then writes
-//              h = act(g) * u per pair.  The block also touches the down rows
-//              and next-layer router rows it will need in C, so they are in
-//              its XCD's L2 by then;
+// One block of 256 threads per CU (16 groups of 16 lanes, one wave per SIMD),
+// every block resident.  Per layer:
+//   A  route   every block loads the layer's router logits (and, in the same
+//              burst, the activations it will need), ranks the experts of each
+//              token in parallel, derives the routing weights and groups the
+//              (token, k) pairs by cache slot -- redundantly and identically in
+//              every block, so routing needs no barrier;
+//   B  gate/up the (segment, intermediate row) work is dealt out evenly.  For
+//              Q4_K each lane owns whole 144-byte blocks: lanes 0-7 of a
+//              16-lane group take the gate row, lanes 8-15 the up row, so a
+//              block's scales are decoded once per 256 weights.  Every lane
+//              issues its first row's loads before the activations are staged.
+//              The block then touches the down rows and next-layer router
+//              columns it will need in C, so they sit in its XCD's L2;
 //   -- all-gather barrier --
-//   C  down    each block owns 8-feature chunks of the output: it stages the h
+//   C  down    each block owns 8-feature output chunks: it stages the h
 //              vectors, dots every (feature, pair), adds the pairs of each
 //              token in ascending slot order (no atomics), applies the
 //              residual, stores bf16 x, and stores its int64 partial sums of
 //              the next layer's router logits;
-//   -- reduce barrier: 8 leader blocks add the partials of every block and
-//      publish the logits --
+//   -- reduce barrier: 32 leader blocks add every block's partials for their
+//      experts and publish the logits --
 //
 // Cross-block data (h, x, router partials, logits, flags) moves with
 // device-coherent relaxed atomic loads and stores (sc1: past the per-XCD L2s),
@@ -32,6 +35,7 @@
 // Integer addition is associative, so the logits (and the top-k) are bit-
 // identical to the CPU oracle's however the chunks are distributed.
 #include <mutex>
+#include <stdlib.h>
 #include <string.h>
 #include <vector>
 
@@ -48,12 +52,14 @@ constexpr int kMaxRows = 8;               // tokens per step served by this kern
 constexpr int kMaxK = 8;                  // routed experts per token
 constexpr int kMaxPairs = kMaxRows * kMaxK;
 constexpr int kMaxE = 256;
-constexpr int kLeaders = 8;               // blocks that reduce the router partials
+constexpr int kLeaders = 32;              // blocks that reduce the router partials
 constexpr int kChunk = NAIWA_ROUTER_CHUNK; // output features per phase-C chunk
 constexpr int kCPairs = 16;               // h vectors staged per phase-C pass
 constexpr int kLine = 64;                 // u32 per 256-byte flag line
 constexpr int kPartPerThread = (kMaxRows * kMaxE + kThreads - 1) / kThreads;
 constexpr int kTraceSlots = 16;
+constexpr int kMaxLayers = 128;           // layer descriptors kept in LDS
+constexpr int kXPre = 8;                  // activation loads per thread issued with the logits
 
 struct LayerDev {
     const float* router;
@@ -96,18 +102,16 @@ struct Smem {
     float pair_w[kMaxPairs];
     uint32_t sorted[kMaxPairs];    // valid pairs in (slot, p) order
     uint32_t seg_begin[kMaxPairs + 1];
-    int nseg;
     uint32_t seg_slot[kMaxPairs];
+    int nseg;
     float lg[kMaxRows][kMaxE];
     uint32_t top_ids[kMaxRows][kMaxK];
-    float top_w[kMaxRows][kMaxK];
-    int rank_tmp[kMaxE];
-    float ex_tmp[kMaxE];
+    float top_ex[kMaxRows][kMaxK];
     float partial[kChunk][kMaxPairs];
     float xnew[kMaxRows][kChunk];
+    float xown[kMaxRows][kChunk];
+    long long lsum[kThreads / 16];
 };
-
-constexpr int kMaxLayers = 128;           // layer descriptors kept in LDS
 
 __device__ __forceinline__ unsigned ld_flag(const unsigned* f) {
     return __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -133,12 +137,19 @@ __device__ __forceinline__ uint32_t ld_coh(const uint32_t* p) {
 // This wave's stores have completed (reached the device-coherent level).
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Wait for *f >= target.  Bounded: after spin_limit ticks the wait counts a
+// timeout and gives up; once any wait has timed out (status[0] != 0) every
+// later wait returns at once, so a grid that is not fully resident drains
+// quickly with an error instead of waiting out every barrier.
 __device__ inline void spin_ge(const unsigned* f, unsigned target, const Params& p, bool sleep) {
     const uint64_t t0 = wall_clock64();
-    while (ld_flag(f) < target) {
-        if (wall_clock64() - t0 > p.spin_limit) {
-            atomicAdd(&p.status[0], 1);
-            return;
+    for (unsigned n = 0; ld_flag(f) < target; ++n) {
+        if ((n & 63) == 63) {
+            if (__hip_atomic_load(&p.status[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
+            if (wall_clock64() - t0 > p.spin_limit) {
+                atomicAdd(&p.status[0], 1);
+                return;
+            }
         }
         if (sleep) __builtin_amdgcn_s_sleep(1);
     }
@@ -153,48 +164,111 @@ __device__ inline void barrier_all(const Params& p, unsigned epoch) {
     __syncthreads();
 }
 
+// Sum over aligned groups of W lanes of an exact int64.
+template <int W>
+__device__ __forceinline__ long long group_sum_i64(long long v) {
+    if (W >= 2) v += naiwa_dpp_i64<0xB1>(v);
+    if (W >= 4) v += naiwa_dpp_i64<0x4E>(v);
+    if (W >= 8) v += naiwa_dpp_i64<0x141>(v);
+    if (W >= 16) v += naiwa_dpp_i64<0x140>(v);
+#pragma unroll
+    for (int m = 16; m < W; m <<= 1) v += __shfl_xor(v, m, W);
+    return v;
+}
+
 // Barrier that also publishes the logits: leader L waits for every block,
 // adds all blocks' partials of its experts and raises its release flag; the
 // others wait for the leaders only.
-__device__ inline void barrier_reduce(const Params& p, Smem& sm, unsigned epoch) {
+template <int LPI>
+__device__ inline void leader_reduce(const Params& p, int items, int e0, int ne) {
+    const int tid = threadIdx.x, G = gridDim.x;
+    const int it = tid / LPI, li = tid % LPI;
+    long long s = 0;
+    int t = 0, e = 0;
+    if (it < items) {
+        t = it / ne;
+        e = e0 + it % ne;
+        const long long* src = p.part + (size_t)t * p.E + e;
+        const size_t bstride = (size_t)p.rows * p.E;
+#pragma unroll 1
+        for (int b0 = li; b0 < G; b0 += 8 * LPI) {
+            long long v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int b = b0 + j * LPI;
+                v[j] = b < G ? ld_coh(src + (size_t)b * bstride) : 0;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) s += v[j];
+        }
+    }
+    s = group_sum_i64<LPI>(s);
+    if (it < items && li == 0) st_coh(&p.logits[(size_t)t * p.E + e], s);
+}
+
+__device__ inline void barrier_reduce(const Params& p, unsigned epoch) {
     const int tid = threadIdx.x, bid = blockIdx.x, G = gridDim.x;
     wait_stores();
     __syncthreads();
     if (tid == 0) st_flag(&p.arrive[bid * kLine], epoch);
-    const int epl = (p.E + kLeaders - 1) / kLeaders;
-    if (bid < kLeaders) {
+    const int nlead = min(kLeaders, G);
+    const int epl = (p.E + nlead - 1) / nlead;
+    if (bid < nlead) {
         for (int i = tid; i < G; i += kThreads) spin_ge(&p.arrive[i * kLine], epoch, p, false);
         __syncthreads();
         const int e0 = bid * epl;
         const int ne = max(0, min(epl, p.E - e0));
         const int items = p.rows * ne;
-        const int grp = tid / NAIWA_GROUP, lr = tid % NAIWA_GROUP;
-        const size_t bstride = (size_t)p.rows * p.E;
-        // one 16-lane group per (token, expert); lane lr adds blocks lr, lr + 16, ...
-        for (int it = grp; it < items; it += kGroups) {
-            const int t = it / ne, e = e0 + it % ne;
-            const long long* src = p.part + (size_t)t * p.E + e;
-            long long s = 0;
+        if (items > 0) {
+            if (items <= 4) leader_reduce<64>(p, items, e0, ne);
+            else if (items <= 8) leader_reduce<32>(p, items, e0, ne);
+            else if (items <= 16) leader_reduce<16>(p, items, e0, ne);
+            else {
 #pragma unroll 1
-            for (int b0 = lr; b0 < G; b0 += 8 * NAIWA_GROUP) {
-                long long v[8];
+                for (int i0 = 0; i0 < items; i0 += 16) {
+                    // 16 items per pass, 16 lanes each
+                    const int n = min(16, items - i0);
+                    const int it = tid / 16, li = tid % 16;
+                    long long s = 0;
+                    int t = 0, e = 0;
+                    if (it < n) {
+                        t = (i0 + it) / ne;
+                        e = e0 + (i0 + it) % ne;
+                        const long long* src = p.part + (size_t)t * p.E + e;
+                        const size_t bstride = (size_t)p.rows * p.E;
+#pragma unroll 1
+                        for (int b0 = li; b0 < G; b0 += 128) {
+                            long long v[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int b = b0 + j * NAIWA_GROUP;
-                    v[j] = b < G ? ld_coh(src + (size_t)b * bstride) : 0;
+                            for (int j = 0; j < 8; ++j) {
+                                const int b = b0 + j * 16;
+                                v[j] = b < G ? ld_coh(src + (size_t)b * bstride) : 0;
+                            }
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) s += v[j];
+                        }
+                    }
+                    s = group_sum_i64<16>(s);
+                    if (it < n && li == 0) st_coh(&p.logits[(size_t)t * p.E + e], s);
                 }
-#pragma unroll
-                for (int j = 0; j < 8; ++j) s += v[j];
             }
-            s = naiwa_group_sum16_i64(s);
-            if (lr == 0) st_coh(&p.logits[(size_t)t * p.E + e], s);
         }
         wait_stores();
         __syncthreads();
         if (tid == 0) st_flag(&p.release[bid * kLine], epoch);
     }
-    if (tid < kLeaders) spin_ge(&p.release[tid * kLine], epoch, p, true);
+    if (tid < nlead) spin_ge(&p.release[tid * kLine], epoch, p, true);
     __syncthreads();
+}
+
+// The output-feature chunk handled at position p (= block + j * blocks).
+// Blocks are dealt to the XCDs round-robin, so position p runs on XCD p % 8;
+// this mapping gives the 4 chunks that share a 128-byte line of every router
+// row (4 x 8 f32) to blocks of one XCD, which then fetches the line once.
+__device__ __forceinline__ int chunk_at(int p, int nchunks) {
+    if (nchunks % 32) return p;
+    const int x = p & 7, r = p >> 3;
+    return (((r >> 2) << 3) + x) * 4 + (r & 3);
 }
 
 // Router partials of this block's chunks for (token, expert) items; the
@@ -219,12 +293,108 @@ __device__ inline void router_store_partials(const Params& p, const long long* a
     }
 }
 
-// One gate/up row of a segment for every token of the segment: h = act(g) * u.
-// With `preloaded`, the first batch of codes is already in fg/fu.
+// ---------------------------------------------------------------------------
+// Q4_K gate/up with one 144-byte block per lane
+// ---------------------------------------------------------------------------
+
+// Dot of one Q4_K block (9 x 16 bytes in registers) with its 256 staged
+// activations: words = the block's 128 bf16 perm words, sums = its 16 sums of 16.
+__device__ __forceinline__ float q4k_block_dot(const uint4* blk, const uint32_t* words, const float* sums) {
+    const uint4 hd = blk[0];
+    const float d = naiwa_f16_to_f32(hd.x & 0xffffu);
+    const float dmin = naiwa_f16_to_f32(hd.x >> 16);
+    // the 8 six-bit scales and mins, one per byte (ggml get_scale_min_k4)
+    const uint32_t sc_lo = hd.y & 0x3F3F3F3Fu;                                   // sc0..sc3
+    const uint32_t m_lo = hd.z & 0x3F3F3F3Fu;                                    // m0..m3
+    const uint32_t sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);   // sc4..sc7
+    const uint32_t m_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u); // m4..m7
+    float total = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint4 qa = blk[1 + 2 * c], qb = blk[2 + 2 * c];
+        const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        const uint4* xl = reinterpret_cast<const uint4*>(words + 32 * c);
+        const uint4* xh = reinterpret_cast<const uint4*>(words + 32 * c + 16);
+        float alo = 0.0f, ahi = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint4 lo = xl[i], hi = xh[i];
+            const uint32_t x_lo[4] = {lo.x, lo.y, lo.z, lo.w};
+            const uint32_t x_hi[4] = {hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t q = w[2 * i + h];
+                alo = naiwa_dot2_bf16((q & 0x000F000Fu) | 0x43004300u, x_lo[2 * h], alo);
+                alo = naiwa_dot2_bf16(((q >> 8) & 0x000F000Fu) | 0x43004300u, x_lo[2 * h + 1], alo);
+                ahi = naiwa_dot2_bf16(((q >> 4) & 0x000F000Fu) | 0x43004300u, x_hi[2 * h], ahi);
+                ahi = naiwa_dot2_bf16(((q >> 12) & 0x000F000Fu) | 0x43004300u, x_hi[2 * h + 1], ahi);
+            }
+        }
+        const float4 sv = reinterpret_cast<const float4*>(sums)[c];
+        const float slo = sv.x + sv.y, shi = sv.z + sv.w;
+        const uint32_t scw = c < 2 ? sc_lo : sc_hi, mw = c < 2 ? m_lo : m_hi;
+        const int sh = (c & 1) * 16;
+        const float sc0 = (float)((scw >> sh) & 0xFFu), sc1 = (float)((scw >> (sh + 8)) & 0xFFu);
+        const float m0 = (float)((mw >> sh) & 0xFFu), m1 = (float)((mw >> (sh + 8)) & 0xFFu);
+        total += d * (sc0 * (alo - 128.0f * slo) + sc1 * (ahi - 128.0f * shi)) - dmin * (m0 * slo + m1 * shi);
+        // keep the scheduler from hoisting every chunk's LDS reads at once
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return total;
+}
+
+struct Q4Row {
+    uint4 blk[9];
+};
+
+// Loads of the Q4_K block this lane owns in the first 8 blocks of row r of the
+// slot: lanes 0-7 the gate row, lanes 8-15 the up row, block lr % 8 + 8 * grp8.
+__device__ __forceinline__ const uint8_t* q4_row_ptr(const LayerDev& L, uint32_t slot, int r, int64_t rb, int lr) {
+    return (lr >= 8 ? L.up + (int64_t)slot * L.up_stride : L.gate + (int64_t)slot * L.gate_stride) + (int64_t)r * rb;
+}
+
+__device__ __forceinline__ void q4_block_load(const uint8_t* row, int b, int nb, Q4Row& f) {
+    if (b < nb) {
+        const uint4* src = reinterpret_cast<const uint4*>(row + b * NAIWA_Q4_K_BYTES);
+#pragma unroll
+        for (int j = 0; j < 9; ++j) f.blk[j] = src[j];
+    }
+}
+
+// h of every token of the segment for one intermediate row.  f holds this
+// lane's block of the first 8; rows longer than 8 blocks load the rest here.
+__device__ inline void q4_row_compute(const Params& p, const Smem& sm, const LayerDev& L, const uint8_t* dyn,
+                                      int xstage, int q, int64_t rb, int nb, int lr, const Q4Row& f) {
+    const int I = p.I, H = p.H, k = p.k;
+    const int s = q / I, r = q % I;
+    const int b = (int)sm.seg_begin[s], e = (int)sm.seg_begin[s + 1];
+    const int b0 = lr & 7;
+    for (int tt = b; tt < e; ++tt) {
+        const int t = (int)sm.sorted[tt] / k;
+        const uint32_t* words = (const uint32_t*)(dyn + t * xstage);
+        const float* sums = (const float*)(words + H / 2);
+        float acc = b0 < nb ? q4k_block_dot(f.blk, words + b0 * 128, sums + b0 * 16) : 0.0f;
+        if (nb > 8) {
+            const uint8_t* row = q4_row_ptr(L, sm.seg_slot[s], r, rb, lr);
+#pragma unroll 1
+            for (int bb = b0 + 8; bb < nb; bb += 8) {
+                Q4Row g;
+                q4_block_load(row, bb, nb, g);
+                acc += q4k_block_dot(g.blk, words + bb * 128, sums + bb * 16);
+            }
+        }
+        acc = naiwa_group_sum<8>(acc);                 // lanes 0-7: gate . x, lanes 8-15: up . x
+        const float uv = naiwa_dpp<0x128>(acc);        // row_ror:8 -- lane 0 receives lane 8
+        if (lr == 0) st_coh(&p.h[(size_t)sm.sorted[tt] * I + r], naiwa_act(p.act, acc) * uv);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Q8_0 gate/up with 16 lanes per row pair (units of two blocks)
+// ---------------------------------------------------------------------------
 template <int DG>
-__device__ inline void gate_up_row(const Params& p, const Smem& sm, const LayerDev& L, const uint8_t* dyn,
-                                   int q, int xstage, int64_t rb, int nu, int lr,
-                                   typename Fmt<DG>::Frag* fg, typename Fmt<DG>::Frag* fu, bool preloaded) {
+__device__ inline void unit_row(const Params& p, const Smem& sm, const LayerDev& L, const uint8_t* dyn,
+                                int q, int xstage, int64_t rb, int nu, int lr) {
     constexpr int UM = Umax<DG>::v;
     const int I = p.I, H = p.H, k = p.k;
     const int s = q / I, r = q % I;
@@ -232,24 +402,19 @@ __device__ inline void gate_up_row(const Params& p, const Smem& sm, const LayerD
     const uint8_t* grow = L.gate + (int64_t)slot * L.gate_stride + (int64_t)r * rb;
     const uint8_t* urow = L.up + (int64_t)slot * L.up_stride + (int64_t)r * rb;
     const int b = (int)sm.seg_begin[s], e = (int)sm.seg_begin[s + 1];
-    const int nbatch = (nu + NAIWA_GROUP * UM - 1) / (NAIWA_GROUP * UM);
     for (int tt = b; tt < e; ++tt) {
         const int t = (int)sm.sorted[tt] / k;
         const uint32_t* words = (const uint32_t*)(dyn + t * xstage);
         const float* sums = (const float*)(words + H / 2);
         float ag = 0.0f, au = 0.0f;
-        for (int bt = 0; bt < nbatch; ++bt) {
-            const int base = lr + bt * NAIWA_GROUP * UM;
-            // batch 0 stays in registers across tokens when it is the only batch
-            const bool have = bt == 0 && ((tt == b && preloaded) || (tt > b && nbatch == 1));
-            if (!have) {
+        for (int base = lr; base < nu; base += NAIWA_GROUP * UM) {
+            typename Fmt<DG>::Frag fg[UM], fu[UM];
 #pragma unroll
-                for (int i = 0; i < UM; ++i) {
-                    const int u = base + NAIWA_GROUP * i;
-                    if (u < nu) {
-                        fg[i] = Fmt<DG>::load(grow, u);
-                        fu[i] = Fmt<DG>::load(urow, u);
-                    }
+            for (int i = 0; i < UM; ++i) {
+                const int u = base + NAIWA_GROUP * i;
+                if (u < nu) {
+                    fg[i] = Fmt<DG>::load(grow, u);
+                    fu[i] = Fmt<DG>::load(urow, u);
                 }
             }
 #pragma unroll
@@ -267,22 +432,37 @@ __device__ inline void gate_up_row(const Params& p, const Smem& sm, const LayerD
     }
 }
 
-// Issue the loads of the first batch of a row's gate and up codes.
+// Convert prefetched activation groups (4 bf16 each) into the staged layout.
 template <int DG>
-__device__ inline void gate_up_preload(const Params& p, const Smem& sm, const LayerDev& L, int q,
-                                       int64_t rb, int nu, int lr, typename Fmt<DG>::Frag* fg,
-                                       typename Fmt<DG>::Frag* fu) {
-    constexpr int UM = Umax<DG>::v;
-    const int s = q / p.I, r = q % p.I;
-    const uint32_t slot = sm.seg_slot[s];
-    const uint8_t* grow = L.gate + (int64_t)slot * L.gate_stride + (int64_t)r * rb;
-    const uint8_t* urow = L.up + (int64_t)slot * L.up_stride + (int64_t)r * rb;
+__device__ inline void convert_x_groups(const uint2* xr, int ngroups_total, int gpt_h, uint8_t* dyn,
+                                        int xstage, int H) {
+    constexpr int span = Fmt<DG>::kSumSpan;
+    constexpr int gpg = span / 4;
 #pragma unroll
-    for (int i = 0; i < UM; ++i) {
-        const int u = lr + NAIWA_GROUP * i;
-        if (u < nu) {
-            fg[i] = Fmt<DG>::load(grow, u);
-            fu[i] = Fmt<DG>::load(urow, u);
+    for (int j = 0; j < kXPre; ++j) {
+        const int g = threadIdx.x + j * kThreads;
+        const bool in = g < ngroups_total;
+        float part = 0.0f;
+        if (in) {
+            const int t = g / gpt_h, gg = g % gpt_h;
+            uint32_t* words = (uint32_t*)(dyn + t * xstage);
+            float v[4] = {naiwa_bf16_to_f32(xr[j].x & 0xffffu), naiwa_bf16_to_f32(xr[j].x >> 16),
+                          naiwa_bf16_to_f32(xr[j].y & 0xffffu), naiwa_bf16_to_f32(xr[j].y >> 16)};
+            uint32_t hh[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                hh[i] = Fmt<DG>::to16(v[i]);
+                v[i] = Fmt<DG>::from16(hh[i]);
+            }
+            words[2 * gg] = hh[0] | (hh[2] << 16);
+            words[2 * gg + 1] = hh[1] | (hh[3] << 16);
+            part = (v[0] + v[1]) + (v[2] + v[3]);
+        }
+        part = naiwa_group_sum<gpg>(part);
+        if (in && (g % gpg) == 0) {
+            const int t = g / gpt_h, gg = g % gpt_h;
+            float* sums = (float*)((uint32_t*)(dyn + t * xstage) + H / 2);
+            sums[gg / gpg] = part;
         }
     }
 }
@@ -303,8 +483,9 @@ stack_kernel(Params p) {
     const int nchunks = H / kChunk;
     const int64_t rb = naiwa_row_bytes(DG == NAIWA_Q8_0_ODD ? NAIWA_Q8_0 : DG, H);
     const int64_t drb = naiwa_row_bytes(DD == NAIWA_Q8_0_ODD ? NAIWA_Q8_0 : DD, I);
+    const int nb = H / NAIWA_QK_K;            // Q4_K blocks per gate/up row
     const int nu = Fmt<DG>::units(H);
-    constexpr int UM = Umax<DG>::v;
+    const int gpt_h = H / 4;                  // 4-value groups per token
     unsigned epoch = 0;
     uint32_t touch = 0;
 
@@ -318,7 +499,8 @@ stack_kernel(Params p) {
         long long acc[kPartPerThread];
 #pragma unroll
         for (int j = 0; j < kPartPerThread; ++j) acc[j] = 0;
-        for (int c = bid; c < nchunks; c += G) {
+        for (int cp = bid; cp < nchunks; cp += G) {
+            const int c = chunk_at(cp, nchunks);
             __syncthreads();
             if (tid < rows * kChunk) {
                 const int t = tid / kChunk, i = tid % kChunk;
@@ -329,55 +511,97 @@ stack_kernel(Params p) {
         }
         router_store_partials(p, acc);
         mark(p, p.n_layers, 1);
-        barrier_reduce(p, sm, ++epoch);
+        barrier_reduce(p, ++epoch);
         mark(p, p.n_layers, 2);
     }
 
     for (int l = 0; l < p.n_layers; ++l) {
         const LayerDev L = layers_lds[l];
         // ---- A: route (every block, identically) ----
-        {
-            const int n = rows * E;
-#pragma unroll 1
-            for (int i0 = tid; i0 < n; i0 += 8 * kThreads) {
-                long long v[8];
+        // one burst: the logits and (up to kXPre groups per thread) the activations
+        long long lgv[kPartPerThread];
+        uint2 xr[kXPre];
+        const int nlog = rows * E, ngroups = rows * gpt_h;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int i = i0 + j * kThreads;
-                    v[j] = i < n ? ld_coh(&p.logits[i]) : 0;
-                }
+        for (int j = 0; j < kPartPerThread; ++j) {
+            const int i = tid + j * kThreads;
+            lgv[j] = i < nlog ? ld_coh(&p.logits[i]) : 0;
+        }
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int i = i0 + j * kThreads;
-                    if (i < n) sm.lg[i / E][i % E] = naiwa_router_fix_to_f32(v[j]);
-                }
-            }
+        for (int j = 0; j < kXPre; ++j) {
+            const int g = tid + j * kThreads;
+            xr[j] = g < ngroups ? naiwa_ld8<true>(p.x + (size_t)(g / gpt_h) * H + 4 * (g % gpt_h))
+                                : make_uint2(0u, 0u);
+        }
+#pragma unroll
+        for (int j = 0; j < kPartPerThread; ++j) {
+            const int i = tid + j * kThreads;
+            if (i < nlog) sm.lg[i / E][i % E] = naiwa_router_fix_to_f32(lgv[j]);
+        }
+        if (E & 3) {
+            // the ranking reads whole float4s: pad each row with -inf, which
+            // neither beats nor ties a finite logit
+            const int pad = 4 - (E & 3);
+            if (tid < rows * pad) sm.lg[tid / pad][E + tid % pad] = -INFINITY;
         }
         __syncthreads();
         mark(p, l, 0);
-        for (int t = 0; t < rows; ++t)
-            naiwa_block_topk<kThreads>(sm.lg[t], E, k, p.mode, sm.top_ids[t], sm.top_w[t], sm.rank_tmp, sm.ex_tmp);
-        if (tid < npairs) {
-            const int t = tid / k, j = tid % k;
-            const uint32_t e = sm.top_ids[t][j];
-            const int32_t s = L.slot_of ? L.slot_of[e] : (int32_t)e;
-            const bool ok = s >= 0 && s < L.slots;
-            sm.pair_slot[tid] = ok ? (uint32_t)s : 0u;
-            sm.pair_w[tid] = ok ? sm.top_w[t][j] : 0.0f;
-            if (!ok && bid == 0) atomicAdd(&p.status[1], 1);
-            if (bid == 0 && p.ids_out) {
-                p.ids_out[(size_t)l * npairs + tid] = e;
-                p.w_out[(size_t)l * npairs + tid] = sm.top_w[t][j];
+        // rank of every (token, expert): ties to the lower id (top_k_ids order)
+        for (int t = 0; t < rows; ++t) {
+            for (int e = tid; e < E; e += kThreads) {
+                const float me = sm.lg[t][e];
+                int rank = 0;
+                const float4* lv = reinterpret_cast<const float4*>(sm.lg[t]);
+#pragma unroll 4
+                for (int o4 = 0; o4 < (E + 3) / 4; ++o4) {
+                    const float4 v = lv[o4];
+                    const int o = 4 * o4;
+                    rank += (v.x > me) | ((v.x == me) & (o < e));
+                    rank += (v.y > me) | ((v.y == me) & (o + 1 < e));
+                    rank += (v.z > me) | ((v.z == me) & (o + 2 < e));
+                    rank += (v.w > me) | ((v.w == me) & (o + 3 < e));
+                }
+                if (rank < k) {
+                    sm.top_ids[t][rank] = (uint32_t)e;
+                    sm.top_ex[t][rank] = me;
+                }
             }
         }
         __syncthreads();
         mark(p, l, 1);
-        // group the valid pairs by slot (ascending slot, then pair index):
-        // one wave, one pair per lane, ranks and segment starts by counting
         if (wave == 0) {
+            // weights (rank-order sums, the oracle's order), slot lookup, and the
+            // grouping of valid pairs by slot: one pair per lane
             const int q = lane;
-            const bool valid = q < npairs && sm.pair_w[q] != 0.0f;
-            const uint32_t sq = valid ? sm.pair_slot[q] : 0u;
+            const bool inp = q < npairs;
+            const int t = inp ? q / k : 0, j = inp ? q % k : 0;
+            float w = 0.0f;
+            uint32_t e = 0;
+            if (inp) {
+                const float mx = sm.top_ex[t][0];
+                float denom = 0.0f;
+                if (p.mode == NAIWA_ROUTE_SOFTMAX_TOPK) {
+                    for (int o = 0; o < E; ++o) denom += expf(sm.lg[t][o] - mx);
+                } else {
+                    for (int o = 0; o < k; ++o) denom += expf(sm.top_ex[t][o] - mx);
+                }
+                w = expf(sm.top_ex[t][j] - mx) / denom;
+                e = sm.top_ids[t][j];
+            }
+            const int32_t s = inp ? (L.slot_of ? L.slot_of[e] : (int32_t)e) : -1;
+            const bool ok = inp && s >= 0 && s < L.slots;
+            if (inp && !ok && bid == 0) atomicAdd(&p.status[1], 1);
+            if (inp && bid == 0 && p.ids_out) {
+                p.ids_out[(size_t)l * npairs + q] = e;
+                p.w_out[(size_t)l * npairs + q] = w;
+            }
+            const bool valid = ok && w != 0.0f;
+            const uint32_t sq = valid ? (uint32_t)s : 0u;
+            sm.pair_slot[q] = sq;
+            sm.pair_w[q] = valid ? w : 0.0f;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             int rank = 0;
             bool start = valid;
             for (int o = 0; o < npairs; ++o) {
@@ -391,8 +615,7 @@ stack_kernel(Params p) {
             const unsigned long long starts = __ballot(start);
             const unsigned long long valids = __ballot(valid);
             int segidx = 0;
-            for (int o = 0; o < npairs; ++o)
-                segidx += ((starts >> o) & 1ull) && sm.pair_slot[o] < sq;
+            for (int o = 0; o < npairs; ++o) segidx += ((starts >> o) & 1ull) && sm.pair_slot[o] < sq;
             if (valid) sm.sorted[rank] = (uint32_t)q;
             if (start) {
                 sm.seg_begin[segidx] = (uint32_t)rank;
@@ -404,6 +627,49 @@ stack_kernel(Params p) {
                 sm.nseg = ns;
             }
         }
+        // every thread converts the activation groups it loaded with the logits
+        convert_x_groups<DG>(xr, min(ngroups, kXPre * kThreads), gpt_h, dyn, xstage, H);
+        if (ngroups > kXPre * kThreads) {
+            // tokens beyond the first burst
+            for (int g0 = kXPre * kThreads; g0 < ngroups; g0 += kXPre * kThreads) {
+                uint2 xr2[kXPre];
+#pragma unroll
+                for (int j = 0; j < kXPre; ++j) {
+                    const int g = g0 + tid + j * kThreads;
+                    xr2[j] = g < ngroups ? naiwa_ld8<true>(p.x + (size_t)(g / gpt_h) * H + 4 * (g % gpt_h))
+                                         : make_uint2(0u, 0u);
+                }
+                // shift the group numbering: convert_x_groups counts from 0
+                constexpr int span = Fmt<DG>::kSumSpan;
+                constexpr int gpg = span / 4;
+#pragma unroll
+                for (int j = 0; j < kXPre; ++j) {
+                    const int g = g0 + tid + j * kThreads;
+                    const bool in = g < ngroups;
+                    float part = 0.0f;
+                    if (in) {
+                        const int t = g / gpt_h, gg = g % gpt_h;
+                        uint32_t* words = (uint32_t*)(dyn + t * xstage);
+                        float v[4] = {naiwa_bf16_to_f32(xr2[j].x & 0xffffu), naiwa_bf16_to_f32(xr2[j].x >> 16),
+                                      naiwa_bf16_to_f32(xr2[j].y & 0xffffu), naiwa_bf16_to_f32(xr2[j].y >> 16)};
+                        uint32_t hh[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            hh[i] = Fmt<DG>::to16(v[i]);
+                            v[i] = Fmt<DG>::from16(hh[i]);
+                        }
+                        words[2 * gg] = hh[0] | (hh[2] << 16);
+                        words[2 * gg + 1] = hh[1] | (hh[3] << 16);
+                        part = (v[0] + v[1]) + (v[2] + v[3]);
+                    }
+                    part = naiwa_group_sum<gpg>(part);
+                    if (in && (g % gpg) == 0) {
+                        const int t = g / gpt_h, gg = g % gpt_h;
+                        ((float*)((uint32_t*)(dyn + t * xstage) + H / 2))[gg / gpg] = part;
+                    }
+                }
+            }
+        }
         __syncthreads();
         const int nseg = sm.nseg;
         const int nvalid = (int)sm.seg_begin[nseg];
@@ -413,60 +679,56 @@ stack_kernel(Params p) {
         const int total = nseg * I;
         const int per = (total + G - 1) / G;
         const int q0 = bid * per, q1 = min(total, q0 + per);
-        // this group's first two rows: issue their loads before staging anything
-        typename Fmt<DG>::Frag fg0[UM], fu0[UM], fg1[UM], fu1[UM];
-        const int qa = q0 + grp, qb = q0 + grp + kGroups;
-        if (qa < q1) gate_up_preload<DG>(p, sm, L, qa, rb, nu, lr, fg0, fu0);
-        if (qb < q1) gate_up_preload<DG>(p, sm, L, qb, rb, nu, lr, fg1, fu1);
-        mark(p, l, 3);
-        // touch the down rows of this block's C chunks (the 16-byte pieces that
-        // cover them; each slot is 16-byte aligned and padded to 16) and the next
-        // router's columns, so C finds them in this XCD's L2.  Eight loads are
-        // in flight per thread before any result is used.
-        {
-            const float* Wn = l + 1 < p.n_layers ? layers_lds[l + 1].router : nullptr;
-            for (int c = bid; c < nchunks; c += G) {
+        if constexpr (DG == NAIWA_Q4_K) {
+            Q4Row f;
+            const int qa = q0 + grp;
+            if (qa < q1) q4_block_load(q4_row_ptr(L, sm.seg_slot[qa / I], qa % I, rb, lr), lr & 7, nb, f);
+            mark(p, l, 3);
+            // touch the down rows of this block's C chunks and the next router's
+            // columns (loads issued now, consumed after the barrier)
+            uint32_t tv[8];
+            {
+                // the rows of this block's first chunk c span [c*8*drb, (c+1)*8*drb):
+                // one dword of every 16-byte piece that starts inside the span
+                // (rows are 4-byte multiples, so each dword lies inside it)
+                const int c = chunk_at(bid < nchunks ? bid : 0, nchunks);
                 const int64_t lo = (int64_t)c * kChunk * drb, hi = lo + kChunk * drb;
                 const int64_t a0 = lo & ~int64_t(15);
                 const int per_seg = (int)((hi - a0 + 15) / 16);
-                const int npieces = nseg * per_seg;
-#pragma unroll 1
-                for (int i0 = tid; i0 < npieces; i0 += 8 * kThreads) {
-                    uint32_t v[8];
+                const int npieces = bid < nchunks ? nseg * per_seg : 0;
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const int i = min(i0 + j * kThreads, npieces - 1);
-                        const int s = i / per_seg, piece = i % per_seg;
-                        const uint32_t slot = sm.seg_slot[s];
-                        v[j] = reinterpret_cast<const uint4*>(L.down + (int64_t)slot * L.down_stride + a0 + 16 * piece)->x;
+                for (int j = 0; j < 8; ++j) {
+                    const int i = tid + j * kThreads;
+                    tv[j] = 0;
+                    if (i < npieces) {
+                        const int sg = i / per_seg, piece = i % per_seg;
+                        const int64_t off = piece == 0 ? lo : a0 + 16 * (int64_t)piece;
+                        tv[j] = *reinterpret_cast<const uint32_t*>(L.down + (int64_t)sm.seg_slot[sg] * L.down_stride + off);
                     }
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) touch ^= v[j];
                 }
-                if (Wn)
-                    for (int e = tid; e < E; e += kThreads) touch ^= __float_as_uint(Wn[(size_t)e * H + c * kChunk]);
             }
-        }
-        mark(p, l, 4);
-        // stage every token's activations
-        {
-            const void* srcs[kMaxRows];
-#pragma unroll
-            for (int t = 0; t < kMaxRows; ++t) srcs[t] = p.x + (size_t)min(t, rows - 1) * H;
-            naiwa_stage_multi<DG, true, kMaxRows>(srcs, rows, true, H, dyn, xstage, tid, kThreads);
-        }
-        __syncthreads();
-        mark(p, l, 5);
+            mark(p, l, 4);
+            __syncthreads();
+            mark(p, l, 5);
 #pragma unroll 1
-        for (int q = qa, j = 0; q < q1; q += kGroups, ++j) {
-            if (j == 1) {
-#pragma unroll
-                for (int i = 0; i < UM; ++i) {
-                    fg0[i] = fg1[i];
-                    fu0[i] = fu1[i];
-                }
+            for (int q = qa, j = 0; q < q1; q += kGroups, ++j) {
+                if (j > 0) q4_block_load(q4_row_ptr(L, sm.seg_slot[q / I], q % I, rb, lr), lr & 7, nb, f);
+                q4_row_compute(p, sm, L, dyn, xstage, q, rb, nb, lr, f);
             }
-            gate_up_row<DG>(p, sm, L, dyn, q, xstage, rb, nu, lr, fg0, fu0, j < 2);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) touch ^= tv[j];
+        } else {
+            mark(p, l, 3);
+            mark(p, l, 4);
+            __syncthreads();
+            mark(p, l, 5);
+#pragma unroll 1
+            for (int q = q0 + grp; q < q1; q += kGroups) unit_row<DG>(p, sm, L, dyn, q, xstage, rb, nu, lr);
+        }
+        if (l + 1 < p.n_layers && tid < E) {
+            const float* Wn = layers_lds[l + 1].router;
+            for (int cp = bid; cp < nchunks; cp += G)
+                touch ^= __float_as_uint(Wn[(size_t)tid * H + chunk_at(cp, nchunks) * kChunk]);
         }
         mark(p, l, 6);
         barrier_all(p, ++epoch);
@@ -476,30 +738,32 @@ stack_kernel(Params p) {
         long long racc[kPartPerThread];
 #pragma unroll
         for (int j = 0; j < kPartPerThread; ++j) racc[j] = 0;
-        for (int c = bid; c < nchunks; c += G) {
-            const int f0 = c * kChunk;
+        for (int cp = bid; cp < nchunks; cp += G) {
+            const int f0 = chunk_at(cp, nchunks) * kChunk;
+            // this chunk's current activations (the residual input)
+            uint32_t xo_pair = 0;
+            if (tid < rows * kChunk / 2) {
+                const int t = tid / (kChunk / 2), fi = 2 * (tid % (kChunk / 2));
+                xo_pair = ld_coh((const uint32_t*)(p.x + (size_t)t * H + f0 + fi));
+            }
             for (int b0 = 0; b0 < nvalid; b0 += kCPairs) {
-                const int nb = min(kCPairs, nvalid - b0);
+                const int nbp = min(kCPairs, nvalid - b0);
                 __syncthreads();
-                {
 #pragma unroll 1
-                    for (int v0 = 0; v0 < nb; v0 += 8) {
-                        const void* srcs[8];
+                for (int v0 = 0; v0 < nbp; v0 += 8) {
+                    const void* srcs[8];
 #pragma unroll
-                        for (int i = 0; i < 8; ++i)
-                            srcs[i] = p.h + (size_t)sm.sorted[b0 + min(v0 + i, nb - 1)] * I;
-                        naiwa_stage_multi<DD, true, 8>(srcs, min(8, nb - v0), false, I, dyn + v0 * hstage,
-                                                       hstage, tid, kThreads);
-                    }
+                    for (int i = 0; i < 8; ++i)
+                        srcs[i] = p.h + (size_t)sm.sorted[b0 + min(v0 + i, nbp - 1)] * I;
+                    naiwa_stage_multi<DD, true, 8>(srcs, min(8, nbp - v0), false, I, dyn + v0 * hstage,
+                                                   hstage, tid, kThreads);
                 }
                 __syncthreads();
                 mark(p, l, 8);
-                // (feature, staged pair) items, kCB per group at a time: all
-                // their loads are issued before the first dot
-                constexpr int kCB = 4;
+                constexpr int kCB = 2;
                 constexpr int DUM = 2;
                 const int dnu = Fmt<DD>::units(I);
-                const int nitems = kChunk * nb;
+                const int nitems = kChunk * nbp;
                 for (int it0 = grp; it0 < nitems; it0 += kGroups * kCB) {
                     typename Fmt<DD>::Frag fr[kCB][DUM];
                     float acc[kCB];
@@ -538,6 +802,11 @@ stack_kernel(Params p) {
                     }
                 }
             }
+            if (tid < rows * kChunk / 2) {
+                const int t = tid / (kChunk / 2), fi = 2 * (tid % (kChunk / 2));
+                sm.xown[t][fi] = naiwa_bf16_to_f32(xo_pair & 0xffffu);
+                sm.xown[t][fi + 1] = naiwa_bf16_to_f32(xo_pair >> 16);
+            }
             __syncthreads();
             mark(p, l, 9);
             if (tid < rows * kChunk) {
@@ -547,9 +816,7 @@ stack_kernel(Params p) {
                     const uint32_t pr = sm.sorted[i];
                     if ((int)pr / k == t) y += sm.pair_w[pr] * sm.partial[fi][i];
                 }
-                const uint32_t pair = ld_coh((const uint32_t*)(p.x + (size_t)t * H + f0 + (fi & ~1)));
-                const float xo = naiwa_bf16_to_f32((fi & 1) ? pair >> 16 : pair & 0xffffu);
-                sm.xnew[t][fi] = naiwa_bf16_to_f32(naiwa_f32_to_bf16(xo + y));
+                sm.xnew[t][fi] = naiwa_bf16_to_f32(naiwa_f32_to_bf16(sm.xown[t][fi] + y));
             }
             __syncthreads();
             if (tid < rows * kChunk / 2) {
@@ -564,7 +831,7 @@ stack_kernel(Params p) {
         mark(p, l, 11);
         if (l + 1 < p.n_layers) {
             router_store_partials(p, racc);
-            barrier_reduce(p, sm, ++epoch);
+            barrier_reduce(p, ++epoch);
         }
         mark(p, l, 12);
     }
@@ -590,7 +857,18 @@ int launch(const Params& prm, int blocks, size_t lds, hipStream_t st) {
     void* args[] = {&copy};
     hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return (int)e;
-    e = hipLaunchCooperativeKernel((const void*)fn, dim3(blocks), dim3(kThreads), args, (unsigned)lds, st);
+    // The grid never exceeds the blocks every CU can hold at once; the
+    // cooperative launch also makes the runtime check it.  NAIWA_STACK_LAUNCH=
+    // normal uses a plain launch (profilers that cannot follow cooperative
+    // launches); the bounded barrier waits keep that safe.
+    static const bool normal = [] {
+        const char* v = getenv("NAIWA_STACK_LAUNCH");
+        return v && strcmp(v, "normal") == 0;
+    }();
+    if (normal)
+        e = hipLaunchKernel((const void*)fn, dim3(blocks), dim3(kThreads), args, (unsigned)lds, st);
+    else
+        e = hipLaunchCooperativeKernel((const void*)fn, dim3(blocks), dim3(kThreads), args, (unsigned)lds, st);
     return naiwa_hip_rc(e);
 }
 
