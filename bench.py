@@ -31,6 +31,22 @@ HBM_PEAK_GBS = 8000.0
 Q4K_BLOCK, Q4K_BYTES = 256, 144
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "stack_kernel_qwen3_bs1_traffic.txt")
+
+
+def measured_traffic(rows: int, layers: int, fused: bool):
+    """HBM bytes per launch of the fused kernel on this exact workload (bs1, 48
+    layers), from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, scaled
+    by a device copy of known size; None for any other workload."""
+    if not (fused and rows == 1 and layers == 48) or not os.path.exists(TRAFFIC_PROFILE):
+        return None
+    with open(TRAFFIC_PROFILE) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    return None
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -197,7 +213,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(rows, L, fused),
             "kernel": "stack_kernel<Q4_K,Q4_K>" if fused else "layered chain",
             "bytes_per_launch": alg_bytes,
             "kernel_avg_us": round(kern_avg_ms * 1e3, 2),
