@@ -238,8 +238,9 @@ def print_trace(nm, run, stream, L, khz):
     nl = C.c_int(0)
     nm._lib.check(lib.naiwa_stack_trace_read(buf, n, C.byref(nl)), "trace_read")
     t = np.frombuffer(buf, dtype=np.uint64).astype(np.float64).reshape(2, L + 1, slots) / (khz / 1000.0)
-    names = ["logits", "topk", "segments", "preload", "touch", "stage_x", "gate_up", "barrier_Y",
-             "stage_h", "down_dots", "combine", "router", "reduce_X"]
+    names = ["poll_logits_x", "rank", "route", "issue_loads", "gate_up", "poll_h", "down", "combine_x",
+             "partials", "reduce"]
+    end = len(names) - 1
     for who in range(2):
         pro = t[who, L]
         log(f"trace block {'first' if who == 0 else 'last'}: prologue partials {pro[1] - pro[0]:.2f} us, "
@@ -248,13 +249,13 @@ def print_trace(nm, run, stream, L, khz):
         prev = t[who, L, 2]
         for l in range(L):
             m = t[who, l]
-            row = [m[0] - prev] + [m[i] - m[i - 1] for i in range(1, 13)]
+            row = [m[0] - prev] + [m[i] - m[i - 1] for i in range(1, end + 1)]
             per.append(row)
-            prev = m[12]
+            prev = m[end]
         per = np.array(per)
         log("  mean us/layer: " + ", ".join(f"{nme} {v:.2f}" for nme, v in zip(names, per.mean(0)))
             + f" | total {per.sum(1).mean():.2f}")
-    log(f"trace: kernel span {t[0, L - 1, 12] - t[0, L, 0]:.1f} us")
+    log(f"trace: kernel span {t[0, L - 1, end] - t[0, L, 0]:.1f} us")
 
 
 def layers_host_sample(nm, keep, L, E, H, I, n_layers: int = 4):

@@ -20,6 +20,31 @@
 
 #include "../../include/naiwa_moe.h"
 
+// Loads through an explicit address space: AS 1 = global, 3 = LDS, 0 =
+// generic.  Pointers that come out of LDS-resident descriptors are generic to
+// the compiler, and generic (flat) accesses wait on both memory counters.
+#define NAIWA_AS_GLOBAL 1
+#define NAIWA_AS_LDS 3
+// 16-byte types (uint4, float4: class types whose copy constructor would take
+// a generic reference) are loaded as a native 4 x u32 vector.
+template <class T, int AS>
+__device__ __forceinline__ T naiwa_ld(const void* p) {
+    if constexpr (sizeof(T) == 16) {
+        typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+        v4u v;
+        if constexpr (AS == NAIWA_AS_GLOBAL) v = *(const __attribute__((address_space(1))) v4u*)p;
+        else if constexpr (AS == NAIWA_AS_LDS) v = *(const __attribute__((address_space(3))) v4u*)p;
+        else v = *(const v4u*)p;
+        T out;
+        __builtin_memcpy(&out, &v, 16);
+        return out;
+    } else {
+        if constexpr (AS == NAIWA_AS_GLOBAL) return *(const __attribute__((address_space(1))) T*)p;
+        else if constexpr (AS == NAIWA_AS_LDS) return *(const __attribute__((address_space(3))) T*)p;
+        else return *(const T*)p;
+    }
+}
+
 #define NAIWA_QK8_0 32
 #define NAIWA_QK_K 256
 #define NAIWA_Q8_0_BYTES 34

@@ -29,9 +29,10 @@ __device__ __forceinline__ void naiwa_load_x8(const void* x, int x_bf16, int64_t
 
 // One chunk: f32 fma chain over 8 features, rounded half-to-even to int64
 // with 32 fractional bits (scaling by 2^32 is exact).
+template <int AS = 0>
 __device__ __forceinline__ long long naiwa_router_chunk(const float* w8, const float* xv) {
-    const float4 a = *reinterpret_cast<const float4*>(w8);
-    const float4 b = *reinterpret_cast<const float4*>(w8 + 4);
+    const float4 a = naiwa_ld<float4, AS>(w8);
+    const float4 b = naiwa_ld<float4, AS>(w8 + 4);
     const float wv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
     float p = 0.0f;
 #pragma unroll

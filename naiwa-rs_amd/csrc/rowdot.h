@@ -18,15 +18,16 @@ template <> struct Fmt<NAIWA_Q4_K> {
         uint4 q, hd;
     };
     __device__ static int units(int k) { return (k / NAIWA_QK_K) * 8; }
-    __device__ static Frag load(const uint8_t* row, int u) {
+    template <int AS = 0>
+    __device__ __forceinline__ static Frag load(const uint8_t* row, int u) {
         const uint8_t* blk = row + (u >> 3) * NAIWA_Q4_K_BYTES;
         Frag f;
-        f.hd = *reinterpret_cast<const uint4*>(blk);
-        f.q = *reinterpret_cast<const uint4*>(blk + 16 + 16 * (u & 7));
+        f.hd = naiwa_ld<uint4, AS>(blk);
+        f.q = naiwa_ld<uint4, AS>(blk + 16 + 16 * (u & 7));
         return f;
     }
     // words: perm words of the vector (K/2), sums: K/16 sums
-    __device__ static float dot(const Frag& f, int u, const uint32_t* words, const float* sums) {
+    __device__ __forceinline__ static float dot(const Frag& f, int u, const uint32_t* words, const float* sums) {
         const int j = u & 7, c = j >> 1;
         const int elo = (u >> 3) * NAIWA_QK_K + 64 * c + 16 * (j & 1);
         const uint4* xl = reinterpret_cast<const uint4*>(words + elo / 2);
@@ -49,14 +50,15 @@ template <> struct Fmt<NAIWA_Q8_0> {
         uint32_t d[17];
     };
     __device__ static int units(int k) { return k / (2 * NAIWA_QK8_0); }
-    __device__ static Frag load(const uint8_t* row, int u) {
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(row + 68 * u);
+    template <int AS = 0>
+    __device__ __forceinline__ static Frag load(const uint8_t* row, int u) {
+        const uint8_t* p = row + 68 * u;
         Frag f;
 #pragma unroll
-        for (int i = 0; i < 17; ++i) f.d[i] = p[i];
+        for (int i = 0; i < 17; ++i) f.d[i] = naiwa_ld<uint32_t, AS>(p + 4 * i);
         return f;
     }
-    __device__ static float dot(const Frag& f, int u, const uint32_t* words, const float* sums) {
+    __device__ __forceinline__ static float dot(const Frag& f, int u, const uint32_t* words, const float* sums) {
         uint32_t xw[32];
         const uint4* xv = reinterpret_cast<const uint4*>(words + 32 * u);
 #pragma unroll
@@ -81,15 +83,18 @@ template <> struct Fmt<NAIWA_Q8_0_ODD> {
         uint32_t q[8];
     };
     __device__ static int units(int k) { return k / NAIWA_QK8_0; }
-    __device__ static Frag load(const uint8_t* row, int u) {
-        const uint16_t* p = reinterpret_cast<const uint16_t*>(row + NAIWA_Q8_0_BYTES * u);
+    template <int AS = 0>
+    __device__ __forceinline__ static Frag load(const uint8_t* row, int u) {
+        const uint8_t* p = row + NAIWA_Q8_0_BYTES * u;
         Frag f;
-        f.d = p[0];
+        f.d = naiwa_ld<uint16_t, AS>(p);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) f.q[i] = (uint32_t)p[1 + 2 * i] | ((uint32_t)p[2 + 2 * i] << 16);
+        for (int i = 0; i < 8; ++i)
+            f.q[i] = (uint32_t)naiwa_ld<uint16_t, AS>(p + 2 + 4 * i) |
+                     ((uint32_t)naiwa_ld<uint16_t, AS>(p + 4 + 4 * i) << 16);
         return f;
     }
-    __device__ static float dot(const Frag& f, int u, const uint32_t* words, const float* sums) {
+    __device__ __forceinline__ static float dot(const Frag& f, int u, const uint32_t* words, const float* sums) {
         const uint4* xv = reinterpret_cast<const uint4*>(words + 16 * u);
         float a = 0.0f;
 #pragma unroll

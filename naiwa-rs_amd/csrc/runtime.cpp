@@ -15,7 +15,10 @@ std::mutex g_scratch_mu;
 NaiwaScratch g_scratch[kMaxDevices][NAIWA_SCRATCH_TAGS];
 } // namespace
 
-void* naiwa_scratch(int tag, size_t bytes, int* rc) {
+void* naiwa_scratch(int tag, size_t bytes, int* rc) { return naiwa_scratch(tag, bytes, rc, nullptr); }
+
+void* naiwa_scratch(int tag, size_t bytes, int* rc, bool* fresh) {
+    if (fresh) *fresh = false;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess || dev < 0 || dev >= kMaxDevices || tag < 0 || tag >= NAIWA_SCRATCH_TAGS) {
@@ -42,6 +45,7 @@ void* naiwa_scratch(int tag, size_t bytes, int* rc) {
             return nullptr;
         }
         s.bytes = want;
+        if (fresh) *fresh = true;
     }
     *rc = NAIWA_OK;
     return s.ptr;

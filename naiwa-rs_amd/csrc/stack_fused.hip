@@ -1,34 +1,38 @@
 // NAIWA_STACK_FUSED: one persistent, cooperatively launched kernel runs a
 // whole decode step through every MoE layer, x <- bf16(x + MoE_l(x)).
 //
-// One block of 256 threads per CU (16 groups of 16 lanes, one wave per SIMD),
-// every block resident.  Per layer:
-//   A  route   every block loads the layer's router logits (and, in the same
-//              burst, the activations it will need), ranks the experts of each
-//              token in parallel, derives the routing weights and groups the
-//              (token, k) pairs by cache slot -- redundantly and identically in
-//              every block, so routing needs no barrier;
+// One workgroup of 256 threads per CU (16 groups of 16 lanes, one wave per
+// SIMD), every workgroup resident.  Per layer:
+//   A  route   every workgroup polls the layer's logits and activations, ranks
+//              the experts of each token, derives the routing weights and
+//              groups the (token, k) pairs by cache slot -- redundantly and
+//              identically everywhere, so routing needs no exchange;
 //   B  gate/up the (segment, intermediate row) work is dealt out evenly.  For
-//              Q4_K each lane owns whole 144-byte blocks: lanes 0-7 of a
-//              16-lane group take the gate row, lanes 8-15 the up row, so a
-//              block's scales are decoded once per 256 weights.  Every lane
-//              issues its first row's loads before the activations are staged.
-//              The block then touches the down rows and next-layer router
-//              columns it will need in C, so they sit in its XCD's L2;
-//   -- all-gather barrier --
-//   C  down    each block owns 8-feature output chunks: it stages the h
+//              Q4_K each lane owns whole 144-byte blocks: lanes 0-7 of a group
+//              take the gate row, lanes 8-15 the up row, so a block's scales
+//              are decoded once per 256 weights.  Two rows' loads per group are
+//              in flight before the first is used, and the down rows and next
+//              router columns that phase C needs are loaded into registers in
+//              the same burst;
+//   C  down    each workgroup owns 8-feature output chunks: it polls the h
 //              vectors, dots every (feature, pair), adds the pairs of each
 //              token in ascending slot order (no atomics), applies the
-//              residual, stores bf16 x, and stores its int64 partial sums of
-//              the next layer's router logits;
-//   -- reduce barrier: 32 leader blocks add every block's partials for their
-//      experts and publish the logits --
+//              residual, publishes its x chunk and its int64 partial sums of
+//              the next layer's router logits; 32 leader workgroups add every
+//              chunk's partials for their experts and publish the logits.
 //
-// Cross-block data (h, x, router partials, logits, flags) moves with
-// device-coherent relaxed atomic loads and stores (sc1: past the per-XCD L2s),
-// and every block waits for its own stores to complete before it raises its
-// arrival flag, so no barrier needs an L2 writeback or invalidate.  Weights are
-// read with ordinary cached loads; they never change during the kernel.
+// There is no grid barrier.  Every value one workgroup hands to another (x,
+// h, router partials, logits) is a 64-bit word (tag << 32) | payload written
+// with one device-coherent store (past the per-XCD L2s), where the tag names
+// the launch and the layer.  A consumer loads the words it needs and reloads
+// those whose tag is not yet current, so each hand-off costs one round trip
+// and no workgroup waits for more than the data it reads.  Every wait is
+// bounded; a timeout is counted and makes every later wait give up at once.
+// Reuse is safe without barriers: a workgroup can only reach layer l+1 after
+// seeing layer l+1's logits, which need every chunk's layer-l partials, which
+// each workgroup produces after its last layer-l read of h and of the logits;
+// x alternates between two buffers, since idle workgroups may still read x_l
+// while chunk owners publish x_{l+1}.
 //
 // Router logits: each chunk of 8 features is an f32 fma chain rounded to
 // int64 with 32 fractional bits, and the chunks are added as integers.
@@ -45,21 +49,26 @@
 
 namespace {
 
+typedef unsigned long long u64;
+
 constexpr int kThreads = 256;             // 4 waves, 16 groups of 16 lanes
 constexpr int kGroups = kThreads / NAIWA_GROUP;
-constexpr int kWaves = kThreads / 64;
 constexpr int kMaxRows = 8;               // tokens per step served by this kernel
 constexpr int kMaxK = 8;                  // routed experts per token
 constexpr int kMaxPairs = kMaxRows * kMaxK;
 constexpr int kMaxE = 256;
-constexpr int kLeaders = 32;              // blocks that reduce the router partials
+constexpr int kLeaders = 32;              // workgroups that add the router partials
 constexpr int kChunk = NAIWA_ROUTER_CHUNK; // output features per phase-C chunk
+constexpr int kMaxChunks = 4;             // chunks per workgroup
 constexpr int kCPairs = 16;               // h vectors staged per phase-C pass
-constexpr int kLine = 64;                 // u32 per 256-byte flag line
-constexpr int kPartPerThread = (kMaxRows * kMaxE + kThreads - 1) / kThreads;
+constexpr int kPartPerThread = kMaxRows * kMaxE / kThreads;
 constexpr int kTraceSlots = 16;
-constexpr int kMaxLayers = 128;           // layer descriptors kept in LDS
-constexpr int kXPre = 8;                  // activation loads per thread issued with the logits
+constexpr int kMaxLayers = 128;           // layer descriptors kept in LDS (tags hold layer + 1 < 256)
+constexpr int kXG = 8;                    // activation groups (4 values) per thread per poll round
+constexpr int kHG = 8;                    // h groups (4 values, 2 words) per thread per poll round
+constexpr int kDJ = 4;                    // down rows per group prefetched into LDS (one-chunk path)
+constexpr int kDUM = 2;                   // units per lane of such a row
+constexpr int kCB = 2;                    // down rows per group in flight (general path)
 
 struct LayerDev {
     const float* router;
@@ -75,21 +84,21 @@ struct LayerDev {
 struct Params {
     const LayerDev* layers;
     int n_layers, rows, H, I, E, k, mode, act;
-    uint16_t* x;                 // [rows, H] bf16, in/out
-    float* h;                    // [kMaxPairs, I] f32
-    long long* part;             // [blocks, rows, E] int64 router partials
-    long long* logits;           // [rows, E] int64 fixed point
-    unsigned* arrive;            // [blocks] flag lines
-    unsigned* release;           // [kLeaders] flag lines
-    int* status;                 // [0] barrier timeouts, [1] missing experts
+    uint16_t* x;                 // [rows, H] bf16: layer-0 input, last layer's output
+    u64* xt;                     // [2][rows][H/2] tagged bf16 pairs (x of layer l in buffer l & 1)
+    u64* h;                      // [kMaxPairs][I/2] tagged pairs of 16-bit values (down format)
+    u64* part;                   // [chunk owners][rows * E][2] tagged int64 halves
+    u64* logits;                 // [rows * E] tagged f32
+    int* status;                 // [0] wait timeouts, [1] missing experts
     uint32_t* ids_out;           // [n_layers, rows, k] or null
     float* w_out;
     uint64_t spin_limit;         // wall-clock ticks before a wait gives up
-    int never;                   // always 0: keeps the prefetch touches alive
+    uint32_t seq;                // launch number; tag of layer l = seq << 8 | (l + 1)
+    int down_lds;                // dynamic LDS holds kGroups * kDJ down rows after the staging areas
     unsigned long long* trace;   // optional [2][n_layers + 1][kTraceSlots] phase timestamps
 };
 
-// Phase timestamps (s_memrealtime) of the first and last block, when tracing.
+// Phase timestamps (s_memrealtime) of the first and last workgroup, when tracing.
 __device__ __forceinline__ void mark(const Params& p, int layer, int slot) {
     if (!p.trace || threadIdx.x != 0) return;
     const int who = blockIdx.x == 0 ? 0 : (blockIdx.x == gridDim.x - 1 ? 1 : -1);
@@ -98,70 +107,86 @@ __device__ __forceinline__ void mark(const Params& p, int layer, int slot) {
 }
 
 struct Smem {
+    alignas(16) u64 key[kMaxRows][kMaxE + 2];  // ranking keys: ordered logit bits << 32 | ~expert
+    float lg[kMaxRows][kMaxE];
+    int32_t slot_tab[kMaxE];
+    uint32_t top_ids[kMaxRows][kMaxK];
+    float top_ex[kMaxRows][kMaxK];
+    float exv[kMaxPairs];
     uint32_t pair_slot[kMaxPairs]; // slot of pair p = t*k + j
     float pair_w[kMaxPairs];
     uint32_t sorted[kMaxPairs];    // valid pairs in (slot, p) order
+    uint32_t srt_slot[kMaxPairs];
     uint32_t seg_begin[kMaxPairs + 1];
     uint32_t seg_slot[kMaxPairs];
     int nseg;
-    float lg[kMaxRows][kMaxE];
-    uint32_t top_ids[kMaxRows][kMaxK];
-    float top_ex[kMaxRows][kMaxK];
     float partial[kChunk][kMaxPairs];
-    float xnew[kMaxRows][kChunk];
-    float xown[kMaxRows][kChunk];
-    long long lsum[kThreads / 16];
+    float xown[kMaxChunks][kMaxRows][kChunk]; // this workgroup's chunks of x (bf16 values)
+    alignas(16) float wch[kMaxE][kChunk];     // next router's columns of this workgroup's chunk
 };
 
-__device__ __forceinline__ unsigned ld_flag(const unsigned* f) {
-    return __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+typedef __attribute__((address_space(1))) u64 gu64;
+__device__ __forceinline__ u64 ld64(const u64* p) {
+    return __hip_atomic_load((const gu64*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_flag(unsigned* f, unsigned v) {
-    __hip_atomic_store(f, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void st64(u64* p, u64 v) {
+    __hip_atomic_store((gu64*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_coh(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_coh(uint32_t* p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_coh(long long* p, long long v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ long long ld_coh(const long long* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t ld_coh(const uint32_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// This wave's stores have completed (reached the device-coherent level).
-__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ u64 tagged(uint32_t tag, uint32_t v) { return ((u64)tag << 32) | v; }
 
-// Wait for *f >= target.  Bounded: after spin_limit ticks the wait counts a
-// timeout and gives up; once any wait has timed out (status[0] != 0) every
-// later wait returns at once, so a grid that is not fully resident drains
-// quickly with an error instead of waiting out every barrier.
-__device__ inline void spin_ge(const unsigned* f, unsigned target, const Params& p, bool sleep) {
-    const uint64_t t0 = wall_clock64();
-    for (unsigned n = 0; ld_flag(f) < target; ++n) {
-        if ((n & 63) == 63) {
-            if (__hip_atomic_load(&p.status[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
-            if (wall_clock64() - t0 > p.spin_limit) {
-                atomicAdd(&p.status[0], 1);
-                return;
-            }
+// 16 bytes from global memory straight into LDS (no registers; counted by
+// vmcnt): lane i of the wave writes wave_base + 16 * i.  Both addresses must be
+// 16-byte aligned, and wave_base must be the same in every active lane.
+__device__ __forceinline__ void lds_dma16(const void* src, void* wave_base) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)wave_base, 16, 0, 0);
+}
+__device__ __forceinline__ bool tag_ok(u64 w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
+__device__ __forceinline__ uint32_t layer_tag(const Params& p, int l) { return (p.seq << 8) | (uint32_t)(l + 1); }
+
+// Bounded-wait bookkeeping: false once this wait has run past spin_limit (the
+// timeout is counted) or any wait anywhere has (status[0] != 0).
+struct Poll {
+    uint64_t t0 = 0;
+    unsigned n = 0;
+};
+__device__ inline bool poll_continue(const Params& p, Poll& s) {
+    if (s.n++ == 0) {
+        s.t0 = wall_clock64();
+        return true;
+    }
+    if ((s.n & 7) == 0) {
+        if (__hip_atomic_load(&p.status[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+        if (wall_clock64() - s.t0 > p.spin_limit) {
+            atomicAdd(&p.status[0], 1);
+            return false;
         }
-        if (sleep) __builtin_amdgcn_s_sleep(1);
+    }
+    return true;
+}
+
+// Tagged loads of N words: addr(j) gives word j's address, or null for none.
+template <int N, class F>
+__device__ __forceinline__ void issue_tagged(u64 (&w)[N], const F& addr, uint32_t tag) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        const u64* a = addr(j);
+        w[j] = a ? ld64(a) : tagged(tag, 0u);
     }
 }
-
-// Every block raises its flag and waits for every other block's.
-__device__ inline void barrier_all(const Params& p, unsigned epoch) {
-    wait_stores();
-    __syncthreads();
-    if (threadIdx.x == 0) st_flag(&p.arrive[blockIdx.x * kLine], epoch);
-    for (int i = threadIdx.x; i < (int)gridDim.x; i += kThreads) spin_ge(&p.arrive[i * kLine], epoch, p, true);
-    __syncthreads();
+// Reload the words whose tag is not current until all are (or the wait gives up).
+template <int N, class F>
+__device__ inline void wait_tagged(u64 (&w)[N], const F& addr, uint32_t tag, const Params& p) {
+    Poll s;
+    while (true) {
+        bool ok = true;
+#pragma unroll
+        for (int j = 0; j < N; ++j) ok &= tag_ok(w[j], tag);
+        if (ok || !poll_continue(p, s)) return;
+#pragma unroll
+        for (int j = 0; j < N; ++j)
+            if (!tag_ok(w[j], tag)) w[j] = ld64(addr(j));
+    }
 }
 
 // Sum over aligned groups of W lanes of an exact int64.
@@ -176,121 +201,94 @@ __device__ __forceinline__ long long group_sum_i64(long long v) {
     return v;
 }
 
-// Barrier that also publishes the logits: leader L waits for every block,
-// adds all blocks' partials of its experts and raises its release flag; the
-// others wait for the leaders only.
-template <int LPI>
-__device__ inline void leader_reduce(const Params& p, int items, int e0, int ne) {
-    const int tid = threadIdx.x, G = gridDim.x;
-    const int it = tid / LPI, li = tid % LPI;
-    long long s = 0;
-    int t = 0, e = 0;
-    if (it < items) {
-        t = it / ne;
-        e = e0 + it % ne;
-        const long long* src = p.part + (size_t)t * p.E + e;
-        const size_t bstride = (size_t)p.rows * p.E;
-#pragma unroll 1
-        for (int b0 = li; b0 < G; b0 += 8 * LPI) {
-            long long v[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int b = b0 + j * LPI;
-                v[j] = b < G ? ld_coh(src + (size_t)b * bstride) : 0;
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) s += v[j];
-        }
-    }
-    s = group_sum_i64<LPI>(s);
-    if (it < items && li == 0) st_coh(&p.logits[(size_t)t * p.E + e], s);
-}
-
-__device__ inline void barrier_reduce(const Params& p, unsigned epoch) {
-    const int tid = threadIdx.x, bid = blockIdx.x, G = gridDim.x;
-    wait_stores();
-    __syncthreads();
-    if (tid == 0) st_flag(&p.arrive[bid * kLine], epoch);
-    const int nlead = min(kLeaders, G);
-    const int epl = (p.E + nlead - 1) / nlead;
-    if (bid < nlead) {
-        for (int i = tid; i < G; i += kThreads) spin_ge(&p.arrive[i * kLine], epoch, p, false);
-        __syncthreads();
-        const int e0 = bid * epl;
-        const int ne = max(0, min(epl, p.E - e0));
-        const int items = p.rows * ne;
-        if (items > 0) {
-            if (items <= 4) leader_reduce<64>(p, items, e0, ne);
-            else if (items <= 8) leader_reduce<32>(p, items, e0, ne);
-            else if (items <= 16) leader_reduce<16>(p, items, e0, ne);
-            else {
-#pragma unroll 1
-                for (int i0 = 0; i0 < items; i0 += 16) {
-                    // 16 items per pass, 16 lanes each
-                    const int n = min(16, items - i0);
-                    const int it = tid / 16, li = tid % 16;
-                    long long s = 0;
-                    int t = 0, e = 0;
-                    if (it < n) {
-                        t = (i0 + it) / ne;
-                        e = e0 + (i0 + it) % ne;
-                        const long long* src = p.part + (size_t)t * p.E + e;
-                        const size_t bstride = (size_t)p.rows * p.E;
-#pragma unroll 1
-                        for (int b0 = li; b0 < G; b0 += 128) {
-                            long long v[8];
-#pragma unroll
-                            for (int j = 0; j < 8; ++j) {
-                                const int b = b0 + j * 16;
-                                v[j] = b < G ? ld_coh(src + (size_t)b * bstride) : 0;
-                            }
-#pragma unroll
-                            for (int j = 0; j < 8; ++j) s += v[j];
-                        }
-                    }
-                    s = group_sum_i64<16>(s);
-                    if (it < n && li == 0) st_coh(&p.logits[(size_t)t * p.E + e], s);
-                }
-            }
-        }
-        wait_stores();
-        __syncthreads();
-        if (tid == 0) st_flag(&p.release[bid * kLine], epoch);
-    }
-    if (tid < nlead) spin_ge(&p.release[tid * kLine], epoch, p, true);
-    __syncthreads();
-}
-
-// The output-feature chunk handled at position p (= block + j * blocks).
-// Blocks are dealt to the XCDs round-robin, so position p runs on XCD p % 8;
+// The output-feature chunk handled at position p (= workgroup + j * workgroups).
+// Workgroups are dealt to the XCDs round-robin, so position p runs on XCD p % 8;
 // this mapping gives the 4 chunks that share a 128-byte line of every router
-// row (4 x 8 f32) to blocks of one XCD, which then fetches the line once.
+// row (4 x 8 f32) to workgroups of one XCD, which then fetches the line once.
 __device__ __forceinline__ int chunk_at(int p, int nchunks) {
     if (nchunks % 32) return p;
     const int x = p & 7, r = p >> 3;
     return (((r >> 2) << 3) + x) * 4 + (r & 3);
 }
 
-// Router partials of this block's chunks for (token, expert) items; the
-// chunk's 8 activations come from LDS.  acc holds kPartPerThread items.
-__device__ inline void router_chunk_accumulate(const Params& p, const float* W, int f0,
-                                               const float (*xv)[kChunk], long long* acc) {
+// Publish this workgroup's router partials for layer tag `tag`.
+__device__ inline void store_partials(const Params& p, const long long* acc, uint32_t tag) {
+    const int items = p.rows * p.E;
+#pragma unroll
+    for (int j = 0; j < kPartPerThread; ++j) {
+        const int it = threadIdx.x + j * kThreads;
+        if (it < items) {
+            u64* dst = p.part + ((size_t)blockIdx.x * items + it) * 2;
+            st64(dst, tagged(tag, (uint32_t)(unsigned long long)acc[j]));
+            st64(dst + 1, tagged(tag, (uint32_t)((unsigned long long)acc[j] >> 32)));
+        }
+    }
+}
+
+// Leader bid adds, for its experts, the partials of every chunk owner and
+// publishes the logits (tagged f32).  LPI lanes per (token, expert) item.
+template <int LPI>
+__device__ inline void leader_pass(const Params& p, int i0, int items, int e0, int ne, int nprod, uint32_t tag) {
+    const int tid = threadIdx.x;
+    const int it = i0 + tid / LPI, li = tid % LPI;
+    const bool in = it < items;
+    const int t = in ? it / ne : 0, e = in ? e0 + it % ne : 0;
+    const size_t idx = (size_t)t * p.E + e;
+    const size_t stride = (size_t)p.rows * p.E * 2;
+    long long s = 0;
+#pragma unroll 1
+    for (int b0 = li; b0 < nprod; b0 += 8 * LPI) {
+        u64 w[16];
+        auto addr = [&](int j) -> const u64* {
+            const int b = b0 + (j >> 1) * LPI;
+            return (in && b < nprod) ? p.part + b * stride + idx * 2 + (j & 1) : nullptr;
+        };
+        issue_tagged(w, addr, tag);
+        wait_tagged(w, addr, tag, p);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            s += (long long)(((u64)(uint32_t)w[2 * j + 1] << 32) | (uint32_t)w[2 * j]);
+    }
+    s = group_sum_i64<LPI>(s);
+    if (in && li == 0) st64(&p.logits[idx], tagged(tag, __float_as_uint(naiwa_router_fix_to_f32(s))));
+}
+
+__device__ inline void leader_reduce(const Params& p, int nprod, uint32_t tag) {
+    const int nlead = min(kLeaders, (int)gridDim.x);
+    const int epl = (p.E + nlead - 1) / nlead;
+    const int e0 = blockIdx.x * epl;
+    const int ne = max(0, min(epl, p.E - e0));
+    const int items = p.rows * ne;
+    if (items <= 4) {
+        if (items > 0) leader_pass<64>(p, 0, items, e0, ne, nprod, tag);
+    } else if (items <= 8) {
+        leader_pass<32>(p, 0, items, e0, ne, nprod, tag);
+    } else {
+#pragma unroll 1
+        for (int i0 = 0; i0 < items; i0 += 16) leader_pass<16>(p, i0, items, e0, ne, nprod, tag);
+    }
+}
+
+// Router partials of one chunk for every (token, expert) item: W8(e) gives the
+// chunk's 8 router weights of expert e, xv[t] the chunk's activations.
+template <int AS, class F>
+__device__ __forceinline__ void router_chunk_accumulate(const Params& p, const F& W8, const float (*xv)[kChunk],
+                                                        long long* acc) {
 #pragma unroll
     for (int j = 0; j < kPartPerThread; ++j) {
         const int it = threadIdx.x + j * kThreads;
         if (it < p.rows * p.E) {
             const int t = it / p.E, e = it % p.E;
-            acc[j] += naiwa_router_chunk(W + (size_t)e * p.H + f0, xv[t]);
+            acc[j] += naiwa_router_chunk<AS>(W8(e), xv[t]);
         }
     }
 }
 
-__device__ inline void router_store_partials(const Params& p, const long long* acc) {
-#pragma unroll
-    for (int j = 0; j < kPartPerThread; ++j) {
-        const int it = threadIdx.x + j * kThreads;
-        if (it < p.rows * p.E) st_coh(&p.part[(size_t)blockIdx.x * p.rows * p.E + it], acc[j]);
-    }
+// Order-preserving 64-bit ranking key: larger key = earlier in (logit desc, id asc).
+__device__ __forceinline__ u64 rank_key(float f, int e) {
+    const uint32_t u = __float_as_uint(f + 0.0f); // -0 -> +0, which compare equal as floats
+    const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((u64)o << 32) | (uint32_t)~(uint32_t)e;
 }
 
 // ---------------------------------------------------------------------------
@@ -357,114 +355,171 @@ __device__ __forceinline__ void q4_block_load(const uint8_t* row, int b, int nb,
     if (b < nb) {
         const uint4* src = reinterpret_cast<const uint4*>(row + b * NAIWA_Q4_K_BYTES);
 #pragma unroll
-        for (int j = 0; j < 9; ++j) f.blk[j] = src[j];
+        for (int j = 0; j < 9; ++j) f.blk[j] = naiwa_ld<uint4, NAIWA_AS_GLOBAL>(src + j);
     }
 }
 
-// h of every token of the segment for one intermediate row.  f holds this
-// lane's block of the first 8; rows longer than 8 blocks load the rest here.
-__device__ inline void q4_row_compute(const Params& p, const Smem& sm, const LayerDev& L, const uint8_t* dyn,
-                                      int xstage, int q, int64_t rb, int nb, int lr, const Q4Row& f) {
-    const int I = p.I, H = p.H, k = p.k;
-    const int s = q / I, r = q % I;
+// h of every token of the segment for intermediate rows r, r + 1 (pair q):
+// f0 / f1 hold this lane's block of the first 8 of each row; rows longer than
+// 8 blocks load the rest here.  The two results go out as one tagged word in
+// the down projection's 16-bit format DD.
+template <int DD>
+__device__ inline void q4_pair_compute(const Params& p, const Smem& sm, const LayerDev& L, const uint8_t* dyn,
+                                       int xstage, int q, int64_t rb, int nb, int lr, const Q4Row& f0,
+                                       const Q4Row& f1, uint32_t tag) {
+    const int I = p.I, H = p.H, k = p.k, I2 = I / 2;
+    const int s = q / I2, r = 2 * (q % I2);
     const int b = (int)sm.seg_begin[s], e = (int)sm.seg_begin[s + 1];
     const int b0 = lr & 7;
+    const uint8_t* row0 = q4_row_ptr(L, sm.seg_slot[s], r, rb, lr);
     for (int tt = b; tt < e; ++tt) {
         const int t = (int)sm.sorted[tt] / k;
-        const uint32_t* words = (const uint32_t*)(dyn + t * xstage);
-        const float* sums = (const float*)(words + H / 2);
-        float acc = b0 < nb ? q4k_block_dot(f.blk, words + b0 * 128, sums + b0 * 16) : 0.0f;
-        if (nb > 8) {
-            const uint8_t* row = q4_row_ptr(L, sm.seg_slot[s], r, rb, lr);
+        const uint32_t* words = (const uint32_t*)(dyn + t * xstage);   // 132 words per block (padded)
+        const float* sums = (const float*)(words + H / 2 + 4 * nb);
+        float h0 = 0.0f, h1 = 0.0f;
+#pragma unroll 1
+        for (int rr = 0; rr < 2; ++rr) {
+            Q4Row f = rr ? f1 : f0;
+            float acc = b0 < nb ? q4k_block_dot(f.blk, words + b0 * 132, sums + b0 * 16) : 0.0f;
 #pragma unroll 1
             for (int bb = b0 + 8; bb < nb; bb += 8) {
-                Q4Row g;
-                q4_block_load(row, bb, nb, g);
-                acc += q4k_block_dot(g.blk, words + bb * 128, sums + bb * 16);
+                q4_block_load(row0 + rr * rb, bb, nb, f);
+                acc += q4k_block_dot(f.blk, words + bb * 132, sums + bb * 16);
             }
+            acc = naiwa_group_sum<8>(acc);                 // lanes 0-7: gate . x, lanes 8-15: up . x
+            const float uv = naiwa_dpp<0x128>(acc);        // row_ror:8 -- lane 0 receives lane 8
+            const float hv = naiwa_act(p.act, acc) * uv;
+            h0 = rr ? h0 : hv;
+            h1 = rr ? hv : h1;
         }
-        acc = naiwa_group_sum<8>(acc);                 // lanes 0-7: gate . x, lanes 8-15: up . x
-        const float uv = naiwa_dpp<0x128>(acc);        // row_ror:8 -- lane 0 receives lane 8
-        if (lr == 0) st_coh(&p.h[(size_t)sm.sorted[tt] * I + r], naiwa_act(p.act, acc) * uv);
+        if (lr == 0)
+            st64(&p.h[(size_t)sm.sorted[tt] * I2 + r / 2],
+                 tagged(tag, Fmt<DD>::to16(h0) | (Fmt<DD>::to16(h1) << 16)));
     }
 }
 
 // ---------------------------------------------------------------------------
 // Q8_0 gate/up with 16 lanes per row pair (units of two blocks)
 // ---------------------------------------------------------------------------
-template <int DG>
-__device__ inline void unit_row(const Params& p, const Smem& sm, const LayerDev& L, const uint8_t* dyn,
-                                int q, int xstage, int64_t rb, int nu, int lr) {
+template <int DG, int DD>
+__device__ inline void unit_pair(const Params& p, const Smem& sm, const LayerDev& L, const uint8_t* dyn,
+                                 int q, int xstage, int64_t rb, int nu, int lr, uint32_t tag) {
     constexpr int UM = Umax<DG>::v;
-    const int I = p.I, H = p.H, k = p.k;
-    const int s = q / I, r = q % I;
+    const int I = p.I, H = p.H, k = p.k, I2 = I / 2;
+    const int s = q / I2, r = 2 * (q % I2);
     const uint32_t slot = sm.seg_slot[s];
-    const uint8_t* grow = L.gate + (int64_t)slot * L.gate_stride + (int64_t)r * rb;
-    const uint8_t* urow = L.up + (int64_t)slot * L.up_stride + (int64_t)r * rb;
     const int b = (int)sm.seg_begin[s], e = (int)sm.seg_begin[s + 1];
     for (int tt = b; tt < e; ++tt) {
         const int t = (int)sm.sorted[tt] / k;
         const uint32_t* words = (const uint32_t*)(dyn + t * xstage);
         const float* sums = (const float*)(words + H / 2);
-        float ag = 0.0f, au = 0.0f;
-        for (int base = lr; base < nu; base += NAIWA_GROUP * UM) {
-            typename Fmt<DG>::Frag fg[UM], fu[UM];
+        float hv[2];
+#pragma unroll 1
+        for (int rr = 0; rr < 2; ++rr) {
+            const uint8_t* grow = L.gate + (int64_t)slot * L.gate_stride + (int64_t)(r + rr) * rb;
+            const uint8_t* urow = L.up + (int64_t)slot * L.up_stride + (int64_t)(r + rr) * rb;
+            float ag = 0.0f, au = 0.0f;
+            for (int base = lr; base < nu; base += NAIWA_GROUP * UM) {
+                typename Fmt<DG>::Frag fg[UM], fu[UM];
 #pragma unroll
-            for (int i = 0; i < UM; ++i) {
-                const int u = base + NAIWA_GROUP * i;
-                if (u < nu) {
-                    fg[i] = Fmt<DG>::load(grow, u);
-                    fu[i] = Fmt<DG>::load(urow, u);
+                for (int i = 0; i < UM; ++i) {
+                    const int u = base + NAIWA_GROUP * i;
+                    if (u < nu) {
+                        fg[i] = Fmt<DG>::template load<NAIWA_AS_GLOBAL>(grow, u);
+                        fu[i] = Fmt<DG>::template load<NAIWA_AS_GLOBAL>(urow, u);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < UM; ++i) {
+                    const int u = base + NAIWA_GROUP * i;
+                    if (u < nu) {
+                        ag += Fmt<DG>::dot(fg[i], u, words, sums);
+                        au += Fmt<DG>::dot(fu[i], u, words, sums);
+                    }
                 }
             }
-#pragma unroll
-            for (int i = 0; i < UM; ++i) {
-                const int u = base + NAIWA_GROUP * i;
-                if (u < nu) {
-                    ag += Fmt<DG>::dot(fg[i], u, words, sums);
-                    au += Fmt<DG>::dot(fu[i], u, words, sums);
-                }
-            }
+            const float gv = naiwa_group_sum<NAIWA_GROUP>(ag);
+            const float uv = naiwa_group_sum<NAIWA_GROUP>(au);
+            hv[rr] = naiwa_act(p.act, gv) * uv;
         }
-        const float gv = naiwa_group_sum<NAIWA_GROUP>(ag);
-        const float uv = naiwa_group_sum<NAIWA_GROUP>(au);
-        if (lr == 0) st_coh(&p.h[(size_t)sm.sorted[tt] * I + r], naiwa_act(p.act, gv) * uv);
+        if (lr == 0)
+            st64(&p.h[(size_t)sm.sorted[tt] * I2 + r / 2],
+                 tagged(tag, Fmt<DD>::to16(hv[0]) | (Fmt<DD>::to16(hv[1]) << 16)));
     }
 }
 
-// Convert prefetched activation groups (4 bf16 each) into the staged layout.
-template <int DG>
-__device__ inline void convert_x_groups(const uint2* xr, int ngroups_total, int gpt_h, uint8_t* dyn,
-                                        int xstage, int H) {
-    constexpr int span = Fmt<DG>::kSumSpan;
-    constexpr int gpg = span / 4;
+// Stage 4 consecutive values v[0..3] of group gg of a vector in the dot
+// layout of DT (pair words + sums over the format's span); every lane of the
+// wave must call it (the sums use DPP), with `in` false for no group.
+// PAD: 4 words of padding after every 256 values (128 words), so the lanes
+// of a group that read 8 different blocks hit 8 different LDS bank sets.
+template <int DT, bool PAD = false>
+__device__ __forceinline__ void stage_group(float v0, float v1, float v2, float v3, bool in, int gg, uint8_t* vec,
+                                            int k) {
+    constexpr int gpg = Fmt<DT>::kSumSpan / 4;
+    float part = 0.0f;
+    if (in) {
+        const uint32_t h0 = Fmt<DT>::to16(v0), h1 = Fmt<DT>::to16(v1), h2 = Fmt<DT>::to16(v2),
+                       h3 = Fmt<DT>::to16(v3);
+        uint32_t* words = (uint32_t*)vec + (PAD ? 4 * (gg >> 6) : 0);
+        words[2 * gg] = h0 | (h2 << 16);
+        words[2 * gg + 1] = h1 | (h3 << 16);
+        part = (Fmt<DT>::from16(h0) + Fmt<DT>::from16(h1)) + (Fmt<DT>::from16(h2) + Fmt<DT>::from16(h3));
+    }
+    part = naiwa_group_sum<gpg>(part);
+    if (in && (gg % gpg) == 0)
+        ((float*)((uint32_t*)vec + k / 2 + (PAD ? 4 * (k / NAIWA_QK_K) : 0)))[gg / gpg] = part;
+}
+
+// LDS bytes of one staged activation vector of the fused kernel (Q4_K: padded).
+__host__ __device__ inline int fused_xstage(int dt, int h) {
+    return naiwa_stage_bytes(dt, h) + (dt == NAIWA_Q4_K ? 16 * (h / NAIWA_QK_K) : 0);
+}
+
+// Poll the tagged h vectors of sorted pairs [v0, v0 + nv) (I/2 words each,
+// two 16-bit values of format DD per word) and stage them at dst.
+template <int DD>
+__device__ inline void stage_h(const Params& p, const Smem& sm, int v0, int nv, uint8_t* dst, int stride,
+                               uint32_t tag) {
+    constexpr int gpg = Fmt<DD>::kSumSpan / 4;
+    const int I = p.I, I2 = I / 2, gpv = I / 4, total = nv * gpv;
+    for (int g0 = 0; g0 < total; g0 += kHG * kThreads) {
+        u64 w[2 * kHG];
+        auto addr = [&](int j) -> const u64* {
+            const int g = g0 + threadIdx.x + (j >> 1) * kThreads;
+            if (g >= total) return nullptr;
+            const int v = g / gpv, gg = g % gpv;
+            return p.h + (size_t)sm.sorted[v0 + v] * I2 + 2 * gg + (j & 1);
+        };
+        issue_tagged(w, addr, tag);
+        wait_tagged(w, addr, tag, p);
 #pragma unroll
-    for (int j = 0; j < kXPre; ++j) {
-        const int g = threadIdx.x + j * kThreads;
-        const bool in = g < ngroups_total;
-        float part = 0.0f;
-        if (in) {
-            const int t = g / gpt_h, gg = g % gpt_h;
-            uint32_t* words = (uint32_t*)(dyn + t * xstage);
-            float v[4] = {naiwa_bf16_to_f32(xr[j].x & 0xffffu), naiwa_bf16_to_f32(xr[j].x >> 16),
-                          naiwa_bf16_to_f32(xr[j].y & 0xffffu), naiwa_bf16_to_f32(xr[j].y >> 16)};
-            uint32_t hh[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                hh[i] = Fmt<DG>::to16(v[i]);
-                v[i] = Fmt<DG>::from16(hh[i]);
+        for (int j = 0; j < kHG; ++j) {
+            const int g = g0 + threadIdx.x + j * kThreads;
+            const bool in = g < total;
+            const int v = in ? g / gpv : 0, gg = in ? g % gpv : 0;
+            const uint32_t A = (uint32_t)w[2 * j], B = (uint32_t)w[2 * j + 1]; // (h0, h1), (h2, h3)
+            float part = 0.0f;
+            if (in) {
+                uint32_t* words = (uint32_t*)(dst + v * stride);
+                words[2 * gg] = (A & 0xffffu) | (B << 16);
+                words[2 * gg + 1] = (A >> 16) | (B & 0xffff0000u);
+                part = (Fmt<DD>::from16(A & 0xffffu) + Fmt<DD>::from16(A >> 16)) +
+                       (Fmt<DD>::from16(B & 0xffffu) + Fmt<DD>::from16(B >> 16));
             }
-            words[2 * gg] = hh[0] | (hh[2] << 16);
-            words[2 * gg + 1] = hh[1] | (hh[3] << 16);
-            part = (v[0] + v[1]) + (v[2] + v[3]);
-        }
-        part = naiwa_group_sum<gpg>(part);
-        if (in && (g % gpg) == 0) {
-            const int t = g / gpt_h, gg = g % gpt_h;
-            float* sums = (float*)((uint32_t*)(dyn + t * xstage) + H / 2);
-            sums[gg / gpg] = part;
+            part = naiwa_group_sum<gpg>(part);
+            if (in && (gg % gpg) == 0) ((float*)((uint32_t*)(dst + v * stride) + I / 2))[gg / gpg] = part;
         }
     }
+}
+
+// The pointer, as a value the compiler cannot see through: address math on it
+// is then redone inside the layer loop instead of being hoisted out and kept
+// live in registers across all layers.
+template <class T>
+__device__ __forceinline__ T* opaque(T* ptr) {
+    asm volatile("" : "+s"(ptr));
+    return ptr;
 }
 
 template <int DG, int DD>
@@ -478,117 +533,167 @@ stack_kernel(Params p) {
     const int G = gridDim.x, bid = blockIdx.x;
     const int H = p.H, I = p.I, E = p.E, k = p.k, rows = p.rows;
     const int npairs = rows * k;
-    const int xstage = naiwa_stage_bytes(DG, H);
+    const int xstage = fused_xstage(DG, H);
     const int hstage = naiwa_stage_bytes(DD, I);
     const int nchunks = H / kChunk;
+    const int nprod = min(G, nchunks);        // workgroups that own chunks
+    const int nlead = min(kLeaders, G);
     const int64_t rb = naiwa_row_bytes(DG == NAIWA_Q8_0_ODD ? NAIWA_Q8_0 : DG, H);
     const int64_t drb = naiwa_row_bytes(DD == NAIWA_Q8_0_ODD ? NAIWA_Q8_0 : DD, I);
     const int nb = H / NAIWA_QK_K;            // Q4_K blocks per gate/up row
     const int nu = Fmt<DG>::units(H);
+    const int dnu = Fmt<DD>::units(I);
     const int gpt_h = H / 4;                  // 4-value groups per token
-    unsigned epoch = 0;
-    uint32_t touch = 0;
+    const int half_h = H / 2;                 // tagged words per token
+    const int nlog = rows * E;
+    uint8_t* const hdyn = dyn + rows * xstage;      // h staging, after the activations
+    uint8_t* const ddyn = hdyn + kCPairs * hstage;  // prefetched down rows, after the h staging
 
-    // ---- prologue: layer descriptors into LDS, layer 0's router logits ----
+    // ---- prologue: layer descriptors into LDS; own chunks of x; layer-0 logits ----
     mark(p, p.n_layers, 0);
     for (int i = tid; i < p.n_layers * (int)(sizeof(LayerDev) / 8); i += kThreads)
         reinterpret_cast<unsigned long long*>(layers_lds)[i] =
             reinterpret_cast<const unsigned long long*>(p.layers)[i];
-    __syncthreads();
     {
-        long long acc[kPartPerThread];
-#pragma unroll
-        for (int j = 0; j < kPartPerThread; ++j) acc[j] = 0;
-        for (int cp = bid; cp < nchunks; cp += G) {
-            const int c = chunk_at(cp, nchunks);
-            __syncthreads();
-            if (tid < rows * kChunk) {
-                const int t = tid / kChunk, i = tid % kChunk;
-                sm.xnew[t][i] = naiwa_bf16_to_f32(p.x[(size_t)t * H + c * kChunk + i]);
+        const uint32_t tag0 = layer_tag(p, 0);
+        if (tid < rows * kChunk / 2) {
+            const int t = tid / (kChunk / 2), pi = tid % (kChunk / 2);
+            for (int cp = bid, ci = 0; cp < nchunks; cp += G, ++ci) {
+                const int c = chunk_at(cp, nchunks);
+                // written before the launch; each workgroup reads only its own chunks
+                const uint32_t pr = *reinterpret_cast<const uint32_t*>(p.x + (size_t)t * H + c * kChunk + 2 * pi);
+                sm.xown[ci][t][2 * pi] = naiwa_bf16_to_f32(pr & 0xffffu);
+                sm.xown[ci][t][2 * pi + 1] = naiwa_bf16_to_f32(pr >> 16);
+                st64(&p.xt[(size_t)t * half_h + c * (kChunk / 2) + pi], tagged(tag0, pr));
             }
-            __syncthreads();
-            router_chunk_accumulate(p, layers_lds[0].router, c * kChunk, sm.xnew, acc);
         }
-        router_store_partials(p, acc);
+        __syncthreads();
+        if (bid < nprod) {
+            long long acc[kPartPerThread];
+#pragma unroll
+            for (int j = 0; j < kPartPerThread; ++j) acc[j] = 0;
+            const float* W = layers_lds[0].router;
+            for (int cp = bid, ci = 0; cp < nchunks; cp += G, ++ci) {
+                const int f0 = chunk_at(cp, nchunks) * kChunk;
+                router_chunk_accumulate<NAIWA_AS_GLOBAL>(p, [&](int e) { return W + (size_t)e * H + f0; }, sm.xown[ci], acc);
+            }
+            store_partials(p, acc, tag0);
+        }
         mark(p, p.n_layers, 1);
-        barrier_reduce(p, ++epoch);
+        if (bid < nlead) leader_reduce(p, nprod, tag0);
         mark(p, p.n_layers, 2);
     }
 
     for (int l = 0; l < p.n_layers; ++l) {
+        p.h = opaque(p.h);
+        p.part = opaque(p.part);
+        p.logits = opaque(p.logits);
+        p.xt = opaque(p.xt);
+        p.x = opaque(p.x);
         const LayerDev L = layers_lds[l];
-        // ---- A: route (every block, identically) ----
-        // one burst: the logits and (up to kXPre groups per thread) the activations
-        long long lgv[kPartPerThread];
-        uint2 xr[kXPre];
-        const int nlog = rows * E, ngroups = rows * gpt_h;
+        const uint32_t tag = layer_tag(p, l);
+        const bool last = l + 1 == p.n_layers;
+        const uint32_t tag_next = layer_tag(p, l + 1);
+        const u64* xt_l = p.xt + (size_t)(l & 1) * rows * half_h;
+
+        // ---- A: poll logits + activations, rank, weights, segments ----
+        const int ngroups = rows * gpt_h;
+        for (int g0 = 0; g0 < ngroups; g0 += kXG * kThreads) {
+            u64 xw[2 * kXG];
+            auto xaddr = [&](int j) -> const u64* {
+                const int g = g0 + tid + (j >> 1) * kThreads;
+                if (g >= ngroups) return nullptr;
+                return xt_l + (size_t)(g / gpt_h) * half_h + 2 * (g % gpt_h) + (j & 1);
+            };
+            issue_tagged(xw, xaddr, tag);
+            if (g0 == 0) {
+                u64 lw[kPartPerThread];
+                auto laddr = [&](int j) -> const u64* {
+                    const int i = tid + j * kThreads;
+                    return i < nlog ? p.logits + i : nullptr;
+                };
+                issue_tagged(lw, laddr, tag);
+                if (L.slot_of && tid < E) sm.slot_tab[tid] = naiwa_ld<int32_t, NAIWA_AS_GLOBAL>(L.slot_of + tid);
+                wait_tagged(lw, laddr, tag, p);
 #pragma unroll
-        for (int j = 0; j < kPartPerThread; ++j) {
-            const int i = tid + j * kThreads;
-            lgv[j] = i < nlog ? ld_coh(&p.logits[i]) : 0;
-        }
+                for (int j = 0; j < kPartPerThread; ++j) {
+                    const int i = tid + j * kThreads;
+                    if (i < nlog) {
+                        const float f = __uint_as_float((uint32_t)lw[j]);
+                        sm.lg[i / E][i % E] = f;
+                        sm.key[i / E][i % E] = rank_key(f, i % E);
+                    }
+                }
+                if ((E & 1) && tid < rows) sm.key[tid][E] = 0; // pad: below every real key
+            }
+            wait_tagged(xw, xaddr, tag, p);
 #pragma unroll
-        for (int j = 0; j < kXPre; ++j) {
-            const int g = tid + j * kThreads;
-            xr[j] = g < ngroups ? naiwa_ld8<true>(p.x + (size_t)(g / gpt_h) * H + 4 * (g % gpt_h))
-                                : make_uint2(0u, 0u);
-        }
-#pragma unroll
-        for (int j = 0; j < kPartPerThread; ++j) {
-            const int i = tid + j * kThreads;
-            if (i < nlog) sm.lg[i / E][i % E] = naiwa_router_fix_to_f32(lgv[j]);
-        }
-        if (E & 3) {
-            // the ranking reads whole float4s: pad each row with -inf, which
-            // neither beats nor ties a finite logit
-            const int pad = 4 - (E & 3);
-            if (tid < rows * pad) sm.lg[tid / pad][E + tid % pad] = -INFINITY;
+            for (int j = 0; j < kXG; ++j) {
+                const int g = g0 + tid + j * kThreads;
+                const bool in = g < ngroups;
+                const int t = in ? g / gpt_h : 0, gg = in ? g % gpt_h : 0;
+                const uint32_t a = (uint32_t)xw[2 * j], b = (uint32_t)xw[2 * j + 1];
+                stage_group<DG, DG == NAIWA_Q4_K>(naiwa_bf16_to_f32(a & 0xffffu), naiwa_bf16_to_f32(a >> 16),
+                                naiwa_bf16_to_f32(b & 0xffffu), naiwa_bf16_to_f32(b >> 16), in, gg,
+                                dyn + t * xstage, H);
+            }
         }
         __syncthreads();
         mark(p, l, 0);
-        // rank of every (token, expert): ties to the lower id (top_k_ids order)
-        for (int t = 0; t < rows; ++t) {
-            for (int e = tid; e < E; e += kThreads) {
-                const float me = sm.lg[t][e];
-                int rank = 0;
-                const float4* lv = reinterpret_cast<const float4*>(sm.lg[t]);
+        {
+            // rank of every (token, expert): the number of keys above its own;
+            // tpi lanes per item split the comparisons
+            const int items = rows * E;
+            const int tpi = items * 4 <= kThreads ? 4 : (items * 2 <= kThreads ? 2 : 1);
+            const int sub = tid % tpi;
+            const int half_e = (E + 1) / 2;
+            for (int it = tid / tpi; it < (items + (kThreads / tpi) - 1) / (kThreads / tpi) * (kThreads / tpi);
+                 it += kThreads / tpi) {
+                const bool in = it < items;
+                const int t = in ? it / E : 0, e = in ? it % E : 0;
+                const u64 me = sm.key[t][e];
+                const ulonglong2* kv = reinterpret_cast<const ulonglong2*>(sm.key[t]);
+                int cnt = 0;
+                if (in) {
 #pragma unroll 4
-                for (int o4 = 0; o4 < (E + 3) / 4; ++o4) {
-                    const float4 v = lv[o4];
-                    const int o = 4 * o4;
-                    rank += (v.x > me) | ((v.x == me) & (o < e));
-                    rank += (v.y > me) | ((v.y == me) & (o + 1 < e));
-                    rank += (v.z > me) | ((v.z == me) & (o + 2 < e));
-                    rank += (v.w > me) | ((v.w == me) & (o + 3 < e));
+                    for (int o = sub; o < half_e; o += tpi) {
+                        const ulonglong2 v = kv[o];
+                        cnt += (v.x > me) + (v.y > me);
+                    }
                 }
-                if (rank < k) {
-                    sm.top_ids[t][rank] = (uint32_t)e;
-                    sm.top_ex[t][rank] = me;
+                if (tpi >= 2) cnt += __builtin_amdgcn_update_dpp(0, cnt, 0xB1, 0xF, 0xF, true);
+                if (tpi >= 4) cnt += __builtin_amdgcn_update_dpp(0, cnt, 0x4E, 0xF, 0xF, true);
+                if (in && sub == 0 && cnt < k) {
+                    sm.top_ids[t][cnt] = (uint32_t)e;
+                    sm.top_ex[t][cnt] = sm.lg[t][e];
                 }
             }
         }
         __syncthreads();
         mark(p, l, 1);
         if (wave == 0) {
-            // weights (rank-order sums, the oracle's order), slot lookup, and the
-            // grouping of valid pairs by slot: one pair per lane
+            // weights (denominators summed in rank order, as the oracle does), slot
+            // lookup, and the grouping of valid pairs by slot: one pair per lane
             const int q = lane;
             const bool inp = q < npairs;
             const int t = inp ? q / k : 0, j = inp ? q % k : 0;
-            float w = 0.0f;
-            uint32_t e = 0;
+            const float mx = sm.top_ex[t][0];
+            const uint32_t e = inp ? sm.top_ids[t][j] : 0u;
+            const float ex = inp ? expf(sm.top_ex[t][j] - mx) : 0.0f;
+            sm.exv[q] = ex;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            float denom = 0.0f;
             if (inp) {
-                const float mx = sm.top_ex[t][0];
-                float denom = 0.0f;
                 if (p.mode == NAIWA_ROUTE_SOFTMAX_TOPK) {
                     for (int o = 0; o < E; ++o) denom += expf(sm.lg[t][o] - mx);
                 } else {
-                    for (int o = 0; o < k; ++o) denom += expf(sm.top_ex[t][o] - mx);
+                    for (int o = 0; o < k; ++o) denom += sm.exv[t * k + o];
                 }
-                w = expf(sm.top_ex[t][j] - mx) / denom;
-                e = sm.top_ids[t][j];
             }
-            const int32_t s = inp ? (L.slot_of ? L.slot_of[e] : (int32_t)e) : -1;
+            const float w = inp ? ex / denom : 0.0f;
+            const int32_t s = inp ? (L.slot_of ? sm.slot_tab[e] : (int32_t)e) : -1;
             const bool ok = inp && s >= 0 && s < L.slots;
             if (inp && !ok && bid == 0) atomicAdd(&p.status[1], 1);
             if (inp && bid == 0 && p.ids_out) {
@@ -596,78 +701,33 @@ stack_kernel(Params p) {
                 p.w_out[(size_t)l * npairs + q] = w;
             }
             const bool valid = ok && w != 0.0f;
-            const uint32_t sq = valid ? (uint32_t)s : 0u;
-            sm.pair_slot[q] = sq;
+            // sort key (slot, pair); invalid pairs sort last
+            const uint32_t key = valid ? (((uint32_t)s << 6) | (uint32_t)q) : 0xFFFFFFFFu;
+            int rank = 0;
+            for (int o = 0; o < npairs; ++o) rank += (uint32_t)__builtin_amdgcn_readlane((int)key, o) < key;
+            sm.pair_slot[q] = valid ? (uint32_t)s : 0u;
             sm.pair_w[q] = valid ? w : 0.0f;
+            if (valid) {
+                sm.sorted[rank] = (uint32_t)q;
+                sm.srt_slot[rank] = (uint32_t)s;
+            }
+            const unsigned long long valids = __ballot(valid);
+            const int nvalid = __popcll(valids);
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            int rank = 0;
-            bool start = valid;
-            for (int o = 0; o < npairs; ++o) {
-                const bool vo = sm.pair_w[o] != 0.0f;
-                const uint32_t so = sm.pair_slot[o];
-                if (vo) {
-                    rank += so < sq || (so == sq && o < q);
-                    if (so == sq && o < q) start = false;
-                }
-            }
+            // lane r looks at sorted position r: a segment starts where the slot changes
+            const bool start = lane < nvalid && (lane == 0 || sm.srt_slot[lane] != sm.srt_slot[lane - 1]);
             const unsigned long long starts = __ballot(start);
-            const unsigned long long valids = __ballot(valid);
-            int segidx = 0;
-            for (int o = 0; o < npairs; ++o) segidx += ((starts >> o) & 1ull) && sm.pair_slot[o] < sq;
-            if (valid) sm.sorted[rank] = (uint32_t)q;
             if (start) {
-                sm.seg_begin[segidx] = (uint32_t)rank;
-                sm.seg_slot[segidx] = sq;
+                const int si = __popcll(starts & ((1ull << lane) - 1ull));
+                sm.seg_begin[si] = (uint32_t)lane;
+                sm.seg_slot[si] = sm.srt_slot[lane];
             }
             if (lane == 0) {
                 const int ns = __popcll(starts);
-                sm.seg_begin[ns] = (uint32_t)__popcll(valids);
+                sm.seg_begin[ns] = (uint32_t)nvalid;
                 sm.nseg = ns;
-            }
-        }
-        // every thread converts the activation groups it loaded with the logits
-        convert_x_groups<DG>(xr, min(ngroups, kXPre * kThreads), gpt_h, dyn, xstage, H);
-        if (ngroups > kXPre * kThreads) {
-            // tokens beyond the first burst
-            for (int g0 = kXPre * kThreads; g0 < ngroups; g0 += kXPre * kThreads) {
-                uint2 xr2[kXPre];
-#pragma unroll
-                for (int j = 0; j < kXPre; ++j) {
-                    const int g = g0 + tid + j * kThreads;
-                    xr2[j] = g < ngroups ? naiwa_ld8<true>(p.x + (size_t)(g / gpt_h) * H + 4 * (g % gpt_h))
-                                         : make_uint2(0u, 0u);
-                }
-                // shift the group numbering: convert_x_groups counts from 0
-                constexpr int span = Fmt<DG>::kSumSpan;
-                constexpr int gpg = span / 4;
-#pragma unroll
-                for (int j = 0; j < kXPre; ++j) {
-                    const int g = g0 + tid + j * kThreads;
-                    const bool in = g < ngroups;
-                    float part = 0.0f;
-                    if (in) {
-                        const int t = g / gpt_h, gg = g % gpt_h;
-                        uint32_t* words = (uint32_t*)(dyn + t * xstage);
-                        float v[4] = {naiwa_bf16_to_f32(xr2[j].x & 0xffffu), naiwa_bf16_to_f32(xr2[j].x >> 16),
-                                      naiwa_bf16_to_f32(xr2[j].y & 0xffffu), naiwa_bf16_to_f32(xr2[j].y >> 16)};
-                        uint32_t hh[4];
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            hh[i] = Fmt<DG>::to16(v[i]);
-                            v[i] = Fmt<DG>::from16(hh[i]);
-                        }
-                        words[2 * gg] = hh[0] | (hh[2] << 16);
-                        words[2 * gg + 1] = hh[1] | (hh[3] << 16);
-                        part = (v[0] + v[1]) + (v[2] + v[3]);
-                    }
-                    part = naiwa_group_sum<gpg>(part);
-                    if (in && (g % gpg) == 0) {
-                        const int t = g / gpt_h, gg = g % gpt_h;
-                        ((float*)((uint32_t*)(dyn + t * xstage) + H / 2))[gg / gpg] = part;
-                    }
-                }
             }
         }
         __syncthreads();
@@ -675,167 +735,189 @@ stack_kernel(Params p) {
         const int nvalid = (int)sm.seg_begin[nseg];
         mark(p, l, 2);
 
-        // ---- B: gate/up ----
-        const int total = nseg * I;
+        // ---- B: gate/up, with phase C's down rows and router columns loaded alongside ----
+        const int total = nseg * (I / 2);        // (segment, row pair) items
         const int per = (total + G - 1) / G;
         const int q0 = bid * per, q1 = min(total, q0 + per);
+        const bool owner = bid < nchunks;
+        const int c0 = owner ? chunk_at(bid, nchunks) : 0;
+        const int nitems = kChunk * nvalid;
+        // one chunk, all (feature, pair) rows in registers, each row within kDUM units per lane
+        const bool direct = p.down_lds && owner && nchunks <= G && nitems <= kGroups * kDJ &&
+                            dnu <= NAIWA_GROUP * kDUM;
+        // gate/up work item q = (segment, row pair); fa/fb hold the pair's rows,
+        // fc/fd the group's next pair (loads in flight)
+        Q4Row fa, fb, fc, fd;
+        const int qa = q0 + grp, qb = qa + kGroups;
+        const int I2 = I / 2;
+        auto pair_rows = [&](int q, Q4Row& x0, Q4Row& x1) {
+            const uint8_t* r0 = q4_row_ptr(L, sm.seg_slot[q / I2], 2 * (q % I2), rb, lr);
+            q4_block_load(r0, lr & 7, nb, x0);
+            q4_block_load(r0 + rb, lr & 7, nb, x1);
+        };
         if constexpr (DG == NAIWA_Q4_K) {
-            Q4Row f;
-            const int qa = q0 + grp;
-            if (qa < q1) q4_block_load(q4_row_ptr(L, sm.seg_slot[qa / I], qa % I, rb, lr), lr & 7, nb, f);
-            mark(p, l, 3);
-            // touch the down rows of this block's C chunks and the next router's
-            // columns (loads issued now, consumed after the barrier)
-            uint32_t tv[8];
-            {
-                // the rows of this block's first chunk c span [c*8*drb, (c+1)*8*drb):
-                // one dword of every 16-byte piece that starts inside the span
-                // (rows are 4-byte multiples, so each dword lies inside it)
-                const int c = chunk_at(bid < nchunks ? bid : 0, nchunks);
-                const int64_t lo = (int64_t)c * kChunk * drb, hi = lo + kChunk * drb;
-                const int64_t a0 = lo & ~int64_t(15);
-                const int per_seg = (int)((hi - a0 + 15) / 16);
-                const int npieces = bid < nchunks ? nseg * per_seg : 0;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int i = tid + j * kThreads;
-                    tv[j] = 0;
-                    if (i < npieces) {
-                        const int sg = i / per_seg, piece = i % per_seg;
-                        const int64_t off = piece == 0 ? lo : a0 + 16 * (int64_t)piece;
-                        tv[j] = *reinterpret_cast<const uint32_t*>(L.down + (int64_t)sm.seg_slot[sg] * L.down_stride + off);
-                    }
+            if (qa < q1) pair_rows(qa, fa, fb);
+            if (qb < q1) pair_rows(qb, fc, fd);
+        }
+        if (direct) {
+            // the chunk's 8 rows of each routed pair are contiguous in the bank:
+            // 16-byte piece P of the LDS area is piece P % ppp of pair P / ppp
+            const int ppp = (int)(kChunk * drb / 16);
+            const int npieces = nvalid * ppp;
+            for (int P0 = wave * 64; P0 < npieces; P0 += kThreads) {
+                const int P = P0 + lane;
+                if (P < npieces) {
+                    const int pi = P / ppp;
+                    const uint8_t* src = L.down + (int64_t)sm.pair_slot[sm.sorted[pi]] * L.down_stride +
+                                         (int64_t)c0 * kChunk * drb + (int64_t)(P - pi * ppp) * 16;
+                    lds_dma16(src, ddyn + (size_t)P0 * 16);
                 }
             }
-            mark(p, l, 4);
-            __syncthreads();
-            mark(p, l, 5);
-#pragma unroll 1
-            for (int q = qa, j = 0; q < q1; q += kGroups, ++j) {
-                if (j > 0) q4_block_load(q4_row_ptr(L, sm.seg_slot[q / I], q % I, rb, lr), lr & 7, nb, f);
-                q4_row_compute(p, sm, L, dyn, xstage, q, rb, nb, lr, f);
+            if (!last) {
+                // next layer's router columns of the chunk: wch[e][0..7], two pieces per expert
+                const float* Wn = layers_lds[l + 1].router + c0 * kChunk;
+                for (int P0 = wave * 64; P0 < 2 * E; P0 += kThreads) {
+                    const int P = P0 + lane;
+                    if (P < 2 * E) lds_dma16(Wn + (size_t)(P >> 1) * H + (P & 1) * 4, &sm.wch[0][0] + P0 * 4);
+                }
             }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) touch ^= tv[j];
+        }
+        mark(p, l, 3);
+        if constexpr (DG == NAIWA_Q4_K) {
+#pragma unroll 1
+            for (int q = qa; q < q1; q += kGroups) {
+                q4_pair_compute<DD>(p, sm, L, dyn, xstage, q, rb, nb, lr, fa, fb, tag);
+                fa = fc;
+                fb = fd;
+                if (q + 2 * kGroups < q1) pair_rows(q + 2 * kGroups, fc, fd);
+            }
         } else {
-            mark(p, l, 3);
-            mark(p, l, 4);
-            __syncthreads();
-            mark(p, l, 5);
 #pragma unroll 1
-            for (int q = q0 + grp; q < q1; q += kGroups) unit_row<DG>(p, sm, L, dyn, q, xstage, rb, nu, lr);
+            for (int q = qa; q < q1; q += kGroups) unit_pair<DG, DD>(p, sm, L, dyn, q, xstage, rb, nu, lr, tag);
         }
-        if (l + 1 < p.n_layers && tid < E) {
-            const float* Wn = layers_lds[l + 1].router;
-            for (int cp = bid; cp < nchunks; cp += G)
-                touch ^= __float_as_uint(Wn[(size_t)tid * H + chunk_at(cp, nchunks) * kChunk]);
-        }
-        mark(p, l, 6);
-        barrier_all(p, ++epoch);
-        mark(p, l, 7);
+        mark(p, l, 4);
 
-        // ---- C: down + ordered combine + residual + next router partials ----
-        long long racc[kPartPerThread];
+        // ---- C: down + ordered combine + residual + next layer's router partials ----
+        if (owner) {
+            long long racc[kPartPerThread];
 #pragma unroll
-        for (int j = 0; j < kPartPerThread; ++j) racc[j] = 0;
-        for (int cp = bid; cp < nchunks; cp += G) {
-            const int f0 = chunk_at(cp, nchunks) * kChunk;
-            // this chunk's current activations (the residual input)
-            uint32_t xo_pair = 0;
-            if (tid < rows * kChunk / 2) {
-                const int t = tid / (kChunk / 2), fi = 2 * (tid % (kChunk / 2));
-                xo_pair = ld_coh((const uint32_t*)(p.x + (size_t)t * H + f0 + fi));
-            }
-            for (int b0 = 0; b0 < nvalid; b0 += kCPairs) {
-                const int nbp = min(kCPairs, nvalid - b0);
-                __syncthreads();
-#pragma unroll 1
-                for (int v0 = 0; v0 < nbp; v0 += 8) {
-                    const void* srcs[8];
+            for (int j = 0; j < kPartPerThread; ++j) racc[j] = 0;
+            u64* xt_next = p.xt + (size_t)((l + 1) & 1) * rows * half_h;
+            for (int cp = bid, ci = 0; cp < nchunks; cp += G, ++ci) {
+                const int c = chunk_at(cp, nchunks);
+                const int f0 = c * kChunk;
+                for (int b0 = 0; b0 < nvalid; b0 += kCPairs) {
+                    const int nbp = min(kCPairs, nvalid - b0);
+                    if (ci > 0 || b0 > 0) __syncthreads(); // the previous pass's dots read hdyn
+                    stage_h<DD>(p, sm, b0, nbp, hdyn, hstage, tag);
+                    if (direct) asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // this wave's LDS prefetch
+                    __syncthreads();
+                    mark(p, l, 5);
+                    if (direct) {
+                        // one pass (nvalid <= kCPairs), rows already in LDS (item it at it * drb)
 #pragma unroll
-                    for (int i = 0; i < 8; ++i)
-                        srcs[i] = p.h + (size_t)sm.sorted[b0 + min(v0 + i, nbp - 1)] * I;
-                    naiwa_stage_multi<DD, true, 8>(srcs, min(8, nbp - v0), false, I, dyn + v0 * hstage,
-                                                   hstage, tid, kThreads);
-                }
-                __syncthreads();
-                mark(p, l, 8);
-                constexpr int kCB = 2;
-                constexpr int DUM = 2;
-                const int dnu = Fmt<DD>::units(I);
-                const int nitems = kChunk * nbp;
-                for (int it0 = grp; it0 < nitems; it0 += kGroups * kCB) {
-                    typename Fmt<DD>::Frag fr[kCB][DUM];
-                    float acc[kCB];
+                        for (int j = 0; j < kDJ; ++j) {
+                            const int it = grp + kGroups * j;
+                            const int pi = min(it, nitems - 1) / kChunk;
+                            const uint32_t* words = (const uint32_t*)(hdyn + pi * hstage);
+                            const uint8_t* drow = ddyn + (size_t)min(it, nitems - 1) * drb;
+                            float acc = 0.0f;
+                            if (it < nitems) {
 #pragma unroll
-                    for (int j = 0; j < kCB; ++j) acc[j] = 0.0f;
-                    for (int base = lr; base < dnu; base += NAIWA_GROUP * DUM) {
-#pragma unroll
-                        for (int j = 0; j < kCB; ++j) {
-                            const int it = min(it0 + j * kGroups, nitems - 1);
-                            const int fi = it % kChunk, pi = it / kChunk;
-                            const uint8_t* drow = L.down + (int64_t)sm.pair_slot[sm.sorted[b0 + pi]] * L.down_stride +
-                                                  (int64_t)(f0 + fi) * drb;
-#pragma unroll
-                            for (int i = 0; i < DUM; ++i) {
-                                const int u = base + NAIWA_GROUP * i;
-                                if (u < dnu) fr[j][i] = Fmt<DD>::load(drow, u);
+                                for (int i = 0; i < kDUM; ++i) {
+                                    const int u = lr + NAIWA_GROUP * i;
+                                    if (u < dnu)
+                                        acc += Fmt<DD>::dot(Fmt<DD>::template load<NAIWA_AS_LDS>(drow, u), u, words,
+                                                            (const float*)(words + I / 2));
+                                }
                             }
+                            const float v = naiwa_group_sum<NAIWA_GROUP>(acc);
+                            if (it < nitems && lr == 0) sm.partial[it % kChunk][pi] = v;
                         }
+                    } else {
+                        constexpr int DUM = 2;
+                        const int nit = kChunk * nbp;
+                        for (int it0 = grp; it0 < nit; it0 += kGroups * kCB) {
+                            typename Fmt<DD>::Frag frg[kCB][DUM];
+                            float acc[kCB];
 #pragma unroll
-                        for (int j = 0; j < kCB; ++j) {
-                            const int it = min(it0 + j * kGroups, nitems - 1);
-                            const int pi = it / kChunk;
-                            const uint32_t* words = (const uint32_t*)(dyn + pi * hstage);
+                            for (int j = 0; j < kCB; ++j) acc[j] = 0.0f;
+                            for (int base = lr; base < dnu; base += NAIWA_GROUP * DUM) {
 #pragma unroll
-                            for (int i = 0; i < DUM; ++i) {
-                                const int u = base + NAIWA_GROUP * i;
-                                if (u < dnu) acc[j] += Fmt<DD>::dot(fr[j][i], u, words, (const float*)(words + I / 2));
+                                for (int j = 0; j < kCB; ++j) {
+                                    const int it = min(it0 + j * kGroups, nit - 1);
+                                    const int fi = it % kChunk, pi = it / kChunk;
+                                    const uint8_t* drow = L.down +
+                                                          (int64_t)sm.pair_slot[sm.sorted[b0 + pi]] * L.down_stride +
+                                                          (int64_t)(f0 + fi) * drb;
+#pragma unroll
+                                    for (int i = 0; i < DUM; ++i) {
+                                        const int u = base + NAIWA_GROUP * i;
+                                        if (u < dnu) frg[j][i] = Fmt<DD>::template load<NAIWA_AS_GLOBAL>(drow, u);
+                                    }
+                                }
+#pragma unroll
+                                for (int j = 0; j < kCB; ++j) {
+                                    const int it = min(it0 + j * kGroups, nit - 1);
+                                    const uint32_t* words = (const uint32_t*)(hdyn + (it / kChunk) * hstage);
+#pragma unroll
+                                    for (int i = 0; i < DUM; ++i) {
+                                        const int u = base + NAIWA_GROUP * i;
+                                        if (u < dnu)
+                                            acc[j] += Fmt<DD>::dot(frg[j][i], u, words, (const float*)(words + I / 2));
+                                    }
+                                }
+                            }
+#pragma unroll
+                            for (int j = 0; j < kCB; ++j) {
+                                const int it = it0 + j * kGroups;
+                                const float v = naiwa_group_sum<NAIWA_GROUP>(acc[j]);
+                                if (it < nit && lr == 0) sm.partial[it % kChunk][b0 + it / kChunk] = v;
                             }
                         }
                     }
-#pragma unroll
-                    for (int j = 0; j < kCB; ++j) {
-                        const int it = it0 + j * kGroups;
-                        const float v = naiwa_group_sum<NAIWA_GROUP>(acc[j]);
-                        if (it < nitems && lr == 0) sm.partial[it % kChunk][b0 + it / kChunk] = v;
+                }
+                __syncthreads();
+                mark(p, l, 6);
+                if (tid < rows * kChunk) {
+                    // ascending slot order per token, then the residual in f32 and the bf16 store value
+                    const int t = tid / kChunk, fi = tid % kChunk;
+                    float y = 0.0f;
+                    for (int i = 0; i < nvalid; ++i) {
+                        const uint32_t pr = sm.sorted[i];
+                        if ((int)pr / k == t) y += sm.pair_w[pr] * sm.partial[fi][i];
+                    }
+                    sm.xown[ci][t][fi] = naiwa_bf16_to_f32(naiwa_f32_to_bf16(sm.xown[ci][t][fi] + y));
+                }
+                __syncthreads();
+                if (tid < rows * kChunk / 2) {
+                    const int t = tid / (kChunk / 2), pi = tid % (kChunk / 2);
+                    const uint32_t pr = naiwa_f32_to_bf16(sm.xown[ci][t][2 * pi]) |
+                                        (naiwa_f32_to_bf16(sm.xown[ci][t][2 * pi + 1]) << 16);
+                    if (last)
+                        *(__attribute__((address_space(1))) uint32_t*)(p.x + (size_t)t * H + f0 + 2 * pi) = pr;
+                    else
+                        st64(&xt_next[(size_t)t * half_h + c * (kChunk / 2) + pi], tagged(tag_next, pr));
+                }
+                mark(p, l, 7);
+                if (!last) {
+                    if (direct) {
+                        router_chunk_accumulate<NAIWA_AS_LDS>(p, [&](int e) { return &sm.wch[e][0]; }, sm.xown[ci], racc);
+                    } else {
+                        const float* Wn = layers_lds[l + 1].router;
+                        router_chunk_accumulate<NAIWA_AS_GLOBAL>(p, [&](int e) { return Wn + (size_t)e * H + f0; },
+                                                                 sm.xown[ci], racc);
                     }
                 }
             }
-            if (tid < rows * kChunk / 2) {
-                const int t = tid / (kChunk / 2), fi = 2 * (tid % (kChunk / 2));
-                sm.xown[t][fi] = naiwa_bf16_to_f32(xo_pair & 0xffffu);
-                sm.xown[t][fi + 1] = naiwa_bf16_to_f32(xo_pair >> 16);
-            }
-            __syncthreads();
-            mark(p, l, 9);
-            if (tid < rows * kChunk) {
-                const int t = tid / kChunk, fi = tid % kChunk;
-                float y = 0.0f;
-                for (int i = 0; i < nvalid; ++i) {
-                    const uint32_t pr = sm.sorted[i];
-                    if ((int)pr / k == t) y += sm.pair_w[pr] * sm.partial[fi][i];
-                }
-                sm.xnew[t][fi] = naiwa_bf16_to_f32(naiwa_f32_to_bf16(sm.xown[t][fi] + y));
-            }
-            __syncthreads();
-            if (tid < rows * kChunk / 2) {
-                const int t = tid / (kChunk / 2), fi = 2 * (tid % (kChunk / 2));
-                const uint32_t packed = naiwa_f32_to_bf16(sm.xnew[t][fi]) |
-                                        (naiwa_f32_to_bf16(sm.xnew[t][fi + 1]) << 16);
-                st_coh((uint32_t*)(p.x + (size_t)t * H + f0 + fi), packed);
-            }
-            mark(p, l, 10);
-            if (l + 1 < p.n_layers) router_chunk_accumulate(p, layers_lds[l + 1].router, f0, sm.xnew, racc);
+            if (!last) store_partials(p, racc, tag_next);
         }
-        mark(p, l, 11);
-        if (l + 1 < p.n_layers) {
-            router_store_partials(p, racc);
-            barrier_reduce(p, ++epoch);
-        }
-        mark(p, l, 12);
+        mark(p, l, 8);
+        if (!last && bid < nlead) leader_reduce(p, nprod, tag_next);
+        mark(p, l, 9);
+        // LDS reuse across layers (dyn, sm) is ordered by this barrier
+        __syncthreads();
     }
-    if (touch == 0x9E3779B9u && p.never) p.status[2] = (int)touch;
 }
 
 __global__ void zero_u32(unsigned int* ptr, int n) {
@@ -860,7 +942,7 @@ int launch(const Params& prm, int blocks, size_t lds, hipStream_t st) {
     // The grid never exceeds the blocks every CU can hold at once; the
     // cooperative launch also makes the runtime check it.  NAIWA_STACK_LAUNCH=
     // normal uses a plain launch (profilers that cannot follow cooperative
-    // launches); the bounded barrier waits keep that safe.
+    // launches); the bounded waits keep that safe.
     static const bool normal = [] {
         const char* v = getenv("NAIWA_STACK_LAUNCH");
         return v && strcmp(v, "normal") == 0;
@@ -911,12 +993,18 @@ extern "C" int naiwa_stack_set_blocks_per_cu(int n) {
 }
 
 namespace {
-// status words live after the flag lines in the sync scratch
-constexpr size_t kStatusOff = 0;
+constexpr size_t kStatusOff = 0;   // status words at the start of the sync scratch
+constexpr int kMaxDev = 64;
+// Per device: the launch counter behind the tags, and how many bytes of the
+// tagged scratch are known to hold no current-looking tag (zeroed since the
+// buffer was allocated and since the counter last wrapped).
+uint32_t g_seq[kMaxDev];
+size_t g_tag_clean[kMaxDev];
+std::mutex g_seq_mu;
 }
 
-// Status of the last fused launches: barrier waits that gave up after their
-// 2 s bound, and routed experts that had no resident slot.  Synchronizes.
+// Status of the last fused launches: waits that gave up after their 2 s
+// bound, and routed experts that had no resident slot.  Synchronizes.
 extern "C" int naiwa_stack_status(int* barrier_timeouts, int* missing_experts) {
     int rc = 0;
     uint8_t* sync = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK + 1, 4096, &rc);
@@ -958,10 +1046,18 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     }
     const int fg = naiwa_kernel_fmt(L0.gate.dtype, H), fd = naiwa_kernel_fmt(L0.down.dtype, I);
     if (fg == NAIWA_Q8_0_ODD) return NAIWA_E_UNSUPPORTED;
-    const size_t lds_x = (size_t)rows * naiwa_stage_bytes(fg, H);
+    // dynamic LDS: activations | h staging | (when it fits) the prefetched down rows
+    constexpr size_t kMaxDynLds = 104 * 1024;   // 160 KB per CU minus the static LDS
+    const size_t lds_x = (size_t)rows * fused_xstage(fg, H);
     const size_t lds_h = (size_t)kCPairs * naiwa_stage_bytes(fd, I);
-    const size_t lds = lds_x > lds_h ? lds_x : lds_h;
-    if (lds > 96 * 1024) return NAIWA_E_UNSUPPORTED;
+    const int64_t drb = naiwa_row_bytes(L0.down.dtype, I);
+    size_t lds = lds_x + lds_h;
+    int down_lds = 0;
+    if (drb % 16 == 0 && lds + (size_t)kGroups * kDJ * drb <= kMaxDynLds) {
+        lds += (size_t)kGroups * kDJ * drb;
+        down_lds = 1;
+    }
+    if (lds > kMaxDynLds) return NAIWA_E_UNSUPPORTED;
 
     hipStream_t st = (hipStream_t)stream;
     int rc = 0, dev = 0, cus = 0, khz = 0;
@@ -981,16 +1077,38 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     const int blocks = cus * bpc;
     if (blocks < kLeaders || blocks > 4096) return NAIWA_E_UNSUPPORTED;
 
-    // scratch: h [kMaxPairs * I] f32 | part [blocks * rows * E] i64 | logits [rows * E] i64
-    const size_t h_bytes = ((size_t)kMaxPairs * I * 4 + 255) & ~size_t(255);
-    const size_t part_bytes = ((size_t)blocks * rows * E * 8 + 255) & ~size_t(255);
-    const size_t lg_bytes = ((size_t)rows * E * 8 + 255) & ~size_t(255);
-    uint8_t* ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK, h_bytes + part_bytes + lg_bytes, &rc);
+    const int nchunks = H / kChunk;
+    if ((nchunks + blocks - 1) / blocks > kMaxChunks) return NAIWA_E_UNSUPPORTED;
+    const int nprod = blocks < nchunks ? blocks : nchunks;
+    if (dev < 0 || dev >= kMaxDev) return NAIWA_E_UNSUPPORTED;
+
+    // tagged scratch: h [kMaxPairs][I] | partials [nprod][rows*E][2] | logits [rows*E] | x [2][rows][H/2]
+    auto a256 = [](size_t b) { return (b + 255) & ~size_t(255); };
+    const size_t h_bytes = a256((size_t)kMaxPairs * I * 8);
+    const size_t part_bytes = a256((size_t)nprod * rows * E * 16);
+    const size_t lg_bytes = a256((size_t)rows * E * 8);
+    const size_t xt_bytes = a256((size_t)2 * rows * (H / 2) * 8);
+    const size_t tag_bytes = h_bytes + part_bytes + lg_bytes + xt_bytes;
+    bool fresh = false;
+    uint8_t* ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK, tag_bytes, &rc, &fresh);
     if (!ws) return rc;
-    // sync scratch: status (256 B) | release lines | arrive lines
-    const size_t sync_bytes = 256 + (size_t)(kLeaders + blocks) * kLine * 4;
-    uint8_t* sync = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK + 1, sync_bytes, &rc);
+    uint8_t* sync = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK + 1, 256, &rc);
     if (!sync) return rc;
+    uint32_t seq = 0;
+    {
+        std::lock_guard<std::mutex> lock(g_seq_mu);
+        if (fresh) g_tag_clean[dev] = 0;
+        if (++g_seq[dev] >= (1u << 24)) { // tags hold seq << 8: start over on clean memory
+            g_seq[dev] = 1;
+            g_tag_clean[dev] = 0;
+        }
+        seq = g_seq[dev];
+        if (g_tag_clean[dev] < tag_bytes) {
+            const int n = (int)(tag_bytes / 4);
+            zero_u32<<<(n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096, 256, 0, st>>>((unsigned int*)ws, n);
+            g_tag_clean[dev] = tag_bytes;
+        }
+    }
 
     // layer descriptors on the device (re-uploaded only when they change)
     std::vector<LayerDev> desc(n_layers);
@@ -1035,23 +1153,22 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     prm.mode = mode;
     prm.act = act;
     prm.x = (uint16_t*)x;
-    prm.h = (float*)ws;
-    prm.part = (long long*)(ws + h_bytes);
-    prm.logits = (long long*)(ws + h_bytes + part_bytes);
+    prm.h = (u64*)ws;
+    prm.part = (u64*)(ws + h_bytes);
+    prm.logits = (u64*)(ws + h_bytes + part_bytes);
+    prm.xt = (u64*)(ws + h_bytes + part_bytes + lg_bytes);
     prm.status = (int*)(sync + kStatusOff);
-    prm.release = (unsigned*)(sync + 256);
-    prm.arrive = (unsigned*)(sync + 256 + (size_t)kLeaders * kLine * 4);
     prm.ids_out = ids_out;
     prm.w_out = w_out;
     prm.spin_limit = (uint64_t)khz * 2000ull; // 2 s
-    prm.never = 0;
+    prm.seq = seq;
+    prm.down_lds = down_lds;
     prm.trace = g_trace_enabled ? (unsigned long long*)naiwa_scratch(NAIWA_SCRATCH_STACK + 2,
                                                                      (size_t)2 * (n_layers + 1) * kTraceSlots * 8, &rc)
                                 : nullptr;
     if (g_trace_enabled && !prm.trace) return rc;
     g_trace_layers = n_layers;
-    const int nzero = (int)(sync_bytes / 4);
-    zero_u32<<<(nzero + 255) / 256, 256, 0, st>>>((unsigned int*)sync, nzero);
+    zero_u32<<<1, 64, 0, st>>>((unsigned int*)(sync + kStatusOff), 64);
     if (fg == NAIWA_Q4_K && fd == NAIWA_Q4_K) return launch<NAIWA_Q4_K, NAIWA_Q4_K>(prm, blocks, lds, st);
     if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0) return launch<NAIWA_Q4_K, NAIWA_Q8_0>(prm, blocks, lds, st);
     if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0_ODD) return launch<NAIWA_Q4_K, NAIWA_Q8_0_ODD>(prm, blocks, lds, st);

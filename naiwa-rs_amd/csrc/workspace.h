@@ -20,5 +20,8 @@ struct NaiwaScratch {
 // Returns a device pointer of at least `bytes` for (device, tag), growing the
 // buffer (with a device sync, since a kernel may still read the old one).
 void* naiwa_scratch(int tag, size_t bytes, int* rc);
+// As above; *fresh tells whether this call (re)allocated the buffer, whose
+// contents are then undefined.
+void* naiwa_scratch(int tag, size_t bytes, int* rc, bool* fresh);
 
 enum { NAIWA_SCRATCH_DECODE = 0, NAIWA_SCRATCH_ROUTER = 1, NAIWA_SCRATCH_STACK = 2, NAIWA_SCRATCH_TAGS = 6 };
