@@ -41,6 +41,16 @@ class Layer(C.Structure):
 
 STACK_LAYERED, STACK_FUSED = 0, 1
 
+STAGING_RING_FIRST = 1 << 30
+
+STATS_FIELDS = ("hits", "promotions", "misses", "staged", "lookahead_loads", "swaps", "lookahead_dropped",
+                "sync_waits", "pcie_misses", "pcie_bytes", "result_stalls")
+
+
+class CacheStats(C.Structure):
+    """naiwa_cache_stats (include/naiwa_policy.h)."""
+    _fields_ = [(f, C.c_uint64) for f in STATS_FIELDS]
+
 
 _lib: C.CDLL | None = None
 
@@ -95,6 +105,33 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_residual_add_bf16": (i32, [vp, vp, i64, i64]),
     "naiwa_stack_trace_enable": (i32, [i32]),
     "naiwa_stack_trace_read": (i32, [_P(u64), i32, _P(i32)]),
+    # include/naiwa_policy.h (host only)
+    "naiwa_cache_create": (i32, [i32, i32, i32, _P(vp)]),
+    "naiwa_cache_destroy": (i32, [vp]),
+    "naiwa_cache_route": (i32, [vp, vp, i32, i32, vp]),
+    "naiwa_cache_fill_candidate": (i32, [vp, _P(i32), _P(i32)]),
+    "naiwa_cache_lru_victim": (i32, [vp, vp, i32, _P(i32), _P(i32), _P(i32)]),
+    "naiwa_cache_admit": (i32, [vp, i32, _P(i32)]),
+    "naiwa_cache_replace": (i32, [vp, i32, vp, i32, _P(i32)]),
+    "naiwa_cache_publish": (i32, [vp, i32]),
+    "naiwa_cache_unreserve": (i32, [vp, i32]),
+    "naiwa_cache_promote_pick": (i32, [vp, vp, i32, i32, u64, vp, vp, _P(i32)]),
+    "naiwa_cache_slot_table": (i32, [vp, vp]),
+    "naiwa_cache_slot_state": (i32, [vp, i32, _P(i32), _P(i32), _P(u64)]),
+    "naiwa_cache_hit_counts": (i32, [vp, vp]),
+    "naiwa_cache_tick": (i32, [vp, _P(u64)]),
+    "naiwa_cache_seed_hits": (i32, [vp, vp]),
+    "naiwa_cache_place": (i32, [vp, i32, i32, u64]),
+    "naiwa_top_k_ids": (i32, [vp, i32, i32, vp, _P(i32)]),
+    "naiwa_union_by_votes": (i32, [vp, vp, i32, vp, i32, _P(i32)]),
+    "naiwa_streamed_misses": (i32, [vp, vp, i32, f32, i32, vp, _P(i32)]),
+    "naiwa_staging_ring_slots": (i32, []),
+    "naiwa_ring_create": (i32, [i32, _P(vp)]),
+    "naiwa_ring_destroy": (i32, [vp]),
+    "naiwa_ring_acquire": (i32, [vp, i32, _P(i32)]),
+    "naiwa_cache_stage": (i32, [vp, vp, vp, i32, i32, f32, vp, vp, vp, _P(i32)]),
+    "naiwa_stats_read": (i32, [vp, i32]),
+    "naiwa_stats_add": (i32, [vp]),
 }
 
 

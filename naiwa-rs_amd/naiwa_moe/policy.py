@@ -1,0 +1,206 @@
+"""Host-side expert-cache policy over include/naiwa_policy.h.
+
+Mirrors the reference's CachedLayer residency rules (src/moe/cached_layer.rs,
+src/moe/stages/route.rs, src/moe/stages/dma_miss.rs, src/moe/staging.rs) with
+the same names: route / fill_candidate / lru_victim / admit / replace /
+promote_staged selection, top_k_ids, union_by_votes, streamed_misses and the
+staging ring.  Everything runs in the C++ library on the host.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from ._lib import STAGING_RING_FIRST, STATS_FIELDS, CacheStats, check, lib
+
+
+def _u32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.uint32))
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.int32))
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data if a.size else None
+
+
+class ExpertCache:
+    """One layer's slot cache: `slots` slots, the first `usable` of which hold experts."""
+
+    def __init__(self, num_experts: int, slots: int, usable: int | None = None):
+        self.num_experts = num_experts
+        self.slots = slots
+        h = C.c_void_p()
+        check(lib().naiwa_cache_create(num_experts, slots, slots if usable is None else usable, C.byref(h)),
+              "cache_create")
+        self._h = h
+
+    def __del__(self):
+        if getattr(self, "_h", None) and self._h.value:
+            lib().naiwa_cache_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def route(self, ids) -> np.ndarray:
+        """Route::submit: returns slot per (row, k) pair, -1 for a miss."""
+        ids = _u32(ids)
+        rows, k = ids.shape
+        out = np.empty((rows, k), dtype=np.int32)
+        check(lib().naiwa_cache_route(self._h, _ptr(ids), rows, k, _ptr(out)), "cache_route")
+        return out
+
+    def fill_candidate(self) -> int | None:
+        e, found = C.c_int(), C.c_int()
+        check(lib().naiwa_cache_fill_candidate(self._h, C.byref(e), C.byref(found)), "fill_candidate")
+        return e.value if found.value else None
+
+    def lru_victim(self, protect=()) -> tuple[int, int] | None:
+        p = _i32(list(protect))
+        e, s, found = C.c_int(), C.c_int(), C.c_int()
+        check(lib().naiwa_cache_lru_victim(self._h, _ptr(p), p.size, C.byref(e), C.byref(s), C.byref(found)),
+              "lru_victim")
+        return (e.value, s.value) if found.value else None
+
+    def admit(self, expert: int) -> int | None:
+        s = C.c_int()
+        check(lib().naiwa_cache_admit(self._h, expert, C.byref(s)), "admit")
+        return s.value if s.value >= 0 else None
+
+    def replace(self, expert: int, protect=()) -> int | None:
+        p = _i32(list(protect))
+        s = C.c_int()
+        check(lib().naiwa_cache_replace(self._h, expert, _ptr(p), p.size, C.byref(s)), "replace")
+        return s.value if s.value >= 0 else None
+
+    def publish(self, slot: int) -> None:
+        check(lib().naiwa_cache_publish(self._h, slot), "publish")
+
+    def unreserve(self, slot: int) -> None:
+        check(lib().naiwa_cache_unreserve(self._h, slot), "unreserve")
+
+    def promote_pick(self, staged, cap: int = 1, min_hits: int = 4) -> list[tuple[int, int]]:
+        st = _u32(list(staged))
+        ex = np.empty(max(cap, 1), dtype=np.int32)
+        sl = np.empty(max(cap, 1), dtype=np.int32)
+        n = C.c_int()
+        check(lib().naiwa_cache_promote_pick(self._h, _ptr(st), st.size, cap, min_hits, _ptr(ex), _ptr(sl),
+                                             C.byref(n)), "promote_pick")
+        return [(int(ex[i]), int(sl[i])) for i in range(n.value)]
+
+    def slot_table(self) -> np.ndarray:
+        out = np.empty(self.num_experts, dtype=np.int32)
+        check(lib().naiwa_cache_slot_table(self._h, _ptr(out)), "slot_table")
+        return out
+
+    def slot_state(self, slot: int) -> tuple[int | None, bool, int]:
+        e, pub, lu = C.c_int(), C.c_int(), C.c_uint64()
+        check(lib().naiwa_cache_slot_state(self._h, slot, C.byref(e), C.byref(pub), C.byref(lu)), "slot_state")
+        return (e.value if e.value >= 0 else None, bool(pub.value), lu.value)
+
+    def hit_counts(self) -> np.ndarray:
+        out = np.empty(self.num_experts, dtype=np.uint64)
+        check(lib().naiwa_cache_hit_counts(self._h, _ptr(out)), "hit_counts")
+        return out
+
+    def seed_hits(self, counts) -> None:
+        c = np.ascontiguousarray(np.asarray(counts, dtype=np.uint64))
+        assert c.size == self.num_experts
+        check(lib().naiwa_cache_seed_hits(self._h, _ptr(c)), "seed_hits")
+
+    @property
+    def tick(self) -> int:
+        t = C.c_uint64()
+        check(lib().naiwa_cache_tick(self._h, C.byref(t)), "tick")
+        return t.value
+
+    def place(self, expert: int, slot: int, last_use: int = 0) -> None:
+        check(lib().naiwa_cache_place(self._h, expert, slot, last_use), "place")
+
+
+class StagingRing:
+    """The round-robin staging ring (ring slots are NAIWA_STAGING_RING_FIRST + position)."""
+
+    def __init__(self, length: int | None = None):
+        self.length = staging_ring_slots() if length is None else length
+        h = C.c_void_p()
+        check(lib().naiwa_ring_create(self.length, C.byref(h)), "ring_create")
+        self._h = h
+
+    def __del__(self):
+        if getattr(self, "_h", None) and self._h.value:
+            lib().naiwa_ring_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def acquire(self, n: int) -> int:
+        start = C.c_int()
+        check(lib().naiwa_ring_acquire(self._h, n, C.byref(start)), "ring_acquire")
+        return start.value
+
+    def stage(self, ids, w, slots, frac: float) -> list[tuple[int, int]]:
+        """stage_misses selection: updates `slots` in place (staged misses become ring slots) and
+        returns (expert, ring position) per staged expert."""
+        ids, w = _u32(ids), _f32(w)
+        rows, k = ids.shape
+        assert slots.dtype == np.int32 and slots.flags.c_contiguous and slots.shape == (rows, k)
+        chosen = np.empty(self.length, dtype=np.uint32)
+        pos = np.empty(self.length, dtype=np.int32)
+        n = C.c_int()
+        check(lib().naiwa_cache_stage(self._h, _ptr(ids), _ptr(w), rows, k, frac, _ptr(slots), _ptr(chosen),
+                                      _ptr(pos), C.byref(n)), "cache_stage")
+        return [(int(chosen[i]), int(pos[i])) for i in range(n.value)]
+
+
+def staging_ring_slots() -> int:
+    return int(lib().naiwa_staging_ring_slots())
+
+
+def top_k_ids(logits, k: int) -> list[int]:
+    x = _f32(logits)
+    out = np.empty(max(min(k, x.size), 1), dtype=np.uint32)
+    n = C.c_int()
+    check(lib().naiwa_top_k_ids(_ptr(x), x.size, k, _ptr(out), C.byref(n)), "top_k_ids")
+    return [int(v) for v in out[:n.value]]
+
+
+def union_by_votes(rankings) -> list[int]:
+    rankings = [list(r) for r in rankings]
+    flat = _u32([e for r in rankings for e in r])
+    lens = _i32([len(r) for r in rankings])
+    out = np.empty(max(flat.size, 1), dtype=np.uint32)
+    n = C.c_int()
+    check(lib().naiwa_union_by_votes(_ptr(flat), _ptr(lens), len(rankings), _ptr(out), out.size, C.byref(n)),
+          "union_by_votes")
+    return [int(v) for v in out[:n.value]]
+
+
+def streamed_misses(misses, frac: float, cap: int) -> list[int]:
+    """misses: rows of (id, weight) pairs, as the reference's Vec<Vec<(u32, f32)>>."""
+    flat = [p for row in misses for p in row]
+    ids = _u32([p[0] for p in flat])
+    w = _f32([p[1] for p in flat])
+    out = np.empty(max(cap, 1), dtype=np.uint32)
+    n = C.c_int()
+    check(lib().naiwa_streamed_misses(_ptr(ids), _ptr(w), ids.size, frac, cap, _ptr(out), C.byref(n)),
+          "streamed_misses")
+    return [int(v) for v in out[:n.value]]
+
+
+def stats(reset: bool = False) -> dict[str, int]:
+    s = CacheStats()
+    check(lib().naiwa_stats_read(C.byref(s), int(reset)), "stats_read")
+    return {f: int(getattr(s, f)) for f in STATS_FIELDS}
+
+
+def stats_add(**delta: int) -> None:
+    s = CacheStats(**{f: int(delta.get(f, 0)) for f in STATS_FIELDS})
+    check(lib().naiwa_stats_add(C.byref(s)), "stats_add")
+
+
+__all__ = ["ExpertCache", "StagingRing", "STAGING_RING_FIRST", "staging_ring_slots", "top_k_ids",
+           "union_by_votes", "streamed_misses", "stats", "stats_add"]
