@@ -18,8 +18,9 @@
  *                         src/moe/cached_layer.rs:357-363)
  *   naiwa_moe_gather      the per-bank grouping of src/moe/stages/gpu.rs:100-133
  *   naiwa_upload_expert   CopyStream::queue_async, src/copy_stream.rs:387-409
- *   naiwa_policy_*        the slot policy of src/moe/cached_layer.rs and
+ *   naiwa_cache_* etc.    the slot policy of src/moe/cached_layer.rs and
  *                         src/moe/stages/{route,dma_miss}.rs, src/moe/staging.rs
+ *                         (include/naiwa_policy.h)
  */
 #ifndef NAIWA_MOE_H
 #define NAIWA_MOE_H
@@ -158,6 +159,12 @@ int naiwa_moe_decode(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_b
  * [rows, k]; logits_out [rows, E] f32 or NULL.  H % 8 == 0, E <= 1024, k <= 32. */
 int naiwa_router_topk(const void* x, int x_dtype, const float* W, int rows, int H, int E, int k,
                       int mode, uint32_t* ids_out, float* w_out, float* logits_out, int64_t stream);
+/* As naiwa_router_topk with a per-expert f32 bias added to each logit after
+ * the fixed-point sum (logit = sum * 2^-32 + bias[e], one f32 add); bias may
+ * be null.  Routers with a bias term (and routing-skew studies) use it. */
+int naiwa_router_topk_biased(const void* x, int x_dtype, const float* W, const float* bias, int rows, int H,
+                             int E, int k, int mode, uint32_t* ids_out, float* w_out, float* logits_out,
+                             int64_t stream);
 
 /* Gather: stable counting sort of the n flattened ids by value.
  * perm_out[n] = flat (t*k + j) indices grouped by id, offsets_out[E+1] =
@@ -205,6 +212,18 @@ int naiwa_stack_trace_read(uint64_t* out, int capacity, int* n_layers);
 
 /* x[i] <- bf16(f32(x[i]) + y[i]) for i < n (the residual of the stack). */
 int naiwa_residual_add_bf16(void* x, const float* y, int64_t n, int64_t stream);
+
+/* ======================================================================== */
+/* Expert upload (CopyStream::queue_async + ReadFence, src/copy_stream.rs:   */
+/* 387-409): on copy_stream, wait for read_fence (an event the compute      */
+/* stream recorded after the last kernel that read the slot; 0 = none),     */
+/* then copy the expert's gate/up/down bytes host -> device, then record    */
+/* done_event (0 = none), which the compute stream waits on before reading  */
+/* the slot.  src must be pinned (naiwa_host_alloc) for the copies to be    */
+/* asynchronous DMA; it must stay valid until done_event completes.         */
+/* ======================================================================== */
+int naiwa_upload_expert(void* const dst[3], const void* const src[3], const size_t bytes[3],
+                        int64_t copy_stream, int64_t read_fence, int64_t done_event);
 
 /* ======================================================================== */
 /* Synthetic data (benchmarks and tests): n values of the N(mean, std)       */

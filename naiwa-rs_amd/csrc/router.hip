@@ -17,7 +17,7 @@ namespace {
 constexpr int kLogitThreads = 256;
 
 __global__ void __launch_bounds__(kLogitThreads)
-router_logits_kernel(const void* x, int x_bf16, const float* W, int rows, int H, int E,
+router_logits_kernel(const void* x, int x_bf16, const float* W, const float* bias, int rows, int H, int E,
                      float* logits) {
     __shared__ long long part[kLogitThreads / 64];
     const int e = blockIdx.x, tid = threadIdx.x;
@@ -36,7 +36,7 @@ router_logits_kernel(const void* x, int x_bf16, const float* W, int rows, int H,
         if (tid == 0) {
             long long s = 0;
             for (int i = 0; i < kLogitThreads / 64; ++i) s += part[i];
-            logits[(int64_t)t * E + e] = naiwa_router_fix_to_f32(s);
+            logits[(int64_t)t * E + e] = naiwa_router_fix_to_f32(s) + (bias ? bias[e] : 0.0f);
         }
         __syncthreads();
     }
@@ -63,9 +63,9 @@ router_topk_kernel(const float* logits, int E, int k, int mode, uint32_t* ids, f
 
 } // namespace
 
-extern "C" int naiwa_router_topk(const void* x, int x_dtype, const float* W, int rows, int H,
-                                 int E, int k, int mode, uint32_t* ids_out, float* w_out,
-                                 float* logits_out, int64_t stream) {
+extern "C" int naiwa_router_topk_biased(const void* x, int x_dtype, const float* W, const float* bias, int rows,
+                                        int H, int E, int k, int mode, uint32_t* ids_out, float* w_out,
+                                        float* logits_out, int64_t stream) {
     if (x_dtype != NAIWA_BF16 && x_dtype != NAIWA_F32) return NAIWA_E_UNSUPPORTED;
     if (mode < NAIWA_ROUTE_SOFTMAX_TOPK_RENORM || mode > NAIWA_ROUTE_SOFTMAX_TOPK)
         return NAIWA_E_UNSUPPORTED;
@@ -81,7 +81,13 @@ extern "C" int naiwa_router_topk(const void* x, int x_dtype, const float* W, int
         logits = (float*)naiwa_scratch(NAIWA_SCRATCH_ROUTER, (size_t)rows * E * 4, &rc);
         if (!logits) return rc;
     }
-    router_logits_kernel<<<E, kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, W, rows, H, E, logits);
+    router_logits_kernel<<<E, kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, W, bias, rows, H, E, logits);
     router_topk_kernel<<<rows, kTopkThreads, 0, st>>>(logits, E, k, mode, ids_out, w_out);
     return naiwa_hip_rc(hipGetLastError());
+}
+
+extern "C" int naiwa_router_topk(const void* x, int x_dtype, const float* W, int rows, int H, int E, int k,
+                                 int mode, uint32_t* ids_out, float* w_out, float* logits_out, int64_t stream) {
+    return naiwa_router_topk_biased(x, x_dtype, W, nullptr, rows, H, E, k, mode, ids_out, w_out, logits_out,
+                                    stream);
 }

@@ -119,6 +119,21 @@ int naiwa_memcpy_d2d(void* dst, const void* src, size_t bytes, int64_t stream) {
     return naiwa_hip_rc(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
 }
 
+int naiwa_upload_expert(void* const dst[3], const void* const src[3], const size_t bytes[3],
+                        int64_t copy_stream, int64_t read_fence, int64_t done_event) {
+    if (!dst || !src || !bytes) return NAIWA_E_INVALID;
+    for (int i = 0; i < 3; ++i)
+        if (bytes[i] && (!dst[i] || !src[i])) return NAIWA_E_INVALID;
+    hipStream_t st = (hipStream_t)copy_stream;
+    int rc = 0;
+    if (read_fence && (rc = naiwa_hip_rc(hipStreamWaitEvent(st, (hipEvent_t)read_fence, 0)))) return rc;
+    for (int i = 0; i < 3; ++i)
+        if (bytes[i] && (rc = naiwa_hip_rc(hipMemcpyAsync(dst[i], src[i], bytes[i], hipMemcpyHostToDevice, st))))
+            return rc;
+    if (done_event) return naiwa_hip_rc(hipEventRecord((hipEvent_t)done_event, st));
+    return NAIWA_OK;
+}
+
 int naiwa_memset(void* p, int value, size_t bytes, int64_t stream) {
     return naiwa_hip_rc(hipMemsetAsync(p, value, bytes, (hipStream_t)stream));
 }

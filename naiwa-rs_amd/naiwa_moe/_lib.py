@@ -43,6 +43,20 @@ STACK_LAYERED, STACK_FUSED = 0, 1
 
 STAGING_RING_FIRST = 1 << 30
 
+
+class CachedLayerDesc(C.Structure):
+    """naiwa_cached_layer_desc (include/naiwa_cached.h)."""
+    _fields_ = [("router", C.c_void_p), ("router_bias", C.c_void_p), ("gate", Bank), ("up", Bank),
+                ("down", Bank), ("host_gate", C.c_void_p), ("host_up", C.c_void_p), ("host_down", C.c_void_p),
+                ("num_experts", C.c_int), ("top_k", C.c_int), ("hidden", C.c_int), ("inter", C.c_int),
+                ("usable", C.c_int), ("mode", C.c_int), ("act", C.c_int)]
+
+
+class CachedStep(C.Structure):
+    """naiwa_cached_step (include/naiwa_cached.h)."""
+    _fields_ = [("hits", C.c_int), ("staged", C.c_int), ("staged_experts", C.c_int), ("promoted", C.c_int),
+                ("pcie_bytes", C.c_int64)]
+
 STATS_FIELDS = ("hits", "promotions", "misses", "staged", "lookahead_loads", "swaps", "lookahead_dropped",
                 "sync_waits", "pcie_misses", "pcie_bytes", "result_stalls")
 
@@ -97,6 +111,7 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_projection_bytes": (i64, [i32, i64, i64]),
     "naiwa_moe_decode": (i32, [_P(Bank), _P(Bank), _P(Bank), vp, i32, vp, vp, i32, i32, i32, vp, i64]),
     "naiwa_router_topk": (i32, [vp, i32, vp, i32, i32, i32, i32, i32, vp, vp, vp, i64]),
+    "naiwa_router_topk_biased": (i32, [vp, i32, vp, vp, i32, i32, i32, i32, i32, vp, vp, vp, i64]),
     "naiwa_moe_gather": (i32, [vp, i32, i32, vp, vp, vp, i64]),
     "naiwa_synth": (i32, [i32, u64, u64, i64, f32, f32, vp, i64]),
     "naiwa_stack_decode": (i32, [_P(Layer), i32, vp, i32, i32, i32, i32, i32, i32, vp, vp, i32, i64]),
@@ -105,6 +120,14 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_residual_add_bf16": (i32, [vp, vp, i64, i64]),
     "naiwa_stack_trace_enable": (i32, [i32]),
     "naiwa_stack_trace_read": (i32, [_P(u64), i32, _P(i32)]),
+    "naiwa_upload_expert": (i32, [vp, vp, vp, i64, i64, i64]),
+    # include/naiwa_cached.h
+    "naiwa_cached_layer_create": (i32, [_P(CachedLayerDesc), vp, i32, i64, _P(vp)]),
+    "naiwa_cached_layer_destroy": (i32, [vp]),
+    "naiwa_cached_layer_cache": (i32, [vp, _P(vp)]),
+    "naiwa_cached_layer_fill": (i32, [vp, i32, _P(i32)]),
+    "naiwa_cached_layer_forward": (i32, [vp, vp, i32, vp, f32, i32, u64, i64, _P(CachedStep)]),
+    "naiwa_cached_layer_routing": (i32, [vp, vp, vp, i32]),
     # include/naiwa_policy.h (host only)
     "naiwa_cache_create": (i32, [i32, i32, i32, _P(vp)]),
     "naiwa_cache_destroy": (i32, [vp]),

@@ -17,7 +17,7 @@ import numpy as np
 
 from ._lib import (ACT_SILU, BF16, F32, Q4_K, Q8_0, ROUTE_SOFTMAX_TOPK_RENORM, STACK_FUSED,
                    STACK_LAYERED, Bank, Layer, check, lib)
-from .device import DeviceBuffer
+from .device import DeviceBuffer, PinnedBuffer
 
 BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144)}
 
@@ -86,6 +86,44 @@ class LayerBanks:
 
 def _dev(a) -> int:
     return a.ptr if isinstance(a, DeviceBuffer) else int(a)
+
+
+class HostExpertStacks:
+    """Pinned host copies of one layer's stacked [E, N, K] projections, the sources
+    of expert uploads (the reference pins its GGUF stacks, src/host_memory.rs:30-170;
+    here they live in pinned allocations, since registering existing memory is not
+    available).  Expert e of a projection is at expert_range(e)."""
+
+    def __init__(self, experts: int, hidden: int, inter: int, dtypes: tuple[int, int, int]):
+        self.experts = experts
+        shapes = ((inter, hidden, dtypes[0]), (inter, hidden, dtypes[1]), (hidden, inter, dtypes[2]))
+        self.expert_bytes = [n * row_bytes(dt, k) for n, k, dt in shapes]
+        self.buffers = [PinnedBuffer(experts * b) for b in self.expert_bytes]
+
+    def view(self, proj: int) -> np.ndarray:
+        """[E, expert_bytes] uint8 view of projection proj (0 gate, 1 up, 2 down)."""
+        return self.buffers[proj].view().reshape(self.experts, self.expert_bytes[proj])
+
+    def expert_ptrs(self, e: int) -> list[int]:
+        if not 0 <= e < self.experts:
+            raise IndexError(f"expert {e} outside [0, {self.experts})")
+        return [buf.ptr + e * b for buf, b in zip(self.buffers, self.expert_bytes)]
+
+
+def upload_expert(banks: "LayerBanks", slot: int, stacks: HostExpertStacks, expert: int, copy_stream: int,
+                  read_fence=None, done=None) -> None:
+    """Queue expert `expert`'s three projections into `slot` on copy_stream, after read_fence
+    (an Event the compute stream recorded after the slot's last reader) and before done."""
+    dst = (C.c_void_p * 3)(banks.gate.slot_ptr(slot), banks.up.slot_ptr(slot), banks.down.slot_ptr(slot))
+    src = (C.c_void_p * 3)(*stacks.expert_ptrs(expert))
+    sizes = (C.c_size_t * 3)(*stacks.expert_bytes)
+    for bank, b in zip((banks.gate, banks.up, banks.down), stacks.expert_bytes):
+        if bank.expert_bytes != b:
+            raise ValueError("host stacks and slot banks disagree on an expert's size")
+    rc = lib().naiwa_upload_expert(dst, src, sizes, copy_stream,
+                                   read_fence.handle if read_fence is not None else 0,
+                                   done.handle if done is not None else 0)
+    check(rc, "naiwa_upload_expert")
 
 
 def indexed_moe_fused_decode(banks: LayerBanks, x, x_dtype: int, slot_ids, weights, rows: int,

@@ -12,7 +12,7 @@ import ctypes as C
 
 import numpy as np
 
-from ._lib import STAGING_RING_FIRST, STATS_FIELDS, CacheStats, check, lib
+from ._lib import (STAGING_RING_FIRST, STATS_FIELDS, CacheStats, CachedLayerDesc, CachedStep, check, lib)
 
 
 def _u32(a) -> np.ndarray:
@@ -34,16 +34,20 @@ def _ptr(a: np.ndarray):
 class ExpertCache:
     """One layer's slot cache: `slots` slots, the first `usable` of which hold experts."""
 
-    def __init__(self, num_experts: int, slots: int, usable: int | None = None):
+    def __init__(self, num_experts: int, slots: int, usable: int | None = None, _borrowed=None):
         self.num_experts = num_experts
         self.slots = slots
+        self._owned = _borrowed is None
+        if _borrowed is not None:
+            self._h = _borrowed
+            return
         h = C.c_void_p()
         check(lib().naiwa_cache_create(num_experts, slots, slots if usable is None else usable, C.byref(h)),
               "cache_create")
         self._h = h
 
     def __del__(self):
-        if getattr(self, "_h", None) and self._h.value:
+        if getattr(self, "_owned", False) and getattr(self, "_h", None) and self._h.value:
             lib().naiwa_cache_destroy(self._h)
             self._h = C.c_void_p()
 
@@ -156,6 +160,51 @@ class StagingRing:
         return [(int(chosen[i]), int(pos[i])) for i in range(n.value)]
 
 
+class CachedLayer:
+    """One layer's decode step over a partial cache (include/naiwa_cached.h): the reference's
+    CachedExperts::forward for decode rows, with PCIe staging and promotion."""
+
+    def __init__(self, router, banks, stacks, num_experts: int, top_k: int, usable: int, ring: "StagingRing",
+                 copy_stream: int, mode: int = 0, act: int = 0, router_bias=None):
+        from .ops import _dev
+        d = CachedLayerDesc(_dev(router), _dev(router_bias) if router_bias is not None else None,
+                            banks.gate.desc(), banks.up.desc(), banks.down.desc(),
+                            *[b.ptr for b in stacks.buffers], num_experts, top_k, banks.hidden, banks.inter, usable,
+                            mode, act)
+        h = C.c_void_p()
+        check(lib().naiwa_cached_layer_create(C.byref(d), ring._h, ring.length, copy_stream, C.byref(h)),
+              "cached_layer_create")
+        self._h, self.top_k, self.usable = h, top_k, usable
+        self._keep = (router, banks, stacks, ring, router_bias)
+        c = C.c_void_p()
+        check(lib().naiwa_cached_layer_cache(h, C.byref(c)), "cached_layer_cache")
+        self.cache = ExpertCache(num_experts, usable, _borrowed=c)
+
+    def __del__(self):
+        if getattr(self, "_h", None) and self._h.value:
+            lib().naiwa_cached_layer_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def fill(self, expert: int) -> int | None:
+        s = C.c_int()
+        check(lib().naiwa_cached_layer_fill(self._h, expert, C.byref(s)), "cached_layer_fill")
+        return s.value if s.value >= 0 else None
+
+    def forward(self, x, rows: int, out, pcie_frac: float = 1.0, promote_cap: int = 1, min_hits: int = 4,
+                stream: int = 0) -> dict:
+        from .ops import _dev
+        info = CachedStep()
+        check(lib().naiwa_cached_layer_forward(self._h, _dev(x), rows, _dev(out), pcie_frac, promote_cap, min_hits,
+                                               stream, C.byref(info)), "cached_layer_forward")
+        return {f: getattr(info, f) for f, _ in CachedStep._fields_}
+
+    def routing(self, rows: int) -> tuple[np.ndarray, np.ndarray]:
+        ids = np.empty((rows, self.top_k), dtype=np.uint32)
+        w = np.empty((rows, self.top_k), dtype=np.float32)
+        check(lib().naiwa_cached_layer_routing(self._h, _ptr(ids), _ptr(w), ids.size), "cached_layer_routing")
+        return ids, w
+
+
 def staging_ring_slots() -> int:
     return int(lib().naiwa_staging_ring_slots())
 
@@ -202,5 +251,5 @@ def stats_add(**delta: int) -> None:
     check(lib().naiwa_stats_add(C.byref(s)), "stats_add")
 
 
-__all__ = ["ExpertCache", "StagingRing", "STAGING_RING_FIRST", "staging_ring_slots", "top_k_ids",
+__all__ = ["ExpertCache", "StagingRing", "CachedLayer", "STAGING_RING_FIRST", "staging_ring_slots", "top_k_ids",
            "union_by_votes", "streamed_misses", "stats", "stats_add"]
