@@ -8,7 +8,7 @@ from ._lib import (ACT_GELU_PYTORCH_TANH, ACT_SILU, BF16, F16, F32, Q4_K, Q8_0,
                    ROUTE_SOFTMAX_TOPK, ROUTE_SOFTMAX_TOPK_RENORM, ROUTE_TOPK_SOFTMAX, LIB_PATH,
                    NaiwaError, lib)
 from .device import DeviceBuffer, Event, PinnedBuffer, Stream, device_count, device_info, synchronize
-from . import policy
+from . import doorbells, policy
 from .ops import (HostExpertStacks, LayerBanks, SlotBank, expert_range, indexed_moe_fused_decode, layer_desc,
                   moe_gather, router_topk, row_bytes, slot_stride, stack_decode, stack_status, synth,
                   upload_expert)
@@ -19,5 +19,5 @@ __all__ = [
     "NaiwaError", "lib", "DeviceBuffer", "Event", "PinnedBuffer", "Stream", "device_count",
     "device_info", "synchronize", "LayerBanks", "SlotBank", "expert_range",
     "indexed_moe_fused_decode", "moe_gather", "router_topk", "row_bytes", "slot_stride",
-    "layer_desc", "stack_decode", "stack_status", "synth", "policy", "HostExpertStacks", "upload_expert",
+    "layer_desc", "stack_decode", "stack_status", "synth", "policy", "doorbells", "HostExpertStacks", "upload_expert",
 ]

@@ -52,6 +52,15 @@ class CachedLayerDesc(C.Structure):
                 ("usable", C.c_int), ("mode", C.c_int), ("act", C.c_int)]
 
 
+class Pending(C.Structure):
+    """naiwa_pending (include/naiwa_doorbell.h)."""
+    _fields_ = [("seq", C.c_uint32), ("len", C.c_int), ("chan", C.c_int)]
+
+
+TASK_FN = C.CFUNCTYPE(None, C.c_void_p)
+RESULT_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(C.c_float), C.c_int)
+
+
 class CachedStep(C.Structure):
     """naiwa_cached_step (include/naiwa_cached.h)."""
     _fields_ = [("hits", C.c_int), ("staged", C.c_int), ("staged_experts", C.c_int), ("promoted", C.c_int),
@@ -121,6 +130,34 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_stack_trace_enable": (i32, [i32]),
     "naiwa_stack_trace_read": (i32, [_P(u64), i32, _P(i32)]),
     "naiwa_upload_expert": (i32, [vp, vp, vp, i64, i64, i64]),
+    # include/naiwa_doorbell.h
+    "naiwa_topk_doorbell_create": (i32, [i32, _P(vp)]),
+    "naiwa_topk_doorbell_destroy": (i32, [vp]),
+    "naiwa_topk_doorbell_publish_and_read": (i32, [vp, vp, vp, i32, i64, vp, vp, i64]),
+    "naiwa_act_doorbell_create": (i32, [i32, _P(vp)]),
+    "naiwa_act_doorbell_destroy": (i32, [vp]),
+    "naiwa_act_doorbell_publish": (i32, [vp, vp, i32, u32, i64]),
+    "naiwa_act_doorbell_wait_publish": (i32, [vp, u32, i32, vp, i64, _P(i32)]),
+    "naiwa_result_doorbell_create": (i32, [i32, _P(vp)]),
+    "naiwa_result_doorbell_destroy": (i32, [vp]),
+    "naiwa_result_doorbell_max_n": (i32, [vp]),
+    "naiwa_result_doorbell_publish": (i32, [vp, vp, i32, u32, _P(i32)]),
+    "naiwa_result_doorbell_wait_copy": (i32, [vp, u32, i32, vp, i64]),
+    "naiwa_result_doorbell_consumed": (i32, [vp, _P(u32)]),
+    "naiwa_pass_cell_create": (i32, [_P(vp)]),
+    "naiwa_pass_cell_destroy": (i32, [vp]),
+    "naiwa_pass_cell_claim": (i32, [vp, i64, _P(u32)]),
+    "naiwa_pass_cell_wait_latest": (i32, [vp, i64, _P(u32)]),
+    "naiwa_pass_cell_claimed": (i32, [vp, _P(u32)]),
+    "naiwa_executor_create": (i32, [_P(vp)]),
+    "naiwa_executor_destroy": (i32, [vp]),
+    "naiwa_executor_submit": (i32, [vp, TASK_FN, vp]),
+    "naiwa_executor_is_idle": (i32, [vp]),
+    "naiwa_executor_wait_idle": (i32, [vp, i64]),
+    "naiwa_executor_submit_result": (i32, [vp, i32, RESULT_FN, vp, _P(Pending)]),
+    "naiwa_pending_upload": (i32, [vp, _P(Pending), vp, i64]),
+    "naiwa_executor_take_error": (i32, [vp, C.c_char_p, i32]),
+    "naiwa_executor_stalls": (i32, [vp, _P(u64)]),
     # include/naiwa_cached.h
     "naiwa_cached_layer_create": (i32, [_P(CachedLayerDesc), vp, i32, i64, _P(vp)]),
     "naiwa_cached_layer_destroy": (i32, [vp]),

@@ -16,9 +16,10 @@ def declared_functions():
     for h in HEADERS:
         text = open(h).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-        for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][\w]*\s*\*?\s*\b([a-z_][a-z0-9_]*)\s*\(",
+        for m in re.finditer(r"^\s*(?:const\s+)?([A-Za-z_][\w]*)\s*\*?\s*\b([a-z_][a-z0-9_]*)\s*\(",
                              text, flags=re.M):
-            names.append(m.group(1))
+            if m.group(1) != "typedef":   # function-pointer typedefs declare no symbol
+                names.append(m.group(2))
     return sorted(set(names))
 
 
