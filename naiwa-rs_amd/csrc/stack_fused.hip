@@ -61,13 +61,10 @@ constexpr int kLeaders = 32;              // workgroups that add the router part
 constexpr int kChunk = NAIWA_ROUTER_CHUNK; // output features per phase-C chunk
 constexpr int kMaxChunks = 4;             // chunks per workgroup
 constexpr int kCPairs = 16;               // h vectors staged per phase-C pass
-constexpr int kPartPerThread = kMaxRows * kMaxE / kThreads;
 constexpr int kTraceSlots = 16;
 constexpr int kMaxLayers = 128;           // layer descriptors kept in LDS (tags hold layer + 1 < 256)
 constexpr int kXG = 8;                    // activation groups (4 values) per thread per poll round
 constexpr int kHG = 8;                    // h groups (4 values, 2 words) per thread per poll round
-constexpr int kDJ = 4;                    // down rows per group prefetched into LDS (one-chunk path)
-constexpr int kDUM = 2;                   // units per lane of such a row
 constexpr int kCB = 2;                    // down rows per group in flight (general path)
 
 struct LayerDev {
@@ -94,7 +91,6 @@ struct Params {
     float* w_out;
     uint64_t spin_limit;         // wall-clock ticks before a wait gives up
     uint32_t seq;                // launch number; tag of layer l = seq << 8 | (l + 1)
-    int down_lds;                // dynamic LDS holds kGroups * kDJ down rows after the staging areas
     unsigned long long* trace;   // optional [2][n_layers + 1][kTraceSlots] phase timestamps
 };
 
@@ -117,12 +113,12 @@ struct Smem {
     float pair_w[kMaxPairs];
     uint32_t sorted[kMaxPairs];    // valid pairs in (slot, p) order
     uint32_t srt_slot[kMaxPairs];
+    uint32_t srt_tok[kMaxPairs];   // token of sorted position i
     uint32_t seg_begin[kMaxPairs + 1];
     uint32_t seg_slot[kMaxPairs];
     int nseg;
     float partial[kChunk][kMaxPairs];
     float xown[kMaxChunks][kMaxRows][kChunk]; // this workgroup's chunks of x (bf16 values)
-    alignas(16) float wch[kMaxE][kChunk];     // next router's columns of this workgroup's chunk
 };
 
 typedef __attribute__((address_space(1))) u64 gu64;
@@ -134,13 +130,6 @@ __device__ __forceinline__ void st64(u64* p, u64 v) {
 }
 __device__ __forceinline__ u64 tagged(uint32_t tag, uint32_t v) { return ((u64)tag << 32) | v; }
 
-// 16 bytes from global memory straight into LDS (no registers; counted by
-// vmcnt): lane i of the wave writes wave_base + 16 * i.  Both addresses must be
-// 16-byte aligned, and wave_base must be the same in every active lane.
-__device__ __forceinline__ void lds_dma16(const void* src, void* wave_base) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                     (__attribute__((address_space(3))) void*)wave_base, 16, 0, 0);
-}
 __device__ __forceinline__ bool tag_ok(u64 w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
 __device__ __forceinline__ uint32_t layer_tag(const Params& p, int l) { return (p.seq << 8) | (uint32_t)(l + 1); }
 
@@ -212,10 +201,11 @@ __device__ __forceinline__ int chunk_at(int p, int nchunks) {
 }
 
 // Publish this workgroup's router partials for layer tag `tag`.
+template <int PPT>
 __device__ inline void store_partials(const Params& p, const long long* acc, uint32_t tag) {
     const int items = p.rows * p.E;
 #pragma unroll
-    for (int j = 0; j < kPartPerThread; ++j) {
+    for (int j = 0; j < PPT; ++j) {
         const int it = threadIdx.x + j * kThreads;
         if (it < items) {
             u64* dst = p.part + ((size_t)blockIdx.x * items + it) * 2;
@@ -271,11 +261,11 @@ __device__ inline void leader_reduce(const Params& p, int nprod, uint32_t tag) {
 
 // Router partials of one chunk for every (token, expert) item: W8(e) gives the
 // chunk's 8 router weights of expert e, xv[t] the chunk's activations.
-template <int AS, class F>
+template <int PPT, int AS, class F>
 __device__ __forceinline__ void router_chunk_accumulate(const Params& p, const F& W8, const float (*xv)[kChunk],
                                                         long long* acc) {
 #pragma unroll
-    for (int j = 0; j < kPartPerThread; ++j) {
+    for (int j = 0; j < PPT; ++j) {
         const int it = threadIdx.x + j * kThreads;
         if (it < p.rows * p.E) {
             const int t = it / p.E, e = it % p.E;
@@ -295,50 +285,71 @@ __device__ __forceinline__ u64 rank_key(float f, int e) {
 // Q4_K gate/up with one 144-byte block per lane
 // ---------------------------------------------------------------------------
 
-// Dot of one Q4_K block (9 x 16 bytes in registers) with its 256 staged
-// activations: words = the block's 128 bf16 perm words, sums = its 16 sums of 16.
-__device__ __forceinline__ float q4k_block_dot(const uint4* blk, const uint32_t* words, const float* sums) {
-    const uint4 hd = blk[0];
-    const float d = naiwa_f16_to_f32(hd.x & 0xffffu);
-    const float dmin = naiwa_f16_to_f32(hd.x >> 16);
-    // the 8 six-bit scales and mins, one per byte (ggml get_scale_min_k4)
-    const uint32_t sc_lo = hd.y & 0x3F3F3F3Fu;                                   // sc0..sc3
-    const uint32_t m_lo = hd.z & 0x3F3F3F3Fu;                                    // m0..m3
-    const uint32_t sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);   // sc4..sc7
-    const uint32_t m_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u); // m4..m7
-    float total = 0.0f;
+// Scales and mins of one Q4_K block header (ggml get_scale_min_k4), one per byte.
+struct Q4Scales {
+    float d, dmin;
+    uint32_t sc_lo, m_lo, sc_hi, m_hi;
+};
+__device__ __forceinline__ Q4Scales q4k_scales(const uint4& hd) {
+    Q4Scales s;
+    s.d = naiwa_f16_to_f32(hd.x & 0xffffu);
+    s.dmin = naiwa_f16_to_f32(hd.x >> 16);
+    s.sc_lo = hd.y & 0x3F3F3F3Fu;                                    // sc0..sc3
+    s.m_lo = hd.z & 0x3F3F3F3Fu;                                     // m0..m3
+    s.sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);    // sc4..sc7
+    s.m_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u); // m4..m7
+    return s;
+}
+// Chunk c (64 values: sub-blocks 2c, 2c+1) of a block: d*(sc0*qlo + sc1*qhi) - dmin*(m0*slo + m1*shi),
+// with qlo = alo - 128*slo (alo / ahi: dots of the nibbles + 128 offset).
+__device__ __forceinline__ float q4k_chunk(const Q4Scales& s, int c, float alo, float ahi, float slo, float shi) {
+    const uint32_t scw = c < 2 ? s.sc_lo : s.sc_hi, mw = c < 2 ? s.m_lo : s.m_hi;
+    const int sh = (c & 1) * 16;
+    const float sc0 = (float)((scw >> sh) & 0xFFu), sc1 = (float)((scw >> (sh + 8)) & 0xFFu);
+    const float m0 = (float)((mw >> sh) & 0xFFu), m1 = (float)((mw >> (sh + 8)) & 0xFFu);
+    return s.d * (sc0 * (alo - 128.0f * slo) + sc1 * (ahi - 128.0f * shi)) - s.dmin * (m0 * slo + m1 * shi);
+}
+
+// Dots of two Q4_K blocks (rows A and B, 9 x 16 bytes each in registers) with the
+// same 256 staged activations: words = the block's 128 bf16 pair words, sums =
+// its 16 sums of 16.  Each activation word is loaded once and feeds both rows.
+__device__ __forceinline__ void q4k_block_dot2(const uint4* A, const uint4* B, const uint32_t* words,
+                                               const float* sums, float& ra, float& rb) {
+    const Q4Scales sa = q4k_scales(A[0]), sb = q4k_scales(B[0]);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-        const uint4 qa = blk[1 + 2 * c], qb = blk[2 + 2 * c];
-        const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-        const uint4* xl = reinterpret_cast<const uint4*>(words + 32 * c);
-        const uint4* xh = reinterpret_cast<const uint4*>(words + 32 * c + 16);
-        float alo = 0.0f, ahi = 0.0f;
+        // the chunk's 32 activation words, all loads in flight before the first use
+        uint4 x[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = reinterpret_cast<const uint4*>(words + 32 * c)[i];
+        const float4 sv = reinterpret_cast<const float4*>(sums)[c];
+        const uint4 qa0 = A[1 + 2 * c], qa1 = A[2 + 2 * c], qb0 = B[1 + 2 * c], qb1 = B[2 + 2 * c];
+        const uint32_t wa[8] = {qa0.x, qa0.y, qa0.z, qa0.w, qa1.x, qa1.y, qa1.z, qa1.w};
+        const uint32_t wb[8] = {qb0.x, qb0.y, qb0.z, qb0.w, qb1.x, qb1.y, qb1.z, qb1.w};
+        float alo = 0.0f, ahi = 0.0f, blo = 0.0f, bhi = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint4 lo = xl[i], hi = xh[i];
-            const uint32_t x_lo[4] = {lo.x, lo.y, lo.z, lo.w};
-            const uint32_t x_hi[4] = {hi.x, hi.y, hi.z, hi.w};
+            const uint32_t xl[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+            const uint32_t xh[4] = {x[4 + i].x, x[4 + i].y, x[4 + i].z, x[4 + i].w};
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const uint32_t q = w[2 * i + h];
-                alo = naiwa_dot2_bf16((q & 0x000F000Fu) | 0x43004300u, x_lo[2 * h], alo);
-                alo = naiwa_dot2_bf16(((q >> 8) & 0x000F000Fu) | 0x43004300u, x_lo[2 * h + 1], alo);
-                ahi = naiwa_dot2_bf16(((q >> 4) & 0x000F000Fu) | 0x43004300u, x_hi[2 * h], ahi);
-                ahi = naiwa_dot2_bf16(((q >> 12) & 0x000F000Fu) | 0x43004300u, x_hi[2 * h + 1], ahi);
+                const uint32_t qa = wa[2 * i + h], qb = wb[2 * i + h];
+                alo = naiwa_dot2_bf16((qa & 0x000F000Fu) | 0x43004300u, xl[2 * h], alo);
+                blo = naiwa_dot2_bf16((qb & 0x000F000Fu) | 0x43004300u, xl[2 * h], blo);
+                alo = naiwa_dot2_bf16(((qa >> 8) & 0x000F000Fu) | 0x43004300u, xl[2 * h + 1], alo);
+                blo = naiwa_dot2_bf16(((qb >> 8) & 0x000F000Fu) | 0x43004300u, xl[2 * h + 1], blo);
+                ahi = naiwa_dot2_bf16(((qa >> 4) & 0x000F000Fu) | 0x43004300u, xh[2 * h], ahi);
+                bhi = naiwa_dot2_bf16(((qb >> 4) & 0x000F000Fu) | 0x43004300u, xh[2 * h], bhi);
+                ahi = naiwa_dot2_bf16(((qa >> 12) & 0x000F000Fu) | 0x43004300u, xh[2 * h + 1], ahi);
+                bhi = naiwa_dot2_bf16(((qb >> 12) & 0x000F000Fu) | 0x43004300u, xh[2 * h + 1], bhi);
             }
         }
-        const float4 sv = reinterpret_cast<const float4*>(sums)[c];
         const float slo = sv.x + sv.y, shi = sv.z + sv.w;
-        const uint32_t scw = c < 2 ? sc_lo : sc_hi, mw = c < 2 ? m_lo : m_hi;
-        const int sh = (c & 1) * 16;
-        const float sc0 = (float)((scw >> sh) & 0xFFu), sc1 = (float)((scw >> (sh + 8)) & 0xFFu);
-        const float m0 = (float)((mw >> sh) & 0xFFu), m1 = (float)((mw >> (sh + 8)) & 0xFFu);
-        total += d * (sc0 * (alo - 128.0f * slo) + sc1 * (ahi - 128.0f * shi)) - dmin * (m0 * slo + m1 * shi);
-        // keep the scheduler from hoisting every chunk's LDS reads at once
+        ra += q4k_chunk(sa, c, alo, ahi, slo, shi);
+        rb += q4k_chunk(sb, c, blo, bhi, slo, shi);
+        // keep the scheduler from hoisting every chunk's loads at once
         __builtin_amdgcn_sched_barrier(0);
     }
-    return total;
 }
 
 struct Q4Row {
@@ -360,8 +371,7 @@ __device__ __forceinline__ void q4_block_load(const uint8_t* row, int b, int nb,
 }
 
 // h of every token of the segment for intermediate rows r, r + 1 (pair q):
-// f0 / f1 hold this lane's block of the first 8 of each row; rows longer than
-// 8 blocks load the rest here.  The two results go out as one tagged word in
+// f0 / f1 hold this lane's block of each row (rows of at most 8 blocks, H <= 2048).  The two results go out as one tagged word in
 // the down projection's 16-bit format DD.
 template <int DD>
 __device__ inline void q4_pair_compute(const Params& p, const Smem& sm, const LayerDev& L, const uint8_t* dyn,
@@ -371,27 +381,17 @@ __device__ inline void q4_pair_compute(const Params& p, const Smem& sm, const La
     const int s = q / I2, r = 2 * (q % I2);
     const int b = (int)sm.seg_begin[s], e = (int)sm.seg_begin[s + 1];
     const int b0 = lr & 7;
-    const uint8_t* row0 = q4_row_ptr(L, sm.seg_slot[s], r, rb, lr);
     for (int tt = b; tt < e; ++tt) {
         const int t = (int)sm.sorted[tt] / k;
         const uint32_t* words = (const uint32_t*)(dyn + t * xstage);   // 132 words per block (padded)
         const float* sums = (const float*)(words + H / 2 + 4 * nb);
-        float h0 = 0.0f, h1 = 0.0f;
-#pragma unroll 1
-        for (int rr = 0; rr < 2; ++rr) {
-            Q4Row f = rr ? f1 : f0;
-            float acc = b0 < nb ? q4k_block_dot(f.blk, words + b0 * 132, sums + b0 * 16) : 0.0f;
-#pragma unroll 1
-            for (int bb = b0 + 8; bb < nb; bb += 8) {
-                q4_block_load(row0 + rr * rb, bb, nb, f);
-                acc += q4k_block_dot(f.blk, words + bb * 132, sums + bb * 16);
-            }
-            acc = naiwa_group_sum<8>(acc);                 // lanes 0-7: gate . x, lanes 8-15: up . x
-            const float uv = naiwa_dpp<0x128>(acc);        // row_ror:8 -- lane 0 receives lane 8
-            const float hv = naiwa_act(p.act, acc) * uv;
-            h0 = rr ? h0 : hv;
-            h1 = rr ? hv : h1;
-        }
+        float g0 = 0.0f, g1 = 0.0f;   // this lane's share of row r and row r + 1
+        if (b0 < nb) q4k_block_dot2(f0.blk, f1.blk, words + b0 * 132, sums + b0 * 16, g0, g1);
+        // lanes 0-7: gate . x, lanes 8-15: up . x; row_ror:8 brings lane 8 to lane 0
+        g0 = naiwa_group_sum<8>(g0);
+        g1 = naiwa_group_sum<8>(g1);
+        const float h0 = naiwa_act(p.act, g0) * naiwa_dpp<0x128>(g0);
+        const float h1 = naiwa_act(p.act, g1) * naiwa_dpp<0x128>(g1);
         if (lr == 0)
             st64(&p.h[(size_t)sm.sorted[tt] * I2 + r / 2],
                  tagged(tag, Fmt<DD>::to16(h0) | (Fmt<DD>::to16(h1) << 16)));
@@ -522,9 +522,13 @@ __device__ __forceinline__ T* opaque(T* ptr) {
     return ptr;
 }
 
-template <int DG, int DD>
+// MR: the largest rows (tokens per step) this instantiation serves, 1 or kMaxRows;
+// it sizes the per-thread (token, expert) item arrays.
+template <int DG, int DD, int MR>
 __global__ void __launch_bounds__(kThreads)
 stack_kernel(Params p) {
+    constexpr int PPT = (MR * kMaxE + kThreads - 1) / kThreads; // router items per thread
+    constexpr int XG = MR == 1 ? 4 : kXG;                       // activation groups per thread per round
     extern __shared__ __align__(16) uint8_t dyn[];
     __shared__ Smem sm;
     __shared__ LayerDev layers_lds[kMaxLayers];
@@ -547,7 +551,6 @@ stack_kernel(Params p) {
     const int half_h = H / 2;                 // tagged words per token
     const int nlog = rows * E;
     uint8_t* const hdyn = dyn + rows * xstage;      // h staging, after the activations
-    uint8_t* const ddyn = hdyn + kCPairs * hstage;  // prefetched down rows, after the h staging
 
     // ---- prologue: layer descriptors into LDS; own chunks of x; layer-0 logits ----
     mark(p, p.n_layers, 0);
@@ -569,15 +572,15 @@ stack_kernel(Params p) {
         }
         __syncthreads();
         if (bid < nprod) {
-            long long acc[kPartPerThread];
+            long long acc[PPT];
 #pragma unroll
-            for (int j = 0; j < kPartPerThread; ++j) acc[j] = 0;
+            for (int j = 0; j < PPT; ++j) acc[j] = 0;
             const float* W = layers_lds[0].router;
             for (int cp = bid, ci = 0; cp < nchunks; cp += G, ++ci) {
                 const int f0 = chunk_at(cp, nchunks) * kChunk;
-                router_chunk_accumulate<NAIWA_AS_GLOBAL>(p, [&](int e) { return W + (size_t)e * H + f0; }, sm.xown[ci], acc);
+                router_chunk_accumulate<PPT, NAIWA_AS_GLOBAL>(p, [&](int e) { return W + (size_t)e * H + f0; }, sm.xown[ci], acc);
             }
-            store_partials(p, acc, tag0);
+            store_partials<PPT>(p, acc, tag0);
         }
         mark(p, p.n_layers, 1);
         if (bid < nlead) leader_reduce(p, nprod, tag0);
@@ -598,8 +601,8 @@ stack_kernel(Params p) {
 
         // ---- A: poll logits + activations, rank, weights, segments ----
         const int ngroups = rows * gpt_h;
-        for (int g0 = 0; g0 < ngroups; g0 += kXG * kThreads) {
-            u64 xw[2 * kXG];
+        for (int g0 = 0; g0 < ngroups; g0 += XG * kThreads) {
+            u64 xw[2 * XG];
             auto xaddr = [&](int j) -> const u64* {
                 const int g = g0 + tid + (j >> 1) * kThreads;
                 if (g >= ngroups) return nullptr;
@@ -607,7 +610,7 @@ stack_kernel(Params p) {
             };
             issue_tagged(xw, xaddr, tag);
             if (g0 == 0) {
-                u64 lw[kPartPerThread];
+                u64 lw[PPT];
                 auto laddr = [&](int j) -> const u64* {
                     const int i = tid + j * kThreads;
                     return i < nlog ? p.logits + i : nullptr;
@@ -616,7 +619,7 @@ stack_kernel(Params p) {
                 if (L.slot_of && tid < E) sm.slot_tab[tid] = naiwa_ld<int32_t, NAIWA_AS_GLOBAL>(L.slot_of + tid);
                 wait_tagged(lw, laddr, tag, p);
 #pragma unroll
-                for (int j = 0; j < kPartPerThread; ++j) {
+                for (int j = 0; j < PPT; ++j) {
                     const int i = tid + j * kThreads;
                     if (i < nlog) {
                         const float f = __uint_as_float((uint32_t)lw[j]);
@@ -628,7 +631,7 @@ stack_kernel(Params p) {
             }
             wait_tagged(xw, xaddr, tag, p);
 #pragma unroll
-            for (int j = 0; j < kXG; ++j) {
+            for (int j = 0; j < XG; ++j) {
                 const int g = g0 + tid + j * kThreads;
                 const bool in = g < ngroups;
                 const int t = in ? g / gpt_h : 0, gg = in ? g % gpt_h : 0;
@@ -655,6 +658,7 @@ stack_kernel(Params p) {
                 const ulonglong2* kv = reinterpret_cast<const ulonglong2*>(sm.key[t]);
                 int cnt = 0;
                 if (in) {
+                    // 8 key pairs in flight per batch; a zero key is below every real key
 #pragma unroll 4
                     for (int o = sub; o < half_e; o += tpi) {
                         const ulonglong2 v = kv[o];
@@ -710,6 +714,7 @@ stack_kernel(Params p) {
             if (valid) {
                 sm.sorted[rank] = (uint32_t)q;
                 sm.srt_slot[rank] = (uint32_t)s;
+                sm.srt_tok[rank] = (uint32_t)t;
             }
             const unsigned long long valids = __ballot(valid);
             const int nvalid = __popcll(valids);
@@ -740,11 +745,6 @@ stack_kernel(Params p) {
         const int per = (total + G - 1) / G;
         const int q0 = bid * per, q1 = min(total, q0 + per);
         const bool owner = bid < nchunks;
-        const int c0 = owner ? chunk_at(bid, nchunks) : 0;
-        const int nitems = kChunk * nvalid;
-        // one chunk, all (feature, pair) rows in registers, each row within kDUM units per lane
-        const bool direct = p.down_lds && owner && nchunks <= G && nitems <= kGroups * kDJ &&
-                            dnu <= NAIWA_GROUP * kDUM;
         // gate/up work item q = (segment, row pair); fa/fb hold the pair's rows,
         // fc/fd the group's next pair (loads in flight)
         Q4Row fa, fb, fc, fd;
@@ -758,29 +758,6 @@ stack_kernel(Params p) {
         if constexpr (DG == NAIWA_Q4_K) {
             if (qa < q1) pair_rows(qa, fa, fb);
             if (qb < q1) pair_rows(qb, fc, fd);
-        }
-        if (direct) {
-            // the chunk's 8 rows of each routed pair are contiguous in the bank:
-            // 16-byte piece P of the LDS area is piece P % ppp of pair P / ppp
-            const int ppp = (int)(kChunk * drb / 16);
-            const int npieces = nvalid * ppp;
-            for (int P0 = wave * 64; P0 < npieces; P0 += kThreads) {
-                const int P = P0 + lane;
-                if (P < npieces) {
-                    const int pi = P / ppp;
-                    const uint8_t* src = L.down + (int64_t)sm.pair_slot[sm.sorted[pi]] * L.down_stride +
-                                         (int64_t)c0 * kChunk * drb + (int64_t)(P - pi * ppp) * 16;
-                    lds_dma16(src, ddyn + (size_t)P0 * 16);
-                }
-            }
-            if (!last) {
-                // next layer's router columns of the chunk: wch[e][0..7], two pieces per expert
-                const float* Wn = layers_lds[l + 1].router + c0 * kChunk;
-                for (int P0 = wave * 64; P0 < 2 * E; P0 += kThreads) {
-                    const int P = P0 + lane;
-                    if (P < 2 * E) lds_dma16(Wn + (size_t)(P >> 1) * H + (P & 1) * 4, &sm.wch[0][0] + P0 * 4);
-                }
-            }
         }
         mark(p, l, 3);
         if constexpr (DG == NAIWA_Q4_K) {
@@ -799,9 +776,9 @@ stack_kernel(Params p) {
 
         // ---- C: down + ordered combine + residual + next layer's router partials ----
         if (owner) {
-            long long racc[kPartPerThread];
+            long long racc[PPT];
 #pragma unroll
-            for (int j = 0; j < kPartPerThread; ++j) racc[j] = 0;
+            for (int j = 0; j < PPT; ++j) racc[j] = 0;
             u64* xt_next = p.xt + (size_t)((l + 1) & 1) * rows * half_h;
             for (int cp = bid, ci = 0; cp < nchunks; cp += G, ++ci) {
                 const int c = chunk_at(cp, nchunks);
@@ -810,31 +787,9 @@ stack_kernel(Params p) {
                     const int nbp = min(kCPairs, nvalid - b0);
                     if (ci > 0 || b0 > 0) __syncthreads(); // the previous pass's dots read hdyn
                     stage_h<DD>(p, sm, b0, nbp, hdyn, hstage, tag);
-                    if (direct) asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // this wave's LDS prefetch
                     __syncthreads();
                     mark(p, l, 5);
-                    if (direct) {
-                        // one pass (nvalid <= kCPairs), rows already in LDS (item it at it * drb)
-#pragma unroll
-                        for (int j = 0; j < kDJ; ++j) {
-                            const int it = grp + kGroups * j;
-                            const int pi = min(it, nitems - 1) / kChunk;
-                            const uint32_t* words = (const uint32_t*)(hdyn + pi * hstage);
-                            const uint8_t* drow = ddyn + (size_t)min(it, nitems - 1) * drb;
-                            float acc = 0.0f;
-                            if (it < nitems) {
-#pragma unroll
-                                for (int i = 0; i < kDUM; ++i) {
-                                    const int u = lr + NAIWA_GROUP * i;
-                                    if (u < dnu)
-                                        acc += Fmt<DD>::dot(Fmt<DD>::template load<NAIWA_AS_LDS>(drow, u), u, words,
-                                                            (const float*)(words + I / 2));
-                                }
-                            }
-                            const float v = naiwa_group_sum<NAIWA_GROUP>(acc);
-                            if (it < nitems && lr == 0) sm.partial[it % kChunk][pi] = v;
-                        }
-                    } else {
+                    {
                         constexpr int DUM = 2;
                         const int nit = kChunk * nbp;
                         for (int it0 = grp; it0 < nit; it0 += kGroups * kCB) {
@@ -872,7 +827,9 @@ stack_kernel(Params p) {
                             for (int j = 0; j < kCB; ++j) {
                                 const int it = it0 + j * kGroups;
                                 const float v = naiwa_group_sum<NAIWA_GROUP>(acc[j]);
-                                if (it < nit && lr == 0) sm.partial[it % kChunk][b0 + it / kChunk] = v;
+                                if (it < nit && lr == 0)
+                                    sm.partial[it % kChunk][b0 + it / kChunk] =
+                                        v * sm.pair_w[sm.sorted[b0 + it / kChunk]];
                             }
                         }
                     }
@@ -883,9 +840,18 @@ stack_kernel(Params p) {
                     // ascending slot order per token, then the residual in f32 and the bf16 store value
                     const int t = tid / kChunk, fi = tid % kChunk;
                     float y = 0.0f;
-                    for (int i = 0; i < nvalid; ++i) {
-                        const uint32_t pr = sm.sorted[i];
-                        if ((int)pr / k == t) y += sm.pair_w[pr] * sm.partial[fi][i];
+#pragma unroll 1
+                    for (int i0 = 0; i0 < nvalid; i0 += 8) {
+                        float pv[8];
+                        uint32_t tk[8];
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const int i = i0 + j;
+                            pv[j] = i < nvalid ? sm.partial[fi][i] : 0.0f;   // w * (down . h)
+                            tk[j] = i < nvalid ? sm.srt_tok[i] : 0xFFFFFFFFu;
+                        }
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) y += tk[j] == (uint32_t)t ? pv[j] : 0.0f;
                     }
                     sm.xown[ci][t][fi] = naiwa_bf16_to_f32(naiwa_f32_to_bf16(sm.xown[ci][t][fi] + y));
                 }
@@ -901,16 +867,12 @@ stack_kernel(Params p) {
                 }
                 mark(p, l, 7);
                 if (!last) {
-                    if (direct) {
-                        router_chunk_accumulate<NAIWA_AS_LDS>(p, [&](int e) { return &sm.wch[e][0]; }, sm.xown[ci], racc);
-                    } else {
-                        const float* Wn = layers_lds[l + 1].router;
-                        router_chunk_accumulate<NAIWA_AS_GLOBAL>(p, [&](int e) { return Wn + (size_t)e * H + f0; },
-                                                                 sm.xown[ci], racc);
-                    }
+                    const float* Wn = layers_lds[l + 1].router;
+                    router_chunk_accumulate<PPT, NAIWA_AS_GLOBAL>(p, [&](int e) { return Wn + (size_t)e * H + f0; },
+                                                             sm.xown[ci], racc);
                 }
             }
-            if (!last) store_partials(p, racc, tag_next);
+            if (!last) store_partials<PPT>(p, racc, tag_next);
         }
         mark(p, l, 8);
         if (!last && bid < nlead) leader_reduce(p, nprod, tag_next);
@@ -932,9 +894,9 @@ struct FusedCache {
 };
 FusedCache g_fused;
 
-template <int DG, int DD>
+template <int DG, int DD, int MR>
 int launch(const Params& prm, int blocks, size_t lds, hipStream_t st) {
-    auto fn = stack_kernel<DG, DD>;
+    auto fn = stack_kernel<DG, DD, MR>;
     Params copy = prm;
     void* args[] = {&copy};
     hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -954,11 +916,38 @@ int launch(const Params& prm, int blocks, size_t lds, hipStream_t st) {
     return naiwa_hip_rc(e);
 }
 
-template <int DG, int DD>
+template <int DG, int DD, int MR>
 int occupancy(size_t lds, int* per_cu) {
-    return naiwa_hip_rc(hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, stack_kernel<DG, DD>,
+    return naiwa_hip_rc(hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, stack_kernel<DG, DD, MR>,
                                                                      kThreads, lds));
 }
+
+// The instantiation for (gate/up format, down format, rows class): op(fn) on it.
+template <int MR, class Op>
+int with_kernel(int fg, int fd, const Op& op) {
+    if (fg == NAIWA_Q4_K && fd == NAIWA_Q4_K) return op.template run<NAIWA_Q4_K, NAIWA_Q4_K, MR>();
+    if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0) return op.template run<NAIWA_Q4_K, NAIWA_Q8_0, MR>();
+    if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0_ODD) return op.template run<NAIWA_Q4_K, NAIWA_Q8_0_ODD, MR>();
+    if (fg == NAIWA_Q8_0 && fd == NAIWA_Q8_0) return op.template run<NAIWA_Q8_0, NAIWA_Q8_0, MR>();
+    if (fg == NAIWA_Q8_0 && fd == NAIWA_Q8_0_ODD) return op.template run<NAIWA_Q8_0, NAIWA_Q8_0_ODD, MR>();
+    return NAIWA_E_UNSUPPORTED;
+}
+
+struct OccupancyOp {
+    size_t lds;
+    int* per_cu;
+    template <int DG, int DD, int MR>
+    int run() const { return occupancy<DG, DD, MR>(lds, per_cu); }
+};
+
+struct LaunchOp {
+    const Params* prm;
+    int blocks;
+    size_t lds;
+    hipStream_t st;
+    template <int DG, int DD, int MR>
+    int run() const { return launch<DG, DD, MR>(*prm, blocks, lds, st); }
+};
 
 } // namespace
 
@@ -1046,17 +1035,12 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     }
     const int fg = naiwa_kernel_fmt(L0.gate.dtype, H), fd = naiwa_kernel_fmt(L0.down.dtype, I);
     if (fg == NAIWA_Q8_0_ODD) return NAIWA_E_UNSUPPORTED;
-    // dynamic LDS: activations | h staging | (when it fits) the prefetched down rows
+    if (fg == NAIWA_Q4_K && H > 8 * NAIWA_QK_K) return NAIWA_E_UNSUPPORTED; // one block per lane: H <= 2048
+    // dynamic LDS: activations | h staging
     constexpr size_t kMaxDynLds = 104 * 1024;   // 160 KB per CU minus the static LDS
     const size_t lds_x = (size_t)rows * fused_xstage(fg, H);
     const size_t lds_h = (size_t)kCPairs * naiwa_stage_bytes(fd, I);
-    const int64_t drb = naiwa_row_bytes(L0.down.dtype, I);
     size_t lds = lds_x + lds_h;
-    int down_lds = 0;
-    if (drb % 16 == 0 && lds + (size_t)kGroups * kDJ * drb <= kMaxDynLds) {
-        lds += (size_t)kGroups * kDJ * drb;
-        down_lds = 1;
-    }
     if (lds > kMaxDynLds) return NAIWA_E_UNSUPPORTED;
 
     hipStream_t st = (hipStream_t)stream;
@@ -1065,12 +1049,8 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     if ((rc = naiwa_hip_rc(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)))) return rc;
     if ((rc = naiwa_hip_rc(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev)))) return rc;
     int per_cu = 0;
-    if (fg == NAIWA_Q4_K && fd == NAIWA_Q4_K) rc = occupancy<NAIWA_Q4_K, NAIWA_Q4_K>(lds, &per_cu);
-    else if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0) rc = occupancy<NAIWA_Q4_K, NAIWA_Q8_0>(lds, &per_cu);
-    else if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0_ODD) rc = occupancy<NAIWA_Q4_K, NAIWA_Q8_0_ODD>(lds, &per_cu);
-    else if (fg == NAIWA_Q8_0 && fd == NAIWA_Q8_0) rc = occupancy<NAIWA_Q8_0, NAIWA_Q8_0>(lds, &per_cu);
-    else if (fg == NAIWA_Q8_0 && fd == NAIWA_Q8_0_ODD) rc = occupancy<NAIWA_Q8_0, NAIWA_Q8_0_ODD>(lds, &per_cu);
-    else return NAIWA_E_UNSUPPORTED;
+    const OccupancyOp occ{lds, &per_cu};
+    rc = rows == 1 ? with_kernel<1>(fg, fd, occ) : with_kernel<kMaxRows>(fg, fd, occ);
     if (rc) return rc;
     const int bpc = per_cu < g_fused_blocks_per_cu ? per_cu : g_fused_blocks_per_cu;
     if (bpc < 1) return NAIWA_E_UNSUPPORTED;
@@ -1162,16 +1142,12 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     prm.w_out = w_out;
     prm.spin_limit = (uint64_t)khz * 2000ull; // 2 s
     prm.seq = seq;
-    prm.down_lds = down_lds;
     prm.trace = g_trace_enabled ? (unsigned long long*)naiwa_scratch(NAIWA_SCRATCH_STACK + 2,
                                                                      (size_t)2 * (n_layers + 1) * kTraceSlots * 8, &rc)
                                 : nullptr;
     if (g_trace_enabled && !prm.trace) return rc;
     g_trace_layers = n_layers;
     zero_u32<<<1, 64, 0, st>>>((unsigned int*)(sync + kStatusOff), 64);
-    if (fg == NAIWA_Q4_K && fd == NAIWA_Q4_K) return launch<NAIWA_Q4_K, NAIWA_Q4_K>(prm, blocks, lds, st);
-    if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0) return launch<NAIWA_Q4_K, NAIWA_Q8_0>(prm, blocks, lds, st);
-    if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0_ODD) return launch<NAIWA_Q4_K, NAIWA_Q8_0_ODD>(prm, blocks, lds, st);
-    if (fg == NAIWA_Q8_0 && fd == NAIWA_Q8_0) return launch<NAIWA_Q8_0, NAIWA_Q8_0>(prm, blocks, lds, st);
-    return launch<NAIWA_Q8_0, NAIWA_Q8_0_ODD>(prm, blocks, lds, st);
+    const LaunchOp go{&prm, blocks, lds, st};
+    return rows == 1 ? with_kernel<1>(fg, fd, go) : with_kernel<kMaxRows>(fg, fd, go);
 }

@@ -10,7 +10,8 @@ import ctypes as C
 import os
 
 PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(PKG_ROOT, "libnaiwa_moe.so")
+# NAIWA_MOE_LIB: load another build of the same ABI (e.g. an alternative kernel build)
+LIB_PATH = os.environ.get("NAIWA_MOE_LIB") or os.path.join(PKG_ROOT, "libnaiwa_moe.so")
 
 OK = 0
 E_INVALID, E_UNSUPPORTED, E_TIMEOUT, E_NOMEM, E_BAD_ID, E_NOT_FOUND, E_DEVICE = -1, -2, -3, -4, -5, -6, -7
