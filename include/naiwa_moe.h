@@ -17,6 +17,8 @@
  *                         src/moe/decode.rs:33-39 (tie rule of
  *                         src/moe/cached_layer.rs:357-363)
  *   naiwa_moe_gather      the per-bank grouping of src/moe/stages/gpu.rs:100-133
+ *   naiwa_moe_prefill     the fork's grouped MoEExperts::forward, called at
+ *                         src/prefill_stream.rs:2080-2102
  *   naiwa_upload_expert   CopyStream::queue_async, src/copy_stream.rs:387-409
  *   naiwa_cache_* etc.    the slot policy of src/moe/cached_layer.rs and
  *                         src/moe/stages/{route,dma_miss}.rs, src/moe/staging.rs
@@ -172,6 +174,21 @@ int naiwa_router_topk_biased(const void* x, int x_dtype, const float* W, const f
  * *bad_out (device int, may be NULL) and left out of every segment. */
 int naiwa_moe_gather(const uint32_t* ids, int n, int E, uint32_t* perm_out, uint32_t* offsets_out,
                      int* bad_out, int64_t stream);
+
+/* Prefill: the routed experts of a chunk of T tokens (many tokens per expert) as
+ * grouped GEMMs on the matrix cores -- the counterpart of the fork's grouped
+ * MoEExperts::forward (src/prefill_stream.rs:2080-2102).  Same banks, slot ids
+ * and weights [T, k] as naiwa_moe_decode; x is bf16 [T, H]; out f32 [T, H].
+ * Weights are dequantised to bf16 per 128-wide K-step and multiplied with
+ * v_mfma_f32_32x32x16_bf16 (f32 accumulation); h is rounded to bf16.  Needs
+ * H, I multiples of 128; gate/up Q4_K (H % 256 == 0) or Q8_0, down Q4_K (I %
+ * 256 == 0) or Q8_0; T * k <= 65536; slots <= 4096.  Slot ids outside the
+ * bank contribute nothing.  flags: NAIWA_PREFILL_ACCUMULATE adds to out
+ * (e.g. shared experts on top of the routed ones) instead of overwriting. */
+#define NAIWA_PREFILL_ACCUMULATE 1
+int naiwa_moe_prefill(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, const void* x,
+                      const uint32_t* slot_ids, const float* w, int T, int k, int act, float* out, int flags,
+                      int64_t stream);
 
 /* ======================================================================== */
 /* A decode stack: per layer, x <- bf16(x + MoE_l(x)) with the router,      */

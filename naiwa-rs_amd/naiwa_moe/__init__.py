@@ -10,7 +10,7 @@ from ._lib import (ACT_GELU_PYTORCH_TANH, ACT_SILU, BF16, F16, F32, Q4_K, Q8_0,
 from .device import DeviceBuffer, Event, PinnedBuffer, Stream, device_count, device_info, synchronize
 from . import doorbells, policy
 from .ops import (HostExpertStacks, LayerBanks, SlotBank, expert_range, indexed_moe_fused_decode, layer_desc,
-                  moe_gather, router_topk, row_bytes, slot_stride, stack_decode, stack_status, synth,
+                  moe_gather, moe_prefill, router_topk, row_bytes, slot_stride, stack_decode, stack_status, synth,
                   upload_expert)
 
 __all__ = [
@@ -18,6 +18,6 @@ __all__ = [
     "ROUTE_SOFTMAX_TOPK", "ROUTE_SOFTMAX_TOPK_RENORM", "ROUTE_TOPK_SOFTMAX", "LIB_PATH",
     "NaiwaError", "lib", "DeviceBuffer", "Event", "PinnedBuffer", "Stream", "device_count",
     "device_info", "synchronize", "LayerBanks", "SlotBank", "expert_range",
-    "indexed_moe_fused_decode", "moe_gather", "router_topk", "row_bytes", "slot_stride",
+    "indexed_moe_fused_decode", "moe_gather", "moe_prefill", "router_topk", "row_bytes", "slot_stride",
     "layer_desc", "stack_decode", "stack_status", "synth", "policy", "doorbells", "HostExpertStacks", "upload_expert",
 ]

@@ -122,6 +122,7 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_moe_decode": (i32, [_P(Bank), _P(Bank), _P(Bank), vp, i32, vp, vp, i32, i32, i32, vp, i64]),
     "naiwa_router_topk": (i32, [vp, i32, vp, i32, i32, i32, i32, i32, vp, vp, vp, i64]),
     "naiwa_router_topk_biased": (i32, [vp, i32, vp, vp, i32, i32, i32, i32, i32, vp, vp, vp, i64]),
+    "naiwa_moe_prefill": (i32, [_P(Bank), _P(Bank), _P(Bank), vp, vp, vp, i32, i32, i32, vp, i32, i64]),
     "naiwa_moe_gather": (i32, [vp, i32, i32, vp, vp, vp, i64]),
     "naiwa_synth": (i32, [i32, u64, u64, i64, f32, f32, vp, i64]),
     "naiwa_stack_decode": (i32, [_P(Layer), i32, vp, i32, i32, i32, i32, i32, i32, vp, vp, i32, i64]),

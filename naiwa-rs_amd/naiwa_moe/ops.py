@@ -135,6 +135,16 @@ def indexed_moe_fused_decode(banks: LayerBanks, x, x_dtype: int, slot_ids, weigh
     check(rc, "naiwa_moe_decode")
 
 
+def moe_prefill(banks: LayerBanks, x, slot_ids, weights, T: int, topk: int, out, act: int = ACT_SILU,
+                accumulate: bool = False, stream: int = 0) -> None:
+    """out[T, hidden] f32 (+)= sum_j w[t,j] * expert(slot_ids[t,j])(x[t]) for a prefill chunk
+    (x bf16 [T, hidden]), as grouped MFMA GEMMs; all device pointers."""
+    g, u, d = banks.gate.desc(), banks.up.desc(), banks.down.desc()
+    rc = lib().naiwa_moe_prefill(C.byref(g), C.byref(u), C.byref(d), _dev(x), _dev(slot_ids), _dev(weights),
+                                 T, topk, act, _dev(out), 1 if accumulate else 0, stream)
+    check(rc, "naiwa_moe_prefill")
+
+
 def router_topk(x, x_dtype: int, W, rows: int, H: int, E: int, k: int, ids_out, w_out,
                 mode: int = ROUTE_SOFTMAX_TOPK_RENORM, logits_out=None, stream: int = 0) -> None:
     rc = lib().naiwa_router_topk(_dev(x), x_dtype, _dev(W), rows, H, E, k, mode, _dev(ids_out),
