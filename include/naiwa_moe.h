@@ -213,16 +213,16 @@ int naiwa_stack_decode(const naiwa_layer* layers, int n_layers, void* x, int row
                        int k, int mode, int act, uint32_t* ids_out, float* w_out, int flags,
                        int64_t stream);
 
-/* Blocks per CU of the fused kernel (1..8, capped by occupancy; default 2). */
+/* Blocks per CU of the fused kernel (1..8, capped by occupancy; default 1). */
 int naiwa_stack_set_blocks_per_cu(int n);
-/* Counters of the last fused launch: grid-barrier waits that gave up after
- * their 2 s bound, and routed experts with no resident slot (weight dropped).
- * Synchronizes the device. */
+/* Counters of the last fused launch: waits for another workgroup's data that
+ * gave up after their 2 s bound, and routed experts with no resident slot
+ * (weight dropped).  Synchronizes the device. */
 int naiwa_stack_status(int* barrier_timeouts, int* missing_experts);
 
 /* Diagnostic phase timestamps of the fused kernel: when enabled, the first
  * and last block record s_memrealtime ticks at each phase boundary.
- * naiwa_stack_trace_read copies [2][n_layers + 1][8] ticks of the last launch
+ * naiwa_stack_trace_read copies [2][n_layers + 1][16] ticks of the last launch
  * (row n_layers is the prologue) and synchronizes the device. */
 int naiwa_stack_trace_enable(int on);
 int naiwa_stack_trace_read(uint64_t* out, int capacity, int* n_layers);
