@@ -234,7 +234,9 @@ def main() -> int:
 
 
 def print_trace(nm, run, stream, L, khz):
-    """One extra (untimed) fused step with phase timestamps: block 0 and the last block."""
+    """One extra (untimed) fused step with every workgroup's phase timestamps, reduced to
+    the critical path of each layer: logits published -> all received -> gate/up done
+    (slowest producer) -> h received -> down + partials done (slowest) -> next logits."""
     import ctypes as C
     lib = nm.lib()
     lib.naiwa_stack_trace_enable(1)
@@ -242,29 +244,63 @@ def print_trace(nm, run, stream, L, khz):
     stream.sync()
     lib.naiwa_stack_trace_enable(0)
     slots = 16
-    n = 2 * (L + 1) * slots
-    buf = (C.c_uint64 * n)()
-    nl = C.c_int(0)
-    nm._lib.check(lib.naiwa_stack_trace_read(buf, n, C.byref(nl)), "trace_read")
-    t = np.frombuffer(buf, dtype=np.uint64).astype(np.float64).reshape(2, L + 1, slots) / (khz / 1000.0)
-    names = ["poll_logits_x", "rank", "route", "issue_loads", "gate_up", "poll_h", "down", "combine_x",
-             "partials", "reduce"]
-    end = len(names) - 1
-    for who in range(2):
-        pro = t[who, L]
-        log(f"trace block {'first' if who == 0 else 'last'}: prologue partials {pro[1] - pro[0]:.2f} us, "
-            f"reduce {pro[2] - pro[1]:.2f} us")
-        per = []
-        prev = t[who, L, 2]
-        for l in range(L):
-            m = t[who, l]
-            row = [m[0] - prev] + [m[i] - m[i - 1] for i in range(1, end + 1)]
-            per.append(row)
-            prev = m[end]
-        per = np.array(per)
-        log("  mean us/layer: " + ", ".join(f"{nme} {v:.2f}" for nme, v in zip(names, per.mean(0)))
-            + f" | total {per.sum(1).mean():.2f}")
-    log(f"trace: kernel span {t[0, L - 1, end] - t[0, L, 0]:.1f} us")
+    cap = 2048 * (L + 1) * slots
+    buf = (C.c_uint64 * cap)()
+    nl, nb = C.c_int(0), C.c_int(0)
+    nm._lib.check(lib.naiwa_stack_trace_read(buf, cap, C.byref(nl), C.byref(nb)), "trace_read")
+    G = nb.value
+    t = np.frombuffer(buf, dtype=np.uint64)[: G * (L + 1) * slots].astype(np.float64)
+    t = t.reshape(G, L + 1, slots) / (khz / 1000.0)
+    nlead = min(32, G)
+    names = ["recv", "rank", "route", "issue", "gate_up", "h_recv", "down", "combine", "partials", "reduce"]
+    med = {n: [] for n in names[1:]}
+    crit = {"logits->recv(max)": [], "recv->gate_up end(max)": [], "h hop": [], "h recv spread": [],
+            "h recv->partials(max)": [], "reduce hop": []}
+    late_gu, late_dn = np.zeros(8), np.zeros(8)
+    pub = t[:nlead, L, 2].max()
+    for l in range(L - 1):
+        m = t[:, l]
+        for i, n in enumerate(names[1:], start=1):
+            if n in ("h_recv",):
+                continue
+            med[n].append(np.median(m[:, i] - m[:, i - 1]))
+        gu_end = m[:, 4].max()
+        crit["logits->recv(max)"].append(m[:, 0].max() - pub)
+        crit["recv->gate_up end(max)"].append(gu_end - m[:, 0].max())
+        crit["h hop"].append(m[:, 5].min() - gu_end)
+        crit["h recv spread"].append(m[:, 5].max() - m[:, 5].min())
+        crit["h recv->partials(max)"].append(m[:, 8].max() - m[:, 5].max())
+        nxt = m[:nlead, 9].max()
+        crit["reduce hop"].append(nxt - m[:, 8].max())
+        pub = nxt
+        for w in np.argsort(m[:, 4])[-16:]:
+            late_gu[w % 8] += 1
+        for w in np.argsort(m[:, 8])[-16:]:
+            late_dn[w % 8] += 1
+    log("trace: median per-workgroup phase us/layer: " +
+        ", ".join(f"{n} {np.mean(v):.2f}" for n, v in med.items() if v))
+    log("trace: critical path us/layer: " + ", ".join(f"{n} {np.mean(v):.2f}" for n, v in crit.items()) +
+        f" | sum {sum(np.mean(v) for n, v in crit.items() if n != 'h recv spread'):.2f}")
+    gu = t[:, : L - 1, 4] - t[:, : L - 1, 3]
+    log(f"trace: gate_up (issue->done) us: median {np.median(gu):.2f} p90 {np.percentile(gu, 90):.2f} "
+        f"max {gu.max():.2f}; recv spread {np.mean(t[:, :L-1, 0].max(0) - t[:, :L-1, 0].min(0)):.2f}")
+    sub = {"logits seen": [], "x staged (wave 1)": [], "keys+barrier": [], "weights": [], "pairs": []}
+    pub = t[:nlead, L, 2].max()
+    for l in range(L - 1):
+        m = t[:, l]
+        if m[:, 10].min() > 0:
+            sub["logits seen"].append(np.median(m[:, 10]) - pub)
+            sub["x staged (wave 1)"].append(np.median(m[:, 13]) - pub)
+            sub["keys+barrier"].append(np.median(m[:, 0] - m[:, 10]))
+            sub["weights"].append(np.median(m[:, 11] - m[:, 1]))
+            sub["pairs"].append(np.median(m[:, 12] - m[:, 11]))
+        pub = m[:nlead, 9].max()
+    if sub["weights"]:
+        log("trace: one-token routing, median us after the last logits publish: " +
+            ", ".join(f"{n} {np.mean(v):.2f}" for n, v in sub.items()))
+    log("trace: XCD of the 16 latest gate/up finishers " + str(late_gu.astype(int).tolist()) +
+        ", of the 16 latest partials " + str(late_dn.astype(int).tolist()))
+    log(f"trace: kernel span {t[:, L - 1, 9].max() - t[:, L, 0].min():.1f} us over {G} workgroups")
 
 
 def layers_host_sample(nm, keep, L, E, H, I, n_layers: int = 4):

@@ -220,12 +220,12 @@ int naiwa_stack_set_blocks_per_cu(int n);
  * (weight dropped).  Synchronizes the device. */
 int naiwa_stack_status(int* barrier_timeouts, int* missing_experts);
 
-/* Diagnostic phase timestamps of the fused kernel: when enabled, the first
- * and last block record s_memrealtime ticks at each phase boundary.
- * naiwa_stack_trace_read copies [2][n_layers + 1][16] ticks of the last launch
- * (row n_layers is the prologue) and synchronizes the device. */
+/* Diagnostic phase timestamps of the fused kernel: when enabled, every block
+ * records s_memrealtime ticks at each phase boundary.  naiwa_stack_trace_read
+ * copies [blocks][n_layers + 1][16] ticks of the last launch (row n_layers is
+ * the prologue) and synchronizes the device. */
 int naiwa_stack_trace_enable(int on);
-int naiwa_stack_trace_read(uint64_t* out, int capacity, int* n_layers);
+int naiwa_stack_trace_read(uint64_t* out, int capacity, int* n_layers, int* blocks);
 
 /* x[i] <- bf16(f32(x[i]) + y[i]) for i < n (the residual of the stack). */
 int naiwa_residual_add_bf16(void* x, const float* y, int64_t n, int64_t stream);

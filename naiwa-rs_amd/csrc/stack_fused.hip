@@ -38,6 +38,8 @@
 // int64 with 32 fractional bits, and the chunks are added as integers.
 // Integer addition is associative, so the logits (and the top-k) are bit-
 // identical to the CPU oracle's however the chunks are distributed.
+#include <algorithm>
+#include <type_traits>
 #include <mutex>
 #include <stdlib.h>
 #include <string.h>
@@ -91,20 +93,28 @@ struct Params {
     float* w_out;
     uint64_t spin_limit;         // wall-clock ticks before a wait gives up
     uint32_t seq;                // launch number; tag of layer l = seq << 8 | (l + 1)
-    unsigned long long* trace;   // optional [2][n_layers + 1][kTraceSlots] phase timestamps
+    unsigned long long* trace;   // optional [grid][n_layers + 1][kTraceSlots] phase timestamps
+    int bitems;                  // Q4_K gate/up: (segment, row pair) items per LDS round
+    int hpairs;                  // h vectors staged per phase-C pass
+    int dpre;                    // Q4_K down: pairs whose rows are prefetched into LDS (0 = none)
 };
 
-// Phase timestamps (s_memrealtime) of the first and last workgroup, when tracing.
+// Phase timestamps (s_memrealtime, one device-wide clock) of every workgroup, when tracing.
 __device__ __forceinline__ void mark(const Params& p, int layer, int slot) {
     if (!p.trace || threadIdx.x != 0) return;
-    const int who = blockIdx.x == 0 ? 0 : (blockIdx.x == gridDim.x - 1 ? 1 : -1);
-    if (who < 0) return;
-    p.trace[((size_t)who * (p.n_layers + 1) + layer) * kTraceSlots + slot] = wall_clock64();
+    p.trace[((size_t)blockIdx.x * (p.n_layers + 1) + layer) * kTraceSlots + slot] = wall_clock64();
+}
+
+// The same, recorded by the first lane of the calling wave.
+__device__ __forceinline__ void mark_wave(const Params& p, int layer, int slot) {
+    if (!p.trace || (threadIdx.x & 63) != 0) return;
+    p.trace[((size_t)blockIdx.x * (p.n_layers + 1) + layer) * kTraceSlots + slot] = wall_clock64();
 }
 
 struct Smem {
     alignas(16) u64 key[kMaxRows][kMaxE + 2];  // ranking keys: ordered logit bits << 32 | ~expert
     float lg[kMaxRows][kMaxE];
+    int32_t rcnt[kThreads / 64][kMaxE]; // one-token ranking: counts per wave's key slice
     int32_t slot_tab[kMaxE];
     uint32_t top_ids[kMaxRows][kMaxK];
     float top_ex[kMaxRows][kMaxK];
@@ -129,6 +139,14 @@ __device__ __forceinline__ void st64(u64* p, u64 v) {
     __hip_atomic_store((gu64*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ u64 tagged(uint32_t tag, uint32_t v) { return ((u64)tag << 32) | v; }
+
+// 16 bytes from global memory straight into LDS (no registers; counted by
+// vmcnt): lane i of the wave writes wave_base + 16 * i.  Both addresses must be
+// 16-byte aligned, and wave_base must be the same in every active lane.
+__device__ __forceinline__ void lds_dma16(const void* src, void* wave_base) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)wave_base, 16, 0, 0);
+}
 
 __device__ __forceinline__ bool tag_ok(u64 w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
 __device__ __forceinline__ uint32_t layer_tag(const Params& p, int l) { return (p.seq << 8) | (uint32_t)(l + 1); }
@@ -280,6 +298,159 @@ __device__ __forceinline__ u64 rank_key(float f, int e) {
     const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((u64)o << 32) | (uint32_t)~(uint32_t)e;
 }
+// The logit of a key's high word (rank_key's order bits; -0 comes back as +0).
+__device__ __forceinline__ float key_logit(uint32_t o) {
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+}
+
+// Maximum over the 64 lanes of the wave (every lane active): DPP within each
+// row of 16, then the four row results.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(a, b), max(c, d));
+}
+__device__ __forceinline__ float readlane_f32(float v, int ln) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), ln));
+}
+
+// Wave 0, one lane per (token, rank) pair q = t * k + j (inp: q < rows * k):
+// slot lookup, the routing outputs, and the grouping of valid pairs by slot
+// (sorted by (slot, q); a segment per distinct slot).
+__device__ inline void group_pairs(const Params& p, Smem& sm, const LayerDev& L, int l, int lane, bool inp, int t,
+                                   uint32_t e, float w) {
+    const int npairs = p.rows * p.k;
+    const int q = lane;
+    const int32_t s = inp ? (L.slot_of ? sm.slot_tab[e] : (int32_t)e) : -1;
+    const bool ok = inp && s >= 0 && s < L.slots;
+    if (inp && !ok && blockIdx.x == 0) atomicAdd(&p.status[1], 1);
+    if (inp && blockIdx.x == 0 && p.ids_out) {
+        p.ids_out[(size_t)l * npairs + q] = e;
+        p.w_out[(size_t)l * npairs + q] = w;
+    }
+    const bool valid = ok && w != 0.0f;
+    // sort key (slot, pair); invalid pairs sort last
+    const uint32_t key = valid ? (((uint32_t)s << 6) | (uint32_t)q) : 0xFFFFFFFFu;
+    int rank = 0;
+    for (int o = 0; o < npairs; ++o) rank += (uint32_t)__builtin_amdgcn_readlane((int)key, o) < key;
+    sm.pair_slot[q] = valid ? (uint32_t)s : 0u;
+    sm.pair_w[q] = valid ? w : 0.0f;
+    if (valid) {
+        sm.sorted[rank] = (uint32_t)q;
+        sm.srt_slot[rank] = (uint32_t)s;
+        sm.srt_tok[rank] = (uint32_t)t;
+    }
+    const unsigned long long valids = __ballot(valid);
+    const int nvalid = __popcll(valids);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // lane r looks at sorted position r: a segment starts where the slot changes
+    const bool start = lane < nvalid && (lane == 0 || sm.srt_slot[lane] != sm.srt_slot[lane - 1]);
+    const unsigned long long starts = __ballot(start);
+    if (start) {
+        const int si = __popcll(starts & ((1ull << lane) - 1ull));
+        sm.seg_begin[si] = (uint32_t)lane;
+        sm.seg_slot[si] = sm.srt_slot[lane];
+    }
+    if (lane == 0) {
+        const int ns = __popcll(starts);
+        sm.seg_begin[ns] = (uint32_t)nvalid;
+        sm.nseg = ns;
+    }
+}
+
+__device__ __forceinline__ u64 readlane_u64(u64 v, int ln) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, ln);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), ln);
+    return ((u64)hi << 32) | lo;
+}
+
+// One token (rows == 1), wave 0: poll the E logits (lane l holds experts
+// l + 64 j) and the slot table; their ranking keys, logits and slots go to LDS.
+__device__ inline void poll_one_row(const Params& p, Smem& sm, const LayerDev& L, int l, uint32_t tag, int lane) {
+    constexpr int KPL = kMaxE / 64;
+    const int E = p.E;
+    u64 lw[KPL];
+    auto laddr = [&](int j) -> const u64* {
+        const int e = lane + 64 * j;
+        return e < E ? p.logits + e : nullptr;
+    };
+    issue_tagged(lw, laddr, tag);
+    int32_t st[KPL];
+#pragma unroll
+    for (int j = 0; j < KPL; ++j)
+        st[j] = (L.slot_of && lane + 64 * j < E) ? naiwa_ld<int32_t, NAIWA_AS_GLOBAL>(L.slot_of + lane + 64 * j) : 0;
+    wait_tagged(lw, laddr, tag, p);
+    mark_wave(p, l, 10);
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E) {
+            const float f = __uint_as_float((uint32_t)lw[j]);
+            sm.lg[0][e] = f;
+            sm.key[0][e] = rank_key(f, e);
+            if (L.slot_of) sm.slot_tab[e] = st[j];
+        }
+    }
+}
+
+// One token, every wave: the number of keys above each key that lie in this
+// wave's quarter of the experts (its slice, at most 64 keys, one per lane),
+// broadcast one key at a time from the lane holding it.  KPL: keys per lane.
+template <int KPL>
+__device__ inline void rank_slice(const Params& p, Smem& sm, int wave, int lane) {
+    const int E = p.E;
+    const int per = (E + 3) / 4, s0 = wave * per, ns = max(0, min(E, s0 + per) - s0);
+    const u64 ks = lane < ns ? sm.key[0][s0 + lane] : 0ull;
+    u64 mine[KPL];
+    int cnt[KPL];
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+        mine[j] = lane + 64 * j < E ? sm.key[0][lane + 64 * j] : 0ull;
+        cnt[j] = 0;
+    }
+    for (int s = 0; s < ns; ++s) {
+        const u64 K = readlane_u64(ks, s);
+#pragma unroll
+        for (int j = 0; j < KPL; ++j) cnt[j] += K > mine[j];
+    }
+#pragma unroll
+    for (int j = 0; j < KPL; ++j)
+        if (lane + 64 * j < E) sm.rcnt[wave][lane + 64 * j] = cnt[j];
+}
+
+// One token, wave 0, after the ranks: lane j < k takes the rank-j expert; the
+// weights (denominators summed in rank order, or in expert order over all E
+// for the softmax-without-renormalisation mode, as the oracle sums them),
+// then slots and the grouping of valid pairs.
+__device__ inline void weigh_one_row(const Params& p, Smem& sm, const LayerDev& L, int l, int lane) {
+    const int E = p.E, k = p.k;
+    const bool inp = lane < k;
+    const uint32_t my_e = inp ? sm.top_ids[0][lane] : 0u;
+    const float my_f = inp ? sm.top_ex[0][lane] : 0.0f;
+    const float mx = readlane_f32(my_f, 0);
+    const float ex = inp ? expf(my_f - mx) : 0.0f;
+    float denom = 0.0f;
+    if (p.mode == NAIWA_ROUTE_SOFTMAX_TOPK) {
+        constexpr int KPL = kMaxE / 64;
+        float ea[KPL];
+#pragma unroll
+        for (int j = 0; j < KPL; ++j) ea[j] = lane + 64 * j < E ? expf(sm.lg[0][lane + 64 * j] - mx) : 0.0f;
+#pragma unroll
+        for (int j = 0; j < KPL; ++j)
+            for (int ln = 0; ln < 64 && 64 * j + ln < E; ++ln) denom += readlane_f32(ea[j], ln);
+    } else {
+        for (int o = 0; o < k; ++o) denom += readlane_f32(ex, o);
+    }
+    mark_wave(p, l, 11);
+    group_pairs(p, sm, L, l, lane, inp, 0, my_e, inp ? ex / denom : 0.0f);
+    mark_wave(p, l, 12);
+}
 
 // ---------------------------------------------------------------------------
 // Q4_K gate/up with one 144-byte block per lane
@@ -310,12 +481,14 @@ __device__ __forceinline__ float q4k_chunk(const Q4Scales& s, int c, float alo, 
     return s.d * (sc0 * (alo - 128.0f * slo) + sc1 * (ahi - 128.0f * shi)) - s.dmin * (m0 * slo + m1 * shi);
 }
 
-// Dots of two Q4_K blocks (rows A and B, 9 x 16 bytes each in registers) with the
+// Dots of two Q4_K blocks (rows A and B, 9 x 16 bytes each in LDS) with the
 // same 256 staged activations: words = the block's 128 bf16 pair words, sums =
 // its 16 sums of 16.  Each activation word is loaded once and feeds both rows.
-__device__ __forceinline__ void q4k_block_dot2(const uint4* A, const uint4* B, const uint32_t* words,
+__device__ __forceinline__ void q4k_block_dot2(const uint8_t* A8, const uint8_t* B8, const uint32_t* words,
                                                const float* sums, float& ra, float& rb) {
-    const Q4Scales sa = q4k_scales(A[0]), sb = q4k_scales(B[0]);
+    auto A = [&](int j) { return naiwa_ld<uint4, NAIWA_AS_LDS>(A8 + 16 * j); };
+    auto B = [&](int j) { return naiwa_ld<uint4, NAIWA_AS_LDS>(B8 + 16 * j); };
+    const Q4Scales sa = q4k_scales(A(0)), sb = q4k_scales(B(0));
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         // the chunk's 32 activation words, all loads in flight before the first use
@@ -323,7 +496,7 @@ __device__ __forceinline__ void q4k_block_dot2(const uint4* A, const uint4* B, c
 #pragma unroll
         for (int i = 0; i < 8; ++i) x[i] = reinterpret_cast<const uint4*>(words + 32 * c)[i];
         const float4 sv = reinterpret_cast<const float4*>(sums)[c];
-        const uint4 qa0 = A[1 + 2 * c], qa1 = A[2 + 2 * c], qb0 = B[1 + 2 * c], qb1 = B[2 + 2 * c];
+        const uint4 qa0 = A(1 + 2 * c), qa1 = A(2 + 2 * c), qb0 = B(1 + 2 * c), qb1 = B(2 + 2 * c);
         const uint32_t wa[8] = {qa0.x, qa0.y, qa0.z, qa0.w, qa1.x, qa1.y, qa1.z, qa1.w};
         const uint32_t wb[8] = {qb0.x, qb0.y, qb0.z, qb0.w, qb1.x, qb1.y, qb1.z, qb1.w};
         float alo = 0.0f, ahi = 0.0f, blo = 0.0f, bhi = 0.0f;
@@ -352,41 +525,26 @@ __device__ __forceinline__ void q4k_block_dot2(const uint4* A, const uint4* B, c
     }
 }
 
-struct Q4Row {
-    uint4 blk[9];
-};
-
-// Loads of the Q4_K block this lane owns in the first 8 blocks of row r of the
-// slot: lanes 0-7 the gate row, lanes 8-15 the up row, block lr % 8 + 8 * grp8.
-__device__ __forceinline__ const uint8_t* q4_row_ptr(const LayerDev& L, uint32_t slot, int r, int64_t rb, int lr) {
-    return (lr >= 8 ? L.up + (int64_t)slot * L.up_stride : L.gate + (int64_t)slot * L.gate_stride) + (int64_t)r * rb;
-}
-
-__device__ __forceinline__ void q4_block_load(const uint8_t* row, int b, int nb, Q4Row& f) {
-    if (b < nb) {
-        const uint4* src = reinterpret_cast<const uint4*>(row + b * NAIWA_Q4_K_BYTES);
-#pragma unroll
-        for (int j = 0; j < 9; ++j) f.blk[j] = naiwa_ld<uint4, NAIWA_AS_GLOBAL>(src + j);
-    }
-}
-
-// h of every token of the segment for intermediate rows r, r + 1 (pair q):
-// f0 / f1 hold this lane's block of each row (rows of at most 8 blocks, H <= 2048).  The two results go out as one tagged word in
-// the down projection's 16-bit format DD.
+// h of every token of the segment for intermediate rows r, r + 1 (pair q),
+// with the item's rows in LDS: [gate row r][gate row r + 1][up row r][up row r + 1]
+// (rb bytes each).  Lane lr takes block lr % 8 of the gate rows (lanes 0-7) or
+// of the up rows (lanes 8-15), both rows at once; rows of at most 8 blocks
+// (H <= 2048).  The two results go out as one tagged word in the down
+// projection's 16-bit format DD.
 template <int DD>
-__device__ inline void q4_pair_compute(const Params& p, const Smem& sm, const LayerDev& L, const uint8_t* dyn,
-                                       int xstage, int q, int64_t rb, int nb, int lr, const Q4Row& f0,
-                                       const Q4Row& f1, uint32_t tag) {
-    const int I = p.I, H = p.H, k = p.k, I2 = I / 2;
+__device__ inline void q4_pair_compute(const Params& p, const Smem& sm, const uint8_t* dyn, int xstage, int q,
+                                       int nb, int lr, const uint8_t* item, int64_t rb, uint32_t tag) {
+    const int I2 = p.I / 2, H = p.H, k = p.k;
     const int s = q / I2, r = 2 * (q % I2);
     const int b = (int)sm.seg_begin[s], e = (int)sm.seg_begin[s + 1];
     const int b0 = lr & 7;
+    const uint8_t* A = item + (lr >= 8 ? 2 * rb : 0) + b0 * NAIWA_Q4_K_BYTES;
     for (int tt = b; tt < e; ++tt) {
         const int t = (int)sm.sorted[tt] / k;
         const uint32_t* words = (const uint32_t*)(dyn + t * xstage);   // 132 words per block (padded)
         const float* sums = (const float*)(words + H / 2 + 4 * nb);
         float g0 = 0.0f, g1 = 0.0f;   // this lane's share of row r and row r + 1
-        if (b0 < nb) q4k_block_dot2(f0.blk, f1.blk, words + b0 * 132, sums + b0 * 16, g0, g1);
+        if (b0 < nb) q4k_block_dot2(A, A + rb, words + b0 * 132, sums + b0 * 16, g0, g1);
         // lanes 0-7: gate . x, lanes 8-15: up . x; row_ror:8 brings lane 8 to lane 0
         g0 = naiwa_group_sum<8>(g0);
         g1 = naiwa_group_sum<8>(g1);
@@ -533,7 +691,7 @@ stack_kernel(Params p) {
     __shared__ Smem sm;
     __shared__ LayerDev layers_lds[kMaxLayers];
     const int tid = threadIdx.x, grp = tid / NAIWA_GROUP, lr = tid % NAIWA_GROUP;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = gridDim.x, bid = blockIdx.x;
     const int H = p.H, I = p.I, E = p.E, k = p.k, rows = p.rows;
     const int npairs = rows * k;
@@ -551,6 +709,8 @@ stack_kernel(Params p) {
     const int half_h = H / 2;                 // tagged words per token
     const int nlog = rows * E;
     uint8_t* const hdyn = dyn + rows * xstage;      // h staging, after the activations
+    uint8_t* const dbuf = hdyn + p.hpairs * hstage; // prefetched down rows: [pair][kChunk][drb]
+    uint8_t* const wb = dbuf + (size_t)p.dpre * kChunk * drb; // gate/up rounds
 
     // ---- prologue: layer descriptors into LDS; own chunks of x; layer-0 logits ----
     mark(p, p.n_layers, 0);
@@ -601,138 +761,147 @@ stack_kernel(Params p) {
 
         // ---- A: poll logits + activations, rank, weights, segments ----
         const int ngroups = rows * gpt_h;
-        for (int g0 = 0; g0 < ngroups; g0 += XG * kThreads) {
-            u64 xw[2 * XG];
-            auto xaddr = [&](int j) -> const u64* {
-                const int g = g0 + tid + (j >> 1) * kThreads;
-                if (g >= ngroups) return nullptr;
-                return xt_l + (size_t)(g / gpt_h) * half_h + 2 * (g % gpt_h) + (j & 1);
-            };
-            issue_tagged(xw, xaddr, tag);
-            if (g0 == 0) {
-                u64 lw[PPT];
-                auto laddr = [&](int j) -> const u64* {
-                    const int i = tid + j * kThreads;
-                    return i < nlog ? p.logits + i : nullptr;
+        if constexpr (MR == 1) {
+            // wave 0 routes the token while waves 1-3 poll and stage its activations
+            if (wave == 0) {
+                poll_one_row(p, sm, L, l, tag, lane);
+            } else {
+                constexpr int NT = kThreads - 64;
+                const int tx = tid - 64;
+                for (int g0 = 0; g0 < ngroups; g0 += XG * NT) {
+                    u64 xw[2 * XG];
+                    auto xaddr = [&](int j) -> const u64* {
+                        const int g = g0 + tx + (j >> 1) * NT;
+                        return g < ngroups ? xt_l + 2 * g + (j & 1) : nullptr;
+                    };
+                    issue_tagged(xw, xaddr, tag);
+                    wait_tagged(xw, xaddr, tag, p);
+#pragma unroll
+                    for (int j = 0; j < XG; ++j) {
+                        const int g = g0 + tx + j * NT;
+                        const bool in = g < ngroups;
+                        const uint32_t a = (uint32_t)xw[2 * j], b = (uint32_t)xw[2 * j + 1];
+                        stage_group<DG, DG == NAIWA_Q4_K>(naiwa_bf16_to_f32(a & 0xffffu), naiwa_bf16_to_f32(a >> 16),
+                                                          naiwa_bf16_to_f32(b & 0xffffu), naiwa_bf16_to_f32(b >> 16),
+                                                          in, in ? g : 0, dyn, H);
+                    }
+                }
+                if (wave == 1) mark_wave(p, l, 13);
+            }
+            __syncthreads();
+            mark(p, l, 0);
+            if (E <= 128)
+                rank_slice<2>(p, sm, wave, lane);
+            else
+                rank_slice<kMaxE / 64>(p, sm, wave, lane);
+            __syncthreads();
+            if (tid < E) {
+                const int r = sm.rcnt[0][tid] + sm.rcnt[1][tid] + sm.rcnt[2][tid] + sm.rcnt[3][tid];
+                if (r < k) {
+                    sm.top_ids[0][r] = (uint32_t)tid;
+                    sm.top_ex[0][r] = sm.lg[0][tid];
+                }
+            }
+            __syncthreads();
+            mark(p, l, 1);
+            if (wave == 0) weigh_one_row(p, sm, L, l, lane);
+        } else {
+            for (int g0 = 0; g0 < ngroups; g0 += XG * kThreads) {
+                u64 xw[2 * XG];
+                auto xaddr = [&](int j) -> const u64* {
+                    const int g = g0 + tid + (j >> 1) * kThreads;
+                    if (g >= ngroups) return nullptr;
+                    return xt_l + (size_t)(g / gpt_h) * half_h + 2 * (g % gpt_h) + (j & 1);
                 };
-                issue_tagged(lw, laddr, tag);
-                if (L.slot_of && tid < E) sm.slot_tab[tid] = naiwa_ld<int32_t, NAIWA_AS_GLOBAL>(L.slot_of + tid);
-                wait_tagged(lw, laddr, tag, p);
+                issue_tagged(xw, xaddr, tag);
+                if (g0 == 0) {
+                    u64 lw[PPT];
+                    auto laddr = [&](int j) -> const u64* {
+                        const int i = tid + j * kThreads;
+                        return i < nlog ? p.logits + i : nullptr;
+                    };
+                    issue_tagged(lw, laddr, tag);
+                    if (L.slot_of && tid < E) sm.slot_tab[tid] = naiwa_ld<int32_t, NAIWA_AS_GLOBAL>(L.slot_of + tid);
+                    wait_tagged(lw, laddr, tag, p);
 #pragma unroll
-                for (int j = 0; j < PPT; ++j) {
-                    const int i = tid + j * kThreads;
-                    if (i < nlog) {
-                        const float f = __uint_as_float((uint32_t)lw[j]);
-                        sm.lg[i / E][i % E] = f;
-                        sm.key[i / E][i % E] = rank_key(f, i % E);
+                    for (int j = 0; j < PPT; ++j) {
+                        const int i = tid + j * kThreads;
+                        if (i < nlog) {
+                            const float f = __uint_as_float((uint32_t)lw[j]);
+                            sm.lg[i / E][i % E] = f;
+                            sm.key[i / E][i % E] = rank_key(f, i % E);
+                        }
                     }
+                    if ((E & 1) && tid < rows) sm.key[tid][E] = 0; // pad: below every real key
                 }
-                if ((E & 1) && tid < rows) sm.key[tid][E] = 0; // pad: below every real key
-            }
-            wait_tagged(xw, xaddr, tag, p);
+                wait_tagged(xw, xaddr, tag, p);
 #pragma unroll
-            for (int j = 0; j < XG; ++j) {
-                const int g = g0 + tid + j * kThreads;
-                const bool in = g < ngroups;
-                const int t = in ? g / gpt_h : 0, gg = in ? g % gpt_h : 0;
-                const uint32_t a = (uint32_t)xw[2 * j], b = (uint32_t)xw[2 * j + 1];
-                stage_group<DG, DG == NAIWA_Q4_K>(naiwa_bf16_to_f32(a & 0xffffu), naiwa_bf16_to_f32(a >> 16),
-                                naiwa_bf16_to_f32(b & 0xffffu), naiwa_bf16_to_f32(b >> 16), in, gg,
-                                dyn + t * xstage, H);
+                for (int j = 0; j < XG; ++j) {
+                    const int g = g0 + tid + j * kThreads;
+                    const bool in = g < ngroups;
+                    const int t = in ? g / gpt_h : 0, gg = in ? g % gpt_h : 0;
+                    const uint32_t a = (uint32_t)xw[2 * j], b = (uint32_t)xw[2 * j + 1];
+                    stage_group<DG, DG == NAIWA_Q4_K>(naiwa_bf16_to_f32(a & 0xffffu), naiwa_bf16_to_f32(a >> 16),
+                                                      naiwa_bf16_to_f32(b & 0xffffu), naiwa_bf16_to_f32(b >> 16),
+                                                      in, gg, dyn + t * xstage, H);
+                }
             }
-        }
-        __syncthreads();
-        mark(p, l, 0);
-        {
-            // rank of every (token, expert): the number of keys above its own;
-            // tpi lanes per item split the comparisons
-            const int items = rows * E;
-            const int tpi = items * 4 <= kThreads ? 4 : (items * 2 <= kThreads ? 2 : 1);
-            const int sub = tid % tpi;
-            const int half_e = (E + 1) / 2;
-            for (int it = tid / tpi; it < (items + (kThreads / tpi) - 1) / (kThreads / tpi) * (kThreads / tpi);
-                 it += kThreads / tpi) {
-                const bool in = it < items;
-                const int t = in ? it / E : 0, e = in ? it % E : 0;
-                const u64 me = sm.key[t][e];
-                const ulonglong2* kv = reinterpret_cast<const ulonglong2*>(sm.key[t]);
-                int cnt = 0;
-                if (in) {
-                    // 8 key pairs in flight per batch; a zero key is below every real key
+            __syncthreads();
+            mark(p, l, 0);
+            {
+                // rank of every (token, expert): the number of keys above its own;
+                // tpi lanes per item split the comparisons
+                const int items = rows * E;
+                const int tpi = items * 4 <= kThreads ? 4 : (items * 2 <= kThreads ? 2 : 1);
+                const int sub = tid % tpi;
+                const int half_e = (E + 1) / 2;
+                for (int it = tid / tpi; it < (items + (kThreads / tpi) - 1) / (kThreads / tpi) * (kThreads / tpi);
+                     it += kThreads / tpi) {
+                    const bool in = it < items;
+                    const int t = in ? it / E : 0, e = in ? it % E : 0;
+                    const u64 me = sm.key[t][e];
+                    const ulonglong2* kv = reinterpret_cast<const ulonglong2*>(sm.key[t]);
+                    int cnt = 0;
+                    if (in) {
+                        // 8 key pairs in flight per batch; a zero key is below every real key
 #pragma unroll 4
-                    for (int o = sub; o < half_e; o += tpi) {
-                        const ulonglong2 v = kv[o];
-                        cnt += (v.x > me) + (v.y > me);
+                        for (int o = sub; o < half_e; o += tpi) {
+                            const ulonglong2 v = kv[o];
+                            cnt += (v.x > me) + (v.y > me);
+                        }
+                    }
+                    if (tpi >= 2) cnt += __builtin_amdgcn_update_dpp(0, cnt, 0xB1, 0xF, 0xF, true);
+                    if (tpi >= 4) cnt += __builtin_amdgcn_update_dpp(0, cnt, 0x4E, 0xF, 0xF, true);
+                    if (in && sub == 0 && cnt < k) {
+                        sm.top_ids[t][cnt] = (uint32_t)e;
+                        sm.top_ex[t][cnt] = sm.lg[t][e];
                     }
                 }
-                if (tpi >= 2) cnt += __builtin_amdgcn_update_dpp(0, cnt, 0xB1, 0xF, 0xF, true);
-                if (tpi >= 4) cnt += __builtin_amdgcn_update_dpp(0, cnt, 0x4E, 0xF, 0xF, true);
-                if (in && sub == 0 && cnt < k) {
-                    sm.top_ids[t][cnt] = (uint32_t)e;
-                    sm.top_ex[t][cnt] = sm.lg[t][e];
+            }
+            __syncthreads();
+            mark(p, l, 1);
+            if (wave == 0) {
+                // weights (denominators summed in rank order, as the oracle does), then
+                // slots and the grouping of valid pairs: one pair per lane
+                const int q = lane;
+                const bool inp = q < npairs;
+                const int t = inp ? q / k : 0, j = inp ? q % k : 0;
+                const float mx = sm.top_ex[t][0];
+                const uint32_t e = inp ? sm.top_ids[t][j] : 0u;
+                const float ex = inp ? expf(sm.top_ex[t][j] - mx) : 0.0f;
+                sm.exv[q] = ex;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                float denom = 0.0f;
+                if (inp) {
+                    if (p.mode == NAIWA_ROUTE_SOFTMAX_TOPK) {
+                        for (int o = 0; o < E; ++o) denom += expf(sm.lg[t][o] - mx);
+                    } else {
+                        for (int o = 0; o < k; ++o) denom += sm.exv[t * k + o];
+                    }
                 }
-            }
-        }
-        __syncthreads();
-        mark(p, l, 1);
-        if (wave == 0) {
-            // weights (denominators summed in rank order, as the oracle does), slot
-            // lookup, and the grouping of valid pairs by slot: one pair per lane
-            const int q = lane;
-            const bool inp = q < npairs;
-            const int t = inp ? q / k : 0, j = inp ? q % k : 0;
-            const float mx = sm.top_ex[t][0];
-            const uint32_t e = inp ? sm.top_ids[t][j] : 0u;
-            const float ex = inp ? expf(sm.top_ex[t][j] - mx) : 0.0f;
-            sm.exv[q] = ex;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            float denom = 0.0f;
-            if (inp) {
-                if (p.mode == NAIWA_ROUTE_SOFTMAX_TOPK) {
-                    for (int o = 0; o < E; ++o) denom += expf(sm.lg[t][o] - mx);
-                } else {
-                    for (int o = 0; o < k; ++o) denom += sm.exv[t * k + o];
-                }
-            }
-            const float w = inp ? ex / denom : 0.0f;
-            const int32_t s = inp ? (L.slot_of ? sm.slot_tab[e] : (int32_t)e) : -1;
-            const bool ok = inp && s >= 0 && s < L.slots;
-            if (inp && !ok && bid == 0) atomicAdd(&p.status[1], 1);
-            if (inp && bid == 0 && p.ids_out) {
-                p.ids_out[(size_t)l * npairs + q] = e;
-                p.w_out[(size_t)l * npairs + q] = w;
-            }
-            const bool valid = ok && w != 0.0f;
-            // sort key (slot, pair); invalid pairs sort last
-            const uint32_t key = valid ? (((uint32_t)s << 6) | (uint32_t)q) : 0xFFFFFFFFu;
-            int rank = 0;
-            for (int o = 0; o < npairs; ++o) rank += (uint32_t)__builtin_amdgcn_readlane((int)key, o) < key;
-            sm.pair_slot[q] = valid ? (uint32_t)s : 0u;
-            sm.pair_w[q] = valid ? w : 0.0f;
-            if (valid) {
-                sm.sorted[rank] = (uint32_t)q;
-                sm.srt_slot[rank] = (uint32_t)s;
-                sm.srt_tok[rank] = (uint32_t)t;
-            }
-            const unsigned long long valids = __ballot(valid);
-            const int nvalid = __popcll(valids);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            // lane r looks at sorted position r: a segment starts where the slot changes
-            const bool start = lane < nvalid && (lane == 0 || sm.srt_slot[lane] != sm.srt_slot[lane - 1]);
-            const unsigned long long starts = __ballot(start);
-            if (start) {
-                const int si = __popcll(starts & ((1ull << lane) - 1ull));
-                sm.seg_begin[si] = (uint32_t)lane;
-                sm.seg_slot[si] = sm.srt_slot[lane];
-            }
-            if (lane == 0) {
-                const int ns = __popcll(starts);
-                sm.seg_begin[ns] = (uint32_t)nvalid;
-                sm.nseg = ns;
+                group_pairs(p, sm, L, l, lane, inp, t, e, inp ? ex / denom : 0.0f);
             }
         }
         __syncthreads();
@@ -740,37 +909,65 @@ stack_kernel(Params p) {
         const int nvalid = (int)sm.seg_begin[nseg];
         mark(p, l, 2);
 
-        // ---- B: gate/up, with phase C's down rows and router columns loaded alongside ----
+        // ---- B: gate/up ----
         const int total = nseg * (I / 2);        // (segment, row pair) items
         const int per = (total + G - 1) / G;
         const int q0 = bid * per, q1 = min(total, q0 + per);
         const bool owner = bid < nchunks;
-        // gate/up work item q = (segment, row pair); fa/fb hold the pair's rows,
-        // fc/fd the group's next pair (loads in flight)
-        Q4Row fa, fb, fc, fd;
-        const int qa = q0 + grp, qb = qa + kGroups;
         const int I2 = I / 2;
-        auto pair_rows = [&](int q, Q4Row& x0, Q4Row& x1) {
-            const uint8_t* r0 = q4_row_ptr(L, sm.seg_slot[q / I2], 2 * (q % I2), rb, lr);
-            q4_block_load(r0, lr & 7, nb, x0);
-            q4_block_load(r0 + rb, lr & 7, nb, x1);
+        // down rows of the first chunk for the first pairs: they depend on the
+        // routing only, so they are on their way during gate/up and the h wait
+        const int npre = owner ? min(p.dpre, nvalid) : 0;
+        auto prefetch_down = [&]() {
+            const int f0 = chunk_at(bid, nchunks) * kChunk;
+            const int span = kChunk * (int)drb / 16; // 16-byte pieces of kChunk consecutive rows
+            for (int v = wave; v < npre; v += kThreads / 64) {
+                const uint8_t* src = L.down + (int64_t)sm.pair_slot[sm.sorted[v]] * L.down_stride + (int64_t)f0 * drb;
+                uint8_t* dst = dbuf + (size_t)v * kChunk * drb;
+                for (int c = 0; c * 64 < span; ++c)
+                    if (c * 64 + lane < span) lds_dma16(src + (c * 64 + lane) * 16, dst + c * 1024);
+            }
         };
         if constexpr (DG == NAIWA_Q4_K) {
-            if (qa < q1) pair_rows(qa, fa, fb);
-            if (qb < q1) pair_rows(qb, fc, fd);
-        }
-        mark(p, l, 3);
-        if constexpr (DG == NAIWA_Q4_K) {
-#pragma unroll 1
-            for (int q = qa; q < q1; q += kGroups) {
-                q4_pair_compute<DD>(p, sm, L, dyn, xstage, q, rb, nb, lr, fa, fb, tag);
-                fa = fc;
-                fb = fd;
-                if (q + 2 * kGroups < q1) pair_rows(q + 2 * kGroups, fc, fd);
+            // rounds of up to p.bitems items: the gate and up row pairs of each item
+            // are gathered into LDS with coalesced 16-byte DMA pieces (wave w takes
+            // items w, w + 4, ...), then group g computes item g of the round
+            const int pair_pieces = (int)(rb / 8);       // two rows, 16-byte pieces
+            const size_t item_bytes = 4 * (size_t)rb;
+            for (int r0 = q0; r0 < q1; r0 += p.bitems) {
+                const int nr = min(p.bitems, q1 - r0);
+                if (r0 > q0) __syncthreads(); // the previous round's items are consumed
+                for (int i = wave; i < nr; i += kThreads / 64) {
+                    const int q = r0 + i;
+                    const uint32_t slot = sm.seg_slot[q / I2];
+                    const int64_t roff = (int64_t)(2 * (q % I2)) * rb;
+                    const uint8_t* g = L.gate + (int64_t)slot * L.gate_stride + roff;
+                    const uint8_t* u = L.up + (int64_t)slot * L.up_stride + roff;
+                    uint8_t* dst = wb + (size_t)i * item_bytes;
+                    for (int c = 0; c * 64 < pair_pieces; ++c) {
+                        if (c * 64 + lane < pair_pieces) {
+                            lds_dma16(g + (c * 64 + lane) * 16, dst + c * 1024);
+                            lds_dma16(u + (c * 64 + lane) * 16, dst + 2 * rb + c * 1024);
+                        }
+                    }
+                }
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+                if (r0 == q0) {
+                    mark(p, l, 3);
+                    prefetch_down();
+                }
+                if (grp < nr) q4_pair_compute<DD>(p, sm, dyn, xstage, r0 + grp, nb, lr, wb + grp * item_bytes, rb, tag);
+            }
+            if (q0 >= q1) {
+                mark(p, l, 3);
+                prefetch_down();
             }
         } else {
+            mark(p, l, 3);
+            prefetch_down();
 #pragma unroll 1
-            for (int q = qa; q < q1; q += kGroups) unit_pair<DG, DD>(p, sm, L, dyn, q, xstage, rb, nu, lr, tag);
+            for (int q = q0 + grp; q < q1; q += kGroups) unit_pair<DG, DD>(p, sm, L, dyn, q, xstage, rb, nu, lr, tag);
         }
         mark(p, l, 4);
 
@@ -783,13 +980,20 @@ stack_kernel(Params p) {
             for (int cp = bid, ci = 0; cp < nchunks; cp += G, ++ci) {
                 const int c = chunk_at(cp, nchunks);
                 const int f0 = c * kChunk;
-                for (int b0 = 0; b0 < nvalid; b0 += kCPairs) {
-                    const int nbp = min(kCPairs, nvalid - b0);
+                for (int b0 = 0; b0 < nvalid; b0 += p.hpairs) {
+                    const int nbp = min(p.hpairs, nvalid - b0);
                     if (ci > 0 || b0 > 0) __syncthreads(); // the previous pass's dots read hdyn
                     stage_h<DD>(p, sm, b0, nbp, hdyn, hstage, tag);
+                    // the prefetched rows have landed (vmcnt also counts LDS DMA)
+                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                     __syncthreads();
+                    // this pass's rows come from LDS when they were prefetched
+                    const bool from_lds = ci == 0 && b0 == 0 && nbp <= npre;
                     mark(p, l, 5);
-                    {
+                    // dots of every (feature, pair) row with the pair's h: AS says
+                    // where the rows are read from (global memory, or the LDS prefetch)
+                    auto dots = [&](auto as) {
+                        constexpr int AS = decltype(as)::value;
                         constexpr int DUM = 2;
                         const int nit = kChunk * nbp;
                         for (int it0 = grp; it0 < nit; it0 += kGroups * kCB) {
@@ -802,13 +1006,15 @@ stack_kernel(Params p) {
                                 for (int j = 0; j < kCB; ++j) {
                                     const int it = min(it0 + j * kGroups, nit - 1);
                                     const int fi = it % kChunk, pi = it / kChunk;
-                                    const uint8_t* drow = L.down +
-                                                          (int64_t)sm.pair_slot[sm.sorted[b0 + pi]] * L.down_stride +
-                                                          (int64_t)(f0 + fi) * drb;
+                                    const uint8_t* drow =
+                                        AS == NAIWA_AS_LDS
+                                            ? dbuf + (size_t)(pi * kChunk + fi) * drb
+                                            : L.down + (int64_t)sm.pair_slot[sm.sorted[b0 + pi]] * L.down_stride +
+                                                  (int64_t)(f0 + fi) * drb;
 #pragma unroll
                                     for (int i = 0; i < DUM; ++i) {
                                         const int u = base + NAIWA_GROUP * i;
-                                        if (u < dnu) frg[j][i] = Fmt<DD>::template load<NAIWA_AS_GLOBAL>(drow, u);
+                                        if (u < dnu) frg[j][i] = Fmt<DD>::template load<AS>(drow, u);
                                     }
                                 }
 #pragma unroll
@@ -832,7 +1038,11 @@ stack_kernel(Params p) {
                                         v * sm.pair_w[sm.sorted[b0 + it / kChunk]];
                             }
                         }
-                    }
+                    };
+                    if (DD == NAIWA_Q4_K && from_lds)
+                        dots(std::integral_constant<int, NAIWA_AS_LDS>());
+                    else
+                        dots(std::integral_constant<int, NAIWA_AS_GLOBAL>());
                 }
                 __syncthreads();
                 mark(p, l, 6);
@@ -954,24 +1164,26 @@ struct LaunchOp {
 static int g_fused_blocks_per_cu = 1;
 static bool g_trace_enabled = false;
 static int g_trace_layers = 0;
+static int g_trace_blocks = 0;
 
-// Phase timestamps of the fused kernel (diagnostic): when on, the first and
-// last block record s_memrealtime ticks at each phase boundary of every layer.
+// Phase timestamps of the fused kernel (diagnostic): when on, every block
+// records s_memrealtime ticks at each phase boundary of every layer.
 extern "C" int naiwa_stack_trace_enable(int on) {
     g_trace_enabled = on != 0;
     return NAIWA_OK;
 }
 
-// Copies the last traced launch's timestamps: [2][n_layers + 1][8] u64 ticks
-// (the extra layer row is the prologue).  Synchronizes the device.
-extern "C" int naiwa_stack_trace_read(uint64_t* out, int capacity, int* n_layers) {
+// Copies the last traced launch's timestamps: [blocks][n_layers + 1][16] u64
+// ticks (the extra layer row is the prologue).  Synchronizes the device.
+extern "C" int naiwa_stack_trace_read(uint64_t* out, int capacity, int* n_layers, int* blocks) {
     int rc = 0;
     if (!g_trace_layers) return NAIWA_E_NOT_FOUND;
-    const size_t n = (size_t)2 * (g_trace_layers + 1) * kTraceSlots;
-    if (!out || capacity < (int)n) return NAIWA_E_INVALID;
+    const size_t n = (size_t)g_trace_blocks * (g_trace_layers + 1) * kTraceSlots;
+    if (!out || capacity < 0 || (size_t)capacity < n) return NAIWA_E_INVALID;
     void* t = naiwa_scratch(NAIWA_SCRATCH_STACK + 2, n * 8, &rc);
     if (!t) return rc;
     if (n_layers) *n_layers = g_trace_layers;
+    if (blocks) *blocks = g_trace_blocks;
     return naiwa_hip_rc(hipMemcpy(out, t, n * 8, hipMemcpyDeviceToHost));
 }
 
@@ -1038,10 +1250,32 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     if (fg == NAIWA_Q4_K && H > 8 * NAIWA_QK_K) return NAIWA_E_UNSUPPORTED; // one block per lane: H <= 2048
     // dynamic LDS: activations | h staging
     constexpr size_t kMaxDynLds = 104 * 1024;   // 160 KB per CU minus the static LDS
+    const int hpairs = std::min(kCPairs, rows * k);
     const size_t lds_x = (size_t)rows * fused_xstage(fg, H);
-    const size_t lds_h = (size_t)kCPairs * naiwa_stage_bytes(fd, I);
+    const size_t lds_h = (size_t)hpairs * naiwa_stage_bytes(fd, I);
     size_t lds = lds_x + lds_h;
     if (lds > kMaxDynLds) return NAIWA_E_UNSUPPORTED;
+    // Q4_K down rows of the first phase-C pass, prefetched into LDS when they fit
+    // beside at least one gate/up item
+    int dpre = 0;
+    if (fd == NAIWA_Q4_K) {
+        const size_t pre = (size_t)hpairs * kChunk * (size_t)naiwa_row_bytes(NAIWA_Q4_K, I);
+        const size_t gu = fg == NAIWA_Q4_K ? 4 * (size_t)naiwa_row_bytes(NAIWA_Q4_K, H) : 0;
+        if (lds + pre + gu <= kMaxDynLds) {
+            dpre = hpairs;
+            lds += pre;
+        }
+    }
+    // Q4_K gate/up rounds: at most one item per 16-lane group, at most what one
+    // workgroup's share of a full step needs, within the LDS left over
+    int bitems = 0;
+    if (fg == NAIWA_Q4_K) {
+        const size_t item = 4 * (size_t)naiwa_row_bytes(NAIWA_Q4_K, H);
+        const int share = (rows * k * (I / 2) + 255) / 256;
+        bitems = (int)std::min<size_t>((size_t)std::min(kGroups, share), (kMaxDynLds - lds) / item);
+        if (bitems < 1) return NAIWA_E_UNSUPPORTED;
+        lds += (size_t)bitems * item;
+    }
 
     hipStream_t st = (hipStream_t)stream;
     int rc = 0, dev = 0, cus = 0, khz = 0;
@@ -1142,11 +1376,15 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     prm.w_out = w_out;
     prm.spin_limit = (uint64_t)khz * 2000ull; // 2 s
     prm.seq = seq;
-    prm.trace = g_trace_enabled ? (unsigned long long*)naiwa_scratch(NAIWA_SCRATCH_STACK + 2,
-                                                                     (size_t)2 * (n_layers + 1) * kTraceSlots * 8, &rc)
+    prm.bitems = bitems;
+    prm.hpairs = hpairs;
+    prm.dpre = dpre;
+    prm.trace = g_trace_enabled ? (unsigned long long*)naiwa_scratch(
+                                      NAIWA_SCRATCH_STACK + 2, (size_t)blocks * (n_layers + 1) * kTraceSlots * 8, &rc)
                                 : nullptr;
     if (g_trace_enabled && !prm.trace) return rc;
     g_trace_layers = n_layers;
+    g_trace_blocks = blocks;
     zero_u32<<<1, 64, 0, st>>>((unsigned int*)(sync + kStatusOff), 64);
     const LaunchOp go{&prm, blocks, lds, st};
     return rows == 1 ? with_kernel<1>(fg, fd, go) : with_kernel<kMaxRows>(fg, fd, go);

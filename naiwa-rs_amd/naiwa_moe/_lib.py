@@ -130,7 +130,7 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_stack_status": (i32, [_P(i32), _P(i32)]),
     "naiwa_residual_add_bf16": (i32, [vp, vp, i64, i64]),
     "naiwa_stack_trace_enable": (i32, [i32]),
-    "naiwa_stack_trace_read": (i32, [_P(u64), i32, _P(i32)]),
+    "naiwa_stack_trace_read": (i32, [_P(u64), i32, _P(i32), _P(i32)]),
     "naiwa_upload_expert": (i32, [vp, vp, vp, i64, i64, i64]),
     # include/naiwa_doorbell.h
     "naiwa_topk_doorbell_create": (i32, [i32, _P(vp)]),

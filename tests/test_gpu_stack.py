@@ -12,10 +12,14 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-2
 
 
-def build_stack(nm, L, H, E, I, dt, seed, slots_perm=False):
+def build_stack(nm, L, H, E, I, dt, seed, slots_perm=False, tie_pairs=False):
     layers, host, keep = [], [], []
     for l in range(L):
         g, u, d, r = S.layer(seed + l, E, H, I, dt)
+        if tie_pairs:
+            # experts 2j and 2j + 1 share a router row: their logits are equal
+            r = r.copy()
+            r[1::2] = r[0::2]
         banks = nm.LayerBanks(E + (3 if slots_perm else 0), H, I, dt)
         slot_of = np.arange(E, dtype=np.int32)
         if slots_perm:
@@ -42,6 +46,9 @@ def oracle_layer(host_layer, x_bf16, E, k, mode, H):
 @pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("rows,L,H,E,k,I,dt,mode,perm", [
     (1, 3, 2048, 128, 8, 768, (O.Q4_K,) * 3, O.ROUTE_SOFTMAX_TOPK_RENORM, False),  # Qwen3 shape
+    (1, 2, 1024, 8, 2, 2048, (O.Q8_0,) * 3, O.ROUTE_TOPK_SOFTMAX, True),
+    (1, 2, 2048, 64, 6, 1408, (O.Q4_K, O.Q4_K, O.Q8_0), O.ROUTE_SOFTMAX_TOPK, True),
+    (1, 2, 512, 256, 8, 256, (O.Q8_0,) * 3, O.ROUTE_SOFTMAX_TOPK_RENORM, True),   # 256 experts
     (8, 2, 2048, 128, 8, 768, (O.Q4_K,) * 3, O.ROUTE_SOFTMAX_TOPK_RENORM, True),
     (3, 2, 1024, 8, 2, 2048, (O.Q8_0,) * 3, O.ROUTE_TOPK_SOFTMAX, False),          # C1 shape
     (2, 2, 2048, 64, 6, 1408, (O.Q4_K, O.Q4_K, O.Q8_0), O.ROUTE_SOFTMAX_TOPK, True),  # DS-V2-Lite
@@ -113,3 +120,33 @@ def test_fused_is_deterministic(gpu):
         nm.synchronize()
         outs.append(xd.download(np.uint16))
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
+@pytest.mark.parametrize("rows,mode", [(1, O.ROUTE_SOFTMAX_TOPK_RENORM), (1, O.ROUTE_SOFTMAX_TOPK),
+                                       (2, O.ROUTE_TOPK_SOFTMAX)])
+def test_fused_routing_ties_take_the_lower_id(gpu, rows, mode):
+    """Router rows duplicated in pairs make every selected logit tie with its
+    twin: the order is (logit desc, id asc), so ids and weights stay bit-exact
+    with the oracle's selection."""
+    nm = gpu
+    H, E, k, I = 1024, 64, 8, 256
+    dt = (O.Q8_0,) * 3
+    layers, host, keep = build_stack(nm, 1, H, E, I, dt, 990 + rows, tie_pairs=True)
+    x = S.activations_bf16(991 + rows, rows, H)
+    xd = nm.DeviceBuffer.from_array(x)
+    ids_d = nm.DeviceBuffer(rows * k * 4)
+    w_d = nm.DeviceBuffer(rows * k * 4)
+    print(f"[stack ties rows={rows} mode={mode}]", flush=True)
+    nm.stack_decode(layers, xd, rows, H, E, k, mode=mode, ids_out=ids_d, w_out=w_d, fused=True)
+    nm.synchronize()
+    assert nm.stack_status() == (0, 0)
+    ids = ids_d.download(np.uint32).reshape(rows, k)
+    w = w_d.download(np.float32).reshape(rows, k)
+    want_ids, want_w, y = oracle_layer(host[0], x, E, k, mode, H)
+    # the twins come out adjacent, even id first
+    assert np.all(want_ids[:, 0::2] % 2 == 0) and np.array_equal(want_ids[:, 1::2], want_ids[:, 0::2] + 1)
+    assert np.array_equal(ids, want_ids), (ids, want_ids)
+    assert np.allclose(w, want_w, rtol=1e-5, atol=1e-7)
+    got_y = O.from_bf16(xd.download(np.uint16).reshape(rows, H)) - O.from_bf16(x)
+    slack = np.abs(O.from_bf16(x)).max() * 2.0 ** -8 / max(np.abs(y).max(), 1e-30)
+    assert S.max_rel_err(got_y, y) < TOL + slack
