@@ -243,7 +243,7 @@ def print_trace(nm, run, stream, L, khz):
     run()
     stream.sync()
     lib.naiwa_stack_trace_enable(0)
-    slots = 16
+    slots = 24
     cap = 2048 * (L + 1) * slots
     buf = (C.c_uint64 * cap)()
     nl, nb = C.c_int(0), C.c_int(0)
@@ -300,6 +300,23 @@ def print_trace(nm, run, stream, L, khz):
             ", ".join(f"{n} {np.mean(v):.2f}" for n, v in sub.items()))
     log("trace: XCD of the 16 latest gate/up finishers " + str(late_gu.astype(int).tolist()) +
         ", of the 16 latest partials " + str(late_dn.astype(int).tolist()))
+    # per-XCD medians (workgroup b runs on XCD b % 8), us after the last logits publish
+    rows = []
+    pubs = np.concatenate([[t[:nlead, L, 2].max()], t[:nlead, : L - 2, 9].max(0)])
+    rel = t[:, : L - 1, :] - pubs[None, :, None]
+    for x in range(8):
+        m = rel[x::8]
+        rows.append(f"xcd{x}: recv {np.median(m[:, :, 0]):.2f} dma {np.median(m[:, :, 3] - m[:, :, 2]):.2f} "
+                    f"gu_end {np.median(m[:, :, 4]):.2f} h_recv {np.median(m[:, :, 5]):.2f} "
+                    f"gu_last_wave {np.median(m[:, :, 16]):.2f} max {np.median(m[:, :, 16].max(0)):.2f} "
+                    f"ind {np.median(m[:, :, 14]):.2f} h_loads {np.median(m[:, :, 17]):.2f} "
+                    f"polls {np.median(t[x::8, : L - 1, 18] * (khz / 1000.0)):.0f} h_read {np.median(m[:, :, 15]):.2f} "
+                    f"down {np.median(m[:, :, 6] - m[:, :, 5]):.2f} part_end {np.median(m[:, :, 8]):.2f}")
+    log("trace: per XCD, median us after the logits publish:\n  " + "\n  ".join(rows))
+    lead = rel[:nlead]
+    log(f"trace: leaders: part_end(own) {np.median(lead[:, :, 8]):.2f} partials seen {np.median(lead[:, :, 19]):.2f} "
+        f"(polls {np.median(t[:nlead, : L - 1, 20] * (khz / 1000.0)):.0f}) published {np.median(lead[:, :, 9]):.2f}; "
+        f"all part_end max {np.median(rel[:, :, 8].max(0)):.2f}")
     log(f"trace: kernel span {t[:, L - 1, 9].max() - t[:, L, 0].min():.1f} us over {G} workgroups")
 
 

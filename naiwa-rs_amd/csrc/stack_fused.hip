@@ -53,7 +53,7 @@ namespace {
 
 typedef unsigned long long u64;
 
-constexpr int kThreads = 256;             // 4 waves, 16 groups of 16 lanes
+constexpr int kThreads = 512;             // 8 waves (two per SIMD), 32 groups of 16 lanes
 constexpr int kGroups = kThreads / NAIWA_GROUP;
 constexpr int kMaxRows = 8;               // tokens per step served by this kernel
 constexpr int kMaxK = 8;                  // routed experts per token
@@ -63,10 +63,10 @@ constexpr int kLeaders = 32;              // workgroups that add the router part
 constexpr int kChunk = NAIWA_ROUTER_CHUNK; // output features per phase-C chunk
 constexpr int kMaxChunks = 4;             // chunks per workgroup
 constexpr int kCPairs = 16;               // h vectors staged per phase-C pass
-constexpr int kTraceSlots = 16;
+constexpr int kTraceSlots = 24;
 constexpr int kMaxLayers = 128;           // layer descriptors kept in LDS (tags hold layer + 1 < 256)
 constexpr int kXG = 8;                    // activation groups (4 values) per thread per poll round
-constexpr int kHG = 8;                    // h groups (4 values, 2 words) per thread per poll round
+constexpr int kHG = 4;                    // h groups (4 values, 2 words) per thread per poll round
 constexpr int kCB = 2;                    // down rows per group in flight (general path)
 
 struct LayerDev {
@@ -86,8 +86,9 @@ struct Params {
     uint16_t* x;                 // [rows, H] bf16: layer-0 input, last layer's output
     u64* xt;                     // [2][rows][H/2] tagged bf16 pairs (x of layer l in buffer l & 1)
     u64* h;                      // [kMaxPairs][I/2] tagged pairs of 16-bit values (down format)
-    u64* part;                   // [chunk owners][rows * E][2] tagged int64 halves
+    u64* part;                   // [rows * E][chunk owners][2] tagged int64 halves
     u64* logits;                 // [rows * E] tagged f32
+    u64* done;                   // [grid] tagged: the workgroup's h words of the layer are stored
     int* status;                 // [0] wait timeouts, [1] missing experts
     uint32_t* ids_out;           // [n_layers, rows, k] or null
     float* w_out;
@@ -97,18 +98,25 @@ struct Params {
     int bitems;                  // Q4_K gate/up: (segment, row pair) items per LDS round
     int hpairs;                  // h vectors staged per phase-C pass
     int dpre;                    // Q4_K down: pairs whose rows are prefetched into LDS (0 = none)
+    int trace_layer;             // the layer being traced (diagnostics)
 };
 
+// One diagnostic value of this workgroup for a layer (row n_layers: the
+// prologue), when tracing; anything outside the trace buffer is dropped.
+__device__ __forceinline__ void trace_put(const Params& p, int layer, int slot, unsigned long long v) {
+    if (!p.trace || layer < 0 || layer > p.n_layers || slot < 0 || slot >= kTraceSlots) return;
+    p.trace[((size_t)blockIdx.x * (p.n_layers + 1) + layer) * kTraceSlots + slot] = v;
+}
 // Phase timestamps (s_memrealtime, one device-wide clock) of every workgroup, when tracing.
 __device__ __forceinline__ void mark(const Params& p, int layer, int slot) {
     if (!p.trace || threadIdx.x != 0) return;
-    p.trace[((size_t)blockIdx.x * (p.n_layers + 1) + layer) * kTraceSlots + slot] = wall_clock64();
+    trace_put(p, layer, slot, wall_clock64());
 }
 
 // The same, recorded by the first lane of the calling wave.
 __device__ __forceinline__ void mark_wave(const Params& p, int layer, int slot) {
     if (!p.trace || (threadIdx.x & 63) != 0) return;
-    p.trace[((size_t)blockIdx.x * (p.n_layers + 1) + layer) * kTraceSlots + slot] = wall_clock64();
+    trace_put(p, layer, slot, wall_clock64());
 }
 
 struct Smem {
@@ -183,13 +191,13 @@ __device__ __forceinline__ void issue_tagged(u64 (&w)[N], const F& addr, uint32_
 }
 // Reload the words whose tag is not current until all are (or the wait gives up).
 template <int N, class F>
-__device__ inline void wait_tagged(u64 (&w)[N], const F& addr, uint32_t tag, const Params& p) {
+__device__ inline unsigned wait_tagged(u64 (&w)[N], const F& addr, uint32_t tag, const Params& p) {
     Poll s;
     while (true) {
         bool ok = true;
 #pragma unroll
         for (int j = 0; j < N; ++j) ok &= tag_ok(w[j], tag);
-        if (ok || !poll_continue(p, s)) return;
+        if (ok || !poll_continue(p, s)) return s.n;
 #pragma unroll
         for (int j = 0; j < N; ++j)
             if (!tag_ok(w[j], tag)) w[j] = ld64(addr(j));
@@ -218,15 +226,24 @@ __device__ __forceinline__ int chunk_at(int p, int nchunks) {
     return (((r >> 2) << 3) + x) * 4 + (r & 3);
 }
 
-// Publish this workgroup's router partials for layer tag `tag`.
+// The thread that owns router item slot 0 of the partials: the upper half of
+// the workgroup first, so that the waves polling right after phase C (the
+// leaders' reduction on the lower waves, wave 0's logits) have no stores of
+// their own in flight (vmcnt counts stores too, so a load's wait would include
+// them).
+__device__ __forceinline__ int item_thread() { return (threadIdx.x + kThreads / 2) % kThreads; }
+
+// Publish this workgroup's router partials for layer tag `tag`: item it of
+// chunk owner b at part[(it * nprod + b) * 2 ...], so that a leader reads the
+// owners of one item from consecutive words.
 template <int PPT>
-__device__ inline void store_partials(const Params& p, const long long* acc, uint32_t tag) {
+__device__ inline void store_partials(const Params& p, const long long* acc, int nprod, uint32_t tag) {
     const int items = p.rows * p.E;
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
-        const int it = threadIdx.x + j * kThreads;
+        const int it = item_thread() + j * kThreads;
         if (it < items) {
-            u64* dst = p.part + ((size_t)blockIdx.x * items + it) * 2;
+            u64* dst = p.part + ((size_t)it * nprod + blockIdx.x) * 2;
             st64(dst, tagged(tag, (uint32_t)(unsigned long long)acc[j]));
             st64(dst + 1, tagged(tag, (uint32_t)((unsigned long long)acc[j] >> 32)));
         }
@@ -242,17 +259,20 @@ __device__ inline void leader_pass(const Params& p, int i0, int items, int e0, i
     const bool in = it < items;
     const int t = in ? it / ne : 0, e = in ? e0 + it % ne : 0;
     const size_t idx = (size_t)t * p.E + e;
-    const size_t stride = (size_t)p.rows * p.E * 2;
     long long s = 0;
 #pragma unroll 1
     for (int b0 = li; b0 < nprod; b0 += 8 * LPI) {
         u64 w[16];
         auto addr = [&](int j) -> const u64* {
             const int b = b0 + (j >> 1) * LPI;
-            return (in && b < nprod) ? p.part + b * stride + idx * 2 + (j & 1) : nullptr;
+            return (in && b < nprod) ? p.part + (idx * nprod + b) * 2 + (j & 1) : nullptr;
         };
         issue_tagged(w, addr, tag);
-        wait_tagged(w, addr, tag, p);
+        const unsigned polls = wait_tagged(w, addr, tag, p);
+        if (p.trace && threadIdx.x == 0 && b0 == 0) {
+            mark(p, p.trace_layer, 19);
+            trace_put(p, p.trace_layer, 20, polls);
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j)
             s += (long long)(((u64)(uint32_t)w[2 * j + 1] << 32) | (uint32_t)w[2 * j]);
@@ -284,7 +304,7 @@ __device__ __forceinline__ void router_chunk_accumulate(const Params& p, const F
                                                         long long* acc) {
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
-        const int it = threadIdx.x + j * kThreads;
+        const int it = item_thread() + j * kThreads;
         if (it < p.rows * p.E) {
             const int t = it / p.E, e = it % p.E;
             acc[j] += naiwa_router_chunk<AS>(W8(e), xv[t]);
@@ -400,12 +420,13 @@ __device__ inline void poll_one_row(const Params& p, Smem& sm, const LayerDev& L
 }
 
 // One token, every wave: the number of keys above each key that lie in this
-// wave's quarter of the experts (its slice, at most 64 keys, one per lane),
-// broadcast one key at a time from the lane holding it.  KPL: keys per lane.
+// wave's slice of the experts (one slice per wave, at most 64 keys, one per
+// lane), broadcast one key at a time from the lane holding it.  KPL: keys per lane.
 template <int KPL>
 __device__ inline void rank_slice(const Params& p, Smem& sm, int wave, int lane) {
+    constexpr int NW = kThreads / 64;
     const int E = p.E;
-    const int per = (E + 3) / 4, s0 = wave * per, ns = max(0, min(E, s0 + per) - s0);
+    const int per = (E + NW - 1) / NW, s0 = wave * per, ns = max(0, min(E, s0 + per) - s0);
     const u64 ks = lane < ns ? sm.key[0][s0 + lane] : 0ull;
     u64 mine[KPL];
     int cnt[KPL];
@@ -424,12 +445,81 @@ __device__ inline void rank_slice(const Params& p, Smem& sm, int wave, int lane)
         if (lane + 64 * j < E) sm.rcnt[wave][lane + 64 * j] = cnt[j];
 }
 
-// One token, wave 0, after the ranks: lane j < k takes the rank-j expert; the
-// weights (denominators summed in rank order, or in expert order over all E
-// for the softmax-without-renormalisation mode, as the oracle sums them),
-// then slots and the grouping of valid pairs.
-__device__ inline void weigh_one_row(const Params& p, Smem& sm, const LayerDev& L, int l, int lane) {
+// One token, wave 0: the grouping of its k pairs (lane q = pair q, inp: q < k)
+// by slot, all in registers: each pair's position in (slot, q) order and its
+// predecessor's slot come from the other lanes' keys, one readlane each.
+__device__ inline void group_pairs_one(const Params& p, Smem& sm, const LayerDev& L, int l, int lane, bool inp,
+                                       uint32_t e, float w) {
+    const int k = p.k;
+    const int q = lane;
+    const int32_t s = inp ? (L.slot_of ? sm.slot_tab[e] : (int32_t)e) : -1;
+    const bool ok = inp && s >= 0 && s < L.slots;
+    if (inp && !ok && blockIdx.x == 0) atomicAdd(&p.status[1], 1);
+    if (inp && blockIdx.x == 0 && p.ids_out) {
+        p.ids_out[(size_t)l * k + q] = e;
+        p.w_out[(size_t)l * k + q] = w;
+    }
+    const bool valid = ok && w != 0.0f;
+    const uint32_t key = valid ? (((uint32_t)s << 6) | (uint32_t)q) : 0xFFFFFFFFu; // invalid pairs sort last
+    int rank = 0;
+    long long pk = -1; // the largest key below this one
+#pragma unroll
+    for (int o = 0; o < kMaxK; ++o) {
+        const uint32_t ko = (uint32_t)__builtin_amdgcn_readlane((int)key, o);
+        if (o < k && ko < key) {
+            ++rank;
+            pk = max(pk, (long long)ko);
+        }
+    }
+    const bool start = valid && (rank == 0 || (uint32_t)(pk >> 6) != (uint32_t)s);
+    // segment index: the starts that sort before this one
+    const uint32_t sk = start ? key : 0xFFFFFFFFu;
+    int si = 0;
+#pragma unroll
+    for (int o = 0; o < kMaxK; ++o) si += o < k && (uint32_t)__builtin_amdgcn_readlane((int)sk, o) < key;
+    const int nvalid = __popcll(__ballot(valid));
+    const int nseg = __popcll(__ballot(start));
+    sm.pair_slot[q] = valid ? (uint32_t)s : 0u;
+    sm.pair_w[q] = valid ? w : 0.0f;
+    if (valid) {
+        sm.sorted[rank] = (uint32_t)q;
+        sm.srt_slot[rank] = (uint32_t)s;
+        sm.srt_tok[rank] = 0u;
+    }
+    if (start) {
+        sm.seg_begin[si] = (uint32_t)rank;
+        sm.seg_slot[si] = (uint32_t)s;
+    }
+    if (lane == 0) {
+        sm.seg_begin[nseg] = (uint32_t)nvalid;
+        sm.nseg = nseg;
+    }
+}
+
+// One token, wave 0, after every wave's key-slice counts: the rank of each
+// expert (lane l: experts l + 64 j), the top k through LDS (lane j takes the
+// rank-j expert), the weights (denominators summed in rank order, or in expert
+// order over all E for the softmax-without-renormalisation mode, as the oracle
+// sums them), then the grouping of the pairs.
+template <int KPL>
+__device__ inline void route_one_row(const Params& p, Smem& sm, const LayerDev& L, int l, int lane) {
     const int E = p.E, k = p.k;
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E) {
+            int r = 0;
+#pragma unroll
+            for (int w = 0; w < kThreads / 64; ++w) r += sm.rcnt[w][e];
+            if (r < k) {
+                sm.top_ids[0][r] = (uint32_t)e;
+                sm.top_ex[0][r] = sm.lg[0][e];
+            }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const bool inp = lane < k;
     const uint32_t my_e = inp ? sm.top_ids[0][lane] : 0u;
     const float my_f = inp ? sm.top_ex[0][lane] : 0.0f;
@@ -437,18 +527,19 @@ __device__ inline void weigh_one_row(const Params& p, Smem& sm, const LayerDev& 
     const float ex = inp ? expf(my_f - mx) : 0.0f;
     float denom = 0.0f;
     if (p.mode == NAIWA_ROUTE_SOFTMAX_TOPK) {
-        constexpr int KPL = kMaxE / 64;
-        float ea[KPL];
+        constexpr int KA = kMaxE / 64;
+        float ea[KA];
 #pragma unroll
-        for (int j = 0; j < KPL; ++j) ea[j] = lane + 64 * j < E ? expf(sm.lg[0][lane + 64 * j] - mx) : 0.0f;
+        for (int j = 0; j < KA; ++j) ea[j] = lane + 64 * j < E ? expf(sm.lg[0][lane + 64 * j] - mx) : 0.0f;
 #pragma unroll
-        for (int j = 0; j < KPL; ++j)
+        for (int j = 0; j < KA; ++j)
             for (int ln = 0; ln < 64 && 64 * j + ln < E; ++ln) denom += readlane_f32(ea[j], ln);
     } else {
-        for (int o = 0; o < k; ++o) denom += readlane_f32(ex, o);
+#pragma unroll
+        for (int o = 0; o < kMaxK; ++o) denom += o < k ? readlane_f32(ex, o) : 0.0f;
     }
     mark_wave(p, l, 11);
-    group_pairs(p, sm, L, l, lane, inp, 0, my_e, inp ? ex / denom : 0.0f);
+    group_pairs_one(p, sm, L, l, lane, inp, my_e, inp ? ex / denom : 0.0f);
     mark_wave(p, l, 12);
 }
 
@@ -481,16 +572,18 @@ __device__ __forceinline__ float q4k_chunk(const Q4Scales& s, int c, float alo, 
     return s.d * (sc0 * (alo - 128.0f * slo) + sc1 * (ahi - 128.0f * shi)) - s.dmin * (m0 * slo + m1 * shi);
 }
 
-// Dots of two Q4_K blocks (rows A and B, 9 x 16 bytes each in LDS) with the
-// same 256 staged activations: words = the block's 128 bf16 pair words, sums =
-// its 16 sums of 16.  Each activation word is loaded once and feeds both rows.
+// Dots of chunks c0 and c0 + 1 (64 values each) of two Q4_K blocks (rows A and
+// B, 9 x 16 bytes each in LDS) with the same staged activations: words = the
+// block's 128 bf16 pair words, sums = its 16 sums of 16.  Each activation word
+// is loaded once and feeds both rows.
 __device__ __forceinline__ void q4k_block_dot2(const uint8_t* A8, const uint8_t* B8, const uint32_t* words,
-                                               const float* sums, float& ra, float& rb) {
+                                               const float* sums, int c0, float& ra, float& rb) {
     auto A = [&](int j) { return naiwa_ld<uint4, NAIWA_AS_LDS>(A8 + 16 * j); };
     auto B = [&](int j) { return naiwa_ld<uint4, NAIWA_AS_LDS>(B8 + 16 * j); };
     const Q4Scales sa = q4k_scales(A(0)), sb = q4k_scales(B(0));
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int cc = 0; cc < 2; ++cc) {
+        const int c = c0 + cc;
         // the chunk's 32 activation words, all loads in flight before the first use
         uint4 x[8];
 #pragma unroll
@@ -527,31 +620,36 @@ __device__ __forceinline__ void q4k_block_dot2(const uint8_t* A8, const uint8_t*
 
 // h of every token of the segment for intermediate rows r, r + 1 (pair q),
 // with the item's rows in LDS: [gate row r][gate row r + 1][up row r][up row r + 1]
-// (rb bytes each).  Lane lr takes block lr % 8 of the gate rows (lanes 0-7) or
-// of the up rows (lanes 8-15), both rows at once; rows of at most 8 blocks
-// (H <= 2048).  The two results go out as one tagged word in the down
-// projection's 16-bit format DD.
+// (rb bytes each), on 32 lanes: lane il = 16 u + 8 h + b takes chunks 2h, 2h + 1
+// of block b of the gate rows (u = 0) or of the up rows (u = 1), both rows at
+// once; rows of at most 8 blocks (H <= 2048).  The two results go out as one
+// tagged word in the down projection's 16-bit format DD.
 template <int DD>
 __device__ inline void q4_pair_compute(const Params& p, const Smem& sm, const uint8_t* dyn, int xstage, int q,
-                                       int nb, int lr, const uint8_t* item, int64_t rb, uint32_t tag) {
+                                       int nb, int il, const uint8_t* item, int64_t rb, uint32_t tag) {
     const int I2 = p.I / 2, H = p.H, k = p.k;
     const int s = q / I2, r = 2 * (q % I2);
     const int b = (int)sm.seg_begin[s], e = (int)sm.seg_begin[s + 1];
-    const int b0 = lr & 7;
-    const uint8_t* A = item + (lr >= 8 ? 2 * rb : 0) + b0 * NAIWA_Q4_K_BYTES;
+    const int b0 = il & 7, c0 = (il >> 2) & 2;
+    const uint8_t* A = item + (il >= 16 ? 2 * rb : 0) + b0 * NAIWA_Q4_K_BYTES;
     for (int tt = b; tt < e; ++tt) {
         const int t = (int)sm.sorted[tt] / k;
         const uint32_t* words = (const uint32_t*)(dyn + t * xstage);   // 132 words per block (padded)
         const float* sums = (const float*)(words + H / 2 + 4 * nb);
         float g0 = 0.0f, g1 = 0.0f;   // this lane's share of row r and row r + 1
-        if (b0 < nb) q4k_block_dot2(A, A + rb, words + b0 * 132, sums + b0 * 16, g0, g1);
-        // lanes 0-7: gate . x, lanes 8-15: up . x; row_ror:8 brings lane 8 to lane 0
-        g0 = naiwa_group_sum<8>(g0);
-        g1 = naiwa_group_sum<8>(g1);
-        const float h0 = naiwa_act(p.act, g0) * naiwa_dpp<0x128>(g0);
-        const float h1 = naiwa_act(p.act, g1) * naiwa_dpp<0x128>(g1);
-        if (lr == 0)
-            st64(&p.h[(size_t)sm.sorted[tt] * I2 + r / 2],
+        if (b0 < nb) q4k_block_dot2(A, A + rb, words + b0 * 132, sums + b0 * 16, c0, g0, g1);
+        // lanes 0-15: gate . x, lanes 16-31: up . x (one DPP row each); then the
+        // up row takes the gate sums from the last lane of the gate row
+        g0 = naiwa_group_sum<16>(g0);
+        g1 = naiwa_group_sum<16>(g1);
+        const float ga = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                                       0, __builtin_bit_cast(int, g0), 0x142, 0xA, 0xF, false));
+        const float gb = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                                       0, __builtin_bit_cast(int, g1), 0x142, 0xA, 0xF, false));
+        const float h0 = naiwa_act(p.act, ga) * g0;
+        const float h1 = naiwa_act(p.act, gb) * g1;
+        if (il == 16)
+            st64(&p.h[(size_t)tt * I2 + r / 2],
                  tagged(tag, Fmt<DD>::to16(h0) | (Fmt<DD>::to16(h1) << 16)));
     }
 }
@@ -601,7 +699,7 @@ __device__ inline void unit_pair(const Params& p, const Smem& sm, const LayerDev
             hv[rr] = naiwa_act(p.act, gv) * uv;
         }
         if (lr == 0)
-            st64(&p.h[(size_t)sm.sorted[tt] * I2 + r / 2],
+            st64(&p.h[(size_t)tt * I2 + r / 2],
                  tagged(tag, Fmt<DD>::to16(hv[0]) | (Fmt<DD>::to16(hv[1]) << 16)));
     }
 }
@@ -634,39 +732,41 @@ __host__ __device__ inline int fused_xstage(int dt, int h) {
     return naiwa_stage_bytes(dt, h) + (dt == NAIWA_Q4_K ? 16 * (h / NAIWA_QK_K) : 0);
 }
 
-// Poll the tagged h vectors of sorted pairs [v0, v0 + nv) (I/2 words each,
-// two 16-bit values of format DD per word) and stage them at dst.
+// Poll the tagged h vectors of sorted positions [v0, v0 + nv) (I/2 words each,
+// two 16-bit values of format DD per word; vector v at h + v * I/2) and stage
+// them: words at hw[v * I/2 ...] in the dot layout of DD, sums of kSumSpan
+// values at hs[v * I/kSumSpan ...].
 template <int DD>
-__device__ inline void stage_h(const Params& p, const Smem& sm, int v0, int nv, uint8_t* dst, int stride,
-                               uint32_t tag) {
+__device__ inline void stage_h(const Params& p, int v0, int nv, uint32_t* hw, float* hs, uint32_t tag) {
     constexpr int gpg = Fmt<DD>::kSumSpan / 4;
-    const int I = p.I, I2 = I / 2, gpv = I / 4, total = nv * gpv;
+    const int gpv = p.I / 4, total = nv * gpv;
+    const u64* src = p.h + (size_t)v0 * (p.I / 2);
     for (int g0 = 0; g0 < total; g0 += kHG * kThreads) {
         u64 w[2 * kHG];
         auto addr = [&](int j) -> const u64* {
             const int g = g0 + threadIdx.x + (j >> 1) * kThreads;
-            if (g >= total) return nullptr;
-            const int v = g / gpv, gg = g % gpv;
-            return p.h + (size_t)sm.sorted[v0 + v] * I2 + 2 * gg + (j & 1);
+            return g < total ? src + 2 * g + (j & 1) : nullptr;
         };
         issue_tagged(w, addr, tag);
-        wait_tagged(w, addr, tag, p);
+        const unsigned polls = wait_tagged(w, addr, tag, p);
+        if (p.trace && threadIdx.x == 0) {
+            mark(p, p.trace_layer, 17);
+            trace_put(p, p.trace_layer, 18, polls);
+        }
 #pragma unroll
         for (int j = 0; j < kHG; ++j) {
             const int g = g0 + threadIdx.x + j * kThreads;
             const bool in = g < total;
-            const int v = in ? g / gpv : 0, gg = in ? g % gpv : 0;
             const uint32_t A = (uint32_t)w[2 * j], B = (uint32_t)w[2 * j + 1]; // (h0, h1), (h2, h3)
             float part = 0.0f;
             if (in) {
-                uint32_t* words = (uint32_t*)(dst + v * stride);
-                words[2 * gg] = (A & 0xffffu) | (B << 16);
-                words[2 * gg + 1] = (A >> 16) | (B & 0xffff0000u);
+                hw[2 * g] = (A & 0xffffu) | (B << 16);
+                hw[2 * g + 1] = (A >> 16) | (B & 0xffff0000u);
                 part = (Fmt<DD>::from16(A & 0xffffu) + Fmt<DD>::from16(A >> 16)) +
                        (Fmt<DD>::from16(B & 0xffffu) + Fmt<DD>::from16(B >> 16));
             }
             part = naiwa_group_sum<gpg>(part);
-            if (in && (gg % gpg) == 0) ((float*)((uint32_t*)(dst + v * stride) + I / 2))[gg / gpg] = part;
+            if (in && (g % gpg) == 0) hs[g / gpg] = part;
         }
     }
 }
@@ -686,7 +786,7 @@ template <int DG, int DD, int MR>
 __global__ void __launch_bounds__(kThreads)
 stack_kernel(Params p) {
     constexpr int PPT = (MR * kMaxE + kThreads - 1) / kThreads; // router items per thread
-    constexpr int XG = MR == 1 ? 4 : kXG;                       // activation groups per thread per round
+    constexpr int XG = MR == 1 ? 2 : kXG;                       // activation groups per thread per round
     extern __shared__ __align__(16) uint8_t dyn[];
     __shared__ Smem sm;
     __shared__ LayerDev layers_lds[kMaxLayers];
@@ -709,10 +809,14 @@ stack_kernel(Params p) {
     const int half_h = H / 2;                 // tagged words per token
     const int nlog = rows * E;
     uint8_t* const hdyn = dyn + rows * xstage;      // h staging, after the activations
+    uint32_t* const hw = (uint32_t*)hdyn;           // [hpairs][I/2] words
+    float* const hs = (float*)(hdyn + (size_t)p.hpairs * I * 2); // [hpairs][I / kSumSpan] sums
     uint8_t* const dbuf = hdyn + p.hpairs * hstage; // prefetched down rows: [pair][kChunk][drb]
-    uint8_t* const wb = dbuf + (size_t)p.dpre * kChunk * drb; // gate/up rounds
+    float* const rbuf = (float*)(dbuf + (size_t)p.dpre * kChunk * drb); // next router columns [E][kChunk]
+    uint8_t* const wb = (uint8_t*)(rbuf + (size_t)E * kChunk);           // gate/up rounds
 
     // ---- prologue: layer descriptors into LDS; own chunks of x; layer-0 logits ----
+    p.trace_layer = p.n_layers; // the prologue's row of the trace
     mark(p, p.n_layers, 0);
     for (int i = tid; i < p.n_layers * (int)(sizeof(LayerDev) / 8); i += kThreads)
         reinterpret_cast<unsigned long long*>(layers_lds)[i] =
@@ -740,7 +844,7 @@ stack_kernel(Params p) {
                 const int f0 = chunk_at(cp, nchunks) * kChunk;
                 router_chunk_accumulate<PPT, NAIWA_AS_GLOBAL>(p, [&](int e) { return W + (size_t)e * H + f0; }, sm.xown[ci], acc);
             }
-            store_partials<PPT>(p, acc, tag0);
+            store_partials<PPT>(p, acc, nprod, tag0);
         }
         mark(p, p.n_layers, 1);
         if (bid < nlead) leader_reduce(p, nprod, tag0);
@@ -749,6 +853,7 @@ stack_kernel(Params p) {
 
     for (int l = 0; l < p.n_layers; ++l) {
         p.h = opaque(p.h);
+        p.trace_layer = l;
         p.part = opaque(p.part);
         p.logits = opaque(p.logits);
         p.xt = opaque(p.xt);
@@ -795,16 +900,13 @@ stack_kernel(Params p) {
             else
                 rank_slice<kMaxE / 64>(p, sm, wave, lane);
             __syncthreads();
-            if (tid < E) {
-                const int r = sm.rcnt[0][tid] + sm.rcnt[1][tid] + sm.rcnt[2][tid] + sm.rcnt[3][tid];
-                if (r < k) {
-                    sm.top_ids[0][r] = (uint32_t)tid;
-                    sm.top_ex[0][r] = sm.lg[0][tid];
-                }
-            }
-            __syncthreads();
             mark(p, l, 1);
-            if (wave == 0) weigh_one_row(p, sm, L, l, lane);
+            if (wave == 0) {
+                if (E <= 128)
+                    route_one_row<2>(p, sm, L, l, lane);
+                else
+                    route_one_row<kMaxE / 64>(p, sm, L, l, lane);
+            }
         } else {
             for (int g0 = 0; g0 < ngroups; g0 += XG * kThreads) {
                 u64 xw[2 * XG];
@@ -918,7 +1020,9 @@ stack_kernel(Params p) {
         // down rows of the first chunk for the first pairs: they depend on the
         // routing only, so they are on their way during gate/up and the h wait
         const int npre = owner ? min(p.dpre, nvalid) : 0;
+        // (and the next layer's router columns of the first chunk, for its partials)
         auto prefetch_down = [&]() {
+            if (!owner) return;
             const int f0 = chunk_at(bid, nchunks) * kChunk;
             const int span = kChunk * (int)drb / 16; // 16-byte pieces of kChunk consecutive rows
             for (int v = wave; v < npre; v += kThreads / 64) {
@@ -927,16 +1031,27 @@ stack_kernel(Params p) {
                 for (int c = 0; c * 64 < span; ++c)
                     if (c * 64 + lane < span) lds_dma16(src + (c * 64 + lane) * 16, dst + c * 1024);
             }
+            if (!last) {
+                // expert e's 8 columns (two 16-byte pieces) land at rbuf[e * kChunk]
+                const float* Wn = layers_lds[l + 1].router;
+                const int rpieces = 2 * E;
+                for (int c = wave; c * 64 < rpieces; c += kThreads / 64) {
+                    const int pc = c * 64 + lane;
+                    if (pc < rpieces) lds_dma16(Wn + (size_t)(pc >> 1) * H + f0 + 4 * (pc & 1), rbuf + c * 256);
+                }
+            }
         };
         if constexpr (DG == NAIWA_Q4_K) {
             // rounds of up to p.bitems items: the gate and up row pairs of each item
-            // are gathered into LDS with coalesced 16-byte DMA pieces (wave w takes
-            // items w, w + 4, ...), then group g computes item g of the round
+            // are gathered into LDS with coalesced 16-byte DMA pieces by the wave
+            // that computes it (items w and w + 8 of a round go to wave w, on its
+            // two 32-lane halves), so each wave waits for its own pieces only
             const int pair_pieces = (int)(rb / 8);       // two rows, 16-byte pieces
             const size_t item_bytes = 4 * (size_t)rb;
+            const int half = (tid >> 5) & 1, il = tid & 31;
+            const int my_item = wave + 8 * half;
             for (int r0 = q0; r0 < q1; r0 += p.bitems) {
                 const int nr = min(p.bitems, q1 - r0);
-                if (r0 > q0) __syncthreads(); // the previous round's items are consumed
                 for (int i = wave; i < nr; i += kThreads / 64) {
                     const int q = r0 + i;
                     const uint32_t slot = sm.seg_slot[q / I2];
@@ -952,13 +1067,14 @@ stack_kernel(Params p) {
                     }
                 }
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                __syncthreads();
                 if (r0 == q0) {
                     mark(p, l, 3);
                     prefetch_down();
                 }
-                if (grp < nr) q4_pair_compute<DD>(p, sm, dyn, xstage, r0 + grp, nb, lr, wb + grp * item_bytes, rb, tag);
+                if (my_item < nr)
+                    q4_pair_compute<DD>(p, sm, dyn, xstage, r0 + my_item, nb, il, wb + my_item * item_bytes, rb, tag);
             }
+            mark_wave(p, l, 16); // every wave: the last one to store wins
             if (q0 >= q1) {
                 mark(p, l, 3);
                 prefetch_down();
@@ -969,6 +1085,10 @@ stack_kernel(Params p) {
 #pragma unroll 1
             for (int q = q0 + grp; q < q1; q += kGroups) unit_pair<DG, DD>(p, sm, L, dyn, q, xstage, rb, nu, lr, tag);
         }
+        // every h word of this workgroup is stored: say so with one tagged word
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0 && q0 < q1) st64(&p.done[bid], tagged(tag, 0u));
         mark(p, l, 4);
 
         // ---- C: down + ordered combine + residual + next layer's router partials ----
@@ -977,13 +1097,29 @@ stack_kernel(Params p) {
 #pragma unroll
             for (int j = 0; j < PPT; ++j) racc[j] = 0;
             u64* xt_next = p.xt + (size_t)((l + 1) & 1) * rows * half_h;
+            // before reading all of h, wait (cheaply) for the done word of every
+            // workgroup with gate/up items.  The full read below still checks every
+            // word's tag; this only keeps the polling traffic small while the last
+            // producers are still computing.
+            {
+                const int nprod_h = (total + per - 1) / per;
+                for (int b2 = tid; b2 < nprod_h; b2 += kThreads) {
+                    u64 v[1];
+                    auto addr = [&](int) -> const u64* { return p.done + b2; };
+                    issue_tagged(v, addr, tag);
+                    wait_tagged(v, addr, tag, p);
+                }
+                __syncthreads();
+                mark(p, l, 14);
+            }
             for (int cp = bid, ci = 0; cp < nchunks; cp += G, ++ci) {
                 const int c = chunk_at(cp, nchunks);
                 const int f0 = c * kChunk;
                 for (int b0 = 0; b0 < nvalid; b0 += p.hpairs) {
                     const int nbp = min(p.hpairs, nvalid - b0);
                     if (ci > 0 || b0 > 0) __syncthreads(); // the previous pass's dots read hdyn
-                    stage_h<DD>(p, sm, b0, nbp, hdyn, hstage, tag);
+                    stage_h<DD>(p, b0, nbp, hw, hs, tag);
+                    mark(p, l, 15);
                     // the prefetched rows have landed (vmcnt also counts LDS DMA)
                     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                     __syncthreads();
@@ -1020,12 +1156,12 @@ stack_kernel(Params p) {
 #pragma unroll
                                 for (int j = 0; j < kCB; ++j) {
                                     const int it = min(it0 + j * kGroups, nit - 1);
-                                    const uint32_t* words = (const uint32_t*)(hdyn + (it / kChunk) * hstage);
+                                    const uint32_t* words = hw + (size_t)(it / kChunk) * (I / 2);
+                                    const float* sums = hs + (size_t)(it / kChunk) * (I / Fmt<DD>::kSumSpan);
 #pragma unroll
                                     for (int i = 0; i < DUM; ++i) {
                                         const int u = base + NAIWA_GROUP * i;
-                                        if (u < dnu)
-                                            acc[j] += Fmt<DD>::dot(frg[j][i], u, words, (const float*)(words + I / 2));
+                                        if (u < dnu) acc[j] += Fmt<DD>::dot(frg[j][i], u, words, sums);
                                     }
                                 }
                             }
@@ -1044,6 +1180,8 @@ stack_kernel(Params p) {
                     else
                         dots(std::integral_constant<int, NAIWA_AS_GLOBAL>());
                 }
+                // prefetched pieces have landed even when no pass ran (no valid pair)
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 __syncthreads();
                 mark(p, l, 6);
                 if (tid < rows * kChunk) {
@@ -1066,8 +1204,10 @@ stack_kernel(Params p) {
                     sm.xown[ci][t][fi] = naiwa_bf16_to_f32(naiwa_f32_to_bf16(sm.xown[ci][t][fi] + y));
                 }
                 __syncthreads();
-                if (tid < rows * kChunk / 2) {
-                    const int t = tid / (kChunk / 2), pi = tid % (kChunk / 2);
+                // the chunk's x words go out from the last wave (see item_thread)
+                const int xs = tid - (kThreads - 64);
+                if (xs >= 0 && xs < rows * kChunk / 2) {
+                    const int t = xs / (kChunk / 2), pi = xs % (kChunk / 2);
                     const uint32_t pr = naiwa_f32_to_bf16(sm.xown[ci][t][2 * pi]) |
                                         (naiwa_f32_to_bf16(sm.xown[ci][t][2 * pi + 1]) << 16);
                     if (last)
@@ -1076,13 +1216,17 @@ stack_kernel(Params p) {
                         st64(&xt_next[(size_t)t * half_h + c * (kChunk / 2) + pi], tagged(tag_next, pr));
                 }
                 mark(p, l, 7);
-                if (!last) {
+                if (!last && ci == 0) {
+                    // the first chunk's columns were prefetched into LDS
+                    router_chunk_accumulate<PPT, NAIWA_AS_LDS>(p, [&](int e) { return rbuf + e * kChunk; },
+                                                              sm.xown[ci], racc);
+                } else if (!last) {
                     const float* Wn = layers_lds[l + 1].router;
                     router_chunk_accumulate<PPT, NAIWA_AS_GLOBAL>(p, [&](int e) { return Wn + (size_t)e * H + f0; },
                                                              sm.xown[ci], racc);
                 }
             }
-            if (!last) store_partials<PPT>(p, racc, tag_next);
+            if (!last) store_partials<PPT>(p, racc, nprod, tag_next);
         }
         mark(p, l, 8);
         if (!last && bid < nlead) leader_reduce(p, nprod, tag_next);
@@ -1173,7 +1317,7 @@ extern "C" int naiwa_stack_trace_enable(int on) {
     return NAIWA_OK;
 }
 
-// Copies the last traced launch's timestamps: [blocks][n_layers + 1][16] u64
+// Copies the last traced launch's timestamps: [blocks][n_layers + 1][24] u64
 // ticks (the extra layer row is the prologue).  Synchronizes the device.
 extern "C" int naiwa_stack_trace_read(uint64_t* out, int capacity, int* n_layers, int* blocks) {
     int rc = 0;
@@ -1255,6 +1399,8 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     const size_t lds_h = (size_t)hpairs * naiwa_stage_bytes(fd, I);
     size_t lds = lds_x + lds_h;
     if (lds > kMaxDynLds) return NAIWA_E_UNSUPPORTED;
+    lds += (size_t)E * kChunk * 4; // the next layer's router columns of the first chunk
+    if (lds > kMaxDynLds) return NAIWA_E_UNSUPPORTED;
     // Q4_K down rows of the first phase-C pass, prefetched into LDS when they fit
     // beside at least one gate/up item
     int dpre = 0;
@@ -1272,7 +1418,7 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     if (fg == NAIWA_Q4_K) {
         const size_t item = 4 * (size_t)naiwa_row_bytes(NAIWA_Q4_K, H);
         const int share = (rows * k * (I / 2) + 255) / 256;
-        bitems = (int)std::min<size_t>((size_t)std::min(kGroups, share), (kMaxDynLds - lds) / item);
+        bitems = (int)std::min<size_t>((size_t)std::min(kThreads / 32, share), (kMaxDynLds - lds) / item);
         if (bitems < 1) return NAIWA_E_UNSUPPORTED;
         lds += (size_t)bitems * item;
     }
@@ -1296,13 +1442,15 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     const int nprod = blocks < nchunks ? blocks : nchunks;
     if (dev < 0 || dev >= kMaxDev) return NAIWA_E_UNSUPPORTED;
 
-    // tagged scratch: h [kMaxPairs][I] | partials [nprod][rows*E][2] | logits [rows*E] | x [2][rows][H/2]
+    // tagged scratch: h [kMaxPairs][I] | partials [rows*E][nprod][2] | logits [rows*E] | x [2][rows][H/2] |
+    // done [blocks]
     auto a256 = [](size_t b) { return (b + 255) & ~size_t(255); };
     const size_t h_bytes = a256((size_t)kMaxPairs * I * 8);
     const size_t part_bytes = a256((size_t)nprod * rows * E * 16);
     const size_t lg_bytes = a256((size_t)rows * E * 8);
     const size_t xt_bytes = a256((size_t)2 * rows * (H / 2) * 8);
-    const size_t tag_bytes = h_bytes + part_bytes + lg_bytes + xt_bytes;
+    const size_t done_bytes = a256((size_t)blocks * 8);
+    const size_t tag_bytes = h_bytes + part_bytes + lg_bytes + xt_bytes + done_bytes;
     bool fresh = false;
     uint8_t* ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK, tag_bytes, &rc, &fresh);
     if (!ws) return rc;
@@ -1356,7 +1504,7 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
         dev_layers = g_fused.dev_layers;
     }
 
-    Params prm;
+    Params prm{};
     prm.layers = dev_layers;
     prm.n_layers = n_layers;
     prm.rows = rows;
@@ -1371,6 +1519,7 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     prm.part = (u64*)(ws + h_bytes);
     prm.logits = (u64*)(ws + h_bytes + part_bytes);
     prm.xt = (u64*)(ws + h_bytes + part_bytes + lg_bytes);
+    prm.done = (u64*)(ws + h_bytes + part_bytes + lg_bytes + xt_bytes);
     prm.status = (int*)(sync + kStatusOff);
     prm.ids_out = ids_out;
     prm.w_out = w_out;
