@@ -163,16 +163,32 @@ __device__ __forceinline__ float naiwa_act(int act, float g) {
 // (d, dmin, scales).  The unit covers elements 64c + 16h + [0,16) with
 // sub-block 2c and the same +32 with sub-block 2c+1 (c = j/2, h = j%2).
 // xlo/xhi are the 8 perm words of those two 16-element runs, slo/shi their sums.
+// Two Q4_K nibbles (bits 0-3 and 16-19 of q) as the bf16 pair (128 + n0, 128 + n1):
+// (q & 0x000F000F) | 0x43004300 in one v_and_or_b32, with the mask held in a
+// VGPR and the exponent bits in an SGPR (a gfx9 VOP3 takes no literal and reads
+// at most one SGPR; with both as literals it takes two instructions).
+struct NaiwaNib {
+    uint32_t mask, magic;
+};
+__device__ __forceinline__ NaiwaNib naiwa_nib_consts() {
+    uint32_t m = 0x000F000Fu, g = 0x43004300u;
+    asm volatile("" : "+v"(m));
+    asm volatile("" : "+s"(g));
+    return {m, g};
+}
+__device__ __forceinline__ uint32_t naiwa_nib(uint32_t q, const NaiwaNib& c) { return (q & c.mask) | c.magic; }
+
 __device__ __forceinline__ float naiwa_q4k_unit(uint4 q, uint4 hd, int c, const uint32_t* xlo,
                                                 const uint32_t* xhi, float slo, float shi) {
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    const NaiwaNib nc = naiwa_nib_consts();
     float alo = 0.0f, ahi = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t a0 = (w[i] & 0x000F000Fu) | 0x43004300u;
-        const uint32_t a1 = ((w[i] >> 8) & 0x000F000Fu) | 0x43004300u;
-        const uint32_t b0 = ((w[i] >> 4) & 0x000F000Fu) | 0x43004300u;
-        const uint32_t b1 = ((w[i] >> 12) & 0x000F000Fu) | 0x43004300u;
+        const uint32_t a0 = naiwa_nib(w[i], nc);
+        const uint32_t a1 = naiwa_nib(w[i] >> 8, nc);
+        const uint32_t b0 = naiwa_nib(w[i] >> 4, nc);
+        const uint32_t b1 = naiwa_nib(w[i] >> 12, nc);
         alo = naiwa_dot2_bf16(a0, xlo[2 * i], alo);
         alo = naiwa_dot2_bf16(a1, xlo[2 * i + 1], alo);
         ahi = naiwa_dot2_bf16(b0, xhi[2 * i], ahi);

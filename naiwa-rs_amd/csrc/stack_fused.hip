@@ -593,6 +593,7 @@ __device__ __forceinline__ void q4k_block_dot2(const uint8_t* A8, const uint8_t*
         const uint32_t wa[8] = {qa0.x, qa0.y, qa0.z, qa0.w, qa1.x, qa1.y, qa1.z, qa1.w};
         const uint32_t wb[8] = {qb0.x, qb0.y, qb0.z, qb0.w, qb1.x, qb1.y, qb1.z, qb1.w};
         float alo = 0.0f, ahi = 0.0f, blo = 0.0f, bhi = 0.0f;
+        const NaiwaNib nc = naiwa_nib_consts();
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t xl[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
@@ -600,14 +601,14 @@ __device__ __forceinline__ void q4k_block_dot2(const uint8_t* A8, const uint8_t*
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const uint32_t qa = wa[2 * i + h], qb = wb[2 * i + h];
-                alo = naiwa_dot2_bf16((qa & 0x000F000Fu) | 0x43004300u, xl[2 * h], alo);
-                blo = naiwa_dot2_bf16((qb & 0x000F000Fu) | 0x43004300u, xl[2 * h], blo);
-                alo = naiwa_dot2_bf16(((qa >> 8) & 0x000F000Fu) | 0x43004300u, xl[2 * h + 1], alo);
-                blo = naiwa_dot2_bf16(((qb >> 8) & 0x000F000Fu) | 0x43004300u, xl[2 * h + 1], blo);
-                ahi = naiwa_dot2_bf16(((qa >> 4) & 0x000F000Fu) | 0x43004300u, xh[2 * h], ahi);
-                bhi = naiwa_dot2_bf16(((qb >> 4) & 0x000F000Fu) | 0x43004300u, xh[2 * h], bhi);
-                ahi = naiwa_dot2_bf16(((qa >> 12) & 0x000F000Fu) | 0x43004300u, xh[2 * h + 1], ahi);
-                bhi = naiwa_dot2_bf16(((qb >> 12) & 0x000F000Fu) | 0x43004300u, xh[2 * h + 1], bhi);
+                alo = naiwa_dot2_bf16(naiwa_nib(qa, nc), xl[2 * h], alo);
+                blo = naiwa_dot2_bf16(naiwa_nib(qb, nc), xl[2 * h], blo);
+                alo = naiwa_dot2_bf16(naiwa_nib(qa >> 8, nc), xl[2 * h + 1], alo);
+                blo = naiwa_dot2_bf16(naiwa_nib(qb >> 8, nc), xl[2 * h + 1], blo);
+                ahi = naiwa_dot2_bf16(naiwa_nib(qa >> 4, nc), xh[2 * h], ahi);
+                bhi = naiwa_dot2_bf16(naiwa_nib(qb >> 4, nc), xh[2 * h], bhi);
+                ahi = naiwa_dot2_bf16(naiwa_nib(qa >> 12, nc), xh[2 * h + 1], ahi);
+                bhi = naiwa_dot2_bf16(naiwa_nib(qb >> 12, nc), xh[2 * h + 1], bhi);
             }
         }
         const float slo = sv.x + sv.y, shi = sv.z + sv.w;
