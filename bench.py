@@ -292,8 +292,8 @@ def print_trace(nm, run, stream, L, khz):
             sub["logits seen"].append(np.median(m[:, 10]) - pub)
             sub["x staged (wave 1)"].append(np.median(m[:, 13]) - pub)
             sub["keys+barrier"].append(np.median(m[:, 0] - m[:, 10]))
-            sub["weights"].append(np.median(m[:, 11] - m[:, 1]))
-            sub["pairs"].append(np.median(m[:, 12] - m[:, 11]))
+            sub["weights"].append(np.median(m[:, 11] - m[:, 2]))
+            sub["pairs"].append(np.median(m[:, 12] - m[:, 1]))
         pub = m[:nlead, 9].max()
     if sub["weights"]:
         log("trace: one-token routing, median us after the last logits publish: " +

@@ -445,21 +445,17 @@ __device__ inline void rank_slice(const Params& p, Smem& sm, int wave, int lane)
         if (lane + 64 * j < E) sm.rcnt[wave][lane + 64 * j] = cnt[j];
 }
 
-// One token, wave 0: the grouping of its k pairs (lane q = pair q, inp: q < k)
-// by slot, all in registers: each pair's position in (slot, q) order and its
-// predecessor's slot come from the other lanes' keys, one readlane each.
-__device__ inline void group_pairs_one(const Params& p, Smem& sm, const LayerDev& L, int l, int lane, bool inp,
-                                       uint32_t e, float w) {
+// One token, wave 0: the grouping of its k pairs (lane q = pair q = the rank-q
+// expert e, inp: q < k) by slot, all in registers: each pair's position in
+// (slot, q) order and its predecessor's slot come from the other lanes' keys,
+// one readlane each.  A pair is grouped when its expert has a slot; its weight
+// comes later (weigh_one_row), and a zero weight is skipped at the combine.
+__device__ inline void group_pairs_one(const Params& p, Smem& sm, const LayerDev& L, int lane, bool inp, uint32_t e) {
     const int k = p.k;
     const int q = lane;
     const int32_t s = inp ? (L.slot_of ? sm.slot_tab[e] : (int32_t)e) : -1;
-    const bool ok = inp && s >= 0 && s < L.slots;
-    if (inp && !ok && blockIdx.x == 0) atomicAdd(&p.status[1], 1);
-    if (inp && blockIdx.x == 0 && p.ids_out) {
-        p.ids_out[(size_t)l * k + q] = e;
-        p.w_out[(size_t)l * k + q] = w;
-    }
-    const bool valid = ok && w != 0.0f;
+    const bool valid = inp && s >= 0 && s < L.slots;
+    if (inp && !valid && blockIdx.x == 0) atomicAdd(&p.status[1], 1);
     const uint32_t key = valid ? (((uint32_t)s << 6) | (uint32_t)q) : 0xFFFFFFFFu; // invalid pairs sort last
     int rank = 0;
     long long pk = -1; // the largest key below this one
@@ -480,7 +476,6 @@ __device__ inline void group_pairs_one(const Params& p, Smem& sm, const LayerDev
     const int nvalid = __popcll(__ballot(valid));
     const int nseg = __popcll(__ballot(start));
     sm.pair_slot[q] = valid ? (uint32_t)s : 0u;
-    sm.pair_w[q] = valid ? w : 0.0f;
     if (valid) {
         sm.sorted[rank] = (uint32_t)q;
         sm.srt_slot[rank] = (uint32_t)s;
@@ -498,11 +493,10 @@ __device__ inline void group_pairs_one(const Params& p, Smem& sm, const LayerDev
 
 // One token, wave 0, after every wave's key-slice counts: the rank of each
 // expert (lane l: experts l + 64 j), the top k through LDS (lane j takes the
-// rank-j expert), the weights (denominators summed in rank order, or in expert
-// order over all E for the softmax-without-renormalisation mode, as the oracle
-// sums them), then the grouping of the pairs.
+// rank-j expert: my_e, its logit my_f), then the grouping of the pairs.
 template <int KPL>
-__device__ inline void route_one_row(const Params& p, Smem& sm, const LayerDev& L, int l, int lane) {
+__device__ inline void route_one_row(const Params& p, Smem& sm, const LayerDev& L, int l, int lane, uint32_t& my_e,
+                                     float& my_f) {
     const int E = p.E, k = p.k;
 #pragma unroll
     for (int j = 0; j < KPL; ++j) {
@@ -521,8 +515,20 @@ __device__ inline void route_one_row(const Params& p, Smem& sm, const LayerDev& 
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const bool inp = lane < k;
-    const uint32_t my_e = inp ? sm.top_ids[0][lane] : 0u;
-    const float my_f = inp ? sm.top_ex[0][lane] : 0.0f;
+    my_e = inp ? sm.top_ids[0][lane] : 0u;
+    my_f = inp ? sm.top_ex[0][lane] : 0.0f;
+    group_pairs_one(p, sm, L, lane, inp, my_e);
+    mark_wave(p, l, 12);
+}
+
+// One token, wave 0: the routing weights of the k pairs (denominators summed in
+// rank order, or in expert order over all E for the softmax-without-
+// renormalisation mode, as the oracle sums them) into pair_w, and the routing
+// outputs.  Runs while the gate/up rows are on their way; pair_w is first read
+// in phase C.
+__device__ inline void weigh_one_row(const Params& p, Smem& sm, int l, int lane, uint32_t my_e, float my_f) {
+    const int E = p.E, k = p.k;
+    const bool inp = lane < k;
     const float mx = readlane_f32(my_f, 0);
     const float ex = inp ? expf(my_f - mx) : 0.0f;
     float denom = 0.0f;
@@ -538,9 +544,13 @@ __device__ inline void route_one_row(const Params& p, Smem& sm, const LayerDev& 
 #pragma unroll
         for (int o = 0; o < kMaxK; ++o) denom += o < k ? readlane_f32(ex, o) : 0.0f;
     }
+    const float w = inp ? ex / denom : 0.0f;
+    if (inp) sm.pair_w[lane] = w;
+    if (inp && blockIdx.x == 0 && p.ids_out) {
+        p.ids_out[(size_t)l * k + lane] = my_e;
+        p.w_out[(size_t)l * k + lane] = w;
+    }
     mark_wave(p, l, 11);
-    group_pairs_one(p, sm, L, l, lane, inp, my_e, inp ? ex / denom : 0.0f);
-    mark_wave(p, l, 12);
 }
 
 // ---------------------------------------------------------------------------
@@ -867,6 +877,13 @@ stack_kernel(Params p) {
 
         // ---- A: poll logits + activations, rank, weights, segments ----
         const int ngroups = rows * gpt_h;
+        uint32_t r_e = 0; // one token: wave 0 lane j's rank-j expert and its logit
+        float r_f = 0.0f;
+        // one token: the weights, computed by wave 0 once its gate/up loads are out
+        auto weigh = [&]() {
+            if constexpr (MR == 1)
+                if (wave == 0) weigh_one_row(p, sm, l, lane, r_e, r_f);
+        };
         if constexpr (MR == 1) {
             // wave 0 routes the token while waves 1-3 poll and stage its activations
             if (wave == 0) {
@@ -904,9 +921,9 @@ stack_kernel(Params p) {
             mark(p, l, 1);
             if (wave == 0) {
                 if (E <= 128)
-                    route_one_row<2>(p, sm, L, l, lane);
+                    route_one_row<2>(p, sm, L, l, lane, r_e, r_f);
                 else
-                    route_one_row<kMaxE / 64>(p, sm, L, l, lane);
+                    route_one_row<kMaxE / 64>(p, sm, L, l, lane, r_e, r_f);
             }
         } else {
             for (int g0 = 0; g0 < ngroups; g0 += XG * kThreads) {
@@ -1067,6 +1084,7 @@ stack_kernel(Params p) {
                         }
                     }
                 }
+                if (r0 == q0) weigh();
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 if (r0 == q0) {
                     mark(p, l, 3);
@@ -1077,10 +1095,12 @@ stack_kernel(Params p) {
             }
             mark_wave(p, l, 16); // every wave: the last one to store wins
             if (q0 >= q1) {
+                weigh();
                 mark(p, l, 3);
                 prefetch_down();
             }
         } else {
+            weigh();
             mark(p, l, 3);
             prefetch_down();
 #pragma unroll 1
@@ -1170,9 +1190,11 @@ stack_kernel(Params p) {
                             for (int j = 0; j < kCB; ++j) {
                                 const int it = it0 + j * kGroups;
                                 const float v = naiwa_group_sum<NAIWA_GROUP>(acc[j]);
-                                if (it < nit && lr == 0)
-                                    sm.partial[it % kChunk][b0 + it / kChunk] =
-                                        v * sm.pair_w[sm.sorted[b0 + it / kChunk]];
+                                if (it < nit && lr == 0) {
+                                    // a zero weight contributes nothing, whatever the dot
+                                    const float w = sm.pair_w[sm.sorted[b0 + it / kChunk]];
+                                    sm.partial[it % kChunk][b0 + it / kChunk] = w != 0.0f ? v * w : 0.0f;
+                                }
                             }
                         }
                     };
