@@ -1,38 +1,42 @@
-// NAIWA_STACK_FUSED: one persistent, cooperatively launched kernel runs a
-// whole decode step through every MoE layer, x <- bf16(x + MoE_l(x)).
+// NAIWA_STACK_FUSED: one persistent kernel runs a whole decode step through
+// every MoE layer, x <- bf16(x + MoE_l(x)).
 //
-// One workgroup of 256 threads per CU (16 groups of 16 lanes, one wave per
-// SIMD), every workgroup resident.  Per layer:
-//   A  route   every workgroup polls the layer's logits and activations, ranks
-//              the experts of each token, derives the routing weights and
-//              groups the (token, k) pairs by cache slot -- redundantly and
-//              identically everywhere, so routing needs no exchange;
-//   B  gate/up the (segment, intermediate row) work is dealt out evenly.  For
-//              Q4_K each lane owns whole 144-byte blocks: lanes 0-7 of a group
-//              take the gate row, lanes 8-15 the up row, so a block's scales
-//              are decoded once per 256 weights.  Two rows' loads per group are
-//              in flight before the first is used, and the down rows and next
-//              router columns that phase C needs are loaded into registers in
-//              the same burst;
-//   C  down    each workgroup owns 8-feature output chunks: it polls the h
-//              vectors, dots every (feature, pair), adds the pairs of each
-//              token in ascending slot order (no atomics), applies the
-//              residual, publishes its x chunk and its int64 partial sums of
-//              the next layer's router logits; 32 leader workgroups add every
-//              chunk's partials for their experts and publish the logits.
+// One workgroup of 512 threads per CU (8 waves, two per SIMD), every
+// workgroup resident.  Per layer:
+//   A  route   every workgroup polls the layer's logits and activations and
+//              routes redundantly and identically: for one token, wave 0 polls
+//              the logits while the other waves stage x; every wave counts, for
+//              each expert, the keys above it in one slice of the experts; wave
+//              0 adds the counts, takes the top k and groups the pairs by slot
+//              (its weights follow while the gate/up rows load);
+//   B  gate/up the (segment, row pair) items are dealt out evenly.  A wave
+//              gathers its items' gate and up row pairs into LDS with coalesced
+//              16-byte DMA pieces, then 32 lanes per item take one 144-byte Q4_K
+//              block's half (both rows at once, each activation word feeding
+//              two dots); h goes out as tagged pairs of 16-bit values, then one
+//              tagged done word per workgroup.  The down rows and next router
+//              columns of the workgroup's first output chunk are DMA'd into LDS
+//              meanwhile;
+//   C  down    each workgroup owns 8-feature output chunks: it waits for every
+//              done word, reads all h once, dots every (feature, pair), adds the
+//              pairs of each token in ascending slot order (no atomics),
+//              applies the residual, publishes its x chunk and its int64 partial
+//              sums of the next layer's router logits; 32 leader workgroups add
+//              every chunk's partials for their experts and publish the logits.
 //
 // There is no grid barrier.  Every value one workgroup hands to another (x,
-// h, router partials, logits) is a 64-bit word (tag << 32) | payload written
-// with one device-coherent store (past the per-XCD L2s), where the tag names
-// the launch and the layer.  A consumer loads the words it needs and reloads
-// those whose tag is not yet current, so each hand-off costs one round trip
-// and no workgroup waits for more than the data it reads.  Every wait is
-// bounded; a timeout is counted and makes every later wait give up at once.
-// Reuse is safe without barriers: a workgroup can only reach layer l+1 after
-// seeing layer l+1's logits, which need every chunk's layer-l partials, which
-// each workgroup produces after its last layer-l read of h and of the logits;
-// x alternates between two buffers, since idle workgroups may still read x_l
-// while chunk owners publish x_{l+1}.
+// h, done words, router partials, logits) is a 64-bit word (tag << 32) |
+// payload written with one device-coherent store, where the tag names the
+// launch and the layer.  A consumer loads the words it needs and reloads those
+// whose tag is not yet current.  Every wait is bounded; a timeout is counted
+// and makes every later wait give up at once, so a grid that cannot be
+// co-resident drains instead of hanging.  Reuse is safe without barriers: a
+// workgroup can only reach layer l+1 after seeing layer l+1's logits, which
+// need every chunk's layer-l partials, which each workgroup produces after its
+// last layer-l read of h and of the logits; x alternates between two buffers,
+// since idle workgroups may still read x_l while chunk owners publish x_{l+1}.
+// vmcnt counts stores as well as loads, so the stores that end phase C come
+// from the waves that do not poll right after it.
 //
 // Router logits: each chunk of 8 features is an f32 fma chain rounded to
 // int64 with 32 fractional bits, and the chunks are added as integers.
@@ -1278,13 +1282,14 @@ int launch(const Params& prm, int blocks, size_t lds, hipStream_t st) {
     void* args[] = {&copy};
     hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return (int)e;
-    // The grid never exceeds the blocks every CU can hold at once; the
-    // cooperative launch also makes the runtime check it.  NAIWA_STACK_LAUNCH=
-    // normal uses a plain launch (profilers that cannot follow cooperative
-    // launches); the bounded waits keep that safe.
+    // The grid never exceeds the blocks every CU can hold at once (checked
+    // against the occupancy above), so a plain launch is resident when the
+    // device is not shared; the bounded waits keep it safe when it is.
+    // NAIWA_STACK_LAUNCH=cooperative makes the runtime check residency too (a
+    // cooperative launch costs about 20 us more per step here).
     static const bool normal = [] {
         const char* v = getenv("NAIWA_STACK_LAUNCH");
-        return v && strcmp(v, "normal") == 0;
+        return !(v && strcmp(v, "cooperative") == 0);
     }();
     if (normal)
         e = hipLaunchKernel((const void*)fn, dim3(blocks), dim3(kThreads), args, (unsigned)lds, st);
