@@ -1110,9 +1110,12 @@ stack_kernel(Params p) {
 #pragma unroll 1
             for (int q = q0 + grp; q < q1; q += kGroups) unit_pair<DG, DD>(p, sm, L, dyn, q, xstage, rb, nu, lr, tag);
         }
-        // every h word of this workgroup is stored: say so with one tagged word
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+        // every h word of this workgroup is issued: say so with one tagged word,
+        // right behind them (a consumer still checks every h word's tag, so the
+        // done word only needs to follow the stores, not their completion)
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
         if (tid == 0 && q0 < q1) st64(&p.done[bid], tagged(tag, 0u));
         mark(p, l, 4);
 
@@ -1126,13 +1129,19 @@ stack_kernel(Params p) {
             // workgroup with gate/up items.  The full read below still checks every
             // word's tag; this only keeps the polling traffic small while the last
             // producers are still computing.
+            // (wave 0 alone polls, four words per lane per round: fewer loads in flight)
             {
                 const int nprod_h = (total + per - 1) / per;
-                for (int b2 = tid; b2 < nprod_h; b2 += kThreads) {
-                    u64 v[1];
-                    auto addr = [&](int) -> const u64* { return p.done + b2; };
-                    issue_tagged(v, addr, tag);
-                    wait_tagged(v, addr, tag, p);
+                if (wave == 0) {
+                    for (int b0 = 0; b0 < nprod_h; b0 += 256) {
+                        u64 v[4];
+                        auto addr = [&](int j) -> const u64* {
+                            const int b2 = b0 + lane + 64 * j;
+                            return b2 < nprod_h ? p.done + b2 : nullptr;
+                        };
+                        issue_tagged(v, addr, tag);
+                        wait_tagged(v, addr, tag, p);
+                    }
                 }
                 __syncthreads();
                 mark(p, l, 14);
