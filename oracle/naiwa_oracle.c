@@ -8,6 +8,7 @@
 #include "naiwa_oracle.h"
 
 #include <math.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -437,6 +438,91 @@ int orc_fused_moe_decode(const orc_stack* gate, const orc_stack* up, const orc_s
     return 0;
 }
 
+/* The same computation on `threads` host threads (the CPU baseline): pass 1's
+ * (pair, row) values and pass 2's output features are split into contiguous
+ * ranges, and each value is computed exactly as in orc_fused_moe_decode, so
+ * the result is bit-identical to it. */
+typedef struct {
+    const orc_stack *gate, *up, *down;
+    const float* x;
+    const uint32_t* id;
+    const float* wt;
+    const int* owner;
+    float* h;
+    float* o;
+    int width, pass, lo, hi; /* pass 1: flat (j * I + r) range; pass 2: feature range */
+} mt_job;
+
+static void* mt_run(void* arg) {
+    const mt_job* jb = (const mt_job*)arg;
+    const int H = jb->gate->k, I = jb->gate->n;
+    if (jb->pass == 1) {
+        for (int f = jb->lo; f < jb->hi; ++f) {
+            const int j = f / I, r = f % I;
+            if (jb->owner[j] != j) continue;
+            float g = orc_vec_dot(jb->gate->dtype, expert_row(jb->gate, (int)jb->id[j], r), jb->x, H);
+            float u = orc_vec_dot(jb->up->dtype, expert_row(jb->up, (int)jb->id[j], r), jb->x, H);
+            float s = g / (1.0f + expf(-g));
+            jb->h[(int64_t)j * I + r] = s * u;
+        }
+    } else {
+        for (int r = jb->lo; r < jb->hi; ++r) {
+            float acc = 0.0f;
+            for (int j = 0; j < jb->width; ++j) {
+                if (jb->owner[j] < 0) continue;
+                float y = orc_vec_dot(jb->down->dtype, expert_row(jb->down, (int)jb->id[j], r),
+                                      jb->h + (int64_t)jb->owner[j] * I, I);
+                acc += jb->wt[j] * y;
+            }
+            jb->o[r] = acc;
+        }
+    }
+    return NULL;
+}
+
+int orc_fused_moe_decode_mt(const orc_stack* gate, const orc_stack* up, const orc_stack* down,
+                            const float* xs, const uint32_t* ids, const float* w,
+                            int rows, int width, float* out, int threads) {
+    if (check_stacks(gate, up, down)) return -1;
+    if (threads < 1 || threads > 256) return -1;
+    const int H = gate->k, I = gate->n, E = gate->e;
+    for (int i = 0; i < rows * width; ++i)
+        if (ids[i] >= (uint32_t)E) return -1;
+    float* h = (float*)malloc(sizeof(float) * (size_t)width * (size_t)I);
+    int* owner = (int*)malloc(sizeof(int) * (size_t)width);
+    mt_job* jobs = (mt_job*)malloc(sizeof(mt_job) * (size_t)threads);
+    pthread_t* tid = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)threads);
+    if (!h || !owner || !jobs || !tid) { free(h); free(owner); free(jobs); free(tid); return -2; }
+    int rc = 0;
+    for (int t = 0; t < rows && !rc; ++t) {
+        const uint32_t* id = ids + (int64_t)t * width;
+        const float* wt = w + (int64_t)t * width;
+        for (int j = 0; j < width; ++j) { /* the same owners as the single-threaded pass 1 */
+            owner[j] = -1;
+            if (wt[j] == 0.0f) continue;
+            for (int i = 0; i < j; ++i)
+                if (owner[i] >= 0 && id[i] == id[j]) { owner[j] = owner[i]; break; }
+            if (owner[j] < 0) owner[j] = j;
+        }
+        for (int pass = 1; pass <= 2 && !rc; ++pass) {
+            const int n = pass == 1 ? width * I : H;
+            int started = 0;
+            for (int k = 0; k < threads; ++k) {
+                jobs[k] = (mt_job){gate, up, down, xs + (int64_t)t * H, id, wt, owner, h, out + (int64_t)t * H,
+                                   width, pass, (int)((int64_t)n * k / threads), (int)((int64_t)n * (k + 1) / threads)};
+                if (pthread_create(&tid[k], NULL, mt_run, &jobs[k]) != 0) { rc = -2; break; }
+                ++started;
+            }
+            for (int k = 0; k < started; ++k) pthread_join(tid[k], NULL);
+        }
+    }
+    free(h);
+    free(owner);
+    free(jobs);
+    free(tid);
+    return rc;
+}
+
 int orc_fused_moe_decode_f64(const orc_stack* gate, const orc_stack* up, const orc_stack* down,
                              const float* xs, const uint32_t* ids, const float* w,
                              int rows, int width, double* out) {
@@ -554,8 +640,8 @@ int orc_gather(const uint32_t* ids, int n, int E, uint32_t* perm, uint32_t* offs
 /* stack decode                                                              */
 /* ------------------------------------------------------------------------- */
 
-int orc_stack_decode(const orc_layer* layers, int n_layers, uint16_t* x, int rows, int H,
-                     int E, int k, int mode, uint32_t* ids_out, float* w_out) {
+static int stack_decode_impl(const orc_layer* layers, int n_layers, uint16_t* x, int rows, int H,
+                             int E, int k, int mode, uint32_t* ids_out, float* w_out, int threads) {
     float* xf = (float*)malloc(sizeof(float) * (size_t)rows * H);
     float* y = (float*)malloc(sizeof(float) * (size_t)rows * H);
     float* logits = (float*)malloc(sizeof(float) * (size_t)rows * E);
@@ -570,7 +656,9 @@ int orc_stack_decode(const orc_layer* layers, int n_layers, uint16_t* x, int row
         if ((rc = orc_topk(logits, rows, E, k, mode, ids, w))) break;
         if (ids_out) memcpy(ids_out + (int64_t)l * rows * k, ids, sizeof(uint32_t) * (size_t)rows * k);
         if (w_out) memcpy(w_out + (int64_t)l * rows * k, w, sizeof(float) * (size_t)rows * k);
-        if ((rc = orc_fused_moe_decode(&L->gate, &L->up, &L->down, xf, ids, w, rows, k, y))) break;
+        rc = threads > 0 ? orc_fused_moe_decode_mt(&L->gate, &L->up, &L->down, xf, ids, w, rows, k, y, threads)
+                         : orc_fused_moe_decode(&L->gate, &L->up, &L->down, xf, ids, w, rows, k, y);
+        if (rc) break;
         for (int64_t i = 0; i < (int64_t)rows * H; ++i) x[i] = orc_f32_to_bf16(xf[i] + y[i]);
     }
 done:
@@ -580,4 +668,15 @@ done:
     free(ids);
     free(w);
     return rc;
+}
+
+int orc_stack_decode(const orc_layer* layers, int n_layers, uint16_t* x, int rows, int H,
+                     int E, int k, int mode, uint32_t* ids_out, float* w_out) {
+    return stack_decode_impl(layers, n_layers, x, rows, H, E, k, mode, ids_out, w_out, 0);
+}
+
+int orc_stack_decode_mt(const orc_layer* layers, int n_layers, uint16_t* x, int rows, int H,
+                        int E, int k, int mode, uint32_t* ids_out, float* w_out, int threads) {
+    if (threads < 1) return -1;
+    return stack_decode_impl(layers, n_layers, x, rows, H, E, k, mode, ids_out, w_out, threads);
 }

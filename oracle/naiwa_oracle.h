@@ -100,6 +100,10 @@ int      orc_fused_moe_decode(const orc_stack* gate, const orc_stack* up, const 
                               const float* xs, const uint32_t* ids, const float* w,
                               int rows, int width, float* out);
 /* The same computation in fp64 end to end (brute-force pin). */
+/* The same on `threads` host threads, bit-identical (CPU baseline). */
+int      orc_fused_moe_decode_mt(const orc_stack* gate, const orc_stack* up, const orc_stack* down,
+                                 const float* xs, const uint32_t* ids, const float* w,
+                                 int rows, int width, float* out, int threads);
 int      orc_fused_moe_decode_f64(const orc_stack* gate, const orc_stack* up, const orc_stack* down,
                                   const float* xs, const uint32_t* ids, const float* w,
                                   int rows, int width, double* out);
@@ -125,6 +129,9 @@ typedef struct orc_layer {
  * (optional) receives [layers, rows, k] routed ids. */
 int      orc_stack_decode(const orc_layer* layers, int n_layers, uint16_t* x, int rows, int H,
                           int E, int k, int mode, uint32_t* ids_out, float* w_out);
+/* The same with the expert path on `threads` host threads (bit-identical). */
+int      orc_stack_decode_mt(const orc_layer* layers, int n_layers, uint16_t* x, int rows, int H,
+                             int E, int k, int mode, uint32_t* ids_out, float* w_out, int threads);
 
 #ifdef __cplusplus
 }

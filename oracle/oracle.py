@@ -84,6 +84,10 @@ def _declare(L: C.CDLL) -> None:
     L.orc_gather.argtypes = [vp, i32, i32, vp, vp]
     L.orc_stack_decode.restype = i32
     L.orc_stack_decode.argtypes = [C.POINTER(Layer), i32, vp, i32, i32, i32, i32, i32, vp, vp]
+    L.orc_stack_decode_mt.restype = i32
+    L.orc_stack_decode_mt.argtypes = [C.POINTER(Layer), i32, vp, i32, i32, i32, i32, i32, vp, vp, i32]
+    L.orc_fused_moe_decode_mt.restype = i32
+    L.orc_fused_moe_decode_mt.argtypes = [sp, sp, sp, vp, vp, vp, i32, i32, vp, i32]
 
 
 def _p(a: np.ndarray) -> int:
@@ -190,6 +194,21 @@ def fused_moe_decode(gate: Stack, up: Stack, down: Stack, xs: np.ndarray, ids: n
     return out
 
 
+def fused_moe_decode_mt(gate: Stack, up: Stack, down: Stack, xs: np.ndarray, ids: np.ndarray,
+                        w: np.ndarray, threads: int) -> np.ndarray:
+    """fused_moe_decode on `threads` host threads (bit-identical; the CPU baseline)."""
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, width = ids.shape
+    out = np.empty((rows, gate.k), dtype=np.float32)
+    rc = lib().orc_fused_moe_decode_mt(C.byref(gate), C.byref(up), C.byref(down), _p(xs), _p(ids),
+                                       _p(w), rows, width, _p(out), threads)
+    if rc != 0:
+        raise ValueError(f"orc_fused_moe_decode_mt failed ({rc})")
+    return out
+
+
 def fused_moe_decode_f64(gate: Stack, up: Stack, down: Stack, xs: np.ndarray, ids: np.ndarray,
                          w: np.ndarray) -> np.ndarray:
     xs = np.ascontiguousarray(xs, dtype=np.float32)
@@ -235,8 +254,9 @@ def gather(ids: np.ndarray, E: int):
 
 
 def stack_decode(layers: list, x_bf16: np.ndarray, E: int, k: int,
-                 mode: int = ROUTE_SOFTMAX_TOPK_RENORM):
+                 mode: int = ROUTE_SOFTMAX_TOPK_RENORM, threads: int = 0):
     """layers: list of (router f32 [E,H], (gate_q, up_q, down_q), (dtype_g, dtype_u, dtype_d), I).
+    threads > 0 runs the expert path on that many host threads (bit-identical).
 
     Returns (x_out bf16 [rows,H], ids [L,rows,k], w [L,rows,k])."""
     x = np.array(x_bf16, dtype=np.uint16, copy=True, order="C")
@@ -252,7 +272,10 @@ def stack_decode(layers: list, x_bf16: np.ndarray, E: int, k: int,
         arr[i].down = stack(dq, dd, H, inter)
     ids = np.empty((len(layers), rows, k), dtype=np.uint32)
     w = np.empty((len(layers), rows, k), dtype=np.float32)
-    rc = lib().orc_stack_decode(arr, len(layers), _p(x), rows, H, E, k, mode, _p(ids), _p(w))
+    if threads > 0:
+        rc = lib().orc_stack_decode_mt(arr, len(layers), _p(x), rows, H, E, k, mode, _p(ids), _p(w), threads)
+    else:
+        rc = lib().orc_stack_decode(arr, len(layers), _p(x), rows, H, E, k, mode, _p(ids), _p(w))
     if rc != 0:
         raise ValueError(f"orc_stack_decode failed ({rc})")
     return x, ids, w

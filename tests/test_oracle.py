@@ -319,6 +319,25 @@ def test_stack_decode_is_residual_chain():
     assert np.array_equal(O.to_bf16(x), x1)
 
 
+@pytest.mark.parametrize("threads", [1, 3, 8])
+def test_threaded_expert_path_is_bit_identical(threads):
+    """The CPU baseline's threaded expert path splits rows and features over
+    threads but computes every value as the single-threaded pass does."""
+    H, I, E, k = 512, 256, 8, 3
+    g, u, d, r = S.layer(60, E, H, I, (O.Q4_K, O.Q4_K, O.Q8_0))
+    gs, us, ds = _stacks(g, u, d, H, I, (O.Q4_K, O.Q4_K, O.Q8_0))
+    x = O.from_bf16(S.activations_bf16(61, 3, H))
+    ids = np.array([[1, 5, 1], [7, 0, 2], [3, 3, 6]], dtype=np.uint32)   # repeats share pass 1
+    w = np.array([[0.5, 0.25, 0.25], [0.0, 0.6, 0.4], [0.3, 0.3, 0.4]], dtype=np.float32)
+    want = O.fused_moe_decode(gs, us, ds, x, ids, w)
+    assert np.array_equal(O.fused_moe_decode_mt(gs, us, ds, x, ids, w, threads), want)
+    layers = [(r, (g, u, d), (O.Q4_K, O.Q4_K, O.Q8_0), I)]
+    x0 = S.activations_bf16(62, 2, H)
+    a = O.stack_decode(layers, x0, E, 2)
+    b = O.stack_decode(layers, x0, E, 2, threads=threads)
+    assert all(np.array_equal(p, q) for p, q in zip(a, b))
+
+
 # ---- gather ---------------------------------------------------------------------------
 
 def test_gather_brute_force():
