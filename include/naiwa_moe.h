@@ -43,6 +43,8 @@ extern "C" {
 #define NAIWA_E_BAD_ID      -5  /* expert or slot id out of range            */
 #define NAIWA_E_NOT_FOUND   -6  /* no such expert / slot / entry             */
 #define NAIWA_E_DEVICE      -7  /* the device reported a failed condition    */
+#define NAIWA_E_FORMAT      -8  /* malformed or unsupported file (GGUF)      */
+#define NAIWA_E_IO          -9  /* a file cannot be opened or mapped         */
 
 /* ---- GGML type ids --------------------------------------------------------- */
 #define NAIWA_F32  0

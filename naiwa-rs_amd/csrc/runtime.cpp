@@ -63,6 +63,8 @@ const char* naiwa_status_string(int rc) {
     case NAIWA_E_BAD_ID: return "expert or slot id out of range";
     case NAIWA_E_NOT_FOUND: return "not found";
     case NAIWA_E_DEVICE: return "device reported failure";
+    case NAIWA_E_FORMAT: return "malformed or unsupported file";
+    case NAIWA_E_IO: return "file cannot be opened or mapped";
     default: return rc > 0 ? hipGetErrorString((hipError_t)rc) : "unknown status";
     }
 }

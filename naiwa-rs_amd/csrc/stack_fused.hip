@@ -322,22 +322,6 @@ __device__ __forceinline__ u64 rank_key(float f, int e) {
     const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((u64)o << 32) | (uint32_t)~(uint32_t)e;
 }
-// The logit of a key's high word (rank_key's order bits; -0 comes back as +0).
-__device__ __forceinline__ float key_logit(uint32_t o) {
-    return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
-}
-
-// Maximum over the 64 lanes of the wave (every lane active): DPP within each
-// row of 16, then the four row results.
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
-    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
-    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
-    return max(max(a, b), max(c, d));
-}
 __device__ __forceinline__ float readlane_f32(float v, int ln) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), ln));
 }

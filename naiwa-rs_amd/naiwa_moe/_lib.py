@@ -15,6 +15,7 @@ LIB_PATH = os.environ.get("NAIWA_MOE_LIB") or os.path.join(PKG_ROOT, "libnaiwa_m
 
 OK = 0
 E_INVALID, E_UNSUPPORTED, E_TIMEOUT, E_NOMEM, E_BAD_ID, E_NOT_FOUND, E_DEVICE = -1, -2, -3, -4, -5, -6, -7
+E_FORMAT, E_IO = -8, -9
 
 F32, F16, Q8_0, Q4_K, BF16 = 0, 1, 8, 12, 30
 ACT_SILU, ACT_GELU_PYTORCH_TANH = 0, 1
@@ -194,6 +195,18 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_cache_stage": (i32, [vp, vp, vp, i32, i32, f32, vp, vp, vp, _P(i32)]),
     "naiwa_stats_read": (i32, [vp, i32]),
     "naiwa_stats_add": (i32, [vp]),
+    # include/naiwa_gguf.h
+    "naiwa_gguf_open": (i32, [C.c_char_p, _P(vp)]),
+    "naiwa_gguf_close": (i32, [vp]),
+    "naiwa_gguf_version": (i32, [vp, _P(u32)]),
+    "naiwa_gguf_alignment": (i32, [vp, _P(u64)]),
+    "naiwa_gguf_tensor_count": (i32, [vp, _P(i32)]),
+    "naiwa_gguf_tensor_at": (i32, [vp, i32, vp]),
+    "naiwa_gguf_find": (i32, [vp, C.c_char_p, vp]),
+    "naiwa_gguf_meta_u64": (i32, [vp, C.c_char_p, _P(u64)]),
+    "naiwa_gguf_meta_string": (i32, [vp, C.c_char_p, C.c_char_p, i32, _P(i32)]),
+    "naiwa_ggml_type_size": (i32, [i32, _P(i32), _P(i32)]),
+    "naiwa_gguf_expert_stack": (i32, [vp, i32, i32, vp]),
 }
 
 
