@@ -68,6 +68,9 @@ def parse() -> argparse.Namespace:
                          "reference for HBM traffic counters)")
     ap.add_argument("--trace", action="store_true",
                     help="print per-phase times of one fused step (diagnostic, untimed)")
+    ap.add_argument("--lookahead-swaps", type=int, default=-1, metavar="N",
+                    help="cache25: predict each next layer's experts from this layer's activation and load them "
+                         "(at most N LRU swaps per row, the reference's --lookahead-swaps); -1 = off")
     ap.add_argument("--workload", choices=["resident", "cache25", "prefill"], default="resident",
                     help="resident: every expert in HBM (the headline); cache25: 32 of 128 experts "
                          "cached per layer, Zipf(1.1) routing, misses streamed over PCIe; prefill: "
@@ -417,11 +420,21 @@ def run_cache25(args) -> int:
     y = nm.DeviceBuffer(rows * H * 4)
     lib = nm.lib()
 
+    swaps = args.lookahead_swaps
+    ahead_tot = {"loads": 0, "swaps": 0, "predicted": 0, "resident": 0}
+
     def step(i: int) -> dict:
         tot = {"hits": 0, "staged": 0, "staged_experts": 0, "promoted": 0, "pcie_bytes": 0}
         lib.naiwa_memcpy_d2d(x.ptr, xs.ptr + i * rows * H * 2, rows * H * 2, compute.handle)
-        for layer in layers:
-            info = layer.forward(x, rows, y, pcie_frac=1.0, promote_cap=1, min_hits=4, stream=compute.handle)
+        for l, layer in enumerate(layers):
+            if swaps >= 0 and l + 1 < L:
+                # the next layer's experts predicted from this layer's activation
+                info, ahead = layer.forward_ahead(layers[l + 1], x, rows, y, lookahead_swaps=swaps, pcie_frac=1.0,
+                                                  promote_cap=1, min_hits=4, stream=compute.handle)
+                for k_ in ahead_tot:
+                    ahead_tot[k_] += ahead[k_]
+            else:
+                info = layer.forward(x, rows, y, pcie_frac=1.0, promote_cap=1, min_hits=4, stream=compute.handle)
             nm._lib.check(lib.naiwa_residual_add_bf16(x.ptr, y.ptr, rows * H, compute.handle), "residual")
             for k_ in tot:
                 tot[k_] += info[k_]
@@ -432,6 +445,8 @@ def run_cache25(args) -> int:
     compute.sync()
     copy.sync()
     nm.policy.stats(reset=True)
+    for k_ in ahead_tot:
+        ahead_tot[k_] = 0
     tot = {"hits": 0, "staged": 0, "staged_experts": 0, "promoted": 0, "pcie_bytes": 0}
     e0, e1 = nm.Event(), nm.Event()
     e0.record(compute.handle)
@@ -450,6 +465,9 @@ def run_cache25(args) -> int:
     log(f"cache25: {ms / steps * 1e3:.1f} us/step, {tok_s:.1f} tok/s, hit rate {tot['hits'] / pairs:.3f}, "
         f"{tot['staged_experts'] / (steps * L):.2f} staged experts/layer/token, {tot['promoted']} promotions, "
         f"PCIe {pcie_gbs:.1f} GB/s, wall {wall:.2f}s")
+    if swaps >= 0:
+        log(f"cache25 lookahead (swaps {swaps}/row): {ahead_tot['loads']} loads, {ahead_tot['swaps']} swaps, "
+            f"{ahead_tot['resident'] / max(ahead_tot['predicted'], 1):.3f} of predictions already resident")
     result = {
         "metric": "MoE decode tok/s, 25% expert cache, Zipf(1.1) routing (Qwen3-30B-A3B shape, Q4_K)",
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
@@ -458,10 +476,12 @@ def run_cache25(args) -> int:
         "config": {"workload": "Qwen3-30B-A3B-shaped MoE stack decode, bs1, 32/128 experts cached per layer, "
                                "Zipf(1.1) routing bias, misses staged over PCIe (16-slot ring)",
                    "layers": L, "hidden": H, "experts": E, "top_k": K, "intermediate": I, "cached": usable,
-                   "ring": ring.length, "pcie_frac": 1.0, "promote_cap": 1, "parallelism": "none (1 GPU)"},
+                   "ring": ring.length, "pcie_frac": 1.0, "promote_cap": 1,
+                   "lookahead_swaps": swaps if swaps >= 0 else None, "parallelism": "none (1 GPU)"},
         "cache": {"hit_rate": round(tot["hits"] / pairs, 4),
                   "staged_experts_per_layer_token": round(tot["staged_experts"] / (steps * L), 3),
                   "promotions": tot["promoted"], "pcie_bytes": tot["pcie_bytes"],
+                  "lookahead": dict(ahead_tot) if swaps >= 0 else None,
                   "stats": nm.policy.stats()},
         "roofline": {"bound": "pcie", "achieved": round(pcie_gbs, 2), "peak": 64.0, "unit": "GB/s",
                      "frac": round(pcie_gbs / 64.0, 4), "traffic": None},

@@ -1,9 +1,12 @@
 // One MoE layer's decode step over a partial expert cache (include/naiwa_cached.h):
 // device routing, host policy, PCIe staging into ring slots, the expert kernel
 // over resident + staged slots, and promotion -- the stage order of the
-// reference's decode path (src/moe/decode.rs:241-381).
+// reference's decode path (src/moe/decode.rs:241-381) -- plus the lookahead
+// that loads the next layer's predicted experts while this layer computes
+// (src/moe/cached_layer.rs:1236-1300, src/moe/stages/preload.rs:18-111).
 #include <hip/hip_runtime.h>
 
+#include <initializer_list>
 #include <new>
 #include <vector>
 
@@ -39,6 +42,18 @@ struct naiwa_cached_layer {
     std::vector<hipEvent_t> ring_fence;  // per ring position: recorded after the step that read it
     std::vector<char> ring_fenced;
     hipEvent_t staged_done = nullptr;
+    // lookahead: this layer's prediction (its router on the previous layer's
+    // activation), the fence after the last step that read its cache slots,
+    // and the claim a forward waits for before its expert kernel
+    uint32_t* pred_ids_dev = nullptr;
+    float* pred_w_dev = nullptr;
+    uint32_t* pred_ids_h = nullptr;
+    int pred_rows = 0;
+    std::vector<uint32_t> predicted;
+    hipEvent_t read_done = nullptr;
+    bool read_recorded = false;
+    hipEvent_t ahead_done = nullptr;
+    bool ahead_claimed = false;
 
     void release_buffers() {
         if (ids_dev) (void)hipFree(ids_dev);
@@ -48,6 +63,12 @@ struct naiwa_cached_layer {
         if (w_h) (void)hipHostFree(w_h);
         if (slots_h) (void)hipHostFree(slots_h);
         if (slots_up) (void)hipHostFree(slots_up);
+        if (pred_ids_dev) (void)hipFree(pred_ids_dev);
+        if (pred_w_dev) (void)hipFree(pred_w_dev);
+        if (pred_ids_h) (void)hipHostFree(pred_ids_h);
+        pred_ids_dev = nullptr;
+        pred_w_dev = nullptr;
+        pred_ids_h = nullptr;
         ids_dev = nullptr;
         w_dev = nullptr;
         slots_dev = nullptr;
@@ -56,6 +77,8 @@ struct naiwa_cached_layer {
         slots_h = nullptr;
         slots_up = nullptr;
         cap_rows = 0;
+        last_rows = 0;
+        pred_rows = 0;
     }
 
     int ensure_rows(int rows) {
@@ -67,7 +90,8 @@ struct naiwa_cached_layer {
         if (hipMalloc(&ids_dev, n * 4) != hipSuccess || hipMalloc(&w_dev, n * 4) != hipSuccess ||
             hipMalloc(&slots_dev, n * 4) != hipSuccess || hipHostMalloc(&ids_h, n * 4, 0) != hipSuccess ||
             hipHostMalloc(&w_h, n * 4, 0) != hipSuccess || hipHostMalloc(&slots_h, n * 4, 0) != hipSuccess ||
-            hipHostMalloc(&slots_up, n * 4, 0) != hipSuccess) {
+            hipHostMalloc(&slots_up, n * 4, 0) != hipSuccess || hipMalloc(&pred_ids_dev, n * 4) != hipSuccess ||
+            hipMalloc(&pred_w_dev, n * 4) != hipSuccess || hipHostMalloc(&pred_ids_h, n * 4, 0) != hipSuccess) {
             release_buffers();
             return NAIWA_E_NOMEM;
         }
@@ -85,96 +109,103 @@ struct naiwa_cached_layer {
         src[1] = (const uint8_t*)d.host_up + (size_t)expert * bytes[1];
         src[2] = (const uint8_t*)d.host_down + (size_t)expert * bytes[2];
     }
+
+    // predict (src/moe/cached_layer.rs:1245-1259): this layer's router on the
+    // previous layer's activation, ranked by its logits (the bias term included,
+    // as in this layer's own routing; without one these are the reference's raw
+    // logits), read back with the caller's next synchronisation of `stream`
+    int predict_launch(const void* x, int rows, int64_t stream) {
+        const int n = rows * d.top_k;
+        int rc = naiwa_router_topk_biased(x, NAIWA_BF16, d.router, d.router_bias, rows, d.hidden, d.num_experts,
+                                          d.top_k, NAIWA_ROUTE_TOPK_SOFTMAX, pred_ids_dev, pred_w_dev, nullptr,
+                                          stream);
+        if (rc) return rc;
+        if ((rc = naiwa_hip_rc(hipMemcpyAsync(pred_ids_h, pred_ids_dev, (size_t)n * 4, hipMemcpyDeviceToHost,
+                                              (hipStream_t)stream))))
+            return rc;
+        pred_rows = rows;
+        return NAIWA_OK;
+    }
+
+    // prefetch_predicted (src/moe/cached_layer.rs:1268-1300) once the prediction
+    // is on the host: the union of the rows' top-k by votes; each predicted
+    // expert is admitted into an empty slot, else, while swaps < swaps_per_row *
+    // rows, replaces the LRU resident outside the prediction.  Uploads go on
+    // the copy stream behind the last step that read this layer's slots; the
+    // slots are published at once, because the only reader, this layer's next
+    // expert kernel, waits for the claim (ahead_done) recorded after them.
+    int prefetch_apply(int swaps_per_row, naiwa_lookahead_step* info) {
+        naiwa_lookahead_step a{};
+        const int rows = pred_rows, k = d.top_k;
+        std::vector<int> lens((size_t)rows, k);
+        predicted.assign((size_t)rows * k, 0u);
+        int np = 0;
+        int rc = naiwa_union_by_votes(pred_ids_h, lens.data(), rows, predicted.data(), (int)predicted.size(), &np);
+        if (rc) return rc;
+        predicted.resize((size_t)np);
+        a.predicted = np;
+        std::vector<int32_t> table((size_t)d.num_experts), protect(predicted.begin(), predicted.end());
+        if ((rc = naiwa_cache_slot_table(cache, table.data()))) return rc;
+        for (uint32_t e : predicted)
+            if (e < (uint32_t)d.num_experts && table[e] >= 0) ++a.resident;
+        const int max_swaps = swaps_per_row * rows;
+        const int64_t fence = read_recorded ? (int64_t)read_done : 0;
+        for (uint32_t e : predicted) {
+            if (e >= (uint32_t)d.num_experts) continue;
+            int slot = -1;
+            bool swap = false;
+            if ((rc = naiwa_cache_admit(cache, (int)e, &slot))) return rc;
+            if (slot < 0 && a.swaps < max_swaps) {
+                if ((rc = naiwa_cache_replace(cache, (int)e, protect.data(), (int)protect.size(), &slot))) return rc;
+                swap = slot >= 0;
+            }
+            if (slot < 0) continue;
+            void* dst[3];
+            const void* src[3];
+            slot_ptrs(slot, dst);
+            host_ptrs((int)e, src);
+            if ((rc = naiwa_upload_expert(dst, src, bytes, (int64_t)copy, fence, 0))) {
+                naiwa_cache_unreserve(cache, slot);
+                return rc;
+            }
+            if ((rc = naiwa_cache_publish(cache, slot))) return rc;
+            ++(swap ? a.swaps : a.loads);
+            a.pcie_bytes += (int64_t)(bytes[0] + bytes[1] + bytes[2]);
+        }
+        // the claim: recorded after the batch, before a reader can see it
+        if ((rc = naiwa_hip_rc(hipEventRecord(ahead_done, copy)))) return rc;
+        ahead_claimed = true;
+        naiwa_cache_stats s{};
+        s.lookahead_loads = (uint64_t)a.loads;
+        s.swaps = (uint64_t)a.swaps;
+        naiwa_stats_add(&s);
+        if (info) *info = a;
+        return NAIWA_OK;
+    }
 };
 
-extern "C" {
+namespace {
 
-int naiwa_cached_layer_create(const naiwa_cached_layer_desc* d, naiwa_ring* ring, int ring_len,
-                              int64_t copy_stream, naiwa_cached_layer** out) {
-    if (!d || !ring || !out || ring_len <= 0 || d->num_experts <= 0 || d->top_k <= 0 || d->usable < 0 ||
-        !d->router || !d->host_gate || !d->host_up || !d->host_down)
-        return NAIWA_E_INVALID;
-    const int need = d->usable + ring_len;
-    if (!bank_ok(d->gate, d->inter, d->hidden, need) || !bank_ok(d->up, d->inter, d->hidden, need) ||
-        !bank_ok(d->down, d->hidden, d->inter, need))
-        return NAIWA_E_INVALID;
-    naiwa_cached_layer* L = new (std::nothrow) naiwa_cached_layer;
-    if (!L) return NAIWA_E_NOMEM;
-    L->d = *d;
-    L->ring = ring;
-    L->ring_len = ring_len;
-    L->copy = (hipStream_t)copy_stream;
-    L->bytes[0] = (size_t)naiwa_projection_bytes(d->gate.dtype, d->inter, d->hidden);
-    L->bytes[1] = (size_t)naiwa_projection_bytes(d->up.dtype, d->inter, d->hidden);
-    L->bytes[2] = (size_t)naiwa_projection_bytes(d->down.dtype, d->hidden, d->inter);
-    int rc = naiwa_cache_create(d->num_experts, d->usable, d->usable, &L->cache);
-    if (rc) {
-        delete L;
-        return rc;
-    }
-    L->ring_fence.assign((size_t)ring_len, nullptr);
-    L->ring_fenced.assign((size_t)ring_len, 0);
-    for (auto& ev : L->ring_fence)
-        if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) rc = NAIWA_E_DEVICE;
-    if (hipEventCreateWithFlags(&L->staged_done, hipEventDisableTiming) != hipSuccess) rc = NAIWA_E_DEVICE;
-    if (!rc) rc = L->ensure_rows(8);
-    if (rc) {
-        naiwa_cached_layer_destroy(L);
-        return rc;
-    }
-    *out = L;
-    return NAIWA_OK;
-}
-
-int naiwa_cached_layer_destroy(naiwa_cached_layer* L) {
-    if (!L) return NAIWA_OK;
-    (void)hipDeviceSynchronize();
-    L->release_buffers();
-    for (auto ev : L->ring_fence)
-        if (ev) (void)hipEventDestroy(ev);
-    if (L->staged_done) (void)hipEventDestroy(L->staged_done);
-    naiwa_cache_destroy(L->cache);
-    delete L;
-    return NAIWA_OK;
-}
-
-int naiwa_cached_layer_cache(naiwa_cached_layer* L, naiwa_cache** out) {
-    if (!L || !out) return NAIWA_E_INVALID;
-    *out = L->cache;
-    return NAIWA_OK;
-}
-
-int naiwa_cached_layer_fill(naiwa_cached_layer* L, int expert, int* slot_out) {
-    if (!L || !slot_out) return NAIWA_E_INVALID;
-    int rc = naiwa_cache_admit(L->cache, expert, slot_out);
-    if (rc || *slot_out < 0) return rc;
-    void* dst[3];
-    const void* src[3];
-    L->slot_ptrs(*slot_out, dst);
-    L->host_ptrs(expert, src);
-    rc = naiwa_upload_expert(dst, src, L->bytes, (int64_t)L->copy, 0, 0);
-    if (!rc) rc = naiwa_hip_rc(hipStreamSynchronize(L->copy));
-    if (rc) {
-        naiwa_cache_unreserve(L->cache, *slot_out);
-        *slot_out = -1;
-        return rc;
-    }
-    return naiwa_cache_publish(L->cache, *slot_out);
-}
-
-int naiwa_cached_layer_forward(naiwa_cached_layer* L, const void* x, int rows, float* out, float pcie_frac,
-                               int promote_cap, uint64_t min_hits, int64_t stream, naiwa_cached_step* info) {
-    if (!L || !x || !out || rows <= 0) return NAIWA_E_INVALID;
+// One decode step of L; with `next`, also the next layer's lookahead on the same
+// activation: its router runs beside L's before the one routing read-back, and
+// its uploads are queued after L's expert kernel, so they overlap L's compute.
+int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_row, const void* x, int rows,
+                 float* out, float pcie_frac, int promote_cap, uint64_t min_hits, int64_t stream,
+                 naiwa_cached_step* info, naiwa_lookahead_step* ahead) {
+    if (!L || !x || !out || rows <= 0 || swaps_per_row < 0) return NAIWA_E_INVALID;
+    if (next && (next == L || next->d.hidden != L->d.hidden)) return NAIWA_E_INVALID;
     const naiwa_cached_layer_desc& d = L->d;
     const int k = d.top_k, n = rows * k;
     hipStream_t st = (hipStream_t)stream;
     int rc = L->ensure_rows(rows);
+    if (!rc && next) rc = next->ensure_rows(rows);
     if (rc) return rc;
     naiwa_cached_step step{};
 
     // route on the device, then read the top-k back (the routing round trip)
     rc = naiwa_router_topk_biased(x, NAIWA_BF16, d.router, d.router_bias, rows, d.hidden, d.num_experts, k, d.mode,
                                   L->ids_dev, L->w_dev, nullptr, stream);
+    if (!rc && next) rc = next->predict_launch(x, rows, stream);
     if (rc) return rc;
     if ((rc = naiwa_hip_rc(hipMemcpyAsync(L->ids_h, L->ids_dev, (size_t)n * 4, hipMemcpyDeviceToHost, st))) ||
         (rc = naiwa_hip_rc(hipMemcpyAsync(L->w_h, L->w_dev, (size_t)n * 4, hipMemcpyDeviceToHost, st))) ||
@@ -218,9 +249,14 @@ int naiwa_cached_layer_forward(naiwa_cached_layer* L, const void* x, int rows, f
             return rc;
     }
 
-    // the expert kernel over cache + ring slots
+    // the expert kernel over cache + ring slots, after the latest lookahead claim
+    // (src/moe/cached_layer.rs:808-819): a slot it published may still be in flight
     if ((rc = naiwa_hip_rc(hipMemcpyAsync(L->slots_dev, L->slots_up, (size_t)n * 4, hipMemcpyHostToDevice, st))))
         return rc;
+    if (L->ahead_claimed) {
+        if ((rc = naiwa_hip_rc(hipStreamWaitEvent(st, L->ahead_done, 0)))) return rc;
+        ++step.preload_waits;
+    }
     if ((rc = naiwa_moe_decode(&d.gate, &d.up, &d.down, x, NAIWA_BF16, L->slots_dev, L->w_dev, rows, k, d.act, out,
                                stream)))
         return rc;
@@ -255,15 +291,132 @@ int naiwa_cached_layer_forward(naiwa_cached_layer* L, const void* x, int rows, f
         }
     }
 
+    // every read of this layer's cache slots is before this point on `stream`
+    if ((rc = naiwa_hip_rc(hipEventRecord(L->read_done, st)))) return rc;
+    L->read_recorded = true;
+
     naiwa_cache_stats s{};
     s.hits = (uint64_t)step.hits;
     s.staged = (uint64_t)step.staged;
     s.pcie_misses = (uint64_t)nc;
     s.pcie_bytes = (uint64_t)step.pcie_bytes;
     s.promotions = (uint64_t)step.promoted;
-    s.sync_waits = nc ? 1 : 0;
+    s.sync_waits = (uint64_t)((nc ? 1 : 0) + step.preload_waits);
     naiwa_stats_add(&s);
     if (info) *info = step;
+    if (next) return next->prefetch_apply(swaps_per_row, ahead);
+    return NAIWA_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+int naiwa_cached_layer_create(const naiwa_cached_layer_desc* d, naiwa_ring* ring, int ring_len,
+                              int64_t copy_stream, naiwa_cached_layer** out) {
+    if (!d || !ring || !out || ring_len <= 0 || d->num_experts <= 0 || d->top_k <= 0 || d->usable < 0 ||
+        !d->router || !d->host_gate || !d->host_up || !d->host_down)
+        return NAIWA_E_INVALID;
+    const int need = d->usable + ring_len;
+    if (!bank_ok(d->gate, d->inter, d->hidden, need) || !bank_ok(d->up, d->inter, d->hidden, need) ||
+        !bank_ok(d->down, d->hidden, d->inter, need))
+        return NAIWA_E_INVALID;
+    naiwa_cached_layer* L = new (std::nothrow) naiwa_cached_layer;
+    if (!L) return NAIWA_E_NOMEM;
+    L->d = *d;
+    L->ring = ring;
+    L->ring_len = ring_len;
+    L->copy = (hipStream_t)copy_stream;
+    L->bytes[0] = (size_t)naiwa_projection_bytes(d->gate.dtype, d->inter, d->hidden);
+    L->bytes[1] = (size_t)naiwa_projection_bytes(d->up.dtype, d->inter, d->hidden);
+    L->bytes[2] = (size_t)naiwa_projection_bytes(d->down.dtype, d->hidden, d->inter);
+    int rc = naiwa_cache_create(d->num_experts, d->usable, d->usable, &L->cache);
+    if (rc) {
+        delete L;
+        return rc;
+    }
+    L->ring_fence.assign((size_t)ring_len, nullptr);
+    L->ring_fenced.assign((size_t)ring_len, 0);
+    for (auto& ev : L->ring_fence)
+        if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) rc = NAIWA_E_DEVICE;
+    for (hipEvent_t* ev : {&L->staged_done, &L->read_done, &L->ahead_done})
+        if (hipEventCreateWithFlags(ev, hipEventDisableTiming) != hipSuccess) rc = NAIWA_E_DEVICE;
+    if (!rc) rc = L->ensure_rows(8);
+    if (rc) {
+        naiwa_cached_layer_destroy(L);
+        return rc;
+    }
+    *out = L;
+    return NAIWA_OK;
+}
+
+int naiwa_cached_layer_destroy(naiwa_cached_layer* L) {
+    if (!L) return NAIWA_OK;
+    (void)hipDeviceSynchronize();
+    L->release_buffers();
+    for (auto ev : L->ring_fence)
+        if (ev) (void)hipEventDestroy(ev);
+    for (hipEvent_t ev : {L->staged_done, L->read_done, L->ahead_done})
+        if (ev) (void)hipEventDestroy(ev);
+    naiwa_cache_destroy(L->cache);
+    delete L;
+    return NAIWA_OK;
+}
+
+int naiwa_cached_layer_cache(naiwa_cached_layer* L, naiwa_cache** out) {
+    if (!L || !out) return NAIWA_E_INVALID;
+    *out = L->cache;
+    return NAIWA_OK;
+}
+
+int naiwa_cached_layer_fill(naiwa_cached_layer* L, int expert, int* slot_out) {
+    if (!L || !slot_out) return NAIWA_E_INVALID;
+    int rc = naiwa_cache_admit(L->cache, expert, slot_out);
+    if (rc || *slot_out < 0) return rc;
+    void* dst[3];
+    const void* src[3];
+    L->slot_ptrs(*slot_out, dst);
+    L->host_ptrs(expert, src);
+    rc = naiwa_upload_expert(dst, src, L->bytes, (int64_t)L->copy, 0, 0);
+    if (!rc) rc = naiwa_hip_rc(hipStreamSynchronize(L->copy));
+    if (rc) {
+        naiwa_cache_unreserve(L->cache, *slot_out);
+        *slot_out = -1;
+        return rc;
+    }
+    return naiwa_cache_publish(L->cache, *slot_out);
+}
+
+int naiwa_cached_layer_forward(naiwa_cached_layer* L, const void* x, int rows, float* out, float pcie_frac,
+                               int promote_cap, uint64_t min_hits, int64_t stream, naiwa_cached_step* info) {
+    return forward_impl(L, nullptr, 0, x, rows, out, pcie_frac, promote_cap, min_hits, stream, info, nullptr);
+}
+
+int naiwa_cached_layer_forward_ahead(naiwa_cached_layer* L, naiwa_cached_layer* next, int lookahead_swaps,
+                                     const void* x, int rows, float* out, float pcie_frac, int promote_cap,
+                                     uint64_t min_hits, int64_t stream, naiwa_cached_step* info,
+                                     naiwa_lookahead_step* ahead) {
+    if (!next) return NAIWA_E_INVALID;
+    return forward_impl(L, next, lookahead_swaps, x, rows, out, pcie_frac, promote_cap, min_hits, stream, info,
+                        ahead);
+}
+
+int naiwa_cached_layer_prefetch(naiwa_cached_layer* next, const void* x, int rows, int lookahead_swaps,
+                                int64_t stream, naiwa_lookahead_step* info) {
+    if (!next || !x || rows <= 0 || lookahead_swaps < 0) return NAIWA_E_INVALID;
+    int rc = next->ensure_rows(rows);
+    if (!rc) rc = next->predict_launch(x, rows, stream);
+    if (!rc) rc = naiwa_hip_rc(hipStreamSynchronize((hipStream_t)stream));
+    if (rc) return rc;
+    return next->prefetch_apply(lookahead_swaps, info);
+}
+
+int naiwa_cached_layer_predicted(const naiwa_cached_layer* L, uint32_t* ids, int capacity, int* n_out) {
+    if (!L || !n_out || (capacity > 0 && !ids)) return NAIWA_E_INVALID;
+    const int n = (int)L->predicted.size();
+    if (capacity < n) return NAIWA_E_INVALID;
+    for (int i = 0; i < n; ++i) ids[i] = L->predicted[(size_t)i];
+    *n_out = n;
     return NAIWA_OK;
 }
 

@@ -66,7 +66,14 @@ RESULT_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(C.c_float), C.c_int)
 class CachedStep(C.Structure):
     """naiwa_cached_step (include/naiwa_cached.h)."""
     _fields_ = [("hits", C.c_int), ("staged", C.c_int), ("staged_experts", C.c_int), ("promoted", C.c_int),
+                ("pcie_bytes", C.c_int64), ("preload_waits", C.c_int)]
+
+
+class LookaheadStep(C.Structure):
+    """naiwa_lookahead_step (include/naiwa_cached.h)."""
+    _fields_ = [("predicted", C.c_int), ("resident", C.c_int), ("loads", C.c_int), ("swaps", C.c_int),
                 ("pcie_bytes", C.c_int64)]
+
 
 STATS_FIELDS = ("hits", "promotions", "misses", "staged", "lookahead_loads", "swaps", "lookahead_dropped",
                 "sync_waits", "pcie_misses", "pcie_bytes", "result_stalls")
@@ -168,6 +175,10 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_cached_layer_fill": (i32, [vp, i32, _P(i32)]),
     "naiwa_cached_layer_forward": (i32, [vp, vp, i32, vp, f32, i32, u64, i64, _P(CachedStep)]),
     "naiwa_cached_layer_routing": (i32, [vp, vp, vp, i32]),
+    "naiwa_cached_layer_forward_ahead": (i32, [vp, vp, i32, vp, i32, vp, f32, i32, u64, i64, _P(CachedStep),
+                                               _P(LookaheadStep)]),
+    "naiwa_cached_layer_prefetch": (i32, [vp, vp, i32, i32, i64, _P(LookaheadStep)]),
+    "naiwa_cached_layer_predicted": (i32, [vp, vp, i32, _P(i32)]),
     # include/naiwa_policy.h (host only)
     "naiwa_cache_create": (i32, [i32, i32, i32, _P(vp)]),
     "naiwa_cache_destroy": (i32, [vp]),

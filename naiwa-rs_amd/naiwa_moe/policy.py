@@ -12,7 +12,8 @@ import ctypes as C
 
 import numpy as np
 
-from ._lib import (STAGING_RING_FIRST, STATS_FIELDS, CacheStats, CachedLayerDesc, CachedStep, check, lib)
+from ._lib import (STAGING_RING_FIRST, STATS_FIELDS, CacheStats, CachedLayerDesc, CachedStep, LookaheadStep, check,
+                   lib)
 
 
 def _u32(a) -> np.ndarray:
@@ -197,6 +198,32 @@ class CachedLayer:
         check(lib().naiwa_cached_layer_forward(self._h, _dev(x), rows, _dev(out), pcie_frac, promote_cap, min_hits,
                                                stream, C.byref(info)), "cached_layer_forward")
         return {f: getattr(info, f) for f, _ in CachedStep._fields_}
+
+    def forward_ahead(self, next_layer: "CachedLayer", x, rows: int, out, lookahead_swaps: int = 2,
+                      pcie_frac: float = 1.0, promote_cap: int = 1, min_hits: int = 4,
+                      stream: int = 0) -> tuple[dict, dict]:
+        """forward, plus next_layer's lookahead on the same x (one routing read-back)."""
+        from .ops import _dev
+        info, ahead = CachedStep(), LookaheadStep()
+        check(lib().naiwa_cached_layer_forward_ahead(self._h, next_layer._h, lookahead_swaps, _dev(x), rows, _dev(out),
+                                                     pcie_frac, promote_cap, min_hits, stream, C.byref(info),
+                                                     C.byref(ahead)), "cached_layer_forward_ahead")
+        return ({f: getattr(info, f) for f, _ in CachedStep._fields_},
+                {f: getattr(ahead, f) for f, _ in LookaheadStep._fields_})
+
+    def prefetch_predicted(self, x, rows: int, lookahead_swaps: int = 2, stream: int = 0) -> dict:
+        """This layer's lookahead on the previous layer's activation x."""
+        from .ops import _dev
+        ahead = LookaheadStep()
+        check(lib().naiwa_cached_layer_prefetch(self._h, _dev(x), rows, lookahead_swaps, stream, C.byref(ahead)),
+              "cached_layer_prefetch")
+        return {f: getattr(ahead, f) for f, _ in LookaheadStep._fields_}
+
+    def predicted(self) -> list[int]:
+        out = np.empty(max(self.cache.num_experts, 1), dtype=np.uint32)
+        n = C.c_int()
+        check(lib().naiwa_cached_layer_predicted(self._h, _ptr(out), out.size, C.byref(n)), "cached_layer_predicted")
+        return [int(v) for v in out[:n.value]]
 
     def routing(self, rows: int) -> tuple[np.ndarray, np.ndarray]:
         ids = np.empty((rows, self.top_k), dtype=np.uint32)

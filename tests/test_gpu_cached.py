@@ -1,8 +1,10 @@
 """GPU parity of the partial-cache decode step (include/naiwa_cached.h): device
 routing with a per-expert bias is bit-exact with the oracle, the hit/miss split
 and staging follow the host policy, staged experts are uploaded byte-exactly into
-their ring slots, promotion moves them into the cache, and every step's expert
-output is within the 1e-2 relative bar of the oracle over the same routed set."""
+their ring slots, promotion moves them into the cache, the lookahead loads the
+next layer's predicted experts by the reference's admit/replace rules, and every
+step's expert output is within the 1e-2 relative bar of the oracle over the same
+routed set."""
 import numpy as np
 import pytest
 
@@ -114,3 +116,121 @@ def test_staged_bytes_land_in_their_ring_slot(gpu):
         for proj, bank in enumerate((banks.gate, banks.up, banks.down)):
             got = bank.buffer.download(np.uint8, count=bank.expert_bytes, offset=(usable + pos) * bank.stride)
             assert np.array_equal(got, stacks.view(proj)[e])
+
+
+class SlotModel:
+    """The reference's residency rules for a cache with no promotions
+    (src/moe/stages/route.rs:19-158, src/moe/cached_layer.rs:401-410, 1056-1101):
+    route bumps the tick and touches hits; admit takes the first empty slot;
+    replace takes the resident with the smallest (last_use, expert) outside the
+    protected set; a loaded slot is published with last_use = tick."""
+
+    def __init__(self, usable: int):
+        self.expert = [None] * usable
+        self.last = [0] * usable
+        self.tick = 0
+
+    def resident(self, e):
+        return e in self.expert
+
+    def route(self, ids):
+        self.tick += 1
+        hits = 0
+        for e in ids:
+            if e in self.expert:
+                self.last[self.expert.index(e)] = self.tick
+                hits += 1
+        return hits
+
+    def admit(self, e):
+        if e in self.expert or None not in self.expert:
+            return False
+        s = self.expert.index(None)
+        self.expert[s], self.last[s] = e, self.tick
+        return True
+
+    def replace(self, e, protect):
+        if e in self.expert:
+            return False
+        cands = [(self.last[s], x, s) for s, x in enumerate(self.expert) if x is not None and x not in protect]
+        if not cands:
+            return False
+        _, _, s = min(cands)
+        self.expert[s], self.last[s] = e, self.tick
+        return True
+
+    def prefetch(self, predicted, max_swaps):
+        loads = swaps = 0
+        for e in predicted:
+            if self.admit(e):
+                loads += 1
+            elif swaps < max_swaps and self.replace(e, predicted):
+                swaps += 1
+        return loads, swaps
+
+
+@pytest.mark.parametrize("fused,rows", [(True, 1), (False, 1), (True, 3)])
+def test_lookahead_loads_the_next_layers_prediction(gpu, fused, rows):
+    """Layer 1's experts are predicted from layer 0's activation with layer 1's
+    router (its logits, bias included), merged by votes, loaded into empty slots or swapped
+    over LRU residents (lookahead_swaps * rows at most), and layer 1's next
+    step reads them as hits after waiting for the claim; its output stays
+    within the bar of the oracle."""
+    nm = gpu
+    E, H, I, k, swaps_per_row = 16, 256, 256, 4, 2
+    usable1 = 6
+    copy, stream = nm.Stream(), nm.Stream()
+    ring = nm.policy.StagingRing()
+    l0, _, _, host0 = make_layer(nm, 1500, E, H, I, k, E, ring, copy)
+    l1, banks1, stacks1, host1 = make_layer(nm, 1501, E, H, I, k, usable1, ring, copy, bias_scale=0.5)
+    for e in range(E):
+        assert l0.fill(e) == e
+    model = SlotModel(usable1)
+    out0, out1 = nm.DeviceBuffer(rows * H * 4), nm.DeviceBuffer(rows * H * 4)
+    nm.policy.stats(reset=True)
+    loads = swaps = 0
+    for step in range(6):
+        print(f"[lookahead fused={fused} rows={rows} step {step}]", flush=True)
+        x = S.activations_bf16(1600 + step, rows, H)
+        xd = nm.DeviceBuffer.from_array(x)
+        if fused:
+            info0, ahead = l0.forward_ahead(l1, xd, rows, out0, lookahead_swaps=swaps_per_row, promote_cap=0,
+                                            stream=stream.handle)
+            assert info0["hits"] == rows * k
+        else:
+            ahead = l1.prefetch_predicted(xd, rows, lookahead_swaps=swaps_per_row, stream=stream.handle)
+        g, u, d, r, bias, dt, _ = host1
+        logits = (O.router_logits(O.from_bf16(x), r) + bias).astype(np.float32)
+        want_pred = nm.policy.union_by_votes([nm.policy.top_k_ids(row, k) for row in logits])
+        assert l1.predicted() == want_pred
+        resident = sum(model.resident(e) for e in want_pred)
+        want_loads, want_swaps = model.prefetch(want_pred, swaps_per_row * rows)
+        assert (ahead["predicted"], ahead["resident"], ahead["loads"], ahead["swaps"]) == \
+            (len(want_pred), resident, want_loads, want_swaps), (step, ahead)
+        assert ahead["pcie_bytes"] == (want_loads + want_swaps) * sum(stacks1.expert_bytes)
+        loads, swaps = loads + want_loads, swaps + want_swaps
+        # layer 1 runs on the same activation: its routing is the prediction
+        info1 = l1.forward(xd, rows, out1, pcie_frac=1.0, promote_cap=0, stream=stream.handle)
+        stream.sync()
+        ids, _ = l1.routing(rows)
+        assert info1["hits"] == model.route(ids.reshape(-1).tolist())
+        assert info1["preload_waits"] == 1
+        want_ids, _, want = oracle_step(host1, x, E, k, H)
+        assert np.array_equal(ids, want_ids)
+        err = S.max_rel_err(out1.download(np.float32).reshape(rows, H), want)
+        print(f"  ahead={ahead} hits={info1['hits']} err={err:.3e}", flush=True)
+        assert err < TOL
+        if fused:
+            _, _, want0 = oracle_step(host0, x, E, k, H)
+            assert S.max_rel_err(out0.download(np.float32).reshape(rows, H), want0) < TOL
+    assert swaps > 0 and loads == usable1
+    st = nm.policy.stats()
+    assert st["lookahead_loads"] == loads and st["swaps"] == swaps
+    # the slots hold the experts the policy says, byte for byte
+    table = l1.cache.slot_table()
+    assert sorted(int(e) for e in np.nonzero(table >= 0)[0]) == sorted(model.expert)
+    for e in np.nonzero(table >= 0)[0]:
+        s = int(table[e])
+        for proj, bank in enumerate((banks1.gate, banks1.up, banks1.down)):
+            got = bank.buffer.download(np.uint8, count=bank.expert_bytes, offset=s * bank.stride)
+            assert np.array_equal(got, stacks1.view(proj)[e]), (e, s, proj)
