@@ -375,7 +375,8 @@ def run_cache25(args) -> int:
     step (include/naiwa_cached.h): device routing, top-k read-back, the host policy's
     hit/miss split, misses streamed from pinned host stacks into the 16-slot staging ring
     (pcie_frac 1), the expert kernel over cache + ring slots, one promotion per layer per
-    step (min 4 sightings).  Caches start with each layer's 32 most popular experts."""
+    step (min 4 sightings).  Caches start with each layer's 32 most popular experts, seeded from an
+    expert profile (include/naiwa_policy.h) written from the bias ranks."""
     import naiwa_moe as nm
 
     if nm.device_count() < 1:
@@ -390,7 +391,7 @@ def run_cache25(args) -> int:
     ring = nm.policy.StagingRing()
     proj = I * (H // Q4K_BLOCK) * Q4K_BYTES
     tmp = nm.DeviceBuffer(E * proj)
-    layers, keep = [], []
+    layers, keep, ranking = [], [], []
     for l in range(L):
         stacks = nm.HostExpertStacks(E, H, I, dt)
         for t in range(3):
@@ -407,13 +408,19 @@ def run_cache25(args) -> int:
         banks = nm.LayerBanks(usable + ring.length, H, I, dt)
         layer = nm.policy.CachedLayer(router, banks, stacks, E, K, usable, ring, copy.handle,
                                       mode=nm.ROUTE_SOFTMAX_TOPK_RENORM, router_bias=bias_d)
-        for e in np.argsort(ranks)[:usable]:
-            layer.fill(int(e))
+        ranking += [(l, int(e)) for e in np.argsort(ranks)]
         layers.append(layer)
         keep += [stacks, router, bias_d, banks]
     del tmp
+    # the caches start hot from an expert profile: each layer's experts by popularity
+    import tempfile
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "profile.bin")
+        nm.policy.write_profile(path, ranking, L, E, slots=L * usable)
+        profile = nm.policy.ExpertProfile(path, L, E)
+    seeded = sum(layer.seed(profile.layer(l)) for l, layer in enumerate(layers))
     log(f"cache25: {L} layers, {usable}/{E} cached + {ring.length} ring slots, pinned host stacks "
-        f"{L * 3 * E * proj / 1e9:.1f} GB, set-up {time.time() - t0:.1f}s")
+        f"{L * 3 * E * proj / 1e9:.1f} GB, {seeded} slots seeded from {profile.source}, set-up {time.time() - t0:.1f}s")
     xs = nm.DeviceBuffer((warmup + steps) * rows * H * 2)
     nm.synth(nm.BF16, 999, (warmup + steps) * rows * H, xs, 0.0, 1.0, stream=compute.handle)
     x = nm.DeviceBuffer(rows * H * 2)

@@ -74,6 +74,15 @@ int naiwa_cached_layer_cache(naiwa_cached_layer* L, naiwa_cache** out);
  * the copy is done (synchronous).  *slot_out = -1 when not admitted. */
 int naiwa_cached_layer_fill(naiwa_cached_layer* L, int expert, int* slot_out);
 
+/* Profile seeding before the first token (src/moe/provider.rs:214-256): the
+ * first round(usable * fill_share) experts of `experts` (one layer's profile
+ * ranking, best first; fill_share is the reference's NAIWA_PROFILE_FILL,
+ * 1 by default) are admitted in order -- an expert already resident, one
+ * past the model, or one that finds no empty slot uses its place in the
+ * budget and is skipped -- uploaded on the copy stream, and published after
+ * one synchronisation.  *filled = experts placed. */
+int naiwa_cached_layer_seed(naiwa_cached_layer* L, const uint32_t* experts, int n, float fill_share, int* filled);
+
 /* One decode step: x bf16 [rows, H] -> out f32 [rows, H], all on `stream`
  * except the routing read-back, which synchronises it (the reference's
  * top-k round trip).  pcie_frac, promote_cap and min_hits are the

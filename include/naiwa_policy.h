@@ -19,6 +19,7 @@
  *   naiwa_ring_*            StagingRing            src/moe/staging.rs:23-120
  *   naiwa_cache_stage       stage_misses selection src/moe/stages/dma_miss.rs:58-202
  *   naiwa_stats_*           CacheStats             src/stats/cache.rs:7-33
+ *   naiwa_profile_*         Profile                src/moe/profile.rs:50-112
  *
  * Return values: NAIWA_OK (0) or a negative NAIWA_E_* code (naiwa_moe.h).
  * A cache object is not thread-safe by itself; the reference serialises the
@@ -128,6 +129,22 @@ int naiwa_ring_acquire(naiwa_ring* r, int n, int* start);
  * it there before any kernel reads the step. */
 int naiwa_cache_stage(naiwa_ring* r, const uint32_t* ids, const float* w, int rows, int k, float frac,
                       int32_t* slot_io, uint32_t* chosen_out, int32_t* pos_out, int* n_chosen);
+
+/* The expert-cache profile (src/moe/profile.rs:50-112): a file of (layer,
+ * expert) pairs ranked best first ("STRP", u32 version 1, layers, experts,
+ * slots, n, then n u16 pairs; the trailing rank table is not read).  Each
+ * layer keeps its own pairs in rank order; pairs with layer >= num_layers or
+ * expert >= num_experts are dropped, and a repeated pair is kept once.
+ * Errors: NAIWA_E_IO (cannot open), NAIWA_E_FORMAT (no magic / shorter than
+ * its header, or a truncated ranking), NAIWA_E_UNSUPPORTED (version != 1). */
+typedef struct naiwa_profile naiwa_profile;
+int naiwa_profile_read(const char* path, int num_layers, int num_experts, naiwa_profile** out);
+int naiwa_profile_destroy(naiwa_profile* p);
+/* This layer's experts, best first (a layer the profile lacks: none). */
+int naiwa_profile_layer(const naiwa_profile* p, int layer, uint32_t* experts, int capacity, int* n_out);
+/* Pairs kept after the filter, and the file's own header sizes (any may be null). */
+int naiwa_profile_info(const naiwa_profile* p, int* pairs, uint32_t* file_layers, uint32_t* file_experts,
+                       uint32_t* file_pairs);
 
 /* CacheStats (src/stats/cache.rs:7-33), process-wide. */
 typedef struct naiwa_cache_stats {

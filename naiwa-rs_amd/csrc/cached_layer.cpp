@@ -6,6 +6,7 @@
 // (src/moe/cached_layer.rs:1236-1300, src/moe/stages/preload.rs:18-111).
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <initializer_list>
 #include <new>
 #include <vector>
@@ -385,6 +386,36 @@ int naiwa_cached_layer_fill(naiwa_cached_layer* L, int expert, int* slot_out) {
         return rc;
     }
     return naiwa_cache_publish(L->cache, *slot_out);
+}
+
+int naiwa_cached_layer_seed(naiwa_cached_layer* L, const uint32_t* experts, int n, float fill_share, int* filled) {
+    if (!L || !filled || n < 0 || (n > 0 && !experts) || !(fill_share >= 0.0f && fill_share <= 1.0f))
+        return NAIWA_E_INVALID;
+    *filled = 0;
+    const int budget = (int)std::llround((double)L->d.usable * (double)fill_share);
+    std::vector<int> slots;
+    int rc = NAIWA_OK;
+    for (int i = 0; i < n && i < budget && !rc; ++i) {
+        if (experts[i] >= (uint32_t)L->d.num_experts) continue; // not in this model: skipped
+        int slot = -1;
+        if ((rc = naiwa_cache_admit(L->cache, (int)experts[i], &slot)) || slot < 0) continue;
+        void* dst[3];
+        const void* src[3];
+        L->slot_ptrs(slot, dst);
+        L->host_ptrs((int)experts[i], src);
+        rc = naiwa_upload_expert(dst, src, L->bytes, (int64_t)L->copy, 0, 0);
+        slots.push_back(slot);
+    }
+    if (!rc) rc = naiwa_hip_rc(hipStreamSynchronize(L->copy));
+    for (int slot : slots) {
+        if (rc) {
+            naiwa_cache_unreserve(L->cache, slot);
+        } else {
+            if ((rc = naiwa_cache_publish(L->cache, slot))) return rc;
+            ++*filled;
+        }
+    }
+    return rc;
 }
 
 int naiwa_cached_layer_forward(naiwa_cached_layer* L, const void* x, int rows, float* out, float pcie_frac,

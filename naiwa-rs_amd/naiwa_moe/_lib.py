@@ -173,6 +173,7 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_cached_layer_destroy": (i32, [vp]),
     "naiwa_cached_layer_cache": (i32, [vp, _P(vp)]),
     "naiwa_cached_layer_fill": (i32, [vp, i32, _P(i32)]),
+    "naiwa_cached_layer_seed": (i32, [vp, vp, i32, f32, _P(i32)]),
     "naiwa_cached_layer_forward": (i32, [vp, vp, i32, vp, f32, i32, u64, i64, _P(CachedStep)]),
     "naiwa_cached_layer_routing": (i32, [vp, vp, vp, i32]),
     "naiwa_cached_layer_forward_ahead": (i32, [vp, vp, i32, vp, i32, vp, f32, i32, u64, i64, _P(CachedStep),
@@ -207,6 +208,10 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_stats_read": (i32, [vp, i32]),
     "naiwa_stats_add": (i32, [vp]),
     # include/naiwa_gguf.h
+    "naiwa_profile_read": (i32, [C.c_char_p, i32, i32, _P(vp)]),
+    "naiwa_profile_destroy": (i32, [vp]),
+    "naiwa_profile_layer": (i32, [vp, i32, vp, i32, _P(i32)]),
+    "naiwa_profile_info": (i32, [vp, _P(i32), _P(C.c_uint32), _P(C.c_uint32), _P(C.c_uint32)]),
     "naiwa_gguf_open": (i32, [C.c_char_p, _P(vp)]),
     "naiwa_gguf_close": (i32, [vp]),
     "naiwa_gguf_version": (i32, [vp, _P(u32)]),

@@ -191,6 +191,13 @@ class CachedLayer:
         check(lib().naiwa_cached_layer_fill(self._h, expert, C.byref(s)), "cached_layer_fill")
         return s.value if s.value >= 0 else None
 
+    def seed(self, experts, fill_share: float = 1.0) -> int:
+        """Profile seeding: the first round(usable * fill_share) ranked experts, admitted in order."""
+        e = _u32(list(experts))
+        n = C.c_int()
+        check(lib().naiwa_cached_layer_seed(self._h, _ptr(e), e.size, fill_share, C.byref(n)), "cached_layer_seed")
+        return n.value
+
     def forward(self, x, rows: int, out, pcie_frac: float = 1.0, promote_cap: int = 1, min_hits: int = 4,
                 stream: int = 0) -> dict:
         from .ops import _dev
@@ -230,6 +237,55 @@ class CachedLayer:
         w = np.empty((rows, self.top_k), dtype=np.float32)
         check(lib().naiwa_cached_layer_routing(self._h, _ptr(ids), _ptr(w), ids.size), "cached_layer_routing")
         return ids, w
+
+
+class ExpertProfile:
+    """The expert-cache profile (src/moe/profile.rs): per layer, its experts best first."""
+
+    # the reference reads with generous bounds and filters to the model (src/load.rs:25-29)
+    LAYERS, EXPERTS = 128, 1024
+
+    def __init__(self, path, num_layers: int = LAYERS, num_experts: int = EXPERTS):
+        h = C.c_void_p()
+        check(lib().naiwa_profile_read(str(path).encode(), num_layers, num_experts, C.byref(h)), "profile_read")
+        self._h, self.num_experts = h, num_experts
+        pairs = C.c_int()
+        fl, fe, fp = C.c_uint32(), C.c_uint32(), C.c_uint32()
+        check(lib().naiwa_profile_info(h, C.byref(pairs), C.byref(fl), C.byref(fe), C.byref(fp)), "profile_info")
+        self.pairs = pairs.value
+        self.source = f"{path} ({fl.value}x{fe.value}, {fp.value} ranked pairs)"
+
+    def __del__(self):
+        if getattr(self, "_h", None) and self._h.value:
+            lib().naiwa_profile_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def layer(self, layer: int) -> list[int]:
+        out = np.empty(max(self.num_experts, 1), dtype=np.uint32)
+        n = C.c_int()
+        check(lib().naiwa_profile_layer(self._h, layer, _ptr(out), out.size, C.byref(n)), "profile_layer")
+        return [int(v) for v in out[:n.value]]
+
+
+def write_profile(path, pairs, layers: int, experts: int, slots: int | None = None) -> None:
+    """Write a profile file: the ranking (layer, expert) best first, then the rank table."""
+    import struct
+    n = len(pairs)
+    out = bytearray(b"STRP" + struct.pack("<5I", 1, layers, experts, n if slots is None else slots, n))
+    for l, e in pairs:
+        out += struct.pack("<HH", l, e)
+    table = np.full((layers, experts), -1, dtype="<i4")
+    for r, (l, e) in enumerate(pairs):
+        if l < layers and e < experts and table[l, e] < 0:
+            table[l, e] = r
+    out += table.tobytes()
+    with open(path, "wb") as f:
+        f.write(bytes(out))
+
+
+def hit_rate(s: dict) -> float:
+    """CacheStats::hit_rate (src/stats/cache.rs:121-124): hits / (hits + misses)."""
+    return s["hits"] / max(s["hits"] + s["misses"], 1)
 
 
 def staging_ring_slots() -> int:
@@ -278,5 +334,5 @@ def stats_add(**delta: int) -> None:
     check(lib().naiwa_stats_add(C.byref(s)), "stats_add")
 
 
-__all__ = ["ExpertCache", "StagingRing", "CachedLayer", "STAGING_RING_FIRST", "staging_ring_slots", "top_k_ids",
-           "union_by_votes", "streamed_misses", "stats", "stats_add"]
+__all__ = ["ExpertCache", "StagingRing", "CachedLayer", "ExpertProfile", "STAGING_RING_FIRST", "staging_ring_slots",
+           "top_k_ids", "union_by_votes", "streamed_misses", "stats", "stats_add", "hit_rate", "write_profile"]

@@ -234,3 +234,42 @@ def test_lookahead_loads_the_next_layers_prediction(gpu, fused, rows):
         for proj, bank in enumerate((banks1.gate, banks1.up, banks1.down)):
             got = bank.buffer.download(np.uint8, count=bank.expert_bytes, offset=s * bank.stride)
             assert np.array_equal(got, stacks1.view(proj)[e]), (e, s, proj)
+
+
+def test_profile_seeds_the_cache(gpu, tmp_path):
+    """Seeding from an expert profile (src/moe/provider.rs:214-256): each layer
+    takes the first round(usable * fill_share) experts of its ranking in order,
+    a resident or out-of-model expert using its place; the seeded slots hold the
+    experts' bytes and a step over them matches the oracle."""
+    nm = gpu
+    from naiwa_moe.policy import ExpertProfile, write_profile
+    E, H, I, k, usable, rows = 16, 256, 256, 4, 6, 1
+    ranking = [5, 9, 5, 20, 3, 1, 14, 8, 2]
+    path = tmp_path / "profile.bin"
+    write_profile(path, [(0, e) for e in ranking] + [(1, 7)], 2, 32)
+    prof = ExpertProfile(path)
+    assert prof.layer(0) == [5, 9, 20, 3, 1, 14, 8, 2]
+    copy, stream = nm.Stream(), nm.Stream()
+    ring = nm.policy.StagingRing()
+    layer, banks, stacks, host = make_layer(nm, 1700, E, H, I, k, usable, ring, copy)
+    assert layer.fill(3) == 0
+    print("[profile] seeding", flush=True)
+    assert layer.seed(prof.layer(0)) == 4   # 5, 9, 1, 14 (20: not in the model, 3: resident)
+    table = layer.cache.slot_table()
+    assert {e: int(table[e]) for e in np.nonzero(table >= 0)[0]} == {3: 0, 5: 1, 9: 2, 1: 3, 14: 4}
+    for e, s in ((5, 1), (9, 2), (1, 3), (14, 4)):
+        for proj, bank in enumerate((banks.gate, banks.up, banks.down)):
+            got = bank.buffer.download(np.uint8, count=bank.expert_bytes, offset=s * bank.stride)
+            assert np.array_equal(got, stacks.view(proj)[e]), (e, s, proj)
+    out = nm.DeviceBuffer(rows * H * 4)
+    x = S.activations_bf16(1701, rows, H)
+    xd = nm.DeviceBuffer.from_array(x)
+    layer.forward(xd, rows, out, pcie_frac=1.0, promote_cap=0, stream=stream.handle)
+    stream.sync()
+    _, _, want = oracle_step(host, x, E, k, H)
+    assert S.max_rel_err(out.download(np.float32).reshape(rows, H), want) < TOL
+    # half the slots: the first 3 of the ranking (20 is skipped, so 2 placed)
+    layer2, _, _, _ = make_layer(nm, 1702, E, H, I, k, usable, ring, copy)
+    assert layer2.seed(prof.layer(0), fill_share=0.5) == 2
+    t2 = layer2.cache.slot_table()
+    assert int(t2[5]) == 0 and int(t2[9]) == 1 and int((t2 >= 0).sum()) == 2
