@@ -3,42 +3,93 @@
 // MoEExperts::forward called from src/prefill_stream.rs:2080-2102.
 //
 //   1. gather:   (token, k) pairs sorted by slot (stable), offsets per slot;
-//   2. tiles:    the sorted pairs cut into tiles of 32 pairs of one slot;
-//   3. gate/up:  per (tile, 128 intermediate features): x rows [32, H] times the
-//                slot's gate and up rows, K-steps of 128 dequantised to bf16 in
-//                LDS, v_mfma_f32_32x32x16_bf16 with f32 accumulation; the
-//                epilogue writes h = act(gate) * up as bf16;
-//   4. down:     per (tile, 128 output features): h rows [32, I] times the down
-//                rows, the epilogue scales by the pair's routing weight and
-//                writes the pair's f32 output row;
-//   5. combine:  out[t] = sum over j ascending of the pair outputs (no atomics).
+//   2. tiles:    the sorted pairs cut into tiles of 64 pairs of one slot;
+//   3. prep:     x (bf16) converted once to f16 and laid out in the K order of
+//                the gate/up weight format (below);
+//   4. gate/up:  per (tile, 128 intermediate features): 64 x rows times the
+//                slot's gate and up rows with v_mfma_f32_32x32x16_f16; every
+//                lane dequantises its own weight values to f16 in registers,
+//                straight into the MFMA B operand; the epilogue writes
+//                h = act(gate) * up as f16 in the K order of the down format;
+//   5. down:     per (tile, 128 output features): h rows times the down rows,
+//                scaled by the pair's routing weight into the pair's f32 row;
+//   6. combine:  out[t] = sum over j ascending of the pair rows (no atomics).
 //
-// MFMA 32x32x16 bf16 operand layout: lane l holds A[l % 32][8 (l / 32) + 0..7]
-// and B[8 (l / 32) + 0..7][l % 32]; accumulator v of lane l is D[8 (v / 4) +
+// MFMA 32x32x16 operand layout: lane l holds A[l % 32][8 (l / 32) + 0..7] and
+// B[8 (l / 32) + 0..7][l % 32]; accumulator v of lane l is D[8 (v / 4) +
 // 4 (l / 32) + v % 4][l % 32].
+//
+// K order.  A dot product may visit K in any order as long as A and B agree,
+// so each format fixes the order its blocks unpack fastest in.  The K dimension
+// is cut into K-blocks (Q4_K: one 256-value block; Q8_0: four 32-value blocks,
+// 128 values); MFMA step s of a K-block takes 8 values from each lane half h
+// (lanes 0-31: h = 0, lanes 32-63: h = 1), a "run" of 8 consecutive values of
+// the row, in the order the lane's unpacking yields them:
+//   Q4_K: step s = 4c + t reads, in 64-value chunk c, the bytes 16h + 8 (t % 2)
+//         + 0..7 of the chunk's 32 quant bytes, low nibbles for t < 2 and high
+//         ones for t >= 2: run r = 8c + 4 (t / 2) + 2h + t % 2, elements in
+//         byte order 0 2 1 3 4 6 5 7 (one mask-and-or unpacks bytes 0 and 2);
+//   Q8_0: step s = 4j + u reads block b = 2j + h, its values 8u + 0..7:
+//         run r = 4b + u, elements in order.
+// The activations (x for gate/up, h for down) are stored as groups g = 2s + h
+// of 8 f16 in that order, so the A operand of a step is one 16-byte read.
 #include "common.h"
 #include "workspace.h"
 
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;
-constexpr int kTM = 32;          // pairs per tile
-constexpr int kTN = 128;         // output features per block (4 waves x 32)
-constexpr int kKS = 128;         // K per step
-constexpr int kLdsRow = kKS + 8; // bf16 per LDS row (16 bytes of padding)
+constexpr int kThreads = 256;  // gather helpers, prep, combine
+constexpr int kGemm = 512;     // GEMM blocks: 8 waves, one 32-feature weight strip each
+constexpr int kTM = 64;        // pairs per tile: two 32-row MFMA subtiles
+constexpr int kTNG = 128;      // gate/up features per block (waves 0-3 gate, 4-7 up)
+constexpr int kTND = 256;      // down output features per block
 constexpr int NAIWA_SCRATCH_PREFILL = 5;
+
+template <int DT> struct KBlock;
+template <> struct KBlock<NAIWA_Q4_K> {
+    static constexpr int kVals = 256, kSteps = 16;
+};
+template <> struct KBlock<NAIWA_Q8_0> {
+    static constexpr int kVals = 128, kSteps = 8;
+};
+
+// Element i of a laid-out Q4_K run holds byte q4_elem(i) of the run (an involution).
+__host__ __device__ constexpr int q4_elem(int i) { return (i == 1 || i == 2 || i == 5 || i == 6) ? (i ^ 3) : i; }
+
+// The group (2s + h) that holds run r of a K-block.
+template <int DT>
+__host__ __device__ inline int group_of_run(int r) {
+    if (DT == NAIWA_Q4_K) {
+        const int c = r / 8, q = r % 8;
+        const int t = 2 * (q / 4) + (q % 2), h = (q / 2) % 2;
+        return 2 * (4 * c + t) + h;
+    } else {
+        const int b = r / 4, u = r % 4;
+        return 2 * (4 * (b / 2) + u) + (b % 2);
+    }
+}
+
+// Position, in the laid-out row, of value f of the original row.
+template <int DT>
+__host__ __device__ inline int laid_pos(int f) {
+    constexpr int KV = KBlock<DT>::kVals;
+    const int kb = f / KV, r = (f % KV) / 8, e = f % 8;
+    return kb * KV + 8 * group_of_run<DT>(r) + (DT == NAIWA_Q4_K ? q4_elem(e) : e);
+}
 
 struct Tiles {
     int* start; // first sorted position of the tile
-    int* count; // pairs in the tile (<= 32)
+    int* count; // pairs in the tile (<= kTM)
     int* slot;  // the tile's slot
     int* n;     // number of tiles
 };
 
-// Cut the sorted pairs into tiles of <= 32 pairs of one slot.  One block.
+// Cut the sorted pairs into tiles of <= kTM pairs of one slot.  One block.
 __global__ void __launch_bounds__(kThreads) tiles_kernel(const uint32_t* offsets, int slots, Tiles t) {
     __shared__ int part[kThreads + 1];
     const int tid = threadIdx.x;
@@ -70,83 +121,168 @@ __global__ void __launch_bounds__(kThreads) tiles_kernel(const uint32_t* offsets
     }
 }
 
-// Dequantise K-step [k0, k0 + 128) of one weight row into 128 bf16 at dst (LDS).
+__device__ __forceinline__ uint32_t f16x2_bits(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+
+// x bf16 [T, H] -> xp f16 [T, H] in the K order of DT.  One thread per run of
+// 8 values.  bf16 values are exact in f16 inside its range; larger magnitudes
+// are clamped to +-65504 (the expert inputs are normalised activations).
 template <int DT>
-__device__ inline void dequant_step(const uint8_t* row, int k0, __bf16* dst);
-
-template <>
-__device__ inline void dequant_step<NAIWA_Q4_K>(const uint8_t* row, int k0, __bf16* dst) {
-    const uint8_t* blk = row + (k0 / NAIWA_QK_K) * NAIWA_Q4_K_BYTES;
-    const uint4 hd = *reinterpret_cast<const uint4*>(blk);
-    const float d = naiwa_f16_to_f32(hd.x & 0xffffu), dmin = naiwa_f16_to_f32(hd.x >> 16);
-    auto sc = [&](int j) -> int { // scale byte j (0..11): bytes 4..15 of the header
-        const uint32_t wd = j < 4 ? hd.y : (j < 8 ? hd.z : hd.w);
-        return (int)((wd >> (8 * (j & 3))) & 0xFFu);
-    };
-    const int c0 = ((k0 / 128) & 1) * 2;                             // first 64-value chunk of the step
+__global__ void __launch_bounds__(kThreads) prep_kernel(const uint16_t* x, int T, int H, uint16_t* xp) {
+    const int runs = H / 8;
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= (int64_t)T * runs) return;
+    const int t = (int)(i / runs), run = (int)(i % runs);
+    const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)t * H + 8 * run);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    float f[8];
 #pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
-        const int c = c0 + cc;
-        // sub-blocks 2c (low nibbles) and 2c + 1 (high nibbles): ggml get_scale_min_k4
-        float scale[2], mn[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int j = 2 * c + h;
-            int s, m;
-            if (j < 4) {
-                s = sc(j) & 63;
-                m = sc(j + 4) & 63;
-            } else {
-                s = (sc(j + 4) & 0xF) | ((sc(j - 4) >> 6) << 4);
-                m = (sc(j + 4) >> 4) | ((sc(j) >> 6) << 4);
-            }
-            scale[h] = d * (float)s;
-            mn[h] = dmin * (float)m;
-        }
-        const uint4* q = reinterpret_cast<const uint4*>(blk + 16 + 32 * c);
-        const uint4 qa = q[0], qb = q[1];
-        const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-        __bf16 lo[32], hi[32];
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            const uint32_t byte = (w[i / 4] >> (8 * (i % 4))) & 0xFFu;
-            lo[i] = (__bf16)(scale[0] * (float)(byte & 0xF) - mn[0]);
-            hi[i] = (__bf16)(scale[1] * (float)(byte >> 4) - mn[1]);
-        }
-        __bf16* o = dst + 64 * cc;
-#pragma unroll
-        for (int i = 0; i < 32; i += 8) {
-            *reinterpret_cast<bf16x8*>(o + i) = *reinterpret_cast<const bf16x8*>(lo + i);
-            *reinterpret_cast<bf16x8*>(o + 32 + i) = *reinterpret_cast<const bf16x8*>(hi + i);
-        }
+    for (int j = 0; j < 4; ++j) {
+        f[2 * j] = fminf(fmaxf(__uint_as_float(w[j] << 16), -65504.0f), 65504.0f);
+        f[2 * j + 1] = fminf(fmaxf(__uint_as_float(w[j] & 0xffff0000u), -65504.0f), 65504.0f);
     }
+    float g[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) g[e] = f[DT == NAIWA_Q4_K ? q4_elem(e) : e];
+    const int dst = laid_pos<DT>(8 * run); // the run's group (its element 0 is byte 0)
+    uint4 o;
+    o.x = f16x2_bits(g[0], g[1]);
+    o.y = f16x2_bits(g[2], g[3]);
+    o.z = f16x2_bits(g[4], g[5]);
+    o.w = f16x2_bits(g[6], g[7]);
+    *reinterpret_cast<uint4*>(xp + (size_t)t * H + dst) = o;
 }
 
-template <>
-__device__ inline void dequant_step<NAIWA_Q8_0>(const uint8_t* row, int k0, __bf16* dst) {
-    // 4 blocks of {fp16 d, int8 q[32]}, 136 bytes, 4-byte aligned (k0 is a multiple of 128)
-    const uint32_t* p = reinterpret_cast<const uint32_t*>(row + (k0 / NAIWA_QK8_0) * NAIWA_Q8_0_BYTES);
+// One lane's share of a weight row for one K-block: raw words, then unpacked
+// step by step into the MFMA B operand (8 f16).
+template <int DT> struct BRow;
+
+template <> struct BRow<NAIWA_Q4_K> {
+    u32x4 hd;   // d, dmin, 12 scale bytes
+    u32x4 q[4]; // per 64-value chunk: bytes 16h .. 16h + 15 of its 32 quant bytes
+
+    __device__ __forceinline__ void load(const uint8_t* row, int kb, int h) {
+        const uint8_t* blk = row + (size_t)kb * NAIWA_Q4_K_BYTES;
+        hd = *reinterpret_cast<const u32x4*>(blk);
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        // block b is bytes [34 b, 34 b + 34): halfword-aligned, covered by the 9 aligned
-        // words from 34 b / 4 (never past the 136 bytes of the step)
-        uint32_t wds[9];
-        const int w0 = (34 * b) / 4, sh = ((34 * b) % 4) * 8;
-#pragma unroll
-        for (int i = 0; i < 9; ++i) wds[i] = p[w0 + i];
-        auto byte_at = [&](int i) -> uint32_t { // byte i of the block (0..33)
-            const int bit = sh + 8 * i;
-            return (wds[bit / 32] >> (bit % 32)) & 0xFFu;
-        };
-        const float d = naiwa_f16_to_f32(byte_at(0) | (byte_at(1) << 8));
-        __bf16 v[32];
-#pragma unroll
-        for (int i = 0; i < 32; ++i) v[i] = (__bf16)(d * (float)(int8_t)byte_at(2 + i));
-#pragma unroll
-        for (int i = 0; i < 32; i += 8)
-            *reinterpret_cast<bf16x8*>(dst + 32 * b + i) = *reinterpret_cast<const bf16x8*>(v + i);
+        for (int c = 0; c < 4; ++c) q[c] = *reinterpret_cast<const u32x4*>(blk + 16 + 32 * c + 16 * h);
     }
-}
+    // (d * scale, -dmin * min) of 32-value sub-block j (ggml's get_scale_min_k4), as f16
+    __device__ __forceinline__ void scale_min(int j, _Float16& sc, _Float16& mn) const {
+        const uint32_t s3[3] = {hd.y, hd.z, hd.w};
+        auto sb = [&](int i) -> int { return (int)((s3[i >> 2] >> (8 * (i & 3))) & 0xFFu); };
+        int s, m;
+        if (j < 4) {
+            s = sb(j) & 63;
+            m = sb(j + 4) & 63;
+        } else {
+            s = (sb(j + 4) & 0xF) | ((sb(j - 4) >> 6) << 4);
+            m = (sb(j + 4) >> 4) | ((sb(j) >> 6) << 4);
+        }
+        sc = (_Float16)(naiwa_f16_to_f32(hd.x & 0xffffu) * (float)s);
+        mn = (_Float16)(-(naiwa_f16_to_f32(hd.x >> 16) * (float)m));
+    }
+    __device__ __forceinline__ half8 step(int s) const {
+        const int c = s / 4, t = s % 4, sh = 4 * (t / 2);
+        const uint32_t da = (t % 2) ? q[c].z : q[c].x, db = (t % 2) ? q[c].w : q[c].y;
+        _Float16 a, b;
+        scale_min(2 * c + t / 2, a, b);
+        const half2v scv = {a, a}, mnv = {b, b};
+        const half2v k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+        half2v p[4];
+        p[0] = __builtin_bit_cast(half2v, ((da >> sh) & 0x000F000Fu) | 0x64006400u);
+        p[1] = __builtin_bit_cast(half2v, ((da >> (sh + 8)) & 0x000F000Fu) | 0x64006400u);
+        p[2] = __builtin_bit_cast(half2v, ((db >> sh) & 0x000F000Fu) | 0x64006400u);
+        p[3] = __builtin_bit_cast(half2v, ((db >> (sh + 8)) & 0x000F000Fu) | 0x64006400u);
+        half8 out;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const half2v w = __builtin_elementwise_fma(p[i] + k1024, scv, mnv);
+            out[2 * i] = w[0];
+            out[2 * i + 1] = w[1];
+        }
+        return out;
+    }
+};
+
+template <> struct BRow<NAIWA_Q8_0> {
+    uint32_t w[2][9]; // blocks 2j + h (j = 0, 1): 9 words from the block's aligned start
+    int sh[2];        // byte offset of each block within its first word (0 or 2)
+
+    __device__ __forceinline__ void load(const uint8_t* row, int kb, int h) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int off = (4 * kb + 2 * j + h) * NAIWA_Q8_0_BYTES;
+            sh[j] = off & 3;
+            const uint32_t* p = reinterpret_cast<const uint32_t*>(row + (off & ~3));
+#pragma unroll
+            for (int i = 0; i < 9; ++i) w[j][i] = p[i];
+        }
+    }
+    __device__ __forceinline__ half8 step(int s) const {
+        const int j = s / 4, u = s % 4;
+        // values 8u .. 8u + 7 are bytes sh + 2 + 8u .. of the window: words 2u + 1 and
+        // 2u + 2 when the block starts at byte 2 of its first word, else shifted by 2
+        const uint32_t d0 = sh[j] ? w[j][2 * u + 1] : __builtin_amdgcn_alignbyte(w[j][2 * u + 1], w[j][2 * u], 2);
+        const uint32_t d1 =
+            sh[j] ? w[j][2 * u + 2] : __builtin_amdgcn_alignbyte(w[j][2 * u + 2], w[j][2 * u + 1], 2);
+        const uint32_t dbits = sh[j] ? (w[j][0] >> 16) : (w[j][0] & 0xffffu);
+        const _Float16 dv = __builtin_bit_cast(_Float16, (uint16_t)dbits);
+        const half2v d = {dv, dv};
+        const half2v k1152 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+        half2v p[4];
+        // (q0, q1) -> f16 1024 + (q ^ 0x80) = 1152 + q for the signed byte q
+        p[0] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(d0, d0, 0x0C010C00u) ^ 0x64806480u);
+        p[1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(d0, d0, 0x0C030C02u) ^ 0x64806480u);
+        p[2] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(d1, d1, 0x0C010C00u) ^ 0x64806480u);
+        p[3] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(d1, d1, 0x0C030C02u) ^ 0x64806480u);
+        half8 out;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const half2v v = (p[i] + k1152) * d;
+            out[2 * i] = v[0];
+            out[2 * i + 1] = v[1];
+        }
+        return out;
+    }
+};
+
+// LDS A tile of one K-block: group g of tile row m at [g][m ^ (g % 32)] (16 bytes
+// each): a step's read of 32 rows of one group covers 32 consecutive slots, and a
+// staging store of the 32 groups of one row spreads over the banks.
+template <int DT> struct ATile {
+    static constexpr int kGroups = 2 * KBlock<DT>::kSteps;
+    u32x4 v[kGroups][kTM];
+    __device__ __forceinline__ u32x4& at(int g, int m) { return v[g][m ^ (g & 31)]; }
+    __device__ __forceinline__ const u32x4& at(int g, int m) const { return v[g][m ^ (g & 31)]; }
+};
+
+// Each thread's share of staging one K-block of the A tile: global -> registers
+// (issued early) -> LDS (after the previous step's reads).
+template <int DT> struct AStage {
+    static constexpr int kPer = ATile<DT>::kGroups * kTM / kGemm; // 16-byte pieces per thread
+    u32x4 r[kPer];
+    // base: the activation matrix (a kernel argument, so the loads are global ones);
+    // rows[m]: element offset of tile row m
+    // piece p: row p / G, group p % G, so the lanes of a load cover whole rows
+    __device__ __forceinline__ void load(const uint16_t* base, const int* rows, int kb, int tid) {
+        constexpr int G = ATile<DT>::kGroups;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int p = tid + kGemm * i, m = p / G, g = p % G;
+            r[i] = *reinterpret_cast<const u32x4*>(base + rows[m] + kb * KBlock<DT>::kVals + 8 * g);
+        }
+    }
+    __device__ __forceinline__ void store(ATile<DT>& a, int tid) const {
+        constexpr int G = ATile<DT>::kGroups;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int p = tid + kGemm * i;
+            a.at(p % G, p / G) = r[i];
+        }
+    }
+};
 
 struct Bank {
     const uint8_t* base;
@@ -154,100 +290,145 @@ struct Bank {
     int64_t row_bytes;
 };
 
-// gate/up: one tile of <= 32 pairs x 128 intermediate features.
-template <int DG>
-__global__ void __launch_bounds__(kThreads)
-gateup_kernel(Bank gate, Bank up, const uint16_t* x, int H, int I, int k, const uint32_t* perm, Tiles tl,
-              int act, uint16_t* hbuf) {
-    __shared__ __align__(16) __bf16 xs[kTM][kLdsRow];
-    __shared__ __align__(16) __bf16 wg[kTN][kLdsRow];
-    __shared__ __align__(16) __bf16 wu[kTN][kLdsRow];
+// gate/up: one tile of <= 64 pairs x 128 intermediate features; waves 0-3 the
+// gate rows, waves 4-7 the up rows of the same 4 x 32 features.  xp: x in the K
+// order of DG; hp (out): h in the K order of DD, f16 [pairs, I].
+template <int DG, int DD>
+__global__ void __launch_bounds__(kGemm, 2)
+gateup_kernel(Bank gate, Bank up, const uint16_t* xp, int H, int I, int k, const uint32_t* perm, Tiles tl,
+              int act, uint16_t* hp) {
+    __shared__ ATile<DG> as[2];
+    __shared__ int rows[kTM];
     const int tile = blockIdx.y;
     if (tile >= *tl.n) return;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5;
+    const int is_up = wave >> 2, strip = wave & 3;
     const int start = tl.start[tile], cnt = tl.count[tile], slot = tl.slot[tile];
-    const int n0 = blockIdx.x * kTN;
-    const uint8_t* grow0 = gate.base + (int64_t)slot * gate.stride + (int64_t)n0 * gate.row_bytes;
-    const uint8_t* urow0 = up.base + (int64_t)slot * up.stride + (int64_t)n0 * up.row_bytes;
-    floatx16 accg = {}, accu = {};
-    for (int k0 = 0; k0 < H; k0 += kKS) {
-        __syncthreads(); // the previous step's MFMAs read the tiles
-        // activations: 32 rows x 128 bf16, 16 bytes per thread per pass (2 passes)
+    if (tid < kTM) rows[tid] = (int)(perm[start + min(tid, cnt - 1)] / k) * H;
+    const int n = blockIdx.x * kTNG + 32 * strip + (lane & 31); // this lane's weight row
+    const Bank& bank = is_up ? up : gate;
+    const uint8_t* wrow = bank.base + (int64_t)slot * bank.stride + (int64_t)n * bank.row_bytes;
+    const int nkb = H / KBlock<DG>::kVals;
+    __syncthreads();
+
+    AStage<DG> st;
+    BRow<DG> b0, b1; // this K-block's row share and the next one's, alternating
+    st.load(xp, rows, 0, tid);
+    b0.load(wrow, 0, h);
+    st.store(as[0], tid);
+    __syncthreads();
+    floatx16 acc[2] = {}; // [m subtile]
+    // one K-block; the next block's loads are unconditional (the last block reloads
+    // itself) so the compiler can count them and wait only for this block's registers
+    auto block = [&](int kb, const BRow<DG>& bw, BRow<DG>& nw) {
+        const int kn = min(kb + 1, nkb - 1);
+        st.load(xp, rows, kn, tid);
+        nw.load(wrow, kn, h);
+        const ATile<DG>& a = as[kb & 1];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int v = tid + kThreads * i, r = v / 16, c = (v % 16) * 8;
-            uint4 val = make_uint4(0u, 0u, 0u, 0u);
-            if (r < cnt) {
-                const int t = (int)perm[start + r] / k;
-                val = *reinterpret_cast<const uint4*>(x + (size_t)t * H + k0 + c);
+        for (int s = 0; s < KBlock<DG>::kSteps; ++s) {
+            const half8 wv = bw.step(s);
+#pragma unroll
+            for (int ms = 0; ms < 2; ++ms) {
+                const half8 x8 = __builtin_bit_cast(half8, a.at(2 * s + h, 32 * ms + (lane & 31)));
+                acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x8, wv, acc[ms], 0, 0, 0);
             }
-            *reinterpret_cast<uint4*>(&xs[r][c]) = val;
         }
-        // weights: thread < 128 dequantises gate row n0 + tid, the others up row n0 + tid - 128
-        if (tid < kTN) dequant_step<DG>(grow0 + (int64_t)tid * gate.row_bytes, k0, &wg[tid][0]);
-        else dequant_step<DG>(urow0 + (int64_t)(tid - kTN) * up.row_bytes, k0, &wu[tid - kTN][0]);
+        st.store(as[(kb + 1) & 1], tid);
         __syncthreads();
-        const int r = lane % 32, kh = 8 * (lane / 32), n = 32 * wave + lane % 32;
-#pragma unroll
-        for (int kk = 0; kk < kKS; kk += 16) {
-            const bf16x8 a = *reinterpret_cast<const bf16x8*>(&xs[r][kk + kh]);
-            const bf16x8 bg = *reinterpret_cast<const bf16x8*>(&wg[n][kk + kh]);
-            const bf16x8 bu = *reinterpret_cast<const bf16x8*>(&wu[n][kk + kh]);
-            accg = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bg, accg, 0, 0, 0);
-            accu = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bu, accu, 0, 0, 0);
-        }
+    };
+    int kb = 0;
+    for (; kb + 2 <= nkb; kb += 2) {
+        block(kb, b0, b1);
+        block(kb + 1, b1, b0);
     }
-    // epilogue: h = act(g) * u as bf16, rows of the tile's sorted positions
-    const int col = n0 + 32 * wave + lane % 32;
+    if (kb < nkb) block(kb, b0, b1);
+    // epilogue: the gate waves hand act(g) to the up waves of the same strip through
+    // LDS (the A tiles are no longer read); h = act(g) * u as f16 at its laid-out
+    // position for the down format
+    float* xch = reinterpret_cast<float*>(&as[0]);
+    const int xbase = (strip * 32) * 64 + lane;
+    if (!is_up) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int m = 8 * (v / 4) + 4 * (lane / 32) + v % 4;
-        if (m < cnt) hbuf[(size_t)(start + m) * I + col] = (uint16_t)naiwa_f32_to_bf16(naiwa_act(act, accg[v]) * accu[v]);
+        for (int ms = 0; ms < 2; ++ms)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) xch[xbase + (16 * ms + v) * 64] = naiwa_act(act, acc[ms][v]);
+    }
+    __syncthreads();
+    if (is_up) {
+        const int col = laid_pos<DD>(n);
+#pragma unroll
+        for (int ms = 0; ms < 2; ++ms)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int m = 32 * ms + 8 * (v / 4) + 4 * h + v % 4;
+                if (m < cnt) {
+                    const float g = xch[xbase + (16 * ms + v) * 64];
+                    const _Float16 hv = (_Float16)fminf(fmaxf(g * acc[ms][v], -65504.0f), 65504.0f);
+                    hp[(size_t)(start + m) * I + col] = __builtin_bit_cast(uint16_t, hv);
+                }
+            }
     }
 }
 
-// down: one tile of <= 32 pairs x 128 output features; pair rows scaled by their weight.
+// down: one tile of <= 64 pairs x 256 output features (32 per wave); pair rows
+// scaled by their weight.
 template <int DD>
-__global__ void __launch_bounds__(kThreads)
-down_kernel(Bank down, const uint16_t* hbuf, int H, int I, const uint32_t* perm, const float* w, Tiles tl,
+__global__ void __launch_bounds__(kGemm, 2)
+down_kernel(Bank down, const uint16_t* hp, int H, int I, const uint32_t* perm, const float* w, Tiles tl,
             float* ypair) {
-    __shared__ __align__(16) __bf16 hs[kTM][kLdsRow];
-    __shared__ __align__(16) __bf16 wd[kTN][kLdsRow];
+    __shared__ ATile<DD> as[2];
+    __shared__ int rows[kTM];
     const int tile = blockIdx.y;
     if (tile >= *tl.n) return;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5;
     const int start = tl.start[tile], cnt = tl.count[tile], slot = tl.slot[tile];
-    const int n0 = blockIdx.x * kTN;
-    const uint8_t* drow0 = down.base + (int64_t)slot * down.stride + (int64_t)n0 * down.row_bytes;
-    floatx16 acc = {};
-    for (int k0 = 0; k0 < I; k0 += kKS) {
+    if (tid < kTM) rows[tid] = (start + min(tid, cnt - 1)) * I;
+    const int n = blockIdx.x * kTND + 32 * wave + (lane & 31);
+    const uint8_t* drow = down.base + (int64_t)slot * down.stride + (int64_t)n * down.row_bytes;
+    const int nkb = I / KBlock<DD>::kVals;
+    __syncthreads();
+
+    AStage<DD> st;
+    BRow<DD> d0, d1;
+    st.load(hp, rows, 0, tid);
+    d0.load(drow, 0, h);
+    st.store(as[0], tid);
+    __syncthreads();
+    floatx16 acc[2] = {};
+    auto block = [&](int kb, const BRow<DD>& bd, BRow<DD>& nd) {
+        const int kn = min(kb + 1, nkb - 1);
+        st.load(hp, rows, kn, tid);
+        nd.load(drow, kn, h);
+        const ATile<DD>& a = as[kb & 1];
+#pragma unroll
+        for (int s = 0; s < KBlock<DD>::kSteps; ++s) {
+            const half8 wd = bd.step(s);
+#pragma unroll
+            for (int ms = 0; ms < 2; ++ms) {
+                const half8 h8 = __builtin_bit_cast(half8, a.at(2 * s + h, 32 * ms + (lane & 31)));
+                acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8, wd, acc[ms], 0, 0, 0);
+            }
+        }
+        st.store(as[(kb + 1) & 1], tid);
         __syncthreads();
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int v = tid + kThreads * i, r = v / 16, c = (v % 16) * 8;
-            uint4 val = make_uint4(0u, 0u, 0u, 0u);
-            if (r < cnt) val = *reinterpret_cast<const uint4*>(hbuf + (size_t)(start + r) * I + k0 + c);
-            *reinterpret_cast<uint4*>(&hs[r][c]) = val;
-        }
-        if (tid < kTN) dequant_step<DD>(drow0 + (int64_t)tid * down.row_bytes, k0, &wd[tid][0]);
-        __syncthreads();
-        const int r = lane % 32, kh = 8 * (lane / 32), n = 32 * wave + lane % 32;
-#pragma unroll
-        for (int kk = 0; kk < kKS; kk += 16) {
-            const bf16x8 a = *reinterpret_cast<const bf16x8*>(&hs[r][kk + kh]);
-            const bf16x8 b = *reinterpret_cast<const bf16x8*>(&wd[n][kk + kh]);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
-        }
+    };
+    int kb = 0;
+    for (; kb + 2 <= nkb; kb += 2) {
+        block(kb, d0, d1);
+        block(kb + 1, d1, d0);
     }
-    const int col = n0 + 32 * wave + lane % 32;
+    if (kb < nkb) block(kb, d0, d1);
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int m = 8 * (v / 4) + 4 * (lane / 32) + v % 4;
-        if (m < cnt) {
-            const uint32_t p = perm[start + m];
-            ypair[(size_t)p * H + col] = acc[v] * w[p];
+    for (int ms = 0; ms < 2; ++ms)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int m = 32 * ms + 8 * (v / 4) + 4 * h + v % 4;
+            if (m < cnt) {
+                const uint32_t p = perm[start + m];
+                ypair[(size_t)p * H + n] = acc[ms][v] * w[p];
+            }
         }
-    }
 }
 
 // out[t] = sum over j = 0..k-1 of the pair rows whose slot id is valid.
@@ -262,8 +443,16 @@ combine_kernel(const float* ypair, const uint32_t* ids, int k, int H, int slots,
     }
 }
 
+// K of a projection in this format: whole K-blocks.
 bool fmt_ok(int dtype, int kdim) {
-    return (dtype == NAIWA_Q4_K && kdim % NAIWA_QK_K == 0) || (dtype == NAIWA_Q8_0 && kdim % kKS == 0);
+    return (dtype == NAIWA_Q4_K && kdim % KBlock<NAIWA_Q4_K>::kVals == 0) ||
+           (dtype == NAIWA_Q8_0 && kdim % KBlock<NAIWA_Q8_0>::kVals == 0);
+}
+
+template <int DG, int DD>
+void launch_gateup(dim3 g, hipStream_t st, Bank bg, Bank bu, const uint16_t* xp, int H, int I, int k,
+                   const uint32_t* perm, Tiles tl, int act, uint16_t* hp) {
+    gateup_kernel<DG, DD><<<g, kGemm, 0, st>>>(bg, bu, xp, H, I, k, perm, tl, act, hp);
 }
 
 } // namespace
@@ -278,23 +467,28 @@ extern "C" int naiwa_moe_prefill(const naiwa_bank* gate, const naiwa_bank* up, c
     if (up->k != H || up->n != I || down->n != H || down->k != I || up->slots != slots || down->slots != slots)
         return NAIWA_E_INVALID;
     if (gate->dtype != up->dtype || !fmt_ok(gate->dtype, H) || !fmt_ok(down->dtype, I)) return NAIWA_E_UNSUPPORTED;
-    if (H % kTN || I % kTN || H % kKS || I % kKS) return NAIWA_E_UNSUPPORTED;
+    if (H % kTND || I % kTNG) return NAIWA_E_UNSUPPORTED;
     if (act != NAIWA_ACT_SILU && act != NAIWA_ACT_GELU_PYTORCH_TANH) return NAIWA_E_UNSUPPORTED;
     const int64_t n = (int64_t)T * k;
     if (n > 65536 || slots <= 0 || slots > 4096) return NAIWA_E_UNSUPPORTED;
+    if ((int64_t)T * H > INT32_MAX || n * I > INT32_MAX) return NAIWA_E_UNSUPPORTED; // 32-bit row offsets
     const int64_t rbg = naiwa_row_bytes(gate->dtype, H), rbd = naiwa_row_bytes(down->dtype, I);
     if (gate->slot_stride < rbg * I || up->slot_stride < rbg * I || down->slot_stride < rbd * H) return NAIWA_E_INVALID;
+    // 16-byte loads of x and of Q4_K blocks, 4-byte loads of Q8_0 blocks
     if (((uintptr_t)gate->base | (uintptr_t)up->base | (uintptr_t)down->base | gate->slot_stride | up->slot_stride |
          down->slot_stride | (uintptr_t)x) & 15)
         return NAIWA_E_INVALID;
-    if (gate->dtype == NAIWA_Q4_K && (rbg % 16)) return NAIWA_E_INVALID;
+    if ((gate->dtype == NAIWA_Q4_K && (rbg % 16)) || (down->dtype == NAIWA_Q4_K && (rbd % 16))) return NAIWA_E_INVALID;
+    if ((gate->dtype == NAIWA_Q8_0 && (rbg % 4)) || (down->dtype == NAIWA_Q8_0 && (rbd % 4))) return NAIWA_E_INVALID;
 
-    // scratch: perm [n] | offsets [slots + 1] | bad | tiles 3 x max + n | h bf16 [n, I] | ypair f32 [n, H]
+    // scratch: perm [n] | offsets [slots + 1] | bad | tiles 3 x max + n | xp f16 [T, H] | h f16 [n, I] |
+    //          ypair f32 [n, H]
     const int64_t max_tiles = (n + kTM - 1) / kTM + slots;
     auto a256 = [](size_t b) { return (b + 255) & ~size_t(255); };
     const size_t o_perm = 0, o_off = a256(o_perm + (size_t)n * 4), o_bad = a256(o_off + (size_t)(slots + 1) * 4);
-    const size_t o_tiles = a256(o_bad + 4), o_h = a256(o_tiles + (size_t)(3 * max_tiles + 1) * 4);
-    const size_t o_y = a256(o_h + (size_t)n * I * 2), total = a256(o_y + (size_t)n * H * 4);
+    const size_t o_tiles = a256(o_bad + 4), o_x = a256(o_tiles + (size_t)(3 * max_tiles + 1) * 4);
+    const size_t o_h = a256(o_x + (size_t)T * H * 2), o_y = a256(o_h + (size_t)n * I * 2);
+    const size_t total = a256(o_y + (size_t)n * H * 4);
     int rc = 0;
     uint8_t* ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_PREFILL, total, &rc);
     if (!ws) return rc;
@@ -305,23 +499,34 @@ extern "C" int naiwa_moe_prefill(const naiwa_bank* gate, const naiwa_bank* up, c
     tl.count = tl.start + max_tiles;
     tl.slot = tl.count + max_tiles;
     tl.n = tl.slot + max_tiles;
-    uint16_t* hbuf = (uint16_t*)(ws + o_h);
+    uint16_t* xp = (uint16_t*)(ws + o_x);
+    uint16_t* hp = (uint16_t*)(ws + o_h);
     float* ypair = (float*)(ws + o_y);
     hipStream_t st = (hipStream_t)stream;
 
     if ((rc = naiwa_moe_gather(slot_ids, (int)n, slots, perm, offsets, (int*)(ws + o_bad), stream))) return rc;
     tiles_kernel<<<1, kThreads, 0, st>>>(offsets, slots, tl);
+    const unsigned prep_blocks = (unsigned)(((int64_t)T * (H / 8) + kThreads - 1) / kThreads);
+    if (gate->dtype == NAIWA_Q4_K)
+        prep_kernel<NAIWA_Q4_K><<<prep_blocks, kThreads, 0, st>>>((const uint16_t*)x, T, H, xp);
+    else
+        prep_kernel<NAIWA_Q8_0><<<prep_blocks, kThreads, 0, st>>>((const uint16_t*)x, T, H, xp);
     const Bank bg{(const uint8_t*)gate->base, gate->slot_stride, rbg}, bu{(const uint8_t*)up->base, up->slot_stride, rbg};
     const Bank bd{(const uint8_t*)down->base, down->slot_stride, rbd};
-    const dim3 g1(I / kTN, (unsigned)max_tiles), g2(H / kTN, (unsigned)max_tiles);
-    if (gate->dtype == NAIWA_Q4_K)
-        gateup_kernel<NAIWA_Q4_K><<<g1, kThreads, 0, st>>>(bg, bu, (const uint16_t*)x, H, I, k, perm, tl, act, hbuf);
+    const dim3 g1(I / kTNG, (unsigned)max_tiles), g2(H / kTND, (unsigned)max_tiles);
+    const bool g4 = gate->dtype == NAIWA_Q4_K, d4 = down->dtype == NAIWA_Q4_K;
+    if (g4 && d4)
+        launch_gateup<NAIWA_Q4_K, NAIWA_Q4_K>(g1, st, bg, bu, xp, H, I, k, perm, tl, act, hp);
+    else if (g4)
+        launch_gateup<NAIWA_Q4_K, NAIWA_Q8_0>(g1, st, bg, bu, xp, H, I, k, perm, tl, act, hp);
+    else if (d4)
+        launch_gateup<NAIWA_Q8_0, NAIWA_Q4_K>(g1, st, bg, bu, xp, H, I, k, perm, tl, act, hp);
     else
-        gateup_kernel<NAIWA_Q8_0><<<g1, kThreads, 0, st>>>(bg, bu, (const uint16_t*)x, H, I, k, perm, tl, act, hbuf);
-    if (down->dtype == NAIWA_Q4_K)
-        down_kernel<NAIWA_Q4_K><<<g2, kThreads, 0, st>>>(bd, hbuf, H, I, perm, w, tl, ypair);
+        launch_gateup<NAIWA_Q8_0, NAIWA_Q8_0>(g1, st, bg, bu, xp, H, I, k, perm, tl, act, hp);
+    if (d4)
+        down_kernel<NAIWA_Q4_K><<<g2, kGemm, 0, st>>>(bd, hp, H, I, perm, w, tl, ypair);
     else
-        down_kernel<NAIWA_Q8_0><<<g2, kThreads, 0, st>>>(bd, hbuf, H, I, perm, w, tl, ypair);
+        down_kernel<NAIWA_Q8_0><<<g2, kGemm, 0, st>>>(bd, hp, H, I, perm, w, tl, ypair);
     combine_kernel<<<T, kThreads, 0, st>>>(ypair, slot_ids, k, H, slots, (flags & NAIWA_PREFILL_ACCUMULATE) ? 1 : 0,
                                            out);
     return naiwa_hip_rc(hipGetLastError());

@@ -15,30 +15,27 @@
 namespace {
 
 constexpr int kLogitThreads = 256;
+constexpr int kLogitRows = 16; // rows per block: 4 per wave
 
+// logits[t, e] for expert e = blockIdx.x and rows blockIdx.y * 16 + 0..15, one
+// wave per row at a time: lane l takes the 8-feature chunks l, l + 64, ...  The
+// chunk values are int64 fixed point, so their sum is the same in any order.
 __global__ void __launch_bounds__(kLogitThreads)
 router_logits_kernel(const void* x, int x_bf16, const float* W, const float* bias, int rows, int H, int E,
                      float* logits) {
-    __shared__ long long part[kLogitThreads / 64];
-    const int e = blockIdx.x, tid = threadIdx.x;
+    const int e = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nchunks = H / NAIWA_ROUTER_CHUNK;
     const float* wr = W + (int64_t)e * H;
-    for (int t = 0; t < rows; ++t) {
+    const int t0 = blockIdx.y * kLogitRows;
+    for (int t = t0 + wave; t < min(rows, t0 + kLogitRows); t += kLogitThreads / 64) {
         long long acc = 0;
-        for (int c = tid; c < nchunks; c += kLogitThreads) {
+        for (int c = lane; c < nchunks; c += 64) {
             float xv[8];
             naiwa_load_x8(x, x_bf16, (int64_t)t * H + 8 * c, xv);
             acc += naiwa_router_chunk(wr + 8 * c, xv);
         }
         acc = naiwa_wave_sum_i64(acc);
-        if ((tid & 63) == 0) part[tid >> 6] = acc;
-        __syncthreads();
-        if (tid == 0) {
-            long long s = 0;
-            for (int i = 0; i < kLogitThreads / 64; ++i) s += part[i];
-            logits[(int64_t)t * E + e] = naiwa_router_fix_to_f32(s) + (bias ? bias[e] : 0.0f);
-        }
-        __syncthreads();
+        if (lane == 0) logits[(int64_t)t * E + e] = naiwa_router_fix_to_f32(acc) + (bias ? bias[e] : 0.0f);
     }
 }
 
@@ -81,7 +78,8 @@ extern "C" int naiwa_router_topk_biased(const void* x, int x_dtype, const float*
         logits = (float*)naiwa_scratch(NAIWA_SCRATCH_ROUTER, (size_t)rows * E * 4, &rc);
         if (!logits) return rc;
     }
-    router_logits_kernel<<<E, kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, W, bias, rows, H, E, logits);
+    const dim3 lg((unsigned)E, (unsigned)((rows + kLogitRows - 1) / kLogitRows));
+    router_logits_kernel<<<lg, kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, W, bias, rows, H, E, logits);
     router_topk_kernel<<<rows, kTopkThreads, 0, st>>>(logits, E, k, mode, ids_out, w_out);
     return naiwa_hip_rc(hipGetLastError());
 }

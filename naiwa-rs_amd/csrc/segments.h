@@ -12,10 +12,10 @@
 #define NAIWA_SEG_THREADS 256
 #define NAIWA_SEG_MAX_KEYS 4096
 
-// LDS: hist[NAIWA_SEG_MAX_KEYS] + chunk[NAIWA_SEG_THREADS] + scan scratch.
+// LDS: hist[NAIWA_SEG_MAX_KEYS] + per-wave key counts of one chunk + scan scratch.
 struct NaiwaSegSmem {
     uint32_t hist[NAIWA_SEG_MAX_KEYS];
-    uint32_t chunk[NAIWA_SEG_THREADS];
+    uint16_t wcnt[NAIWA_SEG_THREADS / 64][NAIWA_SEG_MAX_KEYS]; // zero between chunks
     uint32_t part[NAIWA_SEG_THREADS];
     uint32_t bad;
 };
@@ -28,7 +28,11 @@ __device__ inline void naiwa_segment(NaiwaSegSmem& sm, const uint32_t* keys, con
                                      int* seg_count, uint32_t* seg_key, uint32_t* seg_begin,
                                      int* bad) {
     const int tid = threadIdx.x;
-    for (int b = tid; b < nkeys; b += NAIWA_SEG_THREADS) sm.hist[b] = 0;
+    for (int b = tid; b < nkeys; b += NAIWA_SEG_THREADS) {
+        sm.hist[b] = 0;
+#pragma unroll
+        for (int w = 0; w < NAIWA_SEG_THREADS / 64; ++w) sm.wcnt[w][b] = 0;
+    }
     if (tid == 0) sm.bad = 0;
     __syncthreads();
     for (int i = tid; i < n; i += NAIWA_SEG_THREADS) {
@@ -76,7 +80,11 @@ __device__ inline void naiwa_segment(NaiwaSegSmem& sm, const uint32_t* keys, con
         if (bad) *bad = (int)sm.bad;
     }
     __syncthreads();
-    // Stable scatter, one chunk of 256 entries at a time.
+    // Stable scatter, one chunk of 256 entries at a time.  An entry's rank among
+    // the chunk's entries of its key = its rank inside its wave (one ballot per
+    // distinct key of the wave) + the counts of that key in the lower waves.
+    const int lane = tid & 63, wave = tid >> 6;
+    const uint64_t below = (1ull << lane) - 1ull;
     for (int c0 = 0; c0 < n; c0 += NAIWA_SEG_THREADS) {
         const int i = c0 + tid;
         uint32_t k = 0xffffffffu;
@@ -84,18 +92,29 @@ __device__ inline void naiwa_segment(NaiwaSegSmem& sm, const uint32_t* keys, con
             const uint32_t kk = keys[i];
             if (kk < (uint32_t)nkeys && (!weights || weights[i] != 0.0f)) k = kk;
         }
-        sm.chunk[tid] = k;
+        uint32_t rank = 0, lead_cnt = 0; // lead_cnt: the wave's count of k, on the key's first lane
+        uint64_t todo = __ballot(k != 0xffffffffu);
+        while (todo) {
+            const int first = __ffsll((long long)todo) - 1;
+            const uint32_t key = (uint32_t)__builtin_amdgcn_readlane((int)k, first);
+            const uint64_t same = __ballot(k == key);
+            if (k == key) rank = (uint32_t)__popcll(same & below);
+            if (lane == first) lead_cnt = (uint32_t)__popcll(same);
+            todo &= ~same;
+        }
+        if (lead_cnt) sm.wcnt[wave][k] = (uint16_t)lead_cnt;
         __syncthreads();
-        uint32_t rank = 0;
-        bool last = true;
         if (k != 0xffffffffu) {
-            for (int j = 0; j < tid; ++j) rank += sm.chunk[j] == k;
-            for (int j = tid + 1; j < NAIWA_SEG_THREADS; ++j)
-                if (sm.chunk[j] == k) { last = false; break; }
+#pragma unroll
+            for (int w = 0; w < NAIWA_SEG_THREADS / 64; ++w)
+                if (w < wave) rank += sm.wcnt[w][k];
             if (perm) perm[sm.hist[k] + rank] = (uint32_t)i;
         }
         __syncthreads();
-        if (k != 0xffffffffu && last) sm.hist[k] += rank + 1;
+        if (lead_cnt) {
+            atomicAdd(&sm.hist[k], lead_cnt);
+            sm.wcnt[wave][k] = 0;
+        }
         __syncthreads();
     }
 }
