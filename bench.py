@@ -71,7 +71,11 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--lookahead-swaps", type=int, default=-1, metavar="N",
                     help="cache25: predict each next layer's experts from this layer's activation and load them "
                          "(at most N LRU swaps per row, the reference's --lookahead-swaps); -1 = off")
-    ap.add_argument("--workload", choices=["resident", "cache25", "prefill"], default="resident",
+    ap.add_argument("--depth", type=int, default=0, metavar="N",
+                    help="prefill-stream: layer buffers (default: the memory plan's stride)")
+    ap.add_argument("--budget-gb", type=float, default=0.0, metavar="GB",
+                    help="prefill-stream: device memory the plan may assume free (default: what is free)")
+    ap.add_argument("--workload", choices=["resident", "cache25", "prefill", "prefill-stream"], default="resident",
                     help="resident: every expert in HBM (the headline); cache25: 32 of 128 experts "
                          "cached per layer, Zipf(1.1) routing, misses streamed over PCIe; prefill: "
                          "DeepSeek-V2-Lite-shaped 2048-token prefill in 512-token chunks (MFMA)")
@@ -80,10 +84,12 @@ def parse() -> argparse.Namespace:
 
 def main() -> int:
     args = parse()
-    if args.workload in ("cache25", "prefill"):
+    if args.workload in ("cache25", "prefill", "prefill-stream"):
         if args.gpus != 1:
             print("bench.py measures one GPU", file=sys.stderr)
             return 2
+        if args.workload == "prefill-stream":
+            return run_prefill_stream(args)
         return run_cache25(args) if args.workload == "cache25" else run_prefill(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
@@ -498,6 +504,111 @@ def run_cache25(args) -> int:
     return 0
 
 
+def run_prefill_stream(args) -> int:
+    """The DeepSeek-V2-Lite-shaped prefill of --workload prefill with every expert (64 routed
+    + 2 shared per layer) in pinned host memory: each layer's stacks are uploaded into a ring
+    of device layer buffers (include/naiwa_prefill.h) while the previous layer computes.  The
+    memory plan picks the chunk (up to the 2048 prompt tokens) and the depth from the free
+    device memory (or --budget-gb).  One step = the 2048-token prefill through the 26 layers."""
+    import naiwa_moe as nm
+    from naiwa_moe import prefill as P
+
+    if nm.device_count() < 1:
+        log("no HIP device")
+        return 1
+    L = 26 if args.layers == 48 else args.layers
+    H, E, S_, K, I, tokens = 2048, 64, 2, 6, 1408, 2048
+    steps = args.steps if args.steps != 50 else 3
+    warmup = args.warmup if args.warmup != 5 else 1
+    dt = (nm.Q4_K, nm.Q4_K, nm.Q8_0)
+    compute, copy = nm.Stream(), nm.Stream()
+    t0 = time.time()
+    stacks, routers = [], []
+    scratch = nm.DeviceBuffer(max((E + S_) * nm.row_bytes(d, k) * n for d, n, k in ((dt[0], I, H), (dt[2], H, I))))
+    for l in range(L):
+        hs = nm.HostExpertStacks(E + S_, H, I, dt)
+        for t, (n, k) in enumerate(((I, H), (I, H), (H, I))):
+            nbytes = hs.expert_bytes[t] * (E + S_)
+            for e in range(E + S_):
+                nm.synth(dt[t], 3000 + 8 * l + t, n * k, scratch.ptr + e * hs.expert_bytes[t], 0.0, 0.02,
+                         offset=e * n * k, stream=compute.handle)
+            nm.lib().naiwa_memcpy_d2h(hs.buffers[t].ptr, scratch.ptr, nbytes, compute.handle)
+            compute.sync()
+        router = nm.DeviceBuffer(E * H * 4)
+        nm.synth(nm.F32, 3000 + 8 * l + 3, E * H, router, 0.0, 0.02, stream=compute.handle)
+        stacks.append(hs)
+        routers.append(router)
+    del scratch
+    layer_bytes = (E + S_) * sum(stacks[0].expert_bytes)
+    free, total = nm.mem_info()
+    budget = int(args.budget_gb * (1 << 30)) if args.budget_gb > 0 else free
+    planned = P.plan_with_lend_depth(budget, layer_bytes, tokens, False, 0, 0, P.MAX_DEPTH)
+    if planned is None:
+        log(f"prefill-stream: nothing fits in {budget / 2**30:.1f} GiB")
+        return 1
+    stride, chunk = planned
+    depth = args.depth if args.depth > 0 else stride
+    ps = P.PrefillStream(stacks, H, I, dt, depth, copy.handle)
+    log(f"prefill-stream: {L} layers x {E}+{S_} experts in pinned host memory "
+        f"({L * layer_bytes / 1e9:.1f} GB, {layer_bytes / 2**20:.0f} MiB a layer), plan on "
+        f"{budget / 2**30:.1f} GiB: chunk {chunk}, stride {stride}; running depth {depth}; set-up {time.time() - t0:.1f}s")
+    chunk = min(chunk, tokens)
+    xs = nm.DeviceBuffer(tokens * H * 2)
+    nm.synth(nm.BF16, 998, tokens * H, xs, 0.0, 1.0, stream=compute.handle)
+    x = nm.DeviceBuffer(tokens * H * 2)
+    ids, w = nm.DeviceBuffer(chunk * K * 4), nm.DeviceBuffer(chunk * K * 4)
+    sid = nm.DeviceBuffer.from_array(np.tile(np.array([E, E + 1], dtype=np.uint32), (chunk, 1)))
+    sw = nm.DeviceBuffer.from_array(np.ones((chunk, S_), dtype=np.float32))
+    y = nm.DeviceBuffer(chunk * H * 4)
+    compute.sync()
+    lib = nm.lib()
+
+    def step() -> None:
+        lib.naiwa_memcpy_d2d(x.ptr, xs.ptr, tokens * H * 2, compute.handle)
+        for c0 in range(0, tokens, chunk):
+            T = min(chunk, tokens - c0)
+            xc = x.ptr + c0 * H * 2
+            for l in range(L):
+                nm.router_topk(xc, nm.BF16, routers[l], T, H, E, K, ids, w, mode=nm.ROUTE_SOFTMAX_TOPK,
+                               stream=compute.handle)
+                ps.forward(l, xc, ids, w, T, K, y, stream=compute.handle)
+                ps.forward(l, xc, sid, sw, T, S_, y, accumulate=True, stream=compute.handle)
+                nm._lib.check(lib.naiwa_residual_add_bf16(xc, y.ptr, T * H, compute.handle), "residual")
+
+    for _ in range(warmup):
+        step()
+    compute.sync()
+    before = ps.stats()
+    e0, e1 = nm.Event(), nm.Event()
+    e0.record(compute.handle)
+    for _ in range(steps):
+        step()
+    e1.record(compute.handle)
+    compute.sync()
+    ms = e0.elapsed_ms(e1) / steps
+    after = ps.stats()
+    moved = (after["upload_bytes"] - before["upload_bytes"]) / steps
+    tok_s = tokens / (ms / 1e3)
+    pcie = moved / (ms / 1e3) / 1e9
+    log(f"prefill-stream: {ms:.2f} ms per {tokens}-token prefill, {tok_s:.0f} tok/s, {moved / 1e9:.2f} GB uploaded "
+        f"a step, {pcie:.1f} GB/s ({pcie / 64.0 * 100:.0f}% of 64 GB/s PCIe 5.0 x16)")
+    result = {
+        "metric": "MoE prefill tok/s with host-resident experts (DeepSeek-V2-Lite shape, layer stream)",
+        "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic (device-generated N(0,0.02) Q4_K/Q8_0 experts in pinned host stacks)",
+        "config": {"workload": "DeepSeek-V2-Lite-shaped MoE prefill, 26 layers, 64 routed top-6 + 2 shared experts "
+                               "streamed from pinned host memory per layer, 2048 tokens",
+                   "layers": L, "chunk": chunk, "depth": depth, "plan_stride": stride,
+                   "plan_budget_gib": round(budget / 2**30, 1), "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "pcie", "achieved": round(pcie, 2), "peak": 64.0, "unit": "GB/s",
+                     "frac": round(pcie / 64.0, 4), "traffic": None},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def run_prefill(args) -> int:
     """DeepSeek-V2-Lite-shaped MoE prefill: 26 MoE layers, H 2048, 64 routed experts top-6
     (softmax without renormalisation) + 2 shared experts, I 1408, gate/up Q4_K, down Q8_0.
@@ -564,12 +675,12 @@ def run_prefill(args) -> int:
     tflops = flop / (ms / 1e3) / 1e12
     tok_s = tokens / (ms / 1e3)
     log(f"prefill: {ms:.2f} ms per {tokens}-token prefill, {tok_s:.0f} tok/s, {tflops:.1f} TFLOP/s "
-        f"({tflops / 2500 * 100:.1f}% of 2.5 PFLOP/s bf16 dense)")
+        f"({tflops / 2500 * 100:.1f}% of 2.5 PFLOP/s f16 dense)")
     result = {
         "metric": "MoE prefill tok/s (DeepSeek-V2-Lite shape, 2048 tokens in 512-token chunks)",
         "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16", "data": "synthetic (device-generated N(0,0.02) Q4_K/Q8_0 experts, N(0,1) bf16 tokens)",
+        "dtype": "f16", "data": "synthetic (device-generated N(0,0.02) Q4_K/Q8_0 experts, N(0,1) bf16 tokens)",
         "config": {"workload": "DeepSeek-V2-Lite-shaped MoE prefill, 26 layers, 64 routed top-6 + 2 shared "
                                "experts, I 1408, gate/up Q4_K, down Q8_0, 2048 tokens in 512-token chunks",
                    "layers": L, "hidden": H, "experts": E, "shared": S_, "top_k": K, "intermediate": I,

@@ -73,6 +73,8 @@ int naiwa_set_device(int dev);
 int naiwa_device_info(int dev, int* cu_count, int* wall_clock_khz, int64_t* hbm_bytes, char* name, int name_len);
 int naiwa_malloc(void** p, size_t bytes);          /* 256-B aligned device memory */
 int naiwa_free(void* p);
+/* Free and total bytes of the current device (hipMemGetInfo). */
+int naiwa_mem_info(uint64_t* free_bytes, uint64_t* total_bytes);
 int naiwa_host_alloc(void** p, size_t bytes);      /* pinned, portable host memory */
 int naiwa_host_free(void* p);
 int naiwa_memcpy_h2d(void* dst, const void* src, size_t bytes, int64_t stream);

@@ -100,6 +100,15 @@ int naiwa_malloc(void** p, size_t bytes) {
 
 int naiwa_free(void* p) { return naiwa_hip_rc(hipFree(p)); }
 
+int naiwa_mem_info(uint64_t* free_bytes, uint64_t* total_bytes) {
+    if (!free_bytes || !total_bytes) return NAIWA_E_INVALID;
+    size_t f = 0, t = 0;
+    const int rc = naiwa_hip_rc(hipMemGetInfo(&f, &t));
+    *free_bytes = f;
+    *total_bytes = t;
+    return rc;
+}
+
 int naiwa_host_alloc(void** p, size_t bytes) {
     if (!p) return NAIWA_E_INVALID;
     *p = nullptr;

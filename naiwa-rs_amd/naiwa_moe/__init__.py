@@ -8,8 +8,8 @@ from ._lib import (ACT_GELU_PYTORCH_TANH, ACT_SILU, BF16, E_BAD_ID, E_DEVICE, E_
                    E_NOMEM, E_NOT_FOUND, E_TIMEOUT, E_UNSUPPORTED, F16, F32, Q4_K, Q8_0,
                    ROUTE_SOFTMAX_TOPK, ROUTE_SOFTMAX_TOPK_RENORM, ROUTE_TOPK_SOFTMAX, LIB_PATH,
                    NaiwaError, lib)
-from .device import DeviceBuffer, Event, PinnedBuffer, Stream, device_count, device_info, synchronize
-from . import doorbells, gguf, policy
+from .device import DeviceBuffer, Event, PinnedBuffer, Stream, device_count, device_info, mem_info, synchronize
+from . import doorbells, gguf, policy, prefill
 from .ops import (HostExpertStacks, LayerBanks, SlotBank, expert_range, indexed_moe_fused_decode, layer_desc,
                   moe_gather, moe_prefill, router_topk, row_bytes, slot_stride, stack_decode, stack_status, synth,
                   upload_expert)
@@ -19,7 +19,7 @@ __all__ = [
     "E_FORMAT", "E_INVALID", "E_IO", "E_NOMEM", "E_NOT_FOUND", "E_TIMEOUT", "E_UNSUPPORTED",
     "ROUTE_SOFTMAX_TOPK", "ROUTE_SOFTMAX_TOPK_RENORM", "ROUTE_TOPK_SOFTMAX", "LIB_PATH",
     "NaiwaError", "lib", "DeviceBuffer", "Event", "PinnedBuffer", "Stream", "device_count",
-    "device_info", "synchronize", "LayerBanks", "SlotBank", "expert_range",
+    "device_info", "mem_info", "synchronize", "LayerBanks", "SlotBank", "expert_range",
     "indexed_moe_fused_decode", "moe_gather", "moe_prefill", "router_topk", "row_bytes", "slot_stride",
-    "layer_desc", "stack_decode", "stack_status", "synth", "policy", "doorbells", "gguf", "HostExpertStacks", "upload_expert",
+    "layer_desc", "stack_decode", "stack_status", "synth", "policy", "doorbells", "gguf", "prefill", "HostExpertStacks", "upload_expert",
 ]

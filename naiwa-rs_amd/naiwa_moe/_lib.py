@@ -75,6 +75,19 @@ class LookaheadStep(C.Structure):
                 ("pcie_bytes", C.c_int64)]
 
 
+class PrefillStreamDesc(C.Structure):
+    """naiwa_prefill_stream_desc (include/naiwa_prefill.h)."""
+    _fields_ = [("n_layers", C.c_int), ("num_experts", C.c_int), ("hidden", C.c_int), ("inter", C.c_int),
+                ("dtype_gate", C.c_int), ("dtype_up", C.c_int), ("dtype_down", C.c_int),
+                ("host_gate", C.POINTER(C.c_void_p)), ("host_up", C.POINTER(C.c_void_p)),
+                ("host_down", C.POINTER(C.c_void_p)), ("depth", C.c_int)]
+
+
+class PrefillStreamStats(C.Structure):
+    """naiwa_prefill_stream_stats (include/naiwa_prefill.h)."""
+    _fields_ = [("uploads", C.c_uint64), ("upload_bytes", C.c_uint64), ("forwards", C.c_uint64)]
+
+
 STATS_FIELDS = ("hits", "promotions", "misses", "staged", "lookahead_loads", "swaps", "lookahead_dropped",
                 "sync_waits", "pcie_misses", "pcie_bytes", "result_stalls")
 
@@ -93,6 +106,7 @@ _P = C.POINTER
 SIGNATURES: dict[str, tuple] = {
     "naiwa_status_string": (C.c_char_p, [i32]),
     "naiwa_device_count": (i32, [_P(i32)]),
+    "naiwa_mem_info": (i32, [_P(u64), _P(u64)]),
     "naiwa_set_device": (i32, [i32]),
     "naiwa_device_info": (i32, [i32, _P(i32), _P(i32), _P(i64), C.c_char_p, i32]),
     "naiwa_malloc": (i32, [_P(vp), C.c_size_t]),
@@ -208,6 +222,14 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_stats_read": (i32, [vp, i32]),
     "naiwa_stats_add": (i32, [vp]),
     # include/naiwa_gguf.h
+    "naiwa_prefill_chunk_scratch": (u64, [i32]),
+    "naiwa_prefill_activation_bytes": (u64, [i32]),
+    "naiwa_prefill_plan": (i32, [u64, u64, i32, i32, u64, u64, i32, _P(i32), _P(i32)]),
+    "naiwa_prefill_stream_create": (i32, [_P(PrefillStreamDesc), i64, _P(vp)]),
+    "naiwa_prefill_stream_destroy": (i32, [vp]),
+    "naiwa_prefill_stream_forward": (i32, [vp, i32, vp, vp, vp, i32, i32, i32, vp, i32, i64]),
+    "naiwa_prefill_stream_banks": (i32, [vp, i32, vp, vp, vp]),
+    "naiwa_prefill_stream_stats_read": (i32, [vp, _P(PrefillStreamStats)]),
     "naiwa_profile_read": (i32, [C.c_char_p, i32, i32, _P(vp)]),
     "naiwa_profile_destroy": (i32, [vp]),
     "naiwa_profile_layer": (i32, [vp, i32, vp, i32, _P(i32)]),

@@ -27,6 +27,13 @@ def device_info(dev: int = 0) -> dict:
             "arch": name.value.decode()}
 
 
+def mem_info() -> tuple[int, int]:
+    """(free, total) bytes of the current device."""
+    f, t = C.c_uint64(0), C.c_uint64(0)
+    check(lib().naiwa_mem_info(C.byref(f), C.byref(t)), "mem_info")
+    return f.value, t.value
+
+
 def synchronize() -> None:
     check(lib().naiwa_device_sync(), "device sync")
 
