@@ -66,7 +66,7 @@ constexpr int kMaxE = 256;
 constexpr int kLeaders = 32;              // workgroups that add the router partials
 constexpr int kChunk = NAIWA_ROUTER_CHUNK; // output features per phase-C chunk
 constexpr int kMaxChunks = 4;             // chunks per workgroup
-constexpr int kCPairs = 16;               // h vectors staged per phase-C pass
+constexpr int kCPairs = 32;               // h vectors staged per phase-C pass, at most
 constexpr int kTraceSlots = 24;
 constexpr int kMaxLayers = 128;           // layer descriptors kept in LDS (tags hold layer + 1 < 256)
 constexpr int kXG = 8;                    // activation groups (4 values) per thread per poll round
@@ -102,6 +102,7 @@ struct Params {
     int bitems;                  // Q4_K gate/up: (segment, row pair) items per LDS round
     int hpairs;                  // h vectors staged per phase-C pass
     int dpre;                    // Q4_K down: pairs whose rows are prefetched into LDS (0 = none)
+    int hwb_bytes;               // LDS shared by the phase-B gate/up rounds and the phase-C h staging
     int trace_layer;             // the layer being traced (diagnostics)
 };
 
@@ -807,12 +808,15 @@ stack_kernel(Params p) {
     const int gpt_h = H / 4;                  // 4-value groups per token
     const int half_h = H / 2;                 // tagged words per token
     const int nlog = rows * E;
-    uint8_t* const hdyn = dyn + rows * xstage;      // h staging, after the activations
+    // after the activations, one region serves the gate/up rounds of phase B (wb) and the
+    // h staging of phase C (hw, hs): a barrier separates the last read of one from the
+    // first write of the other, in a layer and across layers
+    uint8_t* const hdyn = dyn + rows * xstage;
+    uint8_t* const wb = hdyn;                       // gate/up rounds
     uint32_t* const hw = (uint32_t*)hdyn;           // [hpairs][I/2] words
     float* const hs = (float*)(hdyn + (size_t)p.hpairs * I * 2); // [hpairs][I / kSumSpan] sums
-    uint8_t* const dbuf = hdyn + p.hpairs * hstage; // prefetched down rows: [pair][kChunk][drb]
+    uint8_t* const dbuf = hdyn + p.hwb_bytes;       // prefetched down rows: [pair][kChunk][drb]
     float* const rbuf = (float*)(dbuf + (size_t)p.dpre * kChunk * drb); // next router columns [E][kChunk]
-    uint8_t* const wb = (uint8_t*)(rbuf + (size_t)E * kChunk);           // gate/up rounds
 
     // ---- prologue: layer descriptors into LDS; own chunks of x; layer-0 logits ----
     p.trace_layer = p.n_layers; // the prologue's row of the trace
@@ -1415,34 +1419,40 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     if (fg == NAIWA_Q4_K && H > 8 * NAIWA_QK_K) return NAIWA_E_UNSUPPORTED; // one block per lane: H <= 2048
     // dynamic LDS: activations | h staging
     constexpr size_t kMaxDynLds = 104 * 1024;   // 160 KB per CU minus the static LDS
-    const int hpairs = std::min(kCPairs, rows * k);
     const size_t lds_x = (size_t)rows * fused_xstage(fg, H);
-    const size_t lds_h = (size_t)hpairs * naiwa_stage_bytes(fd, I);
-    size_t lds = lds_x + lds_h;
-    if (lds > kMaxDynLds) return NAIWA_E_UNSUPPORTED;
-    lds += (size_t)E * kChunk * 4; // the next layer's router columns of the first chunk
-    if (lds > kMaxDynLds) return NAIWA_E_UNSUPPORTED;
-    // Q4_K down rows of the first phase-C pass, prefetched into LDS when they fit
-    // beside at least one gate/up item
+    const size_t lds_r = (size_t)E * kChunk * 4; // the next layer's router columns of the first chunk
+    // activations | max(h staging, gate/up rounds) | prefetched down rows | router columns
+    const size_t item = fg == NAIWA_Q4_K ? 4 * (size_t)naiwa_row_bytes(NAIWA_Q4_K, H) : 0;
+    // h vectors per phase-C pass: as many as the pairs need, up to kCPairs, within the LDS
+    int hpairs = std::min(kCPairs, rows * k);
+    const size_t hstage = (size_t)naiwa_stage_bytes(fd, I);
+    while (hpairs > 1 && lds_x + std::max((size_t)hpairs * hstage, item) + lds_r > kMaxDynLds) --hpairs;
+    const size_t lds_h = (size_t)hpairs * hstage;
+    if (lds_x + std::max(lds_h, item) + lds_r > kMaxDynLds) return NAIWA_E_UNSUPPORTED;
+    // Q4_K down rows of the first phase-C pass, prefetched into LDS when phase C makes
+    // a single pass (rows * k <= hpairs) and they fit beside one gate/up item
     int dpre = 0;
-    if (fd == NAIWA_Q4_K) {
+    size_t lds_pre = 0;
+    if (fd == NAIWA_Q4_K && rows * k <= hpairs) {
         const size_t pre = (size_t)hpairs * kChunk * (size_t)naiwa_row_bytes(NAIWA_Q4_K, I);
-        const size_t gu = fg == NAIWA_Q4_K ? 4 * (size_t)naiwa_row_bytes(NAIWA_Q4_K, H) : 0;
-        if (lds + pre + gu <= kMaxDynLds) {
+        if (lds_x + std::max(lds_h, item) + pre + lds_r <= kMaxDynLds) {
             dpre = hpairs;
-            lds += pre;
+            lds_pre = pre;
         }
     }
-    // Q4_K gate/up rounds: at most one item per 16-lane group, at most what one
-    // workgroup's share of a full step needs, within the LDS left over
+    // Q4_K gate/up rounds: at most one item per 32-lane half-wave, at most what one
+    // workgroup's share of a full step needs, within the LDS left over (the h staging
+    // of phase C reuses the same bytes)
     int bitems = 0;
     if (fg == NAIWA_Q4_K) {
-        const size_t item = 4 * (size_t)naiwa_row_bytes(NAIWA_Q4_K, H);
         const int share = (rows * k * (I / 2) + 255) / 256;
-        bitems = (int)std::min<size_t>((size_t)std::min(kThreads / 32, share), (kMaxDynLds - lds) / item);
+        bitems = (int)std::min<size_t>((size_t)std::min(kThreads / 32, share),
+                                       (kMaxDynLds - lds_x - lds_pre - lds_r) / item);
         if (bitems < 1) return NAIWA_E_UNSUPPORTED;
-        lds += (size_t)bitems * item;
     }
+    const size_t hwb = (std::max(lds_h, (size_t)bitems * item) + 15) & ~size_t(15);
+    size_t lds = lds_x + hwb + lds_pre + lds_r;
+    if (lds > kMaxDynLds) return NAIWA_E_UNSUPPORTED;
 
     hipStream_t st = (hipStream_t)stream;
     int rc = 0, dev = 0, cus = 0, khz = 0;
@@ -1549,6 +1559,7 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     prm.bitems = bitems;
     prm.hpairs = hpairs;
     prm.dpre = dpre;
+    prm.hwb_bytes = (int)hwb;
     prm.trace = g_trace_enabled ? (unsigned long long*)naiwa_scratch(
                                       NAIWA_SCRATCH_STACK + 2, (size_t)blocks * (n_layers + 1) * kTraceSlots * 8, &rc)
                                 : nullptr;
