@@ -157,6 +157,15 @@ int64_t naiwa_projection_bytes(int dtype, int64_t n, int64_t k);
 int naiwa_moe_decode(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down,
                      const void* x, int x_dtype, const uint32_t* slot_ids, const float* w,
                      int rows, int width, int act, float* out, int64_t stream);
+/* As naiwa_moe_decode; flags NAIWA_DECODE_ACCUMULATE continues each output
+ * row's sum from out's values, so a call over the pairs of low slots and then
+ * an accumulating call over the pairs of higher slots add exactly the terms,
+ * in exactly the order, of one call over both (e.g. cache slots first, then
+ * staging slots whose upload is still landing). */
+#define NAIWA_DECODE_ACCUMULATE 1
+int naiwa_moe_decode_ex(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down,
+                        const void* x, int x_dtype, const uint32_t* slot_ids, const float* w,
+                        int rows, int width, int act, float* out, int flags, int64_t stream);
 
 /* Router: logits = W . x with the chunked fixed-point accumulation (chunks of 8
  * features summed as an f32 fma chain, each rounded to int64 with 32

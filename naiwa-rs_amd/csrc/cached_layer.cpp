@@ -39,6 +39,8 @@ struct naiwa_cached_layer {
     float* w_h = nullptr;
     int32_t* slots_h = nullptr;
     uint32_t* slots_up = nullptr;  // pinned source of the slot-id upload
+    float* wsplit_h = nullptr;     // pinned: weights of the cache pairs | of the staged pairs
+    float* wsplit_dev = nullptr;
     int last_rows = 0;
     std::vector<hipEvent_t> ring_fence;  // per ring position: recorded after the step that read it
     std::vector<char> ring_fenced;
@@ -64,6 +66,10 @@ struct naiwa_cached_layer {
         if (w_h) (void)hipHostFree(w_h);
         if (slots_h) (void)hipHostFree(slots_h);
         if (slots_up) (void)hipHostFree(slots_up);
+        if (wsplit_h) (void)hipHostFree(wsplit_h);
+        if (wsplit_dev) (void)hipFree(wsplit_dev);
+        wsplit_h = nullptr;
+        wsplit_dev = nullptr;
         if (pred_ids_dev) (void)hipFree(pred_ids_dev);
         if (pred_w_dev) (void)hipFree(pred_w_dev);
         if (pred_ids_h) (void)hipHostFree(pred_ids_h);
@@ -92,7 +98,8 @@ struct naiwa_cached_layer {
             hipMalloc(&slots_dev, n * 4) != hipSuccess || hipHostMalloc(&ids_h, n * 4, 0) != hipSuccess ||
             hipHostMalloc(&w_h, n * 4, 0) != hipSuccess || hipHostMalloc(&slots_h, n * 4, 0) != hipSuccess ||
             hipHostMalloc(&slots_up, n * 4, 0) != hipSuccess || hipMalloc(&pred_ids_dev, n * 4) != hipSuccess ||
-            hipMalloc(&pred_w_dev, n * 4) != hipSuccess || hipHostMalloc(&pred_ids_h, n * 4, 0) != hipSuccess) {
+            hipMalloc(&pred_w_dev, n * 4) != hipSuccess || hipHostMalloc(&pred_ids_h, n * 4, 0) != hipSuccess ||
+            hipHostMalloc(&wsplit_h, 2 * n * 4, 0) != hipSuccess || hipMalloc(&wsplit_dev, 2 * n * 4) != hipSuccess) {
             release_buffers();
             return NAIWA_E_NOMEM;
         }
@@ -244,23 +251,42 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         step.pcie_bytes += (int64_t)(L->bytes[0] + L->bytes[1] + L->bytes[2]);
     }
     step.staged_experts = nc;
-    if (nc) {
-        if ((rc = naiwa_hip_rc(hipEventRecord(L->staged_done, L->copy))) ||
-            (rc = naiwa_hip_rc(hipStreamWaitEvent(st, L->staged_done, 0))))
-            return rc;
-    }
+    if (nc && (rc = naiwa_hip_rc(hipEventRecord(L->staged_done, L->copy)))) return rc;
 
-    // the expert kernel over cache + ring slots, after the latest lookahead claim
-    // (src/moe/cached_layer.rs:808-819): a slot it published may still be in flight
+    // the expert kernel after the latest lookahead claim (src/moe/cached_layer.rs:808-819):
+    // a slot it published may still be in flight
     if ((rc = naiwa_hip_rc(hipMemcpyAsync(L->slots_dev, L->slots_up, (size_t)n * 4, hipMemcpyHostToDevice, st))))
         return rc;
     if (L->ahead_claimed) {
         if ((rc = naiwa_hip_rc(hipStreamWaitEvent(st, L->ahead_done, 0)))) return rc;
         ++step.preload_waits;
     }
-    if ((rc = naiwa_moe_decode(&d.gate, &d.up, &d.down, x, NAIWA_BF16, L->slots_dev, L->w_dev, rows, k, d.act, out,
-                               stream)))
-        return rc;
+    if (!nc) {
+        if ((rc = naiwa_moe_decode(&d.gate, &d.up, &d.down, x, NAIWA_BF16, L->slots_dev, L->w_dev, rows, k, d.act,
+                                   out, stream)))
+            return rc;
+    } else {
+        // the cache pairs first, while the staged experts are still on the wire, then the
+        // staged pairs added on top: ring slots sort after cache slots, so the two calls
+        // add the terms of one call in its order (src/moe/decode.rs:226-233 runs the
+        // resident experts before the staging wait for the same reason)
+        float* w_res = L->wsplit_h;
+        float* w_stg = L->wsplit_h + n;
+        for (int i = 0; i < n; ++i) {
+            const bool staged_pair = L->slots_up[i] >= (uint32_t)d.usable;
+            w_res[i] = staged_pair ? 0.0f : L->w_h[i];
+            w_stg[i] = staged_pair ? L->w_h[i] : 0.0f;
+        }
+        if ((rc = naiwa_hip_rc(hipMemcpyAsync(L->wsplit_dev, L->wsplit_h, (size_t)n * 8, hipMemcpyHostToDevice, st))))
+            return rc;
+        if ((rc = naiwa_moe_decode_ex(&d.gate, &d.up, &d.down, x, NAIWA_BF16, L->slots_dev, L->wsplit_dev, rows, k,
+                                      d.act, out, 0, stream)))
+            return rc;
+        if ((rc = naiwa_hip_rc(hipStreamWaitEvent(st, L->staged_done, 0)))) return rc;
+        if ((rc = naiwa_moe_decode_ex(&d.gate, &d.up, &d.down, x, NAIWA_BF16, L->slots_dev, L->wsplit_dev + n, rows,
+                                      k, d.act, out, NAIWA_DECODE_ACCUMULATE, stream)))
+            return rc;
+    }
     for (int i = 0; i < nc; ++i) {
         if ((rc = naiwa_hip_rc(hipEventRecord(L->ring_fence[pos[i]], st)))) return rc;
         L->ring_fenced[pos[i]] = 1;

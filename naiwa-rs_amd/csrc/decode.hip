@@ -107,7 +107,7 @@ template <int DT>
 __global__ void __launch_bounds__(kThreads)
 down_kernel(BankArg down, int H, int I, int rows, int width, int tok_max, const int* seg_count,
             const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm,
-            const float* w, const float* hbuf, float* out) {
+            const float* w, const float* hbuf, int accumulate, float* out) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, grp = tid / NAIWA_GROUP, lr = tid % NAIWA_GROUP;
     const int r = blockIdx.x * kRowsPerBlock + grp;
@@ -115,7 +115,11 @@ down_kernel(BankArg down, int H, int I, int rows, int width, int tok_max, const 
     const int acc_bytes = ((rows * kRowsPerBlock * 4) + 15) & ~15;
     uint8_t* stage_base = smem + acc_bytes;
     const int stage = naiwa_stage_bytes(DT, I);
-    for (int i = tid; i < rows * kRowsPerBlock; i += kThreads) acc[i] = 0.0f;
+    // the sum starts at 0, or at out's values (the same additions as one call over both sets)
+    for (int i = tid; i < rows * kRowsPerBlock; i += kThreads) {
+        const int rr = blockIdx.x * kRowsPerBlock + i % kRowsPerBlock;
+        acc[i] = accumulate && rr < H ? out[(int64_t)(i / kRowsPerBlock) * H + rr] : 0.0f;
+    }
     const int nseg = *seg_count;
     const int nu = Fmt<DT>::units(I);
     constexpr int UM = Umax<DT>::v;
@@ -187,10 +191,11 @@ int tok_cap(int dtype, int k) {
 
 } // namespace
 
-extern "C" int naiwa_moe_decode(const naiwa_bank* gate, const naiwa_bank* up,
-                                const naiwa_bank* down, const void* x, int x_dtype,
-                                const uint32_t* slot_ids, const float* w, int rows, int width,
-                                int act, float* out, int64_t stream) {
+extern "C" int naiwa_moe_decode_ex(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down,
+                                   const void* x, int x_dtype, const uint32_t* slot_ids, const float* w, int rows,
+                                   int width, int act, float* out, int flags, int64_t stream) {
+    if (flags & ~NAIWA_DECODE_ACCUMULATE) return NAIWA_E_INVALID;
+    const int accumulate = (flags & NAIWA_DECODE_ACCUMULATE) ? 1 : 0;
     if (!bank_ok(gate) || !bank_ok(up) || !bank_ok(down)) return NAIWA_E_INVALID;
     if (gate->dtype != up->dtype) return NAIWA_E_UNSUPPORTED;
     const int H = gate->k, I = gate->n;
@@ -205,7 +210,7 @@ extern "C" int naiwa_moe_decode(const naiwa_bank* gate, const naiwa_bank* up,
     hipStream_t st = (hipStream_t)stream;
     if (rows == 0) return NAIWA_OK;
     if (!x || !out || (width > 0 && (!slot_ids || !w))) return NAIWA_E_INVALID;
-    if (width == 0) return naiwa_hip_rc(hipMemsetAsync(out, 0, (size_t)rows * H * 4, st));
+    if (width == 0) return accumulate ? NAIWA_OK : naiwa_hip_rc(hipMemsetAsync(out, 0, (size_t)rows * H * 4, st));
     const int tok_g = tok_cap(gate->dtype, H), tok_d = tok_cap(down->dtype, I);
     if (!tok_g || !tok_d) return NAIWA_E_UNSUPPORTED;
     const int acc_bytes = ((rows * kRowsPerBlock * 4) + 15) & ~15;
@@ -254,16 +259,22 @@ extern "C" int naiwa_moe_decode(const naiwa_bank* gate, const naiwa_bank* up,
     switch (naiwa_kernel_fmt(down->dtype, I)) {
     case NAIWA_Q4_K:
         down_kernel<NAIWA_Q4_K><<<dgrid, kThreads, lds_down, st>>>(
-            d, H, I, rows, width, tok_d, seg_count, seg_key, seg_begin, perm, w, hbuf, out);
+            d, H, I, rows, width, tok_d, seg_count, seg_key, seg_begin, perm, w, hbuf, accumulate, out);
         break;
     case NAIWA_Q8_0:
         down_kernel<NAIWA_Q8_0><<<dgrid, kThreads, lds_down, st>>>(
-            d, H, I, rows, width, tok_d, seg_count, seg_key, seg_begin, perm, w, hbuf, out);
+            d, H, I, rows, width, tok_d, seg_count, seg_key, seg_begin, perm, w, hbuf, accumulate, out);
         break;
     default:
         down_kernel<NAIWA_Q8_0_ODD><<<dgrid, kThreads, lds_down, st>>>(
-            d, H, I, rows, width, tok_d, seg_count, seg_key, seg_begin, perm, w, hbuf, out);
+            d, H, I, rows, width, tok_d, seg_count, seg_key, seg_begin, perm, w, hbuf, accumulate, out);
         break;
     }
     return naiwa_hip_rc(hipGetLastError());
+}
+
+extern "C" int naiwa_moe_decode(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down,
+                                const void* x, int x_dtype, const uint32_t* slot_ids, const float* w, int rows,
+                                int width, int act, float* out, int64_t stream) {
+    return naiwa_moe_decode_ex(gate, up, down, x, x_dtype, slot_ids, w, rows, width, act, out, 0, stream);
 }

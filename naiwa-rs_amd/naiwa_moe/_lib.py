@@ -142,6 +142,7 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_host_wait_ge": (i32, [vp, u32, i64, i64]),
     "naiwa_projection_bytes": (i64, [i32, i64, i64]),
     "naiwa_moe_decode": (i32, [_P(Bank), _P(Bank), _P(Bank), vp, i32, vp, vp, i32, i32, i32, vp, i64]),
+    "naiwa_moe_decode_ex": (i32, [_P(Bank), _P(Bank), _P(Bank), vp, i32, vp, vp, i32, i32, i32, vp, i32, i64]),
     "naiwa_router_topk": (i32, [vp, i32, vp, i32, i32, i32, i32, i32, vp, vp, vp, i64]),
     "naiwa_router_topk_biased": (i32, [vp, i32, vp, vp, i32, i32, i32, i32, i32, vp, vp, vp, i64]),
     "naiwa_moe_prefill": (i32, [_P(Bank), _P(Bank), _P(Bank), vp, vp, vp, i32, i32, i32, vp, i32, i64]),

@@ -127,12 +127,14 @@ def upload_expert(banks: "LayerBanks", slot: int, stacks: HostExpertStacks, expe
 
 
 def indexed_moe_fused_decode(banks: LayerBanks, x, x_dtype: int, slot_ids, weights, rows: int,
-                             topk: int, out, act: int = ACT_SILU, stream: int = 0) -> None:
-    """out[rows, hidden] f32 = sum_j w[t,j] * expert(slot_ids[t,j])(x[t]); all device pointers."""
+                             topk: int, out, act: int = ACT_SILU, stream: int = 0, accumulate: bool = False) -> None:
+    """out[rows, hidden] f32 = sum_j w[t,j] * expert(slot_ids[t,j])(x[t]); all device pointers.
+    accumulate: the sums continue from out (naiwa_moe_decode_ex)."""
     g, u, d = banks.gate.desc(), banks.up.desc(), banks.down.desc()
-    rc = lib().naiwa_moe_decode(C.byref(g), C.byref(u), C.byref(d), _dev(x), x_dtype,
-                                _dev(slot_ids), _dev(weights), rows, topk, act, _dev(out), stream)
-    check(rc, "naiwa_moe_decode")
+    rc = lib().naiwa_moe_decode_ex(C.byref(g), C.byref(u), C.byref(d), _dev(x), x_dtype,
+                                   _dev(slot_ids), _dev(weights), rows, topk, act, _dev(out),
+                                   1 if accumulate else 0, stream)
+    check(rc, "naiwa_moe_decode_ex")
 
 
 def moe_prefill(banks: LayerBanks, x, slot_ids, weights, T: int, topk: int, out, act: int = ACT_SILU,

@@ -179,3 +179,28 @@ def test_decode_is_deterministic(gpu):
     a = run_decode(nm, g, u, d, dt, H, I, x, ids, w)
     b = run_decode(nm, g, u, d, dt, H, I, x, ids, w)
     assert np.array_equal(a, b)
+
+
+def test_split_by_slot_with_accumulate_is_bit_identical(gpu):
+    """A call over the pairs of low slots, then an accumulating call over the pairs of
+    higher slots, equals one call over all pairs bit for bit (the partial-cache step runs
+    the cache slots while the staged ones are still landing)."""
+    nm = gpu
+    H, I, E, k, rows = 512, 256, 12, 4, 5
+    dt = (O.Q4_K, O.Q4_K, O.Q8_0)
+    g, u, d, r = S.layer(2100, E, H, I, dt)
+    banks = nm.LayerBanks(E, H, I, dt)
+    for e in range(E):
+        banks.load(e, g[e], u[e], d[e])
+    x = S.activations_bf16(2101, rows, H)
+    ids, w = O.topk(O.router_logits(O.from_bf16(x), r), k)
+    xd, idd = nm.DeviceBuffer.from_array(x), nm.DeviceBuffer.from_array(ids.astype(np.uint32))
+    whole, split = nm.DeviceBuffer(rows * H * 4), nm.DeviceBuffer(rows * H * 4)
+    nm.indexed_moe_fused_decode(banks, xd, nm.BF16, idd, nm.DeviceBuffer.from_array(w), rows, k, whole)
+    for cut in (3, 7, 11):
+        lo = nm.DeviceBuffer.from_array(np.where(ids < cut, w, 0.0).astype(np.float32))
+        hi = nm.DeviceBuffer.from_array(np.where(ids >= cut, w, 0.0).astype(np.float32))
+        nm.indexed_moe_fused_decode(banks, xd, nm.BF16, idd, lo, rows, k, split)
+        nm.indexed_moe_fused_decode(banks, xd, nm.BF16, idd, hi, rows, k, split, accumulate=True)
+        nm.synchronize()
+        assert np.array_equal(whole.download(np.float32), split.download(np.float32)), cut
