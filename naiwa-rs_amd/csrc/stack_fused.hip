@@ -72,6 +72,7 @@ constexpr int kMaxLayers = 128;           // layer descriptors kept in LDS (tags
 constexpr int kXG = 8;                    // activation groups (4 values) per thread per poll round
 constexpr int kHG = 4;                    // h groups (4 values, 2 words) per thread per poll round
 constexpr int kCB = 2;                    // down rows per group in flight (general path)
+constexpr int kDU8 = 3;                   // Q4_K down from LDS: units per lane of an 8-lane row group
 
 struct LayerDev {
     const float* router;
@@ -1054,15 +1055,17 @@ stack_kernel(Params p) {
         if constexpr (DG == NAIWA_Q4_K) {
             // rounds of up to p.bitems items: the gate and up row pairs of each item
             // are gathered into LDS with coalesced 16-byte DMA pieces by the wave
-            // that computes it (items w and w + 8 of a round go to wave w, on its
-            // two 32-lane halves), so each wave waits for its own pieces only
+            // that computes it, so each wave waits for its own pieces only.  Items i
+            // and i + 8 of a round go to wave (i + 1) % 8, on its two 32-lane halves:
+            // wave 0, which also computes the routing weights, gets the last ones
             const int pair_pieces = (int)(rb / 8);       // two rows, 16-byte pieces
             const size_t item_bytes = 4 * (size_t)rb;
             const int half = (tid >> 5) & 1, il = tid & 31;
-            const int my_item = wave + 8 * half;
+            const int wslot = (wave + 7) % 8;
+            const int my_item = wslot + 8 * half;
             for (int r0 = q0; r0 < q1; r0 += p.bitems) {
                 const int nr = min(p.bitems, q1 - r0);
-                for (int i = wave; i < nr; i += kThreads / 64) {
+                for (int i = wslot; i < nr; i += kThreads / 64) {
                     const int q = r0 + i;
                     const uint32_t slot = sm.seg_slot[q / I2];
                     const int64_t roff = (int64_t)(2 * (q % I2)) * rb;
@@ -1199,10 +1202,37 @@ stack_kernel(Params p) {
                             }
                         }
                     };
-                    if (DD == NAIWA_Q4_K && from_lds)
-                        dots(std::integral_constant<int, NAIWA_AS_LDS>());
-                    else
+                    if constexpr (DD == NAIWA_Q4_K) {
+                        if (from_lds && kChunk * nbp <= kThreads / 8 && dnu <= 8 * kDU8) {
+                            // one 8-lane group per (feature, pair) row, at most kDU8 units
+                            // (32 values) per lane: every lane busy at I = 768 (24 units)
+                            const int g8 = tid >> 3, l8 = tid & 7;
+                            const bool in = g8 < kChunk * nbp;
+                            const int fi = in ? g8 % kChunk : 0, pi = in ? g8 / kChunk : 0;
+                            const uint8_t* drow = dbuf + (size_t)(pi * kChunk + fi) * drb;
+                            const uint32_t* words = hw + (size_t)pi * (I / 2);
+                            const float* sums = hs + (size_t)pi * (I / Fmt<DD>::kSumSpan);
+                            typename Fmt<DD>::Frag frg[kDU8];
+#pragma unroll
+                            for (int i = 0; i < kDU8; ++i)
+                                if (in && l8 + 8 * i < dnu) frg[i] = Fmt<DD>::template load<NAIWA_AS_LDS>(drow, l8 + 8 * i);
+                            float acc = 0.0f;
+#pragma unroll
+                            for (int i = 0; i < kDU8; ++i)
+                                if (in && l8 + 8 * i < dnu) acc += Fmt<DD>::dot(frg[i], l8 + 8 * i, words, sums);
+                            const float v = naiwa_group_sum<8>(acc);
+                            if (in && l8 == 0) {
+                                const float w = sm.pair_w[sm.sorted[b0 + pi]];
+                                sm.partial[fi][b0 + pi] = w != 0.0f ? v * w : 0.0f;
+                            }
+                        } else if (from_lds) {
+                            dots(std::integral_constant<int, NAIWA_AS_LDS>());
+                        } else {
+                            dots(std::integral_constant<int, NAIWA_AS_GLOBAL>());
+                        }
+                    } else {
                         dots(std::integral_constant<int, NAIWA_AS_GLOBAL>());
+                    }
                 }
                 // prefetched pieces have landed even when no pass ran (no valid pair)
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
