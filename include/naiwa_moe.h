@@ -255,6 +255,22 @@ int naiwa_residual_add_bf16(void* x, const float* y, int64_t n, int64_t stream);
 int naiwa_upload_expert(void* const dst[3], const void* const src[3], const size_t bytes[3],
                         int64_t copy_stream, int64_t read_fence, int64_t done_event);
 
+/* Many host -> device ranges in one kernel on `stream` (the uploads of a     */
+/* layer's staged experts, queued in the reference as one CopyStream copy    */
+/* per projection, src/copy_stream.rs:387-409).  Every src must lie in      */
+/* pinned host memory mapped for the device (naiwa_host_alloc), every dst   */
+/* in device memory; src, dst and bytes 16-byte aligned.  Sources are        */
+/* checked before the launch: NAIWA_E_UNSUPPORTED (nothing queued) when one  */
+/* is not mapped pinned memory or not aligned, and the caller copies those   */
+/* another way.  The ranges must not overlap.                                */
+#define NAIWA_COPY_BATCH_MAX 64
+typedef struct naiwa_copy {
+    void* dst;
+    const void* src;
+    uint64_t bytes;
+} naiwa_copy;
+int naiwa_copy_batch(const naiwa_copy* items, int n, int64_t stream);
+
 /* ======================================================================== */
 /* Synthetic data (benchmarks and tests): n values of the N(mean, std)       */
 /* stream (seed, offset) -- value i depends only on (seed, offset + i) --    */

@@ -13,6 +13,7 @@
 
 #include "../../include/naiwa_cached.h"
 #include "common.h"
+#include "upload.h"
 
 namespace {
 
@@ -45,6 +46,8 @@ struct naiwa_cached_layer {
     std::vector<hipEvent_t> ring_fence;  // per ring position: recorded after the step that read it
     std::vector<char> ring_fenced;
     hipEvent_t staged_done = nullptr;
+    bool batch_uploads = false;          // staged uploads as one batched copy kernel, reading
+    const void* host_dev[3] = {nullptr, nullptr, nullptr}; // the host stacks' device views
     // lookahead: this layer's prediction (its router on the previous layer's
     // activation), the fence after the last step that read its cache slots,
     // and the claim a forward waits for before its expert kernel
@@ -240,23 +243,39 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         }
     }
 
-    // uploads on the copy stream, each after the last step that read its ring slot
-    for (int i = 0; i < nc; ++i) {
-        void* dst[3];
-        const void* src[3];
-        L->slot_ptrs(d.usable + pos[i], dst);
-        L->host_ptrs((int)chosen[i], src);
-        const int64_t fence = L->ring_fenced[pos[i]] ? (int64_t)L->ring_fence[pos[i]] : 0;
-        if ((rc = naiwa_upload_expert(dst, src, L->bytes, (int64_t)L->copy, fence, 0))) return rc;
-        step.pcie_bytes += (int64_t)(L->bytes[0] + L->bytes[1] + L->bytes[2]);
+    // uploads on the copy stream after the last step that read each ring slot: one kernel
+    // for all of them when the host stacks are mapped pinned memory, else one DMA copy per
+    // projection
+    {
+        naiwa_copy items[NAIWA_COPY_BATCH_MAX];
+        int ni = 0;
+        const bool batch = L->batch_uploads && 3 * nc <= NAIWA_COPY_BATCH_MAX;
+        for (int i = 0; i < nc; ++i) {
+            void* dst[3];
+            L->slot_ptrs(d.usable + pos[i], dst);
+            if (batch) {
+                for (int p = 0; p < 3; ++p)
+                    items[ni++] = naiwa_copy{dst[p], (const uint8_t*)L->host_dev[p] + (size_t)chosen[i] * L->bytes[p],
+                                             (uint64_t)L->bytes[p]};
+                if (L->ring_fenced[pos[i]] && (rc = naiwa_hip_rc(hipStreamWaitEvent(L->copy, L->ring_fence[pos[i]], 0))))
+                    return rc;
+            } else {
+                const void* src[3];
+                L->host_ptrs((int)chosen[i], src);
+                const int64_t fence = L->ring_fenced[pos[i]] ? (int64_t)L->ring_fence[pos[i]] : 0;
+                if ((rc = naiwa_upload_expert(dst, src, L->bytes, (int64_t)L->copy, fence, 0))) return rc;
+            }
+        }
+        if (batch && (rc = naiwa_copy_batch_mapped(items, ni, (int64_t)L->copy))) return rc;
+        step.pcie_bytes += (int64_t)nc * (int64_t)(L->bytes[0] + L->bytes[1] + L->bytes[2]);
     }
     step.staged_experts = nc;
     if (nc && (rc = naiwa_hip_rc(hipEventRecord(L->staged_done, L->copy)))) return rc;
 
-    // the expert kernel after the latest lookahead claim (src/moe/cached_layer.rs:808-819):
-    // a slot it published may still be in flight
     if ((rc = naiwa_hip_rc(hipMemcpyAsync(L->slots_dev, L->slots_up, (size_t)n * 4, hipMemcpyHostToDevice, st))))
         return rc;
+    // the expert kernel after the latest lookahead claim (src/moe/cached_layer.rs:808-819):
+    // a slot it published may still be in flight
     if (L->ahead_claimed) {
         if ((rc = naiwa_hip_rc(hipStreamWaitEvent(st, L->ahead_done, 0)))) return rc;
         ++step.preload_waits;
@@ -357,6 +376,17 @@ int naiwa_cached_layer_create(const naiwa_cached_layer_desc* d, naiwa_ring* ring
     L->bytes[0] = (size_t)naiwa_projection_bytes(d->gate.dtype, d->inter, d->hidden);
     L->bytes[1] = (size_t)naiwa_projection_bytes(d->up.dtype, d->inter, d->hidden);
     L->bytes[2] = (size_t)naiwa_projection_bytes(d->down.dtype, d->hidden, d->inter);
+    // staged uploads read the host stacks through their device mapping when all three
+    // are mapped pinned memory and every expert range is 16-byte aligned
+    {
+        const void* hs[3] = {d->host_gate, d->host_up, d->host_down};
+        bool ok = true;
+        for (int p = 0; p < 3 && ok; ++p) {
+            L->host_dev[p] = naiwa_device_view(hs[p], L->bytes[p] * (size_t)d->num_experts);
+            ok = L->host_dev[p] && !(((uintptr_t)L->host_dev[p] | L->bytes[p]) & 15);
+        }
+        L->batch_uploads = ok;
+    }
     int rc = naiwa_cache_create(d->num_experts, d->usable, d->usable, &L->cache);
     if (rc) {
         delete L;

@@ -797,7 +797,6 @@ stack_kernel(Params p) {
     const int H = p.H, I = p.I, E = p.E, k = p.k, rows = p.rows;
     const int npairs = rows * k;
     const int xstage = fused_xstage(DG, H);
-    const int hstage = naiwa_stage_bytes(DD, I);
     const int nchunks = H / kChunk;
     const int nprod = min(G, nchunks);        // workgroups that own chunks
     const int nlead = min(kLeaders, G);

@@ -10,9 +10,9 @@ from ._lib import (ACT_GELU_PYTORCH_TANH, ACT_SILU, BF16, E_BAD_ID, E_DEVICE, E_
                    NaiwaError, lib)
 from .device import DeviceBuffer, Event, PinnedBuffer, Stream, device_count, device_info, mem_info, synchronize
 from . import doorbells, gguf, policy, prefill
-from .ops import (HostExpertStacks, LayerBanks, SlotBank, expert_range, indexed_moe_fused_decode, layer_desc,
-                  moe_gather, moe_prefill, router_topk, row_bytes, slot_stride, stack_decode, stack_status, synth,
-                  upload_expert)
+from .ops import (HostExpertStacks, LayerBanks, SlotBank, copy_batch, expert_range, indexed_moe_fused_decode,
+                  layer_desc, moe_gather, moe_prefill, router_topk, row_bytes, slot_stride, stack_decode, stack_status,
+                  synth, upload_expert)
 
 __all__ = [
     "ACT_GELU_PYTORCH_TANH", "ACT_SILU", "BF16", "F16", "F32", "Q4_K", "Q8_0", "E_BAD_ID", "E_DEVICE",
@@ -22,4 +22,5 @@ __all__ = [
     "device_info", "mem_info", "synchronize", "LayerBanks", "SlotBank", "expert_range",
     "indexed_moe_fused_decode", "moe_gather", "moe_prefill", "router_topk", "row_bytes", "slot_stride",
     "layer_desc", "stack_decode", "stack_status", "synth", "policy", "doorbells", "gguf", "prefill", "HostExpertStacks", "upload_expert",
+    "copy_batch",
 ]

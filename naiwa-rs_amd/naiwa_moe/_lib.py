@@ -54,6 +54,11 @@ class CachedLayerDesc(C.Structure):
                 ("usable", C.c_int), ("mode", C.c_int), ("act", C.c_int)]
 
 
+class Copy(C.Structure):
+    """naiwa_copy (include/naiwa_moe.h)."""
+    _fields_ = [("dst", C.c_void_p), ("src", C.c_void_p), ("bytes", C.c_uint64)]
+
+
 class Pending(C.Structure):
     """naiwa_pending (include/naiwa_doorbell.h)."""
     _fields_ = [("seq", C.c_uint32), ("len", C.c_int), ("chan", C.c_int)]
@@ -155,6 +160,7 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_stack_trace_enable": (i32, [i32]),
     "naiwa_stack_trace_read": (i32, [_P(u64), i32, _P(i32), _P(i32)]),
     "naiwa_upload_expert": (i32, [vp, vp, vp, i64, i64, i64]),
+    "naiwa_copy_batch": (i32, [_P(Copy), i32, i64]),
     # include/naiwa_doorbell.h
     "naiwa_topk_doorbell_create": (i32, [i32, _P(vp)]),
     "naiwa_topk_doorbell_destroy": (i32, [vp]),

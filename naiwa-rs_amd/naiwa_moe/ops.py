@@ -15,7 +15,8 @@ import ctypes as C
 
 import numpy as np
 
-from ._lib import (ACT_SILU, BF16, F32, Q4_K, Q8_0, ROUTE_SOFTMAX_TOPK_RENORM, STACK_FUSED,
+from . import _lib
+from ._lib import (ACT_SILU, BF16, E_UNSUPPORTED, F32, Q4_K, Q8_0, ROUTE_SOFTMAX_TOPK_RENORM, STACK_FUSED,
                    STACK_LAYERED, Bank, Layer, check, lib)
 from .device import DeviceBuffer, PinnedBuffer
 
@@ -124,6 +125,23 @@ def upload_expert(banks: "LayerBanks", slot: int, stacks: HostExpertStacks, expe
                                    read_fence.handle if read_fence is not None else 0,
                                    done.handle if done is not None else 0)
     check(rc, "naiwa_upload_expert")
+
+
+COPY_BATCH_MAX = 64
+
+
+def copy_batch(items, stream: int = 0) -> bool:
+    """Queue host -> device copies [(dst, src, bytes), ...] (device pointer, pinned host
+    pointer, size; 16-byte aligned) as one kernel on `stream` (naiwa_copy_batch).  False,
+    with nothing queued, when a source is not mapped pinned memory or not aligned."""
+    if len(items) > COPY_BATCH_MAX:
+        raise ValueError(f"at most {COPY_BATCH_MAX} ranges per batch")
+    arr = (_lib.Copy * max(1, len(items)))(*[_lib.Copy(d, s, b) for d, s, b in items])
+    rc = lib().naiwa_copy_batch(arr, len(items), stream)
+    if rc == E_UNSUPPORTED:
+        return False
+    check(rc, "naiwa_copy_batch")
+    return True
 
 
 def indexed_moe_fused_decode(banks: LayerBanks, x, x_dtype: int, slot_ids, weights, rows: int,
