@@ -1,7 +1,7 @@
 /*
  * naiwa_oracle.c -- CPU restatement of naiwa-rs's MoE expert hot path.
  *
- * TEST INFRASTRUCTURE ONLY (the parity checker and the CPU baseline); the
+ * TEST INFRASTRUCTURE ONLY (the parity reference of the tests and the CPU baseline); the
  * product library never links or calls this file.  Build: oracle/Makefile
  * (-O2 -ffp-contract=off so every f32 operation is the one written here).
  */

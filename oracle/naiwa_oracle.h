@@ -1,10 +1,10 @@
 /*
  * naiwa_oracle.h -- CPU restatement of naiwa-rs's MoE expert hot path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity reference for the HIP
  * library under naiwa-rs_amd/.  Only tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py may load it, and only as the checker or as the
- * timed CPU baseline.  The product path never calls into it.
+ * cpu_baseline leg of bench.py may load it, and only as the reference results
+ * or as the timed CPU baseline.  The product path never calls into it.
  *
  * What it restates (reference files are naiwa-rs paths):
  *   - GGML block formats Q8_0 / Q4_K (public ggml layout; the byte stride rule

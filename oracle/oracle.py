@@ -1,7 +1,7 @@
 """ctypes front end of the CPU oracle (liboracle.so, built from naiwa_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py, as the checker or the timed CPU baseline.  The
+cpu_baseline leg of bench.py, as the reference results or the timed CPU baseline.  The
 product library (naiwa-rs_amd/) never imports this module.
 
 The C sources restate naiwa-rs's CPU expert path (src/moe/stages/cpu_miss.rs),

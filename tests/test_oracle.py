@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/naiwa_oracle.c) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/naiwa_oracle.c) before the GPU results are compared with it.
 
 Every check here is independent of the oracle's own formulas: hand-built blocks
 with hand-computed values, IEEE conversion known answers, round-trip bounds that
