@@ -92,8 +92,8 @@ def main() -> int:
             return run_prefill_stream(args)
         return run_cache25(args) if args.workload == "cache25" else run_prefill(args)
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
-              "(the expert path is single-GPU; sharding is a design note only)", file=sys.stderr)
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
+              "(the expert path runs on one GPU; how it would shard is described, not built)", file=sys.stderr)
         return 2
     import naiwa_moe as nm
 

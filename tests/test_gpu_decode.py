@@ -146,7 +146,7 @@ def test_empty_and_all_padding(gpu):
 def test_reference_split_fixture_on_gpu(gpu):
     """src/moe/tests.rs:253-306 on the device: the resident experts run on the GPU
     banks, the misses on the CPU oracle; the sum matches all-CPU within 2e-2
-    (the reference's bound), and within this build's 1e-2 relative bar."""
+    (the reference's bound), and within the 1e-2 relative bar of these tests."""
     import test_oracle as T
     nm = gpu
     g, u, d = T.reference_fixture_stacks()
