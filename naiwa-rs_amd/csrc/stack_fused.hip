@@ -772,6 +772,42 @@ __device__ inline void stage_h(const Params& p, int v0, int nv, uint32_t* hw, fl
     }
 }
 
+// One wave: poll the tagged h vector of sorted position v (I/2 words) and stage
+// it like stage_h (words at hw[v * I/2 ...], sums at hs[v * I/kSumSpan ...]).
+template <int DD>
+__device__ inline void stage_h_wave(const Params& p, int v, uint32_t* hw, float* hs, uint32_t tag, int lane) {
+    constexpr int gpg = Fmt<DD>::kSumSpan / 4;
+    constexpr int G = 3; // 4-value groups per lane per round (I = 768: one round)
+    const int gpv = p.I / 4;
+    const u64* src = p.h + (size_t)v * (p.I / 2);
+    uint32_t* hwv = hw + (size_t)v * (p.I / 2);
+    float* hsv = hs + (size_t)v * (p.I / Fmt<DD>::kSumSpan);
+    for (int g0 = 0; g0 < gpv; g0 += 64 * G) {
+        u64 w[2 * G];
+        auto addr = [&](int j) -> const u64* {
+            const int g = g0 + lane + (j >> 1) * 64;
+            return g < gpv ? src + 2 * g + (j & 1) : nullptr;
+        };
+        issue_tagged(w, addr, tag);
+        wait_tagged(w, addr, tag, p);
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const int g = g0 + lane + j * 64;
+            const bool in = g < gpv;
+            const uint32_t A = (uint32_t)w[2 * j], B = (uint32_t)w[2 * j + 1]; // (h0, h1), (h2, h3)
+            float part = 0.0f;
+            if (in) {
+                hwv[2 * g] = (A & 0xffffu) | (B << 16);
+                hwv[2 * g + 1] = (A >> 16) | (B & 0xffff0000u);
+                part = (Fmt<DD>::from16(A & 0xffffu) + Fmt<DD>::from16(A >> 16)) +
+                       (Fmt<DD>::from16(B & 0xffffu) + Fmt<DD>::from16(B >> 16));
+            }
+            part = naiwa_group_sum<gpg>(part);
+            if (in && (g % gpg) == 0) hsv[g / gpg] = part;
+        }
+    }
+}
+
 // The pointer, as a value the compiler cannot see through: address math on it
 // is then redone inside the layer loop instead of being hoisted out and kept
 // live in registers across all layers.
@@ -1120,7 +1156,14 @@ stack_kernel(Params p) {
             // word's tag; this only keeps the polling traffic small while the last
             // producers are still computing.
             // (wave 0 alone polls, four words per lane per round: fewer loads in flight)
-            {
+            // one token with one pair per segment, every down row prefetched and one
+            // output chunk per workgroup: wave v takes pair v alone -- the done words of
+            // its own producers, its h, its 8 rows -- so the pairs whose producers finish
+            // first are dotted while the last ones are still computing
+            const bool pair_waves = MR == 1 && DD == NAIWA_Q4_K && nchunks <= G && nvalid == nseg &&
+                                    nvalid <= kThreads / 64 && npre >= nvalid && dnu <= 8 * kDU8 &&
+                                    I2 / max(per, 1) + 2 <= 64;
+            if (!pair_waves) {
                 const int nprod_h = (total + per - 1) / per;
                 if (wave == 0) {
                     for (int b0 = 0; b0 < nprod_h; b0 += 256) {
@@ -1139,7 +1182,41 @@ stack_kernel(Params p) {
             for (int cp = bid, ci = 0; cp < nchunks; cp += G, ++ci) {
                 const int c = chunk_at(cp, nchunks);
                 const int f0 = c * kChunk;
-                for (int b0 = 0; b0 < nvalid; b0 += p.hpairs) {
+                if constexpr (MR == 1 && DD == NAIWA_Q4_K) {
+                    if (pair_waves && wave < nvalid) {
+                        const int v = wave; // sorted position = segment
+                        // the producers of this pair's items: workgroups [v I2 / per, ((v + 1) I2 - 1) / per]
+                        const int b_lo = v * I2 / per, b_hi = ((v + 1) * I2 - 1) / per;
+                        u64 dw[1];
+                        auto daddr = [&](int) -> const u64* { return b_lo + lane <= b_hi ? p.done + b_lo + lane : nullptr; };
+                        issue_tagged(dw, daddr, tag);
+                        wait_tagged(dw, daddr, tag, p);
+                        if (wave == 0) mark_wave(p, l, 14);
+                        stage_h_wave<DD>(p, v, hw, hs, tag, lane);
+                        // this wave's prefetched rows (it issued pair v's) and its h staging
+                        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                        __builtin_amdgcn_wave_barrier();
+                        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                        if (wave == 0) mark_wave(p, l, 5);
+                        __builtin_amdgcn_sched_barrier(0);
+                        // 8-lane group fi: output feature fi of the chunk
+                        const int fi = lane >> 3, l8 = lane & 7;
+                        const uint8_t* drow = dbuf + (size_t)(v * kChunk + fi) * drb;
+                        const uint32_t* words = hw + (size_t)v * (I / 2);
+                        const float* sums = hs + (size_t)v * (I / Fmt<DD>::kSumSpan);
+                        float acc = 0.0f;
+#pragma unroll 1
+                        for (int u = l8; u < dnu; u += 8)
+                            acc += Fmt<DD>::dot(Fmt<DD>::template load<NAIWA_AS_LDS>(drow, u), u, words, sums);
+                        const float dv = naiwa_group_sum<8>(acc);
+                        if (l8 == 0) {
+                            const float w = sm.pair_w[sm.sorted[v]];
+                            sm.partial[fi][v] = w != 0.0f ? dv * w : 0.0f;
+                        }
+                    }
+                }
+                for (int b0 = 0; !pair_waves && b0 < nvalid; b0 += p.hpairs) {
                     const int nbp = min(p.hpairs, nvalid - b0);
                     if (ci > 0 || b0 > 0) __syncthreads(); // the previous pass's dots read hdyn
                     stage_h<DD>(p, b0, nbp, hw, hs, tag);
