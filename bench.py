@@ -613,7 +613,8 @@ def run_prefill(args) -> int:
     """DeepSeek-V2-Lite-shaped MoE prefill: 26 MoE layers, H 2048, 64 routed experts top-6
     (softmax without renormalisation) + 2 shared experts, I 1408, gate/up Q4_K, down Q8_0.
     2048 tokens in 4 chunks of 512; per layer and chunk: device routing, the routed experts
-    and the shared experts (weight 1, accumulated) as grouped MFMA GEMMs, residual.  One
+    and the shared experts (weight 1, after each token's routed pairs) in one grouped MFMA
+    call, residual.  One
     step = the whole 2048-token prefill through the MoE layers."""
     import naiwa_moe as nm
 
@@ -642,9 +643,14 @@ def run_prefill(args) -> int:
     xs = nm.DeviceBuffer(tokens * H * 2)
     nm.synth(nm.BF16, 998, tokens * H, xs, 0.0, 1.0, stream=stream.handle)
     x = nm.DeviceBuffer(tokens * H * 2)
+    # one grouped call per layer: each token's K routed pairs, then its S_ shared experts
+    # (slots E.., weight 1), so the shared GEMM tiles run in the routed launch and the
+    # ordered combine adds them after the routed pairs, as a second accumulating call would
+    KA = K + S_
     ids, w = nm.DeviceBuffer(T * K * 4), nm.DeviceBuffer(T * K * 4)
-    sid = nm.DeviceBuffer.from_array(np.tile(np.array([E, E + 1], dtype=np.uint32), (T, 1)))
-    sw = nm.DeviceBuffer.from_array(np.ones((T, S_), dtype=np.float32))
+    ids_all = nm.DeviceBuffer.from_array(np.tile(np.concatenate([np.zeros(K), np.arange(E, E + S_)]).astype(np.uint32),
+                                                 (T, 1)))
+    w_all = nm.DeviceBuffer.from_array(np.tile(np.concatenate([np.zeros(K), np.ones(S_)]).astype(np.float32), (T, 1)))
     y = nm.DeviceBuffer(T * H * 4)
     stream.sync()
     log(f"prefill: {L} layers x {E}+{S_} experts synthesized in {time.time() - t0:.1f}s")
@@ -657,8 +663,10 @@ def run_prefill(args) -> int:
             for banks, router in layers:
                 nm.router_topk(xc, nm.BF16, router, T, H, E, K, ids, w, mode=nm.ROUTE_SOFTMAX_TOPK,
                                stream=stream.handle)
-                nm.moe_prefill(banks, xc, ids, w, T, K, y, stream=stream.handle)
-                nm.moe_prefill(banks, xc, sid, sw, T, S_, y, accumulate=True, stream=stream.handle)
+                for dst, src in ((ids_all, ids), (w_all, w)):
+                    nm._lib.check(lib.naiwa_memcpy_2d_d2d(dst.ptr, KA * 4, src.ptr, K * 4, K * 4, T, stream.handle),
+                                  "routing columns")
+                nm.moe_prefill(banks, xc, ids_all, w_all, T, KA, y, stream=stream.handle)
                 nm._lib.check(lib.naiwa_residual_add_bf16(xc, y.ptr, T * H, stream.handle), "residual")
 
     for _ in range(warmup):

@@ -80,6 +80,10 @@ int naiwa_host_free(void* p);
 int naiwa_memcpy_h2d(void* dst, const void* src, size_t bytes, int64_t stream);
 int naiwa_memcpy_d2h(void* dst, const void* src, size_t bytes, int64_t stream);
 int naiwa_memcpy_d2d(void* dst, const void* src, size_t bytes, int64_t stream);
+/* height rows of width bytes, device to device, rows dpitch / spitch bytes apart
+ * (e.g. a [T, k] routing result into the first k columns of a [T, k + s] one). */
+int naiwa_memcpy_2d_d2d(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width, size_t height,
+                        int64_t stream);
 int naiwa_memset(void* p, int value, size_t bytes, int64_t stream);
 int naiwa_stream_create(int64_t* stream);
 int naiwa_stream_destroy(int64_t stream);

@@ -161,6 +161,7 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_stack_trace_read": (i32, [_P(u64), i32, _P(i32), _P(i32)]),
     "naiwa_upload_expert": (i32, [vp, vp, vp, i64, i64, i64]),
     "naiwa_copy_batch": (i32, [_P(Copy), i32, i64]),
+    "naiwa_memcpy_2d_d2d": (i32, [vp, C.c_size_t, vp, C.c_size_t, C.c_size_t, C.c_size_t, i64]),
     # include/naiwa_doorbell.h
     "naiwa_topk_doorbell_create": (i32, [i32, _P(vp)]),
     "naiwa_topk_doorbell_destroy": (i32, [vp]),

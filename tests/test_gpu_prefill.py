@@ -80,7 +80,21 @@ def test_prefill_accumulates_shared_experts(gpu):
     all_ids = np.concatenate([ids, sid], axis=1)
     all_w = np.concatenate([w, sw], axis=1)
     want = O.fused_moe_decode(gs, us, ds, O.from_bf16(x), all_ids, all_w)
-    assert S.max_rel_err(out.download(np.float32).reshape(T, H), want) < TOL
+    two_calls = out.download(np.float32).reshape(T, H)
+    assert S.max_rel_err(two_calls, want) < TOL
+    # the shared experts as extra pairs of one call (after each token's routed pairs):
+    # the same pair rows, added in the same order, bit for bit
+    one = nm.DeviceBuffer(T * H * 4)
+    ids_all = nm.DeviceBuffer(T * (k + 2) * 4)
+    ids_all.upload(np.zeros((T, k + 2), dtype=np.uint32))
+    routed = nm.DeviceBuffer.from_array(ids.astype(np.uint32)) # alive until the copy has run
+    nm.lib().naiwa_memcpy_2d_d2d(ids_all.ptr, (k + 2) * 4, routed.ptr, k * 4, k * 4, T, 0)
+    nm.synchronize()
+    assert np.array_equal(ids_all.download(np.uint32).reshape(T, k + 2)[:, :k], ids)
+    ids_all.upload(all_ids.astype(np.uint32))
+    nm.moe_prefill(banks, xd, ids_all, nm.DeviceBuffer.from_array(all_w.astype(np.float32)), T, k + 2, one)
+    nm.synchronize()
+    assert np.array_equal(one.download(np.float32).reshape(T, H), two_calls)
 
 
 def test_prefill_one_expert_many_tokens(gpu):
