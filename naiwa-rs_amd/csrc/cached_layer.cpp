@@ -33,6 +33,13 @@ struct naiwa_cached_layer {
     size_t bytes[3] = {0, 0, 0};   // one expert's bytes per projection
     // routing buffers: device results, pinned host copies
     int cap_rows = 0;
+    // one allocation each for the routing read-back [ids | weights] and for the step's
+    // inputs [slot ids | weights of the cache pairs | of the staged pairs], so that each
+    // crosses the link in one copy; the views below are set per step (n = rows * k)
+    uint32_t* route_dev_base = nullptr;
+    uint32_t* route_h_base = nullptr;
+    uint32_t* in_dev_base = nullptr;
+    uint32_t* in_h_base = nullptr;
     uint32_t* ids_dev = nullptr;
     float* w_dev = nullptr;
     uint32_t* slots_dev = nullptr;
@@ -62,30 +69,20 @@ struct naiwa_cached_layer {
     bool ahead_claimed = false;
 
     void release_buffers() {
-        if (ids_dev) (void)hipFree(ids_dev);
-        if (w_dev) (void)hipFree(w_dev);
-        if (slots_dev) (void)hipFree(slots_dev);
-        if (ids_h) (void)hipHostFree(ids_h);
-        if (w_h) (void)hipHostFree(w_h);
+        if (route_dev_base) (void)hipFree(route_dev_base);
+        if (in_dev_base) (void)hipFree(in_dev_base);
+        if (route_h_base) (void)hipHostFree(route_h_base);
+        if (in_h_base) (void)hipHostFree(in_h_base);
         if (slots_h) (void)hipHostFree(slots_h);
-        if (slots_up) (void)hipHostFree(slots_up);
-        if (wsplit_h) (void)hipHostFree(wsplit_h);
-        if (wsplit_dev) (void)hipFree(wsplit_dev);
-        wsplit_h = nullptr;
-        wsplit_dev = nullptr;
+        route_dev_base = route_h_base = in_dev_base = in_h_base = nullptr;
+        views(0);
         if (pred_ids_dev) (void)hipFree(pred_ids_dev);
         if (pred_w_dev) (void)hipFree(pred_w_dev);
         if (pred_ids_h) (void)hipHostFree(pred_ids_h);
         pred_ids_dev = nullptr;
         pred_w_dev = nullptr;
         pred_ids_h = nullptr;
-        ids_dev = nullptr;
-        w_dev = nullptr;
-        slots_dev = nullptr;
-        ids_h = nullptr;
-        w_h = nullptr;
         slots_h = nullptr;
-        slots_up = nullptr;
         cap_rows = 0;
         last_rows = 0;
         pred_rows = 0;
@@ -97,17 +94,27 @@ struct naiwa_cached_layer {
         if (e != hipSuccess) return (int)e;
         release_buffers();
         const size_t n = (size_t)rows * d.top_k;
-        if (hipMalloc(&ids_dev, n * 4) != hipSuccess || hipMalloc(&w_dev, n * 4) != hipSuccess ||
-            hipMalloc(&slots_dev, n * 4) != hipSuccess || hipHostMalloc(&ids_h, n * 4, 0) != hipSuccess ||
-            hipHostMalloc(&w_h, n * 4, 0) != hipSuccess || hipHostMalloc(&slots_h, n * 4, 0) != hipSuccess ||
-            hipHostMalloc(&slots_up, n * 4, 0) != hipSuccess || hipMalloc(&pred_ids_dev, n * 4) != hipSuccess ||
-            hipMalloc(&pred_w_dev, n * 4) != hipSuccess || hipHostMalloc(&pred_ids_h, n * 4, 0) != hipSuccess ||
-            hipHostMalloc(&wsplit_h, 2 * n * 4, 0) != hipSuccess || hipMalloc(&wsplit_dev, 2 * n * 4) != hipSuccess) {
+        if (hipMalloc(&route_dev_base, 2 * n * 4) != hipSuccess || hipHostMalloc(&route_h_base, 2 * n * 4, 0) != hipSuccess ||
+            hipMalloc(&in_dev_base, 3 * n * 4) != hipSuccess || hipHostMalloc(&in_h_base, 3 * n * 4, 0) != hipSuccess ||
+            hipHostMalloc(&slots_h, n * 4, 0) != hipSuccess || hipMalloc(&pred_ids_dev, n * 4) != hipSuccess ||
+            hipMalloc(&pred_w_dev, n * 4) != hipSuccess || hipHostMalloc(&pred_ids_h, n * 4, 0) != hipSuccess) {
             release_buffers();
             return NAIWA_E_NOMEM;
         }
         cap_rows = rows;
         return NAIWA_OK;
+    }
+
+    // the step's views of the combined buffers for n = rows * k pairs (0: none)
+    void views(int n) {
+        ids_dev = route_dev_base;
+        w_dev = route_dev_base ? (float*)(route_dev_base + n) : nullptr;
+        ids_h = route_h_base;
+        w_h = route_h_base ? (float*)(route_h_base + n) : nullptr;
+        slots_dev = in_dev_base;
+        wsplit_dev = in_dev_base ? (float*)(in_dev_base + n) : nullptr;
+        slots_up = in_h_base;
+        wsplit_h = in_h_base ? (float*)(in_h_base + n) : nullptr;
     }
 
     void slot_ptrs(int slot, void* dst[3]) const {
@@ -211,6 +218,7 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     int rc = L->ensure_rows(rows);
     if (!rc && next) rc = next->ensure_rows(rows);
     if (rc) return rc;
+    L->views(n);
     naiwa_cached_step step{};
 
     // route on the device, then read the top-k back (the routing round trip)
@@ -218,8 +226,8 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
                                   L->ids_dev, L->w_dev, nullptr, stream);
     if (!rc && next) rc = next->predict_launch(x, rows, stream);
     if (rc) return rc;
-    if ((rc = naiwa_hip_rc(hipMemcpyAsync(L->ids_h, L->ids_dev, (size_t)n * 4, hipMemcpyDeviceToHost, st))) ||
-        (rc = naiwa_hip_rc(hipMemcpyAsync(L->w_h, L->w_dev, (size_t)n * 4, hipMemcpyDeviceToHost, st))) ||
+    // ids and weights are adjacent: one copy
+    if ((rc = naiwa_hip_rc(hipMemcpyAsync(L->ids_h, L->ids_dev, (size_t)n * 8, hipMemcpyDeviceToHost, st))) ||
         (rc = naiwa_hip_rc(hipStreamSynchronize(st))))
         return rc;
     L->last_rows = rows;
@@ -272,7 +280,19 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     step.staged_experts = nc;
     if (nc && (rc = naiwa_hip_rc(hipEventRecord(L->staged_done, L->copy)))) return rc;
 
-    if ((rc = naiwa_hip_rc(hipMemcpyAsync(L->slots_dev, L->slots_up, (size_t)n * 4, hipMemcpyHostToDevice, st))))
+    // the step's inputs in one copy: slot ids and, with staged pairs, the weights of the
+    // cache pairs and of the staged pairs (adjacent after the slot ids)
+    if (nc) {
+        float* w_res = L->wsplit_h;
+        float* w_stg = L->wsplit_h + n;
+        for (int i = 0; i < n; ++i) {
+            const bool staged_pair = L->slots_up[i] >= (uint32_t)d.usable;
+            w_res[i] = staged_pair ? 0.0f : L->w_h[i];
+            w_stg[i] = staged_pair ? L->w_h[i] : 0.0f;
+        }
+    }
+    if ((rc = naiwa_hip_rc(
+             hipMemcpyAsync(L->slots_dev, L->slots_up, (size_t)n * (nc ? 12 : 4), hipMemcpyHostToDevice, st))))
         return rc;
     // the expert kernel after the latest lookahead claim (src/moe/cached_layer.rs:808-819):
     // a slot it published may still be in flight
@@ -289,15 +309,6 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         // staged pairs added on top: ring slots sort after cache slots, so the two calls
         // add the terms of one call in its order (src/moe/decode.rs:226-233 runs the
         // resident experts before the staging wait for the same reason)
-        float* w_res = L->wsplit_h;
-        float* w_stg = L->wsplit_h + n;
-        for (int i = 0; i < n; ++i) {
-            const bool staged_pair = L->slots_up[i] >= (uint32_t)d.usable;
-            w_res[i] = staged_pair ? 0.0f : L->w_h[i];
-            w_stg[i] = staged_pair ? L->w_h[i] : 0.0f;
-        }
-        if ((rc = naiwa_hip_rc(hipMemcpyAsync(L->wsplit_dev, L->wsplit_h, (size_t)n * 8, hipMemcpyHostToDevice, st))))
-            return rc;
         if ((rc = naiwa_moe_decode_ex(&d.gate, &d.up, &d.down, x, NAIWA_BF16, L->slots_dev, L->wsplit_dev, rows, k,
                                       d.act, out, 0, stream)))
             return rc;
@@ -326,8 +337,15 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
             void* src[3];
             L->slot_ptrs(ps[i], dst);
             L->slot_ptrs(from, src);
-            for (int p = 0; p < 3 && !rc; ++p)
-                rc = naiwa_hip_rc(hipMemcpyAsync(dst[p], src[p], L->bytes[p], hipMemcpyDeviceToDevice, st));
+            // the three projections in one kernel (device to device)
+            naiwa_copy items[3];
+            for (int p = 0; p < 3; ++p) items[p] = naiwa_copy{dst[p], src[p], (uint64_t)L->bytes[p]};
+            rc = naiwa_copy_batch_mapped(items, 3, (int64_t)st);
+            if (rc == NAIWA_E_UNSUPPORTED) { // not 16-byte aligned: one copy per projection
+                rc = NAIWA_OK;
+                for (int p = 0; p < 3 && !rc; ++p)
+                    rc = naiwa_hip_rc(hipMemcpyAsync(dst[p], src[p], L->bytes[p], hipMemcpyDeviceToDevice, st));
+            }
             if (rc) {
                 naiwa_cache_unreserve(L->cache, ps[i]);
                 return rc;
