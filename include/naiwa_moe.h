@@ -229,6 +229,13 @@ typedef struct naiwa_layer {
 int naiwa_stack_decode(const naiwa_layer* layers, int n_layers, void* x, int rows, int H, int E,
                        int k, int mode, int act, uint32_t* ids_out, float* w_out, int flags,
                        int64_t stream);
+/* As naiwa_stack_decode; y_out (may be NULL) is an f32 device buffer
+ * [n_layers, rows, H] receiving each layer's MoE output MoE_l(x_l) before the
+ * residual add and the bf16 store, so a caller can check every layer's expert
+ * output on its own (x_{l+1} = bf16(f32(x_l) + y_l) exactly). */
+int naiwa_stack_decode_y(const naiwa_layer* layers, int n_layers, void* x, int rows, int H, int E,
+                         int k, int mode, int act, uint32_t* ids_out, float* w_out, float* y_out,
+                         int flags, int64_t stream);
 
 /* Blocks per CU of the fused kernel (1..8, capped by occupancy; default 1). */
 int naiwa_stack_set_blocks_per_cu(int n);

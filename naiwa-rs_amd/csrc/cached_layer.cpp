@@ -317,11 +317,6 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
                                       k, d.act, out, NAIWA_DECODE_ACCUMULATE, stream)))
             return rc;
     }
-    for (int i = 0; i < nc; ++i) {
-        if ((rc = naiwa_hip_rc(hipEventRecord(L->ring_fence[pos[i]], st)))) return rc;
-        L->ring_fenced[pos[i]] = 1;
-    }
-
     // promotion: staged -> cache slot copies, ordered after the kernel by the stream
     if (promote_cap > 0 && nc > 0) {
         std::vector<int32_t> pe((size_t)promote_cap), ps((size_t)promote_cap);
@@ -355,6 +350,12 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         }
     }
 
+    // every read of this step's ring slots (the expert kernel's and the promotion copies')
+    // is before this point on `stream`: a later upload into one of them waits for its fence
+    for (int i = 0; i < nc; ++i) {
+        if ((rc = naiwa_hip_rc(hipEventRecord(L->ring_fence[pos[i]], st)))) return rc;
+        L->ring_fenced[pos[i]] = 1;
+    }
     // every read of this layer's cache slots is before this point on `stream`
     if ((rc = naiwa_hip_rc(hipEventRecord(L->read_done, st)))) return rc;
     L->read_recorded = true;

@@ -37,16 +37,23 @@ extern "C" int naiwa_residual_add_bf16(void* x, const float* y, int64_t n, int64
 }
 
 int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows, int H, int E, int k,
-                      int mode, int act, uint32_t* ids_out, float* w_out, int64_t stream);
+                      int mode, int act, uint32_t* ids_out, float* w_out, float* y_out, int64_t stream);
 
 extern "C" int naiwa_stack_decode(const naiwa_layer* layers, int n_layers, void* x, int rows, int H,
                                   int E, int k, int mode, int act, uint32_t* ids_out, float* w_out,
                                   int flags, int64_t stream) {
+    return naiwa_stack_decode_y(layers, n_layers, x, rows, H, E, k, mode, act, ids_out, w_out, nullptr, flags,
+                                stream);
+}
+
+extern "C" int naiwa_stack_decode_y(const naiwa_layer* layers, int n_layers, void* x, int rows, int H,
+                                    int E, int k, int mode, int act, uint32_t* ids_out, float* w_out,
+                                    float* y_out, int flags, int64_t stream) {
     if (!layers || n_layers < 0 || !x || rows < 0 || H <= 0 || E <= 0 || k <= 0 || k > E)
         return NAIWA_E_INVALID;
     if (rows == 0 || n_layers == 0) return NAIWA_OK;
     if (flags == NAIWA_STACK_FUSED)
-        return naiwa_stack_fused(layers, n_layers, x, rows, H, E, k, mode, act, ids_out, w_out, stream);
+        return naiwa_stack_fused(layers, n_layers, x, rows, H, E, k, mode, act, ids_out, w_out, y_out, stream);
     if (flags != NAIWA_STACK_LAYERED) return NAIWA_E_UNSUPPORTED;
     hipStream_t st = (hipStream_t)stream;
     const int n = rows * k;
@@ -75,6 +82,9 @@ extern "C" int naiwa_stack_decode(const naiwa_layer* layers, int n_layers, void*
         }
         if ((rc = naiwa_moe_decode(&L.gate, &L.up, &L.down, x, NAIWA_BF16, dec_ids, dec_w, rows, k, act, y,
                                    stream)))
+            return rc;
+        if (y_out && (rc = naiwa_hip_rc(hipMemcpyAsync(y_out + (size_t)l * rows * H, y, (size_t)rows * H * 4,
+                                                        hipMemcpyDeviceToDevice, st))))
             return rc;
         if ((rc = naiwa_residual_add_bf16(x, y, (int64_t)rows * H, stream))) return rc;
     }

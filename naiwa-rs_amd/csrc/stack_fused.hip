@@ -97,6 +97,7 @@ struct Params {
     int* status;                 // [0] wait timeouts, [1] missing experts
     uint32_t* ids_out;           // [n_layers, rows, k] or null
     float* w_out;
+    float* y_out;                // [n_layers, rows, H] f32 MoE outputs before the residual, or null
     uint64_t spin_limit;         // wall-clock ticks before a wait gives up
     uint32_t seq;                // launch number; tag of layer l = seq << 8 | (l + 1)
     unsigned long long* trace;   // optional [grid][n_layers + 1][kTraceSlots] phase timestamps
@@ -1331,6 +1332,7 @@ stack_kernel(Params p) {
 #pragma unroll
                         for (int j = 0; j < 8; ++j) y += tk[j] == (uint32_t)t ? pv[j] : 0.0f;
                     }
+                    if (p.y_out) p.y_out[((size_t)l * rows + t) * H + f0 + fi] = y;
                     sm.xown[ci][t][fi] = naiwa_bf16_to_f32(naiwa_f32_to_bf16(sm.xown[ci][t][fi] + y));
                 }
                 __syncthreads();
@@ -1494,7 +1496,7 @@ extern "C" int naiwa_stack_status(int* barrier_timeouts, int* missing_experts) {
 }
 
 int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows, int H, int E, int k,
-                      int mode, int act, uint32_t* ids_out, float* w_out, int64_t stream) {
+                      int mode, int act, uint32_t* ids_out, float* w_out, float* y_out, int64_t stream) {
     if (rows > kMaxRows || k > kMaxK || E > kMaxE || n_layers > kMaxLayers) return NAIWA_E_UNSUPPORTED;
     if (H % kChunk || (ids_out == nullptr) != (w_out == nullptr)) return NAIWA_E_INVALID;
     if (mode < 0 || mode > 2 || (act != NAIWA_ACT_SILU && act != NAIWA_ACT_GELU_PYTORCH_TANH))
@@ -1660,6 +1662,7 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     prm.status = (int*)(sync + kStatusOff);
     prm.ids_out = ids_out;
     prm.w_out = w_out;
+    prm.y_out = y_out;
     prm.spin_limit = (uint64_t)khz * 2000ull; // 2 s
     prm.seq = seq;
     prm.bitems = bitems;

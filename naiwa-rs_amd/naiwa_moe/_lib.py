@@ -154,6 +154,7 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_moe_gather": (i32, [vp, i32, i32, vp, vp, vp, i64]),
     "naiwa_synth": (i32, [i32, u64, u64, i64, f32, f32, vp, i64]),
     "naiwa_stack_decode": (i32, [_P(Layer), i32, vp, i32, i32, i32, i32, i32, i32, vp, vp, i32, i64]),
+    "naiwa_stack_decode_y": (i32, [_P(Layer), i32, vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, i32, i64]),
     "naiwa_stack_set_blocks_per_cu": (i32, [i32]),
     "naiwa_stack_status": (i32, [_P(i32), _P(i32)]),
     "naiwa_residual_add_bf16": (i32, [vp, vp, i64, i64]),

@@ -186,14 +186,17 @@ def layer_desc(router, banks: "LayerBanks", slot_of_expert=None) -> Layer:
 
 def stack_decode(layers: list, x, rows: int, H: int, E: int, k: int,
                  mode: int = ROUTE_SOFTMAX_TOPK_RENORM, act: int = ACT_SILU, ids_out=None,
-                 w_out=None, fused: bool = True, stream: int = 0) -> None:
+                 w_out=None, fused: bool = True, stream: int = 0, y_out=None) -> None:
     """One decode step through every layer: x [rows, H] bf16 (device) updated in place.
-    layers: a list of Layer descriptors (layer_desc) or a prebuilt ctypes array."""
+    layers: a list of Layer descriptors (layer_desc) or a prebuilt ctypes array.
+    y_out: optional f32 device buffer [layers, rows, H] for each layer's MoE output
+    before the residual."""
     arr = layers if isinstance(layers, C.Array) else (Layer * len(layers))(*layers)
-    rc = lib().naiwa_stack_decode(arr, len(arr), _dev(x), rows, H, E, k, mode, act,
-                                  _dev(ids_out) if ids_out is not None else None,
-                                  _dev(w_out) if w_out is not None else None,
-                                  STACK_FUSED if fused else STACK_LAYERED, stream)
+    rc = lib().naiwa_stack_decode_y(arr, len(arr), _dev(x), rows, H, E, k, mode, act,
+                                    _dev(ids_out) if ids_out is not None else None,
+                                    _dev(w_out) if w_out is not None else None,
+                                    _dev(y_out) if y_out is not None else None,
+                                    STACK_FUSED if fused else STACK_LAYERED, stream)
     check(rc, "naiwa_stack_decode")
 
 

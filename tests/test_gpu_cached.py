@@ -85,12 +85,17 @@ def test_cached_layer_steps_match_the_oracle(gpu):
     assert st["hits"] == total["hits"] and st["staged"] == total["staged"]
     assert st["pcie_bytes"] == total["pcie_bytes"] and st["promotions"] == total["promoted"]
     assert total["promoted"] > 0   # min_hits 1: every step promotes one staged expert
-    # promoted experts are resident and their bytes are the expert's bytes
+    # promoted experts are resident and all three projections hold the expert's bytes
+    check_resident_bytes(layer, banks, stacks)
+
+
+def check_resident_bytes(layer, banks, stacks):
     table = layer.cache.slot_table()
     for e in np.nonzero(table >= 0)[0]:
         s = int(table[e])
-        got = banks.gate.buffer.download(np.uint8, count=banks.gate.expert_bytes, offset=s * banks.gate.stride)
-        assert np.array_equal(got, stacks.view(0)[e]), (e, s)
+        for proj, bank in enumerate((banks.gate, banks.up, banks.down)):
+            got = bank.buffer.download(np.uint8, count=bank.expert_bytes, offset=s * bank.stride)
+            assert np.array_equal(got, stacks.view(proj)[e]), (e, s, proj)
 
 
 def test_staged_bytes_land_in_their_ring_slot(gpu):
@@ -273,3 +278,187 @@ def test_profile_seeds_the_cache(gpu, tmp_path):
     assert layer2.seed(prof.layer(0), fill_share=0.5) == 2
     t2 = layer2.cache.slot_table()
     assert int(t2[5]) == 0 and int(t2[9]) == 1 and int((t2 >= 0).sum()) == 2
+
+
+class PageableStacks:
+    """Host expert stacks in ordinary pageable memory (e.g. a GGUF file read into
+    a buffer): no device mapping, so staged uploads take one DMA copy per
+    projection instead of the batched copy kernel."""
+
+    def __init__(self, experts, hidden, inter, dtypes):
+        from types import SimpleNamespace
+        shapes = ((inter, hidden, dtypes[0]), (inter, hidden, dtypes[1]), (hidden, inter, dtypes[2]))
+        self.expert_bytes = [n * O.row_bytes(dt, k) for n, k, dt in shapes]
+        self.arrays = [np.zeros((experts, b), dtype=np.uint8) for b in self.expert_bytes]
+        self.buffers = [SimpleNamespace(ptr=a.ctypes.data) for a in self.arrays]
+
+    def view(self, proj):
+        return self.arrays[proj]
+
+
+@pytest.mark.parametrize("host_mem", ["pinned", "pageable"])
+def test_cached_layer_alternating_streams(gpu, host_mem):
+    """Steps alternate between two compute streams with no host synchronisation of
+    their own: a staged upload into a ring slot must wait for every earlier read of
+    that slot -- the expert kernel's and the promotion copy's -- through the slot's
+    fence alone.  Every step's output matches the oracle and every resident
+    (promoted) expert's three projections hold its bytes.  With pageable host
+    stacks the uploads are per-projection DMA copies."""
+    nm = gpu
+    E, H, I, k, usable, rows = 16, 256, 256, 4, 4, 1
+    copy = nm.Stream()
+    streams = [nm.Stream(), nm.Stream()]
+    ring = nm.policy.StagingRing()
+    dt = (O.Q4_K,) * 3
+    g, u, d, r = S.layer(1800, E, H, I, dt)
+    stacks = nm.HostExpertStacks(E, H, I, dt) if host_mem == "pinned" else PageableStacks(E, H, I, dt)
+    for p_, src in enumerate((g, u, d)):
+        stacks.view(p_)[:] = src.reshape(E, -1)
+    banks = nm.LayerBanks(usable + ring.length, H, I, dt)
+    router = nm.DeviceBuffer.from_array(r)
+    bias = zipf_bias(E, 1.1, 1800)
+    bias_d = nm.DeviceBuffer.from_array(bias)
+    layer = nm.policy.CachedLayer(router, banks, stacks, E, k, usable, ring, copy.handle,
+                                  mode=O.ROUTE_SOFTMAX_TOPK_RENORM, router_bias=bias_d)
+    host = (g, u, d, r, bias, dt, I)
+    steps = 10
+    xs = [S.activations_bf16(1810 + i, rows, H) for i in range(steps)]
+    xds = [nm.DeviceBuffer.from_array(x) for x in xs]
+    outs = [nm.DeviceBuffer(rows * H * 4) for _ in range(steps)]
+    promoted = 0
+    for i in range(steps):
+        print(f"[alternating streams {host_mem} step {i}]", flush=True)
+        info = layer.forward(xds[i], rows, outs[i], pcie_frac=1.0, promote_cap=1, min_hits=1,
+                             stream=streams[i % 2].handle)
+        promoted += info["promoted"]
+    for st in streams:
+        st.sync()
+    copy.sync()
+    for i in range(steps):
+        _, _, want = oracle_step(host, xs[i], E, k, H)
+        err = S.max_rel_err(outs[i].download(np.float32).reshape(rows, H), want)
+        assert err < TOL, (i, err)
+    assert promoted > 0
+    check_resident_bytes(layer, banks, stacks)
+
+
+class PromotingSlotModel(SlotModel):
+    """SlotModel plus the reference's promotion (src/moe/cached_layer.rs:892-1051):
+    the step's staged experts in id order, at most cap of them; an expert already
+    resident or seen fewer than min_hits times is skipped; the target is the first
+    empty usable slot, else the slot with the smallest (last_use, slot) among those
+    this step did not read (last_use < tick); a promoted slot is published with
+    last_use = tick."""
+
+    def __init__(self, usable, E):
+        super().__init__(usable)
+        self.hits = [0] * E
+
+    def route(self, ids):
+        for e in ids:
+            self.hits[e] += 1
+        return super().route(ids)
+
+    def promote(self, staged, cap, min_hits):
+        done = []
+        for e in sorted(set(staged)):
+            if len(done) >= cap:
+                break
+            if e in self.expert or self.hits[e] < min_hits:
+                continue
+            if None in self.expert:
+                s = self.expert.index(None)
+            else:
+                cands = [(self.last[s], s) for s in range(len(self.expert)) if self.last[s] < self.tick]
+                if not cands:
+                    continue
+                s = min(cands)[1]
+            self.expert[s], self.last[s] = e, self.tick
+            done.append(e)
+        return done
+
+
+def test_cached_qwen3_shape_zipf(gpu):
+    """The 25 %-cache workload at its real shape: two chained Qwen3-30B-A3B-shaped
+    layers (H 2048, 128 experts, top-8, I 768, Q4_K), 32 cached experts + the
+    16-slot staging ring per layer, Zipf(1.1) routing bias, the caches seeded with
+    each layer's 32 most popular experts, 12 decode steps with staging and one
+    promotion per layer per step (min_hits 2).  Every step: top-k ids bit-exact
+    with the oracle on the GPU's own x_l, hit/staged counts and the slot table
+    equal to an independent replay of the reference's policy, and the layer's
+    output within 1e-2 of the oracle.  At the end every resident expert's three
+    projections hold its bytes."""
+    nm = gpu
+    L, E, H, I, k, usable, rows, steps, min_hits = 2, 128, 2048, 768, 8, 32, 1, 12, 2
+    dt = (O.Q4_K,) * 3
+    copy, stream = nm.Stream(), nm.Stream()
+    ring = nm.policy.StagingRing()
+    proj = [nm.row_bytes(dt[0], H) * I, nm.row_bytes(dt[1], H) * I, nm.row_bytes(dt[2], I) * H]
+    tmp = nm.DeviceBuffer(E * max(proj))
+    layers, models, hosts, keep = [], [], [], []
+    for l in range(L):
+        stacks = nm.HostExpertStacks(E, H, I, dt)
+        for t in range(3):
+            n, kk = (I, H) if t < 2 else (H, I)
+            nm.synth(dt[t], 2000 + 8 * l + t, E * n * kk, tmp, 0.0, 0.02, stream=stream.handle)
+            nm.lib().naiwa_memcpy_d2h(stacks.buffers[t].ptr, tmp.ptr, E * proj[t], stream.handle)
+            stream.sync()
+        r = O.normal(S.stream(2000 + l, S.T_ROUTER), E * H, 0.0, 0.02).reshape(E, H)
+        bias = zipf_bias(E, 1.1, 2100 + l)
+        router, bias_d = nm.DeviceBuffer.from_array(r), nm.DeviceBuffer.from_array(bias)
+        banks = nm.LayerBanks(usable + ring.length, H, I, dt)
+        layer = nm.policy.CachedLayer(router, banks, stacks, E, k, usable, ring, copy.handle,
+                                      mode=O.ROUTE_SOFTMAX_TOPK_RENORM, router_bias=bias_d)
+        # the 32 most popular experts (largest bias) first
+        popular = [int(e) for e in np.argsort(-bias, kind="stable")[:usable]]
+        assert layer.seed(popular) == usable
+        model = PromotingSlotModel(usable, E)
+        for e in popular:
+            model.admit(e)
+        g, u, d = (stacks.view(t).reshape(E, *((I, -1) if t < 2 else (H, -1))) for t in range(3))
+        hosts.append((g, u, d, r, bias, dt, I))
+        layers.append((layer, banks, stacks))
+        models.append(model)
+        keep += [router, bias_d]
+    x = S.activations_bf16(2200, rows, H)
+    xd = nm.DeviceBuffer.from_array(x)
+    out = nm.DeviceBuffer(rows * H * 4)
+    tot = {"staged": 0, "promoted": 0}
+    for step in range(steps):
+        for l, (layer, banks, stacks) in enumerate(layers):
+            print(f"[cached qwen3 step {step} layer {l}]", flush=True)
+            info = layer.forward(xd, rows, out, pcie_frac=1.0, promote_cap=1, min_hits=min_hits,
+                                 stream=stream.handle)
+            stream.sync()
+            ids, w = layer.routing(rows)
+            want_ids, want_w, want = oracle_step(hosts[l], x, E, k, H)
+            assert np.array_equal(ids, want_ids), (step, l, ids, want_ids)
+            assert np.allclose(w, want_w, rtol=1e-5, atol=1e-7)
+            flat = ids.reshape(-1).tolist()
+            model = models[l]
+            staged = sorted(set(e for e in flat if not model.resident(e)))
+            hits = model.route(flat)
+            assert info["hits"] == hits and info["staged_experts"] == len(staged), (step, l, info)
+            promoted = model.promote(staged, 1, min_hits)
+            assert info["promoted"] == len(promoted), (step, l, info, promoted)
+            table = layer.cache.slot_table()
+            want_table = np.full(E, -1, dtype=np.int64)
+            for s_, e in enumerate(model.expert):
+                if e is not None:
+                    want_table[e] = s_
+            assert np.array_equal(table, want_table), (step, l)
+            y = out.download(np.float32).reshape(rows, H)
+            err = S.max_rel_err(y, want)
+            print(f"  hits={info['hits']} staged={info['staged_experts']} promoted={info['promoted']} "
+                  f"err={err:.3e}", flush=True)
+            assert err < TOL, (step, l, err)
+            tot["staged"] += info["staged_experts"]
+            tot["promoted"] += info["promoted"]
+            x = O.to_bf16(O.from_bf16(x).astype(np.float32) + y)
+            xd = nm.DeviceBuffer.from_array(x)
+        # the next step starts from a fresh token
+        x = S.activations_bf16(2201 + step, rows, H)
+        xd = nm.DeviceBuffer.from_array(x)
+    assert tot["staged"] > 0 and tot["promoted"] > 0, tot
+    for layer, banks, stacks in layers:
+        check_resident_bytes(layer, banks, stacks)

@@ -104,3 +104,46 @@ def test_prefill_one_expert_many_tokens(gpu):
         return ids, w
     err, _, _ = run_case(gpu, 1700, 100, 8, 2, 256, 256, (O.Q4_K,) * 3, mutate=mutate)
     assert err < TOL
+
+
+def test_prefill_deepseek_chunk_with_shared_experts(gpu):
+    """The DeepSeek-V2-Lite prefill workload's unit of work at full size: one
+    512-token chunk, 64 routed experts top-6 (softmax without renormalisation)
+    plus the 2 shared experts as extra pairs (weight 1) of the same grouped call,
+    H 2048, I 1408, gate/up Q4_K, down Q8_0.  Routing ids from the device router
+    are bit-exact with the oracle's; the output of all 3072 routed + 1024 shared
+    pairs is within 1e-2 of the oracle's expert path over the same 8 pairs per
+    token."""
+    nm = gpu
+    T, E, S_, k, H, I = 512, 64, 2, 6, 2048, 1408
+    dt = (O.Q4_K, O.Q4_K, O.Q8_0)
+    banks = nm.LayerBanks(E + S_, H, I, dt)
+    print("[prefill deepseek chunk] synthesizing 66 experts", flush=True)
+    for t, bank in enumerate((banks.gate, banks.up, banks.down)):
+        assert bank.stride == bank.expert_bytes
+        nm.synth(dt[t], 5000 + t, (E + S_) * bank.n * bank.k, bank.base, 0.0, 0.02)
+    r = O.normal(S.stream(5000, S.T_ROUTER), E * H, 0.0, 0.02).reshape(E, H)
+    x = S.activations_bf16(5001, T, H)
+    xd = nm.DeviceBuffer.from_array(x)
+    ids_d, w_d = nm.DeviceBuffer(T * k * 4), nm.DeviceBuffer(T * k * 4)
+    nm.router_topk(xd, nm.BF16, nm.DeviceBuffer.from_array(r), T, H, E, k, ids_d, w_d, mode=O.ROUTE_SOFTMAX_TOPK)
+    nm.synchronize()
+    ids = ids_d.download(np.uint32).reshape(T, k)
+    w = w_d.download(np.float32).reshape(T, k)
+    want_ids, want_w = O.topk(O.router_logits(O.from_bf16(x), r), k, O.ROUTE_SOFTMAX_TOPK)
+    assert np.array_equal(ids, want_ids)
+    assert np.allclose(w, want_w, rtol=1e-5, atol=1e-7)
+    all_ids = np.concatenate([ids, np.tile(np.array([E, E + 1], np.uint32), (T, 1))], axis=1)
+    all_w = np.concatenate([w, np.ones((T, S_), np.float32)], axis=1)
+    out = nm.DeviceBuffer(T * H * 4)
+    print(f"[prefill deepseek chunk] T={T} pairs={T * (k + S_)}", flush=True)
+    ids_all_d, w_all_d = nm.DeviceBuffer.from_array(all_ids), nm.DeviceBuffer.from_array(all_w)
+    nm.moe_prefill(banks, xd, ids_all_d, w_all_d, T, k + S_, out)
+    nm.synchronize()
+    got = out.download(np.float32).reshape(T, H)
+    qs = [b.buffer.download(np.uint8).reshape(E + S_, b.n, -1) for b in (banks.gate, banks.up, banks.down)]
+    st = (O.stack(qs[0], dt[0], I, H), O.stack(qs[1], dt[1], I, H), O.stack(qs[2], dt[2], H, I))
+    want = O.fused_moe_decode_mt(*st, O.from_bf16(x), all_ids, all_w, 16)
+    err = S.max_rel_err(got, want)
+    print(f"  max_rel_err={err:.3e}", flush=True)
+    assert err < TOL
