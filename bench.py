@@ -217,7 +217,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16 x Q4_K (f32 accumulate)",
         "data": "synthetic (device-generated N(0,0.02) Q4_K experts, N(0,1) bf16 tokens)",
         "config": {
             "workload": f"Qwen3-30B-A3B-shaped MoE stack decode, bs{rows}, all experts cached",
@@ -341,36 +341,67 @@ def layers_host_sample(nm, keep, L, E, H, I, n_layers: int = 4):
     return out
 
 
-# Host threads for the CPU baseline: the GPU's share of the host cores (16 per GPU).
-CPU_BASELINE_THREADS = 16
+# Host threads for the CPU baseline: every physical core of the host, at most the GPU's
+# share of the host's cores (16 per GPU).
+CPU_BASELINE_MAX_THREADS = 16
 
 
-def cpu_baseline(nm, sample, xs, rows, H, E, K, I, L, budget_s: float):
-    """The oracle (C restatement of the reference's CPU expert path, plus the router)
-    on the sampled layers, its expert path on the host threads the GPU's share allows,
-    one token at a time, until the budget is spent; per-token time is scaled to the
-    full stack depth."""
+def cpu_threads():
+    """(threads used, physical cores from lscpu or None, logical cores)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import cpu_baseline as CB
+
+    phys = CB.physical_cores()
+    logical = os.cpu_count() or 1
+    return max(1, min(CPU_BASELINE_MAX_THREADS, phys or logical)), phys, logical
+
+
+def cpu_baseline(nm, sample, xs, rows, H, E, K, I, L, budget_s: float, repeats: int = 3, dtypes=None):
+    """The reference's CPU expert path (two passes, int8 activations, AVX2 integer dots;
+    oracle/cpu_baseline.c) plus the router and top-k, on the sampled layers, one token at a
+    time, on a persistent pool of every physical core (at most 16).  The sample (tokens x
+    layers) is sized so one pass takes about budget_s / repeats; it runs `repeats` times
+    and the median per-token time, scaled to the full stack depth, is reported."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import cpu_baseline as CB
     import oracle as O
 
-    cores = max(1, min(CPU_BASELINE_THREADS, os.cpu_count() or 1))
-    layers = [(r, qs, (O.Q4_K,) * 3, I) for r, qs in sample]
+    threads, phys, logical = cpu_threads()
+    pool = CB.Pool(threads)
+    dts = dtypes or (O.Q4_K,) * 3
+    layers = [(r, (O.stack(g, dts[0], I, H), O.stack(u, dts[1], I, H), O.stack(d, dts[2], H, I)))
+              for r, (g, u, d) in sample]
     x_all = xs.download(np.uint16).reshape(-1, rows, H)
-    done, spent = 0, 0.0
-    for i in range(x_all.shape[0]):
+
+    def one_token(i):
+        x = O.from_bf16(x_all[i % x_all.shape[0]])
+        for r, st in layers:
+            ids, w = O.topk(O.router_logits(x, r), K, O.ROUTE_SOFTMAX_TOPK_RENORM)
+            y = pool.fused_moe_decode(*st, x, ids, w)
+            x = O.from_bf16(O.to_bf16(x + y))
+
+    # size the sample: tokens whose pass takes about budget_s / repeats
+    t0 = time.perf_counter()
+    one_token(0)
+    per_tok = max(time.perf_counter() - t0, 1e-4)
+    tokens = int(max(3, min(200, budget_s / repeats / per_tok)))
+    runs = []
+    for rep in range(repeats):
         t0 = time.perf_counter()
-        O.stack_decode(layers, x_all[i], E, K, threads=cores)
-        spent += time.perf_counter() - t0
-        done += 1
-        if spent >= budget_s:
-            break
-    per_layer_token = spent / (done * len(layers))
-    tok_s = rows / (per_layer_token * L)
-    log(f"cpu baseline: {done} tokens x {len(layers)} layers in {spent:.1f}s -> {tok_s:.3f} tok/s "
-        f"(host has {os.cpu_count()} logical cores; the oracle's expert path uses {cores} threads)")
-    return {"value": round(tok_s, 4), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{done} tokens x {len(layers)} of {L} layers (bs{rows}, router + top-8 + "
-                      f"fused expert path in f32), scaled to {L} layers"}
+        for i in range(tokens):
+            one_token(i)
+        runs.append((time.perf_counter() - t0) / tokens)
+    pool.close()
+    med = float(np.median(runs))
+    tok_s = rows / (med / len(layers) * L)
+    log(f"cpu baseline: {tokens} tokens x {len(layers)} layers, {repeats} runs "
+        f"{', '.join(f'{r * 1e3:.2f}' for r in runs)} ms/token -> median {tok_s:.3f} tok/s at {L} layers "
+        f"({threads} threads; lscpu physical cores {phys}, logical {logical})")
+    return {"value": round(tok_s, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "physical_cores": phys, "logical_cores": logical,
+            "sample": f"{tokens} tokens x {len(layers)} of {L} layers (bs{rows}; router, top-{K} and the "
+                      f"two-pass expert path with int8 activations and AVX2 integer dots), median of "
+                      f"{repeats} runs, scaled to {L} layers"}
 
 
 def run_cache25(args) -> int:
@@ -485,7 +516,7 @@ def run_cache25(args) -> int:
         "metric": "MoE decode tok/s, 25% expert cache, Zipf(1.1) routing (Qwen3-30B-A3B shape, Q4_K)",
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(ms / steps, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f32", "data": "synthetic (device-generated N(0,0.02) Q4_K experts in pinned host stacks)",
+        "dtype": "bf16 x Q4_K (f32 accumulate)", "data": "synthetic (device-generated N(0,0.02) Q4_K experts in pinned host stacks)",
         "config": {"workload": "Qwen3-30B-A3B-shaped MoE stack decode, bs1, 32/128 experts cached per layer, "
                                "Zipf(1.1) routing bias, misses staged over PCIe (16-slot ring)",
                    "layers": L, "hidden": H, "experts": E, "top_k": K, "intermediate": I, "cached": usable,
