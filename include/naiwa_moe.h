@@ -45,6 +45,7 @@ extern "C" {
 #define NAIWA_E_DEVICE      -7  /* the device reported a failed condition    */
 #define NAIWA_E_FORMAT      -8  /* malformed or unsupported file (GGUF)      */
 #define NAIWA_E_IO          -9  /* a file cannot be opened or mapped         */
+#define NAIWA_E_TOO_LARGE  -10  /* the call needs more than a fixed capacity */
 
 /* ---- GGML type ids --------------------------------------------------------- */
 #define NAIWA_F32  0
@@ -170,6 +171,23 @@ int naiwa_moe_decode(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_b
 int naiwa_moe_decode_ex(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down,
                         const void* x, int x_dtype, const uint32_t* slot_ids, const float* w,
                         int rows, int width, int act, float* out, int flags, int64_t stream);
+/* No counterpart in the reference.  naiwa_moe_decode_ex for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the same kernels and the same results bit for bit, with
+ * the scratch (segments, permutation, h) in a fixed device array of
+ * NAIWA_DECODE_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends,
+ * instead of the library's grow-only buffer.  No hipMalloc, hipFree or
+ * allocating routine is called; nothing is cleared with a memset.  A call needs
+ * 256 + 2 align256(4 n) + align256(4 (n + 1)) + 4 n I bytes (n = rows *
+ * width pairs, I the intermediate size): NAIWA_E_TOO_LARGE when that exceeds
+ * the array (8 MiB holds n <= 146 pairs at I = 14336, n <= 2719 at I = 768).
+ * Every call on one GPU uses that GPU's one array: calls that overlap
+ * on the device (other streams, other host threads) race and must be ordered
+ * by the caller. */
+#define NAIWA_DECODE_NOALLOC_SCRATCH_BYTES (8u << 20)
+int naiwa_moe_decode_noalloc(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down,
+                             const void* x, int x_dtype, const uint32_t* slot_ids, const float* w,
+                             int rows, int width, int act, float* out, int flags, int64_t stream);
 
 /* Router: logits = W . x with the chunked fixed-point accumulation (chunks of 8
  * features summed as an f32 fma chain, each rounded to int64 with 32

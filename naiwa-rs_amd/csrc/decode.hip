@@ -18,6 +18,9 @@
 #include "segments.h"
 #include "workspace.h"
 
+#include <algorithm>
+#include <mutex>
+
 namespace {
 
 constexpr int kRowsPerBlock = 16;                    // 16 groups of 16 lanes
@@ -189,13 +192,27 @@ int tok_cap(int dtype, int k) {
     return cap < 1 ? 0 : (cap > kTokMax ? kTokMax : cap);
 }
 
-} // namespace
+// Scratch of one decode call: seg_count, bad | seg_key[n] | seg_begin[n+1] | perm[n] | h[n*I] f32.
+struct DecodeScratch {
+    size_t off_key, off_begin, off_perm, off_h, total;
+    DecodeScratch(int n, int I) {
+        off_key = 256;
+        off_begin = off_key + (((size_t)n * 4 + 255) & ~size_t(255));
+        off_perm = off_begin + (((size_t)(n + 1) * 4 + 255) & ~size_t(255));
+        off_h = off_perm + (((size_t)n * 4 + 255) & ~size_t(255));
+        total = off_h + (size_t)n * I * 4;
+    }
+};
 
-extern "C" int naiwa_moe_decode_ex(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down,
-                                   const void* x, int x_dtype, const uint32_t* slot_ids, const float* w, int rows,
-                                   int width, int act, float* out, int flags, int64_t stream) {
+__global__ void zero_f32_kernel(float* p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0.0f;
+}
+
+// Argument checks shared by the entry points; 0 when the call is valid.
+int check_args(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, const void* x, int x_dtype,
+               const uint32_t* slot_ids, const float* w, int rows, int width, int act, float* out, int flags) {
     if (flags & ~NAIWA_DECODE_ACCUMULATE) return NAIWA_E_INVALID;
-    const int accumulate = (flags & NAIWA_DECODE_ACCUMULATE) ? 1 : 0;
     if (!bank_ok(gate) || !bank_ok(up) || !bank_ok(down)) return NAIWA_E_INVALID;
     if (gate->dtype != up->dtype) return NAIWA_E_UNSUPPORTED;
     const int H = gate->k, I = gate->n;
@@ -207,31 +224,38 @@ extern "C" int naiwa_moe_decode_ex(const naiwa_bank* gate, const naiwa_bank* up,
     if (rows < 0 || width < 0 || (int64_t)rows * width > 65536) return NAIWA_E_INVALID;
     if (H % 32 || I % 32) return NAIWA_E_INVALID;
     if (rows > 4096) return NAIWA_E_INVALID;
-    hipStream_t st = (hipStream_t)stream;
-    if (rows == 0) return NAIWA_OK;
-    if (!x || !out || (width > 0 && (!slot_ids || !w))) return NAIWA_E_INVALID;
-    if (width == 0) return accumulate ? NAIWA_OK : naiwa_hip_rc(hipMemsetAsync(out, 0, (size_t)rows * H * 4, st));
+    if (rows > 0 && (!x || !out || (width > 0 && (!slot_ids || !w)))) return NAIWA_E_INVALID;
     const int tok_g = tok_cap(gate->dtype, H), tok_d = tok_cap(down->dtype, I);
     if (!tok_g || !tok_d) return NAIWA_E_UNSUPPORTED;
     const int acc_bytes = ((rows * kRowsPerBlock * 4) + 15) & ~15;
     const size_t lds_down = (size_t)acc_bytes + (size_t)tok_d * naiwa_stage_bytes(down->dtype, I);
     if (lds_down > 64 * 1024) return NAIWA_E_UNSUPPORTED;
+    return NAIWA_OK;
+}
 
-    // scratch: seg_count, bad | seg_key[n] | seg_begin[n+1] | perm[n] | h[n*I]
+// The launches of one checked call over scratch ws (DecodeScratch(rows * width, I).total bytes).
+int decode_launch(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, const void* x, int x_dtype,
+                  const uint32_t* slot_ids, const float* w, int rows, int width, int act, float* out, int flags,
+                  uint8_t* ws, hipStream_t st) {
+    const int accumulate = (flags & NAIWA_DECODE_ACCUMULATE) ? 1 : 0;
+    const int H = gate->k, I = gate->n;
+    if (width == 0) {
+        if (accumulate) return NAIWA_OK;
+        const int64_t n = (int64_t)rows * H;
+        zero_f32_kernel<<<(unsigned)std::min<int64_t>((n + 255) / 256, 1024), 256, 0, st>>>(out, n);
+        return naiwa_hip_rc(hipGetLastError());
+    }
+    const int tok_g = tok_cap(gate->dtype, H), tok_d = tok_cap(down->dtype, I);
+    const int acc_bytes = ((rows * kRowsPerBlock * 4) + 15) & ~15;
+    const size_t lds_down = (size_t)acc_bytes + (size_t)tok_d * naiwa_stage_bytes(down->dtype, I);
     const int n = rows * width;
-    const size_t off_key = 256, off_begin = off_key + (((size_t)n * 4 + 255) & ~size_t(255));
-    const size_t off_perm = off_begin + (((size_t)(n + 1) * 4 + 255) & ~size_t(255));
-    const size_t off_h = off_perm + (((size_t)n * 4 + 255) & ~size_t(255));
-    const size_t total = off_h + (size_t)n * I * 4;
-    int rc = 0;
-    uint8_t* ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_DECODE, total, &rc);
-    if (!ws) return rc;
+    const DecodeScratch L(n, I);
     int* seg_count = (int*)ws;
     int* bad = (int*)(ws + 4);
-    uint32_t* seg_key = (uint32_t*)(ws + off_key);
-    uint32_t* seg_begin = (uint32_t*)(ws + off_begin);
-    uint32_t* perm = (uint32_t*)(ws + off_perm);
-    float* hbuf = (float*)(ws + off_h);
+    uint32_t* seg_key = (uint32_t*)(ws + L.off_key);
+    uint32_t* seg_begin = (uint32_t*)(ws + L.off_begin);
+    uint32_t* perm = (uint32_t*)(ws + L.off_perm);
+    float* hbuf = (float*)(ws + L.off_h);
 
     segments_kernel<<<1, NAIWA_SEG_THREADS, 0, st>>>(slot_ids, w, n, gate->slots, perm, seg_count,
                                                      seg_key, seg_begin, bad);
@@ -271,6 +295,63 @@ extern "C" int naiwa_moe_decode_ex(const naiwa_bank* gate, const naiwa_bank* up,
         break;
     }
     return naiwa_hip_rc(hipGetLastError());
+}
+
+// The allocation-free entry point's scratch: one array per device (each GPU the
+// library runs on holds its own copy until the process ends).  Host code never
+// uses the array's name as an address: the device address comes from
+// hipGetSymbolAddress, once per device, with that device current.
+constexpr size_t kNoAllocScratchBytes = NAIWA_DECODE_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+uint8_t* g_noalloc_ptr[kMaxDevices];
+
+// The current device's address of `scratch`, resolved on its first use.
+int noalloc_scratch(uint8_t** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kMaxDevices) return NAIWA_E_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (!ptr) return NAIWA_E_DEVICE;
+        g_noalloc_ptr[dev] = (uint8_t*)ptr;
+    }
+    *out = g_noalloc_ptr[dev];
+    return NAIWA_OK;
+}
+
+} // namespace
+
+extern "C" int naiwa_moe_decode_ex(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down,
+                                   const void* x, int x_dtype, const uint32_t* slot_ids, const float* w, int rows,
+                                   int width, int act, float* out, int flags, int64_t stream) {
+    int rc = check_args(gate, up, down, x, x_dtype, slot_ids, w, rows, width, act, out, flags);
+    if (rc || rows == 0) return rc;
+    uint8_t* ws = nullptr;
+    if (width > 0) {
+        ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_DECODE, DecodeScratch(rows * width, gate->n).total, &rc);
+        if (!ws) return rc;
+    }
+    return decode_launch(gate, up, down, x, x_dtype, slot_ids, w, rows, width, act, out, flags, ws,
+                         (hipStream_t)stream);
+}
+
+extern "C" int naiwa_moe_decode_noalloc(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down,
+                                        const void* x, int x_dtype, const uint32_t* slot_ids, const float* w,
+                                        int rows, int width, int act, float* out, int flags, int64_t stream) {
+    int rc = check_args(gate, up, down, x, x_dtype, slot_ids, w, rows, width, act, out, flags);
+    if (rc || rows == 0) return rc;
+    if (width > 0 && DecodeScratch(rows * width, gate->n).total > kNoAllocScratchBytes) return NAIWA_E_TOO_LARGE;
+    uint8_t* ws = nullptr;
+    if ((rc = noalloc_scratch(&ws))) return rc;
+    return decode_launch(gate, up, down, x, x_dtype, slot_ids, w, rows, width, act, out, flags, ws,
+                         (hipStream_t)stream);
 }
 
 extern "C" int naiwa_moe_decode(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down,

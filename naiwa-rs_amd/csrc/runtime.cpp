@@ -65,6 +65,7 @@ const char* naiwa_status_string(int rc) {
     case NAIWA_E_DEVICE: return "device reported failure";
     case NAIWA_E_FORMAT: return "malformed or unsupported file";
     case NAIWA_E_IO: return "file cannot be opened or mapped";
+    case NAIWA_E_TOO_LARGE: return "request exceeds a fixed capacity";
     default: return rc > 0 ? hipGetErrorString((hipError_t)rc) : "unknown status";
     }
 }

@@ -5,7 +5,7 @@ include/naiwa_moe.h.  Nothing here computes on the CPU: every operator calls
 the HIP library, which must be built (naiwa-rs_amd/build.py).
 """
 from ._lib import (ACT_GELU_PYTORCH_TANH, ACT_SILU, BF16, E_BAD_ID, E_DEVICE, E_FORMAT, E_INVALID, E_IO,
-                   E_NOMEM, E_NOT_FOUND, E_TIMEOUT, E_UNSUPPORTED, F16, F32, Q4_K, Q8_0,
+                   E_NOMEM, E_NOT_FOUND, E_TIMEOUT, E_TOO_LARGE, E_UNSUPPORTED, F16, F32, Q4_K, Q8_0,
                    ROUTE_SOFTMAX_TOPK, ROUTE_SOFTMAX_TOPK_RENORM, ROUTE_TOPK_SOFTMAX, LIB_PATH,
                    NaiwaError, lib)
 from .device import DeviceBuffer, Event, PinnedBuffer, Stream, device_count, device_info, mem_info, synchronize
@@ -16,7 +16,7 @@ from .ops import (HostExpertStacks, LayerBanks, SlotBank, copy_batch, expert_ran
 
 __all__ = [
     "ACT_GELU_PYTORCH_TANH", "ACT_SILU", "BF16", "F16", "F32", "Q4_K", "Q8_0", "E_BAD_ID", "E_DEVICE",
-    "E_FORMAT", "E_INVALID", "E_IO", "E_NOMEM", "E_NOT_FOUND", "E_TIMEOUT", "E_UNSUPPORTED",
+    "E_FORMAT", "E_INVALID", "E_IO", "E_NOMEM", "E_NOT_FOUND", "E_TIMEOUT", "E_TOO_LARGE", "E_UNSUPPORTED",
     "ROUTE_SOFTMAX_TOPK", "ROUTE_SOFTMAX_TOPK_RENORM", "ROUTE_TOPK_SOFTMAX", "LIB_PATH",
     "NaiwaError", "lib", "DeviceBuffer", "Event", "PinnedBuffer", "Stream", "device_count",
     "device_info", "mem_info", "synchronize", "LayerBanks", "SlotBank", "expert_range",

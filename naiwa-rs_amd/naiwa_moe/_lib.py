@@ -15,7 +15,7 @@ LIB_PATH = os.environ.get("NAIWA_MOE_LIB") or os.path.join(PKG_ROOT, "libnaiwa_m
 
 OK = 0
 E_INVALID, E_UNSUPPORTED, E_TIMEOUT, E_NOMEM, E_BAD_ID, E_NOT_FOUND, E_DEVICE = -1, -2, -3, -4, -5, -6, -7
-E_FORMAT, E_IO = -8, -9
+E_FORMAT, E_IO, E_TOO_LARGE = -8, -9, -10
 
 F32, F16, Q8_0, Q4_K, BF16 = 0, 1, 8, 12, 30
 ACT_SILU, ACT_GELU_PYTORCH_TANH = 0, 1
@@ -148,6 +148,7 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_projection_bytes": (i64, [i32, i64, i64]),
     "naiwa_moe_decode": (i32, [_P(Bank), _P(Bank), _P(Bank), vp, i32, vp, vp, i32, i32, i32, vp, i64]),
     "naiwa_moe_decode_ex": (i32, [_P(Bank), _P(Bank), _P(Bank), vp, i32, vp, vp, i32, i32, i32, vp, i32, i64]),
+    "naiwa_moe_decode_noalloc": (i32, [_P(Bank), _P(Bank), _P(Bank), vp, i32, vp, vp, i32, i32, i32, vp, i32, i64]),
     "naiwa_router_topk": (i32, [vp, i32, vp, i32, i32, i32, i32, i32, vp, vp, vp, i64]),
     "naiwa_router_topk_biased": (i32, [vp, i32, vp, vp, i32, i32, i32, i32, i32, vp, vp, vp, i64]),
     "naiwa_moe_prefill": (i32, [_P(Bank), _P(Bank), _P(Bank), vp, vp, vp, i32, i32, i32, vp, i32, i64]),
