@@ -75,7 +75,11 @@ def parse() -> argparse.Namespace:
                     help="prefill-stream: layer buffers (default: the memory plan's stride)")
     ap.add_argument("--budget-gb", type=float, default=0.0, metavar="GB",
                     help="prefill-stream: device memory the plan may assume free (default: what is free)")
-    ap.add_argument("--workload", choices=["resident", "cache25", "prefill", "prefill-stream"], default="resident",
+    ap.add_argument("--cache-layers", type=int, default=32, metavar="N",
+                    help="mixtral: layers of the 4-of-8 cached decode (each pins 0.8 GB of host stacks)")
+    ap.add_argument("--db-iters", type=int, default=20000, help="doorbell: round trips timed")
+    ap.add_argument("--workload", choices=["resident", "cache25", "prefill", "prefill-stream", "mixtral", "doorbell"],
+                    default="resident",
                     help="resident: every expert in HBM (the headline); cache25: 32 of 128 experts "
                          "cached per layer, Zipf(1.1) routing, misses streamed over PCIe; prefill: "
                          "DeepSeek-V2-Lite-shaped 2048-token prefill in 512-token chunks (MFMA)")
@@ -84,12 +88,16 @@ def parse() -> argparse.Namespace:
 
 def main() -> int:
     args = parse()
-    if args.workload in ("cache25", "prefill", "prefill-stream"):
+    if args.workload in ("cache25", "prefill", "prefill-stream", "mixtral", "doorbell"):
         if args.gpus != 1:
             print("bench.py measures one GPU", file=sys.stderr)
             return 2
         if args.workload == "prefill-stream":
             return run_prefill_stream(args)
+        if args.workload == "mixtral":
+            return run_mixtral(args)
+        if args.workload == "doorbell":
+            return run_doorbell(args)
         return run_cache25(args) if args.workload == "cache25" else run_prefill(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
@@ -430,11 +438,12 @@ def run_cache25(args) -> int:
     tmp = nm.DeviceBuffer(E * proj)
     layers, keep, ranking = [], [], []
     for l in range(L):
-        stacks = nm.HostExpertStacks(E, H, I, dt)
+        # each expert's gate | up | down adjacent in host memory and in its slot: one range per upload
+        stacks = nm.HostExpertStacks(E, H, I, dt, interleaved=True)
         for t in range(3):
             nm.synth(nm.Q4_K, 1000 + 8 * l + t, E * proj * 256 // Q4K_BYTES, tmp, 0.0, 0.02, stream=compute.handle)
-            compute.sync()
-            nm.lib().naiwa_memcpy_d2h(stacks.buffers[t].ptr, tmp.ptr, E * proj, compute.handle)
+            nm._lib.check(nm.lib().naiwa_memcpy_2d(stacks.ptrs[t], stacks.stride, tmp.ptr, proj, proj, E,
+                                                   compute.handle), "memcpy_2d")
             compute.sync()
         router = nm.DeviceBuffer(E * H * 4)
         nm.synth(nm.F32, 1000 + 8 * l + 3, E * H, router, 0.0, 0.02, stream=compute.handle)
@@ -442,7 +451,7 @@ def run_cache25(args) -> int:
         p = ranks.astype(np.float64) ** -1.1
         bias = np.log(p / p.sum()).astype(np.float32)
         bias_d = nm.DeviceBuffer.from_array(bias)
-        banks = nm.LayerBanks(usable + ring.length, H, I, dt)
+        banks = nm.LayerBanks(usable + ring.length, H, I, dt, contiguous=True)
         layer = nm.policy.CachedLayer(router, banks, stacks, E, K, usable, ring, copy.handle,
                                       mode=nm.ROUTE_SOFTMAX_TOPK_RENORM, router_bias=bias_d)
         ranking += [(l, int(e)) for e in np.argsort(ranks)]
@@ -627,7 +636,8 @@ def run_prefill_stream(args) -> int:
         "metric": "MoE prefill tok/s with host-resident experts (DeepSeek-V2-Lite shape, layer stream)",
         "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f16", "data": "synthetic (device-generated N(0,0.02) Q4_K/Q8_0 experts in pinned host stacks)",
+        "dtype": "f16 x Q4_K/Q8_0 (f32 accumulate)",
+        "data": "synthetic (device-generated N(0,0.02) Q4_K/Q8_0 experts in pinned host stacks)",
         "config": {"workload": "DeepSeek-V2-Lite-shaped MoE prefill, 26 layers, 64 routed top-6 + 2 shared experts "
                                "streamed from pinned host memory per layer, 2048 tokens",
                    "layers": L, "chunk": chunk, "depth": depth, "plan_stride": stride,
@@ -635,6 +645,246 @@ def run_prefill_stream(args) -> int:
         "roofline": {"bound": "pcie", "achieved": round(pcie, 2), "peak": 64.0, "unit": "GB/s",
                      "frac": round(pcie / 64.0, 4), "traffic": None},
         "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def run_mixtral(args) -> int:
+    """Mixtral-8x7B-shaped MoE (32 layers, H 4096, 8 experts top-2, I 14336, Q4_K, uniform-random
+    router): decode steps at batch 1, 16 and 64 with every expert resident (router, expert decode and
+    residual per layer, layered launches), the 4096-token prefill in one chunk (grouped MFMA GEMMs), and
+    batch-1 decode with 4 of 8 experts cached per layer (misses staged from pinned host stacks).  The
+    JSON line's value is the batch-1 resident decode; the other parts are reported beside it."""
+    import naiwa_moe as nm
+
+    if nm.device_count() < 1:
+        log("no HIP device")
+        return 1
+    L = 32 if args.layers == 48 else args.layers
+    H, E, K, I = 4096, 8, 2, 14336
+    dt = (nm.Q4_K,) * 3
+    stream = nm.Stream()
+    t0 = time.time()
+    layers, keep = [], []
+    proj = I * (H // Q4K_BLOCK) * Q4K_BYTES
+    expert_bytes = 3 * proj
+    for l in range(L):
+        banks = nm.LayerBanks(E, H, I, dt)
+        for t, bank in enumerate((banks.gate, banks.up, banks.down)):
+            nm.synth(nm.Q4_K, 6000 + 8 * l + t, E * bank.n * bank.k, bank.base, 0.0, 0.02, stream=stream.handle)
+        router = nm.DeviceBuffer(E * H * 4)
+        nm.synth(nm.F32, 6000 + 8 * l + 3, E * H, router, 0.0, 0.02, stream=stream.handle)
+        layers.append(nm.layer_desc(router, banks))
+        keep.append((banks, router))
+    arr = (nm._lib.Layer * L)(*layers)
+    max_rows = 4096
+    xs = nm.DeviceBuffer(max_rows * H * 2)
+    nm.synth(nm.BF16, 998, max_rows * H, xs, 0.0, 1.0, stream=stream.handle)
+    stream.sync()
+    log(f"mixtral: {L} layers x {E} experts ({L * E * expert_bytes / 1e9:.1f} GB Q4_K) in {time.time() - t0:.1f}s")
+    lib = nm.lib()
+    out = {}
+
+    # ---- resident decode at batch 1 / 16 / 64 ----
+    for rows in (1, 16, 64):
+        x = nm.DeviceBuffer(rows * H * 2)
+        ids_d, w_d = nm.DeviceBuffer(L * rows * K * 4), nm.DeviceBuffer(L * rows * K * 4)
+        steps = max(3, min(args.steps, 20))
+
+        def step(i):
+            lib.naiwa_memcpy_d2d(x.ptr, xs.ptr + (i * rows % (max_rows - rows + 1)) * H * 2, rows * H * 2,
+                                 stream.handle)
+            nm.stack_decode(arr, x, rows, H, E, K, mode=nm.ROUTE_TOPK_SOFTMAX, ids_out=ids_d, w_out=w_d,
+                            fused=False, stream=stream.handle)
+        for i in range(2):
+            step(i)
+        stream.sync()
+        e0, e1 = nm.Event(), nm.Event()
+        e0.record(stream.handle)
+        for i in range(steps):
+            step(2 + i)
+        e1.record(stream.handle)
+        stream.sync()
+        ms = e0.elapsed_ms(e1) / steps
+        ids = ids_d.download(np.uint32).reshape(L, rows, K)
+        distinct = sum(len(np.unique(ids[l])) for l in range(L))
+        alg = distinct * expert_bytes + L * (E * H * 4 + rows * H * 4)
+        gbs = alg / (ms / 1e3) / 1e9
+        out[f"decode_bs{rows}"] = {"tok_s": round(rows / (ms / 1e3), 2), "ms_per_step": round(ms, 3),
+                                   "distinct_experts_per_layer": round(distinct / L, 2),
+                                   "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"mixtral decode bs{rows}: {ms:.3f} ms/step, {rows / (ms / 1e3):.1f} tok/s, {distinct / L:.2f} "
+            f"experts/layer, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak)")
+
+    # ---- the 4096-token prefill, one chunk per layer ----
+    T = 4096
+    x = nm.DeviceBuffer(T * H * 2)
+    ids, w = nm.DeviceBuffer(T * K * 4), nm.DeviceBuffer(T * K * 4)
+    y = nm.DeviceBuffer(T * H * 4)
+
+    def prefill():
+        lib.naiwa_memcpy_d2d(x.ptr, xs.ptr, T * H * 2, stream.handle)
+        for banks, router in keep:
+            nm.router_topk(x, nm.BF16, router, T, H, E, K, ids, w, mode=nm.ROUTE_TOPK_SOFTMAX, stream=stream.handle)
+            nm.moe_prefill(banks, x, ids, w, T, K, y, stream=stream.handle)
+            nm._lib.check(lib.naiwa_residual_add_bf16(x.ptr, y.ptr, T * H, stream.handle), "residual")
+    prefill()
+    stream.sync()
+    e0, e1 = nm.Event(), nm.Event()
+    e0.record(stream.handle)
+    reps = 2
+    for _ in range(reps):
+        prefill()
+    e1.record(stream.handle)
+    stream.sync()
+    ms = e0.elapsed_ms(e1) / reps
+    flop = 6.0 * H * I * K * T * L
+    tflops = flop / (ms / 1e3) / 1e12
+    out["prefill_4096"] = {"tok_s": round(T / (ms / 1e3), 1), "ms": round(ms, 2), "tflops": round(tflops, 1),
+                           "mfma_frac": round(tflops / 2500.0, 4), "flop": flop}
+    log(f"mixtral prefill {T} tokens: {ms:.1f} ms, {T / (ms / 1e3):.0f} tok/s, {tflops:.0f} TFLOP/s "
+        f"({tflops / 2500 * 100:.1f}% of 2.5 PFLOP/s dense)")
+    del x, ids, w, y
+
+    # ---- batch-1 decode with 4 of 8 experts cached per layer ----
+    usable = 4
+    copy = nm.Stream()
+    ring = nm.policy.StagingRing()
+    cached, ckeep = [], []
+    for l, (banks, router) in enumerate(keep[: min(L, args.cache_layers)]):
+        hs = nm.HostExpertStacks(E, H, I, dt, interleaved=True)
+        for t, bank in enumerate((banks.gate, banks.up, banks.down)):
+            nm._lib.check(lib.naiwa_memcpy_2d(hs.ptrs[t], hs.stride, bank.base, bank.stride, proj, E, stream.handle),
+                          "memcpy_2d")
+        stream.sync()
+        cb = nm.LayerBanks(usable + ring.length, H, I, dt, contiguous=True)
+        layer = nm.policy.CachedLayer(router, cb, hs, E, K, usable, ring, copy.handle, mode=nm.ROUTE_TOPK_SOFTMAX)
+        layer.seed(list(range(usable)))
+        cached.append(layer)
+        ckeep += [hs, cb]
+    Lc = len(cached)
+    xc = nm.DeviceBuffer(H * 2)
+    yc = nm.DeviceBuffer(H * 4)
+    tot = {"hits": 0, "staged": 0, "staged_experts": 0, "pcie_bytes": 0}
+
+    def cstep(i):
+        lib.naiwa_memcpy_d2d(xc.ptr, xs.ptr + i * H * 2, H * 2, stream.handle)
+        for layer in cached:
+            info = layer.forward(xc, 1, yc, pcie_frac=1.0, promote_cap=1, min_hits=4, stream=stream.handle)
+            nm._lib.check(lib.naiwa_residual_add_bf16(xc.ptr, yc.ptr, H, stream.handle), "residual")
+            for k_ in tot:
+                tot[k_] += info[k_]
+    cstep(0)
+    stream.sync()
+    for k_ in tot:
+        tot[k_] = 0
+    csteps = 4
+    e0, e1 = nm.Event(), nm.Event()
+    e0.record(stream.handle)
+    for i in range(csteps):
+        cstep(1 + i)
+    e1.record(stream.handle)
+    stream.sync()
+    ms = e0.elapsed_ms(e1) / csteps
+    pcie = tot["pcie_bytes"] / csteps / (ms / 1e3) / 1e9
+    out["cache_4of8_bs1"] = {"layers": Lc, "ms_per_token": round(ms, 2), "tok_s_at_32_layers": round(1e3 / (ms * 32 / Lc), 3),
+                             "hit_rate": round(tot["hits"] / max(1, tot["hits"] + tot["staged"]), 3),
+                             "staged_experts_per_layer_token": round(tot["staged_experts"] / (csteps * Lc), 3),
+                             "pcie_gbs": round(pcie, 2), "pcie_frac": round(pcie / 64.0, 4)}
+    log(f"mixtral 4-of-8 cache, bs1, {Lc} layers: {ms:.2f} ms/token, hit rate "
+        f"{out['cache_4of8_bs1']['hit_rate']:.3f}, PCIe {pcie:.1f} GB/s ({pcie / 64 * 100:.0f}% of 64 GB/s)")
+    del cached, ckeep
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        sample = []
+        for banks, router in keep[:1]:
+            get = lambda b: b.buffer.download(np.uint8).reshape(E, b.n, -1)
+            sample.append((router.download(np.float32).reshape(E, H), (get(banks.gate), get(banks.up),
+                                                                     get(banks.down))))
+        cpu = cpu_baseline(nm, sample, xs, 1, H, E, K, I, L, args.cpu_seconds)
+    d1 = out["decode_bs1"]
+    result = {
+        "metric": "MoE decode tok/s @bs1 (Mixtral-8x7B shape, Q4_K, all experts resident)",
+        "value": d1["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": max(3, min(args.steps, 20)), "warmup": 2,
+        "ms_per_step": d1["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 x Q4_K (f32 accumulate); prefill f16 x Q4_K (f32 accumulate)",
+        "data": "synthetic (device-generated N(0,0.02) Q4_K experts, N(0,1) bf16 tokens)",
+        "config": {"workload": "Mixtral-8x7B-shaped MoE stack: decode bs 1/16/64 (all resident), 4096-token "
+                               "prefill, bs1 decode with 4 of 8 experts cached", "layers": L, "hidden": H,
+                   "experts": E, "top_k": K, "intermediate": I, "weights": "Q4_K", "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": d1["hbm_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": d1["hbm_frac"], "traffic": None, "kernel": "layered decode step (bs1)"},
+        "parts": out,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def run_doorbell(args) -> int:
+    """Doorbell round trip: the host release-stores seq = i into mapped memory, one
+    persistent device wave (doorbell_poll_serve) observes it and release-stores ack = i,
+    the host observes the ack.  Median and p99 over --db-iters rings (the reference's
+    harness reports 31.7 us per iteration with a stream sync each, docs/worklogs/m0.md:43)."""
+    import ctypes as C
+
+    import naiwa_moe as nm
+
+    if nm.device_count() < 1:
+        log("no HIP device")
+        return 1
+    lib = nm.lib()
+    n = args.db_iters
+    host = C.c_void_p()
+    nm._lib.check(lib.doorbell_alloc_mapped(C.byref(host), 256), "doorbell_alloc_mapped")
+    dev = C.c_void_p()
+    lib.doorbell_get_device_ptr(host, C.byref(dev))
+    if not dev.value:
+        log("no device view of the mapped doorbell")
+        return 1
+    seq_h, ack_h = host.value, host.value + 128
+    seq_d, ack_d = dev.value, dev.value + 128
+    stream = nm.Stream()
+    before = C.c_uint32()
+    lib.naiwa_doorbell_timeouts(C.byref(before))
+    nm._lib.check(lib.doorbell_poll_serve(seq_d, ack_d, 1, n, stream.handle), "doorbell_poll_serve")
+    lat = np.zeros(n)
+    for i in range(1, n + 1):
+        t0 = time.perf_counter_ns()
+        lib.naiwa_host_store_release_u32(seq_h, i)
+        if lib.naiwa_host_wait_ge(ack_h, i, 2_000_000, 50) != 0:
+            log(f"doorbell: ack {i} not seen within 2 s")
+            lib.naiwa_host_store_release_u32(seq_h, n)  # let the wave finish its rings
+            stream.sync()
+            return 1
+        lat[i - 1] = (time.perf_counter_ns() - t0) / 1e3
+    stream.sync()
+    after = C.c_uint32()
+    lib.naiwa_doorbell_timeouts(C.byref(after))
+    # the reference's style: one launch and a stream sync per round trip
+    m = 200
+    sync_lat = np.zeros(m)
+    for i in range(m):
+        t0 = time.perf_counter_ns()
+        nm._lib.check(lib.doorbell_poll_serve(seq_d, ack_d, n, 1, stream.handle), "doorbell_poll_serve")
+        stream.sync()
+        sync_lat[i] = (time.perf_counter_ns() - t0) / 1e3
+    lib.doorbell_free_host(host)
+    med, p99 = float(np.median(lat)), float(np.percentile(lat, 99))
+    log(f"doorbell round trip over {n} rings: median {med:.2f} us, p99 {p99:.2f} us, max {lat.max():.1f} us; "
+        f"launch + stream sync per trip: median {np.median(sync_lat):.1f} us; timeouts {after.value - before.value}")
+    result = {
+        "metric": "doorbell round-trip latency (host ring -> persistent device wave -> host), median",
+        "value": round(med, 3), "unit": "us", "n_gpus": 1, "steps": n, "warmup": 0,
+        "ms_per_step": round(med / 1e3, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u32", "data": "synthetic",
+        "config": {"workload": "doorbell_poll_serve round trips over fine-grained mapped host memory",
+                   "iterations": n},
+        "p99_us": round(p99, 3), "max_us": round(float(lat.max()), 2),
+        "launch_and_sync_us_median": round(float(np.median(sync_lat)), 2),
+        "roofline": None, "cpu_baseline": None,
     }
     print(json.dumps(result), flush=True)
     return 0
@@ -715,18 +965,53 @@ def run_prefill(args) -> int:
     tok_s = tokens / (ms / 1e3)
     log(f"prefill: {ms:.2f} ms per {tokens}-token prefill, {tok_s:.0f} tok/s, {tflops:.1f} TFLOP/s "
         f"({tflops / 2500 * 100:.1f}% of 2.5 PFLOP/s f16 dense)")
+    # The grouped call's roofline: a 512-token chunk's 3072 routed + 1024 shared pairs touch
+    # every expert of the layer (66 x 6,307,840 B of weights) for 70.9 GFLOP, 170 flop/B,
+    # below the ridge of 2.5 PFLOP/s / 8 TB/s = 312 flop/B: the call is HBM-bound.  Each
+    # layer-chunk's naiwa_moe_prefill is timed with events on its stream (one more pass).
+    per_expert = (2 * I * nm.row_bytes(dt[0], H) + H * nm.row_bytes(dt[2], I))
+    ev = [(nm.Event(), nm.Event()) for _ in range(chunks * L)]
+    lib.naiwa_memcpy_d2d(x.ptr, xs.ptr, tokens * H * 2, stream.handle)
+    distinct = []
+    for c in range(chunks):
+        xc = x.ptr + c * T * H * 2
+        for li, (banks, router) in enumerate(layers):
+            nm.router_topk(xc, nm.BF16, router, T, H, E, K, ids, w, mode=nm.ROUTE_SOFTMAX_TOPK, stream=stream.handle)
+            for dst, src in ((ids_all, ids), (w_all, w)):
+                nm._lib.check(lib.naiwa_memcpy_2d_d2d(dst.ptr, KA * 4, src.ptr, K * 4, K * 4, T, stream.handle),
+                              "routing columns")
+            a, b = ev[c * L + li]
+            a.record(stream.handle)
+            nm.moe_prefill(banks, xc, ids_all, w_all, T, KA, y, stream=stream.handle)
+            b.record(stream.handle)
+            nm._lib.check(lib.naiwa_residual_add_bf16(xc, y.ptr, T * H, stream.handle), "residual")
+            if li == 0 and c == 0:
+                stream.sync()
+                distinct.append(len(np.unique(ids.download(np.uint32))))
+    stream.sync()
+    call_ms = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
+    n_exp = (distinct[0] if distinct else E) + S_
+    call_bytes = n_exp * per_expert + T * H * 2 + T * KA * 8 + T * H * 4
+    hbm = call_bytes / (call_ms / 1e3) / 1e9
+    call_flop = 6.0 * H * I * KA * T
+    log(f"prefill call (one layer-chunk): {call_ms * 1e3:.1f} us, {call_bytes / 1e6:.1f} MB ({n_exp} experts), "
+        f"{hbm:.0f} GB/s = {hbm / HBM_PEAK_GBS * 100:.1f}% of HBM peak; {call_flop / (call_ms / 1e3) / 1e12:.0f} TFLOP/s")
     result = {
         "metric": "MoE prefill tok/s (DeepSeek-V2-Lite shape, 2048 tokens in 512-token chunks)",
         "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f16", "data": "synthetic (device-generated N(0,0.02) Q4_K/Q8_0 experts, N(0,1) bf16 tokens)",
+        "dtype": "f16 x Q4_K/Q8_0 (f32 accumulate)",
+        "data": "synthetic (device-generated N(0,0.02) Q4_K/Q8_0 experts, N(0,1) bf16 tokens)",
         "config": {"workload": "DeepSeek-V2-Lite-shaped MoE prefill, 26 layers, 64 routed top-6 + 2 shared "
                                "experts, I 1408, gate/up Q4_K, down Q8_0, 2048 tokens in 512-token chunks",
                    "layers": L, "hidden": H, "experts": E, "shared": S_, "top_k": K, "intermediate": I,
                    "chunk": T, "tokens": tokens, "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
-                     "frac": round(tflops / 2500.0, 4), "traffic": None,
-                     "flop_per_step": flop},
+        "roofline": {"bound": "hbm", "achieved": round(hbm, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(hbm / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "naiwa_moe_prefill (one 512-token layer-chunk: gather, tiles, GEMMs, combine)",
+                     "bytes_per_launch": call_bytes, "call_avg_us": round(call_ms * 1e3, 2),
+                     "mfma_tflops": round(call_flop / (call_ms / 1e3) / 1e12, 2),
+                     "mfma_frac": round(call_flop / (call_ms / 1e3) / 1e12 / 2500.0, 4)},
         "cpu_baseline": None,
     }
     print(json.dumps(result), flush=True)

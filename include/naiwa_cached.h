@@ -35,10 +35,19 @@ typedef struct naiwa_cached_layer_desc {
     const float* router;      /* device [E, H] f32 */
     const float* router_bias; /* device [E] f32 or null */
     naiwa_bank gate, up, down; /* device banks, slots >= usable + ring length */
-    const void* host_gate;    /* pinned stacked [E, I, H] bytes (expert e at e * expert bytes) */
+    const void* host_gate;    /* pinned host bytes of expert 0's gate projection */
     const void* host_up;
     const void* host_down;
     int num_experts, top_k, hidden, inter, usable, mode, act;
+    /* Bytes between consecutive experts in the host stacks.  0: each projection
+     * is a stacked [E, N, K] tensor of its own (expert e at host_p + e * that
+     * projection's bytes, the GGUF layout).  Otherwise every projection's
+     * expert e is at host_p + e * host_expert_stride.  When an expert's gate,
+     * up and down are adjacent both in the host stacks (host_up = host_gate +
+     * gate bytes, host_down = host_up + up bytes) and in every slot (up.base =
+     * gate.base + gate bytes, down.base = up.base + up bytes, one common slot
+     * stride), an upload is one copy of the whole expert. */
+    int64_t host_expert_stride;
 } naiwa_cached_layer_desc;
 
 /* Per-step report of naiwa_cached_layer_forward. */
@@ -83,9 +92,21 @@ int naiwa_cached_layer_fill(naiwa_cached_layer* L, int expert, int* slot_out);
  * one synchronisation.  *filled = experts placed. */
 int naiwa_cached_layer_seed(naiwa_cached_layer* L, const uint32_t* experts, int n, float fill_share, int* filled);
 
-/* One decode step: x bf16 [rows, H] -> out f32 [rows, H], all on `stream`
- * except the routing read-back, which synchronises it (the reference's
- * top-k round trip).  pcie_frac, promote_cap and min_hits are the
+/* One decode step: x bf16 [rows, H] -> out f32 [rows, H], all on `stream`.
+ * Staged uploads are one kernel reading the host stacks through their device
+ * mapping when they are mapped pinned memory, else DMA copies; the
+ * environment variable NAIWA_UPLOAD_PATH=dma takes DMA copies always.
+ * The routing comes back through a mapped doorbell (the reference's
+ * TopkDoorbell, src/doorbell/d2h/topk.rs:20-125): the device writes the
+ * top-k into fine-grained host memory and raises a sequence word, and the
+ * host spins on that word (at most 10 s, else NAIWA_E_TIMEOUT) instead of
+ * synchronising the stream.  Steps of one layer are ordered even when each
+ * is queued on another stream (a step waits for the previous step's last
+ * read of the layer's buffers).  Staged uploads complete into the staged
+ * expert pass through an event the stream waits for, or, with the
+ * environment variable NAIWA_UPLOAD_SYNC=poll, through a device flag the
+ * copy stream raises and one device wave polls (doorbell_poll_signal /
+ * doorbell_poll_wait).  pcie_frac, promote_cap and min_hits are the
  * reference's --pcie-frac, NAIWA_PROMOTE_CAP and NAIWA_PROMOTE_MIN_HITS. */
 int naiwa_cached_layer_forward(naiwa_cached_layer* L, const void* x, int rows, float* out, float pcie_frac,
                                int promote_cap, uint64_t min_hits, int64_t stream, naiwa_cached_step* info);

@@ -85,6 +85,10 @@ int naiwa_memcpy_d2d(void* dst, const void* src, size_t bytes, int64_t stream);
  * (e.g. a [T, k] routing result into the first k columns of a [T, k + s] one). */
 int naiwa_memcpy_2d_d2d(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width, size_t height,
                         int64_t stream);
+/* The same in any direction (host or device pointers on either side, e.g. one
+ * projection's [E] expert ranges into interleaved pinned host stacks). */
+int naiwa_memcpy_2d(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width, size_t height,
+                    int64_t stream);
 int naiwa_memset(void* p, int value, size_t bytes, int64_t stream);
 int naiwa_stream_create(int64_t* stream);
 int naiwa_stream_destroy(int64_t stream);
@@ -122,6 +126,22 @@ void doorbell_copy_f32(void* d_seq, void* d_dst, const void* src, int n, int64_t
  * nothing, leaves d_consumed alone and counts a timeout. */
 void doorbell_wait_copy_f32(void* d_seq, uint32_t target, void* d_payload, int64_t slot_off,
                             void* d_consumed, void* dst, int n, int64_t stream);
+/* The persistent-wave variant of the device-side doorbell waits (the
+ * reference launches one spinning kernel per wait, doorbell.cu:105-149):
+ *  - doorbell_poll_serve: one wave answers `count` host rings in a row: for
+ *    i = 0 .. count-1 it waits until *d_seq >= first + i, then release-stores
+ *    first + i to *d_ack (the host's round trip is ring -> observe ack);
+ *  - doorbell_poll_wait: a stream-ordered wait for *d_flag >= target, polled by
+ *    one wave (e.g. an "upload done" flag another stream raises): work queued
+ *    after it on `stream` starts when it exits;
+ *  - doorbell_poll_signal: release-store `value` to *d_flag once the work
+ *    queued before it on `stream` is done.
+ * Flags are u32 words in device memory or mapped memory (device pointers).
+ * Every wait is bounded like doorbell_wait_copy_f32's; an expired wait counts a
+ * timeout (naiwa_doorbell_timeouts) and the wave exits. */
+int  doorbell_poll_serve(void* d_seq, void* d_ack, uint32_t first, uint32_t count, int64_t stream);
+int  doorbell_poll_wait(const void* d_flag, uint32_t target, int64_t stream);
+int  doorbell_poll_signal(void* d_flag, uint32_t value, int64_t stream);
 /* Bound of every device-side doorbell wait (default 10 s; 0 restores it). */
 int  naiwa_doorbell_set_wait_limit_us(uint64_t us);
 /* Device waits that expired since the library was loaded. */
@@ -257,9 +277,11 @@ int naiwa_stack_decode_y(const naiwa_layer* layers, int n_layers, void* x, int r
 
 /* Blocks per CU of the fused kernel (1..8, capped by occupancy; default 1). */
 int naiwa_stack_set_blocks_per_cu(int n);
-/* Counters of the last fused launch: waits for another workgroup's data that
- * gave up after their 2 s bound, and routed experts with no resident slot
- * (weight dropped).  Synchronizes the device. */
+/* Counters of every fused launch since the last call: waits for another
+ * workgroup's data that gave up after their 2 s bound (the grid was not
+ * co-resident, e.g. another tenant held CUs; that launch's output is invalid),
+ * and routed experts with no resident slot (weight dropped).  Reading resets
+ * them.  Synchronizes the device. */
 int naiwa_stack_status(int* barrier_timeouts, int* missing_experts);
 
 /* Diagnostic phase timestamps of the fused kernel: when enabled, every block

@@ -26,13 +26,21 @@ CFLAGS = [
 ]
 
 
+# Host-code sanitizers (CPU runs only): every -fsanitize flag applies to the host
+# compilation alone (-Xarch_host before it); device code is built as usual.
+SANITIZE = {
+    "address": ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer"],
+    "thread": ["-Xarch_host", "-fsanitize=thread"],
+}
+
+
 def sources() -> list[str]:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
+def _compile(src: str, build_dir: str = BUILD, extra: tuple = ()) -> str:
+    obj = os.path.join(build_dir, os.path.basename(src) + ".o")
+    cmd = [HIPCC, *CFLAGS, *extra, "-c", src, "-o", obj]
     if src.endswith(".cpp"):
         cmd[1:1] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -46,21 +54,31 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(jobs: int = 8) -> str:
-    os.makedirs(BUILD, exist_ok=True)
+def build(jobs: int = 8, sanitize: str | None = None) -> str:
+    """Build the library; with sanitize ("address" or "thread") an instrumented copy of
+    the host code goes to naiwa-rs_amd/_san/libnaiwa_moe_<sanitize>.so instead (for CPU
+    test runs with the matching runtime preloaded; never for the GPU)."""
+    extra = tuple(SANITIZE[sanitize]) if sanitize else ()
+    build_dir = BUILD if not sanitize else os.path.join(HERE, "_san", "obj_" + sanitize)
+    lib = LIB if not sanitize else os.path.join(HERE, "_san", f"libnaiwa_moe_{sanitize}.so")
+    os.makedirs(build_dir, exist_ok=True)
     srcs = sources()
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs,
+        objs = list(ex.map(lambda s_: _compile(s_, build_dir, extra), srcs))
+    tmp = lib + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *extra, "-o", tmp, *objs,
            "-Wl,-rpath,/opt/rocm/lib", "-lpthread"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError("link failed")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":
-    print(build())
+    import argparse
+
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--sanitize", choices=sorted(SANITIZE), default=None)
+    print(build(sanitize=ap.parse_args().sanitize))

@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 #include <initializer_list>
 #include <new>
 #include <vector>
@@ -21,6 +23,42 @@ bool bank_ok(const naiwa_bank& b, int n, int k, int min_slots) {
     return b.base && b.n == n && b.k == k && b.slots >= min_slots &&
            naiwa_projection_bytes(b.dtype, n, k) > 0 && b.slot_stride >= naiwa_projection_bytes(b.dtype, n, k);
 }
+
+// Doorbell layout of a layer's routing read-back (fine-grained mapped host memory):
+// [seq u32][15 pad words][ids n][weights n][predicted ids n].
+constexpr int kDbHead = 16;
+
+// The routing of one step into the mapped doorbell, then seq + 1 behind a system-scope
+// fence: the host spins on seq instead of synchronising the stream (the reference's
+// TopkDoorbell publish, src/doorbell/d2h/topk.rs:20-125).
+__global__ void __launch_bounds__(256)
+routing_publish_kernel(uint32_t* db, const uint32_t* ids, const float* w, int n, const uint32_t* pred, int npred) {
+    volatile uint32_t* out = db + kDbHead;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        out[i] = ids[i];
+        out[n + i] = __float_as_uint(w[i]);
+    }
+    for (int i = threadIdx.x; i < npred; i += blockDim.x) out[2 * n + i] = pred[i];
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t cur = __hip_atomic_load(db, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(db, cur + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
+// Staged-upload completion as a flag polled by one device wave (NAIWA_UPLOAD_SYNC=poll)
+// instead of an event the compute stream waits for (the default).
+bool upload_sync_poll() {
+    static const bool poll = [] {
+        const char* v = getenv("NAIWA_UPLOAD_SYNC");
+        return v && strcmp(v, "poll") == 0;
+    }();
+    return poll;
+}
+
+// Bound of the host's wait for a routing doorbell.
+constexpr int64_t kRouteWaitUs = 10 * 1000 * 1000;
 
 } // namespace
 
@@ -37,7 +75,6 @@ struct naiwa_cached_layer {
     // inputs [slot ids | weights of the cache pairs | of the staged pairs], so that each
     // crosses the link in one copy; the views below are set per step (n = rows * k)
     uint32_t* route_dev_base = nullptr;
-    uint32_t* route_h_base = nullptr;
     uint32_t* in_dev_base = nullptr;
     uint32_t* in_h_base = nullptr;
     uint32_t* ids_dev = nullptr;
@@ -50,11 +87,27 @@ struct naiwa_cached_layer {
     float* wsplit_h = nullptr;     // pinned: weights of the cache pairs | of the staged pairs
     float* wsplit_dev = nullptr;
     int last_rows = 0;
+    // routing read-back doorbell: host view, device view, publishes so far
+    uint32_t* db_host = nullptr;
+    uint32_t* db_dev = nullptr;
+    uint32_t db_seq = 0;
+    // the stream of the previous step: a step on another stream waits for read_done first
+    hipStream_t last_stream = nullptr;
+    bool have_last_stream = false;
+    // staged-upload completion flag (device word) and its epoch, for NAIWA_UPLOAD_SYNC=poll
+    uint32_t* upload_flag = nullptr;
+    uint32_t upload_epoch = 0;
     std::vector<hipEvent_t> ring_fence;  // per ring position: recorded after the step that read it
     std::vector<char> ring_fenced;
     hipEvent_t staged_done = nullptr;
     bool batch_uploads = false;          // staged uploads as one batched copy kernel, reading
     const void* host_dev[3] = {nullptr, nullptr, nullptr}; // the host stacks' device views
+    size_t host_stride[3] = {0, 0, 0};   // bytes between experts in each host stack
+    // an expert's gate | up | down are adjacent both in the host stacks and in a slot:
+    // one expert is one range (one DMA copy, or one range of the batched copy kernel)
+    bool contiguous = false;
+    size_t expert_bytes = 0;
+    bool dma_uploads = false;            // NAIWA_UPLOAD_PATH=dma: staged uploads as DMA copies
     // lookahead: this layer's prediction (its router on the previous layer's
     // activation), the fence after the last step that read its cache slots,
     // and the claim a forward waits for before its expert kernel
@@ -71,10 +124,12 @@ struct naiwa_cached_layer {
     void release_buffers() {
         if (route_dev_base) (void)hipFree(route_dev_base);
         if (in_dev_base) (void)hipFree(in_dev_base);
-        if (route_h_base) (void)hipHostFree(route_h_base);
+        if (db_host) (void)doorbell_free_host(db_host);
+        db_host = db_dev = nullptr;
+        db_seq = 0;
         if (in_h_base) (void)hipHostFree(in_h_base);
         if (slots_h) (void)hipHostFree(slots_h);
-        route_dev_base = route_h_base = in_dev_base = in_h_base = nullptr;
+        route_dev_base = in_dev_base = in_h_base = nullptr;
         views(0);
         if (pred_ids_dev) (void)hipFree(pred_ids_dev);
         if (pred_w_dev) (void)hipFree(pred_w_dev);
@@ -94,13 +149,25 @@ struct naiwa_cached_layer {
         if (e != hipSuccess) return (int)e;
         release_buffers();
         const size_t n = (size_t)rows * d.top_k;
-        if (hipMalloc(&route_dev_base, 2 * n * 4) != hipSuccess || hipHostMalloc(&route_h_base, 2 * n * 4, 0) != hipSuccess ||
+        void* db = nullptr;
+        if (hipMalloc(&route_dev_base, 2 * n * 4) != hipSuccess ||
+            doorbell_alloc_mapped(&db, (kDbHead + 3 * n) * 4) != NAIWA_OK ||
             hipMalloc(&in_dev_base, 3 * n * 4) != hipSuccess || hipHostMalloc(&in_h_base, 3 * n * 4, 0) != hipSuccess ||
             hipHostMalloc(&slots_h, n * 4, 0) != hipSuccess || hipMalloc(&pred_ids_dev, n * 4) != hipSuccess ||
             hipMalloc(&pred_w_dev, n * 4) != hipSuccess || hipHostMalloc(&pred_ids_h, n * 4, 0) != hipSuccess) {
+            if (db) db_host = (uint32_t*)db;
             release_buffers();
             return NAIWA_E_NOMEM;
         }
+        db_host = (uint32_t*)db;
+        void* dv = nullptr;
+        doorbell_get_device_ptr(db, &dv);
+        if (!dv) {
+            release_buffers();
+            return NAIWA_E_DEVICE;
+        }
+        db_dev = (uint32_t*)dv;
+        db_seq = 0;
         cap_rows = rows;
         return NAIWA_OK;
     }
@@ -109,8 +176,8 @@ struct naiwa_cached_layer {
     void views(int n) {
         ids_dev = route_dev_base;
         w_dev = route_dev_base ? (float*)(route_dev_base + n) : nullptr;
-        ids_h = route_h_base;
-        w_h = route_h_base ? (float*)(route_h_base + n) : nullptr;
+        ids_h = db_host ? db_host + kDbHead : nullptr;
+        w_h = db_host ? (float*)(db_host + kDbHead + n) : nullptr;
         slots_dev = in_dev_base;
         wsplit_dev = in_dev_base ? (float*)(in_dev_base + n) : nullptr;
         slots_up = in_h_base;
@@ -123,9 +190,22 @@ struct naiwa_cached_layer {
         dst[2] = (uint8_t*)d.down.base + (int64_t)slot * d.down.slot_stride;
     }
     void host_ptrs(int expert, const void* src[3]) const {
-        src[0] = (const uint8_t*)d.host_gate + (size_t)expert * bytes[0];
-        src[1] = (const uint8_t*)d.host_up + (size_t)expert * bytes[1];
-        src[2] = (const uint8_t*)d.host_down + (size_t)expert * bytes[2];
+        src[0] = (const uint8_t*)d.host_gate + (size_t)expert * host_stride[0];
+        src[1] = (const uint8_t*)d.host_up + (size_t)expert * host_stride[1];
+        src[2] = (const uint8_t*)d.host_down + (size_t)expert * host_stride[2];
+    }
+
+    // Queue the upload of `expert` into `slot` on the copy stream after `fence` (0 = none):
+    // one DMA copy when the expert is contiguous, else one per projection.
+    int upload(int expert, int slot, int64_t fence) const {
+        void* dst[3];
+        const void* src[3];
+        slot_ptrs(slot, dst);
+        host_ptrs(expert, src);
+        if (!contiguous) return naiwa_upload_expert(dst, src, bytes, (int64_t)copy, fence, 0);
+        int rc = 0;
+        if (fence && (rc = naiwa_hip_rc(hipStreamWaitEvent(copy, (hipEvent_t)fence, 0)))) return rc;
+        return naiwa_hip_rc(hipMemcpyAsync(dst[0], src[0], expert_bytes, hipMemcpyHostToDevice, copy));
     }
 
     // predict (src/moe/cached_layer.rs:1245-1259): this layer's router on the
@@ -133,14 +213,10 @@ struct naiwa_cached_layer {
     // as in this layer's own routing; without one these are the reference's raw
     // logits), read back with the caller's next synchronisation of `stream`
     int predict_launch(const void* x, int rows, int64_t stream) {
-        const int n = rows * d.top_k;
         int rc = naiwa_router_topk_biased(x, NAIWA_BF16, d.router, d.router_bias, rows, d.hidden, d.num_experts,
                                           d.top_k, NAIWA_ROUTE_TOPK_SOFTMAX, pred_ids_dev, pred_w_dev, nullptr,
                                           stream);
         if (rc) return rc;
-        if ((rc = naiwa_hip_rc(hipMemcpyAsync(pred_ids_h, pred_ids_dev, (size_t)n * 4, hipMemcpyDeviceToHost,
-                                              (hipStream_t)stream))))
-            return rc;
         pred_rows = rows;
         return NAIWA_OK;
     }
@@ -152,13 +228,13 @@ struct naiwa_cached_layer {
     // the copy stream behind the last step that read this layer's slots; the
     // slots are published at once, because the only reader, this layer's next
     // expert kernel, waits for the claim (ahead_done) recorded after them.
-    int prefetch_apply(int swaps_per_row, naiwa_lookahead_step* info) {
+    int prefetch_apply(const uint32_t* pred_ids, int swaps_per_row, naiwa_lookahead_step* info) {
         naiwa_lookahead_step a{};
         const int rows = pred_rows, k = d.top_k;
         std::vector<int> lens((size_t)rows, k);
         predicted.assign((size_t)rows * k, 0u);
         int np = 0;
-        int rc = naiwa_union_by_votes(pred_ids_h, lens.data(), rows, predicted.data(), (int)predicted.size(), &np);
+        int rc = naiwa_union_by_votes(pred_ids, lens.data(), rows, predicted.data(), (int)predicted.size(), &np);
         if (rc) return rc;
         predicted.resize((size_t)np);
         a.predicted = np;
@@ -178,11 +254,7 @@ struct naiwa_cached_layer {
                 swap = slot >= 0;
             }
             if (slot < 0) continue;
-            void* dst[3];
-            const void* src[3];
-            slot_ptrs(slot, dst);
-            host_ptrs((int)e, src);
-            if ((rc = naiwa_upload_expert(dst, src, bytes, (int64_t)copy, fence, 0))) {
+            if ((rc = upload((int)e, slot, fence))) {
                 naiwa_cache_unreserve(cache, slot);
                 return rc;
             }
@@ -221,15 +293,26 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     L->views(n);
     naiwa_cached_step step{};
 
-    // route on the device, then read the top-k back (the routing round trip)
+    // one layer's steps run in order whatever stream each is queued on: the routing
+    // buffers, the step inputs and the ring slots of the previous step are then free
+    if (L->have_last_stream && L->last_stream != st && L->read_recorded &&
+        (rc = naiwa_hip_rc(hipStreamWaitEvent(st, L->read_done, 0))))
+        return rc;
+    if (next && next->have_last_stream && next->last_stream != st && next->read_recorded &&
+        (rc = naiwa_hip_rc(hipStreamWaitEvent(st, next->read_done, 0))))
+        return rc;
+
+    // route on the device, then read the top-k back through the mapped doorbell: the
+    // router's results (and the lookahead's prediction) are published with seq + 1 and
+    // the host spins on seq, with no stream synchronisation (the routing round trip)
     rc = naiwa_router_topk_biased(x, NAIWA_BF16, d.router, d.router_bias, rows, d.hidden, d.num_experts, k, d.mode,
                                   L->ids_dev, L->w_dev, nullptr, stream);
     if (!rc && next) rc = next->predict_launch(x, rows, stream);
     if (rc) return rc;
-    // ids and weights are adjacent: one copy
-    if ((rc = naiwa_hip_rc(hipMemcpyAsync(L->ids_h, L->ids_dev, (size_t)n * 8, hipMemcpyDeviceToHost, st))) ||
-        (rc = naiwa_hip_rc(hipStreamSynchronize(st))))
-        return rc;
+    routing_publish_kernel<<<1, 256, 0, st>>>(L->db_dev, L->ids_dev, L->w_dev, n, next ? next->pred_ids_dev : nullptr,
+                                              next ? n : 0);
+    if ((rc = naiwa_hip_rc(hipGetLastError()))) return rc;
+    if ((rc = naiwa_host_wait_ge(L->db_host, ++L->db_seq, kRouteWaitUs, 20))) return rc;
     L->last_rows = rows;
 
     // hit/miss split, then the misses to stream into the ring
@@ -252,33 +335,38 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     }
 
     // uploads on the copy stream after the last step that read each ring slot: one kernel
-    // for all of them when the host stacks are mapped pinned memory, else one DMA copy per
-    // projection
+    // for all of them when the host stacks are mapped pinned memory (one range per expert
+    // when its projections are adjacent, else one per projection), else DMA copies (one per
+    // expert when adjacent, else one per projection)
     {
         naiwa_copy items[NAIWA_COPY_BATCH_MAX];
         int ni = 0;
-        const bool batch = L->batch_uploads && 3 * nc <= NAIWA_COPY_BATCH_MAX;
+        const bool batch = L->batch_uploads && !L->dma_uploads && 3 * nc <= NAIWA_COPY_BATCH_MAX;
         for (int i = 0; i < nc; ++i) {
-            void* dst[3];
-            L->slot_ptrs(d.usable + pos[i], dst);
+            const int64_t fence = L->ring_fenced[pos[i]] ? (int64_t)L->ring_fence[pos[i]] : 0;
             if (batch) {
-                for (int p = 0; p < 3; ++p)
-                    items[ni++] = naiwa_copy{dst[p], (const uint8_t*)L->host_dev[p] + (size_t)chosen[i] * L->bytes[p],
-                                             (uint64_t)L->bytes[p]};
-                if (L->ring_fenced[pos[i]] && (rc = naiwa_hip_rc(hipStreamWaitEvent(L->copy, L->ring_fence[pos[i]], 0))))
-                    return rc;
-            } else {
-                const void* src[3];
-                L->host_ptrs((int)chosen[i], src);
-                const int64_t fence = L->ring_fenced[pos[i]] ? (int64_t)L->ring_fence[pos[i]] : 0;
-                if ((rc = naiwa_upload_expert(dst, src, L->bytes, (int64_t)L->copy, fence, 0))) return rc;
+                void* dst[3];
+                L->slot_ptrs(d.usable + pos[i], dst);
+                if (L->contiguous)
+                    items[ni++] = naiwa_copy{dst[0], (const uint8_t*)L->host_dev[0] + (size_t)chosen[i] * L->host_stride[0],
+                                             (uint64_t)L->expert_bytes};
+                else
+                    for (int p = 0; p < 3; ++p)
+                        items[ni++] = naiwa_copy{dst[p],
+                                                 (const uint8_t*)L->host_dev[p] + (size_t)chosen[i] * L->host_stride[p],
+                                                 (uint64_t)L->bytes[p]};
+                if (fence && (rc = naiwa_hip_rc(hipStreamWaitEvent(L->copy, (hipEvent_t)fence, 0)))) return rc;
+            } else if ((rc = L->upload((int)chosen[i], d.usable + pos[i], fence))) {
+                return rc;
             }
         }
         if (batch && (rc = naiwa_copy_batch_mapped(items, ni, (int64_t)L->copy))) return rc;
         step.pcie_bytes += (int64_t)nc * (int64_t)(L->bytes[0] + L->bytes[1] + L->bytes[2]);
     }
     step.staged_experts = nc;
-    if (nc && (rc = naiwa_hip_rc(hipEventRecord(L->staged_done, L->copy)))) return rc;
+    const bool poll = upload_sync_poll();
+    if (nc && poll && (rc = doorbell_poll_signal(L->upload_flag, ++L->upload_epoch, (int64_t)L->copy))) return rc;
+    if (nc && !poll && (rc = naiwa_hip_rc(hipEventRecord(L->staged_done, L->copy)))) return rc;
 
     // the step's inputs in one copy: slot ids and, with staged pairs, the weights of the
     // cache pairs and of the staged pairs (adjacent after the slot ids)
@@ -312,7 +400,11 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         if ((rc = naiwa_moe_decode_ex(&d.gate, &d.up, &d.down, x, NAIWA_BF16, L->slots_dev, L->wsplit_dev, rows, k,
                                       d.act, out, 0, stream)))
             return rc;
-        if ((rc = naiwa_hip_rc(hipStreamWaitEvent(st, L->staged_done, 0)))) return rc;
+        if (poll)
+            rc = doorbell_poll_wait(L->upload_flag, L->upload_epoch, stream);
+        else
+            rc = naiwa_hip_rc(hipStreamWaitEvent(st, L->staged_done, 0));
+        if (rc) return rc;
         if ((rc = naiwa_moe_decode_ex(&d.gate, &d.up, &d.down, x, NAIWA_BF16, L->slots_dev, L->wsplit_dev + n, rows,
                                       k, d.act, out, NAIWA_DECODE_ACCUMULATE, stream)))
             return rc;
@@ -332,14 +424,21 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
             void* src[3];
             L->slot_ptrs(ps[i], dst);
             L->slot_ptrs(from, src);
-            // the three projections in one kernel (device to device)
+            // the three projections in one kernel (device to device), one range when adjacent
             naiwa_copy items[3];
-            for (int p = 0; p < 3; ++p) items[p] = naiwa_copy{dst[p], src[p], (uint64_t)L->bytes[p]};
-            rc = naiwa_copy_batch_mapped(items, 3, (int64_t)st);
-            if (rc == NAIWA_E_UNSUPPORTED) { // not 16-byte aligned: one copy per projection
+            int nitems = 1;
+            if (L->contiguous) {
+                items[0] = naiwa_copy{dst[0], src[0], (uint64_t)L->expert_bytes};
+            } else {
+                nitems = 3;
+                for (int p = 0; p < 3; ++p) items[p] = naiwa_copy{dst[p], src[p], (uint64_t)L->bytes[p]};
+            }
+            rc = naiwa_copy_batch_mapped(items, nitems, (int64_t)st);
+            if (rc == NAIWA_E_UNSUPPORTED) { // not 16-byte aligned: runtime copies
                 rc = NAIWA_OK;
-                for (int p = 0; p < 3 && !rc; ++p)
-                    rc = naiwa_hip_rc(hipMemcpyAsync(dst[p], src[p], L->bytes[p], hipMemcpyDeviceToDevice, st));
+                for (int p = 0; p < nitems && !rc; ++p)
+                    rc = naiwa_hip_rc(hipMemcpyAsync(items[p].dst, items[p].src, items[p].bytes, hipMemcpyDeviceToDevice,
+                                                     st));
             }
             if (rc) {
                 naiwa_cache_unreserve(L->cache, ps[i]);
@@ -369,7 +468,9 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     s.sync_waits = (uint64_t)((nc ? 1 : 0) + step.preload_waits);
     naiwa_stats_add(&s);
     if (info) *info = step;
-    if (next) return next->prefetch_apply(swaps_per_row, ahead);
+    L->last_stream = st;
+    L->have_last_stream = true;
+    if (next) return next->prefetch_apply(L->db_host + kDbHead + 2 * n, swaps_per_row, ahead);
     return NAIWA_OK;
 }
 
@@ -395,14 +496,32 @@ int naiwa_cached_layer_create(const naiwa_cached_layer_desc* d, naiwa_ring* ring
     L->bytes[0] = (size_t)naiwa_projection_bytes(d->gate.dtype, d->inter, d->hidden);
     L->bytes[1] = (size_t)naiwa_projection_bytes(d->up.dtype, d->inter, d->hidden);
     L->bytes[2] = (size_t)naiwa_projection_bytes(d->down.dtype, d->hidden, d->inter);
+    // host stacks: each projection stacked on its own (stride = its bytes), or experts
+    // interleaved with a common stride (host_expert_stride)
+    for (int p = 0; p < 3; ++p) L->host_stride[p] = d->host_expert_stride > 0 ? (size_t)d->host_expert_stride : L->bytes[p];
+    L->expert_bytes = L->bytes[0] + L->bytes[1] + L->bytes[2];
+    {
+        const uint8_t* hg = (const uint8_t*)d->host_gate;
+        const uint8_t* g = (const uint8_t*)d->gate.base;
+        L->contiguous = d->host_expert_stride >= (int64_t)L->expert_bytes &&
+                        (const uint8_t*)d->host_up == hg + L->bytes[0] &&
+                        (const uint8_t*)d->host_down == hg + L->bytes[0] + L->bytes[1] &&
+                        (const uint8_t*)d->up.base == g + L->bytes[0] &&
+                        (const uint8_t*)d->down.base == g + L->bytes[0] + L->bytes[1] &&
+                        d->gate.slot_stride == d->up.slot_stride && d->gate.slot_stride == d->down.slot_stride &&
+                        d->gate.slot_stride >= (int64_t)L->expert_bytes;
+        const char* v = getenv("NAIWA_UPLOAD_PATH");
+        L->dma_uploads = v && strcmp(v, "dma") == 0;
+    }
     // staged uploads read the host stacks through their device mapping when all three
     // are mapped pinned memory and every expert range is 16-byte aligned
     {
         const void* hs[3] = {d->host_gate, d->host_up, d->host_down};
         bool ok = true;
         for (int p = 0; p < 3 && ok; ++p) {
-            L->host_dev[p] = naiwa_device_view(hs[p], L->bytes[p] * (size_t)d->num_experts);
-            ok = L->host_dev[p] && !(((uintptr_t)L->host_dev[p] | L->bytes[p]) & 15);
+            const size_t span = L->host_stride[p] * (size_t)(d->num_experts - 1) + L->bytes[p];
+            L->host_dev[p] = naiwa_device_view(hs[p], span);
+            ok = L->host_dev[p] && !(((uintptr_t)L->host_dev[p] | L->bytes[p] | L->host_stride[p]) & 15);
         }
         L->batch_uploads = ok;
     }
@@ -417,6 +536,8 @@ int naiwa_cached_layer_create(const naiwa_cached_layer_desc* d, naiwa_ring* ring
         if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) rc = NAIWA_E_DEVICE;
     for (hipEvent_t* ev : {&L->staged_done, &L->read_done, &L->ahead_done})
         if (hipEventCreateWithFlags(ev, hipEventDisableTiming) != hipSuccess) rc = NAIWA_E_DEVICE;
+    if (!rc && (hipMalloc(&L->upload_flag, 256) != hipSuccess || hipMemset(L->upload_flag, 0, 256) != hipSuccess))
+        rc = NAIWA_E_NOMEM;
     if (!rc) rc = L->ensure_rows(8);
     if (rc) {
         naiwa_cached_layer_destroy(L);
@@ -434,6 +555,7 @@ int naiwa_cached_layer_destroy(naiwa_cached_layer* L) {
         if (ev) (void)hipEventDestroy(ev);
     for (hipEvent_t ev : {L->staged_done, L->read_done, L->ahead_done})
         if (ev) (void)hipEventDestroy(ev);
+    if (L->upload_flag) (void)hipFree(L->upload_flag);
     naiwa_cache_destroy(L->cache);
     delete L;
     return NAIWA_OK;
@@ -449,11 +571,7 @@ int naiwa_cached_layer_fill(naiwa_cached_layer* L, int expert, int* slot_out) {
     if (!L || !slot_out) return NAIWA_E_INVALID;
     int rc = naiwa_cache_admit(L->cache, expert, slot_out);
     if (rc || *slot_out < 0) return rc;
-    void* dst[3];
-    const void* src[3];
-    L->slot_ptrs(*slot_out, dst);
-    L->host_ptrs(expert, src);
-    rc = naiwa_upload_expert(dst, src, L->bytes, (int64_t)L->copy, 0, 0);
+    rc = L->upload(expert, *slot_out, 0);
     if (!rc) rc = naiwa_hip_rc(hipStreamSynchronize(L->copy));
     if (rc) {
         naiwa_cache_unreserve(L->cache, *slot_out);
@@ -474,11 +592,7 @@ int naiwa_cached_layer_seed(naiwa_cached_layer* L, const uint32_t* experts, int 
         if (experts[i] >= (uint32_t)L->d.num_experts) continue; // not in this model: skipped
         int slot = -1;
         if ((rc = naiwa_cache_admit(L->cache, (int)experts[i], &slot)) || slot < 0) continue;
-        void* dst[3];
-        const void* src[3];
-        L->slot_ptrs(slot, dst);
-        L->host_ptrs((int)experts[i], src);
-        rc = naiwa_upload_expert(dst, src, L->bytes, (int64_t)L->copy, 0, 0);
+        rc = L->upload((int)experts[i], slot, 0);
         slots.push_back(slot);
     }
     if (!rc) rc = naiwa_hip_rc(hipStreamSynchronize(L->copy));
@@ -512,9 +626,12 @@ int naiwa_cached_layer_prefetch(naiwa_cached_layer* next, const void* x, int row
     if (!next || !x || rows <= 0 || lookahead_swaps < 0) return NAIWA_E_INVALID;
     int rc = next->ensure_rows(rows);
     if (!rc) rc = next->predict_launch(x, rows, stream);
+    if (!rc)
+        rc = naiwa_hip_rc(hipMemcpyAsync(next->pred_ids_h, next->pred_ids_dev, (size_t)rows * next->d.top_k * 4,
+                                         hipMemcpyDeviceToHost, (hipStream_t)stream));
     if (!rc) rc = naiwa_hip_rc(hipStreamSynchronize((hipStream_t)stream));
     if (rc) return rc;
-    return next->prefetch_apply(lookahead_swaps, info);
+    return next->prefetch_apply(next->pred_ids_h, lookahead_swaps, info);
 }
 
 int naiwa_cached_layer_predicted(const naiwa_cached_layer* L, uint32_t* ids, int capacity, int* n_out) {

@@ -5,15 +5,18 @@
 // Three launches, all stream-ordered:
 //   1. segments: stable counting sort of the (token, slot) pairs by slot,
 //      weight-0 pairs (the reference's padding, gpu.rs:117-129) left out;
-//   2. gate+up: one block per (slot segment, 16-row tile of the intermediate);
-//      each 16-lane group owns one row of gate and the same row of up, streams
-//      their codes once with 16-byte loads and dots them against every token
-//      of the segment staged in LDS; h = act(g) * u in f32;
-//   3. down+combine: one block per 16-row tile of the output; walks the
-//      segments in ascending slot order, stages the segment's h vectors,
-//      streams each down row once per 4 tokens and accumulates w * (down . h)
-//      per (token, row) in LDS.  No atomics, so every run adds the same terms
-//      in the same order.
+//   2. gate+up: one block per (slot segment, tile of the intermediate); each
+//      16-lane group owns one row of gate and the same row of up, streams their
+//      codes with 16-byte loads and dots every code against up to 8 tokens of
+//      the segment staged in LDS; h = act(g) * u;
+//   3. down+combine: the output rows' (row, segment) items are spread over the
+//      groups of each block; a row is streamed once per 8 tokens of its
+//      segment and the weighted dots are added per (token, row) in ascending
+//      slot order.  No atomics, so every run adds the same terms in the same
+//      order.
+// Calls of at most 512 pairs keep h in global memory in the down format's dot
+// layout (written once by the gate/up blocks, read by the down items); larger
+// calls stage f32 h per block, 4 tokens per pass.
 #include "rowdot.h"
 #include "segments.h"
 #include "workspace.h"
@@ -177,6 +180,187 @@ down_kernel(BankArg down, int H, int I, int rows, int width, int tok_max, const 
         for (int t = 0; t < rows; ++t) out[(int64_t)t * H + r] = acc[t * kRowsPerBlock + grp];
 }
 
+// ---------------------------------------------------------------------------
+// Decode with h staged once in global memory (calls of at most kPairsMax pairs)
+// ---------------------------------------------------------------------------
+// gate_up_staged: one block per (slot segment, span of I rows), span = the down
+// format's sum span (16 rows for Q4_K down, 32 for Q8_0), one 16-lane group per
+// row; up to kTokG tokens of the segment are staged in LDS per pass and every
+// weight unit loaded is dotted with all of them.  The block then writes its
+// rows of each token's h straight in the down format's dot layout (16-bit pair
+// words + span sums, the same rounding and summation order as staging the f32
+// h would give) to hst[pair].
+// down_items: one block per kRowsD output rows; its (row, segment) items are
+// dealt over the block's 16-lane groups, each streaming the row once per
+// kTokD tokens of the segment and reading those tokens' h words from hst; the
+// weighted dots go to LDS by sorted pair position, and each (token, row) sums
+// its pairs in ascending position -- ascending slot -- order, as one pass over
+// all segments would.
+constexpr int kPairsMax = 512;
+constexpr int kTokG = 8;
+constexpr int kTokD = 8;
+constexpr int kRowsDMax = 8;
+constexpr int kDownThreads = 256;
+
+template <int DG, int DD>
+__global__ void __launch_bounds__(512)
+gate_up_staged_kernel(BankArg gate, BankArg up, const void* x, int x_bf16, int H, int I, int width, int tok_max,
+                      const int* seg_count, const uint32_t* seg_key, const uint32_t* seg_begin,
+                      const uint32_t* perm, int act, uint8_t* hst, int hst_stride) {
+    constexpr int SPAN = Fmt<DD>::kSumSpan;   // rows per block (one group of 16 lanes each)
+    constexpr int GPG = SPAN / 4;             // 4-row groups per sum
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ float hloc[kTokG][SPAN];
+    const int s = blockIdx.x;
+    if (s >= *seg_count) return;
+    const int tid = threadIdx.x, grp = tid / NAIWA_GROUP, lr = tid % NAIWA_GROUP;
+    const int r0 = blockIdx.y * SPAN, r = r0 + grp;
+    const uint32_t slot = seg_key[s];
+    const int b = (int)seg_begin[s], e = (int)seg_begin[s + 1];
+    const int stage = naiwa_stage_bytes(DG, H);
+    const uint8_t* grow = gate.base + (int64_t)slot * gate.stride + (int64_t)r * gate.row_bytes;
+    const uint8_t* urow = up.base + (int64_t)slot * up.stride + (int64_t)r * up.row_bytes;
+    const int nu = Fmt<DG>::units(H);
+    constexpr int UM = Umax<DG>::v;
+    for (int c0 = b; c0 < e; c0 += tok_max) {
+        const int nt = min(tok_max, e - c0);
+        __syncthreads();
+        for (int tt = 0; tt < nt; ++tt) {
+            const int t = (int)perm[c0 + tt] / width;
+            const void* src = x_bf16 ? (const void*)((const uint16_t*)x + (int64_t)t * H)
+                                     : (const void*)((const float*)x + (int64_t)t * H);
+            uint32_t* words = (uint32_t*)(smem + tt * stage);
+            naiwa_stage<DG>(src, x_bf16 != 0, H, words, (float*)(words + H / 2), tid, SPAN * NAIWA_GROUP);
+        }
+        __syncthreads();
+        float ag[kTokG], au[kTokG];
+#pragma unroll
+        for (int tt = 0; tt < kTokG; ++tt) ag[tt] = au[tt] = 0.0f;
+        if (r < I) {
+            for (int base = lr; base < nu; base += NAIWA_GROUP * UM) {
+                typename Fmt<DG>::Frag fg[UM], fu[UM];
+#pragma unroll
+                for (int i = 0; i < UM; ++i) {
+                    const int u = base + NAIWA_GROUP * i;
+                    if (u < nu) {
+                        fg[i] = Fmt<DG>::load(grow, u);
+                        fu[i] = Fmt<DG>::load(urow, u);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < UM; ++i) {
+                    const int u = base + NAIWA_GROUP * i;
+                    if (u >= nu) continue;
+#pragma unroll
+                    for (int tt = 0; tt < kTokG; ++tt) {
+                        if (tt >= nt) break;
+                        const uint32_t* words = (const uint32_t*)(smem + tt * stage);
+                        const float* sums = (const float*)(words + H / 2);
+                        ag[tt] += Fmt<DG>::dot(fg[i], u, words, sums);
+                        au[tt] += Fmt<DG>::dot(fu[i], u, words, sums);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < kTokG; ++tt) {
+            const float g = naiwa_group_sum<NAIWA_GROUP>(ag[tt]);
+            const float u = naiwa_group_sum<NAIWA_GROUP>(au[tt]);
+            if (tt < nt && lr == 0) hloc[tt][grp] = r < I ? naiwa_act(act, g) * u : 0.0f;
+        }
+        __syncthreads();
+        // the block's rows of each token's h in the down format's dot layout: thread
+        // (tt, g4) writes the pair words of rows r0 + 4 g4 .. + 3, and the span's sum
+        // (every lane of the first wave takes part in the group sums)
+        if (tid < 64) {
+            const bool in = tid < nt * GPG;
+            const int tt = in ? tid / GPG : 0, g4 = tid % GPG;
+            uint32_t h[4];
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                h[i] = Fmt<DD>::to16(hloc[tt][4 * g4 + i]);
+                v[i] = Fmt<DD>::from16(h[i]);
+            }
+            uint32_t* words = (uint32_t*)(hst + (size_t)perm[c0 + tt] * hst_stride);
+            const int g = r0 / 4 + g4;
+            if (in) {
+                words[2 * g] = h[0] | (h[2] << 16);
+                words[2 * g + 1] = h[1] | (h[3] << 16);
+            }
+            float part = (v[0] + v[1]) + (v[2] + v[3]);
+            part = naiwa_group_sum<GPG>(part);
+            if (in && g4 == 0) ((float*)(words + I / 2))[r0 / SPAN] = part;
+        }
+    }
+}
+
+template <int DD>
+__global__ void __launch_bounds__(kDownThreads)
+down_items_kernel(BankArg down, int H, int I, int rows, int width, int kRowsD, const int* seg_count,
+                  const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm, const float* w,
+                  const uint8_t* hst, int hst_stride, int accumulate, float* out) {
+    __shared__ float part[kPairsMax][kRowsDMax];
+    __shared__ uint32_t tok_of[kPairsMax];
+    const int tid = threadIdx.x, grp = tid / NAIWA_GROUP, lr = tid % NAIWA_GROUP;
+    const int r0 = blockIdx.x * kRowsD;
+    const int nseg = *seg_count;
+    const int npos = (int)seg_begin[nseg];
+    const int nu = Fmt<DD>::units(I);
+    constexpr int UM = Umax<DD>::v;
+    for (int i = tid; i < npos; i += kDownThreads) tok_of[i] = perm[i] / (uint32_t)width;
+    // items (segment, row): groups take them in turn
+    for (int it = grp; it < nseg * kRowsD; it += kDownThreads / NAIWA_GROUP) {
+        const int sgi = it / kRowsD, rr = it % kRowsD, r = r0 + rr;
+        if (r >= H) continue;
+        const uint32_t slot = seg_key[sgi];
+        const int b = (int)seg_begin[sgi], e = (int)seg_begin[sgi + 1];
+        const uint8_t* drow = down.base + (int64_t)slot * down.stride + (int64_t)r * down.row_bytes;
+        for (int c0 = b; c0 < e; c0 += kTokD) {
+            const int nt = min(kTokD, e - c0);
+            float a[kTokD];
+#pragma unroll
+            for (int tt = 0; tt < kTokD; ++tt) a[tt] = 0.0f;
+            for (int base = lr; base < nu; base += NAIWA_GROUP * UM) {
+                typename Fmt<DD>::Frag f[UM];
+#pragma unroll
+                for (int i = 0; i < UM; ++i) {
+                    const int u = base + NAIWA_GROUP * i;
+                    if (u < nu) f[i] = Fmt<DD>::load(drow, u);
+                }
+#pragma unroll
+                for (int i = 0; i < UM; ++i) {
+                    const int u = base + NAIWA_GROUP * i;
+                    if (u >= nu) continue;
+#pragma unroll
+                    for (int tt = 0; tt < kTokD; ++tt) {
+                        if (tt >= nt) break;
+                        const uint32_t* words = (const uint32_t*)(hst + (size_t)perm[c0 + tt] * hst_stride);
+                        a[tt] += Fmt<DD>::dot(f[i], u, words, (const float*)(words + I / 2));
+                    }
+                }
+            }
+#pragma unroll
+            for (int tt = 0; tt < kTokD; ++tt) {
+                const float v = naiwa_group_sum<NAIWA_GROUP>(a[tt]);
+                if (tt < nt && lr == 0) part[c0 + tt][rr] = w[perm[c0 + tt]] * v;
+            }
+        }
+    }
+    __syncthreads();
+    // (token, row): the sum starts at 0, or at out's value, and adds the token's pairs in
+    // ascending sorted position, i.e. ascending slot (the same additions as one call over
+    // both halves of a split by slot)
+    for (int i = tid; i < rows * kRowsD; i += kDownThreads) {
+        const int t = i / kRowsD, rr = i % kRowsD, r = r0 + rr;
+        if (r >= H) continue;
+        float acc = accumulate ? out[(int64_t)t * H + r] : 0.0f;
+        for (int pos = 0; pos < npos; ++pos)
+            if (tok_of[pos] == (uint32_t)t) acc += part[pos][rr];
+        out[(int64_t)t * H + r] = acc;
+    }
+}
+
 bool bank_ok(const naiwa_bank* b) {
     if (!b || !b->base || b->slots <= 0 || b->n <= 0 || b->k <= 0) return false;
     if (b->dtype != NAIWA_Q4_K && b->dtype != NAIWA_Q8_0) return false;
@@ -233,6 +417,54 @@ int check_args(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* d
     return NAIWA_OK;
 }
 
+// The staged-h path: gate/up writes h in the down format's dot layout (one vector
+// of naiwa_stage_bytes(DD, I) per pair, at most DecodeScratch's h bytes), then the
+// item-parallel down + ordered combine.
+template <int DG, int DD>
+int staged_kernels(BankArg g, BankArg u, BankArg d, const void* x, int xb, int H, int I, int rows, int width,
+                   int act, const float* w, float* out, int accumulate, int n, int slots, const int* seg_count,
+                   const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm, uint8_t* hst,
+                   hipStream_t st) {
+    constexpr int SPAN = Fmt<DD>::kSumSpan;
+    const int stage_g = naiwa_stage_bytes(DG, H);
+    const int tok = std::max(1, std::min(kTokG, (64 * 1024) / stage_g));
+    const int hst_stride = naiwa_stage_bytes(DD, I);
+    const dim3 ggrid(n, I / SPAN);
+    gate_up_staged_kernel<DG, DD><<<ggrid, SPAN * NAIWA_GROUP, (size_t)tok * stage_g, st>>>(
+        g, u, x, xb, H, I, width, tok, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride);
+    // rows per down block: about one (row, segment) item per group of the block
+    const int segs = std::max(1, std::min(n, slots));
+    int rd = 1;
+    while (rd < kRowsDMax && rd * 2 * segs <= kDownThreads / NAIWA_GROUP) rd *= 2;
+    down_items_kernel<DD><<<(H + rd - 1) / rd, kDownThreads, 0, st>>>(d, H, I, rows, width, rd, seg_count, seg_key,
+                                                                      seg_begin, perm, w, hst, hst_stride,
+                                                                      accumulate, out);
+    return naiwa_hip_rc(hipGetLastError());
+}
+
+int staged_launch(BankArg g, BankArg u, BankArg d, int gdt, int ddt, const void* x, int x_dtype, int H, int I,
+                  int rows, int width, int act, const float* w, float* out, int accumulate, int n, int slots,
+                  const int* seg_count, const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm,
+                  uint8_t* hst, hipStream_t st) {
+    const int xb = x_dtype == NAIWA_BF16;
+    const int fg = naiwa_kernel_fmt(gdt, H), fd = naiwa_kernel_fmt(ddt, I);
+#define NAIWA_STAGED(FG, FD)                                                                                       \
+    if (fg == FG && fd == FD)                                                                                      \
+        return staged_kernels<FG, FD>(g, u, d, x, xb, H, I, rows, width, act, w, out, accumulate, n, slots,         \
+                                      seg_count, seg_key, seg_begin, perm, hst, st);
+    NAIWA_STAGED(NAIWA_Q4_K, NAIWA_Q4_K)
+    NAIWA_STAGED(NAIWA_Q4_K, NAIWA_Q8_0)
+    NAIWA_STAGED(NAIWA_Q4_K, NAIWA_Q8_0_ODD)
+    NAIWA_STAGED(NAIWA_Q8_0, NAIWA_Q4_K)
+    NAIWA_STAGED(NAIWA_Q8_0, NAIWA_Q8_0)
+    NAIWA_STAGED(NAIWA_Q8_0, NAIWA_Q8_0_ODD)
+    NAIWA_STAGED(NAIWA_Q8_0_ODD, NAIWA_Q4_K)
+    NAIWA_STAGED(NAIWA_Q8_0_ODD, NAIWA_Q8_0)
+    NAIWA_STAGED(NAIWA_Q8_0_ODD, NAIWA_Q8_0_ODD)
+#undef NAIWA_STAGED
+    return NAIWA_E_UNSUPPORTED;
+}
+
 // The launches of one checked call over scratch ws (DecodeScratch(rows * width, I).total bytes).
 int decode_launch(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, const void* x, int x_dtype,
                   const uint32_t* slot_ids, const float* w, int rows, int width, int act, float* out, int flags,
@@ -262,6 +494,9 @@ int decode_launch(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank
     BankArg g{(const uint8_t*)gate->base, gate->slot_stride, naiwa_row_bytes(gate->dtype, H)};
     BankArg u{(const uint8_t*)up->base, up->slot_stride, naiwa_row_bytes(up->dtype, H)};
     BankArg d{(const uint8_t*)down->base, down->slot_stride, naiwa_row_bytes(down->dtype, I)};
+    if (n <= kPairsMax) return staged_launch(g, u, d, gate->dtype, down->dtype, x, x_dtype, H, I, rows, width, act,
+                                             w, out, accumulate, n, gate->slots, seg_count, seg_key, seg_begin, perm,
+                                             (uint8_t*)hbuf, st);
     const dim3 ggrid(n, (I + kRowsPerBlock - 1) / kRowsPerBlock);
     const size_t lds_g = (size_t)tok_g * naiwa_stage_bytes(gate->dtype, H);
     const int xb = x_dtype == NAIWA_BF16;

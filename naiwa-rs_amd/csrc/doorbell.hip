@@ -107,9 +107,74 @@ doorbell_wait_copy_f32_kernel(const uint32_t* d_seq, uint32_t target, const vola
     if (threadIdx.x == 0) store_release_sys(d_consumed, target);
 }
 
+// The persistent-wave doorbell: one wave answers `count` host rings in a row.
+// For ring i it waits (bounded) until *d_seq >= first + i, then release-stores
+// first + i to *d_ack.  A wait that runs past its limit counts a timeout and
+// ends the kernel, so the wave always exits.
+__global__ void __launch_bounds__(64)
+doorbell_poll_serve_kernel(const uint32_t* d_seq, uint32_t* d_ack, uint32_t first, uint32_t count,
+                           uint64_t limit_ticks) {
+    if (threadIdx.x != 0) return;
+    for (uint32_t i = 0; i < count; ++i) {
+        const uint32_t target = first + i;
+        const uint64_t t0 = wall_clock64();
+        while (load_acquire_sys(d_seq) < target) {
+            if (wall_clock64() - t0 > limit_ticks) {
+                atomicAdd(&g_doorbell_timeouts, 1u);
+                return;
+            }
+        }
+        store_release_sys(d_ack, target);
+    }
+}
+
+// A stream-ordered wait on a flag another stream (or the host) raises: one
+// wave spins (bounded) until *d_flag >= target; the kernels queued after it on
+// the stream start once it exits.
+__global__ void __launch_bounds__(64)
+doorbell_poll_wait_kernel(const uint32_t* d_flag, uint32_t target, uint64_t limit_ticks) {
+    if (threadIdx.x != 0) return;
+    const uint64_t t0 = wall_clock64();
+    while (load_acquire_sys(d_flag) < target) {
+        if (wall_clock64() - t0 > limit_ticks) {
+            atomicAdd(&g_doorbell_timeouts, 1u);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Raise *d_flag to value once the work queued before it on the stream is done.
+__global__ void __launch_bounds__(64) doorbell_poll_signal_kernel(uint32_t* d_flag, uint32_t value) {
+    if (threadIdx.x != 0) return;
+    __threadfence_system();
+    store_release_sys(d_flag, value);
+}
+
 } // namespace
 
 extern "C" {
+
+int doorbell_poll_serve(void* d_seq, void* d_ack, uint32_t first, uint32_t count, int64_t stream) {
+    if (!d_seq || !d_ack) return NAIWA_E_INVALID;
+    if (count == 0) return NAIWA_OK;
+    doorbell_poll_serve_kernel<<<1, 64, 0, (hipStream_t)stream>>>((const uint32_t*)d_seq, (uint32_t*)d_ack,
+                                                                   first, count, wait_limit_ticks());
+    return naiwa_hip_rc(hipGetLastError());
+}
+
+int doorbell_poll_wait(const void* d_flag, uint32_t target, int64_t stream) {
+    if (!d_flag) return NAIWA_E_INVALID;
+    doorbell_poll_wait_kernel<<<1, 64, 0, (hipStream_t)stream>>>((const uint32_t*)d_flag, target,
+                                                                  wait_limit_ticks());
+    return naiwa_hip_rc(hipGetLastError());
+}
+
+int doorbell_poll_signal(void* d_flag, uint32_t value, int64_t stream) {
+    if (!d_flag) return NAIWA_E_INVALID;
+    doorbell_poll_signal_kernel<<<1, 64, 0, (hipStream_t)stream>>>((uint32_t*)d_flag, value);
+    return naiwa_hip_rc(hipGetLastError());
+}
 
 int doorbell_alloc_mapped(void** out, size_t bytes) {
     if (!out) return NAIWA_E_INVALID;

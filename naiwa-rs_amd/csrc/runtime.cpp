@@ -139,6 +139,14 @@ int naiwa_memcpy_2d_d2d(void* dst, size_t dpitch, const void* src, size_t spitch
         hipMemcpy2DAsync(dst, dpitch, src, spitch, width, height, hipMemcpyDeviceToDevice, (hipStream_t)stream));
 }
 
+int naiwa_memcpy_2d(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width, size_t height,
+                    int64_t stream) {
+    if (!height || !width) return NAIWA_OK;
+    if (!dst || !src || width > dpitch || width > spitch) return NAIWA_E_INVALID;
+    return naiwa_hip_rc(
+        hipMemcpy2DAsync(dst, dpitch, src, spitch, width, height, hipMemcpyDefault, (hipStream_t)stream));
+}
+
 int naiwa_upload_expert(void* const dst[3], const void* const src[3], const size_t bytes[3],
                         int64_t copy_stream, int64_t read_fence, int64_t done_event) {
     if (!dst || !src || !bytes) return NAIWA_E_INVALID;

@@ -1372,6 +1372,18 @@ __global__ void zero_u32(unsigned int* ptr, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) ptr[i] = 0u;
 }
 
+// Before a launch: fold the previous launch's counters (words 0, 1) into the running
+// totals (words 2, 3) and clear them; a launch's own wait timeout makes its later waits
+// give up, so the per-launch word starts at zero.
+__global__ void roll_status(int* st) {
+    if (threadIdx.x == 0) {
+        st[2] += st[0];
+        st[3] += st[1];
+        st[0] = 0;
+        st[1] = 0;
+    }
+}
+
 struct FusedCache {
     std::mutex mu;
     LayerDev* dev_layers = nullptr;
@@ -1389,17 +1401,10 @@ int launch(const Params& prm, int blocks, size_t lds, hipStream_t st) {
     if (e != hipSuccess) return (int)e;
     // The grid never exceeds the blocks every CU can hold at once (checked
     // against the occupancy above), so a plain launch is resident when the
-    // device is not shared; the bounded waits keep it safe when it is.
-    // NAIWA_STACK_LAUNCH=cooperative makes the runtime check residency too (a
-    // cooperative launch costs about 20 us more per step here).
-    static const bool normal = [] {
-        const char* v = getenv("NAIWA_STACK_LAUNCH");
-        return !(v && strcmp(v, "cooperative") == 0);
-    }();
-    if (normal)
-        e = hipLaunchKernel((const void*)fn, dim3(blocks), dim3(kThreads), args, (unsigned)lds, st);
-    else
-        e = hipLaunchCooperativeKernel((const void*)fn, dim3(blocks), dim3(kThreads), args, (unsigned)lds, st);
+    // device is not shared; the bounded waits keep it safe when it is, and the
+    // status counters report it.  (A cooperative launch, where the runtime
+    // checks residency, measured about 20 us slower per step and is not used.)
+    e = hipLaunchKernel((const void*)fn, dim3(blocks), dim3(kThreads), args, (unsigned)lds, st);
     return naiwa_hip_rc(e);
 }
 
@@ -1481,18 +1486,22 @@ size_t g_tag_clean[kMaxDev];
 std::mutex g_seq_mu;
 }
 
-// Status of the last fused launches: waits that gave up after their 2 s
-// bound, and routed experts that had no resident slot.  Synchronizes.
+// Status of every fused launch since the last read: waits that gave up after their
+// 2 s bound, and routed experts that had no resident slot.  Reading resets the
+// counters.  Synchronizes.
 extern "C" int naiwa_stack_status(int* barrier_timeouts, int* missing_experts) {
     int rc = 0;
-    uint8_t* sync = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK + 1, 4096, &rc);
+    bool fresh = false;
+    uint8_t* sync = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK + 1, 4096, &rc, &fresh);
     if (!sync) return rc;
-    int h[2] = {0, 0};
-    hipError_t e = hipMemcpy(h, sync + kStatusOff, sizeof(h), hipMemcpyDeviceToHost);
+    hipError_t e = hipDeviceSynchronize();
     if (e != hipSuccess) return (int)e;
-    if (barrier_timeouts) *barrier_timeouts = h[0];
-    if (missing_experts) *missing_experts = h[1];
-    return NAIWA_OK;
+    int h[4] = {0, 0, 0, 0};
+    if (!fresh && (e = hipMemcpy(h, sync + kStatusOff, sizeof(h), hipMemcpyDeviceToHost)) != hipSuccess) return (int)e;
+    if (barrier_timeouts) *barrier_timeouts = h[0] + h[2];
+    if (missing_experts) *missing_experts = h[1] + h[3];
+    const int zero[4] = {0, 0, 0, 0};
+    return naiwa_hip_rc(hipMemcpy(sync + kStatusOff, zero, sizeof(zero), hipMemcpyHostToDevice));
 }
 
 int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows, int H, int E, int k,
@@ -1593,7 +1602,8 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     bool fresh = false;
     uint8_t* ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK, tag_bytes, &rc, &fresh);
     if (!ws) return rc;
-    uint8_t* sync = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK + 1, 256, &rc);
+    bool sync_fresh = false;
+    uint8_t* sync = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK + 1, 4096, &rc, &sync_fresh);
     if (!sync) return rc;
     uint32_t seq = 0;
     {
@@ -1675,7 +1685,8 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     if (g_trace_enabled && !prm.trace) return rc;
     g_trace_layers = n_layers;
     g_trace_blocks = blocks;
-    zero_u32<<<1, 64, 0, st>>>((unsigned int*)(sync + kStatusOff), 64);
+    if (sync_fresh) zero_u32<<<1, 64, 0, st>>>((unsigned int*)(sync + kStatusOff), 64);
+    roll_status<<<1, 64, 0, st>>>((int*)(sync + kStatusOff));
     const LaunchOp go{&prm, blocks, lds, st};
     return rows == 1 ? with_kernel<1>(fg, fd, go) : with_kernel<kMaxRows>(fg, fd, go);
 }

@@ -51,7 +51,7 @@ class CachedLayerDesc(C.Structure):
     _fields_ = [("router", C.c_void_p), ("router_bias", C.c_void_p), ("gate", Bank), ("up", Bank),
                 ("down", Bank), ("host_gate", C.c_void_p), ("host_up", C.c_void_p), ("host_down", C.c_void_p),
                 ("num_experts", C.c_int), ("top_k", C.c_int), ("hidden", C.c_int), ("inter", C.c_int),
-                ("usable", C.c_int), ("mode", C.c_int), ("act", C.c_int)]
+                ("usable", C.c_int), ("mode", C.c_int), ("act", C.c_int), ("host_expert_stride", C.c_int64)]
 
 
 class Copy(C.Structure):
@@ -134,6 +134,9 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_event_elapsed_ms": (i32, [_P(f32), i64, i64]),
     "naiwa_device_sync": (i32, []),
     "naiwa_last_error": (i32, []),
+    "doorbell_poll_serve": (i32, [vp, vp, C.c_uint32, C.c_uint32, i64]),
+    "doorbell_poll_wait": (i32, [vp, C.c_uint32, i64]),
+    "doorbell_poll_signal": (i32, [vp, C.c_uint32, i64]),
     "doorbell_alloc_mapped": (i32, [_P(vp), C.c_size_t]),
     "doorbell_free_host": (i32, [vp]),
     "doorbell_get_device_ptr": (None, [vp, _P(vp)]),
@@ -164,6 +167,7 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_upload_expert": (i32, [vp, vp, vp, i64, i64, i64]),
     "naiwa_copy_batch": (i32, [_P(Copy), i32, i64]),
     "naiwa_memcpy_2d_d2d": (i32, [vp, C.c_size_t, vp, C.c_size_t, C.c_size_t, C.c_size_t, i64]),
+    "naiwa_memcpy_2d": (i32, [vp, C.c_size_t, vp, C.c_size_t, C.c_size_t, C.c_size_t, i64]),
     # include/naiwa_doorbell.h
     "naiwa_topk_doorbell_create": (i32, [i32, _P(vp)]),
     "naiwa_topk_doorbell_destroy": (i32, [vp]),

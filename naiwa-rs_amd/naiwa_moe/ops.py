@@ -45,10 +45,11 @@ class SlotBank:
     """One projection's slot bank on the device."""
 
     def __init__(self, slots: int, n: int, k: int, dtype: int, buffer: DeviceBuffer | None = None,
-                 offset: int = 0):
+                 offset: int = 0, stride: int | None = None):
         self.slots, self.n, self.k, self.dtype = slots, n, k, dtype
-        self.stride = slot_stride(dtype, n, k)
+        self.stride = slot_stride(dtype, n, k) if stride is None else stride
         self.expert_bytes = n * row_bytes(dtype, k)
+        assert self.stride >= self.expert_bytes
         if buffer is None:
             buffer = DeviceBuffer(self.stride * slots)
             offset = 0
@@ -71,13 +72,25 @@ class SlotBank:
 
 
 class LayerBanks:
-    """gate/up/down banks of one layer: gate/up [I, H], down [H, I]."""
+    """gate/up/down banks of one layer: gate/up [I, H], down [H, I].  contiguous: one
+    allocation whose slot s holds the expert's gate | up | down adjacently (every bank's
+    slot stride is the expert's bytes rounded to 256), so an expert moves as one range."""
 
-    def __init__(self, slots: int, hidden: int, inter: int, dtypes: tuple[int, int, int]):
+    def __init__(self, slots: int, hidden: int, inter: int, dtypes: tuple[int, int, int],
+                 contiguous: bool = False):
         self.hidden, self.inter, self.slots = hidden, inter, slots
-        self.gate = SlotBank(slots, inter, hidden, dtypes[0])
-        self.up = SlotBank(slots, inter, hidden, dtypes[1])
-        self.down = SlotBank(slots, hidden, inter, dtypes[2])
+        if not contiguous:
+            self.gate = SlotBank(slots, inter, hidden, dtypes[0])
+            self.up = SlotBank(slots, inter, hidden, dtypes[1])
+            self.down = SlotBank(slots, hidden, inter, dtypes[2])
+            return
+        pb = [inter * row_bytes(dtypes[0], hidden), inter * row_bytes(dtypes[1], hidden),
+              hidden * row_bytes(dtypes[2], inter)]
+        stride = (sum(pb) + 255) // 256 * 256
+        buf = DeviceBuffer(stride * slots)
+        self.gate = SlotBank(slots, inter, hidden, dtypes[0], buf, 0, stride)
+        self.up = SlotBank(slots, inter, hidden, dtypes[1], buf, pb[0], stride)
+        self.down = SlotBank(slots, hidden, inter, dtypes[2], buf, pb[0] + pb[1], stride)
 
     def load(self, slot: int, gate: np.ndarray, up: np.ndarray, down: np.ndarray) -> None:
         self.gate.write_slot(slot, gate)
@@ -95,20 +108,38 @@ class HostExpertStacks:
     here they live in pinned allocations, since registering existing memory is not
     available).  Expert e of a projection is at expert_range(e)."""
 
-    def __init__(self, experts: int, hidden: int, inter: int, dtypes: tuple[int, int, int]):
+    def __init__(self, experts: int, hidden: int, inter: int, dtypes: tuple[int, int, int],
+                 interleaved: bool = False):
+        """interleaved: one pinned allocation holding expert e's gate | up | down adjacently
+        at e * stride (stride = the expert's bytes), so an expert uploads as one range."""
         self.experts = experts
         shapes = ((inter, hidden, dtypes[0]), (inter, hidden, dtypes[1]), (hidden, inter, dtypes[2]))
         self.expert_bytes = [n * row_bytes(dt, k) for n, k, dt in shapes]
-        self.buffers = [PinnedBuffer(experts * b) for b in self.expert_bytes]
+        if interleaved:
+            self.stride = sum(self.expert_bytes)
+            self.buffers = [PinnedBuffer(experts * self.stride)]
+            offs = [0, self.expert_bytes[0], self.expert_bytes[0] + self.expert_bytes[1]]
+            self.ptrs = [self.buffers[0].ptr + o for o in offs]
+            self._offs = offs
+        else:
+            self.stride = 0
+            self.buffers = [PinnedBuffer(experts * b) for b in self.expert_bytes]
+            self.ptrs = [b.ptr for b in self.buffers]
 
     def view(self, proj: int) -> np.ndarray:
-        """[E, expert_bytes] uint8 view of projection proj (0 gate, 1 up, 2 down)."""
-        return self.buffers[proj].view().reshape(self.experts, self.expert_bytes[proj])
+        """[E, expert_bytes] uint8 view of projection proj (0 gate, 1 up, 2 down); strided
+        when the stacks are interleaved."""
+        if not self.stride:
+            return self.buffers[proj].view().reshape(self.experts, self.expert_bytes[proj])
+        whole = self.buffers[0].view().reshape(self.experts, self.stride)
+        o = self._offs[proj]
+        return whole[:, o:o + self.expert_bytes[proj]]
 
     def expert_ptrs(self, e: int) -> list[int]:
         if not 0 <= e < self.experts:
             raise IndexError(f"expert {e} outside [0, {self.experts})")
-        return [buf.ptr + e * b for buf, b in zip(self.buffers, self.expert_bytes)]
+        step = [self.stride or b for b in self.expert_bytes]
+        return [p + e * s for p, s in zip(self.ptrs, step)]
 
 
 def upload_expert(banks: "LayerBanks", slot: int, stacks: HostExpertStacks, expert: int, copy_stream: int,

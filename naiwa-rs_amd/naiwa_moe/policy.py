@@ -161,6 +161,12 @@ class StagingRing:
         return [(int(chosen[i]), int(pos[i])) for i in range(n.value)]
 
 
+def _host_ptrs(stacks) -> list[int]:
+    """The host pointers of expert 0's gate, up and down projections."""
+    ptrs = getattr(stacks, "ptrs", None)
+    return list(ptrs) if ptrs is not None else [b.ptr for b in stacks.buffers]
+
+
 class CachedLayer:
     """One layer's decode step over a partial cache (include/naiwa_cached.h): the reference's
     CachedExperts::forward for decode rows, with PCIe staging and promotion."""
@@ -170,8 +176,8 @@ class CachedLayer:
         from .ops import _dev
         d = CachedLayerDesc(_dev(router), _dev(router_bias) if router_bias is not None else None,
                             banks.gate.desc(), banks.up.desc(), banks.down.desc(),
-                            *[b.ptr for b in stacks.buffers], num_experts, top_k, banks.hidden, banks.inter, usable,
-                            mode, act)
+                            *_host_ptrs(stacks), num_experts, top_k, banks.hidden, banks.inter, usable,
+                            mode, act, getattr(stacks, "stride", 0))
         h = C.c_void_p()
         check(lib().naiwa_cached_layer_create(C.byref(d), ring._h, ring.length, copy_stream, C.byref(h)),
               "cached_layer_create")

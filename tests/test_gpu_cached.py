@@ -94,7 +94,7 @@ def check_resident_bytes(layer, banks, stacks):
     for e in np.nonzero(table >= 0)[0]:
         s = int(table[e])
         for proj, bank in enumerate((banks.gate, banks.up, banks.down)):
-            got = bank.buffer.download(np.uint8, count=bank.expert_bytes, offset=s * bank.stride)
+            got = bank.buffer.download(np.uint8, count=bank.expert_bytes, offset=bank.offset + s * bank.stride)
             assert np.array_equal(got, stacks.view(proj)[e]), (e, s, proj)
 
 
@@ -119,7 +119,7 @@ def test_staged_bytes_land_in_their_ring_slot(gpu):
     order = nm.policy.streamed_misses([[(int(i), float(v)) for i, v in zip(ids[0], want_w[0])]], 1.0, 16)
     for pos, e in enumerate(order):
         for proj, bank in enumerate((banks.gate, banks.up, banks.down)):
-            got = bank.buffer.download(np.uint8, count=bank.expert_bytes, offset=(usable + pos) * bank.stride)
+            got = bank.buffer.download(np.uint8, count=bank.expert_bytes, offset=bank.offset + (usable + pos) * bank.stride)
             assert np.array_equal(got, stacks.view(proj)[e])
 
 
@@ -237,7 +237,7 @@ def test_lookahead_loads_the_next_layers_prediction(gpu, fused, rows):
     for e in np.nonzero(table >= 0)[0]:
         s = int(table[e])
         for proj, bank in enumerate((banks1.gate, banks1.up, banks1.down)):
-            got = bank.buffer.download(np.uint8, count=bank.expert_bytes, offset=s * bank.stride)
+            got = bank.buffer.download(np.uint8, count=bank.expert_bytes, offset=bank.offset + s * bank.stride)
             assert np.array_equal(got, stacks1.view(proj)[e]), (e, s, proj)
 
 
@@ -264,7 +264,7 @@ def test_profile_seeds_the_cache(gpu, tmp_path):
     assert {e: int(table[e]) for e in np.nonzero(table >= 0)[0]} == {3: 0, 5: 1, 9: 2, 1: 3, 14: 4}
     for e, s in ((5, 1), (9, 2), (1, 3), (14, 4)):
         for proj, bank in enumerate((banks.gate, banks.up, banks.down)):
-            got = bank.buffer.download(np.uint8, count=bank.expert_bytes, offset=s * bank.stride)
+            got = bank.buffer.download(np.uint8, count=bank.expert_bytes, offset=bank.offset + s * bank.stride)
             assert np.array_equal(got, stacks.view(proj)[e]), (e, s, proj)
     out = nm.DeviceBuffer(rows * H * 4)
     x = S.activations_bf16(1701, rows, H)
@@ -296,7 +296,7 @@ class PageableStacks:
         return self.arrays[proj]
 
 
-@pytest.mark.parametrize("host_mem", ["pinned", "pageable"])
+@pytest.mark.parametrize("host_mem", ["pinned", "pageable", "contiguous"])
 def test_cached_layer_alternating_streams(gpu, host_mem):
     """Steps alternate between two compute streams with no host synchronisation of
     their own: a staged upload into a ring slot must wait for every earlier read of
@@ -311,10 +311,13 @@ def test_cached_layer_alternating_streams(gpu, host_mem):
     ring = nm.policy.StagingRing()
     dt = (O.Q4_K,) * 3
     g, u, d, r = S.layer(1800, E, H, I, dt)
-    stacks = nm.HostExpertStacks(E, H, I, dt) if host_mem == "pinned" else PageableStacks(E, H, I, dt)
+    if host_mem == "pageable":
+        stacks = PageableStacks(E, H, I, dt)
+    else:
+        stacks = nm.HostExpertStacks(E, H, I, dt, interleaved=host_mem == "contiguous")
     for p_, src in enumerate((g, u, d)):
         stacks.view(p_)[:] = src.reshape(E, -1)
-    banks = nm.LayerBanks(usable + ring.length, H, I, dt)
+    banks = nm.LayerBanks(usable + ring.length, H, I, dt, contiguous=host_mem == "contiguous")
     router = nm.DeviceBuffer.from_array(r)
     bias = zipf_bias(E, 1.1, 1800)
     bias_d = nm.DeviceBuffer.from_array(bias)
@@ -397,16 +400,18 @@ def test_cached_qwen3_shape_zipf(gpu):
     tmp = nm.DeviceBuffer(E * max(proj))
     layers, models, hosts, keep = [], [], [], []
     for l in range(L):
-        stacks = nm.HostExpertStacks(E, H, I, dt)
+        # the benchmark's layout: each expert's projections adjacent on the host and in its slot
+        stacks = nm.HostExpertStacks(E, H, I, dt, interleaved=True)
         for t in range(3):
             n, kk = (I, H) if t < 2 else (H, I)
             nm.synth(dt[t], 2000 + 8 * l + t, E * n * kk, tmp, 0.0, 0.02, stream=stream.handle)
-            nm.lib().naiwa_memcpy_d2h(stacks.buffers[t].ptr, tmp.ptr, E * proj[t], stream.handle)
+            assert nm.lib().naiwa_memcpy_2d(stacks.ptrs[t], stacks.stride, tmp.ptr, proj[t], proj[t], E,
+                                            stream.handle) == 0
             stream.sync()
         r = O.normal(S.stream(2000 + l, S.T_ROUTER), E * H, 0.0, 0.02).reshape(E, H)
         bias = zipf_bias(E, 1.1, 2100 + l)
         router, bias_d = nm.DeviceBuffer.from_array(r), nm.DeviceBuffer.from_array(bias)
-        banks = nm.LayerBanks(usable + ring.length, H, I, dt)
+        banks = nm.LayerBanks(usable + ring.length, H, I, dt, contiguous=True)
         layer = nm.policy.CachedLayer(router, banks, stacks, E, k, usable, ring, copy.handle,
                                       mode=O.ROUTE_SOFTMAX_TOPK_RENORM, router_bias=bias_d)
         # the 32 most popular experts (largest bias) first
@@ -415,7 +420,8 @@ def test_cached_qwen3_shape_zipf(gpu):
         model = PromotingSlotModel(usable, E)
         for e in popular:
             model.admit(e)
-        g, u, d = (stacks.view(t).reshape(E, *((I, -1) if t < 2 else (H, -1))) for t in range(3))
+        g, u, d = (np.ascontiguousarray(stacks.view(t)).reshape(E, *((I, -1) if t < 2 else (H, -1)))
+                   for t in range(3))
         hosts.append((g, u, d, r, bias, dt, I))
         layers.append((layer, banks, stacks))
         models.append(model)
