@@ -50,6 +50,19 @@ constexpr int kTNG = 128;      // gate/up features per block (waves 0-3 gate, 4-
 constexpr int kTND = 256;      // down output features per block
 constexpr int NAIWA_SCRATCH_PREFILL = 5;
 
+// f16 operands hold |v| <= 65504: activations (x, h) past that are clamped, and every
+// clamped value is counted here (naiwa_moe_prefill_status reads and resets the count).
+__device__ unsigned long long g_prefill_clamped = 0;
+
+// v clamped to the f16 range; counts (once per wave, by lane count) the values it changed.
+__device__ __forceinline__ float clamp_f16_counted(float v) {
+    const bool big = !(fabsf(v) <= 65504.0f);
+    const unsigned long long m = __ballot(big);
+    if (m && (threadIdx.x & 63) == (unsigned)__ffsll((long long)m) - 1)
+        atomicAdd(&g_prefill_clamped, (unsigned long long)__popcll(m));
+    return fminf(fmaxf(v, -65504.0f), 65504.0f);
+}
+
 template <int DT> struct KBlock;
 template <> struct KBlock<NAIWA_Q4_K> {
     static constexpr int kVals = 256, kSteps = 16;
@@ -127,21 +140,24 @@ __device__ __forceinline__ uint32_t f16x2_bits(float a, float b) {
 
 // x bf16 [T, H] -> xp f16 [T, H] in the K order of DT.  One thread per run of
 // 8 values.  bf16 values are exact in f16 inside its range; larger magnitudes
-// are clamped to +-65504 (the expert inputs are normalised activations).
+// are clamped to +-65504 and counted (the expert inputs are normalised
+// activations, so a nonzero count flags a call whose results are not exact).
 template <int DT>
 __global__ void __launch_bounds__(kThreads) prep_kernel(const uint16_t* x, int T, int H, uint16_t* xp) {
     const int runs = H / 8;
     const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (i >= (int64_t)T * runs) return;
-    const int t = (int)(i / runs), run = (int)(i % runs);
-    const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)t * H + 8 * run);
+    const bool in = i < (int64_t)T * runs;
+    const int t = in ? (int)(i / runs) : 0, run = in ? (int)(i % runs) : 0;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (in) v = *reinterpret_cast<const uint4*>(x + (size_t)t * H + 8 * run);
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
     float f[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        f[2 * j] = fminf(fmaxf(__uint_as_float(w[j] << 16), -65504.0f), 65504.0f);
-        f[2 * j + 1] = fminf(fmaxf(__uint_as_float(w[j] & 0xffff0000u), -65504.0f), 65504.0f);
+        f[2 * j] = clamp_f16_counted(__uint_as_float(w[j] << 16));
+        f[2 * j + 1] = clamp_f16_counted(__uint_as_float(w[j] & 0xffff0000u));
     }
+    if (!in) return;
     float g[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) g[e] = f[DT == NAIWA_Q4_K ? q4_elem(e) : e];
@@ -362,11 +378,9 @@ gateup_kernel(Bank gate, Bank up, const uint16_t* xp, int H, int I, int k, const
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int m = 32 * ms + 8 * (v / 4) + 4 * h + v % 4;
-                if (m < cnt) {
-                    const float g = xch[xbase + (16 * ms + v) * 64];
-                    const _Float16 hv = (_Float16)fminf(fmaxf(g * acc[ms][v], -65504.0f), 65504.0f);
-                    hp[(size_t)(start + m) * I + col] = __builtin_bit_cast(uint16_t, hv);
-                }
+                const float g = xch[xbase + (16 * ms + v) * 64];
+                const _Float16 hv = (_Float16)clamp_f16_counted(m < cnt ? g * acc[ms][v] : 0.0f);
+                if (m < cnt) hp[(size_t)(start + m) * I + col] = __builtin_bit_cast(uint16_t, hv);
             }
     }
 }
@@ -474,6 +488,18 @@ void launch_gateup(dim3 g, hipStream_t st, Bank bg, Bank bu, const uint16_t* xp,
 }
 
 } // namespace
+
+extern "C" int naiwa_moe_prefill_status(uint64_t* clamped) {
+    if (!clamped) return NAIWA_E_INVALID;
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return (int)e;
+    unsigned long long v = 0;
+    if ((e = hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_prefill_clamped), sizeof(v), 0, hipMemcpyDeviceToHost)) != hipSuccess)
+        return (int)e;
+    *clamped = v;
+    v = 0;
+    return naiwa_hip_rc(hipMemcpyToSymbol(HIP_SYMBOL(g_prefill_clamped), &v, sizeof(v), 0, hipMemcpyHostToDevice));
+}
 
 extern "C" int naiwa_moe_prefill(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, const void* x,
                                  const uint32_t* slot_ids, const float* w, int T, int k, int act, float* out,

@@ -241,8 +241,9 @@ __device__ __forceinline__ int chunk_at(int p, int nchunks) {
 __device__ __forceinline__ int item_thread() { return (threadIdx.x + kThreads / 2) % kThreads; }
 
 // Publish this workgroup's router partials for layer tag `tag`: item it of
-// chunk owner b at part[(it * nprod + b) * 2 ...], so that a leader reads the
-// owners of one item from consecutive words.
+// chunk owner b at part[(b * items + it) * 2 ...], so that an owner writes
+// whole cache lines (its items are contiguous) and a leader reads, per owner,
+// one contiguous run of its own items.
 template <int PPT>
 __device__ inline void store_partials(const Params& p, const long long* acc, int nprod, uint32_t tag) {
     const int items = p.rows * p.E;
@@ -250,33 +251,52 @@ __device__ inline void store_partials(const Params& p, const long long* acc, int
     for (int j = 0; j < PPT; ++j) {
         const int it = item_thread() + j * kThreads;
         if (it < items) {
-            u64* dst = p.part + ((size_t)it * nprod + blockIdx.x) * 2;
+            u64* dst = p.part + ((size_t)blockIdx.x * items + it) * 2;
             st64(dst, tagged(tag, (uint32_t)(unsigned long long)acc[j]));
             st64(dst + 1, tagged(tag, (uint32_t)((unsigned long long)acc[j] >> 32)));
         }
     }
 }
 
-// Leader bid adds, for its experts, the partials of every chunk owner and
-// publishes the logits (tagged f32).  LPI lanes per (token, expert) item.
-template <int LPI>
-__device__ inline void leader_pass(const Params& p, int i0, int items, int e0, int ne, int nprod, uint32_t tag) {
-    const int tid = threadIdx.x;
-    const int it = i0 + tid / LPI, li = tid % LPI;
-    const bool in = it < items;
-    const int t = in ? it / ne : 0, e = in ? e0 + it % ne : 0;
-    const size_t idx = (size_t)t * p.E + e;
+// Leader bid adds, for its experts (its items: every token's logit of each),
+// the partials of every chunk owner and publishes the logits (tagged f32).
+// Thread t takes item t % n and the owners t / n, t / n + kThreads / n, ...:
+// consecutive threads read consecutive words of one owner's run.  The int64
+// sums are added across threads with LDS atomics (exact, so in any order).
+constexpr int kLeadItemsMax = kMaxRows * kMaxE / kLeaders;
+__device__ inline void leader_reduce(const Params& p, int nprod, uint32_t tag) {
+    __shared__ long long lacc[kLeadItemsMax];
+    const int nlead = min(kLeaders, (int)gridDim.x);
+    const int epl = (p.E + nlead - 1) / nlead;
+    const int e0 = blockIdx.x * epl;
+    const int ne = max(0, min(epl, p.E - e0));
+    const int n = p.rows * ne;
+    if (n <= 0) return;
+    const int tid = threadIdx.x, items = p.rows * p.E;
+    // barriers that wait for LDS only: the upper waves' partial stores may still be
+    // in flight, and waiting for them would delay the loads below
+    auto lds_barrier = [] {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+    if (tid < n) lacc[tid] = 0;
+    lds_barrier();
+    const int per = kThreads / n;            // threads per item
+    const bool act = tid < per * n;
+    const int li = act ? tid % n : 0, ob = act ? tid / n : 0;
+    const size_t idx = (size_t)(li / ne) * p.E + e0 + li % ne;
     long long s = 0;
 #pragma unroll 1
-    for (int b0 = li; b0 < nprod; b0 += 8 * LPI) {
+    for (int b0 = ob; b0 < nprod; b0 += 8 * per) {
         u64 w[16];
         auto addr = [&](int j) -> const u64* {
-            const int b = b0 + (j >> 1) * LPI;
-            return (in && b < nprod) ? p.part + (idx * nprod + b) * 2 + (j & 1) : nullptr;
+            const int b = b0 + (j >> 1) * per;
+            return (act && b < nprod) ? p.part + ((size_t)b * items + idx) * 2 + (j & 1) : nullptr;
         };
         issue_tagged(w, addr, tag);
         const unsigned polls = wait_tagged(w, addr, tag, p);
-        if (p.trace && threadIdx.x == 0 && b0 == 0) {
+        if (p.trace && threadIdx.x == 0 && b0 == ob) {
             mark(p, p.trace_layer, 19);
             trace_put(p, p.trace_layer, 20, polls);
         }
@@ -284,23 +304,11 @@ __device__ inline void leader_pass(const Params& p, int i0, int items, int e0, i
         for (int j = 0; j < 8; ++j)
             s += (long long)(((u64)(uint32_t)w[2 * j + 1] << 32) | (uint32_t)w[2 * j]);
     }
-    s = group_sum_i64<LPI>(s);
-    if (in && li == 0) st64(&p.logits[idx], tagged(tag, __float_as_uint(naiwa_router_fix_to_f32(s))));
-}
-
-__device__ inline void leader_reduce(const Params& p, int nprod, uint32_t tag) {
-    const int nlead = min(kLeaders, (int)gridDim.x);
-    const int epl = (p.E + nlead - 1) / nlead;
-    const int e0 = blockIdx.x * epl;
-    const int ne = max(0, min(epl, p.E - e0));
-    const int items = p.rows * ne;
-    if (items <= 4) {
-        if (items > 0) leader_pass<64>(p, 0, items, e0, ne, nprod, tag);
-    } else if (items <= 8) {
-        leader_pass<32>(p, 0, items, e0, ne, nprod, tag);
-    } else {
-#pragma unroll 1
-        for (int i0 = 0; i0 < items; i0 += 16) leader_pass<16>(p, i0, items, e0, ne, nprod, tag);
+    if (act) atomicAdd((unsigned long long*)&lacc[li], (unsigned long long)s);
+    lds_barrier();
+    if (tid < n) {
+        const size_t gi = (size_t)(tid / ne) * p.E + e0 + tid % ne;
+        st64(&p.logits[gi], tagged(tag, __float_as_uint(naiwa_router_fix_to_f32(lacc[tid]))));
     }
 }
 
@@ -914,7 +922,7 @@ stack_kernel(Params p) {
                 if (wave == 0) weigh_one_row(p, sm, l, lane, r_e, r_f);
         };
         if constexpr (MR == 1) {
-            // wave 0 routes the token while waves 1-3 poll and stage its activations
+            // wave 0 routes the token while waves 1-7 poll and stage its activations
             if (wave == 0) {
                 poll_one_row(p, sm, L, l, tag, lane);
             } else {
