@@ -51,6 +51,24 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def activation_health(buf, n: int) -> dict:
+    """Largest |value| and count of non-finite values of n bf16 activations on the device
+    (a chained residual stream whose values overflow routes on NaN and measures nothing)."""
+    v = (buf.download(np.uint16)[:n].astype(np.uint32) << 16).view(np.float32)
+    finite = np.isfinite(v)
+    return {"absmax": float(np.abs(v[finite]).max()) if finite.any() else None,
+            "nonfinite": int((~finite).sum())}
+
+
+# Std of the synthetic down projections of the chained prefill and Mixtral stacks.
+# With N(0, 0.02) down weights one layer's output is as large as its unit-scale input
+# and grows with its square, so the residual chain overflows within a few layers; at
+# these values a layer adds about a tenth of the input's scale and the chain stays
+# finite (checked by activation_health on every run).
+DOWN_STD_DEEPSEEK = 0.004
+DOWN_STD_MIXTRAL = 0.0015
+
+
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -201,6 +219,11 @@ def main() -> int:
             log(f"fused kernel status after timing: {to} barrier timeouts, {miss} missing")
             return 1
 
+    health = activation_health(x, rows * H)
+    if health["nonfinite"]:
+        log(f"activations overflowed: {health}")
+        return 1
+
     ms_per_step = total_ms / args.steps
     tok_s = rows * args.steps / (total_ms / 1e3)
     kern_avg_ms = float(np.mean(kernel_ms))
@@ -244,6 +267,7 @@ def main() -> int:
             "bytes_per_launch": alg_bytes,
             "kernel_avg_us": round(kern_avg_ms * 1e3, 2),
         },
+        "activations_after_last_layer": health,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
@@ -570,8 +594,8 @@ def run_prefill_stream(args) -> int:
         for t, (n, k) in enumerate(((I, H), (I, H), (H, I))):
             nbytes = hs.expert_bytes[t] * (E + S_)
             for e in range(E + S_):
-                nm.synth(dt[t], 3000 + 8 * l + t, n * k, scratch.ptr + e * hs.expert_bytes[t], 0.0, 0.02,
-                         offset=e * n * k, stream=compute.handle)
+                nm.synth(dt[t], 3000 + 8 * l + t, n * k, scratch.ptr + e * hs.expert_bytes[t], 0.0,
+                         DOWN_STD_DEEPSEEK if t == 2 else 0.02, offset=e * n * k, stream=compute.handle)
             nm.lib().naiwa_memcpy_d2h(hs.buffers[t].ptr, scratch.ptr, nbytes, compute.handle)
             compute.sync()
         router = nm.DeviceBuffer(E * H * 4)
@@ -626,6 +650,10 @@ def run_prefill_stream(args) -> int:
     e1.record(compute.handle)
     compute.sync()
     ms = e0.elapsed_ms(e1) / steps
+    health = activation_health(x, tokens * H)
+    if health["nonfinite"]:
+        log(f"activations overflowed: {health}")
+        return 1
     after = ps.stats()
     moved = (after["upload_bytes"] - before["upload_bytes"]) / steps
     tok_s = tokens / (ms / 1e3)
@@ -637,13 +665,15 @@ def run_prefill_stream(args) -> int:
         "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16 x Q4_K/Q8_0 (f32 accumulate)",
-        "data": "synthetic (device-generated N(0,0.02) Q4_K/Q8_0 experts in pinned host stacks)",
+        "data": "synthetic (device-generated Q4_K/Q8_0 experts in pinned host stacks: gate/up N(0,0.02), "
+                f"down N(0,{DOWN_STD_DEEPSEEK}); N(0,1) bf16 tokens)",
         "config": {"workload": "DeepSeek-V2-Lite-shaped MoE prefill, 26 layers, 64 routed top-6 + 2 shared experts "
                                "streamed from pinned host memory per layer, 2048 tokens",
                    "layers": L, "chunk": chunk, "depth": depth, "plan_stride": stride,
                    "plan_budget_gib": round(budget / 2**30, 1), "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "pcie", "achieved": round(pcie, 2), "peak": 64.0, "unit": "GB/s",
                      "frac": round(pcie / 64.0, 4), "traffic": None},
+        "activations_after_last_layer": health,
         "cpu_baseline": None,
     }
     print(json.dumps(result), flush=True)
@@ -672,7 +702,8 @@ def run_mixtral(args) -> int:
     for l in range(L):
         banks = nm.LayerBanks(E, H, I, dt)
         for t, bank in enumerate((banks.gate, banks.up, banks.down)):
-            nm.synth(nm.Q4_K, 6000 + 8 * l + t, E * bank.n * bank.k, bank.base, 0.0, 0.02, stream=stream.handle)
+            nm.synth(nm.Q4_K, 6000 + 8 * l + t, E * bank.n * bank.k, bank.base, 0.0,
+                     DOWN_STD_MIXTRAL if t == 2 else 0.02, stream=stream.handle)
         router = nm.DeviceBuffer(E * H * 4)
         nm.synth(nm.F32, 6000 + 8 * l + 3, E * H, router, 0.0, 0.02, stream=stream.handle)
         layers.append(nm.layer_desc(router, banks))
@@ -707,12 +738,17 @@ def run_mixtral(args) -> int:
         e1.record(stream.handle)
         stream.sync()
         ms = e0.elapsed_ms(e1) / steps
+        health = activation_health(x, rows * H)
+        if health["nonfinite"]:
+            log(f"mixtral decode bs{rows}: activations overflowed: {health}")
+            return 1
         ids = ids_d.download(np.uint32).reshape(L, rows, K)
         distinct = sum(len(np.unique(ids[l])) for l in range(L))
         alg = distinct * expert_bytes + L * (E * H * 4 + rows * H * 4)
         gbs = alg / (ms / 1e3) / 1e9
         out[f"decode_bs{rows}"] = {"tok_s": round(rows / (ms / 1e3), 2), "ms_per_step": round(ms, 3),
                                    "distinct_experts_per_layer": round(distinct / L, 2),
+                                   "activation_absmax": health["absmax"],
                                    "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
         log(f"mixtral decode bs{rows}: {ms:.3f} ms/step, {rows / (ms / 1e3):.1f} tok/s, {distinct / L:.2f} "
             f"experts/layer, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM peak)")
@@ -739,10 +775,16 @@ def run_mixtral(args) -> int:
     e1.record(stream.handle)
     stream.sync()
     ms = e0.elapsed_ms(e1) / reps
+    health = activation_health(x, T * H)
+    clamped = nm.prefill_status()
+    if health["nonfinite"] or clamped:
+        log(f"mixtral prefill: activations overflowed: {health}, {clamped} f16 clamps")
+        return 1
     flop = 6.0 * H * I * K * T * L
     tflops = flop / (ms / 1e3) / 1e12
     out["prefill_4096"] = {"tok_s": round(T / (ms / 1e3), 1), "ms": round(ms, 2), "tflops": round(tflops, 1),
-                           "mfma_frac": round(tflops / 2500.0, 4), "flop": flop}
+                           "mfma_frac": round(tflops / 2500.0, 4), "flop": flop,
+                           "activation_absmax": health["absmax"]}
     log(f"mixtral prefill {T} tokens: {ms:.1f} ms, {T / (ms / 1e3):.0f} tok/s, {tflops:.0f} TFLOP/s "
         f"({tflops / 2500 * 100:.1f}% of 2.5 PFLOP/s dense)")
     del x, ids, w, y
@@ -787,6 +829,10 @@ def run_mixtral(args) -> int:
     e1.record(stream.handle)
     stream.sync()
     ms = e0.elapsed_ms(e1) / csteps
+    health = activation_health(xc, H)
+    if health["nonfinite"]:
+        log(f"mixtral 4-of-8 cache: activations overflowed: {health}")
+        return 1
     pcie = tot["pcie_bytes"] / csteps / (ms / 1e3) / 1e9
     out["cache_4of8_bs1"] = {"layers": Lc, "ms_per_token": round(ms, 2), "tok_s_at_32_layers": round(1e3 / (ms * 32 / Lc), 3),
                              "hit_rate": round(tot["hits"] / max(1, tot["hits"] + tot["staged"]), 3),
@@ -810,7 +856,8 @@ def run_mixtral(args) -> int:
         "value": d1["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": max(3, min(args.steps, 20)), "warmup": 2,
         "ms_per_step": d1["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16 x Q4_K (f32 accumulate); prefill f16 x Q4_K (f32 accumulate)",
-        "data": "synthetic (device-generated N(0,0.02) Q4_K experts, N(0,1) bf16 tokens)",
+        "data": f"synthetic (device-generated Q4_K experts: gate/up N(0,0.02), down N(0,{DOWN_STD_MIXTRAL}); "
+                "N(0,1) bf16 tokens)",
         "config": {"workload": "Mixtral-8x7B-shaped MoE stack: decode bs 1/16/64 (all resident), 4096-token "
                                "prefill, bs1 decode with 4 of 8 experts cached", "layers": L, "hidden": H,
                    "experts": E, "top_k": K, "intermediate": I, "weights": "Q4_K", "parallelism": "none (1 GPU)"},
@@ -914,8 +961,8 @@ def run_prefill(args) -> int:
         banks = nm.LayerBanks(E + S_, H, I, dt)
         for t, bank in enumerate((banks.gate, banks.up, banks.down)):
             for e in range(E + S_):
-                nm.synth(dt[t], 3000 + 8 * l + t, bank.n * bank.k, bank.base + e * bank.stride, 0.0, 0.02,
-                         offset=e * bank.n * bank.k, stream=stream.handle)
+                nm.synth(dt[t], 3000 + 8 * l + t, bank.n * bank.k, bank.base + e * bank.stride, 0.0,
+                         DOWN_STD_DEEPSEEK if t == 2 else 0.02, offset=e * bank.n * bank.k, stream=stream.handle)
         router = nm.DeviceBuffer(E * H * 4)
         nm.synth(nm.F32, 3000 + 8 * l + 3, E * H, router, 0.0, 0.02, stream=stream.handle)
         layers.append((banks, router))
@@ -953,6 +1000,7 @@ def run_prefill(args) -> int:
     for _ in range(warmup):
         step()
     stream.sync()
+    nm.prefill_status()
     e0, e1 = nm.Event(), nm.Event()
     e0.record(stream.handle)
     for _ in range(steps):
@@ -960,6 +1008,11 @@ def run_prefill(args) -> int:
     e1.record(stream.handle)
     stream.sync()
     ms = e0.elapsed_ms(e1) / steps
+    health = activation_health(x, tokens * H)
+    clamped = nm.prefill_status()
+    if health["nonfinite"] or clamped:
+        log(f"prefill: activations overflowed: {health}, {clamped} f16 clamps")
+        return 1
     flop = 6.0 * H * I * (K + S_) * tokens * L   # 2 flop/MAC x (gate + up + down)
     tflops = flop / (ms / 1e3) / 1e12
     tok_s = tokens / (ms / 1e3)
@@ -1001,7 +1054,8 @@ def run_prefill(args) -> int:
         "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16 x Q4_K/Q8_0 (f32 accumulate)",
-        "data": "synthetic (device-generated N(0,0.02) Q4_K/Q8_0 experts, N(0,1) bf16 tokens)",
+        "data": f"synthetic (device-generated Q4_K/Q8_0 experts: gate/up N(0,0.02), down N(0,{DOWN_STD_DEEPSEEK}); "
+                "N(0,1) bf16 tokens)",
         "config": {"workload": "DeepSeek-V2-Lite-shaped MoE prefill, 26 layers, 64 routed top-6 + 2 shared "
                                "experts, I 1408, gate/up Q4_K, down Q8_0, 2048 tokens in 512-token chunks",
                    "layers": L, "hidden": H, "experts": E, "shared": S_, "top_k": K, "intermediate": I,
@@ -1012,6 +1066,7 @@ def run_prefill(args) -> int:
                      "bytes_per_launch": call_bytes, "call_avg_us": round(call_ms * 1e3, 2),
                      "mfma_tflops": round(call_flop / (call_ms / 1e3) / 1e12, 2),
                      "mfma_frac": round(call_flop / (call_ms / 1e3) / 1e12 / 2500.0, 4)},
+        "activations_after_last_layer": health, "f16_clamped": clamped,
         "cpu_baseline": None,
     }
     print(json.dumps(result), flush=True)

@@ -54,13 +54,18 @@ constexpr int NAIWA_SCRATCH_PREFILL = 5;
 // clamped value is counted here (naiwa_moe_prefill_status reads and resets the count).
 __device__ unsigned long long g_prefill_clamped = 0;
 
-// v clamped to the f16 range; counts (once per wave, by lane count) the values it changed.
-__device__ __forceinline__ float clamp_f16_counted(float v) {
-    const bool big = !(fabsf(v) <= 65504.0f);
-    const unsigned long long m = __ballot(big);
-    if (m && (threadIdx.x & 63) == (unsigned)__ffsll((long long)m) - 1)
-        atomicAdd(&g_prefill_clamped, (unsigned long long)__popcll(m));
+// v clamped to the f16 range; n counts the values it changed (NaN included).
+__device__ __forceinline__ float clamp_f16(float v, int& n) {
+    n += !(fabsf(v) <= 65504.0f);
     return fminf(fmaxf(v, -65504.0f), 65504.0f);
+}
+// Add this thread's clamp count to the total: one atomic per wave, and only when
+// something was clamped.  Every lane of the wave calls it.
+__device__ __forceinline__ void count_clamped(int n) {
+    if (__ballot(n != 0) == 0) return;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) n += __shfl_xor(n, m, 64);
+    if ((threadIdx.x & 63) == 0) atomicAdd(&g_prefill_clamped, (unsigned long long)n);
 }
 
 template <int DT> struct KBlock;
@@ -152,11 +157,13 @@ __global__ void __launch_bounds__(kThreads) prep_kernel(const uint16_t* x, int T
     if (in) v = *reinterpret_cast<const uint4*>(x + (size_t)t * H + 8 * run);
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
     float f[8];
+    int clamped = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        f[2 * j] = clamp_f16_counted(__uint_as_float(w[j] << 16));
-        f[2 * j + 1] = clamp_f16_counted(__uint_as_float(w[j] & 0xffff0000u));
+        f[2 * j] = clamp_f16(__uint_as_float(w[j] << 16), clamped);
+        f[2 * j + 1] = clamp_f16(__uint_as_float(w[j] & 0xffff0000u), clamped);
     }
+    count_clamped(clamped);
     if (!in) return;
     float g[8];
 #pragma unroll
@@ -373,15 +380,19 @@ gateup_kernel(Bank gate, Bank up, const uint16_t* xp, int H, int I, int k, const
     __syncthreads();
     if (is_up) {
         const int col = laid_pos<DD>(n);
+        int clamped = 0;
 #pragma unroll
         for (int ms = 0; ms < 2; ++ms)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int m = 32 * ms + 8 * (v / 4) + 4 * h + v % 4;
-                const float g = xch[xbase + (16 * ms + v) * 64];
-                const _Float16 hv = (_Float16)clamp_f16_counted(m < cnt ? g * acc[ms][v] : 0.0f);
-                if (m < cnt) hp[(size_t)(start + m) * I + col] = __builtin_bit_cast(uint16_t, hv);
+                if (m < cnt) {
+                    const float g = xch[xbase + (16 * ms + v) * 64];
+                    const _Float16 hv = (_Float16)clamp_f16(g * acc[ms][v], clamped);
+                    hp[(size_t)(start + m) * I + col] = __builtin_bit_cast(uint16_t, hv);
+                }
             }
+        count_clamped(clamped);
     }
 }
 
