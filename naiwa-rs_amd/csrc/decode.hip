@@ -14,14 +14,18 @@
 //      segment and the weighted dots are added per (token, row) in ascending
 //      slot order.  No atomics, so every run adds the same terms in the same
 //      order.
-// Calls of at most 512 pairs keep h in global memory in the down format's dot
-// layout (written once by the gate/up blocks, read by the down items); larger
-// calls stage f32 h per block, 4 tokens per pass.
+// Calls of at most 512 pairs (16 per token) keep h in global memory in the down
+// format's dot layout (written once by the gate/up blocks); the down rows are
+// dotted in K parts of 2048 with the h slices in LDS, and a last launch adds the
+// weighted parts per (token, row) in slot order.  Larger calls stage f32 h per
+// block, 4 tokens per pass.
+#include "decode_mfma.h"
 #include "rowdot.h"
 #include "segments.h"
 #include "workspace.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <mutex>
 
 namespace {
@@ -190,17 +194,30 @@ down_kernel(BankArg down, int H, int I, int rows, int width, int tok_max, const 
 // rows of each token's h straight in the down format's dot layout (16-bit pair
 // words + span sums, the same rounding and summation order as staging the f32
 // h would give) to hst[pair].
-// down_items: one block per kRowsD output rows; its (row, segment) items are
-// dealt over the block's 16-lane groups, each streaming the row once per
-// kTokD tokens of the segment and reading those tokens' h words from hst; the
-// weighted dots go to LDS by sorted pair position, and each (token, row) sums
-// its pairs in ascending position -- ascending slot -- order, as one pass over
-// all segments would.
+// down_split + down_combine: the down rows' dots over K parts of I with the h
+// slices staged in LDS (below), then the ordered per-(token, row) combine.
 constexpr int kPairsMax = 512;
 constexpr int kTokG = 8;
 constexpr int kTokD = 8;
-constexpr int kRowsDMax = 8;
 constexpr int kDownThreads = 256;
+constexpr int kSplitK = 2048;     // I elements per K part of the down projection
+constexpr int kCombineWidth = 16; // most pairs per token the combine orders
+constexpr int kCombineTok = 4;    // tokens per combine wave
+
+// The staged-h path serves calls of at most kPairsMax pairs and kCombineWidth per token.
+bool split_path(int n, int width) { return n <= kPairsMax && width <= kCombineWidth; }
+
+// Calls of at least this many rows run their expert GEMMs on the matrix cores
+// (NAIWA_DECODE_MFMA_ROWS; 0 switches the matrix-core decode off).
+int mfma_rows() {
+    static const int v = [] {
+        const char* e = std::getenv("NAIWA_DECODE_MFMA_ROWS");
+        return e && *e ? std::atoi(e) : 4;
+    }();
+    return v;
+}
+int split_ks(int I) { return I <= kSplitK ? I : kSplitK; }
+int split_parts(int I) { return (I + split_ks(I) - 1) / split_ks(I); }
 
 template <int DG, int DD>
 __global__ void __launch_bounds__(512)
@@ -295,69 +312,142 @@ gate_up_staged_kernel(BankArg gate, BankArg up, const void* x, int x_bf16, int H
     }
 }
 
+// down_split: the down projection in K parts.  Block (row tile, K part, segment):
+// up to tok_max tokens of the segment at a time have their h slice [k0, k0 + kn)
+// copied from hst into LDS, and each 16-lane group streams its rows' slices,
+// two rows at a time, dotting every unit with every staged token.  The unweighted
+// partial dot of (K part, sorted position, row) goes to dpart.
 template <int DD>
 __global__ void __launch_bounds__(kDownThreads)
-down_items_kernel(BankArg down, int H, int I, int rows, int width, int kRowsD, const int* seg_count,
-                  const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm, const float* w,
-                  const uint8_t* hst, int hst_stride, int accumulate, float* out) {
-    __shared__ float part[kPairsMax][kRowsDMax];
-    __shared__ uint32_t tok_of[kPairsMax];
-    const int tid = threadIdx.x, grp = tid / NAIWA_GROUP, lr = tid % NAIWA_GROUP;
-    const int r0 = blockIdx.x * kRowsD;
-    const int nseg = *seg_count;
-    const int npos = (int)seg_begin[nseg];
-    const int nu = Fmt<DD>::units(I);
+down_split_kernel(BankArg down, int H, int I, int ks, int rpg, int tok_max, int n, const int* seg_count,
+                  const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm, const uint8_t* hst,
+                  int hst_stride, float* dpart) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int SPAN = Fmt<DD>::kSumSpan;
     constexpr int UM = Umax<DD>::v;
-    for (int i = tid; i < npos; i += kDownThreads) tok_of[i] = perm[i] / (uint32_t)width;
-    // items (segment, row): groups take them in turn
-    for (int it = grp; it < nseg * kRowsD; it += kDownThreads / NAIWA_GROUP) {
-        const int sgi = it / kRowsD, rr = it % kRowsD, r = r0 + rr;
-        if (r >= H) continue;
-        const uint32_t slot = seg_key[sgi];
-        const int b = (int)seg_begin[sgi], e = (int)seg_begin[sgi + 1];
-        const uint8_t* drow = down.base + (int64_t)slot * down.stride + (int64_t)r * down.row_bytes;
-        for (int c0 = b; c0 < e; c0 += kTokD) {
-            const int nt = min(kTokD, e - c0);
-            float a[kTokD];
+    const int sgi = blockIdx.z;
+    if (sgi >= *seg_count) return;
+    const int tid = threadIdx.x, grp = tid / NAIWA_GROUP, lr = tid % NAIWA_GROUP;
+    const int kp = blockIdx.y, k0 = kp * ks, kn = min(ks, I - k0);
+    const int u0 = Fmt<DD>::units(k0), nus = Fmt<DD>::units(kn);
+    const int wb = kn * 2, nsum = kn / SPAN, nw4 = wb / 16;
+    const int tstride = (wb + nsum * 4 + 15) & ~15;
+    const uint32_t slot = seg_key[sgi];
+    const int b = (int)seg_begin[sgi], e = (int)seg_begin[sgi + 1];
+    const int rfirst = (blockIdx.x * (kDownThreads / NAIWA_GROUP) + grp) * rpg;
+    const uint8_t* dslot = down.base + (int64_t)slot * down.stride;
+    for (int c0 = b; c0 < e; c0 += tok_max) {
+        const int nt = min(tok_max, e - c0);
+        __syncthreads();
+        for (int i = tid; i < nt * nw4; i += kDownThreads) {
+            const int tt = i / nw4, j = i % nw4;
+            const uint8_t* src = hst + (size_t)perm[c0 + tt] * hst_stride + (size_t)k0 * 2;
+            reinterpret_cast<uint4*>(smem + tt * tstride)[j] = reinterpret_cast<const uint4*>(src)[j];
+        }
+        for (int i = tid; i < nt * nsum; i += kDownThreads) {
+            const int tt = i / nsum, j = i % nsum;
+            const float* sums = reinterpret_cast<const float*>(hst + (size_t)perm[c0 + tt] * hst_stride + (size_t)I * 2);
+            reinterpret_cast<float*>(smem + tt * tstride + wb)[j] = sums[k0 / SPAN + j];
+        }
+        __syncthreads();
+        for (int i = 0; i < rpg; i += 2) {
+            const int r = rfirst + i;
+            if (r >= H) break;
+            const bool two = i + 1 < rpg && r + 1 < H;
+            const uint8_t* drow0 = dslot + (int64_t)r * down.row_bytes;
+            const uint8_t* drow1 = drow0 + (two ? down.row_bytes : 0);
+            float a0[kTokD], a1[kTokD];
 #pragma unroll
-            for (int tt = 0; tt < kTokD; ++tt) a[tt] = 0.0f;
-            for (int base = lr; base < nu; base += NAIWA_GROUP * UM) {
-                typename Fmt<DD>::Frag f[UM];
+            for (int tt = 0; tt < kTokD; ++tt) a0[tt] = a1[tt] = 0.0f;
+            for (int base = lr; base < nus; base += NAIWA_GROUP * UM) {
+                typename Fmt<DD>::Frag f0[UM], f1[UM];
 #pragma unroll
-                for (int i = 0; i < UM; ++i) {
-                    const int u = base + NAIWA_GROUP * i;
-                    if (u < nu) f[i] = Fmt<DD>::load(drow, u);
+                for (int q = 0; q < UM; ++q) {
+                    const int u = base + NAIWA_GROUP * q;
+                    if (u < nus) {
+                        f0[q] = Fmt<DD>::load(drow0, u0 + u);
+                        if (two) f1[q] = Fmt<DD>::load(drow1, u0 + u);
+                    }
                 }
 #pragma unroll
-                for (int i = 0; i < UM; ++i) {
-                    const int u = base + NAIWA_GROUP * i;
-                    if (u >= nu) continue;
+                for (int q = 0; q < UM; ++q) {
+                    const int u = base + NAIWA_GROUP * q;
+                    if (u >= nus) continue;
 #pragma unroll
                     for (int tt = 0; tt < kTokD; ++tt) {
                         if (tt >= nt) break;
-                        const uint32_t* words = (const uint32_t*)(hst + (size_t)perm[c0 + tt] * hst_stride);
-                        a[tt] += Fmt<DD>::dot(f[i], u, words, (const float*)(words + I / 2));
+                        const uint32_t* words = reinterpret_cast<const uint32_t*>(smem + tt * tstride);
+                        const float* sums = reinterpret_cast<const float*>(smem + tt * tstride + wb);
+                        a0[tt] += Fmt<DD>::dot(f0[q], u, words, sums);
+                        if (two) a1[tt] += Fmt<DD>::dot(f1[q], u, words, sums);
                     }
                 }
             }
 #pragma unroll
             for (int tt = 0; tt < kTokD; ++tt) {
-                const float v = naiwa_group_sum<NAIWA_GROUP>(a[tt]);
-                if (tt < nt && lr == 0) part[c0 + tt][rr] = w[perm[c0 + tt]] * v;
+                const float v0 = naiwa_group_sum<NAIWA_GROUP>(a0[tt]);
+                const float v1 = naiwa_group_sum<NAIWA_GROUP>(a1[tt]);
+                if (tt < nt && lr == 0) {
+                    float* dst = dpart + ((size_t)kp * n + c0 + tt) * H + r;
+                    dst[0] = v0;
+                    if (two) dst[1] = v1;
+                }
             }
         }
     }
+}
+
+// down_combine: one wave per (64 output rows, kCombineTok tokens).  Each token's
+// sorted positions are listed (weight-0 pairs have none) and ordered ascending;
+// out(t, r) starts at 0, or at out's value, and adds w * (the pair's K parts summed
+// in order) over those positions -- ascending slot, the order of one pass over all
+// segments (and of one call over both halves of a split by slot).
+__global__ void __launch_bounds__(64)
+down_combine_kernel(const float* dpart, int kparts, int n, int H, int rows, int width, const int* seg_count,
+                    const uint32_t* seg_begin, const uint32_t* perm, const float* w, int accumulate, float* out) {
+    __shared__ int list[kCombineTok][kCombineWidth];
+    __shared__ int cnt[kCombineTok];
+    static_assert(kCombineTok * kCombineWidth == 64, "one list entry per lane");
+    const int lane = threadIdx.x;
+    const int t0 = blockIdx.y * kCombineTok;
+    const int tn = min(kCombineTok, rows - t0);
+    const int npos = (int)seg_begin[*seg_count];
+    (&list[0][0])[lane] = -1;
     __syncthreads();
-    // (token, row): the sum starts at 0, or at out's value, and adds the token's pairs in
-    // ascending sorted position, i.e. ascending slot (the same additions as one call over
-    // both halves of a split by slot)
-    for (int i = tid; i < rows * kRowsD; i += kDownThreads) {
-        const int t = i / kRowsD, rr = i % kRowsD, r = r0 + rr;
-        if (r >= H) continue;
-        float acc = accumulate ? out[(int64_t)t * H + r] : 0.0f;
-        for (int pos = 0; pos < npos; ++pos)
-            if (tok_of[pos] == (uint32_t)t) acc += part[pos][rr];
-        out[(int64_t)t * H + r] = acc;
+    for (int pos = lane; pos < npos; pos += 64) {
+        const uint32_t p = perm[pos];
+        const int t = (int)(p / (uint32_t)width) - t0;
+        if (t >= 0 && t < tn) list[t][p % (uint32_t)width] = pos;
+    }
+    __syncthreads();
+    if (lane < tn) {
+        // insertion sort in place; entry j is read before any write reaches index j
+        int c = 0;
+        for (int j = 0; j < width; ++j) {
+            const int v = list[lane][j];
+            if (v < 0) continue;
+            int k = c++;
+            while (k > 0 && list[lane][k - 1] > v) {
+                list[lane][k] = list[lane][k - 1];
+                --k;
+            }
+            list[lane][k] = v;
+        }
+        cnt[lane] = c;
+    }
+    __syncthreads();
+    const int r = blockIdx.x * 64 + lane;
+    if (r >= H) return;
+    for (int tt = 0; tt < tn; ++tt) {
+        const int64_t o = (int64_t)(t0 + tt) * H + r;
+        float acc = accumulate ? out[o] : 0.0f;
+        for (int k = 0; k < cnt[tt]; ++k) {
+            const int pos = list[tt][k];
+            float v = dpart[(size_t)pos * H + r];
+            for (int kp = 1; kp < kparts; ++kp) v += dpart[((size_t)kp * n + pos) * H + r];
+            acc += w[perm[pos]] * v;
+        }
+        out[o] = acc;
     }
 }
 
@@ -376,15 +466,29 @@ int tok_cap(int dtype, int k) {
     return cap < 1 ? 0 : (cap > kTokMax ? kTokMax : cap);
 }
 
-// Scratch of one decode call: seg_count, bad | seg_key[n] | seg_begin[n+1] | perm[n] | h[n*I] f32.
+// Scratch of one decode call (n = rows * width pairs):
+//   seg_count, bad | seg_key[n] | seg_begin[n+1] | perm[n] | h | dpart.
+// Staged-h path: h = n vectors in the down format's dot layout (or, on the matrix
+// cores, f16 x [rows, H] and h [n, I]), dpart = K parts x n x H f32.  Otherwise
+// h = n x I f32 and no dpart.
 struct DecodeScratch {
-    size_t off_key, off_begin, off_perm, off_h, total;
-    DecodeScratch(int n, int I) {
+    size_t off_key, off_begin, off_perm, off_h, off_dpart, total;
+    DecodeScratch(int rows, int width, int H, int I, int down_dtype) {
+        const int n = rows * width;
         off_key = 256;
         off_begin = off_key + (((size_t)n * 4 + 255) & ~size_t(255));
         off_perm = off_begin + (((size_t)(n + 1) * 4 + 255) & ~size_t(255));
         off_h = off_perm + (((size_t)n * 4 + 255) & ~size_t(255));
-        total = off_h + (size_t)n * I * 4;
+        if (split_path(n, width)) {
+            // h in the down format's dot layout, or the matrix-core path's f16 x and h
+            const size_t hb =
+                std::max((size_t)n * naiwa_stage_bytes(down_dtype, I), naiwa_decode_mfma_bytes(rows, n, H, I));
+            off_dpart = off_h + ((hb + 255) & ~size_t(255));
+            total = off_dpart + (size_t)split_parts(I) * n * H * 4;
+        } else {
+            off_dpart = 0;
+            total = off_h + (size_t)n * I * 4;
+        }
     }
 };
 
@@ -417,6 +521,16 @@ int check_args(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* d
     return NAIWA_OK;
 }
 
+// out (token, row) from the K parts' unweighted dots in dpart.
+int combine_launch(const float* dpart, int kparts, int n, int H, int rows, int width, const int* seg_count,
+                   const uint32_t* seg_begin, const uint32_t* perm, const float* w, int accumulate, float* out,
+                   hipStream_t st) {
+    const dim3 cgrid((H + 63) / 64, (rows + kCombineTok - 1) / kCombineTok);
+    down_combine_kernel<<<cgrid, 64, 0, st>>>(dpart, kparts, n, H, rows, width, seg_count, seg_begin, perm, w,
+                                               accumulate, out);
+    return naiwa_hip_rc(hipGetLastError());
+}
+
 // The staged-h path: gate/up writes h in the down format's dot layout (one vector
 // of naiwa_stage_bytes(DD, I) per pair, at most DecodeScratch's h bytes), then the
 // item-parallel down + ordered combine.
@@ -424,34 +538,40 @@ template <int DG, int DD>
 int staged_kernels(BankArg g, BankArg u, BankArg d, const void* x, int xb, int H, int I, int rows, int width,
                    int act, const float* w, float* out, int accumulate, int n, int slots, const int* seg_count,
                    const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm, uint8_t* hst,
-                   hipStream_t st) {
+                   float* dpart, hipStream_t st) {
     constexpr int SPAN = Fmt<DD>::kSumSpan;
     const int stage_g = naiwa_stage_bytes(DG, H);
     const int tok = std::max(1, std::min(kTokG, (64 * 1024) / stage_g));
     const int hst_stride = naiwa_stage_bytes(DD, I);
-    const dim3 ggrid(n, I / SPAN);
+    // one column per possible segment: blocks past the segment count exit at once,
+    // and each still costs a dispatch with its full LDS reservation
+    const dim3 ggrid(std::max(1, std::min(n, slots)), I / SPAN);
     gate_up_staged_kernel<DG, DD><<<ggrid, SPAN * NAIWA_GROUP, (size_t)tok * stage_g, st>>>(
         g, u, x, xb, H, I, width, tok, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride);
-    // rows per down block: about one (row, segment) item per group of the block
+    // down: rows per group doubled while the grid keeps at least 1024 blocks
+    const int ks = split_ks(I), kparts = split_parts(I);
     const int segs = std::max(1, std::min(n, slots));
-    int rd = 1;
-    while (rd < kRowsDMax && rd * 2 * segs <= kDownThreads / NAIWA_GROUP) rd *= 2;
-    down_items_kernel<DD><<<(H + rd - 1) / rd, kDownThreads, 0, st>>>(d, H, I, rows, width, rd, seg_count, seg_key,
-                                                                      seg_begin, perm, w, hst, hst_stride,
-                                                                      accumulate, out);
-    return naiwa_hip_rc(hipGetLastError());
+    const int groups = kDownThreads / NAIWA_GROUP;
+    int rpg = 1;
+    while (rpg < 8 && (int64_t)((H + groups * rpg * 2 - 1) / (groups * rpg * 2)) * kparts * segs >= 1024) rpg *= 2;
+    const int stage_d = naiwa_stage_bytes(DD, ks);
+    const int tok_d = std::max(1, std::min({kTokD, rows, (64 * 1024) / stage_d}));
+    const dim3 dgrid((H + groups * rpg - 1) / (groups * rpg), kparts, segs);
+    down_split_kernel<DD><<<dgrid, kDownThreads, (size_t)tok_d * stage_d, st>>>(
+        d, H, I, ks, rpg, tok_d, n, seg_count, seg_key, seg_begin, perm, hst, hst_stride, dpart);
+    return combine_launch(dpart, kparts, n, H, rows, width, seg_count, seg_begin, perm, w, accumulate, out, st);
 }
 
 int staged_launch(BankArg g, BankArg u, BankArg d, int gdt, int ddt, const void* x, int x_dtype, int H, int I,
                   int rows, int width, int act, const float* w, float* out, int accumulate, int n, int slots,
                   const int* seg_count, const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm,
-                  uint8_t* hst, hipStream_t st) {
+                  uint8_t* hst, float* dpart, hipStream_t st) {
     const int xb = x_dtype == NAIWA_BF16;
     const int fg = naiwa_kernel_fmt(gdt, H), fd = naiwa_kernel_fmt(ddt, I);
 #define NAIWA_STAGED(FG, FD)                                                                                       \
     if (fg == FG && fd == FD)                                                                                      \
         return staged_kernels<FG, FD>(g, u, d, x, xb, H, I, rows, width, act, w, out, accumulate, n, slots,         \
-                                      seg_count, seg_key, seg_begin, perm, hst, st);
+                                      seg_count, seg_key, seg_begin, perm, hst, dpart, st);
     NAIWA_STAGED(NAIWA_Q4_K, NAIWA_Q4_K)
     NAIWA_STAGED(NAIWA_Q4_K, NAIWA_Q8_0)
     NAIWA_STAGED(NAIWA_Q4_K, NAIWA_Q8_0_ODD)
@@ -465,7 +585,7 @@ int staged_launch(BankArg g, BankArg u, BankArg d, int gdt, int ddt, const void*
     return NAIWA_E_UNSUPPORTED;
 }
 
-// The launches of one checked call over scratch ws (DecodeScratch(rows * width, I).total bytes).
+// The launches of one checked call over scratch ws (DecodeScratch(...).total bytes).
 int decode_launch(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, const void* x, int x_dtype,
                   const uint32_t* slot_ids, const float* w, int rows, int width, int act, float* out, int flags,
                   uint8_t* ws, hipStream_t st) {
@@ -481,7 +601,7 @@ int decode_launch(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank
     const int acc_bytes = ((rows * kRowsPerBlock * 4) + 15) & ~15;
     const size_t lds_down = (size_t)acc_bytes + (size_t)tok_d * naiwa_stage_bytes(down->dtype, I);
     const int n = rows * width;
-    const DecodeScratch L(n, I);
+    const DecodeScratch L(rows, width, H, I, down->dtype);
     int* seg_count = (int*)ws;
     int* bad = (int*)(ws + 4);
     uint32_t* seg_key = (uint32_t*)(ws + L.off_key);
@@ -494,9 +614,21 @@ int decode_launch(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank
     BankArg g{(const uint8_t*)gate->base, gate->slot_stride, naiwa_row_bytes(gate->dtype, H)};
     BankArg u{(const uint8_t*)up->base, up->slot_stride, naiwa_row_bytes(up->dtype, H)};
     BankArg d{(const uint8_t*)down->base, down->slot_stride, naiwa_row_bytes(down->dtype, I)};
-    if (n <= kPairsMax) return staged_launch(g, u, d, gate->dtype, down->dtype, x, x_dtype, H, I, rows, width, act,
-                                             w, out, accumulate, n, gate->slots, seg_count, seg_key, seg_begin, perm,
-                                             (uint8_t*)hbuf, st);
+    if (split_path(n, width)) {
+        float* dpart = (float*)(ws + L.off_dpart);
+        const int mr = mfma_rows();
+        if (mr > 0 && rows >= mr && naiwa_decode_mfma_ok(gate, up, down, x)) {
+            const int ks = split_ks(I), segs = std::max(1, std::min(n, gate->slots));
+            int rc = naiwa_decode_mfma_experts(gate, up, down, x, x_dtype, rows, width, act, n, segs, ks, seg_count,
+                                               seg_key, seg_begin, perm, (uint8_t*)hbuf, dpart, st);
+            if (rc) return rc;
+            return combine_launch(dpart, split_parts(I), n, H, rows, width, seg_count, seg_begin, perm, w,
+                                  accumulate, out, st);
+        }
+        return staged_launch(g, u, d, gate->dtype, down->dtype, x, x_dtype, H, I, rows, width, act, w, out,
+                             accumulate, n, gate->slots, seg_count, seg_key, seg_begin, perm, (uint8_t*)hbuf, dpart,
+                             st);
+    }
     const dim3 ggrid(n, (I + kRowsPerBlock - 1) / kRowsPerBlock);
     const size_t lds_g = (size_t)tok_g * naiwa_stage_bytes(gate->dtype, H);
     const int xb = x_dtype == NAIWA_BF16;
@@ -570,7 +702,8 @@ extern "C" int naiwa_moe_decode_ex(const naiwa_bank* gate, const naiwa_bank* up,
     if (rc || rows == 0) return rc;
     uint8_t* ws = nullptr;
     if (width > 0) {
-        ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_DECODE, DecodeScratch(rows * width, gate->n).total, &rc);
+        const DecodeScratch L(rows, width, gate->k, gate->n, down->dtype);
+        ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_DECODE, L.total, &rc);
         if (!ws) return rc;
     }
     return decode_launch(gate, up, down, x, x_dtype, slot_ids, w, rows, width, act, out, flags, ws,
@@ -582,7 +715,8 @@ extern "C" int naiwa_moe_decode_noalloc(const naiwa_bank* gate, const naiwa_bank
                                         int rows, int width, int act, float* out, int flags, int64_t stream) {
     int rc = check_args(gate, up, down, x, x_dtype, slot_ids, w, rows, width, act, out, flags);
     if (rc || rows == 0) return rc;
-    if (width > 0 && DecodeScratch(rows * width, gate->n).total > kNoAllocScratchBytes) return NAIWA_E_TOO_LARGE;
+    if (width > 0 && DecodeScratch(rows, width, gate->k, gate->n, down->dtype).total > kNoAllocScratchBytes)
+        return NAIWA_E_TOO_LARGE;
     uint8_t* ws = nullptr;
     if ((rc = noalloc_scratch(&ws))) return rc;
     return decode_launch(gate, up, down, x, x_dtype, slot_ids, w, rows, width, act, out, flags, ws,

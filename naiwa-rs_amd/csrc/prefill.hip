@@ -34,6 +34,7 @@
 // The activations (x for gate/up, h for down) are stored as groups g = 2s + h
 // of 8 f16 in that order, so the A operand of a step is one 16-byte read.
 #include "common.h"
+#include "decode_mfma.h"
 #include "workspace.h"
 
 namespace {
@@ -41,6 +42,7 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;  // gather helpers, prep, combine
@@ -177,6 +179,63 @@ __global__ void __launch_bounds__(kThreads) prep_kernel(const uint16_t* x, int T
     *reinterpret_cast<uint4*>(xp + (size_t)t * H + dst) = o;
 }
 
+// (d * scale, -dmin * min) of 32-value sub-block j of a Q4_K block whose first 16
+// bytes are hd (ggml's get_scale_min_k4), as f16.
+__device__ __forceinline__ void q4k_scale_min(const u32x4& hd, int j, _Float16& sc, _Float16& mn) {
+    const uint32_t s3[3] = {hd.y, hd.z, hd.w};
+    auto sb = [&](int i) -> int { return (int)((s3[i >> 2] >> (8 * (i & 3))) & 0xFFu); };
+    int s, m;
+    if (j < 4) {
+        s = sb(j) & 63;
+        m = sb(j + 4) & 63;
+    } else {
+        s = (sb(j + 4) & 0xF) | ((sb(j - 4) >> 6) << 4);
+        m = (sb(j + 4) >> 4) | ((sb(j) >> 6) << 4);
+    }
+    sc = (_Float16)(naiwa_f16_to_f32(hd.x & 0xffffu) * (float)s);
+    mn = (_Float16)(-(naiwa_f16_to_f32(hd.x >> 16) * (float)m));
+}
+
+// The 8 f16 weights (1024 + nibble) * sc + mn of quant words da, db (bytes 0-7 of a
+// run), low nibbles when sh = 0 and high ones when sh = 4, in byte order 0 2 1 3 4 6 5 7.
+__device__ __forceinline__ half8 q4k_unpack(uint32_t da, uint32_t db, int sh, _Float16 sc, _Float16 mn) {
+    const half2v scv = {sc, sc}, mnv = {mn, mn};
+    const half2v k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    half2v p[4];
+    p[0] = __builtin_bit_cast(half2v, ((da >> sh) & 0x000F000Fu) | 0x64006400u);
+    p[1] = __builtin_bit_cast(half2v, ((da >> (sh + 8)) & 0x000F000Fu) | 0x64006400u);
+    p[2] = __builtin_bit_cast(half2v, ((db >> sh) & 0x000F000Fu) | 0x64006400u);
+    p[3] = __builtin_bit_cast(half2v, ((db >> (sh + 8)) & 0x000F000Fu) | 0x64006400u);
+    half8 out;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const half2v w = __builtin_elementwise_fma(p[i] + k1024, scv, mnv);
+        out[2 * i] = w[0];
+        out[2 * i + 1] = w[1];
+    }
+    return out;
+}
+
+// The 8 f16 weights d * q of the signed bytes of words d0, d1 (values in order).
+__device__ __forceinline__ half8 q8_unpack(uint32_t d0, uint32_t d1, _Float16 dv) {
+    const half2v d = {dv, dv};
+    const half2v k1152 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    half2v p[4];
+    // (q0, q1) -> f16 1024 + (q ^ 0x80) = 1152 + q for the signed byte q
+    p[0] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(d0, d0, 0x0C010C00u) ^ 0x64806480u);
+    p[1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(d0, d0, 0x0C030C02u) ^ 0x64806480u);
+    p[2] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(d1, d1, 0x0C010C00u) ^ 0x64806480u);
+    p[3] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(d1, d1, 0x0C030C02u) ^ 0x64806480u);
+    half8 out;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const half2v v = (p[i] + k1152) * d;
+        out[2 * i] = v[0];
+        out[2 * i + 1] = v[1];
+    }
+    return out;
+}
+
 // One lane's share of a weight row for one K-block: raw words, then unpacked
 // step by step into the MFMA B operand (8 f16).
 template <int DT> struct BRow;
@@ -191,41 +250,12 @@ template <> struct BRow<NAIWA_Q4_K> {
 #pragma unroll
         for (int c = 0; c < 4; ++c) q[c] = *reinterpret_cast<const u32x4*>(blk + 16 + 32 * c + 16 * h);
     }
-    // (d * scale, -dmin * min) of 32-value sub-block j (ggml's get_scale_min_k4), as f16
-    __device__ __forceinline__ void scale_min(int j, _Float16& sc, _Float16& mn) const {
-        const uint32_t s3[3] = {hd.y, hd.z, hd.w};
-        auto sb = [&](int i) -> int { return (int)((s3[i >> 2] >> (8 * (i & 3))) & 0xFFu); };
-        int s, m;
-        if (j < 4) {
-            s = sb(j) & 63;
-            m = sb(j + 4) & 63;
-        } else {
-            s = (sb(j + 4) & 0xF) | ((sb(j - 4) >> 6) << 4);
-            m = (sb(j + 4) >> 4) | ((sb(j) >> 6) << 4);
-        }
-        sc = (_Float16)(naiwa_f16_to_f32(hd.x & 0xffffu) * (float)s);
-        mn = (_Float16)(-(naiwa_f16_to_f32(hd.x >> 16) * (float)m));
-    }
     __device__ __forceinline__ half8 step(int s) const {
-        const int c = s / 4, t = s % 4, sh = 4 * (t / 2);
+        const int c = s / 4, t = s % 4;
         const uint32_t da = (t % 2) ? q[c].z : q[c].x, db = (t % 2) ? q[c].w : q[c].y;
         _Float16 a, b;
-        scale_min(2 * c + t / 2, a, b);
-        const half2v scv = {a, a}, mnv = {b, b};
-        const half2v k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-        half2v p[4];
-        p[0] = __builtin_bit_cast(half2v, ((da >> sh) & 0x000F000Fu) | 0x64006400u);
-        p[1] = __builtin_bit_cast(half2v, ((da >> (sh + 8)) & 0x000F000Fu) | 0x64006400u);
-        p[2] = __builtin_bit_cast(half2v, ((db >> sh) & 0x000F000Fu) | 0x64006400u);
-        p[3] = __builtin_bit_cast(half2v, ((db >> (sh + 8)) & 0x000F000Fu) | 0x64006400u);
-        half8 out;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const half2v w = __builtin_elementwise_fma(p[i] + k1024, scv, mnv);
-            out[2 * i] = w[0];
-            out[2 * i + 1] = w[1];
-        }
-        return out;
+        q4k_scale_min(hd, 2 * c + t / 2, a, b);
+        return q4k_unpack(da, db, 4 * (t / 2), a, b);
     }
 };
 
@@ -251,23 +281,7 @@ template <> struct BRow<NAIWA_Q8_0> {
         const uint32_t d1 =
             sh[j] ? w[j][2 * u + 2] : __builtin_amdgcn_alignbyte(w[j][2 * u + 2], w[j][2 * u + 1], 2);
         const uint32_t dbits = sh[j] ? (w[j][0] >> 16) : (w[j][0] & 0xffffu);
-        const _Float16 dv = __builtin_bit_cast(_Float16, (uint16_t)dbits);
-        const half2v d = {dv, dv};
-        const half2v k1152 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-        half2v p[4];
-        // (q0, q1) -> f16 1024 + (q ^ 0x80) = 1152 + q for the signed byte q
-        p[0] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(d0, d0, 0x0C010C00u) ^ 0x64806480u);
-        p[1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(d0, d0, 0x0C030C02u) ^ 0x64806480u);
-        p[2] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(d1, d1, 0x0C010C00u) ^ 0x64806480u);
-        p[3] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(d1, d1, 0x0C030C02u) ^ 0x64806480u);
-        half8 out;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const half2v v = (p[i] + k1152) * d;
-            out[2 * i] = v[0];
-            out[2 * i + 1] = v[1];
-        }
-        return out;
+        return q8_unpack(d0, d1, __builtin_bit_cast(_Float16, (uint16_t)dbits));
     }
 };
 
@@ -486,6 +500,276 @@ combine_kernel(const float* ypair, const uint32_t* ids, int k, int H, int slots,
     }
 }
 
+// ---------------------------------------------------------------------------
+// Multi-token decode on the matrix cores
+// ---------------------------------------------------------------------------
+// naiwa_moe_decode calls with several tokens per expert run their expert GEMMs
+// here.  A block of 8 waves takes one slot segment (the sorted pairs of one
+// slot) and 128 features; chunks of up to 16 of the segment's tokens are the A
+// operand of v_mfma_f32_16x16x32_f16 and each lane dequantises its own weight
+// values once into the B operand, so a weight costs the same whatever the
+// token count.  Lane l = 16 g + m holds A[m][8 g + 0..7] (token m of the
+// chunk), B[8 g + 0..7][m] (feature m of the wave's 16) and D[4 g + i][m].
+// Gate and up accumulate in the same wave, so h = act(g) * u is formed in
+// registers.
+//
+// K order of the 16x16x32 steps.  In every K-block lane group g reads:
+//   Q4_K (256 values): 64-value chunk g; step s = 2 p + t takes its quant bytes
+//        8 p + 0..7, low nibbles for t = 0 and high ones for t = 1: values
+//        64 g + 32 t + 8 p + (0 2 1 3 4 6 5 7);
+//   Q8_0 (128 values, 4 blocks): block g; step s takes its values 8 s + 0..7.
+// The activations (x for gate/up, h for down) are stored as groups G = 4 s + g
+// of 8 f16 in that order.
+constexpr int kDecM = 16;       // tokens per MFMA tile
+constexpr int kDecThreads = 512; // 8 waves of 16 features
+constexpr int kDecF = 128;      // features (gate/up) or output rows (down) per block
+
+template <int DT> struct K16;
+template <> struct K16<NAIWA_Q4_K> {
+    static constexpr int kVals = 256, kSteps = 8;
+};
+template <> struct K16<NAIWA_Q8_0> {
+    static constexpr int kVals = 128, kSteps = 4;
+};
+
+// Position, in the laid-out row, of value f of the original row.
+template <int DT>
+__host__ __device__ inline int laid16(int f) {
+    constexpr int KV = K16<DT>::kVals;
+    const int kb = f / KV, r = f % KV;
+    if (DT == NAIWA_Q4_K) {
+        const int g = r / 64, t = (r % 64) / 32, p = (r % 32) / 8;
+        return kb * KV + 8 * (4 * (2 * p + t) + g) + q4_elem(r % 8);
+    }
+    const int g = r / 32, st = (r % 32) / 8;
+    return kb * KV + 8 * (4 * st + g) + r % 8;
+}
+
+// Per-K-block scale state of one lane (Q4_K: its two sub-blocks 2 g and 2 g + 1).
+struct Scl {
+    _Float16 sc[2], mn[2];
+};
+
+// One lane's weights of one K-block (row `row`, lane group g).
+template <int DT> struct W16;
+
+template <> struct W16<NAIWA_Q4_K> {
+    u32x4 hd, q0, q1; // header; quant bytes 0-15 and 16-31 of chunk g
+    __device__ __forceinline__ void load(const uint8_t* row, int kb, int g) {
+        const uint8_t* blk = row + (size_t)kb * NAIWA_Q4_K_BYTES;
+        hd = *reinterpret_cast<const u32x4*>(blk);
+        q0 = *reinterpret_cast<const u32x4*>(blk + 16 + 32 * g);
+        q1 = *reinterpret_cast<const u32x4*>(blk + 32 + 32 * g);
+    }
+    __device__ __forceinline__ void prep(int g, Scl& c) const {
+        q4k_scale_min(hd, 2 * g, c.sc[0], c.mn[0]);
+        q4k_scale_min(hd, 2 * g + 1, c.sc[1], c.mn[1]);
+    }
+    __device__ __forceinline__ half8 step(int s, const Scl& c) const {
+        const int p = s >> 1, t = s & 1;
+        const u32x4& q = p < 2 ? q0 : q1;
+        const uint32_t da = (p & 1) ? q.z : q.x, db = (p & 1) ? q.w : q.y;
+        return q4k_unpack(da, db, 4 * t, c.sc[t], c.mn[t]);
+    }
+};
+
+template <> struct W16<NAIWA_Q8_0> {
+    uint32_t w[9]; // block 4 kb + g: 9 words from its aligned start
+    int sh;        // its byte offset within the first word (0 or 2)
+    __device__ __forceinline__ void load(const uint8_t* row, int kb, int g) {
+        const int off = (4 * kb + g) * NAIWA_Q8_0_BYTES;
+        sh = off & 3;
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(row + (off & ~3));
+#pragma unroll
+        for (int i = 0; i < 9; ++i) w[i] = p[i];
+    }
+    __device__ __forceinline__ void prep(int, Scl&) const {}
+    __device__ __forceinline__ half8 step(int s, const Scl&) const {
+        const uint32_t d0 = sh ? w[2 * s + 1] : __builtin_amdgcn_alignbyte(w[2 * s + 1], w[2 * s], 2);
+        const uint32_t d1 = sh ? w[2 * s + 2] : __builtin_amdgcn_alignbyte(w[2 * s + 2], w[2 * s + 1], 2);
+        const uint32_t dbits = sh ? (w[0] >> 16) : (w[0] & 0xffffu);
+        return q8_unpack(d0, d1, __builtin_bit_cast(_Float16, (uint16_t)dbits));
+    }
+};
+
+// LDS A tile of one K-block: group G of token row m at [G][m ^ (G % 16)].
+template <int DT> struct ATile16 {
+    static constexpr int kGroups = 4 * K16<DT>::kSteps;
+    u32x4 v[kGroups][kDecM];
+    __device__ __forceinline__ u32x4& at(int G, int m) { return v[G][m ^ (G & 15)]; }
+    __device__ __forceinline__ const u32x4& at(int G, int m) const { return v[G][m ^ (G & 15)]; }
+};
+
+// Thread tid's piece of one K-block of the A tile: row tid / G, group tid % G (the
+// lanes of a load cover whole rows); rows[m] < 0 is a zero row.
+template <int DT> struct AStage16 {
+    u32x4 r;
+    __device__ __forceinline__ void load(const uint16_t* base, const int* rows, int kb, int tid) {
+        constexpr int G = ATile16<DT>::kGroups;
+        r = u32x4{0u, 0u, 0u, 0u};
+        if (tid < G * kDecM) {
+            const int ro = rows[tid / G];
+            if (ro >= 0) r = *reinterpret_cast<const u32x4*>(base + ro + kb * K16<DT>::kVals + 8 * (tid % G));
+        }
+    }
+    __device__ __forceinline__ void store(ATile16<DT>& a, int tid) const {
+        constexpr int G = ATile16<DT>::kGroups;
+        if (tid < G * kDecM) a.at(tid % G, tid / G) = r;
+    }
+};
+
+// x (bf16 or f32) [T, H] -> xl f16 [T, H] in the 16x16x32 K order of DT, one thread
+// per run of 8 values; values past the f16 range are clamped and counted.
+template <int DT>
+__global__ void __launch_bounds__(kThreads) dec_prep_kernel(const void* x, int x_bf16, int T, int H, uint16_t* xl) {
+    const int runs = H / 8;
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const bool in = i < (int64_t)T * runs;
+    const int t = in ? (int)(i / runs) : 0, run = in ? (int)(i % runs) : 0;
+    float f[8] = {};
+    if (in) {
+        if (x_bf16) {
+            const uint4 v = *reinterpret_cast<const uint4*>((const uint16_t*)x + (size_t)t * H + 8 * run);
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                f[2 * j] = __uint_as_float(w[j] << 16);
+                f[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+            }
+        } else {
+            const float4* src = reinterpret_cast<const float4*>((const float*)x + (size_t)t * H + 8 * run);
+            const float4 a = src[0], b = src[1];
+            f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+            f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+        }
+    }
+    int clamped = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = clamp_f16(f[e], clamped);
+    count_clamped(clamped);
+    if (!in) return;
+    float g[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) g[e] = f[DT == NAIWA_Q4_K ? q4_elem(e) : e];
+    uint4 o;
+    o.x = f16x2_bits(g[0], g[1]);
+    o.y = f16x2_bits(g[2], g[3]);
+    o.z = f16x2_bits(g[4], g[5]);
+    o.w = f16x2_bits(g[6], g[7]);
+    *reinterpret_cast<uint4*>(xl + (size_t)t * H + laid16<DT>(8 * run)) = o;
+}
+
+// The K-block loop of one 16-token chunk: NP weight rows (gate and up, or down)
+// against the A rows listed in `rows`, K-blocks kb0 .. kb0 + nkb - 1.
+template <int DT, int NP>
+__device__ __forceinline__ void dec_chunk(const uint16_t* abase, const int* rows, const uint8_t* const* wrow,
+                                          int kb0, int nkb, ATile16<DT>* as, int tid, int g, int m,
+                                          floatx4* acc) {
+    AStage16<DT> st;
+    W16<DT> cur[NP], nxt[NP];
+    st.load(abase, rows, kb0, tid);
+#pragma unroll
+    for (int q = 0; q < NP; ++q) cur[q].load(wrow[q], kb0, g);
+    st.store(as[0], tid);
+    __syncthreads();
+    // one K-block; the next one's loads are unconditional (the last block reloads
+    // itself) so the compiler waits only for this block's registers
+    auto block = [&](int j, const W16<DT>* bw, W16<DT>* nw) {
+        const int kn = kb0 + min(j + 1, nkb - 1);
+        st.load(abase, rows, kn, tid);
+#pragma unroll
+        for (int q = 0; q < NP; ++q) nw[q].load(wrow[q], kn, g);
+        Scl c[NP];
+#pragma unroll
+        for (int q = 0; q < NP; ++q) bw[q].prep(g, c[q]);
+        const ATile16<DT>& a = as[j & 1];
+#pragma unroll
+        for (int s = 0; s < K16<DT>::kSteps; ++s) {
+            const half8 x8 = __builtin_bit_cast(half8, a.at(4 * s + g, m));
+#pragma unroll
+            for (int q = 0; q < NP; ++q)
+                acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x8, bw[q].step(s, c[q]), acc[q], 0, 0, 0);
+        }
+        st.store(as[(j + 1) & 1], tid);
+        __syncthreads();
+    };
+    int j = 0;
+    for (; j + 2 <= nkb; j += 2) {
+        block(j, cur, nxt);
+        block(j + 1, nxt, cur);
+    }
+    if (j < nkb) block(j, cur, nxt);
+}
+
+// gate/up: block (128 features, slot segment); h = act(gate) * up as f16 at the
+// pair's sorted position, in the 16x16x32 K order of DD.
+template <int DG, int DD>
+__global__ void __launch_bounds__(kDecThreads, 2)
+dec_gateup_kernel(Bank gate, Bank up, const uint16_t* xl, int H, int I, int width, const int* seg_count,
+                  const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm, int act, uint16_t* hl) {
+    __shared__ ATile16<DG> as[2];
+    __shared__ int rows[kDecM];
+    const int sg = blockIdx.y;
+    if (sg >= *seg_count) return;
+    const int tid = threadIdx.x, lane = tid & 63, m = lane & 15, g = lane >> 4;
+    const uint32_t slot = seg_key[sg];
+    const int b = (int)seg_begin[sg], e = (int)seg_begin[sg + 1];
+    const int n = blockIdx.x * kDecF + 16 * (tid >> 6) + m;
+    const uint8_t* wrow[2] = {gate.base + (int64_t)slot * gate.stride + (int64_t)n * gate.row_bytes,
+                              up.base + (int64_t)slot * up.stride + (int64_t)n * up.row_bytes};
+    const int col = laid16<DD>(n);
+    int clamped = 0;
+    for (int c0 = b; c0 < e; c0 += kDecM) {
+        const int cnt = min(kDecM, e - c0);
+        __syncthreads(); // the previous chunk is done with rows and the A tiles
+        if (tid < kDecM) rows[tid] = tid < cnt ? (int)(perm[c0 + tid] / (uint32_t)width) * H : -1;
+        __syncthreads();
+        floatx4 acc[2] = {};
+        dec_chunk<DG, 2>(xl, rows, wrow, 0, H / K16<DG>::kVals, as, tid, g, m, acc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int mm = 4 * g + i;
+            if (mm < cnt) {
+                const float hv = clamp_f16(naiwa_act(act, acc[0][i]) * acc[1][i], clamped);
+                hl[(size_t)(c0 + mm) * I + col] = __builtin_bit_cast(uint16_t, (_Float16)hv);
+            }
+        }
+    }
+    count_clamped(clamped);
+}
+
+// down: block (128 output rows, K part, slot segment); the unweighted partial dot of
+// (K part, sorted position, row) into dpart.
+template <int DD>
+__global__ void __launch_bounds__(kDecThreads, 2)
+dec_down_kernel(Bank down, const uint16_t* hl, int H, int I, int ks, int npairs, const int* seg_count,
+                const uint32_t* seg_key, const uint32_t* seg_begin, float* dpart) {
+    __shared__ ATile16<DD> as[2];
+    __shared__ int rows[kDecM];
+    const int sg = blockIdx.z;
+    if (sg >= *seg_count) return;
+    const int tid = threadIdx.x, lane = tid & 63, m = lane & 15, g = lane >> 4;
+    const uint32_t slot = seg_key[sg];
+    const int b = (int)seg_begin[sg], e = (int)seg_begin[sg + 1];
+    const int kp = blockIdx.y, k0 = kp * ks;
+    const int r = blockIdx.x * kDecF + 16 * (tid >> 6) + m;
+    const uint8_t* wrow[1] = {down.base + (int64_t)slot * down.stride + (int64_t)r * down.row_bytes};
+    for (int c0 = b; c0 < e; c0 += kDecM) {
+        const int cnt = min(kDecM, e - c0);
+        __syncthreads();
+        if (tid < kDecM) rows[tid] = tid < cnt ? (c0 + tid) * I : -1;
+        __syncthreads();
+        floatx4 acc[1] = {};
+        dec_chunk<DD, 1>(hl, rows, wrow, k0 / K16<DD>::kVals, min(ks, I - k0) / K16<DD>::kVals, as, tid, g, m,
+                         acc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int mm = 4 * g + i;
+            if (mm < cnt) dpart[((size_t)kp * npairs + c0 + mm) * H + r] = acc[0][i];
+        }
+    }
+}
+
 // K of a projection in this format: whole K-blocks.
 bool fmt_ok(int dtype, int kdim) {
     return (dtype == NAIWA_Q4_K && kdim % KBlock<NAIWA_Q4_K>::kVals == 0) ||
@@ -499,6 +783,61 @@ void launch_gateup(dim3 g, hipStream_t st, Bank bg, Bank bu, const uint16_t* xp,
 }
 
 } // namespace
+
+bool naiwa_decode_mfma_ok(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, const void* x) {
+    const int H = gate->k, I = gate->n;
+    auto fmt = [](int dt, int k) {
+        return (dt == NAIWA_Q4_K && k % K16<NAIWA_Q4_K>::kVals == 0) ||
+               (dt == NAIWA_Q8_0 && k % K16<NAIWA_Q8_0>::kVals == 0);
+    };
+    if (gate->dtype != up->dtype || !fmt(gate->dtype, H) || !fmt(down->dtype, I)) return false;
+    if (H % kDecF || I % kDecF) return false;
+    return ((uintptr_t)x & 15) == 0; // 16-byte loads of x
+}
+
+size_t naiwa_decode_mfma_bytes(int rows, int n, int H, int I) {
+    return (((size_t)rows * H * 2 + 255) & ~size_t(255)) + (size_t)n * I * 2;
+}
+
+int naiwa_decode_mfma_experts(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, const void* x,
+                              int x_dtype, int rows, int width, int act, int n, int seg_bound, int ks,
+                              const int* seg_count, const uint32_t* seg_key, const uint32_t* seg_begin,
+                              const uint32_t* perm, uint8_t* ws, float* dpart, hipStream_t st) {
+    const int H = gate->k, I = gate->n;
+    uint16_t* xl = (uint16_t*)ws;
+    uint16_t* hl = (uint16_t*)(ws + (((size_t)rows * H * 2 + 255) & ~size_t(255)));
+    const Bank bg{(const uint8_t*)gate->base, gate->slot_stride, naiwa_row_bytes(gate->dtype, H)};
+    const Bank bu{(const uint8_t*)up->base, up->slot_stride, naiwa_row_bytes(up->dtype, H)};
+    const Bank bd{(const uint8_t*)down->base, down->slot_stride, naiwa_row_bytes(down->dtype, I)};
+    const int xb = x_dtype == NAIWA_BF16;
+    const unsigned pb = (unsigned)(((int64_t)rows * (H / 8) + kThreads - 1) / kThreads);
+    const bool g4 = gate->dtype == NAIWA_Q4_K, d4 = down->dtype == NAIWA_Q4_K;
+    if (g4)
+        dec_prep_kernel<NAIWA_Q4_K><<<pb, kThreads, 0, st>>>(x, xb, rows, H, xl);
+    else
+        dec_prep_kernel<NAIWA_Q8_0><<<pb, kThreads, 0, st>>>(x, xb, rows, H, xl);
+    const dim3 g1(I / kDecF, seg_bound);
+    if (g4 && d4)
+        dec_gateup_kernel<NAIWA_Q4_K, NAIWA_Q4_K><<<g1, kDecThreads, 0, st>>>(bg, bu, xl, H, I, width, seg_count,
+                                                                              seg_key, seg_begin, perm, act, hl);
+    else if (g4)
+        dec_gateup_kernel<NAIWA_Q4_K, NAIWA_Q8_0><<<g1, kDecThreads, 0, st>>>(bg, bu, xl, H, I, width, seg_count,
+                                                                              seg_key, seg_begin, perm, act, hl);
+    else if (d4)
+        dec_gateup_kernel<NAIWA_Q8_0, NAIWA_Q4_K><<<g1, kDecThreads, 0, st>>>(bg, bu, xl, H, I, width, seg_count,
+                                                                              seg_key, seg_begin, perm, act, hl);
+    else
+        dec_gateup_kernel<NAIWA_Q8_0, NAIWA_Q8_0><<<g1, kDecThreads, 0, st>>>(bg, bu, xl, H, I, width, seg_count,
+                                                                              seg_key, seg_begin, perm, act, hl);
+    const dim3 g2(H / kDecF, (I + ks - 1) / ks, seg_bound);
+    if (d4)
+        dec_down_kernel<NAIWA_Q4_K><<<g2, kDecThreads, 0, st>>>(bd, hl, H, I, ks, n, seg_count, seg_key, seg_begin,
+                                                                 dpart);
+    else
+        dec_down_kernel<NAIWA_Q8_0><<<g2, kDecThreads, 0, st>>>(bd, hl, H, I, ks, n, seg_count, seg_key, seg_begin,
+                                                                 dpart);
+    return naiwa_hip_rc(hipGetLastError());
+}
 
 extern "C" int naiwa_moe_prefill_status(uint64_t* clamped) {
     if (!clamped) return NAIWA_E_INVALID;

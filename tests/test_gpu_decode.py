@@ -204,3 +204,82 @@ def test_split_by_slot_with_accumulate_is_bit_identical(gpu):
         nm.indexed_moe_fused_decode(banks, xd, nm.BF16, idd, hi, rows, k, split, accumulate=True)
         nm.synchronize()
         assert np.array_equal(whole.download(np.float32), split.download(np.float32)), cut
+
+
+@pytest.mark.parametrize("dt,H,I,E,k,rows", [
+    ((O.Q4_K,) * 3, 512, 2304, 4, 2, 3),             # down in two K parts: 2048 + 256
+    ((O.Q8_0,) * 3, 256, 2080, 4, 2, 5),             # 65 Q8_0 blocks a row: parts of 2048 + 32
+    ((O.Q4_K, O.Q4_K, O.Q8_0), 256, 6144, 3, 2, 9),  # three full parts, 9 tokens (two passes of 8)
+    ((O.Q4_K,) * 3, 256, 512, 24, 20, 2),            # 20 pairs a token: the f32-h path
+    ((O.Q4_K,) * 3, 256, 256, 16, 8, 80),            # 640 pairs: the f32-h path
+])
+def test_k_parts_and_large_calls(gpu, dt, H, I, E, k, rows):
+    """The down projection split into K parts of 2048 (a short last part, odd Q8_0
+    block counts, token passes), and the calls past the staged path's limits."""
+    nm = gpu
+    g, u, d, r = S.layer(2300 + I + rows, E, H, I, dt)
+    x = S.activations_bf16(2300 + rows, rows, H)
+    ids, w = O.topk(O.router_logits(O.from_bf16(x), r), k)
+    print(f"[k parts H={H} I={I} E={E} k={k} rows={rows}]", flush=True)
+    got = run_decode(nm, g, u, d, dt, H, I, x, ids, w)
+    want = oracle_decode(g, u, d, dt, H, I, x, ids, w)
+    err = S.max_rel_err(got, want)
+    print(f"  max_rel_err={err:.3e}", flush=True)
+    assert err < TOL
+
+
+@pytest.mark.parametrize("dt,H,I,E,k,rows,x_f32,act", [
+    ((O.Q8_0,) * 3, 512, 256, 4, 2, 40, False, 0),            # ~20 tokens a slot: two 16-token chunks
+    ((O.Q4_K,) * 3, 256, 512, 3, 2, 33, True, 0),             # f32 activations, three chunks
+    ((O.Q4_K, O.Q4_K, O.Q8_0), 512, 384, 6, 3, 12, False, 1),  # GELU(tanh), mixed formats
+    ((O.Q8_0, O.Q8_0, O.Q4_K), 384, 2304, 5, 2, 7, False, 0),  # Q4_K down in two K parts
+])
+def test_matrix_core_decode(gpu, dt, H, I, E, k, rows, x_f32, act):
+    """Calls of 4 or more rows run their expert GEMMs on the matrix cores (f16
+    operands, f32 accumulation): every format pairing, tokens past one 16-token
+    tile, K parts of the down projection, f32 input and both activations."""
+    nm = gpu
+    g, u, d, r = S.layer(2500 + rows, E, H, I, dt)
+    x = S.activations_bf16(2500 + rows, rows, H)
+    ids, w = O.topk(O.router_logits(O.from_bf16(x), r), k)
+    print(f"[mfma decode dt={dt} H={H} I={I} rows={rows} act={act}]", flush=True)
+    got = run_decode(nm, g, u, d, dt, H, I, x, ids, w, act=act, x_f32=x_f32)
+    if act == 0:
+        want = oracle_decode(g, u, d, dt, H, I, x, ids, w)
+    else:
+        G = O.dequantize_f64(dt[0], g, H).reshape(E, I, H)
+        U = O.dequantize_f64(dt[1], u, H).reshape(E, I, H)
+        D = O.dequantize_f64(dt[2], d, I).reshape(E, H, I)
+        xf = O.from_bf16(x).astype(np.float64)
+        want = np.zeros((rows, H))
+        for t in range(rows):
+            for j in range(k):
+                e = ids[t, j]
+                gx = G[e] @ xf[t]
+                gel = 0.5 * gx * (1 + np.tanh(np.sqrt(2 / np.pi) * (gx + 0.044715 * gx ** 3)))
+                want[t] += w[t, j] * (D[e] @ (gel * (U[e] @ xf[t])))
+    err = S.max_rel_err(got, want)
+    print(f"  max_rel_err={err:.3e}", flush=True)
+    assert err < TOL
+    assert nm.prefill_status() == 0   # no activation left the f16 range
+
+
+def test_matrix_core_decode_accumulates(gpu):
+    """NAIWA_DECODE_ACCUMULATE on the matrix-core path adds to out's values."""
+    nm = gpu
+    dt = (O.Q4_K,) * 3
+    H, I, E, k, rows = 256, 256, 4, 2, 9
+    g, u, d, r = S.layer(2600, E, H, I, dt)
+    banks = nm.LayerBanks(E, H, I, dt)
+    for e in range(E):
+        banks.load(e, g[e], u[e], d[e])
+    x = S.activations_bf16(2601, rows, H)
+    ids, w = O.topk(O.router_logits(O.from_bf16(x), r), k)
+    start = np.linspace(-1, 1, rows * H, dtype=np.float32).reshape(rows, H)
+    out = nm.DeviceBuffer.from_array(start)
+    nm.indexed_moe_fused_decode(banks, nm.DeviceBuffer.from_array(x), nm.BF16,
+                                nm.DeviceBuffer.from_array(ids.astype(np.uint32)),
+                                nm.DeviceBuffer.from_array(w), rows, k, out, accumulate=True)
+    nm.synchronize()
+    got = out.download(np.float32).reshape(rows, H) - start
+    assert S.max_rel_err(got, oracle_decode(g, u, d, dt, H, I, x, ids, w)) < TOL

@@ -72,7 +72,7 @@ def test_noalloc_rejects_requests_past_its_scratch(gpu):
     H, I, k = 256, 14336, 2
     dt = (O.Q8_0,) * 3
     banks = nm.LayerBanks(2, H, I, dt)
-    rows = 80     # 160 pairs x 14336 x 4 B of h: past the 8 MiB array
+    rows = 128    # 256 pairs: h (30 KB a pair) and the K parts' dots pass the 8 MiB array
     xd = nm.DeviceBuffer(rows * H * 2)
     ids_d = nm.DeviceBuffer.from_array(np.zeros((rows, k), np.uint32))
     w_d = nm.DeviceBuffer.from_array(np.zeros((rows, k), np.float32))
