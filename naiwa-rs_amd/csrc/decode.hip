@@ -203,6 +203,7 @@ constexpr int kDownThreads = 256;
 constexpr int kSplitK = 2048;     // I elements per K part of the down projection
 constexpr int kCombineWidth = 16; // most pairs per token the combine orders
 constexpr int kCombineTok = 4;    // tokens per combine wave
+constexpr int kCombineParts = 8;  // K parts whose loads a combine lane issues at once
 
 // The staged-h path serves calls of at most kPairsMax pairs and kCombineWidth per token.
 bool split_path(int n, int width) { return n <= kPairsMax && width <= kCombineWidth; }
@@ -443,9 +444,18 @@ down_combine_kernel(const float* dpart, int kparts, int n, int H, int rows, int 
         float acc = accumulate ? out[o] : 0.0f;
         for (int k = 0; k < cnt[tt]; ++k) {
             const int pos = list[tt][k];
-            float v = dpart[(size_t)pos * H + r];
-            for (int kp = 1; kp < kparts; ++kp) v += dpart[((size_t)kp * n + pos) * H + r];
-            acc += w[perm[pos]] * v;
+            const float wp = w[perm[pos]];
+            float v = 0.0f;
+            for (int k0 = 0; k0 < kparts; k0 += kCombineParts) {
+                float pv[kCombineParts];
+#pragma unroll
+                for (int i = 0; i < kCombineParts; ++i)
+                    if (k0 + i < kparts) pv[i] = dpart[((size_t)(k0 + i) * n + pos) * H + r];
+#pragma unroll
+                for (int i = 0; i < kCombineParts; ++i)
+                    if (k0 + i < kparts) v = (k0 + i == 0) ? pv[i] : v + pv[i];
+            }
+            acc += wp * v;
         }
         out[o] = acc;
     }

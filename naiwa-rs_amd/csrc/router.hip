@@ -9,33 +9,52 @@
 // chunks over threads (or over the blocks of the fused stack kernel) yields
 // the same bits as the CPU oracle.  Top-k orders by (logit desc, id asc), the
 // tie rule of top_k_ids (src/moe/cached_layer.rs:357-363).
+#include <algorithm>
+
 #include "common.h"
 #include "router.h"
 
 namespace {
 
 constexpr int kLogitThreads = 256;
-constexpr int kLogitRows = 16; // rows per block: 4 per wave
+constexpr int kLogitPer = 4; // chunk loads a thread issues before using any
 
-// logits[t, e] for expert e = blockIdx.x and rows blockIdx.y * 16 + 0..15, one
-// wave per row at a time: lane l takes the 8-feature chunks l, l + 64, ...  The
-// chunk values are int64 fixed point, so their sum is the same in any order.
+// logits[t, e] for expert e = blockIdx.x and rows t = blockIdx.y, + gridDim.y, ...: thread i takes the
+// 8-feature chunks i, i + 256, ..., issuing up to kLogitPer chunks' loads at once;
+// the waves' sums meet in LDS.  The chunk values are int64 fixed point, so their
+// sum is the same in any order.
 __global__ void __launch_bounds__(kLogitThreads)
 router_logits_kernel(const void* x, int x_bf16, const float* W, const float* bias, int rows, int H, int E,
                      float* logits) {
-    const int e = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ long long part[kLogitThreads / 64];
+    const int e = blockIdx.x, tid = threadIdx.x;
     const int nchunks = H / NAIWA_ROUTER_CHUNK;
     const float* wr = W + (int64_t)e * H;
-    const int t0 = blockIdx.y * kLogitRows;
-    for (int t = t0 + wave; t < min(rows, t0 + kLogitRows); t += kLogitThreads / 64) {
+    for (int t = blockIdx.y; t < rows; t += gridDim.y) {
         long long acc = 0;
-        for (int c = lane; c < nchunks; c += 64) {
-            float xv[8];
-            naiwa_load_x8(x, x_bf16, (int64_t)t * H + 8 * c, xv);
-            acc += naiwa_router_chunk(wr + 8 * c, xv);
+        for (int c0 = tid; c0 < nchunks; c0 += kLogitThreads * kLogitPer) {
+            float xv[kLogitPer][8];
+#pragma unroll
+            for (int i = 0; i < kLogitPer; ++i) {
+                const int c = c0 + kLogitThreads * i;
+                if (c < nchunks) naiwa_load_x8(x, x_bf16, (int64_t)t * H + 8 * c, xv[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < kLogitPer; ++i) {
+                const int c = c0 + kLogitThreads * i;
+                if (c < nchunks) acc += naiwa_router_chunk(wr + 8 * c, xv[i]);
+            }
         }
         acc = naiwa_wave_sum_i64(acc);
-        if (lane == 0) logits[(int64_t)t * E + e] = naiwa_router_fix_to_f32(acc) + (bias ? bias[e] : 0.0f);
+        if ((tid & 63) == 0) part[tid >> 6] = acc;
+        __syncthreads();
+        if (tid == 0) {
+            long long sum = 0;
+#pragma unroll
+            for (int i = 0; i < kLogitThreads / 64; ++i) sum += part[i];
+            logits[(int64_t)t * E + e] = naiwa_router_fix_to_f32(sum) + (bias ? bias[e] : 0.0f);
+        }
+        __syncthreads(); // part is reused by the next row
     }
 }
 
@@ -78,7 +97,7 @@ extern "C" int naiwa_router_topk_biased(const void* x, int x_dtype, const float*
         logits = (float*)naiwa_scratch(NAIWA_SCRATCH_ROUTER, (size_t)rows * E * 4, &rc);
         if (!logits) return rc;
     }
-    const dim3 lg((unsigned)E, (unsigned)((rows + kLogitRows - 1) / kLogitRows));
+    const dim3 lg((unsigned)E, (unsigned)std::min(rows, 65535));
     router_logits_kernel<<<lg, kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, W, bias, rows, H, E, logits);
     router_topk_kernel<<<rows, kTopkThreads, 0, st>>>(logits, E, k, mode, ids_out, w_out);
     return naiwa_hip_rc(hipGetLastError());
