@@ -501,21 +501,14 @@ def run_cache25(args) -> int:
     ahead_tot = {"loads": 0, "swaps": 0, "predicted": 0, "resident": 0}
 
     def step(i: int) -> dict:
-        tot = {"hits": 0, "staged": 0, "staged_experts": 0, "promoted": 0, "pcie_bytes": 0}
         lib.naiwa_memcpy_d2d(x.ptr, xs.ptr + i * rows * H * 2, rows * H * 2, compute.handle)
-        for l, layer in enumerate(layers):
-            if swaps >= 0 and l + 1 < L:
-                # the next layer's experts predicted from this layer's activation
-                info, ahead = layer.forward_ahead(layers[l + 1], x, rows, y, lookahead_swaps=swaps, pcie_frac=1.0,
-                                                  promote_cap=1, min_hits=4, stream=compute.handle)
-                for k_ in ahead_tot:
-                    ahead_tot[k_] += ahead[k_]
-            else:
-                info = layer.forward(x, rows, y, pcie_frac=1.0, promote_cap=1, min_hits=4, stream=compute.handle)
-            nm._lib.check(lib.naiwa_residual_add_bf16(x.ptr, y.ptr, rows * H, compute.handle), "residual")
-            for k_ in tot:
-                tot[k_] += info[k_]
-        return tot
+        # every layer's partial-cache step and residual in order (with swaps >= 0 each layer
+        # also predicts the next layer's experts from its activation and loads them)
+        info, ahead = nm.policy.CachedLayer.stack_forward(layers, x, rows, y, pcie_frac=1.0, promote_cap=1,
+                                                          min_hits=4, lookahead_swaps=swaps, stream=compute.handle)
+        for k_ in ahead_tot:
+            ahead_tot[k_] += ahead[k_]
+        return {k_: info[k_] for k_ in ("hits", "staged", "staged_experts", "promoted", "pcie_bytes")}
 
     for i in range(warmup):
         step(i)

@@ -137,6 +137,19 @@ int naiwa_cached_layer_forward_ahead(naiwa_cached_layer* L, naiwa_cached_layer* 
                                      uint64_t min_hits, int64_t stream, naiwa_cached_step* info,
                                      naiwa_lookahead_step* ahead);
 
+/* One decode step through a stack of cached layers, in order: for each layer the
+ * partial-cache step (naiwa_cached_layer_forward) on x bf16 [rows, H] into y f32
+ * [rows, H], then x = bf16(x + y) (naiwa_residual_add_bf16), all on `stream`.
+ * With lookahead_swaps >= 0 every layer but the last also predicts and loads the
+ * next layer's experts (naiwa_cached_layer_forward_ahead).  No counterpart in the
+ * reference, where the model's own layer loop calls each layer's forward
+ * (src/moe/cached_layer.rs:524-531): a host that drives the layers itself calls the
+ * per-layer entry points.  Every layer has the same hidden size.  *total sums the
+ * layers' step reports and *ahead_total their lookahead reports (either may be NULL). */
+int naiwa_cached_stack_forward(naiwa_cached_layer* const* layers, int n_layers, void* x, int rows, float* y,
+                               float pcie_frac, int promote_cap, uint64_t min_hits, int lookahead_swaps,
+                               int64_t stream, naiwa_cached_step* total, naiwa_lookahead_step* ahead_total);
+
 /* The last lookahead's prediction for this layer, in vote order. */
 int naiwa_cached_layer_predicted(const naiwa_cached_layer* L, uint32_t* ids, int capacity, int* n_out);
 

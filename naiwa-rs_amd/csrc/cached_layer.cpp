@@ -634,6 +634,42 @@ int naiwa_cached_layer_prefetch(naiwa_cached_layer* next, const void* x, int row
     return next->prefetch_apply(next->pred_ids_h, lookahead_swaps, info);
 }
 
+int naiwa_cached_stack_forward(naiwa_cached_layer* const* layers, int n_layers, void* x, int rows, float* y,
+                               float pcie_frac, int promote_cap, uint64_t min_hits, int lookahead_swaps,
+                               int64_t stream, naiwa_cached_step* total, naiwa_lookahead_step* ahead_total) {
+    if (!layers || n_layers <= 0 || !x || !y || rows <= 0) return NAIWA_E_INVALID;
+    const int H = layers[0] ? layers[0]->d.hidden : 0;
+    for (int l = 0; l < n_layers; ++l)
+        if (!layers[l] || layers[l]->d.hidden != H) return NAIWA_E_INVALID;
+    if (total) *total = naiwa_cached_step{};
+    if (ahead_total) *ahead_total = naiwa_lookahead_step{};
+    for (int l = 0; l < n_layers; ++l) {
+        naiwa_cached_step s{};
+        naiwa_lookahead_step a{};
+        const bool ahead = lookahead_swaps >= 0 && l + 1 < n_layers;
+        int rc = forward_impl(layers[l], ahead ? layers[l + 1] : nullptr, ahead ? lookahead_swaps : 0, x, rows, y,
+                              pcie_frac, promote_cap, min_hits, stream, &s, ahead ? &a : nullptr);
+        if (!rc) rc = naiwa_residual_add_bf16(x, y, (int64_t)rows * H, stream);
+        if (rc) return rc;
+        if (total) {
+            total->hits += s.hits;
+            total->staged += s.staged;
+            total->staged_experts += s.staged_experts;
+            total->promoted += s.promoted;
+            total->pcie_bytes += s.pcie_bytes;
+            total->preload_waits += s.preload_waits;
+        }
+        if (ahead_total && ahead) {
+            ahead_total->predicted += a.predicted;
+            ahead_total->resident += a.resident;
+            ahead_total->loads += a.loads;
+            ahead_total->swaps += a.swaps;
+            ahead_total->pcie_bytes += a.pcie_bytes;
+        }
+    }
+    return NAIWA_OK;
+}
+
 int naiwa_cached_layer_predicted(const naiwa_cached_layer* L, uint32_t* ids, int capacity, int* n_out) {
     if (!L || !n_out || (capacity > 0 && !ids)) return NAIWA_E_INVALID;
     const int n = (int)L->predicted.size();

@@ -209,6 +209,8 @@ SIGNATURES: dict[str, tuple] = {
                                                _P(LookaheadStep)]),
     "naiwa_cached_layer_prefetch": (i32, [vp, vp, i32, i32, i64, _P(LookaheadStep)]),
     "naiwa_cached_layer_predicted": (i32, [vp, vp, i32, _P(i32)]),
+    "naiwa_cached_stack_forward": (i32, [vp, i32, vp, i32, vp, f32, i32, u64, i32, i64, _P(CachedStep),
+                                         _P(LookaheadStep)]),
     # include/naiwa_policy.h (host only)
     "naiwa_cache_create": (i32, [i32, i32, i32, _P(vp)]),
     "naiwa_cache_destroy": (i32, [vp]),

@@ -232,6 +232,21 @@ class CachedLayer:
               "cached_layer_prefetch")
         return {f: getattr(ahead, f) for f, _ in LookaheadStep._fields_}
 
+    @staticmethod
+    def stack_forward(layers: list["CachedLayer"], x, rows: int, y, pcie_frac: float = 1.0, promote_cap: int = 1,
+                      min_hits: int = 4, lookahead_swaps: int = -1, stream: int = 0) -> tuple[dict, dict]:
+        """One decode step through the layers in order (naiwa_cached_stack_forward): each layer's
+        partial-cache step on x into y, then x = bf16(x + y); lookahead_swaps >= 0 adds the
+        lookahead.  Returns the summed step and lookahead reports."""
+        from .ops import _dev
+        arr = (C.c_void_p * len(layers))(*[layer._h.value for layer in layers])
+        info, ahead = CachedStep(), LookaheadStep()
+        check(lib().naiwa_cached_stack_forward(arr, len(layers), _dev(x), rows, _dev(y), pcie_frac, promote_cap,
+                                               min_hits, lookahead_swaps, stream, C.byref(info), C.byref(ahead)),
+              "cached_stack_forward")
+        return ({f: getattr(info, f) for f, _ in CachedStep._fields_},
+                {f: getattr(ahead, f) for f, _ in LookaheadStep._fields_})
+
     def predicted(self) -> list[int]:
         out = np.empty(max(self.cache.num_experts, 1), dtype=np.uint32)
         n = C.c_int()

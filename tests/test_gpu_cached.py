@@ -468,3 +468,53 @@ def test_cached_qwen3_shape_zipf(gpu):
     assert tot["staged"] > 0 and tot["promoted"] > 0, tot
     for layer, banks, stacks in layers:
         check_resident_bytes(layer, banks, stacks)
+
+
+@pytest.mark.parametrize("swaps", [-1, 2])
+def test_cached_stack_forward_matches_the_layer_calls(gpu, swaps):
+    """naiwa_cached_stack_forward runs each layer's step and residual in order: the
+    same routing, staging, promotions, lookahead and x bits as calling every layer's
+    forward (or forward_ahead) and the residual add one by one."""
+    nm = gpu
+    E, H, I, k, usable, rows, L, steps = 16, 256, 256, 4, 4, 2, 3, 4
+    stream = nm.Stream()
+    runs = []
+    for driver in ("layers", "stack"):
+        copy = nm.Stream()
+        ring = nm.policy.StagingRing()
+        built = [make_layer(nm, 1500 + l, E, H, I, k, usable, ring, copy) for l in range(L)]
+        layers = [b[0] for b in built]
+        for layer in layers:
+            layer.seed(list(range(usable)))
+        x = nm.DeviceBuffer.from_array(S.activations_bf16(1510, rows, H))
+        y = nm.DeviceBuffer(rows * H * 4)
+        reports = []
+        for _ in range(steps):
+            if driver == "stack":
+                info, ahead = nm.policy.CachedLayer.stack_forward(layers, x, rows, y, lookahead_swaps=swaps,
+                                                                  stream=stream.handle)
+            else:
+                info = {"hits": 0, "staged": 0, "staged_experts": 0, "promoted": 0, "pcie_bytes": 0,
+                        "preload_waits": 0}
+                ahead = {"predicted": 0, "resident": 0, "loads": 0, "swaps": 0, "pcie_bytes": 0}
+                for l, layer in enumerate(layers):
+                    if swaps >= 0 and l + 1 < L:
+                        s, a = layer.forward_ahead(layers[l + 1], x, rows, y, lookahead_swaps=swaps,
+                                                   stream=stream.handle)
+                        for f in ahead:
+                            ahead[f] += a[f]
+                    else:
+                        s = layer.forward(x, rows, y, stream=stream.handle)
+                    for f in info:
+                        info[f] += s[f]
+                    nm._lib.check(nm.lib().naiwa_residual_add_bf16(x.ptr, y.ptr, rows * H, stream.handle),
+                                  "residual")
+            reports.append((info, ahead if swaps >= 0 else None))
+        stream.sync()
+        runs.append((x.download(np.uint16), reports, [layer.cache.slot_table().tolist() for layer in layers]))
+        del built, layers
+    (xa, ra, sa), (xb, rb, sb) = runs
+    assert ra == rb
+    assert sa == sb
+    assert np.array_equal(xa, xb)
+    assert any(r[0]["staged"] for r in ra)   # the run stages misses
