@@ -327,11 +327,86 @@ struct Bank {
     int64_t row_bytes;
 };
 
+// The K loop of one tile: acc[ms] += A (64 rows staged through the LDS double buffer
+// `as`) x B (this lane's share of weight row `wrow`), K-blocks 0 .. nkb - 1.  The next
+// K-block's loads are issued before the current one is used; the last K-block reloads
+// itself, so the loads are unconditional and the compiler waits only for the registers
+// each step uses.
+template <int DT>
+__device__ __forceinline__ void tile_k_loop(const uint16_t* abase, const int* rows, const uint8_t* wrow, int nkb,
+                                            ATile<DT>* as, int tid, int lane, int h, floatx16* acc) {
+    AStage<DT> st;
+    if constexpr (DT == NAIWA_Q4_K) {
+        // Rolling prefetch: chunk c of the next K-block replaces chunk c of the current one
+        // as soon as its four steps are done, and the next header waits beside the current
+        // one, so a lane holds one K-block of weights (plus a header) instead of two.  At
+        // most 128 VGPRs then, two 8-wave blocks fit on a CU.
+        BRow<DT> b;
+        st.load(abase, rows, 0, tid);
+        b.load(wrow, 0, h);
+        st.store(as[0], tid);
+        __syncthreads();
+        for (int kb = 0; kb < nkb; ++kb) {
+            const int kn = min(kb + 1, nkb - 1);
+            const uint8_t* nblk = wrow + (size_t)kn * NAIWA_Q4_K_BYTES;
+            st.load(abase, rows, kn, tid);
+            const u32x4 hd_next = *reinterpret_cast<const u32x4*>(nblk);
+            const ATile<DT>& a = as[kb & 1];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int s = 4 * c + t;
+                    const half8 wv = b.step(s);
+#pragma unroll
+                    for (int ms = 0; ms < 2; ++ms) {
+                        const half8 x8 = __builtin_bit_cast(half8, a.at(2 * s + h, 32 * ms + (lane & 31)));
+                        acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x8, wv, acc[ms], 0, 0, 0);
+                    }
+                }
+                b.q[c] = *reinterpret_cast<const u32x4*>(nblk + 16 + 32 * c + 16 * h);
+            }
+            b.hd = hd_next;
+            st.store(as[(kb + 1) & 1], tid);
+            __syncthreads();
+        }
+    } else {
+        BRow<DT> b0, b1; // this K-block's row share and the next one's, alternating
+        st.load(abase, rows, 0, tid);
+        b0.load(wrow, 0, h);
+        st.store(as[0], tid);
+        __syncthreads();
+        auto block = [&](int kb, const BRow<DT>& bw, BRow<DT>& nw) {
+            const int kn = min(kb + 1, nkb - 1);
+            st.load(abase, rows, kn, tid);
+            nw.load(wrow, kn, h);
+            const ATile<DT>& a = as[kb & 1];
+#pragma unroll
+            for (int s = 0; s < KBlock<DT>::kSteps; ++s) {
+                const half8 wv = bw.step(s);
+#pragma unroll
+                for (int ms = 0; ms < 2; ++ms) {
+                    const half8 x8 = __builtin_bit_cast(half8, a.at(2 * s + h, 32 * ms + (lane & 31)));
+                    acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x8, wv, acc[ms], 0, 0, 0);
+                }
+            }
+            st.store(as[(kb + 1) & 1], tid);
+            __syncthreads();
+        };
+        int kb = 0;
+        for (; kb + 2 <= nkb; kb += 2) {
+            block(kb, b0, b1);
+            block(kb + 1, b1, b0);
+        }
+        if (kb < nkb) block(kb, b0, b1);
+    }
+}
+
 // gate/up: one tile of <= 64 pairs x 128 intermediate features; waves 0-3 the
 // gate rows, waves 4-7 the up rows of the same 4 x 32 features.  xp: x in the K
 // order of DG; hp (out): h in the K order of DD, f16 [pairs, I].
 template <int DG, int DD>
-__global__ void __launch_bounds__(kGemm, 2)
+__global__ void __launch_bounds__(kGemm, 4)
 gateup_kernel(Bank gate, Bank up, const uint16_t* xp, int H, int I, int k, const uint32_t* perm, Tiles tl,
               int act, uint16_t* hp) {
     __shared__ ATile<DG> as[2];
@@ -348,38 +423,8 @@ gateup_kernel(Bank gate, Bank up, const uint16_t* xp, int H, int I, int k, const
     const int nkb = H / KBlock<DG>::kVals;
     __syncthreads();
 
-    AStage<DG> st;
-    BRow<DG> b0, b1; // this K-block's row share and the next one's, alternating
-    st.load(xp, rows, 0, tid);
-    b0.load(wrow, 0, h);
-    st.store(as[0], tid);
-    __syncthreads();
     floatx16 acc[2] = {}; // [m subtile]
-    // one K-block; the next block's loads are unconditional (the last block reloads
-    // itself) so the compiler can count them and wait only for this block's registers
-    auto block = [&](int kb, const BRow<DG>& bw, BRow<DG>& nw) {
-        const int kn = min(kb + 1, nkb - 1);
-        st.load(xp, rows, kn, tid);
-        nw.load(wrow, kn, h);
-        const ATile<DG>& a = as[kb & 1];
-#pragma unroll
-        for (int s = 0; s < KBlock<DG>::kSteps; ++s) {
-            const half8 wv = bw.step(s);
-#pragma unroll
-            for (int ms = 0; ms < 2; ++ms) {
-                const half8 x8 = __builtin_bit_cast(half8, a.at(2 * s + h, 32 * ms + (lane & 31)));
-                acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x8, wv, acc[ms], 0, 0, 0);
-            }
-        }
-        st.store(as[(kb + 1) & 1], tid);
-        __syncthreads();
-    };
-    int kb = 0;
-    for (; kb + 2 <= nkb; kb += 2) {
-        block(kb, b0, b1);
-        block(kb + 1, b1, b0);
-    }
-    if (kb < nkb) block(kb, b0, b1);
+    tile_k_loop<DG>(xp, rows, wrow, nkb, as, tid, lane, h, acc);
     // epilogue: the gate waves hand act(g) to the up waves of the same strip through
     // LDS (the A tiles are no longer read); h = act(g) * u as f16 at its laid-out
     // position for the down format
@@ -413,7 +458,7 @@ gateup_kernel(Bank gate, Bank up, const uint16_t* xp, int H, int I, int k, const
 // down: one tile of <= 64 pairs x 256 output features (32 per wave); pair rows
 // scaled by their weight.
 template <int DD>
-__global__ void __launch_bounds__(kGemm, 2)
+__global__ void __launch_bounds__(kGemm, 4)
 down_kernel(Bank down, const uint16_t* hp, int H, int I, const uint32_t* perm, const float* w, Tiles tl,
             float* ypair) {
     __shared__ ATile<DD> as[2];
@@ -428,36 +473,8 @@ down_kernel(Bank down, const uint16_t* hp, int H, int I, const uint32_t* perm, c
     const int nkb = I / KBlock<DD>::kVals;
     __syncthreads();
 
-    AStage<DD> st;
-    BRow<DD> d0, d1;
-    st.load(hp, rows, 0, tid);
-    d0.load(drow, 0, h);
-    st.store(as[0], tid);
-    __syncthreads();
     floatx16 acc[2] = {};
-    auto block = [&](int kb, const BRow<DD>& bd, BRow<DD>& nd) {
-        const int kn = min(kb + 1, nkb - 1);
-        st.load(hp, rows, kn, tid);
-        nd.load(drow, kn, h);
-        const ATile<DD>& a = as[kb & 1];
-#pragma unroll
-        for (int s = 0; s < KBlock<DD>::kSteps; ++s) {
-            const half8 wd = bd.step(s);
-#pragma unroll
-            for (int ms = 0; ms < 2; ++ms) {
-                const half8 h8 = __builtin_bit_cast(half8, a.at(2 * s + h, 32 * ms + (lane & 31)));
-                acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h8, wd, acc[ms], 0, 0, 0);
-            }
-        }
-        st.store(as[(kb + 1) & 1], tid);
-        __syncthreads();
-    };
-    int kb = 0;
-    for (; kb + 2 <= nkb; kb += 2) {
-        block(kb, d0, d1);
-        block(kb + 1, d1, d0);
-    }
-    if (kb < nkb) block(kb, d0, d1);
+    tile_k_loop<DD>(hp, rows, drow, nkb, as, tid, lane, h, acc);
 #pragma unroll
     for (int ms = 0; ms < 2; ++ms)
 #pragma unroll

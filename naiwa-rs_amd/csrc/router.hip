@@ -17,9 +17,32 @@
 namespace {
 
 constexpr int kLogitThreads = 256;
-constexpr int kLogitPer = 4; // chunk loads a thread issues before using any
+constexpr int kLogitPer = 4;      // chunk loads a thread issues before using any
+constexpr int kLogitRows = 16;    // rows per block of the many-row kernel: 4 per wave
+constexpr int kLogitFewRows = 32; // up to this many rows, one block per (expert, row)
 
-// logits[t, e] for expert e = blockIdx.x and rows t = blockIdx.y, + gridDim.y, ...: thread i takes the
+// logits[t, e] for many rows: expert e = blockIdx.x and rows blockIdx.y * 16 + 0..15,
+// one wave per row at a time; lane l takes the chunks l, l + 64, ...
+__global__ void __launch_bounds__(kLogitThreads)
+router_logits_rows_kernel(const void* x, int x_bf16, const float* W, const float* bias, int rows, int H, int E,
+                          float* logits) {
+    const int e = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nchunks = H / NAIWA_ROUTER_CHUNK;
+    const float* wr = W + (int64_t)e * H;
+    const int t0 = blockIdx.y * kLogitRows;
+    for (int t = t0 + wave; t < min(rows, t0 + kLogitRows); t += kLogitThreads / 64) {
+        long long acc = 0;
+        for (int c = lane; c < nchunks; c += 64) {
+            float xv[8];
+            naiwa_load_x8(x, x_bf16, (int64_t)t * H + 8 * c, xv);
+            acc += naiwa_router_chunk(wr + 8 * c, xv);
+        }
+        acc = naiwa_wave_sum_i64(acc);
+        if (lane == 0) logits[(int64_t)t * E + e] = naiwa_router_fix_to_f32(acc) + (bias ? bias[e] : 0.0f);
+    }
+}
+
+// logits[t, e] for few rows: expert e = blockIdx.x and rows t = blockIdx.y, + gridDim.y, ...: thread i takes the
 // 8-feature chunks i, i + 256, ..., issuing up to kLogitPer chunks' loads at once;
 // the waves' sums meet in LDS.  The chunk values are int64 fixed point, so their
 // sum is the same in any order.
@@ -97,8 +120,13 @@ extern "C" int naiwa_router_topk_biased(const void* x, int x_dtype, const float*
         logits = (float*)naiwa_scratch(NAIWA_SCRATCH_ROUTER, (size_t)rows * E * 4, &rc);
         if (!logits) return rc;
     }
-    const dim3 lg((unsigned)E, (unsigned)std::min(rows, 65535));
-    router_logits_kernel<<<lg, kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, W, bias, rows, H, E, logits);
+    if (rows <= kLogitFewRows) {
+        router_logits_kernel<<<dim3((unsigned)E, (unsigned)rows), kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, W,
+                                                                                          bias, rows, H, E, logits);
+    } else {
+        const dim3 lg((unsigned)E, (unsigned)((rows + kLogitRows - 1) / kLogitRows));
+        router_logits_rows_kernel<<<lg, kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, W, bias, rows, H, E, logits);
+    }
     router_topk_kernel<<<rows, kTopkThreads, 0, st>>>(logits, E, k, mode, ids_out, w_out);
     return naiwa_hip_rc(hipGetLastError());
 }
