@@ -1,6 +1,6 @@
 // The expert GEMMs of naiwa_moe_decode calls with several tokens per expert, on
 // the matrix cores (prefill.hip): x -> f16 in the 16x16x32 K order, gate/up per
-// (128 features, slot segment), down per (128 rows, K part, slot segment) into
+// (64 features, slot segment), down per (64 rows, K part, slot segment) into
 // unweighted partial dots that the decode's ordered combine adds up.
 #pragma once
 

@@ -521,8 +521,8 @@ combine_kernel(const float* ypair, const uint32_t* ids, int k, int H, int slots,
 // Multi-token decode on the matrix cores
 // ---------------------------------------------------------------------------
 // naiwa_moe_decode calls with several tokens per expert run their expert GEMMs
-// here.  A block of 8 waves takes one slot segment (the sorted pairs of one
-// slot) and 128 features; chunks of up to 16 of the segment's tokens are the A
+// here.  A block of 4 waves takes one slot segment (the sorted pairs of one
+// slot) and 64 features; chunks of up to 16 of the segment's tokens are the A
 // operand of v_mfma_f32_16x16x32_f16 and each lane dequantises its own weight
 // values once into the B operand, so a weight costs the same whatever the
 // token count.  Lane l = 16 g + m holds A[m][8 g + 0..7] (token m of the
@@ -537,9 +537,9 @@ combine_kernel(const float* ypair, const uint32_t* ids, int k, int H, int slots,
 //   Q8_0 (128 values, 4 blocks): block g; step s takes its values 8 s + 0..7.
 // The activations (x for gate/up, h for down) are stored as groups G = 4 s + g
 // of 8 f16 in that order.
-constexpr int kDecM = 16;       // tokens per MFMA tile
-constexpr int kDecThreads = 512; // 8 waves of 16 features
-constexpr int kDecF = 128;      // features (gate/up) or output rows (down) per block
+constexpr int kDecM = 16;        // tokens per MFMA tile
+constexpr int kDecThreads = 256; // 4 waves of 16 features
+constexpr int kDecF = 64;        // features (gate/up) or output rows (down) per block
 
 template <int DT> struct K16;
 template <> struct K16<NAIWA_Q4_K> {
@@ -617,21 +617,29 @@ template <int DT> struct ATile16 {
     __device__ __forceinline__ const u32x4& at(int G, int m) const { return v[G][m ^ (G & 15)]; }
 };
 
-// Thread tid's piece of one K-block of the A tile: row tid / G, group tid % G (the
-// lanes of a load cover whole rows); rows[m] < 0 is a zero row.
+// Thread tid's pieces of one K-block of the A tile: piece p = tid + kDecThreads * i is
+// row p / G, group p % G (the lanes of a load cover whole rows); rows[m] < 0 is a zero row.
 template <int DT> struct AStage16 {
-    u32x4 r;
+    static constexpr int G = ATile16<DT>::kGroups;
+    static constexpr int kPer = (G * kDecM + kDecThreads - 1) / kDecThreads;
+    u32x4 r[kPer];
     __device__ __forceinline__ void load(const uint16_t* base, const int* rows, int kb, int tid) {
-        constexpr int G = ATile16<DT>::kGroups;
-        r = u32x4{0u, 0u, 0u, 0u};
-        if (tid < G * kDecM) {
-            const int ro = rows[tid / G];
-            if (ro >= 0) r = *reinterpret_cast<const u32x4*>(base + ro + kb * K16<DT>::kVals + 8 * (tid % G));
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int p = tid + kDecThreads * i;
+            r[i] = u32x4{0u, 0u, 0u, 0u};
+            if (p < G * kDecM) {
+                const int ro = rows[p / G];
+                if (ro >= 0) r[i] = *reinterpret_cast<const u32x4*>(base + ro + kb * K16<DT>::kVals + 8 * (p % G));
+            }
         }
     }
     __device__ __forceinline__ void store(ATile16<DT>& a, int tid) const {
-        constexpr int G = ATile16<DT>::kGroups;
-        if (tid < G * kDecM) a.at(tid % G, tid / G) = r;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int p = tid + kDecThreads * i;
+            if (p < G * kDecM) a.at(p % G, p / G) = r[i];
+        }
     }
 };
 
@@ -718,7 +726,7 @@ __device__ __forceinline__ void dec_chunk(const uint16_t* abase, const int* rows
     if (j < nkb) block(j, cur, nxt);
 }
 
-// gate/up: block (128 features, slot segment); h = act(gate) * up as f16 at the
+// gate/up: block (64 features, slot segment); h = act(gate) * up as f16 at the
 // pair's sorted position, in the 16x16x32 K order of DD.
 template <int DG, int DD>
 __global__ void __launch_bounds__(kDecThreads, 2)
@@ -755,7 +763,7 @@ dec_gateup_kernel(Bank gate, Bank up, const uint16_t* xl, int H, int I, int widt
     count_clamped(clamped);
 }
 
-// down: block (128 output rows, K part, slot segment); the unweighted partial dot of
+// down: block (64 output rows, K part, slot segment); the unweighted partial dot of
 // (K part, sorted position, row) into dpart.
 template <int DD>
 __global__ void __launch_bounds__(kDecThreads, 2)
