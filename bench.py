@@ -76,7 +76,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--rows", type=int, default=1, help="decode batch (tokens per step)")
     ap.add_argument("--layers", type=int, default=48)
-    ap.add_argument("--path", choices=["fused", "layered"], default="fused")
+    ap.add_argument("--path", choices=["auto", "fused", "layered"], default="auto",
+                    help="auto: the fused persistent kernel below 4 rows, per-layer launches (matrix-core "
+                         "expert GEMMs) from 4 rows on")
     ap.add_argument("--blocks-per-cu", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="budget of the CPU-baseline sample")
@@ -157,6 +159,8 @@ def main() -> int:
     x = nm.DeviceBuffer(rows * H * 2)
     ids_d = nm.DeviceBuffer(L * rows * K * 4)
     w_d = nm.DeviceBuffer(L * rows * K * 4)
+    if args.path == "auto":
+        args.path = "fused" if rows < 4 else "layered"
     fused = args.path == "fused"
     lib = nm.lib()
 

@@ -197,6 +197,16 @@ down_kernel(BankArg down, int H, int I, int rows, int width, int tok_max, const 
 // down_split + down_combine: the down rows' dots over K parts of I with the h
 // slices staged in LDS (below), then the ordered per-(token, row) combine.
 constexpr int kPairsMax = 512;
+constexpr int kSmallSeg = 64; // calls of at most this many pairs are segmented inside gate/up
+
+// The call's (slot, weight) pairs when gate/up segments them itself (slot_ids null:
+// the segments launch has run).
+struct SegIn {
+    const uint32_t* slot_ids;
+    const float* w;
+    int n, nslots;
+    int* bad;
+};
 constexpr int kTokG = 8;
 constexpr int kTokD = 8;
 constexpr int kDownThreads = 256;
@@ -224,11 +234,29 @@ template <int DG, int DD>
 __global__ void __launch_bounds__(512)
 gate_up_staged_kernel(BankArg gate, BankArg up, const void* x, int x_bf16, int H, int I, int width, int tok_max,
                       const int* seg_count, const uint32_t* seg_key, const uint32_t* seg_begin,
-                      const uint32_t* perm, int act, uint8_t* hst, int hst_stride) {
+                      const uint32_t* perm, int act, uint8_t* hst, int hst_stride, SegIn seg_in) {
     constexpr int SPAN = Fmt<DD>::kSumSpan;   // rows per block (one group of 16 lanes each)
     constexpr int GPG = SPAN / 4;             // 4-row groups per sum
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float hloc[kTokG][SPAN];
+    __shared__ uint32_t l_perm[kSmallSeg], l_key[kSmallSeg], l_begin[kSmallSeg + 1];
+    __shared__ int l_count;
+    if (seg_in.slot_ids) {
+        // the call's few pairs segmented by this block (wave 0) into LDS; block (0, 0)'s
+        // wave 1 also writes the global copy the down launches read
+        const int wave = threadIdx.x >> 6;
+        if (wave == 0)
+            naiwa_segment_small(seg_in.slot_ids, seg_in.w, seg_in.n, seg_in.nslots, l_perm, &l_count, l_key, l_begin,
+                                nullptr);
+        else if (wave == 1 && blockIdx.x == 0 && blockIdx.y == 0)
+            naiwa_segment_small(seg_in.slot_ids, seg_in.w, seg_in.n, seg_in.nslots, (uint32_t*)perm, (int*)seg_count,
+                                (uint32_t*)seg_key, (uint32_t*)seg_begin, seg_in.bad);
+        __syncthreads();
+        seg_count = &l_count;
+        seg_key = l_key;
+        seg_begin = l_begin;
+        perm = l_perm;
+    }
     const int s = blockIdx.x;
     if (s >= *seg_count) return;
     const int tid = threadIdx.x, grp = tid / NAIWA_GROUP, lr = tid % NAIWA_GROUP;
@@ -548,7 +576,7 @@ template <int DG, int DD>
 int staged_kernels(BankArg g, BankArg u, BankArg d, const void* x, int xb, int H, int I, int rows, int width,
                    int act, const float* w, float* out, int accumulate, int n, int slots, const int* seg_count,
                    const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm, uint8_t* hst,
-                   float* dpart, hipStream_t st) {
+                   float* dpart, SegIn seg_in, hipStream_t st) {
     constexpr int SPAN = Fmt<DD>::kSumSpan;
     const int stage_g = naiwa_stage_bytes(DG, H);
     const int tok = std::max(1, std::min(kTokG, (64 * 1024) / stage_g));
@@ -557,7 +585,7 @@ int staged_kernels(BankArg g, BankArg u, BankArg d, const void* x, int xb, int H
     // and each still costs a dispatch with its full LDS reservation
     const dim3 ggrid(std::max(1, std::min(n, slots)), I / SPAN);
     gate_up_staged_kernel<DG, DD><<<ggrid, SPAN * NAIWA_GROUP, (size_t)tok * stage_g, st>>>(
-        g, u, x, xb, H, I, width, tok, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride);
+        g, u, x, xb, H, I, width, tok, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride, seg_in);
     // down: rows per group doubled while the grid keeps at least 1024 blocks
     const int ks = split_ks(I), kparts = split_parts(I);
     const int segs = std::max(1, std::min(n, slots));
@@ -575,13 +603,13 @@ int staged_kernels(BankArg g, BankArg u, BankArg d, const void* x, int xb, int H
 int staged_launch(BankArg g, BankArg u, BankArg d, int gdt, int ddt, const void* x, int x_dtype, int H, int I,
                   int rows, int width, int act, const float* w, float* out, int accumulate, int n, int slots,
                   const int* seg_count, const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm,
-                  uint8_t* hst, float* dpart, hipStream_t st) {
+                  uint8_t* hst, float* dpart, SegIn seg_in, hipStream_t st) {
     const int xb = x_dtype == NAIWA_BF16;
     const int fg = naiwa_kernel_fmt(gdt, H), fd = naiwa_kernel_fmt(ddt, I);
 #define NAIWA_STAGED(FG, FD)                                                                                       \
     if (fg == FG && fd == FD)                                                                                      \
         return staged_kernels<FG, FD>(g, u, d, x, xb, H, I, rows, width, act, w, out, accumulate, n, slots,         \
-                                      seg_count, seg_key, seg_begin, perm, hst, dpart, st);
+                                      seg_count, seg_key, seg_begin, perm, hst, dpart, seg_in, st);
     NAIWA_STAGED(NAIWA_Q4_K, NAIWA_Q4_K)
     NAIWA_STAGED(NAIWA_Q4_K, NAIWA_Q8_0)
     NAIWA_STAGED(NAIWA_Q4_K, NAIWA_Q8_0_ODD)
@@ -619,15 +647,23 @@ int decode_launch(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank
     uint32_t* perm = (uint32_t*)(ws + L.off_perm);
     float* hbuf = (float*)(ws + L.off_h);
 
-    segments_kernel<<<1, NAIWA_SEG_THREADS, 0, st>>>(slot_ids, w, n, gate->slots, perm, seg_count,
-                                                     seg_key, seg_begin, bad);
     BankArg g{(const uint8_t*)gate->base, gate->slot_stride, naiwa_row_bytes(gate->dtype, H)};
     BankArg u{(const uint8_t*)up->base, up->slot_stride, naiwa_row_bytes(up->dtype, H)};
     BankArg d{(const uint8_t*)down->base, down->slot_stride, naiwa_row_bytes(down->dtype, I)};
-    if (split_path(n, width)) {
+    const int mr = mfma_rows();
+    const bool staged = split_path(n, width);
+    const bool mfma = staged && mr > 0 && rows >= mr && naiwa_decode_mfma_ok(gate, up, down, x);
+    // a staged call of few pairs is segmented by its gate/up blocks; every other call
+    // by one segments launch first
+    SegIn seg_in{nullptr, nullptr, 0, 0, nullptr};
+    if (staged && !mfma && n <= kSmallSeg)
+        seg_in = SegIn{slot_ids, w, n, gate->slots, bad};
+    else
+        segments_kernel<<<1, NAIWA_SEG_THREADS, 0, st>>>(slot_ids, w, n, gate->slots, perm, seg_count, seg_key,
+                                                         seg_begin, bad);
+    if (staged) {
         float* dpart = (float*)(ws + L.off_dpart);
-        const int mr = mfma_rows();
-        if (mr > 0 && rows >= mr && naiwa_decode_mfma_ok(gate, up, down, x)) {
+        if (mfma) {
             const int ks = split_ks(I), segs = std::max(1, std::min(n, gate->slots));
             int rc = naiwa_decode_mfma_experts(gate, up, down, x, x_dtype, rows, width, act, n, segs, ks, seg_count,
                                                seg_key, seg_begin, perm, (uint8_t*)hbuf, dpart, st);
@@ -637,7 +673,7 @@ int decode_launch(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank
         }
         return staged_launch(g, u, d, gate->dtype, down->dtype, x, x_dtype, H, I, rows, width, act, w, out,
                              accumulate, n, gate->slots, seg_count, seg_key, seg_begin, perm, (uint8_t*)hbuf, dpart,
-                             st);
+                             seg_in, st);
     }
     const dim3 ggrid(n, (I + kRowsPerBlock - 1) / kRowsPerBlock);
     const size_t lds_g = (size_t)tok_g * naiwa_stage_bytes(gate->dtype, H);

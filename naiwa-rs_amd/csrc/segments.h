@@ -118,3 +118,55 @@ __device__ inline void naiwa_segment(NaiwaSegSmem& sm, const uint32_t* keys, con
         __syncthreads();
     }
 }
+
+// The same segmentation as naiwa_segment for at most 64 entries, by one wave with
+// no LDS scratch: lane i ranks entry i against every other entry (a stable sort by
+// key: lower key, or the same key at a lower index, comes first), so the outputs are
+// naiwa_segment's bit for bit.  Every lane of the wave calls it; the outputs are
+// written by the lanes that own them (perm[nvalid], seg_key/seg_begin[segments],
+// seg_begin[segments], seg_count, bad).
+__device__ inline void naiwa_segment_small(const uint32_t* keys, const float* weights, int n, int nkeys,
+                                           uint32_t* perm, int* seg_count, uint32_t* seg_key, uint32_t* seg_begin,
+                                           int* bad) {
+    const int lane = threadIdx.x & 63;
+    uint32_t k = 0xffffffffu; // invalid: past the keys, weight 0, or no entry
+    bool isbad = false;
+    if (lane < n) {
+        const uint32_t kk = keys[lane];
+        isbad = kk >= (uint32_t)nkeys;
+        if (!isbad && (!weights || weights[lane] != 0.0f)) k = kk;
+    }
+    const bool valid = k != 0xffffffffu;
+    // pass 1: rank among the valid entries, entries of lower keys, first occurrence
+    uint32_t pos = 0, below_key = 0, seg_below = 0;
+    bool first = valid;
+    for (int j = 0; j < n; ++j) {
+        const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)k, j);
+        if (kj == 0xffffffffu) continue;
+        if (kj < k) {
+            ++pos;
+            ++below_key;
+        } else if (kj == k && j < lane) {
+            ++pos;
+            first = false;
+        }
+    }
+    // pass 2: distinct keys below this one (first occurrences of lower keys)
+    const uint64_t fm = __ballot(first);
+    for (int j = 0; j < n; ++j)
+        if ((fm >> j) & 1ull)
+            if ((uint32_t)__builtin_amdgcn_readlane((int)k, j) < k) ++seg_below;
+    const uint64_t vmask = __ballot(valid), fmask = __ballot(first);
+    const int nvalid = __popcll(vmask), nseg = __popcll(fmask);
+    if (valid) perm[pos] = (uint32_t)lane;
+    if (first) {
+        seg_key[seg_below] = k;
+        seg_begin[seg_below] = below_key;
+    }
+    const int nbad = __popcll(__ballot(isbad));
+    if (lane == 0) {
+        seg_begin[nseg] = (uint32_t)nvalid;
+        *seg_count = nseg;
+        if (bad) *bad = nbad;
+    }
+}

@@ -283,3 +283,23 @@ def test_matrix_core_decode_accumulates(gpu):
     nm.synchronize()
     got = out.download(np.float32).reshape(rows, H) - start
     assert S.max_rel_err(got, oracle_decode(g, u, d, dt, H, I, x, ids, w)) < TOL
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3])
+def test_small_calls_segment_in_the_expert_kernel(gpu, rows):
+    """Calls of at most 64 pairs below 4 rows are grouped by slot inside the gate/up
+    launch: repeated slots in a row and across rows, weight-0 padding and permuted
+    slots give the oracle's sums."""
+    nm = gpu
+    H, I, E, width = 256, 512, 6, 5
+    dt = (O.Q4_K,) * 3
+    g, u, d, _ = S.layer(2700 + rows, E, H, I, dt, std=0.1)
+    x = S.activations_bf16(2700 + rows, rows, H)
+    ids = np.array([[2, 2, 5, 0, 3], [5, 1, 1, 4, 2], [0, 3, 3, 3, 5]], np.uint32)[:rows]
+    w = np.array([[0.3, 0.2, 0.1, 0.0, 0.4], [0.5, 0.25, 0.0, 0.15, 0.1], [0.2, 0.2, 0.2, 0.2, 0.2]],
+                 np.float32)[:rows]
+    slot_of = [3, 0, 5, 1, 4, 2]
+    slot_ids = np.vectorize(lambda e: slot_of[e])(ids).astype(np.uint32)
+    got = run_decode(nm, g, u, d, dt, H, I, x, slot_ids, w, slots_of_expert=slot_of)
+    want = oracle_decode(g, u, d, dt, H, I, x, ids, w)
+    assert S.max_rel_err(got, want) < TOL
