@@ -6,6 +6,7 @@
 // (src/moe/cached_layer.rs:1236-1300, src/moe/stages/preload.rs:18-111).
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -75,7 +76,7 @@ struct naiwa_cached_layer {
     // inputs [slot ids | weights of the cache pairs | of the staged pairs], so that each
     // crosses the link in one copy; the views below are set per step (n = rows * k)
     uint32_t* route_dev_base = nullptr;
-    uint32_t* in_dev_base = nullptr;
+    uint32_t* in_dev_base = nullptr; // device view of in_h_base (mapped, coherent host memory)
     uint32_t* in_h_base = nullptr;
     uint32_t* ids_dev = nullptr;
     float* w_dev = nullptr;
@@ -83,8 +84,8 @@ struct naiwa_cached_layer {
     uint32_t* ids_h = nullptr;
     float* w_h = nullptr;
     int32_t* slots_h = nullptr;
-    uint32_t* slots_up = nullptr;  // pinned source of the slot-id upload
-    float* wsplit_h = nullptr;     // pinned: weights of the cache pairs | of the staged pairs
+    uint32_t* slots_up = nullptr;  // host view of the step's slot ids, read by the kernels
+    float* wsplit_h = nullptr;     // host view: weights of the cache pairs | of the staged pairs
     float* wsplit_dev = nullptr;
     int last_rows = 0;
     // routing read-back doorbell: host view, device view, publishes so far
@@ -123,11 +124,10 @@ struct naiwa_cached_layer {
 
     void release_buffers() {
         if (route_dev_base) (void)hipFree(route_dev_base);
-        if (in_dev_base) (void)hipFree(in_dev_base);
         if (db_host) (void)doorbell_free_host(db_host);
         db_host = db_dev = nullptr;
         db_seq = 0;
-        if (in_h_base) (void)hipHostFree(in_h_base);
+        if (in_h_base) (void)doorbell_free_host(in_h_base);
         if (slots_h) (void)hipHostFree(slots_h);
         route_dev_base = in_dev_base = in_h_base = nullptr;
         views(0);
@@ -150,23 +150,29 @@ struct naiwa_cached_layer {
         release_buffers();
         const size_t n = (size_t)rows * d.top_k;
         void* db = nullptr;
+        void* in = nullptr;
         if (hipMalloc(&route_dev_base, 2 * n * 4) != hipSuccess ||
             doorbell_alloc_mapped(&db, (kDbHead + 3 * n) * 4) != NAIWA_OK ||
-            hipMalloc(&in_dev_base, 3 * n * 4) != hipSuccess || hipHostMalloc(&in_h_base, 3 * n * 4, 0) != hipSuccess ||
-            hipHostMalloc(&slots_h, n * 4, 0) != hipSuccess || hipMalloc(&pred_ids_dev, n * 4) != hipSuccess ||
-            hipMalloc(&pred_w_dev, n * 4) != hipSuccess || hipHostMalloc(&pred_ids_h, n * 4, 0) != hipSuccess) {
+            doorbell_alloc_mapped(&in, 3 * n * 4) != NAIWA_OK || hipHostMalloc(&slots_h, n * 4, 0) != hipSuccess ||
+            hipMalloc(&pred_ids_dev, n * 4) != hipSuccess || hipMalloc(&pred_w_dev, n * 4) != hipSuccess ||
+            hipHostMalloc(&pred_ids_h, n * 4, 0) != hipSuccess) {
             if (db) db_host = (uint32_t*)db;
+            if (in) in_h_base = (uint32_t*)in;
             release_buffers();
             return NAIWA_E_NOMEM;
         }
         db_host = (uint32_t*)db;
+        in_h_base = (uint32_t*)in;
         void* dv = nullptr;
+        void* iv = nullptr;
         doorbell_get_device_ptr(db, &dv);
-        if (!dv) {
+        doorbell_get_device_ptr(in, &iv);
+        if (!dv || !iv) {
             release_buffers();
             return NAIWA_E_DEVICE;
         }
         db_dev = (uint32_t*)dv;
+        in_dev_base = (uint32_t*)iv;
         db_seq = 0;
         cap_rows = rows;
         return NAIWA_OK;
@@ -368,8 +374,11 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     if (nc && poll && (rc = doorbell_poll_signal(L->upload_flag, ++L->upload_epoch, (int64_t)L->copy))) return rc;
     if (nc && !poll && (rc = naiwa_hip_rc(hipEventRecord(L->staged_done, L->copy)))) return rc;
 
-    // the step's inputs in one copy: slot ids and, with staged pairs, the weights of the
-    // cache pairs and of the staged pairs (adjacent after the slot ids)
+    // the step's inputs: slot ids and, with staged pairs, the weights of the cache pairs
+    // and of the staged pairs, written into mapped coherent host memory that the expert
+    // kernels read directly (no copy).  The previous step of this layer has finished
+    // reading them: its kernels precede this step's routing, whose doorbell the host
+    // waited for above.
     if (nc) {
         float* w_res = L->wsplit_h;
         float* w_stg = L->wsplit_h + n;
@@ -379,9 +388,7 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
             w_stg[i] = staged_pair ? L->w_h[i] : 0.0f;
         }
     }
-    if ((rc = naiwa_hip_rc(
-             hipMemcpyAsync(L->slots_dev, L->slots_up, (size_t)n * (nc ? 12 : 4), hipMemcpyHostToDevice, st))))
-        return rc;
+    std::atomic_thread_fence(std::memory_order_release);
     // the expert kernel after the latest lookahead claim (src/moe/cached_layer.rs:808-819):
     // a slot it published may still be in flight
     if (L->ahead_claimed) {
