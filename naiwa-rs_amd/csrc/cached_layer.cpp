@@ -48,6 +48,13 @@ routing_publish_kernel(uint32_t* db, const uint32_t* ids, const float* w, int n,
     }
 }
 
+// The step's inputs (slot ids and split weights, nwords words) from mapped host memory
+// into device memory, by one wave: a few reads over PCIe here instead of in every block
+// of the expert kernels.
+__global__ void __launch_bounds__(64) pull_inputs_kernel(uint32_t* dst, const uint32_t* src, int nwords) {
+    for (int i = threadIdx.x; i < nwords; i += 64) dst[i] = src[i];
+}
+
 // Staged-upload completion as a flag polled by one device wave (NAIWA_UPLOAD_SYNC=poll)
 // instead of an event the compute stream waits for (the default).
 bool upload_sync_poll() {
@@ -76,7 +83,8 @@ struct naiwa_cached_layer {
     // inputs [slot ids | weights of the cache pairs | of the staged pairs], so that each
     // crosses the link in one copy; the views below are set per step (n = rows * k)
     uint32_t* route_dev_base = nullptr;
-    uint32_t* in_dev_base = nullptr; // device view of in_h_base (mapped, coherent host memory)
+    uint32_t* in_dev_base = nullptr; // device copy of the step's inputs, read by the kernels
+    uint32_t* in_map_base = nullptr; // device view of in_h_base (mapped, coherent host memory)
     uint32_t* in_h_base = nullptr;
     uint32_t* ids_dev = nullptr;
     float* w_dev = nullptr;
@@ -124,6 +132,8 @@ struct naiwa_cached_layer {
 
     void release_buffers() {
         if (route_dev_base) (void)hipFree(route_dev_base);
+        if (in_dev_base) (void)hipFree(in_dev_base);
+        in_map_base = nullptr;
         if (db_host) (void)doorbell_free_host(db_host);
         db_host = db_dev = nullptr;
         db_seq = 0;
@@ -151,7 +161,7 @@ struct naiwa_cached_layer {
         const size_t n = (size_t)rows * d.top_k;
         void* db = nullptr;
         void* in = nullptr;
-        if (hipMalloc(&route_dev_base, 2 * n * 4) != hipSuccess ||
+        if (hipMalloc(&route_dev_base, 2 * n * 4) != hipSuccess || hipMalloc(&in_dev_base, 3 * n * 4) != hipSuccess ||
             doorbell_alloc_mapped(&db, (kDbHead + 3 * n) * 4) != NAIWA_OK ||
             doorbell_alloc_mapped(&in, 3 * n * 4) != NAIWA_OK || hipHostMalloc(&slots_h, n * 4, 0) != hipSuccess ||
             hipMalloc(&pred_ids_dev, n * 4) != hipSuccess || hipMalloc(&pred_w_dev, n * 4) != hipSuccess ||
@@ -172,7 +182,7 @@ struct naiwa_cached_layer {
             return NAIWA_E_DEVICE;
         }
         db_dev = (uint32_t*)dv;
-        in_dev_base = (uint32_t*)iv;
+        in_map_base = (uint32_t*)iv;
         db_seq = 0;
         cap_rows = rows;
         return NAIWA_OK;
@@ -375,10 +385,10 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     if (nc && !poll && (rc = naiwa_hip_rc(hipEventRecord(L->staged_done, L->copy)))) return rc;
 
     // the step's inputs: slot ids and, with staged pairs, the weights of the cache pairs
-    // and of the staged pairs, written into mapped coherent host memory that the expert
-    // kernels read directly (no copy).  The previous step of this layer has finished
-    // reading them: its kernels precede this step's routing, whose doorbell the host
-    // waited for above.
+    // and of the staged pairs, written into mapped coherent host memory and pulled into
+    // device memory by one wave on the compute stream.  The previous step of this layer
+    // has finished reading them: its kernels precede this step's routing, whose doorbell
+    // the host waited for above.
     if (nc) {
         float* w_res = L->wsplit_h;
         float* w_stg = L->wsplit_h + n;
@@ -389,6 +399,8 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         }
     }
     std::atomic_thread_fence(std::memory_order_release);
+    pull_inputs_kernel<<<1, 64, 0, st>>>(L->in_dev_base, L->in_map_base, n * (nc ? 3 : 1));
+    if ((rc = naiwa_hip_rc(hipGetLastError()))) return rc;
     // the expert kernel after the latest lookahead claim (src/moe/cached_layer.rs:808-819):
     // a slot it published may still be in flight
     if (L->ahead_claimed) {
