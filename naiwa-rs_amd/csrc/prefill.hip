@@ -610,35 +610,37 @@ template <> struct W16<NAIWA_Q8_0> {
 };
 
 // LDS A tile of one K-block: group G of token row m at [G][m ^ (G % 16)].
-template <int DT> struct ATile16 {
+// MT subtiles of 16 token rows (a chunk of 16 MT tokens); the XOR keeps a row in its subtile.
+template <int DT, int MT> struct ATile16 {
     static constexpr int kGroups = 4 * K16<DT>::kSteps;
-    u32x4 v[kGroups][kDecM];
+    u32x4 v[kGroups][kDecM * MT];
     __device__ __forceinline__ u32x4& at(int G, int m) { return v[G][m ^ (G & 15)]; }
     __device__ __forceinline__ const u32x4& at(int G, int m) const { return v[G][m ^ (G & 15)]; }
 };
 
 // Thread tid's pieces of one K-block of the A tile: piece p = tid + kDecThreads * i is
 // row p / G, group p % G (the lanes of a load cover whole rows); rows[m] < 0 is a zero row.
-template <int DT> struct AStage16 {
-    static constexpr int G = ATile16<DT>::kGroups;
-    static constexpr int kPer = (G * kDecM + kDecThreads - 1) / kDecThreads;
+template <int DT, int MT> struct AStage16 {
+    static constexpr int G = ATile16<DT, MT>::kGroups;
+    static constexpr int kRows = kDecM * MT;
+    static constexpr int kPer = (G * kRows + kDecThreads - 1) / kDecThreads;
     u32x4 r[kPer];
     __device__ __forceinline__ void load(const uint16_t* base, const int* rows, int kb, int tid) {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             const int p = tid + kDecThreads * i;
             r[i] = u32x4{0u, 0u, 0u, 0u};
-            if (p < G * kDecM) {
+            if (p < G * kRows) {
                 const int ro = rows[p / G];
                 if (ro >= 0) r[i] = *reinterpret_cast<const u32x4*>(base + ro + kb * K16<DT>::kVals + 8 * (p % G));
             }
         }
     }
-    __device__ __forceinline__ void store(ATile16<DT>& a, int tid) const {
+    __device__ __forceinline__ void store(ATile16<DT, MT>& a, int tid) const {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             const int p = tid + kDecThreads * i;
-            if (p < G * kDecM) a.at(p % G, p / G) = r[i];
+            if (p < G * kRows) a.at(p % G, p / G) = r[i];
         }
     }
 };
@@ -684,13 +686,14 @@ __global__ void __launch_bounds__(kThreads) dec_prep_kernel(const void* x, int x
     *reinterpret_cast<uint4*>(xl + (size_t)t * H + laid16<DT>(8 * run)) = o;
 }
 
-// The K-block loop of one 16-token chunk: NP weight rows (gate and up, or down)
-// against the A rows listed in `rows`, K-blocks kb0 .. kb0 + nkb - 1.
-template <int DT, int NP>
+// The K-block loop of one chunk of 16 MT tokens: NP weight rows (gate and up, or down)
+// against the A rows listed in `rows`, K-blocks kb0 .. kb0 + nkb - 1; each step's
+// dequantised B operand serves the MT subtiles.
+template <int DT, int NP, int MT>
 __device__ __forceinline__ void dec_chunk(const uint16_t* abase, const int* rows, const uint8_t* const* wrow,
-                                          int kb0, int nkb, ATile16<DT>* as, int tid, int g, int m,
-                                          floatx4* acc) {
-    AStage16<DT> st;
+                                          int kb0, int nkb, ATile16<DT, MT>* as, int tid, int g, int m,
+                                          floatx4 (&acc)[NP][MT]) {
+    AStage16<DT, MT> st;
     W16<DT> cur[NP], nxt[NP];
     st.load(abase, rows, kb0, tid);
 #pragma unroll
@@ -707,13 +710,19 @@ __device__ __forceinline__ void dec_chunk(const uint16_t* abase, const int* rows
         Scl c[NP];
 #pragma unroll
         for (int q = 0; q < NP; ++q) bw[q].prep(g, c[q]);
-        const ATile16<DT>& a = as[j & 1];
+        const ATile16<DT, MT>& a = as[j & 1];
 #pragma unroll
         for (int s = 0; s < K16<DT>::kSteps; ++s) {
-            const half8 x8 = __builtin_bit_cast(half8, a.at(4 * s + g, m));
+            half8 x8[MT];
 #pragma unroll
-            for (int q = 0; q < NP; ++q)
-                acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x8, bw[q].step(s, c[q]), acc[q], 0, 0, 0);
+            for (int mt = 0; mt < MT; ++mt) x8[mt] = __builtin_bit_cast(half8, a.at(4 * s + g, kDecM * mt + m));
+#pragma unroll
+            for (int q = 0; q < NP; ++q) {
+                const half8 b = bw[q].step(s, c[q]);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    acc[q][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x8[mt], b, acc[q][mt], 0, 0, 0);
+            }
         }
         st.store(as[(j + 1) & 1], tid);
         __syncthreads();
@@ -728,12 +737,13 @@ __device__ __forceinline__ void dec_chunk(const uint16_t* abase, const int* rows
 
 // gate/up: block (64 features, slot segment); h = act(gate) * up as f16 at the
 // pair's sorted position, in the 16x16x32 K order of DD.
-template <int DG, int DD>
+template <int DG, int DD, int MT>
 __global__ void __launch_bounds__(kDecThreads, 2)
 dec_gateup_kernel(Bank gate, Bank up, const uint16_t* xl, int H, int I, int width, const int* seg_count,
                   const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm, int act, uint16_t* hl) {
-    __shared__ ATile16<DG> as[2];
-    __shared__ int rows[kDecM];
+    constexpr int CM = kDecM * MT; // tokens per chunk
+    __shared__ ATile16<DG, MT> as[2];
+    __shared__ int rows[CM];
     const int sg = blockIdx.y;
     if (sg >= *seg_count) return;
     const int tid = threadIdx.x, lane = tid & 63, m = lane & 15, g = lane >> 4;
@@ -744,33 +754,36 @@ dec_gateup_kernel(Bank gate, Bank up, const uint16_t* xl, int H, int I, int widt
                               up.base + (int64_t)slot * up.stride + (int64_t)n * up.row_bytes};
     const int col = laid16<DD>(n);
     int clamped = 0;
-    for (int c0 = b; c0 < e; c0 += kDecM) {
-        const int cnt = min(kDecM, e - c0);
+    for (int c0 = b; c0 < e; c0 += CM) {
+        const int cnt = min(CM, e - c0);
         __syncthreads(); // the previous chunk is done with rows and the A tiles
-        if (tid < kDecM) rows[tid] = tid < cnt ? (int)(perm[c0 + tid] / (uint32_t)width) * H : -1;
+        if (tid < CM) rows[tid] = tid < cnt ? (int)(perm[c0 + tid] / (uint32_t)width) * H : -1;
         __syncthreads();
-        floatx4 acc[2] = {};
-        dec_chunk<DG, 2>(xl, rows, wrow, 0, H / K16<DG>::kVals, as, tid, g, m, acc);
+        floatx4 acc[2][MT] = {};
+        dec_chunk<DG, 2, MT>(xl, rows, wrow, 0, H / K16<DG>::kVals, as, tid, g, m, acc);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int mm = 4 * g + i;
-            if (mm < cnt) {
-                const float hv = clamp_f16(naiwa_act(act, acc[0][i]) * acc[1][i], clamped);
-                hl[(size_t)(c0 + mm) * I + col] = __builtin_bit_cast(uint16_t, (_Float16)hv);
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int mm = kDecM * mt + 4 * g + i;
+                if (mm < cnt) {
+                    const float hv = clamp_f16(naiwa_act(act, acc[0][mt][i]) * acc[1][mt][i], clamped);
+                    hl[(size_t)(c0 + mm) * I + col] = __builtin_bit_cast(uint16_t, (_Float16)hv);
+                }
             }
-        }
     }
     count_clamped(clamped);
 }
 
 // down: block (64 output rows, K part, slot segment); the unweighted partial dot of
 // (K part, sorted position, row) into dpart.
-template <int DD>
+template <int DD, int MT>
 __global__ void __launch_bounds__(kDecThreads, 2)
 dec_down_kernel(Bank down, const uint16_t* hl, int H, int I, int ks, int npairs, const int* seg_count,
                 const uint32_t* seg_key, const uint32_t* seg_begin, float* dpart) {
-    __shared__ ATile16<DD> as[2];
-    __shared__ int rows[kDecM];
+    constexpr int CM = kDecM * MT;
+    __shared__ ATile16<DD, MT> as[2];
+    __shared__ int rows[CM];
     const int sg = blockIdx.z;
     if (sg >= *seg_count) return;
     const int tid = threadIdx.x, lane = tid & 63, m = lane & 15, g = lane >> 4;
@@ -779,19 +792,21 @@ dec_down_kernel(Bank down, const uint16_t* hl, int H, int I, int ks, int npairs,
     const int kp = blockIdx.y, k0 = kp * ks;
     const int r = blockIdx.x * kDecF + 16 * (tid >> 6) + m;
     const uint8_t* wrow[1] = {down.base + (int64_t)slot * down.stride + (int64_t)r * down.row_bytes};
-    for (int c0 = b; c0 < e; c0 += kDecM) {
-        const int cnt = min(kDecM, e - c0);
+    for (int c0 = b; c0 < e; c0 += CM) {
+        const int cnt = min(CM, e - c0);
         __syncthreads();
-        if (tid < kDecM) rows[tid] = tid < cnt ? (c0 + tid) * I : -1;
+        if (tid < CM) rows[tid] = tid < cnt ? (c0 + tid) * I : -1;
         __syncthreads();
-        floatx4 acc[1] = {};
-        dec_chunk<DD, 1>(hl, rows, wrow, k0 / K16<DD>::kVals, min(ks, I - k0) / K16<DD>::kVals, as, tid, g, m,
-                         acc);
+        floatx4 acc[1][MT] = {};
+        dec_chunk<DD, 1, MT>(hl, rows, wrow, k0 / K16<DD>::kVals, min(ks, I - k0) / K16<DD>::kVals, as, tid, g, m,
+                             acc);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int mm = 4 * g + i;
-            if (mm < cnt) dpart[((size_t)kp * npairs + c0 + mm) * H + r] = acc[0][i];
-        }
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int mm = kDecM * mt + 4 * g + i;
+                if (mm < cnt) dpart[((size_t)kp * npairs + c0 + mm) * H + r] = acc[0][mt][i];
+            }
     }
 }
 
@@ -805,6 +820,30 @@ template <int DG, int DD>
 void launch_gateup(dim3 g, hipStream_t st, Bank bg, Bank bu, const uint16_t* xp, int H, int I, int k,
                    const uint32_t* perm, Tiles tl, int act, uint16_t* hp) {
     gateup_kernel<DG, DD><<<g, kGemm, 0, st>>>(bg, bu, xp, H, I, k, perm, tl, act, hp);
+}
+
+template <int MT>
+void dec_experts(bool g4, bool d4, dim3 g1, dim3 g2, Bank bg, Bank bu, Bank bd, const uint16_t* xl, uint16_t* hl,
+                 int H, int I, int width, int ks, int n, const int* seg_count, const uint32_t* seg_key,
+                 const uint32_t* seg_begin, const uint32_t* perm, int act, float* dpart, hipStream_t st) {
+    if (g4 && d4)
+        dec_gateup_kernel<NAIWA_Q4_K, NAIWA_Q4_K, MT><<<g1, kDecThreads, 0, st>>>(bg, bu, xl, H, I, width, seg_count,
+                                                                                  seg_key, seg_begin, perm, act, hl);
+    else if (g4)
+        dec_gateup_kernel<NAIWA_Q4_K, NAIWA_Q8_0, MT><<<g1, kDecThreads, 0, st>>>(bg, bu, xl, H, I, width, seg_count,
+                                                                                  seg_key, seg_begin, perm, act, hl);
+    else if (d4)
+        dec_gateup_kernel<NAIWA_Q8_0, NAIWA_Q4_K, MT><<<g1, kDecThreads, 0, st>>>(bg, bu, xl, H, I, width, seg_count,
+                                                                                  seg_key, seg_begin, perm, act, hl);
+    else
+        dec_gateup_kernel<NAIWA_Q8_0, NAIWA_Q8_0, MT><<<g1, kDecThreads, 0, st>>>(bg, bu, xl, H, I, width, seg_count,
+                                                                                  seg_key, seg_begin, perm, act, hl);
+    if (d4)
+        dec_down_kernel<NAIWA_Q4_K, MT><<<g2, kDecThreads, 0, st>>>(bd, hl, H, I, ks, n, seg_count, seg_key, seg_begin,
+                                                                     dpart);
+    else
+        dec_down_kernel<NAIWA_Q8_0, MT><<<g2, kDecThreads, 0, st>>>(bd, hl, H, I, ks, n, seg_count, seg_key, seg_begin,
+                                                                     dpart);
 }
 
 } // namespace
@@ -841,26 +880,15 @@ int naiwa_decode_mfma_experts(const naiwa_bank* gate, const naiwa_bank* up, cons
         dec_prep_kernel<NAIWA_Q4_K><<<pb, kThreads, 0, st>>>(x, xb, rows, H, xl);
     else
         dec_prep_kernel<NAIWA_Q8_0><<<pb, kThreads, 0, st>>>(x, xb, rows, H, xl);
-    const dim3 g1(I / kDecF, seg_bound);
-    if (g4 && d4)
-        dec_gateup_kernel<NAIWA_Q4_K, NAIWA_Q4_K><<<g1, kDecThreads, 0, st>>>(bg, bu, xl, H, I, width, seg_count,
-                                                                              seg_key, seg_begin, perm, act, hl);
-    else if (g4)
-        dec_gateup_kernel<NAIWA_Q4_K, NAIWA_Q8_0><<<g1, kDecThreads, 0, st>>>(bg, bu, xl, H, I, width, seg_count,
-                                                                              seg_key, seg_begin, perm, act, hl);
-    else if (d4)
-        dec_gateup_kernel<NAIWA_Q8_0, NAIWA_Q4_K><<<g1, kDecThreads, 0, st>>>(bg, bu, xl, H, I, width, seg_count,
-                                                                              seg_key, seg_begin, perm, act, hl);
+    const dim3 g1(I / kDecF, seg_bound), g2(H / kDecF, (I + ks - 1) / ks, seg_bound);
+    // two 16-token subtiles per chunk when the segments average more than 8 tokens:
+    // each weight is then dequantised once per 32 tokens instead of 16
+    if (n > 8 * seg_bound)
+        dec_experts<2>(g4, d4, g1, g2, bg, bu, bd, xl, hl, H, I, width, ks, n, seg_count, seg_key, seg_begin, perm,
+                       act, dpart, st);
     else
-        dec_gateup_kernel<NAIWA_Q8_0, NAIWA_Q8_0><<<g1, kDecThreads, 0, st>>>(bg, bu, xl, H, I, width, seg_count,
-                                                                              seg_key, seg_begin, perm, act, hl);
-    const dim3 g2(H / kDecF, (I + ks - 1) / ks, seg_bound);
-    if (d4)
-        dec_down_kernel<NAIWA_Q4_K><<<g2, kDecThreads, 0, st>>>(bd, hl, H, I, ks, n, seg_count, seg_key, seg_begin,
-                                                                 dpart);
-    else
-        dec_down_kernel<NAIWA_Q8_0><<<g2, kDecThreads, 0, st>>>(bd, hl, H, I, ks, n, seg_count, seg_key, seg_begin,
-                                                                 dpart);
+        dec_experts<1>(g4, d4, g1, g2, bg, bu, bd, xl, hl, H, I, width, ks, n, seg_count, seg_key, seg_begin, perm,
+                       act, dpart, st);
     return naiwa_hip_rc(hipGetLastError());
 }
 
