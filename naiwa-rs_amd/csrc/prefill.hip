@@ -196,20 +196,37 @@ __device__ __forceinline__ void q4k_scale_min(const u32x4& hd, int j, _Float16& 
     mn = (_Float16)(-(naiwa_f16_to_f32(hd.x >> 16) * (float)m));
 }
 
-// The 8 f16 weights (1024 + nibble) * sc + mn of quant words da, db (bytes 0-7 of a
-// run), low nibbles when sh = 0 and high ones when sh = 4, in byte order 0 2 1 3 4 6 5 7.
-__device__ __forceinline__ half8 q4k_unpack(uint32_t da, uint32_t db, int sh, _Float16 sc, _Float16 mn) {
-    const half2v scv = {sc, sc}, mnv = {mn, mn};
-    const half2v k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+// Nibble masks held in registers.  A nibble masked into the mantissa of an f16 magic
+// number reads as magic + q exactly: a low nibble (bits 0-3) in 1024.0 (0x6400), a
+// high one left at bits 4-7 in 64.0 (0x5400).  With the mask in a VGPR,
+// (w & mask) | magic is one v_and_or_b32 (a VOP3 here takes at most one literal or
+// SGPR, so two immediates would cost a separate and and or).
+struct NibMask {
+    uint32_t m[2]; // low nibbles 0x000F000F, high nibbles 0x00F000F0
+};
+__device__ __forceinline__ NibMask nib_mask() {
+    NibMask n{{0x000F000Fu, 0x00F000F0u}};
+    asm("" : "+v"(n.m[0]));
+    asm("" : "+v"(n.m[1]));
+    return n;
+}
+
+// The 8 f16 weights q * sc + mn of quant words da, db (bytes 0-7 of a run), the low
+// nibbles when hi = 0 and the high ones when hi = 1, in byte order 0 2 1 3 4 6 5 7.
+__device__ __forceinline__ half8 q4k_unpack(uint32_t da, uint32_t db, int hi, const NibMask& nm, _Float16 sc,
+                                            _Float16 mn) {
+    const uint32_t mk = nm.m[hi], magic = hi ? 0x54005400u : 0x64006400u;
+    const _Float16 b = hi ? (_Float16)-64.0f : (_Float16)-1024.0f;
+    const half2v scv = {sc, sc}, mnv = {mn, mn}, bias = {b, b};
     half2v p[4];
-    p[0] = __builtin_bit_cast(half2v, ((da >> sh) & 0x000F000Fu) | 0x64006400u);
-    p[1] = __builtin_bit_cast(half2v, ((da >> (sh + 8)) & 0x000F000Fu) | 0x64006400u);
-    p[2] = __builtin_bit_cast(half2v, ((db >> sh) & 0x000F000Fu) | 0x64006400u);
-    p[3] = __builtin_bit_cast(half2v, ((db >> (sh + 8)) & 0x000F000Fu) | 0x64006400u);
+    p[0] = __builtin_bit_cast(half2v, (da & mk) | magic);
+    p[1] = __builtin_bit_cast(half2v, ((da >> 8) & mk) | magic);
+    p[2] = __builtin_bit_cast(half2v, (db & mk) | magic);
+    p[3] = __builtin_bit_cast(half2v, ((db >> 8) & mk) | magic);
     half8 out;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const half2v w = __builtin_elementwise_fma(p[i] + k1024, scv, mnv);
+        const half2v w = __builtin_elementwise_fma(p[i] + bias, scv, mnv);
         out[2 * i] = w[0];
         out[2 * i + 1] = w[1];
     }
@@ -250,12 +267,12 @@ template <> struct BRow<NAIWA_Q4_K> {
 #pragma unroll
         for (int c = 0; c < 4; ++c) q[c] = *reinterpret_cast<const u32x4*>(blk + 16 + 32 * c + 16 * h);
     }
-    __device__ __forceinline__ half8 step(int s) const {
+    __device__ __forceinline__ half8 step(int s, const NibMask& nm) const {
         const int c = s / 4, t = s % 4;
         const uint32_t da = (t % 2) ? q[c].z : q[c].x, db = (t % 2) ? q[c].w : q[c].y;
         _Float16 a, b;
         q4k_scale_min(hd, 2 * c + t / 2, a, b);
-        return q4k_unpack(da, db, 4 * (t / 2), a, b);
+        return q4k_unpack(da, db, t / 2, nm, a, b);
     }
 };
 
@@ -285,14 +302,16 @@ template <> struct BRow<NAIWA_Q8_0> {
     }
 };
 
-// LDS A tile of one K-block: group g of tile row m at [g][m ^ (g % 32)] (16 bytes
-// each): a step's read of 32 rows of one group covers 32 consecutive slots, and a
-// staging store of the 32 groups of one row spreads over the banks.
+// LDS A tile of one K-block: group g of tile row m at [g][m] (16 bytes each), rows of
+// groups padded to kTM + 1 slots.  A step's read of 32 rows of one group covers 32
+// consecutive slots at an offset fixed at compile time from the lane's own base; a
+// staging store of consecutive groups of one row steps 1040 bytes (16 mod 256) from
+// lane to lane, so it spreads over the banks.
 template <int DT> struct ATile {
     static constexpr int kGroups = 2 * KBlock<DT>::kSteps;
-    u32x4 v[kGroups][kTM];
-    __device__ __forceinline__ u32x4& at(int g, int m) { return v[g][m ^ (g & 31)]; }
-    __device__ __forceinline__ const u32x4& at(int g, int m) const { return v[g][m ^ (g & 31)]; }
+    u32x4 v[kGroups][kTM + 1];
+    __device__ __forceinline__ u32x4& at(int g, int m) { return v[g][m]; }
+    __device__ __forceinline__ const u32x4& at(int g, int m) const { return v[g][m]; }
 };
 
 // Each thread's share of staging one K-block of the A tile: global -> registers
@@ -303,23 +322,34 @@ template <int DT> struct AStage {
     // base: the activation matrix (a kernel argument, so the loads are global ones);
     // rows[m]: element offset of tile row m
     // piece p: row p / G, group p % G, so the lanes of a load cover whole rows
-    __device__ __forceinline__ void load(const uint16_t* base, const int* rows, int kb, int tid) {
+    // pieces i0 .. i1 - 1 only, when given (staging in parts holds fewer registers)
+    __device__ __forceinline__ void load(const uint16_t* base, const int* rows, int kb, int tid, int i0 = 0,
+                                         int i1 = kPer) {
         constexpr int G = ATile<DT>::kGroups;
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
+        for (int i = i0; i < i1; ++i) {
             const int p = tid + kGemm * i, m = p / G, g = p % G;
             r[i] = *reinterpret_cast<const u32x4*>(base + rows[m] + kb * KBlock<DT>::kVals + 8 * g);
         }
     }
-    __device__ __forceinline__ void store(ATile<DT>& a, int tid) const {
+    __device__ __forceinline__ void store(ATile<DT>& a, int tid, int i0 = 0, int i1 = kPer) const {
         constexpr int G = ATile<DT>::kGroups;
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
+        for (int i = i0; i < i1; ++i) {
             const int p = tid + kGemm * i;
             a.at(p % G, p / G) = r[i];
         }
     }
 };
+
+// Workgroup barrier for an LDS hand-off: waits for this wave's LDS operations only.
+// (__syncthreads also waits for every global load in flight, which would make each
+// K-block wait out the latency of the next K-block's weight loads.)
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 
 struct Bank {
     const uint8_t* base;
@@ -338,10 +368,15 @@ __device__ __forceinline__ void tile_k_loop(const uint16_t* abase, const int* ro
     AStage<DT> st;
     if constexpr (DT == NAIWA_Q4_K) {
         // Rolling prefetch: chunk c of the next K-block replaces chunk c of the current one
-        // as soon as its four steps are done, and the next header waits beside the current
-        // one, so a lane holds one K-block of weights (plus a header) instead of two.  At
-        // most 128 VGPRs then, two 8-wave blocks fit on a CU.
+        // as soon as its four steps are done, and the next header replaces the current one
+        // once the last chunk's scales are taken, so a lane holds one K-block of weights
+        // instead of two.  At most 128 VGPRs then, two 8-wave blocks fit on a CU.
         BRow<DT> b;
+        const NibMask nm = nib_mask();
+        // this lane's A operand slot in buffer 0: step s, subtile ms reads
+        // alane[buffer + 2 s (kTM + 1) + 32 ms] (one base register, offsets fixed)
+        const u32x4* alane = &as[0].v[h][lane & 31];
+        constexpr int kBuf = sizeof(ATile<DT>) / sizeof(u32x4);
         st.load(abase, rows, 0, tid);
         b.load(wrow, 0, h);
         st.store(as[0], tid);
@@ -349,26 +384,41 @@ __device__ __forceinline__ void tile_k_loop(const uint16_t* abase, const int* ro
         for (int kb = 0; kb < nkb; ++kb) {
             const int kn = min(kb + 1, nkb - 1);
             const uint8_t* nblk = wrow + (size_t)kn * NAIWA_Q4_K_BYTES;
-            st.load(abase, rows, kn, tid);
-            const u32x4 hd_next = *reinterpret_cast<const u32x4*>(nblk);
-            const ATile<DT>& a = as[kb & 1];
+            // the next A tile goes to the other buffer in two halves during this block (its
+            // last reads were before the previous barrier): half the staging registers
+            constexpr int kHalf = AStage<DT>::kPer / 2;
+            st.load(abase, rows, kn, tid, 0, kHalf);
+            __builtin_amdgcn_sched_barrier(0); // keep the prefetches where they are issued
+            const u32x4* ab = alane + (kb & 1) * kBuf;
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
+                _Float16 sc[2], mn[2];
+                q4k_scale_min(b.hd, 2 * c, sc[0], mn[0]);
+                q4k_scale_min(b.hd, 2 * c + 1, sc[1], mn[1]);
+                // the last chunk's scales are taken: the next header can replace this one
+                if (c == 3) b.hd = *reinterpret_cast<const u32x4*>(nblk);
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     const int s = 4 * c + t;
-                    const half8 wv = b.step(s);
+                    const uint32_t da = (t % 2) ? b.q[c].z : b.q[c].x, db = (t % 2) ? b.q[c].w : b.q[c].y;
+                    const half8 wv = q4k_unpack(da, db, t / 2, nm, sc[t / 2], mn[t / 2]);
 #pragma unroll
                     for (int ms = 0; ms < 2; ++ms) {
-                        const half8 x8 = __builtin_bit_cast(half8, a.at(2 * s + h, 32 * ms + (lane & 31)));
+                        const half8 x8 = __builtin_bit_cast(half8, ab[2 * s * (kTM + 1) + 32 * ms]);
                         acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x8, wv, acc[ms], 0, 0, 0);
                     }
                 }
                 b.q[c] = *reinterpret_cast<const u32x4*>(nblk + 16 + 32 * c + 16 * h);
+                if (c == 0) {
+                    st.store(as[(kb + 1) & 1], tid, 0, kHalf);
+                    st.load(abase, rows, kn, tid, kHalf, AStage<DT>::kPer);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (c == 2) {
+                    st.store(as[(kb + 1) & 1], tid, kHalf, AStage<DT>::kPer);
+                }
             }
-            b.hd = hd_next;
-            st.store(as[(kb + 1) & 1], tid);
-            __syncthreads();
+            lds_barrier();
         }
     } else {
         BRow<DT> b0, b1; // this K-block's row share and the next one's, alternating
@@ -391,7 +441,7 @@ __device__ __forceinline__ void tile_k_loop(const uint16_t* abase, const int* ro
                 }
             }
             st.store(as[(kb + 1) & 1], tid);
-            __syncthreads();
+            lds_barrier();
         };
         int kb = 0;
         for (; kb + 2 <= nkb; kb += 2) {
@@ -582,11 +632,11 @@ template <> struct W16<NAIWA_Q4_K> {
         q4k_scale_min(hd, 2 * g, c.sc[0], c.mn[0]);
         q4k_scale_min(hd, 2 * g + 1, c.sc[1], c.mn[1]);
     }
-    __device__ __forceinline__ half8 step(int s, const Scl& c) const {
+    __device__ __forceinline__ half8 step(int s, const Scl& c, const NibMask& nm) const {
         const int p = s >> 1, t = s & 1;
         const u32x4& q = p < 2 ? q0 : q1;
         const uint32_t da = (p & 1) ? q.z : q.x, db = (p & 1) ? q.w : q.y;
-        return q4k_unpack(da, db, 4 * t, c.sc[t], c.mn[t]);
+        return q4k_unpack(da, db, t, nm, c.sc[t], c.mn[t]);
     }
 };
 
@@ -601,7 +651,7 @@ template <> struct W16<NAIWA_Q8_0> {
         for (int i = 0; i < 9; ++i) w[i] = p[i];
     }
     __device__ __forceinline__ void prep(int, Scl&) const {}
-    __device__ __forceinline__ half8 step(int s, const Scl&) const {
+    __device__ __forceinline__ half8 step(int s, const Scl&, const NibMask&) const {
         const uint32_t d0 = sh ? w[2 * s + 1] : __builtin_amdgcn_alignbyte(w[2 * s + 1], w[2 * s], 2);
         const uint32_t d1 = sh ? w[2 * s + 2] : __builtin_amdgcn_alignbyte(w[2 * s + 2], w[2 * s + 1], 2);
         const uint32_t dbits = sh ? (w[0] >> 16) : (w[0] & 0xffffu);
@@ -695,6 +745,7 @@ __device__ __forceinline__ void dec_chunk(const uint16_t* abase, const int* rows
                                           floatx4 (&acc)[NP][MT]) {
     AStage16<DT, MT> st;
     W16<DT> cur[NP], nxt[NP];
+    const NibMask nm = nib_mask();
     st.load(abase, rows, kb0, tid);
 #pragma unroll
     for (int q = 0; q < NP; ++q) cur[q].load(wrow[q], kb0, g);
@@ -718,14 +769,14 @@ __device__ __forceinline__ void dec_chunk(const uint16_t* abase, const int* rows
             for (int mt = 0; mt < MT; ++mt) x8[mt] = __builtin_bit_cast(half8, a.at(4 * s + g, kDecM * mt + m));
 #pragma unroll
             for (int q = 0; q < NP; ++q) {
-                const half8 b = bw[q].step(s, c[q]);
+                const half8 b = bw[q].step(s, c[q], nm);
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
                     acc[q][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x8[mt], b, acc[q][mt], 0, 0, 0);
             }
         }
         st.store(as[(j + 1) & 1], tid);
-        __syncthreads();
+        lds_barrier();
     };
     int j = 0;
     for (; j + 2 <= nkb; j += 2) {
