@@ -7,11 +7,13 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <initializer_list>
 #include <new>
+#include <thread>
 #include <vector>
 
 #include "../../include/naiwa_cached.h"
@@ -67,6 +69,30 @@ bool upload_sync_poll() {
 
 // Bound of the host's wait for a routing doorbell.
 constexpr int64_t kRouteWaitUs = 10 * 1000 * 1000;
+// How long that wait spins before it sleep-polls.  The routing doorbell rings within
+// tens of microseconds of the call (the device first finishes the previous layer), and
+// a sleep costs the OS timer slack, ~50 us or more, on every layer of every token.
+constexpr int64_t kRouteSpinUs = 2000;
+
+// *word >= target: spin (pause) for up to kRouteSpinUs, then sleep-poll every 20 us,
+// until kRouteWaitUs have passed (NAIWA_E_TIMEOUT).
+int wait_routing(const uint32_t* word, uint32_t target) {
+    using clock = std::chrono::steady_clock;
+    const auto t0 = clock::now();
+    const auto spin_end = t0 + std::chrono::microseconds(kRouteSpinUs);
+    const auto deadline = t0 + std::chrono::microseconds(kRouteWaitUs);
+    for (uint32_t i = 0;; ++i) {
+        if (naiwa_host_load_acquire_u32(word) >= target) return NAIWA_OK;
+        if ((i & 63) == 0) {
+            const auto now = clock::now();
+            if (now >= deadline) return NAIWA_E_TIMEOUT;
+            if (now >= spin_end) std::this_thread::sleep_for(std::chrono::microseconds(20));
+        }
+#if defined(__x86_64__)
+        __builtin_ia32_pause();
+#endif
+    }
+}
 
 } // namespace
 
@@ -328,7 +354,7 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     routing_publish_kernel<<<1, 256, 0, st>>>(L->db_dev, L->ids_dev, L->w_dev, n, next ? next->pred_ids_dev : nullptr,
                                               next ? n : 0);
     if ((rc = naiwa_hip_rc(hipGetLastError()))) return rc;
-    if ((rc = naiwa_host_wait_ge(L->db_host, ++L->db_seq, kRouteWaitUs, 20))) return rc;
+    if ((rc = wait_routing(L->db_host, ++L->db_seq))) return rc;
     L->last_rows = rows;
 
     // hit/miss split, then the misses to stream into the ring
@@ -349,6 +375,25 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
             L->slots_up[i] = (uint32_t)L->slots_h[i];
         }
     }
+
+    // the step's inputs: slot ids and, with staged pairs, the weights of the cache pairs
+    // and of the staged pairs, written into mapped coherent host memory and pulled into
+    // device memory by one wave on the compute stream.  The previous step of this layer
+    // has finished reading them: its kernels precede this step's routing, whose doorbell
+    // the host waited for above.  The pull goes ahead of the staged uploads: its few PCIe
+    // reads would otherwise queue behind megabytes of upload reads.
+    if (nc) {
+        float* w_res = L->wsplit_h;
+        float* w_stg = L->wsplit_h + n;
+        for (int i = 0; i < n; ++i) {
+            const bool staged_pair = L->slots_up[i] >= (uint32_t)d.usable;
+            w_res[i] = staged_pair ? 0.0f : L->w_h[i];
+            w_stg[i] = staged_pair ? L->w_h[i] : 0.0f;
+        }
+    }
+    std::atomic_thread_fence(std::memory_order_release);
+    pull_inputs_kernel<<<1, 64, 0, st>>>(L->in_dev_base, L->in_map_base, n * (nc ? 3 : 1));
+    if ((rc = naiwa_hip_rc(hipGetLastError()))) return rc;
 
     // uploads on the copy stream after the last step that read each ring slot: one kernel
     // for all of them when the host stacks are mapped pinned memory (one range per expert
@@ -384,23 +429,6 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     if (nc && poll && (rc = doorbell_poll_signal(L->upload_flag, ++L->upload_epoch, (int64_t)L->copy))) return rc;
     if (nc && !poll && (rc = naiwa_hip_rc(hipEventRecord(L->staged_done, L->copy)))) return rc;
 
-    // the step's inputs: slot ids and, with staged pairs, the weights of the cache pairs
-    // and of the staged pairs, written into mapped coherent host memory and pulled into
-    // device memory by one wave on the compute stream.  The previous step of this layer
-    // has finished reading them: its kernels precede this step's routing, whose doorbell
-    // the host waited for above.
-    if (nc) {
-        float* w_res = L->wsplit_h;
-        float* w_stg = L->wsplit_h + n;
-        for (int i = 0; i < n; ++i) {
-            const bool staged_pair = L->slots_up[i] >= (uint32_t)d.usable;
-            w_res[i] = staged_pair ? 0.0f : L->w_h[i];
-            w_stg[i] = staged_pair ? L->w_h[i] : 0.0f;
-        }
-    }
-    std::atomic_thread_fence(std::memory_order_release);
-    pull_inputs_kernel<<<1, 64, 0, st>>>(L->in_dev_base, L->in_map_base, n * (nc ? 3 : 1));
-    if ((rc = naiwa_hip_rc(hipGetLastError()))) return rc;
     // the expert kernel after the latest lookahead claim (src/moe/cached_layer.rs:808-819):
     // a slot it published may still be in flight
     if (L->ahead_claimed) {
