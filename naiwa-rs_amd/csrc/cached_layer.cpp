@@ -18,6 +18,7 @@
 
 #include "../../include/naiwa_cached.h"
 #include "common.h"
+#include "router.h"
 #include "upload.h"
 
 namespace {
@@ -347,13 +348,20 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     // route on the device, then read the top-k back through the mapped doorbell: the
     // router's results (and the lookahead's prediction) are published with seq + 1 and
     // the host spins on seq, with no stream synchronisation (the routing round trip)
-    rc = naiwa_router_topk_biased(x, NAIWA_BF16, d.router, d.router_bias, rows, d.hidden, d.num_experts, k, d.mode,
-                                  L->ids_dev, L->w_dev, nullptr, stream);
-    if (!rc && next) rc = next->predict_launch(x, rows, stream);
-    if (rc) return rc;
-    routing_publish_kernel<<<1, 256, 0, st>>>(L->db_dev, L->ids_dev, L->w_dev, n, next ? next->pred_ids_dev : nullptr,
-                                              next ? n : 0);
-    if ((rc = naiwa_hip_rc(hipGetLastError()))) return rc;
+    if (rows == 1 && !next) {
+        // one token and no prediction to publish: the top-k block publishes itself
+        rc = naiwa_router_topk_publish(x, NAIWA_BF16, d.router, d.router_bias, d.hidden, d.num_experts, k, d.mode,
+                                       L->ids_dev, L->w_dev, L->db_dev, L->db_dev + kDbHead, stream);
+        if (rc) return rc;
+    } else {
+        rc = naiwa_router_topk_biased(x, NAIWA_BF16, d.router, d.router_bias, rows, d.hidden, d.num_experts, k,
+                                      d.mode, L->ids_dev, L->w_dev, nullptr, stream);
+        if (!rc && next) rc = next->predict_launch(x, rows, stream);
+        if (rc) return rc;
+        routing_publish_kernel<<<1, 256, 0, st>>>(L->db_dev, L->ids_dev, L->w_dev, n,
+                                                  next ? next->pred_ids_dev : nullptr, next ? n : 0);
+        if ((rc = naiwa_hip_rc(hipGetLastError()))) return rc;
+    }
     if ((rc = wait_routing(L->db_host, ++L->db_seq))) return rc;
     L->last_rows = rows;
 

@@ -171,3 +171,10 @@ __device__ inline void naiwa_wave_topk(const float* l, int E, int k, int mode, u
         w[lane] = expf(my_v - mx) / denom;
     }
 }
+
+// naiwa_router_topk_biased for one row, publishing the routing read-back from the
+// top-k block: ids and weights to pay[0..k) and pay[k..2k) of mapped host memory,
+// then *db_seq + 1 with a system-scope release (the host spins on db_seq).
+int naiwa_router_topk_publish(const void* x, int x_dtype, const float* W, const float* bias, int H, int E, int k,
+                              int mode, uint32_t* ids_out, float* w_out, uint32_t* db_seq, uint32_t* pay,
+                              int64_t stream);

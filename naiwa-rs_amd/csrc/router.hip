@@ -100,7 +100,60 @@ router_topk_kernel(const float* logits, int E, int k, int mode, uint32_t* ids, f
     }
 }
 
+// router_topk_kernel for one row with the routing read-back published from the same
+// block: ids and weights also go to the mapped payload (ids at pay[0..k), weights at
+// pay[k..2k)), then the sequence word goes up by one with a system-scope release --
+// the reference's TopkDoorbell publish (src/doorbell/d2h/topk.rs:20-125) without a
+// launch of its own.
+__global__ void __launch_bounds__(kTopkThreads)
+router_topk_publish_kernel(const float* logits, int E, int k, int mode, uint32_t* ids, float* w, uint32_t* db_seq,
+                           uint32_t* pay) {
+    __shared__ float l[NAIWA_ROUTER_MAX_E];
+    __shared__ int rank_tmp[NAIWA_ROUTER_MAX_E];
+    __shared__ float ex_tmp[NAIWA_ROUTER_MAX_E];
+    __shared__ uint32_t ids_s[NAIWA_ROUTER_MAX_K];
+    __shared__ float w_s[NAIWA_ROUTER_MAX_K];
+    for (int e = threadIdx.x; e < E; e += kTopkThreads) l[e] = logits[e];
+    __syncthreads();
+    naiwa_block_topk<kTopkThreads>(l, E, k, mode, ids_s, w_s, rank_tmp, ex_tmp);
+    if (threadIdx.x < k) {
+        const uint32_t id = ids_s[threadIdx.x];
+        const float wv = w_s[threadIdx.x];
+        ids[threadIdx.x] = id;
+        w[threadIdx.x] = wv;
+        volatile uint32_t* out = pay;
+        out[threadIdx.x] = id;
+        out[k + threadIdx.x] = __float_as_uint(wv);
+    }
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t cur = __hip_atomic_load(db_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(db_seq, cur + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
 } // namespace
+
+int naiwa_router_topk_publish(const void* x, int x_dtype, const float* W, const float* bias, int H, int E, int k,
+                              int mode, uint32_t* ids_out, float* w_out, uint32_t* db_seq, uint32_t* pay,
+                              int64_t stream) {
+    if (x_dtype != NAIWA_BF16 && x_dtype != NAIWA_F32) return NAIWA_E_UNSUPPORTED;
+    if (mode < NAIWA_ROUTE_SOFTMAX_TOPK_RENORM || mode > NAIWA_ROUTE_SOFTMAX_TOPK)
+        return NAIWA_E_UNSUPPORTED;
+    if (H <= 0 || H % NAIWA_ROUTER_CHUNK || E <= 0 || E > NAIWA_ROUTER_MAX_E || k <= 0 || k > E ||
+        k > NAIWA_ROUTER_MAX_K)
+        return NAIWA_E_INVALID;
+    if (!x || !W || !ids_out || !w_out || !db_seq || !pay) return NAIWA_E_INVALID;
+    hipStream_t st = (hipStream_t)stream;
+    int rc = 0;
+    float* logits = (float*)naiwa_scratch(NAIWA_SCRATCH_ROUTER, (size_t)E * 4, &rc);
+    if (!logits) return rc;
+    router_logits_kernel<<<dim3((unsigned)E, 1u), kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, W, bias, 1, H, E,
+                                                                         logits);
+    router_topk_publish_kernel<<<1, kTopkThreads, 0, st>>>(logits, E, k, mode, ids_out, w_out, db_seq, pay);
+    return naiwa_hip_rc(hipGetLastError());
+}
 
 extern "C" int naiwa_router_topk_biased(const void* x, int x_dtype, const float* W, const float* bias, int rows,
                                         int H, int E, int k, int mode, uint32_t* ids_out, float* w_out,
