@@ -384,13 +384,21 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         }
     }
 
-    // the step's inputs: slot ids and, with staged pairs, the weights of the cache pairs
+    // Staged uploads by the batched copy kernel hold up kernels that run beside them (its
+    // PCIe reads stall the memory pipeline they share), so a cache-pair pass queued ahead
+    // of the upload wait would end with the upload anyway: with that kernel, one expert
+    // pass over every pair runs after the upload.  With DMA uploads the cache pairs go
+    // first, during the upload, and the staged pairs after it.
+    const bool batch = L->batch_uploads && !L->dma_uploads && 3 * nc <= NAIWA_COPY_BATCH_MAX;
+    const bool split = nc && !batch;
+
+    // the step's inputs: slot ids and, for split passes, the weights of the cache pairs
     // and of the staged pairs, written into mapped coherent host memory and pulled into
     // device memory by one wave on the compute stream.  The previous step of this layer
     // has finished reading them: its kernels precede this step's routing, whose doorbell
     // the host waited for above.  The pull goes ahead of the staged uploads: its few PCIe
     // reads would otherwise queue behind megabytes of upload reads.
-    if (nc) {
+    if (split) {
         float* w_res = L->wsplit_h;
         float* w_stg = L->wsplit_h + n;
         for (int i = 0; i < n; ++i) {
@@ -400,7 +408,7 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         }
     }
     std::atomic_thread_fence(std::memory_order_release);
-    pull_inputs_kernel<<<1, 64, 0, st>>>(L->in_dev_base, L->in_map_base, n * (nc ? 3 : 1));
+    pull_inputs_kernel<<<1, 64, 0, st>>>(L->in_dev_base, L->in_map_base, n * (split ? 3 : 1));
     if ((rc = naiwa_hip_rc(hipGetLastError()))) return rc;
 
     // uploads on the copy stream after the last step that read each ring slot: one kernel
@@ -410,7 +418,6 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     {
         naiwa_copy items[NAIWA_COPY_BATCH_MAX];
         int ni = 0;
-        const bool batch = L->batch_uploads && !L->dma_uploads && 3 * nc <= NAIWA_COPY_BATCH_MAX;
         for (int i = 0; i < nc; ++i) {
             const int64_t fence = L->ring_fenced[pos[i]] ? (int64_t)L->ring_fence[pos[i]] : 0;
             if (batch) {
@@ -443,7 +450,12 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         if ((rc = naiwa_hip_rc(hipStreamWaitEvent(st, L->ahead_done, 0)))) return rc;
         ++step.preload_waits;
     }
-    if (!nc) {
+    if (!split) {
+        if (nc) {
+            rc = poll ? doorbell_poll_wait(L->upload_flag, L->upload_epoch, stream)
+                      : naiwa_hip_rc(hipStreamWaitEvent(st, L->staged_done, 0));
+            if (rc) return rc;
+        }
         if ((rc = naiwa_moe_decode(&d.gate, &d.up, &d.down, x, NAIWA_BF16, L->slots_dev, L->w_dev, rows, k, d.act,
                                    out, stream)))
             return rc;
