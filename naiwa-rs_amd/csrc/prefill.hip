@@ -505,6 +505,23 @@ gateup_kernel(Bank gate, Bank up, const uint16_t* xp, int H, int I, int k, const
     }
 }
 
+// (tile, column block) of a down block, or false past the last tile.  The hardware
+// deals consecutive workgroup ids to the 8 XCDs in turn, so in the plain order the
+// column blocks of one tile land on 8 XCDs and each XCD's L2 fetches the tile's h rows
+// again.  Here XCD x takes the x-th contiguous run of the tile-major (tile, column)
+// items instead: the column blocks of a tile share one L2 copy of its rows.  A
+// bijection of [0, ntiles * gridDim.x); the ids past that range exit.
+constexpr int kXcds = 8;
+__device__ __forceinline__ bool xcd_item(int ntiles, int& tile, int& col) {
+    const int gx = gridDim.x, id = blockIdx.x + gx * blockIdx.y, total = ntiles * gx;
+    if (id >= total) return false;
+    const int q = total / kXcds, r = total % kXcds, x = id % kXcds, loc = id / kXcds;
+    const int item = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + loc;
+    tile = item / gx;
+    col = item % gx;
+    return true;
+}
+
 // down: one tile of <= 64 pairs x 256 output features (32 per wave); pair rows
 // scaled by their weight.
 template <int DD>
@@ -513,12 +530,12 @@ down_kernel(Bank down, const uint16_t* hp, int H, int I, const uint32_t* perm, c
             float* ypair) {
     __shared__ ATile<DD> as[2];
     __shared__ int rows[kTM];
-    const int tile = blockIdx.y;
-    if (tile >= *tl.n) return;
+    int tile, col;
+    if (!xcd_item(*tl.n, tile, col)) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5;
     const int start = tl.start[tile], cnt = tl.count[tile], slot = tl.slot[tile];
     if (tid < kTM) rows[tid] = (start + min(tid, cnt - 1)) * I;
-    const int n = blockIdx.x * kTND + 32 * wave + (lane & 31);
+    const int n = col * kTND + 32 * wave + (lane & 31);
     const uint8_t* drow = down.base + (int64_t)slot * down.stride + (int64_t)n * down.row_bytes;
     const int nkb = I / KBlock<DD>::kVals;
     __syncthreads();
@@ -548,7 +565,9 @@ combine_kernel(const float* ypair, const uint32_t* ids, int k, int H, int slots,
     const int t = blockIdx.x, HV = H / V;
     const vec* yp = reinterpret_cast<const vec*>(ypair + (size_t)t * k * H);
     vec* o = reinterpret_cast<vec*>(out + (size_t)t * H);
-    for (int c = threadIdx.x; c < HV; c += kThreads) {
+    // blockIdx.y: a slice of kThreads vectors of the token's row, so that every load of
+    // the call is in flight at once rather than in rounds per block
+    for (int c = blockIdx.y * kThreads + threadIdx.x; c < HV; c += kThreads * gridDim.y) {
         vec y = accumulate ? o[c] : vec(0.0f);
         for (int j0 = 0; j0 < k; j0 += kJ) {
             vec v[kJ];
@@ -1026,9 +1045,10 @@ extern "C" int naiwa_moe_prefill(const naiwa_bank* gate, const naiwa_bank* up, c
     else
         down_kernel<NAIWA_Q8_0><<<g2, kGemm, 0, st>>>(bd, hp, H, I, perm, w, tl, ypair);
     const int acc = (flags & NAIWA_PREFILL_ACCUMULATE) ? 1 : 0;
+    const unsigned cs4 = (unsigned)((H / 4 + kThreads - 1) / kThreads), cs1 = (unsigned)((H + kThreads - 1) / kThreads);
     if (((uintptr_t)out & 15) == 0)
-        combine_kernel<4><<<T, kThreads, 0, st>>>(ypair, slot_ids, k, H, slots, acc, out);
+        combine_kernel<4><<<dim3(T, cs4), kThreads, 0, st>>>(ypair, slot_ids, k, H, slots, acc, out);
     else
-        combine_kernel<1><<<T, kThreads, 0, st>>>(ypair, slot_ids, k, H, slots, acc, out);
+        combine_kernel<1><<<dim3(T, cs1), kThreads, 0, st>>>(ypair, slot_ids, k, H, slots, acc, out);
     return naiwa_hip_rc(hipGetLastError());
 }
