@@ -19,6 +19,7 @@
 // dotted in K parts of 2048 with the h slices in LDS, and a last launch adds the
 // weighted parts per (token, row) in slot order.  Larger calls stage f32 h per
 // block, 4 tokens per pass.
+#include "decode.h"
 #include "decode_mfma.h"
 #include "rowdot.h"
 #include "segments.h"
@@ -433,7 +434,8 @@ down_split_kernel(BankArg down, int H, int I, int ks, int rpg, int tok_max, int 
 // segments (and of one call over both halves of a split by slot).
 __global__ void __launch_bounds__(64)
 down_combine_kernel(const float* dpart, int kparts, int n, int H, int rows, int width, const int* seg_count,
-                    const uint32_t* seg_begin, const uint32_t* perm, const float* w, int accumulate, float* out) {
+                    const uint32_t* seg_begin, const uint32_t* perm, const float* w, int accumulate, float* out,
+                    uint16_t* res) {
     __shared__ int list[kCombineTok][kCombineWidth];
     __shared__ int cnt[kCombineTok];
     static_assert(kCombineTok * kCombineWidth == 64, "one list entry per lane");
@@ -485,7 +487,9 @@ down_combine_kernel(const float* dpart, int kparts, int n, int H, int rows, int 
             }
             acc += wp * v;
         }
-        out[o] = acc;
+        // with res (bf16 [rows, H]): the residual x = bf16(x + y) of the same y, in place
+        if (res) res[o] = (uint16_t)naiwa_f32_to_bf16(naiwa_bf16_to_f32(res[o]) + acc);
+        if (out) out[o] = acc;
     }
 }
 
@@ -562,10 +566,10 @@ int check_args(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* d
 // out (token, row) from the K parts' unweighted dots in dpart.
 int combine_launch(const float* dpart, int kparts, int n, int H, int rows, int width, const int* seg_count,
                    const uint32_t* seg_begin, const uint32_t* perm, const float* w, int accumulate, float* out,
-                   hipStream_t st) {
+                   hipStream_t st, uint16_t* res = nullptr) {
     const dim3 cgrid((H + 63) / 64, (rows + kCombineTok - 1) / kCombineTok);
     down_combine_kernel<<<cgrid, 64, 0, st>>>(dpart, kparts, n, H, rows, width, seg_count, seg_begin, perm, w,
-                                               accumulate, out);
+                                               accumulate, out, res);
     return naiwa_hip_rc(hipGetLastError());
 }
 
@@ -576,10 +580,13 @@ template <int DG, int DD>
 int staged_kernels(BankArg g, BankArg u, BankArg d, const void* x, int xb, int H, int I, int rows, int width,
                    int act, const float* w, float* out, int accumulate, int n, int slots, const int* seg_count,
                    const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm, uint8_t* hst,
-                   float* dpart, SegIn seg_in, hipStream_t st) {
+                   float* dpart, SegIn seg_in, hipStream_t st, uint16_t* res) {
     constexpr int SPAN = Fmt<DD>::kSumSpan;
     const int stage_g = naiwa_stage_bytes(DG, H);
-    const int tok = std::max(1, std::min(kTokG, (64 * 1024) / stage_g));
+    // tokens staged per chunk: a segment holds at most `rows` tokens unless a token repeats
+    // a slot (the kernel then takes more chunks), and the LDS reservation sets how many
+    // blocks fit on a CU (one token at H 4096 is 9 KB against 63 KB for seven)
+    const int tok = std::max(1, std::min({kTokG, rows, (64 * 1024) / stage_g}));
     const int hst_stride = naiwa_stage_bytes(DD, I);
     // one column per possible segment: blocks past the segment count exit at once,
     // and each still costs a dispatch with its full LDS reservation
@@ -597,19 +604,20 @@ int staged_kernels(BankArg g, BankArg u, BankArg d, const void* x, int xb, int H
     const dim3 dgrid((H + groups * rpg - 1) / (groups * rpg), kparts, segs);
     down_split_kernel<DD><<<dgrid, kDownThreads, (size_t)tok_d * stage_d, st>>>(
         d, H, I, ks, rpg, tok_d, n, seg_count, seg_key, seg_begin, perm, hst, hst_stride, dpart);
-    return combine_launch(dpart, kparts, n, H, rows, width, seg_count, seg_begin, perm, w, accumulate, out, st);
+    return combine_launch(dpart, kparts, n, H, rows, width, seg_count, seg_begin, perm, w, accumulate, out, st,
+                          res);
 }
 
 int staged_launch(BankArg g, BankArg u, BankArg d, int gdt, int ddt, const void* x, int x_dtype, int H, int I,
                   int rows, int width, int act, const float* w, float* out, int accumulate, int n, int slots,
                   const int* seg_count, const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm,
-                  uint8_t* hst, float* dpart, SegIn seg_in, hipStream_t st) {
+                  uint8_t* hst, float* dpart, SegIn seg_in, hipStream_t st, uint16_t* res) {
     const int xb = x_dtype == NAIWA_BF16;
     const int fg = naiwa_kernel_fmt(gdt, H), fd = naiwa_kernel_fmt(ddt, I);
 #define NAIWA_STAGED(FG, FD)                                                                                       \
     if (fg == FG && fd == FD)                                                                                      \
         return staged_kernels<FG, FD>(g, u, d, x, xb, H, I, rows, width, act, w, out, accumulate, n, slots,         \
-                                      seg_count, seg_key, seg_begin, perm, hst, dpart, seg_in, st);
+                                      seg_count, seg_key, seg_begin, perm, hst, dpart, seg_in, st, res);
     NAIWA_STAGED(NAIWA_Q4_K, NAIWA_Q4_K)
     NAIWA_STAGED(NAIWA_Q4_K, NAIWA_Q8_0)
     NAIWA_STAGED(NAIWA_Q4_K, NAIWA_Q8_0_ODD)
@@ -624,9 +632,11 @@ int staged_launch(BankArg g, BankArg u, BankArg d, int gdt, int ddt, const void*
 }
 
 // The launches of one checked call over scratch ws (DecodeScratch(...).total bytes).
+// res (bf16 x, staged calls only): the ordered combine also adds the result to it in
+// place, x = bf16(x + y); out may then be null.
 int decode_launch(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, const void* x, int x_dtype,
                   const uint32_t* slot_ids, const float* w, int rows, int width, int act, float* out, int flags,
-                  uint8_t* ws, hipStream_t st) {
+                  uint8_t* ws, hipStream_t st, uint16_t* res = nullptr) {
     const int accumulate = (flags & NAIWA_DECODE_ACCUMULATE) ? 1 : 0;
     const int H = gate->k, I = gate->n;
     if (width == 0) {
@@ -669,11 +679,11 @@ int decode_launch(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank
                                                seg_key, seg_begin, perm, (uint8_t*)hbuf, dpart, st);
             if (rc) return rc;
             return combine_launch(dpart, split_parts(I), n, H, rows, width, seg_count, seg_begin, perm, w,
-                                  accumulate, out, st);
+                                  accumulate, out, st, res);
         }
         return staged_launch(g, u, d, gate->dtype, down->dtype, x, x_dtype, H, I, rows, width, act, w, out,
                              accumulate, n, gate->slots, seg_count, seg_key, seg_begin, perm, (uint8_t*)hbuf, dpart,
-                             seg_in, st);
+                             seg_in, st, res);
     }
     const dim3 ggrid(n, (I + kRowsPerBlock - 1) / kRowsPerBlock);
     const size_t lds_g = (size_t)tok_g * naiwa_stage_bytes(gate->dtype, H);
@@ -767,6 +777,23 @@ extern "C" int naiwa_moe_decode_noalloc(const naiwa_bank* gate, const naiwa_bank
     if ((rc = noalloc_scratch(&ws))) return rc;
     return decode_launch(gate, up, down, x, x_dtype, slot_ids, w, rows, width, act, out, flags, ws,
                          (hipStream_t)stream);
+}
+
+int naiwa_moe_decode_residual(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, void* x,
+                              const uint32_t* slot_ids, const float* w, int rows, int width, int act, float* y,
+                              int64_t stream) {
+    int rc = check_args(gate, up, down, x, NAIWA_BF16, slot_ids, w, rows, width, act, y, 0);
+    if (rc || rows == 0 || width == 0) return rc;
+    const DecodeScratch L(rows, width, gate->k, gate->n, down->dtype);
+    uint8_t* ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_DECODE, L.total, &rc);
+    if (!ws) return rc;
+    if (split_path(rows * width, width))
+        return decode_launch(gate, up, down, x, NAIWA_BF16, slot_ids, w, rows, width, act, nullptr, 0, ws,
+                             (hipStream_t)stream, (uint16_t*)x);
+    if ((rc = decode_launch(gate, up, down, x, NAIWA_BF16, slot_ids, w, rows, width, act, y, 0, ws,
+                            (hipStream_t)stream)))
+        return rc;
+    return naiwa_residual_add_bf16(x, y, (int64_t)rows * gate->k, stream);
 }
 
 extern "C" int naiwa_moe_decode(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down,

@@ -135,7 +135,10 @@ __device__ __forceinline__ uint2 naiwa_ld8(const void* p) {
 
 // Stage `k` activations (f32 source, or bf16 when src_bf16) into the perm
 // layout + sums of format DT.  All `nthr` threads of the block take part;
-// k % 32 == 0.  The caller synchronizes afterwards.
+// k % 32 == 0.  The caller synchronizes afterwards.  A thread issues the loads of
+// up to kStageRounds of its rounds before converting any, so staging costs one
+// memory round trip per kStageRounds rounds instead of one per round.
+constexpr int kStageRounds = 4;
 template <int DT, bool COH = false>
 __device__ inline void naiwa_stage(const void* src, bool src_bf16, int k, uint32_t* words,
                                    float* sums, int tid, int nthr) {
@@ -143,35 +146,49 @@ __device__ inline void naiwa_stage(const void* src, bool src_bf16, int k, uint32
     constexpr int gpg = span / 4; // 4-element groups per sum
     // Thread handles groups g = tid, tid + nthr, ...; nthr is a multiple of gpg
     // so the lanes summing one span sit in one aligned run of the wave.
-    for (int g0 = 0; g0 < k / 4; g0 += nthr) {
-        const int g = g0 + tid;
-        float part = 0.0f;
-        if (g < k / 4) {
-            float v[4];
-            if (src_bf16) {
-                const uint2 raw = naiwa_ld8<COH>((const uint16_t*)src + 4 * g);
-                v[0] = naiwa_bf16_to_f32(raw.x & 0xffffu);
-                v[1] = naiwa_bf16_to_f32(raw.x >> 16);
-                v[2] = naiwa_bf16_to_f32(raw.y & 0xffffu);
-                v[3] = naiwa_bf16_to_f32(raw.y >> 16);
-            } else {
-                const uint2 a = naiwa_ld8<COH>((const float*)src + 4 * g);
-                const uint2 b = naiwa_ld8<COH>((const float*)src + 4 * g + 2);
-                v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y);
-                v[2] = __uint_as_float(b.x); v[3] = __uint_as_float(b.y);
-            }
-            uint32_t h[4];
+    for (int g00 = 0; g00 < k / 4; g00 += kStageRounds * nthr) {
+        uint2 raw[kStageRounds][2];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                h[i] = Fmt<DT>::to16(v[i]);
-                v[i] = Fmt<DT>::from16(h[i]);
+        for (int i = 0; i < kStageRounds; ++i) {
+            const int g = g00 + i * nthr + tid;
+            if (g < k / 4) {
+                if (src_bf16) {
+                    raw[i][0] = naiwa_ld8<COH>((const uint16_t*)src + 4 * g);
+                } else {
+                    raw[i][0] = naiwa_ld8<COH>((const float*)src + 4 * g);
+                    raw[i][1] = naiwa_ld8<COH>((const float*)src + 4 * g + 2);
+                }
             }
-            words[2 * g] = h[0] | (h[2] << 16);
-            words[2 * g + 1] = h[1] | (h[3] << 16);
-            part = (v[0] + v[1]) + (v[2] + v[3]);
         }
-        part = naiwa_group_sum<gpg>(part);
-        if (g < k / 4 && (g % gpg) == 0) sums[g / gpg] = part;
+#pragma unroll
+        for (int i = 0; i < kStageRounds; ++i) {
+            if (g00 + i * nthr >= k / 4) break; // uniform: every lane takes the group sums
+            const int g = g00 + i * nthr + tid;
+            float part = 0.0f;
+            if (g < k / 4) {
+                float v[4];
+                if (src_bf16) {
+                    v[0] = naiwa_bf16_to_f32(raw[i][0].x & 0xffffu);
+                    v[1] = naiwa_bf16_to_f32(raw[i][0].x >> 16);
+                    v[2] = naiwa_bf16_to_f32(raw[i][0].y & 0xffffu);
+                    v[3] = naiwa_bf16_to_f32(raw[i][0].y >> 16);
+                } else {
+                    v[0] = __uint_as_float(raw[i][0].x); v[1] = __uint_as_float(raw[i][0].y);
+                    v[2] = __uint_as_float(raw[i][1].x); v[3] = __uint_as_float(raw[i][1].y);
+                }
+                uint32_t h[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    h[j] = Fmt<DT>::to16(v[j]);
+                    v[j] = Fmt<DT>::from16(h[j]);
+                }
+                words[2 * g] = h[0] | (h[2] << 16);
+                words[2 * g + 1] = h[1] | (h[3] << 16);
+                part = (v[0] + v[1]) + (v[2] + v[3]);
+            }
+            part = naiwa_group_sum<gpg>(part);
+            if (g < k / 4 && (g % gpg) == 0) sums[g / gpg] = part;
+        }
     }
 }
 

@@ -3,6 +3,7 @@
 //
 // NAIWA_STACK_LAYERED chains the standalone entry points (router top-k,
 // slot lookup, naiwa_moe_decode, residual) per layer.
+#include "decode.h"
 #include "router.h"
 #include "rowdot.h"
 #include "workspace.h"
@@ -80,11 +81,18 @@ extern "C" int naiwa_stack_decode_y(const naiwa_layer* layers, int n_layers, voi
             dec_ids = slots;
             dec_w = w_mapped;
         }
+        if (!y_out) {
+            // the residual in the decode's ordered combine where it can be (one launch fewer)
+            if ((rc = naiwa_moe_decode_residual(&L.gate, &L.up, &L.down, x, dec_ids, dec_w, rows, k, act, y,
+                                                stream)))
+                return rc;
+            continue;
+        }
         if ((rc = naiwa_moe_decode(&L.gate, &L.up, &L.down, x, NAIWA_BF16, dec_ids, dec_w, rows, k, act, y,
                                    stream)))
             return rc;
-        if (y_out && (rc = naiwa_hip_rc(hipMemcpyAsync(y_out + (size_t)l * rows * H, y, (size_t)rows * H * 4,
-                                                        hipMemcpyDeviceToDevice, st))))
+        if ((rc = naiwa_hip_rc(hipMemcpyAsync(y_out + (size_t)l * rows * H, y, (size_t)rows * H * 4,
+                                              hipMemcpyDeviceToDevice, st))))
             return rc;
         if ((rc = naiwa_residual_add_bf16(x, y, (int64_t)rows * H, stream))) return rc;
     }

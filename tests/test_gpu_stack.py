@@ -175,3 +175,32 @@ def test_fused_routing_ties_take_the_lower_id(gpu, rows, mode):
     assert np.array_equal(ids, want_ids), (ids, want_ids)
     assert np.allclose(w, want_w, rtol=1e-5, atol=1e-7)
     assert S.max_rel_err(y_d.download(np.float32).reshape(rows, H), y) < TOL
+
+
+@pytest.mark.parametrize("rows,E,k,dt", [
+    (1, 128, 8, (O.Q4_K,) * 3),   # one token: the staged GEMV path
+    (8, 128, 8, (O.Q4_K,) * 3),   # the matrix-core path
+    (80, 128, 8, (O.Q4_K,) * 3),  # 640 pairs: the unstaged path (residual launch)
+    (2, 64, 6, (O.Q4_K, O.Q4_K, O.Q8_0)),
+])
+def test_layered_residual_in_the_combine_is_bit_identical(gpu, rows, E, k, dt):
+    """The layered chain without per-layer outputs adds each layer's residual in the
+    decode's ordered combine; with them it keeps y and runs a residual launch.  Both
+    give the same routing and the same final x, bit for bit."""
+    nm = gpu
+    H, L = 2048, 2
+    I = 768 if dt[2] == O.Q4_K else 1408
+    layers, host, keep = build_stack(nm, L, H, E, I, dt, 970 + rows)
+    x = S.activations_bf16(971 + rows, rows, H)
+    outs = []
+    for want_y in (True, False):
+        xd = nm.DeviceBuffer.from_array(x)
+        ids_d = nm.DeviceBuffer(L * rows * k * 4)
+        y_d = nm.DeviceBuffer(L * rows * H * 4) if want_y else None
+        print(f"[layered residual rows={rows} E={E} k={k} y_out={want_y}]", flush=True)
+        nm.stack_decode(layers, xd, rows, H, E, k, mode=O.ROUTE_SOFTMAX_TOPK_RENORM, ids_out=ids_d,
+                        fused=False, y_out=y_d)
+        nm.synchronize()
+        outs.append((ids_d.download(np.uint32), xd.download(np.uint16)))
+    assert np.array_equal(outs[0][0], outs[1][0])
+    assert np.array_equal(outs[0][1], outs[1][1])
