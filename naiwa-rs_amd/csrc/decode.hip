@@ -213,8 +213,8 @@ constexpr int kTokD = 8;
 constexpr int kDownThreads = 256;
 constexpr int kSplitK = 2048;     // I elements per K part of the down projection
 constexpr int kCombineWidth = 16; // most pairs per token the combine orders
-constexpr int kCombineTok = 4;    // tokens per combine wave
 constexpr int kCombineParts = 8;  // K parts whose loads a combine lane issues at once
+constexpr int kCombinePairs = 8;  // pairs whose loads a combine lane issues at once
 
 // The staged-h path serves calls of at most kPairsMax pairs and kCombineWidth per token.
 bool split_path(int n, int width) { return n <= kPairsMax && width <= kCombineWidth; }
@@ -427,70 +427,85 @@ down_split_kernel(BankArg down, int H, int I, int ks, int rpg, int tok_max, int 
     }
 }
 
-// down_combine: one wave per (64 output rows, kCombineTok tokens).  Each token's
-// sorted positions are listed (weight-0 pairs have none) and ordered ascending;
-// out(t, r) starts at 0, or at out's value, and adds w * (the pair's K parts summed
-// in order) over those positions -- ascending slot, the order of one pass over all
-// segments (and of one call over both halves of a split by slot).
+// down_combine: one wave per (64 output rows, token).  The token's sorted positions
+// are listed (weight-0 pairs have none) with their routing weights, and ordered
+// ascending; out(t, r) starts at 0, or at out's value, and adds w * (the pair's K
+// parts summed in order) over those positions -- ascending slot, the order of one pass
+// over all segments (and of one call over both halves of a split by slot).  Each load
+// that does not depend on another is issued with the others, so a call costs a few
+// memory round trips: the segment count, the position count, the permutation and
+// weights, then every pair's parts (and the residual's x).
 __global__ void __launch_bounds__(64)
 down_combine_kernel(const float* dpart, int kparts, int n, int H, int rows, int width, const int* seg_count,
                     const uint32_t* seg_begin, const uint32_t* perm, const float* w, int accumulate, float* out,
                     uint16_t* res) {
-    __shared__ int list[kCombineTok][kCombineWidth];
-    __shared__ int cnt[kCombineTok];
-    static_assert(kCombineTok * kCombineWidth == 64, "one list entry per lane");
+    __shared__ int list[kCombineWidth];
+    __shared__ float wl[kCombineWidth];
+    __shared__ int cnt;
     const int lane = threadIdx.x;
-    const int t0 = blockIdx.y * kCombineTok;
-    const int tn = min(kCombineTok, rows - t0);
+    const int t = blockIdx.y;
     const int npos = (int)seg_begin[*seg_count];
-    (&list[0][0])[lane] = -1;
+    if (lane < kCombineWidth) list[lane] = -1;
     __syncthreads();
     for (int pos = lane; pos < npos; pos += 64) {
         const uint32_t p = perm[pos];
-        const int t = (int)(p / (uint32_t)width) - t0;
-        if (t >= 0 && t < tn) list[t][p % (uint32_t)width] = pos;
+        if ((int)(p / (uint32_t)width) == t) {
+            list[p % (uint32_t)width] = pos;
+            wl[p % (uint32_t)width] = w[p];
+        }
     }
     __syncthreads();
-    if (lane < tn) {
-        // insertion sort in place; entry j is read before any write reaches index j
+    if (lane == 0) {
+        // insertion sort of (position, weight) by position; entry j is read before
+        // any write reaches index j
         int c = 0;
         for (int j = 0; j < width; ++j) {
-            const int v = list[lane][j];
+            const int v = list[j];
             if (v < 0) continue;
+            const float wv = wl[j];
             int k = c++;
-            while (k > 0 && list[lane][k - 1] > v) {
-                list[lane][k] = list[lane][k - 1];
+            while (k > 0 && list[k - 1] > v) {
+                list[k] = list[k - 1];
+                wl[k] = wl[k - 1];
                 --k;
             }
-            list[lane][k] = v;
+            list[k] = v;
+            wl[k] = wv;
         }
-        cnt[lane] = c;
+        cnt = c;
     }
     __syncthreads();
     const int r = blockIdx.x * 64 + lane;
     if (r >= H) return;
-    for (int tt = 0; tt < tn; ++tt) {
-        const int64_t o = (int64_t)(t0 + tt) * H + r;
-        float acc = accumulate ? out[o] : 0.0f;
-        for (int k = 0; k < cnt[tt]; ++k) {
-            const int pos = list[tt][k];
-            const float wp = w[perm[pos]];
-            float v = 0.0f;
-            for (int k0 = 0; k0 < kparts; k0 += kCombineParts) {
-                float pv[kCombineParts];
+    const int64_t o = (int64_t)t * H + r;
+    const float x0 = res ? naiwa_bf16_to_f32(res[o]) : 0.0f;
+    float acc = accumulate ? out[o] : 0.0f;
+    const int c = cnt;
+    for (int k0 = 0; k0 < c; k0 += kCombinePairs) {
+        // the K-part dots of up to kCombinePairs pairs, their loads issued together;
+        // each pair's parts added in part order, then the pairs in list order
+        float v[kCombinePairs];
+        for (int p0 = 0; p0 < kparts; p0 += kCombineParts) {
+            float pv[kCombinePairs][kCombineParts];
+#pragma unroll
+            for (int q = 0; q < kCombinePairs; ++q)
 #pragma unroll
                 for (int i = 0; i < kCombineParts; ++i)
-                    if (k0 + i < kparts) pv[i] = dpart[((size_t)(k0 + i) * n + pos) * H + r];
+                    if (k0 + q < c && p0 + i < kparts)
+                        pv[q][i] = dpart[((size_t)(p0 + i) * n + list[k0 + q]) * H + r];
+#pragma unroll
+            for (int q = 0; q < kCombinePairs; ++q)
 #pragma unroll
                 for (int i = 0; i < kCombineParts; ++i)
-                    if (k0 + i < kparts) v = (k0 + i == 0) ? pv[i] : v + pv[i];
-            }
-            acc += wp * v;
+                    if (k0 + q < c && p0 + i < kparts) v[q] = (p0 + i == 0) ? pv[q][i] : v[q] + pv[q][i];
         }
-        // with res (bf16 [rows, H]): the residual x = bf16(x + y) of the same y, in place
-        if (res) res[o] = (uint16_t)naiwa_f32_to_bf16(naiwa_bf16_to_f32(res[o]) + acc);
-        if (out) out[o] = acc;
+#pragma unroll
+        for (int q = 0; q < kCombinePairs; ++q)
+            if (k0 + q < c) acc += wl[k0 + q] * v[q];
     }
+    // with res (bf16 [rows, H]): the residual x = bf16(x + y) of the same y, in place
+    if (res) res[o] = (uint16_t)naiwa_f32_to_bf16(x0 + acc);
+    if (out) out[o] = acc;
 }
 
 bool bank_ok(const naiwa_bank* b) {
@@ -567,7 +582,7 @@ int check_args(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* d
 int combine_launch(const float* dpart, int kparts, int n, int H, int rows, int width, const int* seg_count,
                    const uint32_t* seg_begin, const uint32_t* perm, const float* w, int accumulate, float* out,
                    hipStream_t st, uint16_t* res = nullptr) {
-    const dim3 cgrid((H + 63) / 64, (rows + kCombineTok - 1) / kCombineTok);
+    const dim3 cgrid((H + 63) / 64, rows);
     down_combine_kernel<<<cgrid, 64, 0, st>>>(dpart, kparts, n, H, rows, width, seg_count, seg_begin, perm, w,
                                                accumulate, out, res);
     return naiwa_hip_rc(hipGetLastError());
