@@ -505,23 +505,6 @@ gateup_kernel(Bank gate, Bank up, const uint16_t* xp, int H, int I, int k, const
     }
 }
 
-// (tile, column block) of a down block, or false past the last tile.  The hardware
-// deals consecutive workgroup ids to the 8 XCDs in turn, so in the plain order the
-// column blocks of one tile land on 8 XCDs and each XCD's L2 fetches the tile's h rows
-// again.  Here XCD x takes the x-th contiguous run of the tile-major (tile, column)
-// items instead: the column blocks of a tile share one L2 copy of its rows.  A
-// bijection of [0, ntiles * gridDim.x); the ids past that range exit.
-constexpr int kXcds = 8;
-__device__ __forceinline__ bool xcd_item(int ntiles, int& tile, int& col) {
-    const int gx = gridDim.x, id = blockIdx.x + gx * blockIdx.y, total = ntiles * gx;
-    if (id >= total) return false;
-    const int q = total / kXcds, r = total % kXcds, x = id % kXcds, loc = id / kXcds;
-    const int item = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + loc;
-    tile = item / gx;
-    col = item % gx;
-    return true;
-}
-
 // down: one tile of <= 64 pairs x 256 output features (32 per wave); pair rows
 // scaled by their weight.
 template <int DD>
@@ -530,8 +513,8 @@ down_kernel(Bank down, const uint16_t* hp, int H, int I, const uint32_t* perm, c
             float* ypair) {
     __shared__ ATile<DD> as[2];
     __shared__ int rows[kTM];
-    int tile, col;
-    if (!xcd_item(*tl.n, tile, col)) return;
+    const int tile = blockIdx.y, col = blockIdx.x;
+    if (tile >= *tl.n) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5;
     const int start = tl.start[tile], cnt = tl.count[tile], slot = tl.slot[tile];
     if (tid < kTM) rows[tid] = (start + min(tid, cnt - 1)) * I;

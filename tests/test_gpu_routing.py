@@ -33,6 +33,9 @@ def gpu_router(nm, x_bf16, W, k, mode, x_f32=False):
     (16, 4096, 8, 2, O.ROUTE_TOPK_SOFTMAX),           # Mixtral-8x7B
     (5, 2048, 64, 6, O.ROUTE_SOFTMAX_TOPK),           # DeepSeek-V2-Lite
     (3, 512, 1000, 32, O.ROUTE_SOFTMAX_TOPK_RENORM),  # wide E, large k
+    (512, 2048, 64, 6, O.ROUTE_SOFTMAX_TOPK),         # a DeepSeek-V2-Lite prefill chunk (tiled kernel)
+    (100, 4096, 8, 2, O.ROUTE_TOPK_SOFTMAX),          # Mixtral prefill rows, ragged row tile
+    (70, 2048, 130, 8, O.ROUTE_SOFTMAX_TOPK_RENORM),  # E not a multiple of the expert tile
 ])
 def test_router_bit_exact(gpu, rows, H, E, k, mode):
     x = S.activations_bf16(700 + rows, rows, H)
