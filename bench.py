@@ -32,19 +32,27 @@ Q4K_BLOCK, Q4K_BYTES = 256, 144
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "stack_kernel_qwen3_bs1_traffic.txt")
+PREFILL_TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "prefill_deepseek_v2_lite_traffic.txt")
 
 
-def measured_traffic(rows: int, layers: int, fused: bool):
-    """HBM bytes per launch of the fused kernel on this exact workload (bs1, 48
-    layers), from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, scaled
-    by a device copy of known size; None for any other workload."""
-    if not (fused and rows == 1 and layers == 48) or not os.path.exists(TRAFFIC_PROFILE):
+def profile_traffic(path: str):
+    """The traffic_bytes_per_launch line of a committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (scaled by a device copy of known size), or None."""
+    if not os.path.exists(path):
         return None
-    with open(TRAFFIC_PROFILE) as f:
+    with open(path) as f:
         for line in f:
             if line.startswith("traffic_bytes_per_launch:"):
                 return int(line.split(":")[1])
     return None
+
+
+def measured_traffic(rows: int, layers: int, fused: bool):
+    """HBM bytes per launch of the fused kernel on this exact workload (bs1, 48
+    layers); None for any other workload."""
+    if not (fused and rows == 1 and layers == 48):
+        return None
+    return profile_traffic(TRAFFIC_PROFILE)
 
 
 def log(msg: str) -> None:
@@ -183,14 +191,7 @@ def main() -> int:
     assert (ids < E).all() and np.allclose(ws.sum(-1), 1.0, atol=1e-4), "routing output invalid"
 
     if args.calibrate_copy:
-        nbytes = args.calibrate_copy << 20
-        a, b = nm.DeviceBuffer(nbytes), nm.DeviceBuffer(nbytes)
-        a.zero(stream.handle)
-        stream.sync()
-        lib.naiwa_memcpy_d2d(b.ptr, a.ptr, nbytes, stream.handle)
-        stream.sync()
-        log(f"calibration copy: {nbytes} bytes device to device")
-        del a, b
+        calibration_copy(nm, args.calibrate_copy, stream)
 
     if args.trace and fused:
         print_trace(nm, lambda: step(0, False), stream, L, info["wall_clock_khz"])
@@ -276,6 +277,19 @@ def main() -> int:
     }
     print(json.dumps(result), flush=True)
     return 0
+
+
+def calibration_copy(nm, mib, stream) -> None:
+    """One device-to-device copy of mib MiB, so a counter profile of the same process
+    can be scaled by what its counters read for bytes of known size."""
+    nbytes = mib << 20
+    a, b = nm.DeviceBuffer(nbytes), nm.DeviceBuffer(nbytes)
+    a.zero(stream.handle)
+    stream.sync()
+    nm.lib().naiwa_memcpy_d2d(b.ptr, a.ptr, nbytes, stream.handle)
+    stream.sync()
+    log(f"calibration copy: {nbytes} bytes device to device")
+    del a, b
 
 
 def print_trace(nm, run, stream, L, khz):
@@ -998,6 +1012,8 @@ def run_prefill(args) -> int:
         step()
     stream.sync()
     nm.prefill_status()
+    if args.calibrate_copy:
+        calibration_copy(nm, args.calibrate_copy, stream)
     e0, e1 = nm.Event(), nm.Event()
     e0.record(stream.handle)
     for _ in range(steps):
@@ -1058,7 +1074,7 @@ def run_prefill(args) -> int:
                    "layers": L, "hidden": H, "experts": E, "shared": S_, "top_k": K, "intermediate": I,
                    "chunk": T, "tokens": tokens, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(hbm, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(hbm / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(hbm / HBM_PEAK_GBS, 4), "traffic": profile_traffic(PREFILL_TRAFFIC_PROFILE),
                      "kernel": "naiwa_moe_prefill (one 512-token layer-chunk: gather, tiles, GEMMs, combine)",
                      "bytes_per_launch": call_bytes, "call_avg_us": round(call_ms * 1e3, 2),
                      "mfma_tflops": round(call_flop / (call_ms / 1e3) / 1e12, 2),

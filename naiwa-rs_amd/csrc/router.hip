@@ -173,9 +173,12 @@ extern "C" int naiwa_router_topk_biased(const void* x, int x_dtype, const float*
         logits = (float*)naiwa_scratch(NAIWA_SCRATCH_ROUTER, (size_t)rows * E * 4, &rc);
         if (!logits) return rc;
     }
-    if (rows <= kLogitFewRows) {
-        router_logits_kernel<<<dim3((unsigned)E, (unsigned)rows), kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, W,
-                                                                                          bias, rows, H, E, logits);
+    // one block per (expert, row) for few rows, and whenever the 16-row blocks would not
+    // fill the CUs (Mixtral at 64 rows: 32 of them); the same bits either way
+    const int64_t row_blocks = (int64_t)E * ((rows + kLogitRows - 1) / kLogitRows);
+    if (rows <= kLogitFewRows || row_blocks < 256) {
+        router_logits_kernel<<<dim3((unsigned)E, (unsigned)std::min(rows, 65535)), kLogitThreads, 0, st>>>(
+            x, x_dtype == NAIWA_BF16, W, bias, rows, H, E, logits);
     } else {
         const dim3 lg((unsigned)E, (unsigned)((rows + kLogitRows - 1) / kLogitRows));
         router_logits_rows_kernel<<<lg, kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, W, bias, rows, H, E, logits);
