@@ -553,17 +553,21 @@ combine_kernel(const float* ypair, const uint32_t* ids, int k, int H, int slots,
     for (int c = blockIdx.y * kThreads + threadIdx.x; c < HV; c += kThreads * gridDim.y) {
         vec y = accumulate ? o[c] : vec(0.0f);
         for (int j0 = 0; j0 < k; j0 += kJ) {
+            // every pair row of the token is in the buffer: its load does not wait for the
+            // slot id, which only decides whether the row is added
             vec v[kJ];
-            bool ok[kJ];
+            uint32_t id[kJ];
 #pragma unroll
             for (int u = 0; u < kJ; ++u) {
                 const int j = j0 + u;
-                ok[u] = j < k && ids[(size_t)t * k + j] < (uint32_t)slots;
-                if (ok[u]) v[u] = yp[(size_t)j * HV + c];
+                if (j < k) {
+                    id[u] = ids[(size_t)t * k + j];
+                    v[u] = yp[(size_t)j * HV + c];
+                }
             }
 #pragma unroll
             for (int u = 0; u < kJ; ++u)
-                if (ok[u]) y += v[u];
+                if (j0 + u < k && id[u] < (uint32_t)slots) y += v[u];
         }
         o[c] = y;
     }
