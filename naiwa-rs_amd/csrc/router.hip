@@ -22,7 +22,11 @@ constexpr int kLogitRows = 16;    // rows per block of the many-row kernel: 4 pe
 constexpr int kLogitFewRows = 32; // up to this many rows, one block per (expert, row)
 
 // logits[t, e] for many rows: expert e = blockIdx.x and rows blockIdx.y * 16 + 0..15,
-// one wave per row at a time; lane l takes the chunks l, l + 64, ...
+// one wave per row at a time; lane l takes the chunks l, l + 64, ...  CPL > 0: exactly
+// CPL chunks per lane (H = 512 CPL); the expert's router chunks are loaded once and
+// kept in registers, and a row's activation chunks are loaded together.  CPL = 0: any
+// H, one chunk at a time.  Each chunk is the same f32 fma chain rounded to int64.
+template <int CPL>
 __global__ void __launch_bounds__(kLogitThreads)
 router_logits_rows_kernel(const void* x, int x_bf16, const float* W, const float* bias, int rows, int H, int E,
                           float* logits) {
@@ -30,12 +34,35 @@ router_logits_rows_kernel(const void* x, int x_bf16, const float* W, const float
     const int nchunks = H / NAIWA_ROUTER_CHUNK;
     const float* wr = W + (int64_t)e * H;
     const int t0 = blockIdx.y * kLogitRows;
+    float wv[CPL > 0 ? CPL : 1][8];
+    if constexpr (CPL > 0) {
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const float4* src = reinterpret_cast<const float4*>(wr + 8 * (lane + 64 * i));
+            const float4 a = src[0], b = src[1];
+            wv[i][0] = a.x; wv[i][1] = a.y; wv[i][2] = a.z; wv[i][3] = a.w;
+            wv[i][4] = b.x; wv[i][5] = b.y; wv[i][6] = b.z; wv[i][7] = b.w;
+        }
+    }
     for (int t = t0 + wave; t < min(rows, t0 + kLogitRows); t += kLogitThreads / 64) {
         long long acc = 0;
-        for (int c = lane; c < nchunks; c += 64) {
-            float xv[8];
-            naiwa_load_x8(x, x_bf16, (int64_t)t * H + 8 * c, xv);
-            acc += naiwa_router_chunk(wr + 8 * c, xv);
+        if constexpr (CPL > 0) {
+            float xv[CPL][8];
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) naiwa_load_x8(x, x_bf16, (int64_t)t * H + 8 * (lane + 64 * i), xv[i]);
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                float p = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) p = __builtin_fmaf(wv[i][q], xv[i][q], p);
+                acc += (long long)__builtin_rintf(p * 4294967296.0f);
+            }
+        } else {
+            for (int c = lane; c < nchunks; c += 64) {
+                float xv[8];
+                naiwa_load_x8(x, x_bf16, (int64_t)t * H + 8 * c, xv);
+                acc += naiwa_router_chunk(wr + 8 * c, xv);
+            }
         }
         acc = naiwa_wave_sum_i64(acc);
         if (lane == 0) logits[(int64_t)t * E + e] = naiwa_router_fix_to_f32(acc) + (bias ? bias[e] : 0.0f);
@@ -181,7 +208,13 @@ extern "C" int naiwa_router_topk_biased(const void* x, int x_dtype, const float*
             x, x_dtype == NAIWA_BF16, W, bias, rows, H, E, logits);
     } else {
         const dim3 lg((unsigned)E, (unsigned)((rows + kLogitRows - 1) / kLogitRows));
-        router_logits_rows_kernel<<<lg, kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, W, bias, rows, H, E, logits);
+        const int xb = x_dtype == NAIWA_BF16;
+        if (H == 512 * 4)
+            router_logits_rows_kernel<4><<<lg, kLogitThreads, 0, st>>>(x, xb, W, bias, rows, H, E, logits);
+        else if (H == 512 * 8)
+            router_logits_rows_kernel<8><<<lg, kLogitThreads, 0, st>>>(x, xb, W, bias, rows, H, E, logits);
+        else
+            router_logits_rows_kernel<0><<<lg, kLogitThreads, 0, st>>>(x, xb, W, bias, rows, H, E, logits);
     }
     router_topk_kernel<<<rows, kTopkThreads, 0, st>>>(logits, E, k, mode, ids_out, w_out);
     return naiwa_hip_rc(hipGetLastError());

@@ -35,7 +35,9 @@ def gpu_router(nm, x_bf16, W, k, mode, x_f32=False):
     (3, 512, 1000, 32, O.ROUTE_SOFTMAX_TOPK_RENORM),  # wide E, large k
     (512, 2048, 64, 6, O.ROUTE_SOFTMAX_TOPK),         # a DeepSeek-V2-Lite prefill chunk (tiled kernel)
     (100, 4096, 8, 2, O.ROUTE_TOPK_SOFTMAX),          # Mixtral prefill rows, ragged row tile
-    (70, 2048, 130, 8, O.ROUTE_SOFTMAX_TOPK_RENORM),  # E not a multiple of the expert tile
+    (70, 2048, 130, 8, O.ROUTE_SOFTMAX_TOPK_RENORM),  # 16-row blocks, 5 row groups
+    (300, 4096, 16, 2, O.ROUTE_TOPK_SOFTMAX),         # 16-row blocks at H 4096
+    (40, 1024, 128, 8, O.ROUTE_SOFTMAX_TOPK_RENORM),  # 16-row blocks at another H
 ])
 def test_router_bit_exact(gpu, rows, H, E, k, mode):
     x = S.activations_bf16(700 + rows, rows, H)
