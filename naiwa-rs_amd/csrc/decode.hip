@@ -369,15 +369,20 @@ down_split_kernel(BankArg down, int H, int I, int ks, int rpg, int tok_max, int 
     for (int c0 = b; c0 < e; c0 += tok_max) {
         const int nt = min(tok_max, e - c0);
         __syncthreads();
-        for (int i = tid; i < nt * nw4; i += kDownThreads) {
-            const int tt = i / nw4, j = i % nw4;
-            const uint8_t* src = hst + (size_t)perm[c0 + tt] * hst_stride + (size_t)k0 * 2;
-            reinterpret_cast<uint4*>(smem + tt * tstride)[j] = reinterpret_cast<const uint4*>(src)[j];
-        }
-        for (int i = tid; i < nt * nsum; i += kDownThreads) {
-            const int tt = i / nsum, j = i % nsum;
-            const float* sums = reinterpret_cast<const float*>(hst + (size_t)perm[c0 + tt] * hst_stride + (size_t)I * 2);
-            reinterpret_cast<float*>(smem + tt * tstride + wb)[j] = sums[k0 / SPAN + j];
+        // the h words and sums of the chunk's tokens: a thread's first word piece and first
+        // sum are loaded together, the rest (more tokens) one round after another
+        for (int i = tid; i < nt * max(nw4, nsum); i += kDownThreads) {
+            const int tw = i / nw4, jw = i % nw4, ts = i / nsum, js = i % nsum;
+            const bool w_in = i < nt * nw4, s_in = i < nt * nsum;
+            uint4 wv = make_uint4(0u, 0u, 0u, 0u);
+            float sv = 0.0f;
+            if (w_in)
+                wv = reinterpret_cast<const uint4*>(hst + (size_t)perm[c0 + tw] * hst_stride + (size_t)k0 * 2)[jw];
+            if (s_in)
+                sv = reinterpret_cast<const float*>(hst + (size_t)perm[c0 + ts] * hst_stride +
+                                                    (size_t)I * 2)[k0 / SPAN + js];
+            if (w_in) reinterpret_cast<uint4*>(smem + tw * tstride)[jw] = wv;
+            if (s_in) reinterpret_cast<float*>(smem + ts * tstride + wb)[js] = sv;
         }
         __syncthreads();
         for (int i = 0; i < rpg; i += 2) {
