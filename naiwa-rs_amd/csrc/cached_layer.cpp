@@ -18,6 +18,7 @@
 
 #include "../../include/naiwa_cached.h"
 #include "common.h"
+#include "decode.h"
 #include "router.h"
 #include "upload.h"
 
@@ -322,9 +323,12 @@ namespace {
 // One decode step of L; with `next`, also the next layer's lookahead on the same
 // activation: its router runs beside L's before the one routing read-back, and
 // its uploads are queued after L's expert kernel, so they overlap L's compute.
+// res_x (the stack driver's x, or null): when the step runs one expert pass, that pass
+// also adds its output to res_x in place (x = bf16(x + out)) and *folded is set.
 int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_row, const void* x, int rows,
                  float* out, float pcie_frac, int promote_cap, uint64_t min_hits, int64_t stream,
-                 naiwa_cached_step* info, naiwa_lookahead_step* ahead) {
+                 naiwa_cached_step* info, naiwa_lookahead_step* ahead, void* res_x = nullptr,
+                 bool* folded = nullptr) {
     if (!L || !x || !out || rows <= 0 || swaps_per_row < 0) return NAIWA_E_INVALID;
     if (next && (next == L || next->d.hidden != L->d.hidden)) return NAIWA_E_INVALID;
     const naiwa_cached_layer_desc& d = L->d;
@@ -456,9 +460,16 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
                       : naiwa_hip_rc(hipStreamWaitEvent(st, L->staged_done, 0));
             if (rc) return rc;
         }
-        if ((rc = naiwa_moe_decode(&d.gate, &d.up, &d.down, x, NAIWA_BF16, L->slots_dev, L->w_dev, rows, k, d.act,
-                                   out, stream)))
+        if (res_x) {
+            // out keeps the layer's output; the residual rides in the ordered combine
+            if ((rc = naiwa_moe_decode_residual(&d.gate, &d.up, &d.down, res_x, L->slots_dev, L->w_dev, rows, k,
+                                                d.act, out, 1, stream)))
+                return rc;
+            if (folded) *folded = true;
+        } else if ((rc = naiwa_moe_decode(&d.gate, &d.up, &d.down, x, NAIWA_BF16, L->slots_dev, L->w_dev, rows, k,
+                                          d.act, out, stream))) {
             return rc;
+        }
     } else {
         // the cache pairs first, while the staged experts are still on the wire, then the
         // staged pairs added on top: ring slots sort after cache slots, so the two calls
@@ -714,9 +725,10 @@ int naiwa_cached_stack_forward(naiwa_cached_layer* const* layers, int n_layers, 
         naiwa_cached_step s{};
         naiwa_lookahead_step a{};
         const bool ahead = lookahead_swaps >= 0 && l + 1 < n_layers;
+        bool folded = false;
         int rc = forward_impl(layers[l], ahead ? layers[l + 1] : nullptr, ahead ? lookahead_swaps : 0, x, rows, y,
-                              pcie_frac, promote_cap, min_hits, stream, &s, ahead ? &a : nullptr);
-        if (!rc) rc = naiwa_residual_add_bf16(x, y, (int64_t)rows * H, stream);
+                              pcie_frac, promote_cap, min_hits, stream, &s, ahead ? &a : nullptr, x, &folded);
+        if (!rc && !folded) rc = naiwa_residual_add_bf16(x, y, (int64_t)rows * H, stream);
         if (rc) return rc;
         if (total) {
             total->hits += s.hits;

@@ -801,15 +801,15 @@ extern "C" int naiwa_moe_decode_noalloc(const naiwa_bank* gate, const naiwa_bank
 
 int naiwa_moe_decode_residual(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, void* x,
                               const uint32_t* slot_ids, const float* w, int rows, int width, int act, float* y,
-                              int64_t stream) {
+                              int keep_y, int64_t stream) {
     int rc = check_args(gate, up, down, x, NAIWA_BF16, slot_ids, w, rows, width, act, y, 0);
     if (rc || rows == 0 || width == 0) return rc;
     const DecodeScratch L(rows, width, gate->k, gate->n, down->dtype);
     uint8_t* ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_DECODE, L.total, &rc);
     if (!ws) return rc;
     if (split_path(rows * width, width))
-        return decode_launch(gate, up, down, x, NAIWA_BF16, slot_ids, w, rows, width, act, nullptr, 0, ws,
-                             (hipStream_t)stream, (uint16_t*)x);
+        return decode_launch(gate, up, down, x, NAIWA_BF16, slot_ids, w, rows, width, act, keep_y ? y : nullptr, 0,
+                             ws, (hipStream_t)stream, (uint16_t*)x);
     if ((rc = decode_launch(gate, up, down, x, NAIWA_BF16, slot_ids, w, rows, width, act, y, 0, ws,
                             (hipStream_t)stream)))
         return rc;

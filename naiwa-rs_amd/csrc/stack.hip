@@ -83,7 +83,7 @@ extern "C" int naiwa_stack_decode_y(const naiwa_layer* layers, int n_layers, voi
         }
         if (!y_out) {
             // the residual in the decode's ordered combine where it can be (one launch fewer)
-            if ((rc = naiwa_moe_decode_residual(&L.gate, &L.up, &L.down, x, dec_ids, dec_w, rows, k, act, y,
+            if ((rc = naiwa_moe_decode_residual(&L.gate, &L.up, &L.down, x, dec_ids, dec_w, rows, k, act, y, 0,
                                                 stream)))
                 return rc;
             continue;
