@@ -340,6 +340,15 @@ def print_trace(nm, run, stream, L, khz):
         ", ".join(f"{n} {np.mean(v):.2f}" for n, v in med.items() if v))
     log("trace: critical path us/layer: " + ", ".join(f"{n} {np.mean(v):.2f}" for n, v in crit.items()) +
         f" | sum {sum(np.mean(v) for n, v in crit.items() if n != 'h recv spread'):.2f}")
+    land = t[:, : L - 1, 21] - t[:, : L - 1, 3]
+    log(f"trace: gate/up rows landed, last wave after wave 0: median {np.median(land):.2f} us; "
+        f"last wave's compute {np.median(t[:, : L - 1, 16] - t[:, : L - 1, 21]):.2f}; "
+        f"wave 0's first round {np.median(t[:, : L - 1, 22] - t[:, : L - 1, 3]):.2f}")
+    cyc = np.frombuffer(buf, dtype=np.uint64)[: G * (L + 1) * slots].reshape(G, L + 1, slots)[:, :L, 23]
+    dc = np.diff(cyc.astype(np.float64), axis=1)
+    dt_us = np.diff(t[:, :L, 2], axis=1)
+    log(f"trace: shader clock over the layers: median {np.median(dc / dt_us):.0f} MHz "
+        f"(min {np.min(dc / dt_us):.0f}, max {np.max(dc / dt_us):.0f})")
     gu = t[:, : L - 1, 4] - t[:, : L - 1, 3]
     log(f"trace: gate_up (issue->done) us: median {np.median(gu):.2f} p90 {np.percentile(gu, 90):.2f} "
         f"max {gu.max():.2f}; recv spread {np.mean(t[:, :L-1, 0].max(0) - t[:, :L-1, 0].min(0)):.2f}")

@@ -231,15 +231,20 @@ int mfma_rows() {
 int split_ks(int I) { return I <= kSplitK ? I : kSplitK; }
 int split_parts(int I) { return (I + split_ks(I) - 1) / split_ks(I); }
 
-template <int DG, int DD>
-__global__ void __launch_bounds__(512)
+// TG: tokens staged per chunk at most (1, 4 or 8).  Calls of few tokens take a
+// small TG: the accumulators of more tokens would hold registers, and with them the
+// occupancy.  With TG <= 4 a Q4_K lane also loads 2 units of each row per round
+// instead of 4; at 136-152 VGPRs a SIMD then keeps 3 waves instead of 2 (Mixtral
+// bs1 367 -> 445 tok/s).
+template <int DG, int DD, int TG>
+__global__ void __launch_bounds__(512, TG == 1 || (TG <= 4 && DG != NAIWA_Q8_0) ? 3 : 1)
 gate_up_staged_kernel(BankArg gate, BankArg up, const void* x, int x_bf16, int H, int I, int width, int tok_max,
                       const int* seg_count, const uint32_t* seg_key, const uint32_t* seg_begin,
                       const uint32_t* perm, int act, uint8_t* hst, int hst_stride, SegIn seg_in) {
     constexpr int SPAN = Fmt<DD>::kSumSpan;   // rows per block (one group of 16 lanes each)
     constexpr int GPG = SPAN / 4;             // 4-row groups per sum
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ float hloc[kTokG][SPAN];
+    __shared__ float hloc[TG][SPAN];
     __shared__ uint32_t l_perm[kSmallSeg], l_key[kSmallSeg], l_begin[kSmallSeg + 1];
     __shared__ int l_count;
     if (seg_in.slot_ids) {
@@ -268,7 +273,7 @@ gate_up_staged_kernel(BankArg gate, BankArg up, const void* x, int x_bf16, int H
     const uint8_t* grow = gate.base + (int64_t)slot * gate.stride + (int64_t)r * gate.row_bytes;
     const uint8_t* urow = up.base + (int64_t)slot * up.stride + (int64_t)r * up.row_bytes;
     const int nu = Fmt<DG>::units(H);
-    constexpr int UM = Umax<DG>::v;
+    constexpr int UM = TG <= 4 && DG == NAIWA_Q4_K ? 2 : Umax<DG>::v;
     for (int c0 = b; c0 < e; c0 += tok_max) {
         const int nt = min(tok_max, e - c0);
         __syncthreads();
@@ -280,9 +285,9 @@ gate_up_staged_kernel(BankArg gate, BankArg up, const void* x, int x_bf16, int H
             naiwa_stage<DG>(src, x_bf16 != 0, H, words, (float*)(words + H / 2), tid, SPAN * NAIWA_GROUP);
         }
         __syncthreads();
-        float ag[kTokG], au[kTokG];
+        float ag[TG], au[TG];
 #pragma unroll
-        for (int tt = 0; tt < kTokG; ++tt) ag[tt] = au[tt] = 0.0f;
+        for (int tt = 0; tt < TG; ++tt) ag[tt] = au[tt] = 0.0f;
         if (r < I) {
             for (int base = lr; base < nu; base += NAIWA_GROUP * UM) {
                 typename Fmt<DG>::Frag fg[UM], fu[UM];
@@ -299,7 +304,7 @@ gate_up_staged_kernel(BankArg gate, BankArg up, const void* x, int x_bf16, int H
                     const int u = base + NAIWA_GROUP * i;
                     if (u >= nu) continue;
 #pragma unroll
-                    for (int tt = 0; tt < kTokG; ++tt) {
+                    for (int tt = 0; tt < TG; ++tt) {
                         if (tt >= nt) break;
                         const uint32_t* words = (const uint32_t*)(smem + tt * stage);
                         const float* sums = (const float*)(words + H / 2);
@@ -310,7 +315,7 @@ gate_up_staged_kernel(BankArg gate, BankArg up, const void* x, int x_bf16, int H
             }
         }
 #pragma unroll
-        for (int tt = 0; tt < kTokG; ++tt) {
+        for (int tt = 0; tt < TG; ++tt) {
             const float g = naiwa_group_sum<NAIWA_GROUP>(ag[tt]);
             const float u = naiwa_group_sum<NAIWA_GROUP>(au[tt]);
             if (tt < nt && lr == 0) hloc[tt][grp] = r < I ? naiwa_act(act, g) * u : 0.0f;
@@ -347,14 +352,16 @@ gate_up_staged_kernel(BankArg gate, BankArg up, const void* x, int x_bf16, int H
 // copied from hst into LDS, and each 16-lane group streams its rows' slices,
 // two rows at a time, dotting every unit with every staged token.  The unweighted
 // partial dot of (K part, sorted position, row) goes to dpart.
-template <int DD>
-__global__ void __launch_bounds__(kDownThreads)
+// TD: tokens staged per chunk at most (1, 4 or 8), as TG of gate/up; one token of a
+// Q4_K down projection loads 2 units per round and fits 4 waves a SIMD.
+template <int DD, int TD>
+__global__ void __launch_bounds__(kDownThreads, TD == 1 ? (DD == NAIWA_Q4_K ? 4 : 3) : (TD <= 4 ? 3 : 1))
 down_split_kernel(BankArg down, int H, int I, int ks, int rpg, int tok_max, int n, const int* seg_count,
                   const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm, const uint8_t* hst,
                   int hst_stride, float* dpart) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int SPAN = Fmt<DD>::kSumSpan;
-    constexpr int UM = Umax<DD>::v;
+    constexpr int UM = TD == 1 && DD == NAIWA_Q4_K ? 2 : Umax<DD>::v;
     const int sgi = blockIdx.z;
     if (sgi >= *seg_count) return;
     const int tid = threadIdx.x, grp = tid / NAIWA_GROUP, lr = tid % NAIWA_GROUP;
@@ -391,9 +398,9 @@ down_split_kernel(BankArg down, int H, int I, int ks, int rpg, int tok_max, int 
             const bool two = i + 1 < rpg && r + 1 < H;
             const uint8_t* drow0 = dslot + (int64_t)r * down.row_bytes;
             const uint8_t* drow1 = drow0 + (two ? down.row_bytes : 0);
-            float a0[kTokD], a1[kTokD];
+            float a0[TD], a1[TD];
 #pragma unroll
-            for (int tt = 0; tt < kTokD; ++tt) a0[tt] = a1[tt] = 0.0f;
+            for (int tt = 0; tt < TD; ++tt) a0[tt] = a1[tt] = 0.0f;
             for (int base = lr; base < nus; base += NAIWA_GROUP * UM) {
                 typename Fmt<DD>::Frag f0[UM], f1[UM];
 #pragma unroll
@@ -409,7 +416,7 @@ down_split_kernel(BankArg down, int H, int I, int ks, int rpg, int tok_max, int 
                     const int u = base + NAIWA_GROUP * q;
                     if (u >= nus) continue;
 #pragma unroll
-                    for (int tt = 0; tt < kTokD; ++tt) {
+                    for (int tt = 0; tt < TD; ++tt) {
                         if (tt >= nt) break;
                         const uint32_t* words = reinterpret_cast<const uint32_t*>(smem + tt * tstride);
                         const float* sums = reinterpret_cast<const float*>(smem + tt * tstride + wb);
@@ -611,8 +618,15 @@ int staged_kernels(BankArg g, BankArg u, BankArg d, const void* x, int xb, int H
     // one column per possible segment: blocks past the segment count exit at once,
     // and each still costs a dispatch with its full LDS reservation
     const dim3 ggrid(std::max(1, std::min(n, slots)), I / SPAN);
-    gate_up_staged_kernel<DG, DD><<<ggrid, SPAN * NAIWA_GROUP, (size_t)tok * stage_g, st>>>(
-        g, u, x, xb, H, I, width, tok, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride, seg_in);
+    if (tok == 1)
+        gate_up_staged_kernel<DG, DD, 1><<<ggrid, SPAN * NAIWA_GROUP, (size_t)stage_g, st>>>(
+            g, u, x, xb, H, I, width, 1, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride, seg_in);
+    else if (tok <= 4)
+        gate_up_staged_kernel<DG, DD, 4><<<ggrid, SPAN * NAIWA_GROUP, (size_t)tok * stage_g, st>>>(
+            g, u, x, xb, H, I, width, tok, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride, seg_in);
+    else
+        gate_up_staged_kernel<DG, DD, kTokG><<<ggrid, SPAN * NAIWA_GROUP, (size_t)tok * stage_g, st>>>(
+            g, u, x, xb, H, I, width, tok, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride, seg_in);
     // down: rows per group doubled while the grid keeps at least 1024 blocks
     const int ks = split_ks(I), kparts = split_parts(I);
     const int segs = std::max(1, std::min(n, slots));
@@ -622,8 +636,15 @@ int staged_kernels(BankArg g, BankArg u, BankArg d, const void* x, int xb, int H
     const int stage_d = naiwa_stage_bytes(DD, ks);
     const int tok_d = std::max(1, std::min({kTokD, rows, (64 * 1024) / stage_d}));
     const dim3 dgrid((H + groups * rpg - 1) / (groups * rpg), kparts, segs);
-    down_split_kernel<DD><<<dgrid, kDownThreads, (size_t)tok_d * stage_d, st>>>(
-        d, H, I, ks, rpg, tok_d, n, seg_count, seg_key, seg_begin, perm, hst, hst_stride, dpart);
+    if (tok_d == 1)
+        down_split_kernel<DD, 1><<<dgrid, kDownThreads, (size_t)stage_d, st>>>(
+            d, H, I, ks, rpg, 1, n, seg_count, seg_key, seg_begin, perm, hst, hst_stride, dpart);
+    else if (tok_d <= 4)
+        down_split_kernel<DD, 4><<<dgrid, kDownThreads, (size_t)tok_d * stage_d, st>>>(
+            d, H, I, ks, rpg, tok_d, n, seg_count, seg_key, seg_begin, perm, hst, hst_stride, dpart);
+    else
+        down_split_kernel<DD, kTokD><<<dgrid, kDownThreads, (size_t)tok_d * stage_d, st>>>(
+            d, H, I, ks, rpg, tok_d, n, seg_count, seg_key, seg_begin, perm, hst, hst_stride, dpart);
     return combine_launch(dpart, kparts, n, H, rows, width, seg_count, seg_begin, perm, w, accumulate, out, st,
                           res);
 }

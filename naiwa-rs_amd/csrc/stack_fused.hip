@@ -1065,6 +1065,7 @@ stack_kernel(Params p) {
         const int nseg = sm.nseg;
         const int nvalid = (int)sm.seg_begin[nseg];
         mark(p, l, 2);
+        if (threadIdx.x == 0) trace_put(p, l, 23, clock64()); // shader clock beside the real-time one
 
         // ---- B: gate/up ----
         const int total = nseg * (I / 2);        // (segment, row pair) items
@@ -1127,10 +1128,12 @@ stack_kernel(Params p) {
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 if (r0 == q0) {
                     mark(p, l, 3);
+                    mark_wave(p, l, 21); // every wave: the last one to land wins
                     prefetch_down();
                 }
                 if (my_item < nr)
                     q4_pair_compute<DD>(p, sm, dyn, xstage, r0 + my_item, nb, il, wb + my_item * item_bytes, rb, tag);
+                if (r0 == q0 && wave == 0) mark_wave(p, l, 22);
             }
             mark_wave(p, l, 16); // every wave: the last one to store wins
             if (q0 >= q1) {
