@@ -213,9 +213,13 @@ __device__ __forceinline__ float naiwa_q4k_unit(uint4 q, uint4 hd, int c, const 
     }
     const float d = naiwa_f16_to_f32(hd.x & 0xffffu);
     const float dmin = naiwa_f16_to_f32(hd.x >> 16);
-    const float qlo = alo - 128.0f * slo; // sum q * x over the low run
-    const float qhi = ahi - 128.0f * shi;
-    return d * ((float)sc0 * qlo + (float)sc1 * qhi) - dmin * ((float)m0 * slo + (float)m1 * shi);
+    // every multiply-add is an explicit fma or stays apart, so no kernel that inlines
+    // this gets a different contraction (and different bits) than another
+    const float qlo = __builtin_fmaf(-128.0f, slo, alo); // sum q * x over the low run
+    const float qhi = __builtin_fmaf(-128.0f, shi, ahi);
+    const float sq = __builtin_fmaf((float)sc0, qlo, (float)sc1 * qhi);
+    const float mm = __builtin_fmaf((float)m0, slo, (float)m1 * shi);
+    return __builtin_fmaf(d, sq, -(dmin * mm));
 }
 
 // Q8_0: a pair of blocks (68 bytes = 17 dwords, 4-byte aligned because every
@@ -243,5 +247,7 @@ __device__ __forceinline__ float naiwa_q8_0_pair(const uint32_t* D, const uint32
     }
     const float d0 = naiwa_f16_to_f32(D[0] & 0xffffu);
     const float d1 = naiwa_f16_to_f32(D[8] >> 16);
-    return d0 * (a0 - 1152.0f * s0) + d1 * (a1 - 1152.0f * s1);
+    // explicit fmas: the same bits in every kernel that inlines this
+    const float t0 = __builtin_fmaf(-1152.0f, s0, a0), t1 = __builtin_fmaf(-1152.0f, s1, a1);
+    return __builtin_fmaf(d0, t0, d1 * t1);
 }

@@ -426,7 +426,7 @@ down_split_kernel(BankArg down, int H, int I, int ks, int rpg, int tok_max, int 
                 }
             }
 #pragma unroll
-            for (int tt = 0; tt < kTokD; ++tt) {
+            for (int tt = 0; tt < TD; ++tt) {
                 const float v0 = naiwa_group_sum<NAIWA_GROUP>(a0[tt]);
                 const float v1 = naiwa_group_sum<NAIWA_GROUP>(a1[tt]);
                 if (tt < nt && lr == 0) {
@@ -513,11 +513,55 @@ down_combine_kernel(const float* dpart, int kparts, int n, int H, int rows, int 
         }
 #pragma unroll
         for (int q = 0; q < kCombinePairs; ++q)
-            if (k0 + q < c) acc += wl[k0 + q] * v[q];
+            if (k0 + q < c) acc = __builtin_fmaf(wl[k0 + q], v[q], acc);
     }
     // with res (bf16 [rows, H]): the residual x = bf16(x + y) of the same y, in place
     if (res) res[o] = (uint16_t)naiwa_f32_to_bf16(x0 + acc);
     if (out) out[o] = acc;
+}
+
+// The combine of a one-token call (rows == 1, n pairs, n * kparts <= kOneLoads):
+// every sorted position belongs to the token and the positions are already in slot
+// order, so a lane issues the loads of every K-part dot of positions < n, its
+// residual and its accumulator together with the permutation, before the position
+// count is known; only the routing weights wait on the permutation.  The sums are
+// those of down_combine_kernel in the same order (parts in part order, then pairs
+// in position order), so the result is the same bit for bit.
+constexpr int kOneLoads = 16;
+__global__ void __launch_bounds__(64)
+down_combine_one_kernel(const float* dpart, int kparts, int n, int H, const int* seg_count,
+                        const uint32_t* seg_begin, const uint32_t* perm, const float* w, int accumulate, float* out,
+                        uint16_t* res) {
+    const int lane = threadIdx.x;
+    const int r = blockIdx.x * 64 + lane;
+    const bool in = r < H;
+    const int rr = in ? r : 0;
+    const int sc = *seg_count;
+    const uint32_t p = lane < n ? perm[lane] : 0u;
+    float pv[kOneLoads];
+#pragma unroll
+    for (int j = 0; j < kOneLoads; ++j) {
+        const int q = j / kparts, i = j - q * kparts;
+        pv[j] = q < n ? dpart[((size_t)i * n + q) * H + rr] : 0.0f;
+    }
+    const float x0 = res ? naiwa_bf16_to_f32(res[rr]) : 0.0f;
+    float acc = accumulate ? out[rr] : 0.0f;
+    const int npos = (int)seg_begin[sc];
+    const float wv = lane < npos ? w[p] : 0.0f;
+    float v = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kOneLoads; ++j) {
+        const int q = j / kparts, i = j - q * kparts;
+        if (q >= npos) break;
+        v = i == 0 ? pv[j] : v + pv[j];
+        if (i == kparts - 1) {
+            const float wq = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wv), q));
+            acc = __builtin_fmaf(wq, v, acc);
+        }
+    }
+    if (!in) return;
+    if (res) res[r] = (uint16_t)naiwa_f32_to_bf16(x0 + acc);
+    if (out) out[r] = acc;
 }
 
 bool bank_ok(const naiwa_bank* b) {
@@ -594,6 +638,11 @@ int check_args(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* d
 int combine_launch(const float* dpart, int kparts, int n, int H, int rows, int width, const int* seg_count,
                    const uint32_t* seg_begin, const uint32_t* perm, const float* w, int accumulate, float* out,
                    hipStream_t st, uint16_t* res = nullptr) {
+    if (rows == 1 && n <= 64 && (int64_t)n * kparts <= kOneLoads) {
+        down_combine_one_kernel<<<(H + 63) / 64, 64, 0, st>>>(dpart, kparts, n, H, seg_count, seg_begin, perm, w,
+                                                              accumulate, out, res);
+        return naiwa_hip_rc(hipGetLastError());
+    }
     const dim3 cgrid((H + 63) / 64, rows);
     down_combine_kernel<<<cgrid, 64, 0, st>>>(dpart, kparts, n, H, rows, width, seg_count, seg_begin, perm, w,
                                                accumulate, out, res);

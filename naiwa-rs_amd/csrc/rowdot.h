@@ -95,6 +95,8 @@ template <> struct Fmt<NAIWA_Q8_0_ODD> {
         return f;
     }
     __device__ __forceinline__ static float dot(const Frag& f, int u, const uint32_t* words, const float* sums) {
+        // the final multiply never fuses into the caller's add (the same bits in every kernel)
+#pragma clang fp contract(off)
         const uint4* xv = reinterpret_cast<const uint4*>(words + 16 * u);
         float a = 0.0f;
 #pragma unroll
@@ -108,7 +110,7 @@ template <> struct Fmt<NAIWA_Q8_0_ODD> {
                 a = naiwa_dot2_f16(((w >> 8) & 0x00FF00FFu) | 0x64006400u, xw[2 * h + 1], a);
             }
         }
-        return naiwa_f16_to_f32(f.d) * (a - 1152.0f * sums[u]);
+        return naiwa_f16_to_f32(f.d) * __builtin_fmaf(-1152.0f, sums[u], a);
     }
     __device__ static uint32_t to16(float v) { return naiwa_f32_to_f16(v); }
     __device__ static float from16(uint32_t h) { return naiwa_f16_to_f32(h); }

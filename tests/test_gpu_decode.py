@@ -206,6 +206,40 @@ def test_split_by_slot_with_accumulate_is_bit_identical(gpu):
         assert np.array_equal(whole.download(np.float32), split.download(np.float32)), cut
 
 
+@pytest.mark.parametrize("dt,H,I,E,k", [
+    ((O.Q4_K,) * 3, 2048, 768, 16, 8),              # one K part, 8 pairs
+    ((O.Q4_K,) * 3, 1024, 4352, 8, 2),              # three K parts: 2048 + 2048 + 256
+    ((O.Q4_K, O.Q4_K, O.Q8_0), 512, 2304, 6, 4),    # Q8_0 down in two K parts
+])
+def test_one_token_combine_matches_the_general_combine(gpu, dt, H, I, E, k):
+    """A one-token call (its combine issues every load up front) gives row 0 of a
+    two-token call over the same pairs (the general combine) bit for bit, plain and
+    accumulating into an output that already holds values."""
+    nm = gpu
+    g, u, d, r = S.layer(2200 + H, E, H, I, dt)
+    banks = nm.LayerBanks(E, H, I, dt)
+    for e in range(E):
+        banks.load(e, g[e], u[e], d[e])
+    x = S.activations_bf16(2201, 2, H)
+    ids, w = O.topk(O.router_logits(O.from_bf16(x), r), k)
+    base = np.random.default_rng(2202).standard_normal((2, H)).astype(np.float32)
+    res = {}
+    for rows in (1, 2):
+        xd = nm.DeviceBuffer.from_array(np.ascontiguousarray(x[:rows]))
+        idd = nm.DeviceBuffer.from_array(np.ascontiguousarray(ids[:rows], np.uint32))
+        wd = nm.DeviceBuffer.from_array(np.ascontiguousarray(w[:rows], np.float32))
+        plain = nm.DeviceBuffer(rows * H * 4)
+        acc = nm.DeviceBuffer.from_array(np.ascontiguousarray(base[:rows]))
+        nm.indexed_moe_fused_decode(banks, xd, nm.BF16, idd, wd, rows, k, plain)
+        nm.indexed_moe_fused_decode(banks, xd, nm.BF16, idd, wd, rows, k, acc, accumulate=True)
+        nm.synchronize()
+        res[rows] = (plain.download(np.float32).reshape(rows, H), acc.download(np.float32).reshape(rows, H))
+    assert np.array_equal(res[1][0][0], res[2][0][0])
+    assert np.array_equal(res[1][1][0], res[2][1][0])
+    want = oracle_decode(g, u, d, dt, H, I, x[:1], ids[:1], w[:1])
+    assert S.max_rel_err(res[1][0], want) < TOL
+
+
 @pytest.mark.parametrize("dt,H,I,E,k,rows", [
     ((O.Q4_K,) * 3, 512, 2304, 4, 2, 3),             # down in two K parts: 2048 + 256
     ((O.Q8_0,) * 3, 256, 2080, 4, 2, 5),             # 65 Q8_0 blocks a row: parts of 2048 + 32
