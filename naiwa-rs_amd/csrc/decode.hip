@@ -457,35 +457,26 @@ down_combine_kernel(const float* dpart, int kparts, int n, int H, int rows, int 
     const int lane = threadIdx.x;
     const int t = blockIdx.y;
     const int npos = (int)seg_begin[*seg_count];
-    if (lane < kCombineWidth) list[lane] = -1;
-    __syncthreads();
-    for (int pos = lane; pos < npos; pos += 64) {
-        const uint32_t p = perm[pos];
-        if ((int)(p / (uint32_t)width) == t) {
-            list[p % (uint32_t)width] = pos;
-            wl[p % (uint32_t)width] = w[p];
+    // the token's positions, compacted in ascending order as the scan meets them (a
+    // ballot per 64 positions), with their routing weights
+    int found = 0;
+    for (int base = 0; base < npos; base += 64) {
+        const int pos = base + lane;
+        uint32_t p = 0;
+        bool mine = false;
+        if (pos < npos) {
+            p = perm[pos];
+            mine = (int)(p / (uint32_t)width) == t;
         }
-    }
-    __syncthreads();
-    if (lane == 0) {
-        // insertion sort of (position, weight) by position; entry j is read before
-        // any write reaches index j
-        int c = 0;
-        for (int j = 0; j < width; ++j) {
-            const int v = list[j];
-            if (v < 0) continue;
-            const float wv = wl[j];
-            int k = c++;
-            while (k > 0 && list[k - 1] > v) {
-                list[k] = list[k - 1];
-                wl[k] = wl[k - 1];
-                --k;
-            }
-            list[k] = v;
-            wl[k] = wv;
+        const unsigned long long m = __ballot(mine);
+        if (mine) {
+            const int idx = found + __popcll(m & ((1ull << lane) - 1ull));
+            list[idx] = pos;
+            wl[idx] = w[p];
         }
-        cnt = c;
+        found += __popcll(m);
     }
+    if (lane == 0) cnt = found;
     __syncthreads();
     const int r = blockIdx.x * 64 + lane;
     if (r >= H) return;
