@@ -397,11 +397,13 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     const bool split = nc && !batch;
 
     // the step's inputs: slot ids and, for split passes, the weights of the cache pairs
-    // and of the staged pairs, written into mapped coherent host memory and pulled into
-    // device memory by one wave on the compute stream.  The previous step of this layer
-    // has finished reading them: its kernels precede this step's routing, whose doorbell
-    // the host waited for above.  The pull goes ahead of the staged uploads: its few PCIe
-    // reads would otherwise queue behind megabytes of upload reads.
+    // and of the staged pairs, written into mapped coherent host memory.  The previous
+    // step of this layer has finished reading them: its kernels precede this step's
+    // routing, whose doorbell the host waited for above.  Split passes run the cache
+    // pairs during the uploads, so their inputs are pulled into device memory by one wave
+    // first (its few PCIe reads would otherwise queue behind megabytes of upload reads).
+    // One pass after the uploads (or with none) reads the slot ids from the mapped memory
+    // itself, in the gate/up segmentation: one launch and its gap fewer per layer.
     if (split) {
         float* w_res = L->wsplit_h;
         float* w_stg = L->wsplit_h + n;
@@ -412,8 +414,11 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         }
     }
     std::atomic_thread_fence(std::memory_order_release);
-    pull_inputs_kernel<<<1, 64, 0, st>>>(L->in_dev_base, L->in_map_base, n * (split ? 3 : 1));
-    if ((rc = naiwa_hip_rc(hipGetLastError()))) return rc;
+    if (split) {
+        pull_inputs_kernel<<<1, 64, 0, st>>>(L->in_dev_base, L->in_map_base, n * 3);
+        if ((rc = naiwa_hip_rc(hipGetLastError()))) return rc;
+    }
+    const uint32_t* slot_ids = split ? L->slots_dev : L->in_map_base;
 
     // uploads on the copy stream after the last step that read each ring slot: one kernel
     // for all of them when the host stacks are mapped pinned memory (one range per expert
@@ -462,11 +467,11 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         }
         if (res_x) {
             // out keeps the layer's output; the residual rides in the ordered combine
-            if ((rc = naiwa_moe_decode_residual(&d.gate, &d.up, &d.down, res_x, L->slots_dev, L->w_dev, rows, k,
+            if ((rc = naiwa_moe_decode_residual(&d.gate, &d.up, &d.down, res_x, slot_ids, L->w_dev, rows, k,
                                                 d.act, out, 1, stream)))
                 return rc;
             if (folded) *folded = true;
-        } else if ((rc = naiwa_moe_decode(&d.gate, &d.up, &d.down, x, NAIWA_BF16, L->slots_dev, L->w_dev, rows, k,
+        } else if ((rc = naiwa_moe_decode(&d.gate, &d.up, &d.down, x, NAIWA_BF16, slot_ids, L->w_dev, rows, k,
                                           d.act, out, stream))) {
             return rc;
         }
