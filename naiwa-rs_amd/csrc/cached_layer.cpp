@@ -357,6 +357,15 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         rc = naiwa_router_topk_publish(x, NAIWA_BF16, d.router, d.router_bias, d.hidden, d.num_experts, k, d.mode,
                                        L->ids_dev, L->w_dev, L->db_dev, L->db_dev + kDbHead, stream);
         if (rc) return rc;
+    } else if (rows == 1 && next->d.top_k == k) {
+        // one token with the prediction: both routers' logits in one launch, both
+        // top-ks and the publish in another (five launches as separate calls)
+        rc = naiwa_router_topk_pair_publish(x, NAIWA_BF16, d.hidden, d.router, d.router_bias, d.num_experts, k,
+                                            d.mode, L->ids_dev, L->w_dev, next->d.router, next->d.router_bias,
+                                            next->d.num_experts, k, NAIWA_ROUTE_TOPK_SOFTMAX, next->pred_ids_dev,
+                                            next->pred_w_dev, L->db_dev, L->db_dev + kDbHead, stream);
+        if (rc) return rc;
+        next->pred_rows = rows;
     } else {
         rc = naiwa_router_topk_biased(x, NAIWA_BF16, d.router, d.router_bias, rows, d.hidden, d.num_experts, k,
                                       d.mode, L->ids_dev, L->w_dev, nullptr, stream);

@@ -178,3 +178,12 @@ __device__ inline void naiwa_wave_topk(const float* l, int E, int k, int mode, u
 int naiwa_router_topk_publish(const void* x, int x_dtype, const float* W, const float* bias, int H, int E, int k,
                               int mode, uint32_t* ids_out, float* w_out, uint32_t* db_seq, uint32_t* pay,
                               int64_t stream);
+
+// One row under two routers in two launches (both logits, then both top-ks and one
+// publish): the layer's routing (ids1, w1 at pay[0..k1) and pay[k1..2k1)) and the
+// lookahead's prediction of the next layer (ids2 at pay[2k1..2k1+k2)), then *db_seq + 1
+// with a system-scope release.
+int naiwa_router_topk_pair_publish(const void* x, int x_dtype, int H, const float* W1, const float* b1, int E1,
+                                   int k1, int mode1, uint32_t* ids1, float* w1, const float* W2, const float* b2,
+                                   int E2, int k2, int mode2, uint32_t* ids2, float* w2, uint32_t* db_seq,
+                                   uint32_t* pay, int64_t stream);

@@ -73,39 +73,57 @@ router_logits_rows_kernel(const void* x, int x_bf16, const float* W, const float
 // 8-feature chunks i, i + 256, ..., issuing up to kLogitPer chunks' loads at once;
 // the waves' sums meet in LDS.  The chunk values are int64 fixed point, so their
 // sum is the same in any order.
+// logit[t, e] by the whole block (part: kLogitThreads / 64 words of LDS).
+__device__ inline void logit_block(const void* x, int x_bf16, const float* W, const float* bias, int H, int E, int e,
+                                   int t, float* logits, long long* part) {
+    const int tid = threadIdx.x;
+    const int nchunks = H / NAIWA_ROUTER_CHUNK;
+    const float* wr = W + (int64_t)e * H;
+    long long acc = 0;
+    for (int c0 = tid; c0 < nchunks; c0 += kLogitThreads * kLogitPer) {
+        float xv[kLogitPer][8];
+#pragma unroll
+        for (int i = 0; i < kLogitPer; ++i) {
+            const int c = c0 + kLogitThreads * i;
+            if (c < nchunks) naiwa_load_x8(x, x_bf16, (int64_t)t * H + 8 * c, xv[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < kLogitPer; ++i) {
+            const int c = c0 + kLogitThreads * i;
+            if (c < nchunks) acc += naiwa_router_chunk(wr + 8 * c, xv[i]);
+        }
+    }
+    acc = naiwa_wave_sum_i64(acc);
+    if ((tid & 63) == 0) part[tid >> 6] = acc;
+    __syncthreads();
+    if (tid == 0) {
+        long long sum = 0;
+#pragma unroll
+        for (int i = 0; i < kLogitThreads / 64; ++i) sum += part[i];
+        logits[(int64_t)t * E + e] = naiwa_router_fix_to_f32(sum) + (bias ? bias[e] : 0.0f);
+    }
+    __syncthreads(); // part is reused by the next call
+}
+
 __global__ void __launch_bounds__(kLogitThreads)
 router_logits_kernel(const void* x, int x_bf16, const float* W, const float* bias, int rows, int H, int E,
                      float* logits) {
     __shared__ long long part[kLogitThreads / 64];
-    const int e = blockIdx.x, tid = threadIdx.x;
-    const int nchunks = H / NAIWA_ROUTER_CHUNK;
-    const float* wr = W + (int64_t)e * H;
-    for (int t = blockIdx.y; t < rows; t += gridDim.y) {
-        long long acc = 0;
-        for (int c0 = tid; c0 < nchunks; c0 += kLogitThreads * kLogitPer) {
-            float xv[kLogitPer][8];
-#pragma unroll
-            for (int i = 0; i < kLogitPer; ++i) {
-                const int c = c0 + kLogitThreads * i;
-                if (c < nchunks) naiwa_load_x8(x, x_bf16, (int64_t)t * H + 8 * c, xv[i]);
-            }
-#pragma unroll
-            for (int i = 0; i < kLogitPer; ++i) {
-                const int c = c0 + kLogitThreads * i;
-                if (c < nchunks) acc += naiwa_router_chunk(wr + 8 * c, xv[i]);
-            }
-        }
-        acc = naiwa_wave_sum_i64(acc);
-        if ((tid & 63) == 0) part[tid >> 6] = acc;
-        __syncthreads();
-        if (tid == 0) {
-            long long sum = 0;
-#pragma unroll
-            for (int i = 0; i < kLogitThreads / 64; ++i) sum += part[i];
-            logits[(int64_t)t * E + e] = naiwa_router_fix_to_f32(sum) + (bias ? bias[e] : 0.0f);
-        }
-        __syncthreads(); // part is reused by the next row
-    }
+    for (int t = blockIdx.y; t < rows; t += gridDim.y)
+        logit_block(x, x_bf16, W, bias, H, E, blockIdx.x, t, logits, part);
+}
+
+// One row under two routers (a layer's, and the next layer's for the lookahead's
+// prediction): blocks [0, E1) take W1's experts, blocks [E1, E1 + E2) W2's.
+__global__ void __launch_bounds__(kLogitThreads)
+router_logits_pair_kernel(const void* x, int x_bf16, int H, const float* W1, const float* b1, int E1, float* l1,
+                          const float* W2, const float* b2, int E2, float* l2) {
+    __shared__ long long part[kLogitThreads / 64];
+    const int b = blockIdx.x;
+    if (b < E1)
+        logit_block(x, x_bf16, W1, b1, H, E1, b, 0, l1, part);
+    else
+        logit_block(x, x_bf16, W2, b2, H, E2, b - E1, 0, l2, part);
 }
 
 constexpr int kTopkThreads = 256;
@@ -160,6 +178,45 @@ router_topk_publish_kernel(const float* logits, int E, int k, int mode, uint32_t
     }
 }
 
+// The top k of both rows of router_logits_pair_kernel in one block, then one publish
+// of the routing read-back: ids1 at pay[0..k1), weights1 at pay[k1..2k1), ids2 at
+// pay[2k1..2k1+k2), and the sequence word up by one with a system-scope release.
+__global__ void __launch_bounds__(kTopkThreads)
+router_topk_pair_publish_kernel(const float* l1, int E1, int k1, int mode1, uint32_t* ids1, float* w1,
+                                const float* l2, int E2, int k2, int mode2, uint32_t* ids2, float* w2,
+                                uint32_t* db_seq, uint32_t* pay) {
+    __shared__ float l[NAIWA_ROUTER_MAX_E];
+    __shared__ int rank_tmp[NAIWA_ROUTER_MAX_E];
+    __shared__ float ex_tmp[NAIWA_ROUTER_MAX_E];
+    __shared__ uint32_t ids_s[NAIWA_ROUTER_MAX_K];
+    __shared__ float w_s[NAIWA_ROUTER_MAX_K];
+    volatile uint32_t* out = pay;
+    for (int e = threadIdx.x; e < E1; e += kTopkThreads) l[e] = l1[e];
+    __syncthreads();
+    naiwa_block_topk<kTopkThreads>(l, E1, k1, mode1, ids_s, w_s, rank_tmp, ex_tmp);
+    if (threadIdx.x < k1) {
+        ids1[threadIdx.x] = ids_s[threadIdx.x];
+        w1[threadIdx.x] = w_s[threadIdx.x];
+        out[threadIdx.x] = ids_s[threadIdx.x];
+        out[k1 + threadIdx.x] = __float_as_uint(w_s[threadIdx.x]);
+    }
+    __syncthreads(); // l, ids_s and w_s are reused
+    for (int e = threadIdx.x; e < E2; e += kTopkThreads) l[e] = l2[e];
+    __syncthreads();
+    naiwa_block_topk<kTopkThreads>(l, E2, k2, mode2, ids_s, w_s, rank_tmp, ex_tmp);
+    if (threadIdx.x < k2) {
+        ids2[threadIdx.x] = ids_s[threadIdx.x];
+        w2[threadIdx.x] = w_s[threadIdx.x];
+        out[2 * k1 + threadIdx.x] = ids_s[threadIdx.x];
+    }
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t cur = __hip_atomic_load(db_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(db_seq, cur + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
 } // namespace
 
 int naiwa_router_topk_publish(const void* x, int x_dtype, const float* W, const float* bias, int H, int E, int k,
@@ -179,6 +236,29 @@ int naiwa_router_topk_publish(const void* x, int x_dtype, const float* W, const 
     router_logits_kernel<<<dim3((unsigned)E, 1u), kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, W, bias, 1, H, E,
                                                                          logits);
     router_topk_publish_kernel<<<1, kTopkThreads, 0, st>>>(logits, E, k, mode, ids_out, w_out, db_seq, pay);
+    return naiwa_hip_rc(hipGetLastError());
+}
+
+int naiwa_router_topk_pair_publish(const void* x, int x_dtype, int H, const float* W1, const float* b1, int E1,
+                                   int k1, int mode1, uint32_t* ids1, float* w1, const float* W2, const float* b2,
+                                   int E2, int k2, int mode2, uint32_t* ids2, float* w2, uint32_t* db_seq,
+                                   uint32_t* pay, int64_t stream) {
+    if (x_dtype != NAIWA_BF16 && x_dtype != NAIWA_F32) return NAIWA_E_UNSUPPORTED;
+    for (int m : {mode1, mode2})
+        if (m < NAIWA_ROUTE_SOFTMAX_TOPK_RENORM || m > NAIWA_ROUTE_SOFTMAX_TOPK) return NAIWA_E_UNSUPPORTED;
+    if (H <= 0 || H % NAIWA_ROUTER_CHUNK || E1 <= 0 || E1 > NAIWA_ROUTER_MAX_E || k1 <= 0 || k1 > E1 ||
+        k1 > NAIWA_ROUTER_MAX_K || E2 <= 0 || E2 > NAIWA_ROUTER_MAX_E || k2 <= 0 || k2 > E2 ||
+        k2 > NAIWA_ROUTER_MAX_K)
+        return NAIWA_E_INVALID;
+    if (!x || !W1 || !W2 || !ids1 || !w1 || !ids2 || !w2 || !db_seq || !pay) return NAIWA_E_INVALID;
+    hipStream_t st = (hipStream_t)stream;
+    int rc = 0;
+    float* logits = (float*)naiwa_scratch(NAIWA_SCRATCH_ROUTER, (size_t)(E1 + E2) * 4, &rc);
+    if (!logits) return rc;
+    router_logits_pair_kernel<<<(unsigned)(E1 + E2), kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, H, W1, b1, E1,
+                                                                           logits, W2, b2, E2, logits + E1);
+    router_topk_pair_publish_kernel<<<1, kTopkThreads, 0, st>>>(logits, E1, k1, mode1, ids1, w1, logits + E1, E2, k2,
+                                                                mode2, ids2, w2, db_seq, pay);
     return naiwa_hip_rc(hipGetLastError());
 }
 
