@@ -343,7 +343,8 @@ def print_trace(nm, run, stream, L, khz):
     land = t[:, : L - 1, 21] - t[:, : L - 1, 3]
     log(f"trace: gate/up rows landed, last wave after wave 0: median {np.median(land):.2f} us; "
         f"last wave's compute {np.median(t[:, : L - 1, 16] - t[:, : L - 1, 21]):.2f}; "
-        f"wave 0's first round {np.median(t[:, : L - 1, 22] - t[:, : L - 1, 3]):.2f}")
+        f"top-k ready {np.median(t[:, : L - 1, 22] - t[:, : L - 1, 1]):.2f} after the ranks, pairs grouped "
+        f"{np.median(t[:, : L - 1, 12] - t[:, : L - 1, 22]):.2f} later")
     cyc = np.frombuffer(buf, dtype=np.uint64)[: G * (L + 1) * slots].reshape(G, L + 1, slots)[:, :L, 23]
     dc = np.diff(cyc.astype(np.float64), axis=1)
     dt_us = np.diff(t[:, :L, 2], axis=1)

@@ -516,6 +516,7 @@ __device__ inline void route_one_row(const Params& p, Smem& sm, const LayerDev& 
     const bool inp = lane < k;
     my_e = inp ? sm.top_ids[0][lane] : 0u;
     my_f = inp ? sm.top_ex[0][lane] : 0.0f;
+    mark_wave(p, l, 22);
     group_pairs_one(p, sm, L, lane, inp, my_e);
     mark_wave(p, l, 12);
 }
@@ -1133,7 +1134,6 @@ stack_kernel(Params p) {
                 }
                 if (my_item < nr)
                     q4_pair_compute<DD>(p, sm, dyn, xstage, r0 + my_item, nb, il, wb + my_item * item_bytes, rb, tag);
-                if (r0 == q0 && wave == 0) mark_wave(p, l, 22);
             }
             mark_wave(p, l, 16); // every wave: the last one to store wins
             if (q0 >= q1) {
