@@ -194,87 +194,6 @@ __device__ inline void naiwa_stage(const void* src, bool src_bf16, int k, uint32
     }
 }
 
-// Stage nv (<= MAXV) vectors of k activations at once: every thread issues
-// the loads of all vectors before converting any, so the vectors cost one
-// memory round trip instead of nv.  Vector v goes to dst + v * stride_bytes.
-template <int DT, bool COH, int MAXV>
-__device__ inline void naiwa_stage_multi(const void* const* srcs, int nv, bool src_bf16, int k,
-                                         uint8_t* dst, int stride_bytes, int tid, int nthr) {
-    constexpr int span = Fmt<DT>::kSumSpan;
-    constexpr int gpg = span / 4;
-    for (int g0 = 0; g0 < k / 4; g0 += nthr) {
-        const int g = g0 + tid;
-        const bool in = g < k / 4;
-        uint2 raw[MAXV][2];
-#pragma unroll
-        for (int v = 0; v < MAXV; ++v) {
-            if (v < nv && in) {
-                if (src_bf16) {
-                    raw[v][0] = naiwa_ld8<COH>((const uint16_t*)srcs[v] + 4 * g);
-                } else {
-                    raw[v][0] = naiwa_ld8<COH>((const float*)srcs[v] + 4 * g);
-                    raw[v][1] = naiwa_ld8<COH>((const float*)srcs[v] + 4 * g + 2);
-                }
-            }
-        }
-#pragma unroll
-        for (int v = 0; v < MAXV; ++v) {
-            if (v < nv) {
-            uint32_t* words = (uint32_t*)(dst + v * stride_bytes);
-            float* sums = (float*)(words + k / 2);
-            float part = 0.0f;
-            if (in) {
-                float x[4];
-                if (src_bf16) {
-                    x[0] = naiwa_bf16_to_f32(raw[v][0].x & 0xffffu);
-                    x[1] = naiwa_bf16_to_f32(raw[v][0].x >> 16);
-                    x[2] = naiwa_bf16_to_f32(raw[v][0].y & 0xffffu);
-                    x[3] = naiwa_bf16_to_f32(raw[v][0].y >> 16);
-                } else {
-                    x[0] = __uint_as_float(raw[v][0].x); x[1] = __uint_as_float(raw[v][0].y);
-                    x[2] = __uint_as_float(raw[v][1].x); x[3] = __uint_as_float(raw[v][1].y);
-                }
-                uint32_t h[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    h[i] = Fmt<DT>::to16(x[i]);
-                    x[i] = Fmt<DT>::from16(h[i]);
-                }
-                words[2 * g] = h[0] | (h[2] << 16);
-                words[2 * g + 1] = h[1] | (h[3] << 16);
-                part = (x[0] + x[1]) + (x[2] + x[3]);
-            }
-            part = naiwa_group_sum<gpg>(part);
-            if (in && (g % gpg) == 0) sums[g / gpg] = part;
-            }
-        }
-    }
-}
-
-// Dot of one quantized row with one staged vector, by the 16 lanes of a
-// group (lr = lane in group).  Loads of up to UMAX units are issued before
-// any of them is used.  Returns the full sum in every lane of the group.
-template <int DT, int UMAX>
-__device__ inline float naiwa_row_dot(const uint8_t* row, int k, const uint32_t* words,
-                                      const float* sums, int lr) {
-    const int nu = Fmt<DT>::units(k);
-    float acc = 0.0f;
-    for (int base = lr; base < nu; base += NAIWA_GROUP * UMAX) {
-        typename Fmt<DT>::Frag f[UMAX];
-#pragma unroll
-        for (int i = 0; i < UMAX; ++i) {
-            const int u = base + NAIWA_GROUP * i;
-            if (u < nu) f[i] = Fmt<DT>::load(row, u);
-        }
-#pragma unroll
-        for (int i = 0; i < UMAX; ++i) {
-            const int u = base + NAIWA_GROUP * i;
-            if (u < nu) acc += Fmt<DT>::dot(f[i], u, words, sums);
-        }
-    }
-    return naiwa_group_sum<NAIWA_GROUP>(acc);
-}
-
 // Loads in flight per lane per pass, by format (about 32 VGPRs of codes).
 template <int DT> struct Umax { static constexpr int v = 4; };
 template <> struct Umax<NAIWA_Q8_0> { static constexpr int v = 2; };
