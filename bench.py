@@ -996,7 +996,6 @@ def run_prefill(args) -> int:
     # (slots E.., weight 1), so the shared GEMM tiles run in the routed launch and the
     # ordered combine adds them after the routed pairs, as a second accumulating call would
     KA = K + S_
-    ids, w = nm.DeviceBuffer(T * K * 4), nm.DeviceBuffer(T * K * 4)
     ids_all = nm.DeviceBuffer.from_array(np.tile(np.concatenate([np.zeros(K), np.arange(E, E + S_)]).astype(np.uint32),
                                                  (T, 1)))
     w_all = nm.DeviceBuffer.from_array(np.tile(np.concatenate([np.zeros(K), np.ones(S_)]).astype(np.float32), (T, 1)))
@@ -1010,11 +1009,9 @@ def run_prefill(args) -> int:
         for c in range(chunks):
             xc = x.ptr + c * T * H * 2
             for banks, router in layers:
-                nm.router_topk(xc, nm.BF16, router, T, H, E, K, ids, w, mode=nm.ROUTE_SOFTMAX_TOPK,
-                               stream=stream.handle)
-                for dst, src in ((ids_all, ids), (w_all, w)):
-                    nm._lib.check(lib.naiwa_memcpy_2d_d2d(dst.ptr, KA * 4, src.ptr, K * 4, K * 4, T, stream.handle),
-                                  "routing columns")
+                # the routed experts straight into columns 0..K-1 of the (routed | shared) table
+                nm.router_topk(xc, nm.BF16, router, T, H, E, K, ids_all, w_all, mode=nm.ROUTE_SOFTMAX_TOPK,
+                               stream=stream.handle, ld=KA)
                 nm.moe_prefill(banks, xc, ids_all, w_all, T, KA, y, stream=stream.handle)
                 nm._lib.check(lib.naiwa_residual_add_bf16(xc, y.ptr, T * H, stream.handle), "residual")
 
@@ -1052,10 +1049,8 @@ def run_prefill(args) -> int:
     for c in range(chunks):
         xc = x.ptr + c * T * H * 2
         for li, (banks, router) in enumerate(layers):
-            nm.router_topk(xc, nm.BF16, router, T, H, E, K, ids, w, mode=nm.ROUTE_SOFTMAX_TOPK, stream=stream.handle)
-            for dst, src in ((ids_all, ids), (w_all, w)):
-                nm._lib.check(lib.naiwa_memcpy_2d_d2d(dst.ptr, KA * 4, src.ptr, K * 4, K * 4, T, stream.handle),
-                              "routing columns")
+            nm.router_topk(xc, nm.BF16, router, T, H, E, K, ids_all, w_all, mode=nm.ROUTE_SOFTMAX_TOPK,
+                           stream=stream.handle, ld=KA)
             a, b = ev[c * L + li]
             a.record(stream.handle)
             nm.moe_prefill(banks, xc, ids_all, w_all, T, KA, y, stream=stream.handle)
@@ -1063,7 +1058,7 @@ def run_prefill(args) -> int:
             nm._lib.check(lib.naiwa_residual_add_bf16(xc, y.ptr, T * H, stream.handle), "residual")
             if li == 0 and c == 0:
                 stream.sync()
-                distinct.append(len(np.unique(ids.download(np.uint32))))
+                distinct.append(len(np.unique(ids_all.download(np.uint32).reshape(T, KA)[:, :K])))
     stream.sync()
     call_ms = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
     n_exp = (distinct[0] if distinct else E) + S_

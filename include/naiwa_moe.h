@@ -222,6 +222,15 @@ int naiwa_router_topk(const void* x, int x_dtype, const float* W, int rows, int 
 int naiwa_router_topk_biased(const void* x, int x_dtype, const float* W, const float* bias, int rows, int H,
                              int E, int k, int mode, uint32_t* ids_out, float* w_out, float* logits_out,
                              int64_t stream);
+/* As naiwa_router_topk_biased with ids_out / w_out rows ld >= k entries apart:
+ * row t's k routed ids and weights go to [t * ld, t * ld + k) and the other
+ * columns are left as they are.  No counterpart in the reference, which routes
+ * one MoE layer's routed experts only: a caller that adds always-on experts
+ * (DeepSeek-V2's shared experts, at weight 1 in columns k..ld-1 of the same
+ * table for naiwa_moe_prefill) fills the table without a copy. */
+int naiwa_router_topk_ld(const void* x, int x_dtype, const float* W, const float* bias, int rows, int H, int E,
+                         int k, int mode, uint32_t* ids_out, float* w_out, int ld, float* logits_out,
+                         int64_t stream);
 
 /* Gather: stable counting sort of the n flattened ids by value.
  * perm_out[n] = flat (t*k + j) indices grouped by id, offsets_out[E+1] =

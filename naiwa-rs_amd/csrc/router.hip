@@ -129,7 +129,7 @@ router_logits_pair_kernel(const void* x, int x_bf16, int H, const float* W1, con
 constexpr int kTopkThreads = 256;
 
 __global__ void __launch_bounds__(kTopkThreads)
-router_topk_kernel(const float* logits, int E, int k, int mode, uint32_t* ids, float* w) {
+router_topk_kernel(const float* logits, int E, int k, int mode, uint32_t* ids, float* w, int ld) {
     __shared__ float l[NAIWA_ROUTER_MAX_E];
     __shared__ int rank_tmp[NAIWA_ROUTER_MAX_E];
     __shared__ float ex_tmp[NAIWA_ROUTER_MAX_E];
@@ -140,8 +140,8 @@ router_topk_kernel(const float* logits, int E, int k, int mode, uint32_t* ids, f
     __syncthreads();
     naiwa_block_topk<kTopkThreads>(l, E, k, mode, ids_s, w_s, rank_tmp, ex_tmp);
     if (threadIdx.x < k) {
-        ids[(int64_t)t * k + threadIdx.x] = ids_s[threadIdx.x];
-        w[(int64_t)t * k + threadIdx.x] = w_s[threadIdx.x];
+        ids[(int64_t)t * ld + threadIdx.x] = ids_s[threadIdx.x];
+        w[(int64_t)t * ld + threadIdx.x] = w_s[threadIdx.x];
     }
 }
 
@@ -262,14 +262,14 @@ int naiwa_router_topk_pair_publish(const void* x, int x_dtype, int H, const floa
     return naiwa_hip_rc(hipGetLastError());
 }
 
-extern "C" int naiwa_router_topk_biased(const void* x, int x_dtype, const float* W, const float* bias, int rows,
-                                        int H, int E, int k, int mode, uint32_t* ids_out, float* w_out,
-                                        float* logits_out, int64_t stream) {
+extern "C" int naiwa_router_topk_ld(const void* x, int x_dtype, const float* W, const float* bias, int rows, int H,
+                                    int E, int k, int mode, uint32_t* ids_out, float* w_out, int ld,
+                                    float* logits_out, int64_t stream) {
     if (x_dtype != NAIWA_BF16 && x_dtype != NAIWA_F32) return NAIWA_E_UNSUPPORTED;
     if (mode < NAIWA_ROUTE_SOFTMAX_TOPK_RENORM || mode > NAIWA_ROUTE_SOFTMAX_TOPK)
         return NAIWA_E_UNSUPPORTED;
     if (rows < 0 || H <= 0 || H % NAIWA_ROUTER_CHUNK || E <= 0 || E > NAIWA_ROUTER_MAX_E || k <= 0 ||
-        k > E || k > NAIWA_ROUTER_MAX_K)
+        k > E || k > NAIWA_ROUTER_MAX_K || ld < k)
         return NAIWA_E_INVALID;
     if (rows == 0) return NAIWA_OK;
     if (!x || !W || !ids_out || !w_out) return NAIWA_E_INVALID;
@@ -296,8 +296,14 @@ extern "C" int naiwa_router_topk_biased(const void* x, int x_dtype, const float*
         else
             router_logits_rows_kernel<0><<<lg, kLogitThreads, 0, st>>>(x, xb, W, bias, rows, H, E, logits);
     }
-    router_topk_kernel<<<rows, kTopkThreads, 0, st>>>(logits, E, k, mode, ids_out, w_out);
+    router_topk_kernel<<<rows, kTopkThreads, 0, st>>>(logits, E, k, mode, ids_out, w_out, ld);
     return naiwa_hip_rc(hipGetLastError());
+}
+
+extern "C" int naiwa_router_topk_biased(const void* x, int x_dtype, const float* W, const float* bias, int rows,
+                                        int H, int E, int k, int mode, uint32_t* ids_out, float* w_out,
+                                        float* logits_out, int64_t stream) {
+    return naiwa_router_topk_ld(x, x_dtype, W, bias, rows, H, E, k, mode, ids_out, w_out, k, logits_out, stream);
 }
 
 extern "C" int naiwa_router_topk(const void* x, int x_dtype, const float* W, int rows, int H, int E, int k,

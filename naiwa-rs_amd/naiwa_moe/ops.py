@@ -204,10 +204,16 @@ def prefill_status() -> int:
 
 
 def router_topk(x, x_dtype: int, W, rows: int, H: int, E: int, k: int, ids_out, w_out,
-                mode: int = ROUTE_SOFTMAX_TOPK_RENORM, logits_out=None, stream: int = 0) -> None:
+                mode: int = ROUTE_SOFTMAX_TOPK_RENORM, logits_out=None, stream: int = 0, ld: int = 0) -> None:
+    """ld > 0: ids_out / w_out rows ld entries apart (the routed experts in columns 0..k-1)."""
+    logits = _dev(logits_out) if logits_out is not None else None
+    if ld:
+        rc = lib().naiwa_router_topk_ld(_dev(x), x_dtype, _dev(W), None, rows, H, E, k, mode, _dev(ids_out),
+                                        _dev(w_out), ld, logits, stream)
+        check(rc, "naiwa_router_topk_ld")
+        return
     rc = lib().naiwa_router_topk(_dev(x), x_dtype, _dev(W), rows, H, E, k, mode, _dev(ids_out),
-                                 _dev(w_out), _dev(logits_out) if logits_out is not None else None,
-                                 stream)
+                                 _dev(w_out), logits, stream)
     check(rc, "naiwa_router_topk")
 
 

@@ -128,3 +128,29 @@ def test_device_synthesis_matches_the_oracle_streams(gpu):
     got = buf.download(np.float32)
     want = O.normal(78, n, 1.0, 2.0)
     assert np.allclose(got, want, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("rows,H,E,k,ld", [
+    (512, 2048, 64, 6, 8),   # DeepSeek-V2-Lite chunk: 6 routed + 2 shared columns
+    (20, 2048, 64, 6, 8),    # the few-row router
+    (3, 1024, 8, 2, 2),      # ld == k: the plain layout
+])
+def test_router_rows_ld_apart(gpu, rows, H, E, k, ld):
+    """naiwa_router_topk_ld writes each row's k ids and weights at [t ld, t ld + k) -- the same
+    values as the packed call -- and leaves the other columns as they were."""
+    nm = gpu
+    x = S.activations_bf16(2300 + rows, rows, H)
+    W = O.normal(S.stream(2301, 0), E * H, 0.0, 0.02).reshape(E, H).astype(np.float32)
+    want_ids, want_w, _ = gpu_router(nm, x, W, k, O.ROUTE_SOFTMAX_TOPK)
+    fill_ids = np.full((rows, ld), 0xA5A5A5A5, np.uint32)
+    fill_w = np.full((rows, ld), -3.5, np.float32)
+    ids_d, w_d = nm.DeviceBuffer.from_array(fill_ids), nm.DeviceBuffer.from_array(fill_w)
+    nm.router_topk(nm.DeviceBuffer.from_array(x), nm.BF16, nm.DeviceBuffer.from_array(W), rows, H, E, k,
+                   ids_d, w_d, mode=O.ROUTE_SOFTMAX_TOPK, ld=ld)
+    nm.synchronize()
+    ids, w = ids_d.download(np.uint32).reshape(rows, ld), w_d.download(np.float32).reshape(rows, ld)
+    assert np.array_equal(ids[:, :k], want_ids)
+    assert np.array_equal(w[:, :k].view(np.uint32), want_w.view(np.uint32))
+    assert (ids[:, k:] == 0xA5A5A5A5).all() and (w[:, k:] == -3.5).all()
+    want_oracle, _ = O.topk(O.router_logits(O.from_bf16(x), W), k, O.ROUTE_SOFTMAX_TOPK)
+    assert np.array_equal(ids[:, :k], want_oracle)
