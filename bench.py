@@ -784,8 +784,7 @@ def run_mixtral(args) -> int:
         lib.naiwa_memcpy_d2d(x.ptr, xs.ptr, T * H * 2, stream.handle)
         for banks, router in keep:
             nm.router_topk(x, nm.BF16, router, T, H, E, K, ids, w, mode=nm.ROUTE_TOPK_SOFTMAX, stream=stream.handle)
-            nm.moe_prefill(banks, x, ids, w, T, K, y, stream=stream.handle)
-            nm._lib.check(lib.naiwa_residual_add_bf16(x.ptr, y.ptr, T * H, stream.handle), "residual")
+            nm.moe_prefill(banks, x, ids, w, T, K, y, stream=stream.handle, residual=True)
     prefill()
     stream.sync()
     e0, e1 = nm.Event(), nm.Event()
@@ -1012,8 +1011,7 @@ def run_prefill(args) -> int:
                 # the routed experts straight into columns 0..K-1 of the (routed | shared) table
                 nm.router_topk(xc, nm.BF16, router, T, H, E, K, ids_all, w_all, mode=nm.ROUTE_SOFTMAX_TOPK,
                                stream=stream.handle, ld=KA)
-                nm.moe_prefill(banks, xc, ids_all, w_all, T, KA, y, stream=stream.handle)
-                nm._lib.check(lib.naiwa_residual_add_bf16(xc, y.ptr, T * H, stream.handle), "residual")
+                nm.moe_prefill(banks, xc, ids_all, w_all, T, KA, y, stream=stream.handle, residual=True)
 
     for _ in range(warmup):
         step()
@@ -1053,9 +1051,8 @@ def run_prefill(args) -> int:
                            stream=stream.handle, ld=KA)
             a, b = ev[c * L + li]
             a.record(stream.handle)
-            nm.moe_prefill(banks, xc, ids_all, w_all, T, KA, y, stream=stream.handle)
+            nm.moe_prefill(banks, xc, ids_all, w_all, T, KA, y, stream=stream.handle, residual=True)
             b.record(stream.handle)
-            nm._lib.check(lib.naiwa_residual_add_bf16(xc, y.ptr, T * H, stream.handle), "residual")
             if li == 0 and c == 0:
                 stream.sync()
                 distinct.append(len(np.unique(ids_all.download(np.uint32).reshape(T, KA)[:, :K])))

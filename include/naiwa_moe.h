@@ -250,6 +250,10 @@ int naiwa_moe_gather(const uint32_t* ids, int n, int E, uint32_t* perm_out, uint
  * bank contribute nothing.  flags: NAIWA_PREFILL_ACCUMULATE adds to out
  * (e.g. shared experts on top of the routed ones) instead of overwriting. */
 #define NAIWA_PREFILL_ACCUMULATE 1
+/* NAIWA_PREFILL_RESIDUAL: also x = bf16(x + out) in place after out is formed, one
+ * launch fewer than a separate residual add (the same bits); x must then be
+ * writable and no other work may read it during the call. */
+#define NAIWA_PREFILL_RESIDUAL 2
 /* The matrix cores take x and h as f16: magnitudes past 65504 are clamped to
  * +-65504, and every clamped value is counted.  naiwa_moe_prefill_status
  * returns the count since its last call (resetting it) after synchronizing

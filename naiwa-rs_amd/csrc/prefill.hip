@@ -540,9 +540,11 @@ down_kernel(Bank down, const uint16_t* hp, int H, int I, const uint32_t* perm, c
 // out[t] = sum over j = 0..k-1 of the pair rows whose slot id is valid, in j order.
 // V = 4: 16 bytes per thread (H % 4 == 0, out 16-byte aligned), the loads of up to
 // 8 pair rows issued before their sums; the same additions in the same order as V = 1.
+// res (bf16 [T, H], or null): also res = bf16(res + out), the residual add.
 template <int V>
 __global__ void __launch_bounds__(kThreads)
-combine_kernel(const float* ypair, const uint32_t* ids, int k, int H, int slots, int accumulate, float* out) {
+combine_kernel(const float* ypair, const uint32_t* ids, int k, int H, int slots, int accumulate, float* out,
+               uint16_t* res) {
     typedef float vec __attribute__((ext_vector_type(V)));
     constexpr int kJ = 8;
     const int t = blockIdx.x, HV = H / V;
@@ -552,6 +554,11 @@ combine_kernel(const float* ypair, const uint32_t* ids, int k, int H, int slots,
     // the call is in flight at once rather than in rounds per block
     for (int c = blockIdx.y * kThreads + threadIdx.x; c < HV; c += kThreads * gridDim.y) {
         vec y = accumulate ? o[c] : vec(0.0f);
+        uint16_t xr[V];
+        if (res) {
+#pragma unroll
+            for (int i = 0; i < V; ++i) xr[i] = res[(size_t)t * H + (size_t)c * V + i];
+        }
         for (int j0 = 0; j0 < k; j0 += kJ) {
             // every pair row of the token is in the buffer: its load does not wait for the
             // slot id, which only decides whether the row is added
@@ -570,6 +577,11 @@ combine_kernel(const float* ypair, const uint32_t* ids, int k, int H, int slots,
                 if (j0 + u < k && id[u] < (uint32_t)slots) y += v[u];
         }
         o[c] = y;
+        if (res) {
+#pragma unroll
+            for (int i = 0; i < V; ++i)
+                res[(size_t)t * H + (size_t)c * V + i] = (uint16_t)naiwa_f32_to_bf16(naiwa_bf16_to_f32(xr[i]) + y[i]);
+        }
     }
 }
 
@@ -964,7 +976,8 @@ extern "C" int naiwa_moe_prefill_status(uint64_t* clamped) {
 extern "C" int naiwa_moe_prefill(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, const void* x,
                                  const uint32_t* slot_ids, const float* w, int T, int k, int act, float* out,
                                  int flags, int64_t stream) {
-    if (!gate || !up || !down || T < 0 || k <= 0 || (flags & ~NAIWA_PREFILL_ACCUMULATE)) return NAIWA_E_INVALID;
+    if (!gate || !up || !down || T < 0 || k <= 0 || (flags & ~(NAIWA_PREFILL_ACCUMULATE | NAIWA_PREFILL_RESIDUAL)))
+        return NAIWA_E_INVALID;
     if (T == 0) return NAIWA_OK;
     if (!x || !slot_ids || !w || !out) return NAIWA_E_INVALID;
     const int H = gate->k, I = gate->n, slots = gate->slots;
@@ -1033,9 +1046,10 @@ extern "C" int naiwa_moe_prefill(const naiwa_bank* gate, const naiwa_bank* up, c
         down_kernel<NAIWA_Q8_0><<<g2, kGemm, 0, st>>>(bd, hp, H, I, perm, w, tl, ypair);
     const int acc = (flags & NAIWA_PREFILL_ACCUMULATE) ? 1 : 0;
     const unsigned cs4 = (unsigned)((H / 4 + kThreads - 1) / kThreads), cs1 = (unsigned)((H + kThreads - 1) / kThreads);
+    uint16_t* res = (flags & NAIWA_PREFILL_RESIDUAL) ? (uint16_t*)const_cast<void*>(x) : nullptr;
     if (((uintptr_t)out & 15) == 0)
-        combine_kernel<4><<<dim3(T, cs4), kThreads, 0, st>>>(ypair, slot_ids, k, H, slots, acc, out);
+        combine_kernel<4><<<dim3(T, cs4), kThreads, 0, st>>>(ypair, slot_ids, k, H, slots, acc, out, res);
     else
-        combine_kernel<1><<<dim3(T, cs1), kThreads, 0, st>>>(ypair, slot_ids, k, H, slots, acc, out);
+        combine_kernel<1><<<dim3(T, cs1), kThreads, 0, st>>>(ypair, slot_ids, k, H, slots, acc, out, res);
     return naiwa_hip_rc(hipGetLastError());
 }

@@ -187,12 +187,14 @@ def indexed_moe_fused_decode(banks: LayerBanks, x, x_dtype: int, slot_ids, weigh
 
 
 def moe_prefill(banks: LayerBanks, x, slot_ids, weights, T: int, topk: int, out, act: int = ACT_SILU,
-                accumulate: bool = False, stream: int = 0) -> None:
+                accumulate: bool = False, stream: int = 0, residual: bool = False) -> None:
     """out[T, hidden] f32 (+)= sum_j w[t,j] * expert(slot_ids[t,j])(x[t]) for a prefill chunk
-    (x bf16 [T, hidden]), as grouped MFMA GEMMs; all device pointers."""
+    (x bf16 [T, hidden]), as grouped MFMA GEMMs; all device pointers.  residual: then also
+    x = bf16(x + out) in place."""
     g, u, d = banks.gate.desc(), banks.up.desc(), banks.down.desc()
+    flags = (1 if accumulate else 0) | (2 if residual else 0)
     rc = lib().naiwa_moe_prefill(C.byref(g), C.byref(u), C.byref(d), _dev(x), _dev(slot_ids), _dev(weights),
-                                 T, topk, act, _dev(out), 1 if accumulate else 0, stream)
+                                 T, topk, act, _dev(out), flags, stream)
     check(rc, "naiwa_moe_prefill")
 
 

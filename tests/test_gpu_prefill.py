@@ -98,6 +98,43 @@ def test_prefill_accumulates_shared_experts(gpu):
     assert np.array_equal(one.download(np.float32).reshape(T, H), two_calls)
 
 
+@pytest.mark.parametrize("H,out_offset", [(512, 0), (256, 4)])   # 16-byte vectors; a 4-byte aligned out
+def test_prefill_residual_flag_matches_a_separate_residual_add(gpu, H, out_offset):
+    """NAIWA_PREFILL_RESIDUAL: out as without the flag and x = bf16(x + out) in place, bit for
+    bit what naiwa_residual_add_bf16 makes after the call; also after an accumulating call."""
+    nm = gpu
+    T, E, k, I, dt = 21, 8, 2, 256, (O.Q4_K,) * 3
+    g, u, d, r = S.layer(1850 + H, E, H, I, dt)
+    banks = nm.LayerBanks(E, H, I, dt)
+    for e in range(E):
+        banks.load(e, g[e], u[e], d[e])
+    x = S.activations_bf16(1851 + H, T, H)
+    ids, w = O.topk(O.router_logits(O.from_bf16(x), r), k, O.ROUTE_SOFTMAX_TOPK)
+    idd = nm.DeviceBuffer.from_array(ids.astype(np.uint32))
+    wd = nm.DeviceBuffer.from_array(w.astype(np.float32))
+    sid = nm.DeviceBuffer.from_array(np.full((T, 1), 3, dtype=np.uint32))
+    sw = nm.DeviceBuffer.from_array(np.ones((T, 1), dtype=np.float32))
+    print(f"[prefill residual H={H} out_offset={out_offset}]", flush=True)
+    results = []
+    for fold in (False, True):
+        xd = nm.DeviceBuffer.from_array(x)
+        ob = nm.DeviceBuffer(T * H * 4 + 16)
+        out = ob.ptr + out_offset
+        nm.moe_prefill(banks, xd, idd, wd, T, k, out)
+        nm.moe_prefill(banks, xd, sid, sw, T, 1, out, accumulate=True, residual=fold)
+        if not fold:
+            nm._lib.check(nm.lib().naiwa_residual_add_bf16(xd.ptr, out, T * H, 0), "residual")
+        nm.synchronize()
+        y = ob.download(np.uint8)[out_offset:out_offset + T * H * 4].view(np.float32).reshape(T, H)
+        results.append((y, xd.download(np.uint16).reshape(T, H)))
+    (y0, x0), (y1, x1) = results
+    assert np.array_equal(y0, y1)
+    assert np.array_equal(x0, x1)
+    assert not np.array_equal(x1, x)
+    want = O.from_bf16(x) + y0
+    assert np.max(np.abs(O.from_bf16(x1) - want) / (np.abs(want) + 1e-3)) < 1e-2
+
+
 def test_prefill_one_expert_many_tokens(gpu):
     # every token on the same two experts: tiles of 32 pairs within one slot
     def mutate(ids, w):
