@@ -158,9 +158,17 @@ __device__ __forceinline__ u64 tagged(uint32_t tag, uint32_t v) { return ((u64)t
 // 16 bytes from global memory straight into LDS (no registers; counted by
 // vmcnt): lane i of the wave writes wave_base + 16 * i.  Both addresses must be
 // 16-byte aligned, and wave_base must be the same in every active lane.
+// Issued as inline assembly so that the compiler does not track it: it would
+// otherwise wait for every outstanding DMA (vmcnt(0)) before any later LDS read
+// that may alias one, which made the gate/up compute wait for the down-row
+// prefetch issued ahead of it.  Every read of DMA'd data here follows an
+// explicit vmcnt wait of the wave that issued it (and a barrier where another
+// wave reads it).
 __device__ __forceinline__ void lds_dma16(const void* src, void* wave_base) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                     (__attribute__((address_space(3))) void*)wave_base, 16, 0, 0);
+    const uint32_t lds = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(size_t)(__attribute__((address_space(3))) void*)wave_base);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(src), "s"(lds) : "memory", "m0");
 }
 
 __device__ __forceinline__ bool tag_ok(u64 w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
