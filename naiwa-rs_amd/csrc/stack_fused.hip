@@ -637,6 +637,56 @@ __device__ __forceinline__ void q4k_block_dot2(const uint8_t* A8, const uint8_t*
     }
 }
 
+// The dot of chunks c0 and c0 + 1 of one Q4_K block: the row-A half of
+// q4k_block_dot2, the same operations in the same order.
+__device__ __forceinline__ void q4k_block_dot1(const uint8_t* A8, const uint32_t* words, const float* sums, int c0,
+                                               float& ra) {
+    auto A = [&](int j) { return naiwa_ld<uint4, NAIWA_AS_LDS>(A8 + 16 * j); };
+    const Q4Scales sa = q4k_scales(A(0));
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+        const int c = c0 + cc;
+        uint4 x[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = reinterpret_cast<const uint4*>(words + 32 * c)[i];
+        const float4 sv = reinterpret_cast<const float4*>(sums)[c];
+        const uint4 qa0 = A(1 + 2 * c), qa1 = A(2 + 2 * c);
+        const uint32_t wa[8] = {qa0.x, qa0.y, qa0.z, qa0.w, qa1.x, qa1.y, qa1.z, qa1.w};
+        float alo = 0.0f, ahi = 0.0f;
+        const NaiwaNib nc = naiwa_nib_consts();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t xl[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+            const uint32_t xh[4] = {x[4 + i].x, x[4 + i].y, x[4 + i].z, x[4 + i].w};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t qa = wa[2 * i + h];
+                alo = naiwa_dot2_bf16(naiwa_nib(qa, nc), xl[2 * h], alo);
+                alo = naiwa_dot2_bf16(naiwa_nib(qa >> 8, nc), xl[2 * h + 1], alo);
+                ahi = naiwa_dot2_bf16(naiwa_nib(qa >> 4, nc), xh[2 * h], ahi);
+                ahi = naiwa_dot2_bf16(naiwa_nib(qa >> 12, nc), xh[2 * h + 1], ahi);
+            }
+        }
+        const float slo = sv.x + sv.y, shi = sv.z + sv.w;
+        ra += q4k_chunk(sa, c, alo, ahi, slo, shi);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Wait until at most n of this wave's vector memory operations are
+// outstanding (they complete in issue order, LDS DMA included); n above 15
+// waits for 15, which is stricter.
+__device__ __forceinline__ void vm_wait_at_most(int n) {
+#define NAIWA_VMW(k) case k: asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); break;
+    switch (n) {
+        NAIWA_VMW(0) NAIWA_VMW(1) NAIWA_VMW(2) NAIWA_VMW(3) NAIWA_VMW(4) NAIWA_VMW(5) NAIWA_VMW(6)
+        NAIWA_VMW(7) NAIWA_VMW(8) NAIWA_VMW(9) NAIWA_VMW(10) NAIWA_VMW(11) NAIWA_VMW(12) NAIWA_VMW(13)
+        NAIWA_VMW(14)
+        default: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
+    }
+#undef NAIWA_VMW
+}
+
 // h of every token of the segment for intermediate rows r, r + 1 (pair q),
 // with the item's rows in LDS: [gate row r][gate row r + 1][up row r][up row r + 1]
 // (rb bytes each), on 32 lanes: lane il = 16 u + 8 h + b takes chunks 2h, 2h + 1
@@ -671,6 +721,43 @@ __device__ inline void q4_pair_compute(const Params& p, const Smem& sm, const ui
             st64(&p.h[(size_t)tt * I2 + r / 2],
                  tagged(tag, Fmt<DD>::to16(h0) | (Fmt<DD>::to16(h1) << 16)));
     }
+}
+
+// One token per segment: row r of the item (its gate and up rows r) was
+// waited for by the caller; row r + 1 may still be landing, with `later` of
+// the wave's memory operations issued after it.  Row r is dotted first, then
+// the wait, then row r + 1: the same per-row arithmetic as q4_pair_compute.
+template <int DD>
+__device__ inline void q4_pair_compute_split(const Params& p, const Smem& sm, const uint8_t* dyn, int xstage, int q,
+                                             int nb, int il, const uint8_t* item, int64_t rb, uint32_t tag,
+                                             int later) {
+    const int I2 = p.I / 2, H = p.H, k = p.k;
+    const int s = q / I2, r = 2 * (q % I2);
+    const int tt = (int)sm.seg_begin[s];
+    if ((int)sm.seg_begin[s + 1] - tt != 1) { // not one token in the segment: everything landed first
+        vm_wait_at_most(later);
+        q4_pair_compute<DD>(p, sm, dyn, xstage, q, nb, il, item, rb, tag);
+        return;
+    }
+    const int b0 = il & 7, c0 = (il >> 2) & 2;
+    const uint8_t* A = item + (il >= 16 ? 2 * rb : 0) + b0 * NAIWA_Q4_K_BYTES;
+    const int t = (int)sm.sorted[tt] / k;
+    const uint32_t* words = (const uint32_t*)(dyn + t * xstage);
+    const float* sums = (const float*)(words + H / 2 + 4 * nb);
+    float g0 = 0.0f, g1 = 0.0f;
+    if (b0 < nb) q4k_block_dot1(A, words + b0 * 132, sums + b0 * 16, c0, g0);
+    vm_wait_at_most(later);
+    if (b0 < nb) q4k_block_dot1(A + rb, words + b0 * 132, sums + b0 * 16, c0, g1);
+    g0 = naiwa_group_sum<16>(g0);
+    g1 = naiwa_group_sum<16>(g1);
+    const float ga = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                                   0, __builtin_bit_cast(int, g0), 0x142, 0xA, 0xF, false));
+    const float gb = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                                   0, __builtin_bit_cast(int, g1), 0x142, 0xA, 0xF, false));
+    const float h0 = naiwa_act(p.act, ga) * g0;
+    const float h1 = naiwa_act(p.act, gb) * g1;
+    if (il == 16)
+        st64(&p.h[(size_t)tt * I2 + r / 2], tagged(tag, Fmt<DD>::to16(h0) | (Fmt<DD>::to16(h1) << 16)));
 }
 
 // ---------------------------------------------------------------------------
@@ -1086,25 +1173,28 @@ stack_kernel(Params p) {
         // routing only, so they are on their way during gate/up and the h wait
         const int npre = owner ? min(p.dpre, nvalid) : 0;
         // (and the next layer's router columns of the first chunk, for its partials)
-        auto prefetch_down = [&]() {
-            if (!owner) return;
+        // (returns the number of DMA instructions this wave issued)
+        auto prefetch_down = [&]() -> int {
+            if (!owner) return 0;
+            int n = 0;
             const int f0 = chunk_at(bid, nchunks) * kChunk;
             const int span = kChunk * (int)drb / 16; // 16-byte pieces of kChunk consecutive rows
             for (int v = wave; v < npre; v += kThreads / 64) {
                 const uint8_t* src = L.down + (int64_t)sm.pair_slot[sm.sorted[v]] * L.down_stride + (int64_t)f0 * drb;
                 uint8_t* dst = dbuf + (size_t)v * kChunk * drb;
-                for (int c = 0; c * 64 < span; ++c)
+                for (int c = 0; c * 64 < span; ++c, ++n)
                     if (c * 64 + lane < span) lds_dma16(src + (c * 64 + lane) * 16, dst + c * 1024);
             }
             if (!last) {
                 // expert e's 8 columns (two 16-byte pieces) land at rbuf[e * kChunk]
                 const float* Wn = layers_lds[l + 1].router;
                 const int rpieces = 2 * E;
-                for (int c = wave; c * 64 < rpieces; c += kThreads / 64) {
+                for (int c = wave; c * 64 < rpieces; c += kThreads / 64, ++n) {
                     const int pc = c * 64 + lane;
                     if (pc < rpieces) lds_dma16(Wn + (size_t)(pc >> 1) * H + f0 + 4 * (pc & 1), rbuf + c * 256);
                 }
             }
+            return n;
         };
         if constexpr (DG == NAIWA_Q4_K) {
             // rounds of up to p.bitems items: the gate and up row pairs of each item
@@ -1117,7 +1207,44 @@ stack_kernel(Params p) {
             const int half = (tid >> 5) & 1, il = tid & 31;
             const int wslot = (wave + 7) % 8;
             const int my_item = wslot + 8 * half;
-            for (int r0 = q0; r0 < q1; r0 += p.bitems) {
+            for (int r0 = q0; r0 < q1 && MR == 1; r0 += p.bitems) {
+                // one token: rows r of the wave's items (gate and up) go out first, then
+                // rows r + 1, and the wave dots rows r while rows r + 1 are landing
+                const int nr = min(p.bitems, q1 - r0);
+                const int row_pieces = (int)(rb / 16);
+                int n1 = 0; // DMA instructions of the rows r + 1
+                for (int rr = 0; rr < 2; ++rr) {
+                    for (int i = wslot; i < nr; i += kThreads / 64) {
+                        const int q = r0 + i;
+                        const uint32_t slot = sm.seg_slot[q / I2];
+                        const int64_t roff = (int64_t)(2 * (q % I2) + rr) * rb;
+                        const uint8_t* g = L.gate + (int64_t)slot * L.gate_stride + roff;
+                        const uint8_t* u = L.up + (int64_t)slot * L.up_stride + roff;
+                        uint8_t* dst = wb + (size_t)i * item_bytes + (size_t)rr * rb;
+                        for (int c = 0; c * 64 < row_pieces; ++c) {
+                            if (c * 64 + lane < row_pieces) {
+                                lds_dma16(g + (c * 64 + lane) * 16, dst + c * 1024);
+                                lds_dma16(u + (c * 64 + lane) * 16, dst + 2 * rb + c * 1024);
+                            }
+                            n1 += 2 * rr;
+                        }
+                    }
+                }
+                if (r0 == q0) weigh();
+                vm_wait_at_most(n1); // rows r have landed (later operations only make it stricter)
+                int npf = 0;
+                if (r0 == q0) {
+                    mark(p, l, 3);
+                    mark_wave(p, l, 21);
+                    npf = prefetch_down();
+                }
+                if (my_item < nr)
+                    q4_pair_compute_split<DD>(p, sm, dyn, xstage, r0 + my_item, nb, il, wb + my_item * item_bytes, rb,
+                                              tag, npf);
+                else
+                    vm_wait_at_most(npf); // the wave's own pieces land before the region is reused
+            }
+            for (int r0 = q0; r0 < q1 && MR != 1; r0 += p.bitems) {
                 const int nr = min(p.bitems, q1 - r0);
                 for (int i = wslot; i < nr; i += kThreads / 64) {
                     const int q = r0 + i;
