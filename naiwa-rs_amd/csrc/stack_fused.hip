@@ -163,7 +163,10 @@ __device__ __forceinline__ u64 tagged(uint32_t tag, uint32_t v) { return ((u64)t
 // that may alias one, which made the gate/up compute wait for the down-row
 // prefetch issued ahead of it.  Every read of DMA'd data here follows an
 // explicit vmcnt wait of the wave that issued it (and a barrier where another
-// wave reads it).
+// wave reads it).  M0 is a reserved register, so the compiler warns that the
+// clobber is not honoured: this is sound only while nothing else in the kernel
+// keeps a value in M0 (no LDS DMA builtins, no relative-indexing moves), which
+// the generated assembly shows and must keep showing after changes here.
 __device__ __forceinline__ void lds_dma16(const void* src, void* wave_base) {
     const uint32_t lds = __builtin_amdgcn_readfirstlane(
         (uint32_t)(size_t)(__attribute__((address_space(3))) void*)wave_base);
