@@ -341,8 +341,9 @@ def print_trace(nm, run, stream, L, khz):
     log("trace: critical path us/layer: " + ", ".join(f"{n} {np.mean(v):.2f}" for n, v in crit.items()) +
         f" | sum {sum(np.mean(v) for n, v in crit.items() if n != 'h recv spread'):.2f}")
     land = t[:, : L - 1, 21] - t[:, : L - 1, 3]
-    log(f"trace: gate/up rows landed, last wave after wave 0: median {np.median(land):.2f} us; "
-        f"last wave's compute {np.median(t[:, : L - 1, 16] - t[:, : L - 1, 21]):.2f}; "
+    # (at one token, marks 21 follow the first of the two landing groups, rows r of each item)
+    log(f"trace: gate/up rows (r) landed, last wave after wave 0: median {np.median(land):.2f} us; "
+        f"last wave's compute (and rows r + 1 landing) {np.median(t[:, : L - 1, 16] - t[:, : L - 1, 21]):.2f}; "
         f"top-k ready {np.median(t[:, : L - 1, 22] - t[:, : L - 1, 1]):.2f} after the ranks, pairs grouped "
         f"{np.median(t[:, : L - 1, 12] - t[:, : L - 1, 22]):.2f} later")
     cyc = np.frombuffer(buf, dtype=np.uint64)[: G * (L + 1) * slots].reshape(G, L + 1, slots)[:, :L, 23]
