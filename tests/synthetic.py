@@ -16,11 +16,31 @@ def stream(seed: int, tensor: int) -> int:
     return seed * 64 + tensor
 
 
+_POOL = None
+
+
+def _pool():
+    global _POOL
+    if _POOL is None:
+        import concurrent.futures as cf
+        import os
+        _POOL = cf.ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1))
+    return _POOL
+
+
 def quantized_stack(seed: int, tensor: int, E: int, N: int, K: int, dtype: int,
                     std: float = 0.02) -> np.ndarray:
-    """uint8 [E, N, row_bytes]: N(0, std) values quantized row by row."""
-    vals = O.normal(stream(seed, tensor), E * N * K, 0.0, std)
-    return O.quantize(dtype, vals.reshape(E, N, K))
+    """uint8 [E, N, row_bytes]: N(0, std) values quantized row by row.  Experts are
+    generated and quantized in parallel (the counter-based stream at each expert's
+    offset gives the same values as one sequential draw)."""
+    out = np.empty((E, N, O.row_bytes(dtype, K)), dtype=np.uint8)
+
+    def one(e):
+        vals = O.normal(stream(seed, tensor), N * K, 0.0, std, offset=e * N * K)
+        out[e] = O.quantize(dtype, vals.reshape(N, K))
+
+    list(_pool().map(one, range(E)))
+    return out
 
 
 def layer(seed: int, E: int, H: int, I: int, dtypes=(O.Q4_K, O.Q4_K, O.Q4_K), std: float = 0.02):
