@@ -106,6 +106,12 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cache-layers", type=int, default=32, metavar="N",
                     help="mixtral: layers of the 4-of-8 cached decode (each pins 0.8 GB of host stacks)")
     ap.add_argument("--db-iters", type=int, default=20000, help="doorbell: round trips timed")
+    ap.add_argument("--upload-sync", choices=["event", "poll"], default="poll",
+                    help="cache25: staged uploads complete into the expert pass through an event the compute "
+                         "stream waits for, or a device flag one wave polls")
+    ap.add_argument("--pcie-frac", type=float, default=1.0,
+                    help="cache25: share of each step's missed experts staged over PCIe; the rest run on the "
+                         "CPU (the reference's default is 0)")
     ap.add_argument("--workload", choices=["resident", "cache25", "prefill", "prefill-stream", "mixtral", "doorbell"],
                     default="resident",
                     help="resident: every expert in HBM (the headline); cache25: 32 of 128 experts "
@@ -507,6 +513,8 @@ def run_cache25(args) -> int:
         banks = nm.LayerBanks(usable + ring.length, H, I, dt, contiguous=True)
         layer = nm.policy.CachedLayer(router, banks, stacks, E, K, usable, ring, copy.handle,
                                       mode=nm.ROUTE_SOFTMAX_TOPK_RENORM, router_bias=bias_d)
+        layer.set_upload_sync(nm.policy.UPLOAD_SYNC_POLL if args.upload_sync == "poll"
+                              else nm.policy.UPLOAD_SYNC_EVENT)
         ranking += [(l, int(e)) for e in np.argsort(ranks)]
         layers.append(layer)
         keep += [stacks, router, bias_d, banks]
@@ -533,11 +541,12 @@ def run_cache25(args) -> int:
         lib.naiwa_memcpy_d2d(x.ptr, xs.ptr + i * rows * H * 2, rows * H * 2, compute.handle)
         # every layer's partial-cache step and residual in order (with swaps >= 0 each layer
         # also predicts the next layer's experts from its activation and loads them)
-        info, ahead = nm.policy.CachedLayer.stack_forward(layers, x, rows, y, pcie_frac=1.0, promote_cap=1,
-                                                          min_hits=4, lookahead_swaps=swaps, stream=compute.handle)
+        info, ahead = nm.policy.CachedLayer.stack_forward(layers, x, rows, y, pcie_frac=args.pcie_frac,
+                                                          promote_cap=1, min_hits=4, lookahead_swaps=swaps,
+                                                          stream=compute.handle)
         for k_ in ahead_tot:
             ahead_tot[k_] += ahead[k_]
-        return {k_: info[k_] for k_ in ("hits", "staged", "staged_experts", "promoted", "pcie_bytes")}
+        return {k_: info[k_] for k_ in ("hits", "staged", "staged_experts", "promoted", "pcie_bytes", "cpu")}
 
     for i in range(warmup):
         step(i)
@@ -546,7 +555,7 @@ def run_cache25(args) -> int:
     nm.policy.stats(reset=True)
     for k_ in ahead_tot:
         ahead_tot[k_] = 0
-    tot = {"hits": 0, "staged": 0, "staged_experts": 0, "promoted": 0, "pcie_bytes": 0}
+    tot = {"hits": 0, "staged": 0, "staged_experts": 0, "promoted": 0, "pcie_bytes": 0, "cpu": 0}
     e0, e1 = nm.Event(), nm.Event()
     e0.record(compute.handle)
     start = time.perf_counter()
@@ -559,10 +568,12 @@ def run_cache25(args) -> int:
     wall = time.perf_counter() - start
     ms = e0.elapsed_ms(e1)
     tok_s = rows * steps / (ms / 1e3)
-    pairs = tot["hits"] + tot["staged"]
+    pairs = tot["hits"] + tot["staged"] + tot["cpu"]
     pcie_gbs = tot["pcie_bytes"] / (ms / 1e3) / 1e9
-    log(f"cache25: {ms / steps * 1e3:.1f} us/step, {tok_s:.1f} tok/s, hit rate {tot['hits'] / pairs:.3f}, "
-        f"{tot['staged_experts'] / (steps * L):.2f} staged experts/layer/token, {tot['promoted']} promotions, "
+    log(f"cache25 ({args.upload_sync}, pcie_frac {args.pcie_frac}): {ms / steps * 1e3:.1f} us/step, "
+        f"{tok_s:.1f} tok/s, hit rate {tot['hits'] / pairs:.3f}, "
+        f"{tot['staged_experts'] / (steps * L):.2f} staged experts/layer/token, "
+        f"{tot['cpu'] / (steps * L):.2f} CPU pairs/layer/token, {tot['promoted']} promotions, "
         f"PCIe {pcie_gbs:.1f} GB/s, wall {wall:.2f}s")
     if swaps >= 0:
         log(f"cache25 lookahead (swaps {swaps}/row): {ahead_tot['loads']} loads, {ahead_tot['swaps']} swaps, "
@@ -573,11 +584,14 @@ def run_cache25(args) -> int:
         "ms_per_step": round(ms / steps, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16 x Q4_K (f32 accumulate)", "data": "synthetic (device-generated N(0,0.02) Q4_K experts in pinned host stacks)",
         "config": {"workload": "Qwen3-30B-A3B-shaped MoE stack decode, bs1, 32/128 experts cached per layer, "
-                               "Zipf(1.1) routing bias, misses staged over PCIe (16-slot ring)",
+                               "Zipf(1.1) routing bias, the pcie_frac share of misses staged over PCIe "
+                               "(16-slot ring), the rest on the CPU",
                    "layers": L, "hidden": H, "experts": E, "top_k": K, "intermediate": I, "cached": usable,
-                   "ring": ring.length, "pcie_frac": 1.0, "promote_cap": 1,
+                   "ring": ring.length, "pcie_frac": args.pcie_frac, "upload_sync": args.upload_sync,
+                   "promote_cap": 1,
                    "lookahead_swaps": swaps if swaps >= 0 else None, "parallelism": "none (1 GPU)"},
         "cache": {"hit_rate": round(tot["hits"] / pairs, 4),
+                  "cpu_pairs_per_layer_token": round(tot["cpu"] / (steps * L), 3),
                   "staged_experts_per_layer_token": round(tot["staged_experts"] / (steps * L), 3),
                   "promotions": tot["promoted"], "pcie_bytes": tot["pcie_bytes"],
                   "lookahead": dict(ahead_tot) if swaps >= 0 else None,

@@ -16,10 +16,12 @@
  * ring slot NAIWA_STAGING_RING_FIRST + p is bank slot usable + p (the
  * reference's `slot - bank.first` for its ring bank).
  *
- * Misses the ring cannot take run on the CPU in the reference; this library
- * has no product CPU expert path, so a step that leaves any miss unstaged
- * fails with NAIWA_E_UNSUPPORTED (use pcie_frac 1 and a ring at least as long
- * as the step's distinct misses).
+ * Misses the ring does not take run on the CPU, as in the reference
+ * (src/moe/stages/cpu_miss.rs:73-162): the step publishes x to mapped host
+ * memory, a CPU job on a one-thread executor computes those pairs from the
+ * host expert stacks (naiwa_cpu_moe_decode), and its result comes back through
+ * a result doorbell that the device waits for on the stream and adds last:
+ * resident, then staged, then CPU (src/moe/decode.rs:371-381).
  */
 #ifndef NAIWA_CACHED_H
 #define NAIWA_CACHED_H
@@ -58,7 +60,31 @@ typedef struct naiwa_cached_step {
     int promoted;    /* experts copied staging -> cache */
     int64_t pcie_bytes;
     int preload_waits; /* 1 when the expert kernel waited for a lookahead claim */
+    int cpu;         /* pairs computed on the CPU (the reference's misses) */
 } naiwa_cached_step;
+
+/* Host expert stacks for the CPU expert path: expert e's projection p at
+ * p + e * p_stride (0: that projection's own bytes, the GGUF [E, N, K] layout);
+ * gate and up are [inter, hidden], down [hidden, inter]; Q4_K or Q8_0. */
+typedef struct naiwa_host_experts {
+    const void* gate;
+    const void* up;
+    const void* down;
+    int64_t gate_stride, up_stride, down_stride;
+    int gate_dtype, up_dtype, down_dtype;
+    int num_experts, hidden, inter;
+} naiwa_host_experts;
+
+/* The reference's CPU expert contract, fused_moe_decode
+ * (src/moe/stages/cpu_miss.rs:13-20, :45): xs f32 [rows, hidden]; ids / w
+ * [rows, width] row-major, weight-0 entries skipped (padding); pass 1 computes
+ * act(gate . x) * (up . x) once per distinct (expert, row), pass 2 writes
+ * out[row] = sum over the row's entries in order of w * (down . h) (f32
+ * [rows, hidden]).  f32 activations, weights dequantised on the fly; host
+ * threads of a persistent pool (one call at a time runs on it).  Synchronous;
+ * no device memory is touched.  NAIWA_E_BAD_ID for an id >= num_experts. */
+int naiwa_cpu_moe_decode(const naiwa_host_experts* ex, const float* xs, const uint32_t* ids, const float* w,
+                         int rows, int width, int act, float* out);
 
 /* Per-call report of the lookahead (src/moe/cached_layer.rs:1262-1295). */
 typedef struct naiwa_lookahead_step {
@@ -103,13 +129,39 @@ int naiwa_cached_layer_seed(naiwa_cached_layer* L, const uint32_t* experts, int 
  * synchronising the stream.  Steps of one layer are ordered even when each
  * is queued on another stream (a step waits for the previous step's last
  * read of the layer's buffers).  Staged uploads complete into the staged
- * expert pass through an event the stream waits for, or, with the
- * environment variable NAIWA_UPLOAD_SYNC=poll, through a device flag the
- * copy stream raises and one device wave polls (doorbell_poll_signal /
- * doorbell_poll_wait).  pcie_frac, promote_cap and min_hits are the
- * reference's --pcie-frac, NAIWA_PROMOTE_CAP and NAIWA_PROMOTE_MIN_HITS. */
+ * expert pass as naiwa_cached_layer_set_upload_sync chooses.  Misses left
+ * out of the ring run on the CPU (naiwa_cpu_moe_decode on the library's
+ * executor) while the device computes the resident and staged pairs; the
+ * device waits for their result doorbell (bounded, naiwa_doorbell_set_wait_limit_us)
+ * and adds it last.  A CPU job that failed is reported (NAIWA_E_DEVICE, or
+ * its own code) by the layer's next call, before that call changes any state.
+ * pcie_frac, promote_cap and min_hits are the reference's --pcie-frac,
+ * NAIWA_PROMOTE_CAP and NAIWA_PROMOTE_MIN_HITS; info->cpu counts the CPU pairs. */
 int naiwa_cached_layer_forward(naiwa_cached_layer* L, const void* x, int rows, float* out, float pcie_frac,
                                int promote_cap, uint64_t min_hits, int64_t stream, naiwa_cached_step* info);
+
+/* How staged uploads complete into the expert pass (per layer):
+ *  NAIWA_UPLOAD_SYNC_EVENT: an event recorded on the copy stream after the
+ *    uploads, which the compute stream waits for;
+ *  NAIWA_UPLOAD_SYNC_POLL (the default): the copy stream raises a device flag behind the
+ *    uploads (doorbell_poll_signal) and one wave on the compute stream polls it
+ *    (the persistent-wave doorbell of the reference's device waits,
+ *    src/doorbell/doorbell.cu:105-149).  The poll is bounded
+ *    (naiwa_doorbell_set_wait_limit_us): a wait that runs out leaves that
+ *    step's output invalid and is counted in the layer's mapped doorbell; the
+ *    layer's next forward returns NAIWA_E_TIMEOUT for it before it changes
+ *    any state, and naiwa_cached_layer_upload_timeouts reads the count. */
+#define NAIWA_UPLOAD_SYNC_EVENT 0
+#define NAIWA_UPLOAD_SYNC_POLL 1
+int naiwa_cached_layer_set_upload_sync(naiwa_cached_layer* L, int mode);
+int naiwa_cached_layer_upload_timeouts(const naiwa_cached_layer* L, uint32_t* count);
+
+/* Misses the ring does not take go to the CPU (1, the default) or, with 0, a
+ * step that would leave any miss unstaged is refused with NAIWA_E_UNSUPPORTED
+ * before the policy is touched (naiwa_cache_plan decides; no tick, hit count or
+ * ring position moves).  No counterpart in the reference, whose misses always
+ * may go to the CPU; for hosts that keep every expert computation on the GPU. */
+int naiwa_cached_layer_set_cpu_misses(naiwa_cached_layer* L, int on);
 
 /* prefetch_predicted (src/moe/cached_layer.rs:1262-1300) for layer `next` on
  * the activation x bf16 [rows, H] of the layer before it: next's router ranks
@@ -131,7 +183,7 @@ int naiwa_cached_layer_prefetch(naiwa_cached_layer* next, const void* x, int row
  * on the same x with one routing read-back: next's router is queued beside
  * L's, and next's uploads after L's expert kernel, so they overlap L's
  * compute (the reference's Preload stage, src/moe/stages/preload.rs:18-111).
- * next != L and has L's hidden size. */
+ * next != L and has L's hidden size and top_k (NAIWA_E_INVALID otherwise). */
 int naiwa_cached_layer_forward_ahead(naiwa_cached_layer* L, naiwa_cached_layer* next, int lookahead_swaps,
                                      const void* x, int rows, float* out, float pcie_frac, int promote_cap,
                                      uint64_t min_hits, int64_t stream, naiwa_cached_step* info,

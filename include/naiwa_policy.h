@@ -130,6 +130,19 @@ int naiwa_ring_acquire(naiwa_ring* r, int n, int* start);
 int naiwa_cache_stage(naiwa_ring* r, const uint32_t* ids, const float* w, int rows, int k, float frac,
                       int32_t* slot_io, uint32_t* chosen_out, int32_t* pos_out, int* n_chosen);
 
+/* A step's split without doing it: what naiwa_cache_route followed by
+ * naiwa_cache_stage (ring of ring_len slots) would report for these ids and
+ * weights -- pairs on a published slot, pairs of the misses chosen for the
+ * ring, the chosen experts, and the pairs left to the CPU -- with no state
+ * changed (tick, hit counts, last_use and the ring cursor stay as they are).
+ * No counterpart in the reference; the partial-cache step checks with it
+ * before it commits a step it could not finish. */
+typedef struct naiwa_step_plan {
+    int hits, staged, staged_experts, cpu;
+} naiwa_step_plan;
+int naiwa_cache_plan(const naiwa_cache* c, int ring_len, const uint32_t* ids, const float* w, int rows, int k,
+                     float frac, naiwa_step_plan* out);
+
 /* The expert-cache profile (src/moe/profile.rs:50-112): a file of (layer,
  * expert) pairs ranked best first ("STRP", u32 version 1, layers, experts,
  * slots, n, then n u16 pairs; the trailing rank table is not read).  Each

@@ -6,17 +6,21 @@
 // (src/moe/cached_layer.rs:1236-1300, src/moe/stages/preload.rs:18-111).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <chrono>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <initializer_list>
+#include <memory>
+#include <mutex>
 #include <new>
 #include <thread>
 #include <vector>
 
 #include "../../include/naiwa_cached.h"
+#include "../../include/naiwa_doorbell.h"
 #include "common.h"
 #include "decode.h"
 #include "router.h"
@@ -59,14 +63,74 @@ __global__ void __launch_bounds__(64) pull_inputs_kernel(uint32_t* dst, const ui
     for (int i = threadIdx.x; i < nwords; i += 64) dst[i] = src[i];
 }
 
-// Staged-upload completion as a flag polled by one device wave (NAIWA_UPLOAD_SYNC=poll)
-// instead of an event the compute stream waits for (the default).
-bool upload_sync_poll() {
-    static const bool poll = [] {
-        const char* v = getenv("NAIWA_UPLOAD_SYNC");
-        return v && strcmp(v, "poll") == 0;
-    }();
-    return poll;
+// The staged-upload wait of the poll mode: one wave spins (bounded) until the copy
+// stream's flag reaches target.  A wait that runs out adds one to *fail (a word of the
+// layer's mapped routing doorbell, read by the host before its next step), so the
+// step's output is known to be invalid instead of silently wrong.
+__global__ void __launch_bounds__(64)
+staged_wait_kernel(const uint32_t* flag, uint32_t target, uint64_t limit_ticks, uint32_t* fail) {
+    if (threadIdx.x != 0) return;
+    const uint64_t t0 = wall_clock64();
+    while (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) < target) {
+        if (wall_clock64() - t0 > limit_ticks) {
+            const uint32_t n = __hip_atomic_load(fail, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(fail, n + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// The step's activations for the CPU job: bf16 x [n] as f32 into mapped host memory
+// behind a sequence word (the reference's ActivationDoorbell publish,
+// src/doorbell/d2h/activation.rs:17-116): payload, system fence, then seq + 1.
+constexpr int kXHead = 64; // words before the payload
+__global__ void __launch_bounds__(256) x_publish_kernel(uint32_t* db, const uint16_t* x, int n) {
+    volatile float* out = reinterpret_cast<volatile float*>(db + kXHead);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = __uint_as_float((uint32_t)x[i] << 16);
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t cur = __hip_atomic_load(db, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(db, cur + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
+// out += cpu (the CPU pairs' sum, added after the resident and staged pairs).
+__global__ void add_f32_kernel(float* out, const float* cpu, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) out[i] += cpu[i];
+}
+
+// The CPU misses run on one process-wide executor worker (the reference's
+// executor::cpu(), src/executor.rs:116-166), created on first use.
+naiwa_executor* cpu_executor(int* rc) {
+    static naiwa_executor* ex = nullptr;
+    static int create_rc = NAIWA_OK;
+    static std::once_flag once;
+    std::call_once(once, [] { create_rc = naiwa_executor_create(&ex); });
+    *rc = create_rc;
+    return ex;
+}
+
+// One CPU job: wait for the published activations (bounded, the reference's 250 ms),
+// copy them out of the mapped page, run the CPU pairs.
+constexpr int64_t kXWaitUs = 250 * 1000;
+struct CpuJob {
+    naiwa_host_experts hx;
+    const uint32_t* seq;   // host view of the publish page
+    uint32_t target;
+    int rows, width, act;
+    std::vector<uint32_t> ids;
+    std::vector<float> w;  // 0 for the pairs served on the device
+};
+int cpu_job_run(void* user, float* out, int len) {
+    std::unique_ptr<CpuJob> j(static_cast<CpuJob*>(user));
+    const int H = j->hx.hidden;
+    if (len != j->rows * H) return NAIWA_E_INVALID;
+    if (naiwa_host_wait_ge(j->seq, j->target, kXWaitUs, 20) != NAIWA_OK) return NAIWA_E_TIMEOUT;
+    const float* src = reinterpret_cast<const float*>(j->seq + kXHead);
+    std::vector<float> x(src, src + (size_t)len);
+    return naiwa_cpu_moe_decode(&j->hx, x.data(), j->ids.data(), j->w.data(), j->rows, j->width, j->act, out);
 }
 
 // Bound of the host's wait for a routing doorbell.
@@ -131,9 +195,20 @@ struct naiwa_cached_layer {
     // the stream of the previous step: a step on another stream waits for read_done first
     hipStream_t last_stream = nullptr;
     bool have_last_stream = false;
-    // staged-upload completion flag (device word) and its epoch, for NAIWA_UPLOAD_SYNC=poll
+    // staged-upload completion: an event the stream waits for, or (poll mode) a device
+    // flag the copy stream raises and one wave polls; the flag and its epoch
+    int upload_sync = NAIWA_UPLOAD_SYNC_POLL; // measured faster on cache25 (165.6 vs 159.9 tok/s)
     uint32_t* upload_flag = nullptr;
     uint32_t upload_epoch = 0;
+    uint32_t upload_fail_seen = 0;       // poll waits that ran out, as already reported
+    // misses left to the CPU: the host stacks, the activation publish page
+    // [seq][pad][rows * H f32] (mapped), its publishes so far, and the CPU sum on the device
+    bool cpu_misses = true;
+    naiwa_host_experts hx{};
+    uint32_t* xpub_host = nullptr;
+    uint32_t* xpub_dev = nullptr;
+    uint32_t xpub_seq = 0;
+    float* cpu_out = nullptr;
     std::vector<hipEvent_t> ring_fence;  // per ring position: recorded after the step that read it
     std::vector<char> ring_fenced;
     hipEvent_t staged_done = nullptr;
@@ -172,6 +247,11 @@ struct naiwa_cached_layer {
         if (pred_ids_dev) (void)hipFree(pred_ids_dev);
         if (pred_w_dev) (void)hipFree(pred_w_dev);
         if (pred_ids_h) (void)hipHostFree(pred_ids_h);
+        if (xpub_host) (void)doorbell_free_host(xpub_host);
+        if (cpu_out) (void)hipFree(cpu_out);
+        xpub_host = xpub_dev = nullptr;
+        xpub_seq = 0;
+        cpu_out = nullptr;
         pred_ids_dev = nullptr;
         pred_w_dev = nullptr;
         pred_ids_h = nullptr;
@@ -189,29 +269,39 @@ struct naiwa_cached_layer {
         const size_t n = (size_t)rows * d.top_k;
         void* db = nullptr;
         void* in = nullptr;
+        void* xp = nullptr;
+        const size_t xn = (size_t)rows * d.hidden;
         if (hipMalloc(&route_dev_base, 2 * n * 4) != hipSuccess || hipMalloc(&in_dev_base, 3 * n * 4) != hipSuccess ||
             doorbell_alloc_mapped(&db, (kDbHead + 3 * n) * 4) != NAIWA_OK ||
             doorbell_alloc_mapped(&in, 3 * n * 4) != NAIWA_OK || hipHostMalloc(&slots_h, n * 4, 0) != hipSuccess ||
             hipMalloc(&pred_ids_dev, n * 4) != hipSuccess || hipMalloc(&pred_w_dev, n * 4) != hipSuccess ||
-            hipHostMalloc(&pred_ids_h, n * 4, 0) != hipSuccess) {
+            hipHostMalloc(&pred_ids_h, n * 4, 0) != hipSuccess ||
+            doorbell_alloc_mapped(&xp, (kXHead + xn) * 4) != NAIWA_OK || hipMalloc(&cpu_out, xn * 4) != hipSuccess) {
             if (db) db_host = (uint32_t*)db;
             if (in) in_h_base = (uint32_t*)in;
+            if (xp) xpub_host = (uint32_t*)xp;
             release_buffers();
             return NAIWA_E_NOMEM;
         }
         db_host = (uint32_t*)db;
         in_h_base = (uint32_t*)in;
+        xpub_host = (uint32_t*)xp;
         void* dv = nullptr;
         void* iv = nullptr;
+        void* xv = nullptr;
         doorbell_get_device_ptr(db, &dv);
         doorbell_get_device_ptr(in, &iv);
-        if (!dv || !iv) {
+        doorbell_get_device_ptr(xp, &xv);
+        if (!dv || !iv || !xv) {
             release_buffers();
             return NAIWA_E_DEVICE;
         }
         db_dev = (uint32_t*)dv;
         in_map_base = (uint32_t*)iv;
+        xpub_dev = (uint32_t*)xv;
         db_seq = 0;
+        upload_fail_seen = 0;
+        xpub_seq = 0;
         cap_rows = rows;
         return NAIWA_OK;
     }
@@ -330,11 +420,19 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
                  naiwa_cached_step* info, naiwa_lookahead_step* ahead, void* res_x = nullptr,
                  bool* folded = nullptr) {
     if (!L || !x || !out || rows <= 0 || swaps_per_row < 0) return NAIWA_E_INVALID;
-    if (next && (next == L || next->d.hidden != L->d.hidden)) return NAIWA_E_INVALID;
+    // the lookahead publishes the next layer's prediction in this layer's routing
+    // doorbell, sized for this layer's top_k
+    if (next && (next == L || next->d.hidden != L->d.hidden || next->d.top_k != L->d.top_k)) return NAIWA_E_INVALID;
     const naiwa_cached_layer_desc& d = L->d;
     const int k = d.top_k, n = rows * k;
     hipStream_t st = (hipStream_t)stream;
-    int rc = L->ensure_rows(rows);
+    // a CPU job of an earlier step that failed (its result was not computed): report it
+    // before this step touches anything
+    int rc = NAIWA_OK;
+    naiwa_executor* ex = L->cpu_misses ? cpu_executor(&rc) : nullptr;
+    if (rc) return rc;
+    if (ex && (rc = naiwa_executor_take_error(ex, nullptr, 0))) return rc;
+    rc = L->ensure_rows(rows);
     if (!rc && next) rc = next->ensure_rows(rows);
     if (rc) return rc;
     L->views(n);
@@ -378,7 +476,25 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     if ((rc = wait_routing(L->db_host, ++L->db_seq))) return rc;
     L->last_rows = rows;
 
-    // hit/miss split, then the misses to stream into the ring
+    // the previous step's staged-upload wait ran out (poll mode; its kernels ran before
+    // this step's routing): that step's output was invalid.  Reported before any policy
+    // state changes.
+    {
+        const uint32_t fails = naiwa_host_load_acquire_u32(L->db_host + 1);
+        if (fails != L->upload_fail_seen) {
+            L->upload_fail_seen = fails;
+            return NAIWA_E_TIMEOUT;
+        }
+    }
+    // without the CPU path, a step that would leave a miss unstaged is refused before
+    // the policy is touched (no tick, hit count or ring position moves)
+    if (!L->cpu_misses) {
+        naiwa_step_plan plan{};
+        if ((rc = naiwa_cache_plan(L->cache, L->ring_len, L->ids_h, L->w_h, rows, k, pcie_frac, &plan))) return rc;
+        if (plan.cpu > 0) return NAIWA_E_UNSUPPORTED;
+    }
+
+    // hit/miss split, then the misses to stream into the ring; the rest go to the CPU
     if ((rc = naiwa_cache_route(L->cache, L->ids_h, rows, k, L->slots_h))) return rc;
     std::vector<uint32_t> chosen((size_t)L->ring_len);
     std::vector<int32_t> pos((size_t)L->ring_len);
@@ -386,9 +502,13 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     if ((rc = naiwa_cache_stage(L->ring, L->ids_h, L->w_h, rows, k, pcie_frac, L->slots_h, chosen.data(), pos.data(),
                                 &nc)))
         return rc;
+    std::vector<char> on_cpu((size_t)n, 0);
     for (int i = 0; i < n; ++i) {
-        if (L->slots_h[i] < 0) return NAIWA_E_UNSUPPORTED; // a CPU miss: no product CPU path here
-        if (L->slots_h[i] >= NAIWA_STAGING_RING_FIRST) {
+        if (L->slots_h[i] < 0) { // a CPU pair: slot 0 with weight 0 on the device
+            ++step.cpu;
+            on_cpu[(size_t)i] = 1;
+            L->slots_up[i] = 0u;
+        } else if (L->slots_h[i] >= NAIWA_STAGING_RING_FIRST) {
             ++step.staged;
             L->slots_up[i] = (uint32_t)(d.usable + (L->slots_h[i] - NAIWA_STAGING_RING_FIRST));
         } else {
@@ -396,6 +516,7 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
             L->slots_up[i] = (uint32_t)L->slots_h[i];
         }
     }
+    const bool cpu = step.cpu > 0;
 
     // Staged uploads by the batched copy kernel hold up kernels that run beside them (its
     // PCIe reads stall the memory pipeline they share), so a cache-pair pass queued ahead
@@ -413,12 +534,13 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     // first (its few PCIe reads would otherwise queue behind megabytes of upload reads).
     // One pass after the uploads (or with none) reads the slot ids from the mapped memory
     // itself, in the gate/up segmentation: one launch and its gap fewer per layer.
-    if (split) {
+    // With CPU pairs, one pass reads the weights there too, the CPU pairs' set to 0.
+    if (split || cpu) {
         float* w_res = L->wsplit_h;
         float* w_stg = L->wsplit_h + n;
         for (int i = 0; i < n; ++i) {
-            const bool staged_pair = L->slots_up[i] >= (uint32_t)d.usable;
-            w_res[i] = staged_pair ? 0.0f : L->w_h[i];
+            const bool staged_pair = !on_cpu[(size_t)i] && L->slots_up[i] >= (uint32_t)d.usable;
+            w_res[i] = on_cpu[(size_t)i] || (split && staged_pair) ? 0.0f : L->w_h[i];
             w_stg[i] = staged_pair ? L->w_h[i] : 0.0f;
         }
     }
@@ -428,6 +550,31 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         if ((rc = naiwa_hip_rc(hipGetLastError()))) return rc;
     }
     const uint32_t* slot_ids = split ? L->slots_dev : L->in_map_base;
+    const float* w_one = cpu ? (const float*)(L->in_map_base + n) : L->w_dev; // one pass: its weights
+
+    // the CPU pairs: x goes out through the publish page, and the job (the pairs' ids,
+    // weights 0 except on the CPU pairs) is queued on the executor now, so it runs while
+    // the device takes the resident and staged pairs (src/moe/stages/cpu_miss.rs:73-162)
+    naiwa_pending pend{};
+    if (cpu) {
+        x_publish_kernel<<<1, 256, 0, st>>>(L->xpub_dev, (const uint16_t*)x, rows * d.hidden);
+        if ((rc = naiwa_hip_rc(hipGetLastError()))) return rc;
+        CpuJob* job = new (std::nothrow) CpuJob;
+        if (!job) return NAIWA_E_NOMEM;
+        job->hx = L->hx;
+        job->seq = L->xpub_host;
+        job->target = ++L->xpub_seq;
+        job->rows = rows;
+        job->width = k;
+        job->act = d.act;
+        job->ids.assign(L->ids_h, L->ids_h + n);
+        job->w.resize((size_t)n);
+        for (int i = 0; i < n; ++i) job->w[(size_t)i] = on_cpu[(size_t)i] ? L->w_h[i] : 0.0f;
+        if ((rc = naiwa_executor_submit_result(ex, rows * d.hidden, cpu_job_run, job, &pend))) {
+            delete job;
+            return rc;
+        }
+    }
 
     // uploads on the copy stream after the last step that read each ring slot: one kernel
     // for all of them when the host stacks are mapped pinned memory (one range per expert
@@ -458,9 +605,16 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         step.pcie_bytes += (int64_t)nc * (int64_t)(L->bytes[0] + L->bytes[1] + L->bytes[2]);
     }
     step.staged_experts = nc;
-    const bool poll = upload_sync_poll();
+    const bool poll = L->upload_sync == NAIWA_UPLOAD_SYNC_POLL;
     if (nc && poll && (rc = doorbell_poll_signal(L->upload_flag, ++L->upload_epoch, (int64_t)L->copy))) return rc;
     if (nc && !poll && (rc = naiwa_hip_rc(hipEventRecord(L->staged_done, L->copy)))) return rc;
+    // the stream's wait for the staged uploads
+    auto wait_staged = [&]() -> int {
+        if (!poll) return naiwa_hip_rc(hipStreamWaitEvent(st, L->staged_done, 0));
+        staged_wait_kernel<<<1, 64, 0, st>>>(L->upload_flag, L->upload_epoch, naiwa_doorbell_wait_limit_ticks(),
+                                             L->db_dev + 1);
+        return naiwa_hip_rc(hipGetLastError());
+    };
 
     // the expert kernel after the latest lookahead claim (src/moe/cached_layer.rs:808-819):
     // a slot it published may still be in flight
@@ -469,18 +623,14 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         ++step.preload_waits;
     }
     if (!split) {
-        if (nc) {
-            rc = poll ? doorbell_poll_wait(L->upload_flag, L->upload_epoch, stream)
-                      : naiwa_hip_rc(hipStreamWaitEvent(st, L->staged_done, 0));
-            if (rc) return rc;
-        }
-        if (res_x) {
+        if (nc && (rc = wait_staged())) return rc;
+        if (res_x && !cpu) {
             // out keeps the layer's output; the residual rides in the ordered combine
-            if ((rc = naiwa_moe_decode_residual(&d.gate, &d.up, &d.down, res_x, slot_ids, L->w_dev, rows, k,
+            if ((rc = naiwa_moe_decode_residual(&d.gate, &d.up, &d.down, res_x, slot_ids, w_one, rows, k,
                                                 d.act, out, 1, stream)))
                 return rc;
             if (folded) *folded = true;
-        } else if ((rc = naiwa_moe_decode(&d.gate, &d.up, &d.down, x, NAIWA_BF16, slot_ids, L->w_dev, rows, k,
+        } else if ((rc = naiwa_moe_decode(&d.gate, &d.up, &d.down, x, NAIWA_BF16, slot_ids, w_one, rows, k,
                                           d.act, out, stream))) {
             return rc;
         }
@@ -492,11 +642,7 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         if ((rc = naiwa_moe_decode_ex(&d.gate, &d.up, &d.down, x, NAIWA_BF16, L->slots_dev, L->wsplit_dev, rows, k,
                                       d.act, out, 0, stream)))
             return rc;
-        if (poll)
-            rc = doorbell_poll_wait(L->upload_flag, L->upload_epoch, stream);
-        else
-            rc = naiwa_hip_rc(hipStreamWaitEvent(st, L->staged_done, 0));
-        if (rc) return rc;
+        if ((rc = wait_staged())) return rc;
         if ((rc = naiwa_moe_decode_ex(&d.gate, &d.up, &d.down, x, NAIWA_BF16, L->slots_dev, L->wsplit_dev + n, rows,
                                       k, d.act, out, NAIWA_DECODE_ACCUMULATE, stream)))
             return rc;
@@ -547,12 +693,22 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         if ((rc = naiwa_hip_rc(hipEventRecord(L->ring_fence[pos[i]], st)))) return rc;
         L->ring_fenced[pos[i]] = 1;
     }
-    // every read of this layer's cache slots is before this point on `stream`
+    // the CPU pairs' sum, added last: the device waits for the job's result doorbell,
+    // copies it and adds it to the resident and staged sum (src/moe/decode.rs:371-381)
+    if (cpu) {
+        if ((rc = naiwa_pending_upload(ex, &pend, L->cpu_out, stream))) return rc;
+        const int nx = rows * d.hidden;
+        add_f32_kernel<<<(nx + 255) / 256 < 1024 ? (nx + 255) / 256 : 1024, 256, 0, st>>>(out, L->cpu_out, nx);
+        if ((rc = naiwa_hip_rc(hipGetLastError()))) return rc;
+    }
+    // every read of this layer's cache slots and of its publish page is before this
+    // point on `stream` (the CPU job has finished reading x once its result arrived)
     if ((rc = naiwa_hip_rc(hipEventRecord(L->read_done, st)))) return rc;
     L->read_recorded = true;
 
     naiwa_cache_stats s{};
     s.hits = (uint64_t)step.hits;
+    s.misses = (uint64_t)step.cpu;
     s.staged = (uint64_t)step.staged;
     s.pcie_misses = (uint64_t)nc;
     s.pcie_bytes = (uint64_t)step.pcie_bytes;
@@ -588,10 +744,20 @@ int naiwa_cached_layer_create(const naiwa_cached_layer_desc* d, naiwa_ring* ring
     L->bytes[0] = (size_t)naiwa_projection_bytes(d->gate.dtype, d->inter, d->hidden);
     L->bytes[1] = (size_t)naiwa_projection_bytes(d->up.dtype, d->inter, d->hidden);
     L->bytes[2] = (size_t)naiwa_projection_bytes(d->down.dtype, d->hidden, d->inter);
+    // a positive stride shorter than a projection would make experts overlap in the stacks
+    if (d->host_expert_stride < 0 ||
+        (d->host_expert_stride > 0 &&
+         (size_t)d->host_expert_stride < std::max(L->bytes[0], std::max(L->bytes[1], L->bytes[2])))) {
+        delete L;
+        return NAIWA_E_INVALID;
+    }
     // host stacks: each projection stacked on its own (stride = its bytes), or experts
     // interleaved with a common stride (host_expert_stride)
     for (int p = 0; p < 3; ++p) L->host_stride[p] = d->host_expert_stride > 0 ? (size_t)d->host_expert_stride : L->bytes[p];
     L->expert_bytes = L->bytes[0] + L->bytes[1] + L->bytes[2];
+    L->hx = naiwa_host_experts{d->host_gate, d->host_up, d->host_down,
+                               (int64_t)L->host_stride[0], (int64_t)L->host_stride[1], (int64_t)L->host_stride[2],
+                               d->gate.dtype, d->up.dtype, d->down.dtype, d->num_experts, d->hidden, d->inter};
     {
         const uint8_t* hg = (const uint8_t*)d->host_gate;
         const uint8_t* g = (const uint8_t*)d->gate.base;
@@ -650,6 +816,24 @@ int naiwa_cached_layer_destroy(naiwa_cached_layer* L) {
     if (L->upload_flag) (void)hipFree(L->upload_flag);
     naiwa_cache_destroy(L->cache);
     delete L;
+    return NAIWA_OK;
+}
+
+int naiwa_cached_layer_set_upload_sync(naiwa_cached_layer* L, int mode) {
+    if (!L || (mode != NAIWA_UPLOAD_SYNC_EVENT && mode != NAIWA_UPLOAD_SYNC_POLL)) return NAIWA_E_INVALID;
+    L->upload_sync = mode;
+    return NAIWA_OK;
+}
+
+int naiwa_cached_layer_set_cpu_misses(naiwa_cached_layer* L, int on) {
+    if (!L) return NAIWA_E_INVALID;
+    L->cpu_misses = on != 0;
+    return NAIWA_OK;
+}
+
+int naiwa_cached_layer_upload_timeouts(const naiwa_cached_layer* L, uint32_t* count) {
+    if (!L || !count) return NAIWA_E_INVALID;
+    *count = L->db_host ? naiwa_host_load_acquire_u32(L->db_host + 1) : 0u;
     return NAIWA_OK;
 }
 
@@ -751,6 +935,7 @@ int naiwa_cached_stack_forward(naiwa_cached_layer* const* layers, int n_layers, 
             total->promoted += s.promoted;
             total->pcie_bytes += s.pcie_bytes;
             total->preload_waits += s.preload_waits;
+            total->cpu += s.cpu;
         }
         if (ahead_total && ahead) {
             ahead_total->predicted += a.predicted;

@@ -251,3 +251,7 @@ __device__ __forceinline__ float naiwa_q8_0_pair(const uint32_t* D, const uint32
     const float t0 = __builtin_fmaf(-1152.0f, s0, a0), t1 = __builtin_fmaf(-1152.0f, s1, a1);
     return __builtin_fmaf(d0, t0, d1 * t1);
 }
+
+// The bound of the device-side doorbell waits in wall-clock ticks (doorbell.hip;
+// naiwa_doorbell_set_wait_limit_us sets it).
+uint64_t naiwa_doorbell_wait_limit_ticks();

@@ -153,6 +153,10 @@ __global__ void __launch_bounds__(64) doorbell_poll_signal_kernel(uint32_t* d_fl
 
 } // namespace
 
+// The bound of the device-side doorbell waits, in wall-clock ticks (for other
+// kernels of the library that wait on a doorbell word).
+uint64_t naiwa_doorbell_wait_limit_ticks() { return wait_limit_ticks(); }
+
 extern "C" {
 
 int doorbell_poll_serve(void* d_seq, void* d_ack, uint32_t first, uint32_t count, int64_t stream) {

@@ -401,6 +401,39 @@ int naiwa_cache_stage(naiwa_ring* r, const uint32_t* ids, const float* w, int ro
     return NAIWA_OK;
 }
 
+int naiwa_cache_plan(const naiwa_cache* c, int ring_len, const uint32_t* ids, const float* w, int rows, int k,
+                     float frac, naiwa_step_plan* out) {
+    if (!c || !out || ring_len < 0 || rows < 0 || k <= 0 || (rows > 0 && (!ids || !w))) return NAIWA_E_INVALID;
+    *out = naiwa_step_plan{};
+    const int n = rows * k;
+    for (int i = 0; i < n; ++i)
+        if (ids[i] >= (uint32_t)c->num_experts) return NAIWA_E_BAD_ID;
+    // the split of naiwa_cache_route (published slot or miss) and the choice of
+    // naiwa_cache_stage (streamed_misses over the misses), with no state touched
+    std::vector<uint32_t> mid;
+    std::vector<float> mw;
+    for (int i = 0; i < n; ++i) {
+        if (c->published_slot_of((int)ids[i]) >= 0) {
+            ++out->hits;
+        } else {
+            mid.push_back(ids[i]);
+            mw.push_back(w[i]);
+        }
+    }
+    std::vector<uint32_t> chosen((size_t)std::max(ring_len, 1));
+    int nc = 0;
+    int rc = naiwa_streamed_misses(mid.data(), mw.data(), (int)mid.size(), frac, ring_len, chosen.data(), &nc);
+    if (rc) return rc;
+    out->staged_experts = nc;
+    for (uint32_t e : mid) {
+        if (std::find(chosen.begin(), chosen.begin() + nc, e) != chosen.begin() + nc)
+            ++out->staged;
+        else
+            ++out->cpu;
+    }
+    return NAIWA_OK;
+}
+
 int naiwa_stats_read(naiwa_cache_stats* out, int reset) {
     if (!out) return NAIWA_E_INVALID;
     std::lock_guard<std::mutex> lock(g_stats_mu);

@@ -71,7 +71,20 @@ RESULT_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(C.c_float), C.c_int)
 class CachedStep(C.Structure):
     """naiwa_cached_step (include/naiwa_cached.h)."""
     _fields_ = [("hits", C.c_int), ("staged", C.c_int), ("staged_experts", C.c_int), ("promoted", C.c_int),
-                ("pcie_bytes", C.c_int64), ("preload_waits", C.c_int)]
+                ("pcie_bytes", C.c_int64), ("preload_waits", C.c_int), ("cpu", C.c_int)]
+
+
+class HostExperts(C.Structure):
+    """naiwa_host_experts (include/naiwa_cached.h)."""
+    _fields_ = [("gate", C.c_void_p), ("up", C.c_void_p), ("down", C.c_void_p), ("gate_stride", C.c_int64),
+                ("up_stride", C.c_int64), ("down_stride", C.c_int64), ("gate_dtype", C.c_int),
+                ("up_dtype", C.c_int), ("down_dtype", C.c_int), ("num_experts", C.c_int), ("hidden", C.c_int),
+                ("inter", C.c_int)]
+
+
+class StepPlan(C.Structure):
+    """naiwa_step_plan (include/naiwa_policy.h)."""
+    _fields_ = [("hits", C.c_int), ("staged", C.c_int), ("staged_experts", C.c_int), ("cpu", C.c_int)]
 
 
 class LookaheadStep(C.Structure):
@@ -210,6 +223,10 @@ SIGNATURES: dict[str, tuple] = {
                                                _P(LookaheadStep)]),
     "naiwa_cached_layer_prefetch": (i32, [vp, vp, i32, i32, i64, _P(LookaheadStep)]),
     "naiwa_cached_layer_predicted": (i32, [vp, vp, i32, _P(i32)]),
+    "naiwa_cached_layer_set_upload_sync": (i32, [vp, i32]),
+    "naiwa_cached_layer_set_cpu_misses": (i32, [vp, i32]),
+    "naiwa_cached_layer_upload_timeouts": (i32, [vp, _P(C.c_uint32)]),
+    "naiwa_cpu_moe_decode": (i32, [_P(HostExperts), vp, vp, vp, i32, i32, i32, vp]),
     "naiwa_cached_stack_forward": (i32, [vp, i32, vp, i32, vp, f32, i32, u64, i32, i64, _P(CachedStep),
                                          _P(LookaheadStep)]),
     # include/naiwa_policy.h (host only)
@@ -237,6 +254,7 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_ring_destroy": (i32, [vp]),
     "naiwa_ring_acquire": (i32, [vp, i32, _P(i32)]),
     "naiwa_cache_stage": (i32, [vp, vp, vp, i32, i32, f32, vp, vp, vp, _P(i32)]),
+    "naiwa_cache_plan": (i32, [vp, i32, vp, vp, i32, i32, f32, _P(StepPlan)]),
     "naiwa_stats_read": (i32, [vp, i32]),
     "naiwa_stats_add": (i32, [vp]),
     # include/naiwa_gguf.h

@@ -127,6 +127,16 @@ class ExpertCache:
     def place(self, expert: int, slot: int, last_use: int = 0) -> None:
         check(lib().naiwa_cache_place(self._h, expert, slot, last_use), "place")
 
+    def plan(self, ids, w, ring_len: int, frac: float) -> dict:
+        """naiwa_cache_plan: the split route + stage would make, with no state changed."""
+        from ._lib import StepPlan
+        ids, w = _u32(ids), _f32(w)
+        rows, k = ids.shape
+        out = StepPlan()
+        check(lib().naiwa_cache_plan(self._h, ring_len, _ptr(ids), _ptr(w), rows, k, frac, C.byref(out)),
+              "cache_plan")
+        return {f: getattr(out, f) for f, _ in StepPlan._fields_}
+
 
 class StagingRing:
     """The round-robin staging ring (ring slots are NAIWA_STAGING_RING_FIRST + position)."""
@@ -253,6 +263,20 @@ class CachedLayer:
         check(lib().naiwa_cached_layer_predicted(self._h, _ptr(out), out.size, C.byref(n)), "cached_layer_predicted")
         return [int(v) for v in out[:n.value]]
 
+    def set_upload_sync(self, mode: int) -> None:
+        """UPLOAD_SYNC_EVENT (0) or UPLOAD_SYNC_POLL (1, the default): how staged uploads
+        complete into the expert pass."""
+        check(lib().naiwa_cached_layer_set_upload_sync(self._h, mode), "cached_layer_set_upload_sync")
+
+    def set_cpu_misses(self, on: bool) -> None:
+        """Misses the ring does not take run on the CPU (default), or such a step is refused."""
+        check(lib().naiwa_cached_layer_set_cpu_misses(self._h, 1 if on else 0), "cached_layer_set_cpu_misses")
+
+    def upload_timeouts(self) -> int:
+        n = C.c_uint32()
+        check(lib().naiwa_cached_layer_upload_timeouts(self._h, C.byref(n)), "cached_layer_upload_timeouts")
+        return n.value
+
     def routing(self, rows: int) -> tuple[np.ndarray, np.ndarray]:
         ids = np.empty((rows, self.top_k), dtype=np.uint32)
         w = np.empty((rows, self.top_k), dtype=np.float32)
@@ -357,3 +381,25 @@ def stats_add(**delta: int) -> None:
 
 __all__ = ["ExpertCache", "StagingRing", "CachedLayer", "ExpertProfile", "STAGING_RING_FIRST", "staging_ring_slots",
            "top_k_ids", "union_by_votes", "streamed_misses", "stats", "stats_add", "hit_rate", "write_profile"]
+
+
+UPLOAD_SYNC_EVENT = 0
+UPLOAD_SYNC_POLL = 1
+
+
+def cpu_moe_decode(gate, up, down, dtypes, hidden: int, inter: int, xs, ids, w, act: int = 0) -> np.ndarray:
+    """naiwa_cpu_moe_decode: the CPU expert path (fused_moe_decode contract) over host
+    stacks gate/up [E, inter, row bytes] and down [E, hidden, row bytes]; xs f32 [rows,
+    hidden]; ids/w [rows, width].  Returns f32 [rows, hidden]."""
+    from ._lib import HostExperts
+    g, u, d = (np.ascontiguousarray(a, dtype=np.uint8) for a in (gate, up, down))
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    ids, w = _u32(ids), _f32(w)
+    rows, width = ids.shape
+    ex = HostExperts(g.ctypes.data, u.ctypes.data, d.ctypes.data, 0, 0, 0, dtypes[0], dtypes[1], dtypes[2],
+                     g.shape[0], hidden, inter)
+    out = np.empty((rows, hidden), dtype=np.float32)
+    check(lib().naiwa_cpu_moe_decode(C.byref(ex), _ptr(xs), _ptr(ids), _ptr(w), rows, width, act, _ptr(out)),
+          "cpu_moe_decode")
+    return out
+

@@ -296,8 +296,9 @@ class PageableStacks:
         return self.arrays[proj]
 
 
+@pytest.mark.parametrize("sync", ["event", "poll"])
 @pytest.mark.parametrize("host_mem", ["pinned", "pageable", "contiguous"])
-def test_cached_layer_alternating_streams(gpu, host_mem):
+def test_cached_layer_alternating_streams(gpu, host_mem, sync):
     """Steps alternate between two compute streams with no host synchronisation of
     their own: a staged upload into a ring slot must wait for every earlier read of
     that slot -- the expert kernel's and the promotion copy's -- through the slot's
@@ -323,6 +324,7 @@ def test_cached_layer_alternating_streams(gpu, host_mem):
     bias_d = nm.DeviceBuffer.from_array(bias)
     layer = nm.policy.CachedLayer(router, banks, stacks, E, k, usable, ring, copy.handle,
                                   mode=O.ROUTE_SOFTMAX_TOPK_RENORM, router_bias=bias_d)
+    layer.set_upload_sync(nm.policy.UPLOAD_SYNC_POLL if sync == "poll" else nm.policy.UPLOAD_SYNC_EVENT)
     host = (g, u, d, r, bias, dt, I)
     steps = 10
     xs = [S.activations_bf16(1810 + i, rows, H) for i in range(steps)]
@@ -330,7 +332,7 @@ def test_cached_layer_alternating_streams(gpu, host_mem):
     outs = [nm.DeviceBuffer(rows * H * 4) for _ in range(steps)]
     promoted = 0
     for i in range(steps):
-        print(f"[alternating streams {host_mem} step {i}]", flush=True)
+        print(f"[alternating streams {host_mem} {sync} step {i}]", flush=True)
         info = layer.forward(xds[i], rows, outs[i], pcie_frac=1.0, promote_cap=1, min_hits=1,
                              stream=streams[i % 2].handle)
         promoted += info["promoted"]
@@ -342,6 +344,7 @@ def test_cached_layer_alternating_streams(gpu, host_mem):
         err = S.max_rel_err(outs[i].download(np.float32).reshape(rows, H), want)
         assert err < TOL, (i, err)
     assert promoted > 0
+    assert layer.upload_timeouts() == 0
     check_resident_bytes(layer, banks, stacks)
 
 
@@ -381,16 +384,37 @@ class PromotingSlotModel(SlotModel):
         return done
 
 
-def test_cached_qwen3_shape_zipf(gpu):
+def streamed(flat_ids, flat_w, resident, frac, cap):
+    """The reference's streamed_misses (src/moe/cached_layer.rs:381-398), restated: the
+    missed ids in order of first appearance with their weights summed in row-major
+    order in f32, take = min(ceil(frac * distinct), cap), ranked by (sum desc, id asc)."""
+    order, sums = [], {}
+    for e, w in zip(flat_ids, flat_w):
+        if resident(e):
+            continue
+        if e not in sums:
+            order.append(e)
+            sums[e] = np.float32(0.0)
+        sums[e] = np.float32(sums[e] + np.float32(w))
+    if not frac > 0:
+        return []
+    take = min(int(np.ceil(np.float32(frac) * np.float32(len(order)))), cap)
+    return sorted(order, key=lambda e: (-float(sums[e]), e))[:take]
+
+
+@pytest.mark.parametrize("sync,frac", [("event", 1.0), ("poll", 1.0), ("event", 0.5), ("event", 0.0)])
+def test_cached_qwen3_shape_zipf(gpu, sync, frac):
     """The 25 %-cache workload at its real shape: two chained Qwen3-30B-A3B-shaped
     layers (H 2048, 128 experts, top-8, I 768, Q4_K), 32 cached experts + the
     16-slot staging ring per layer, Zipf(1.1) routing bias, the caches seeded with
-    each layer's 32 most popular experts, 12 decode steps with staging and one
-    promotion per layer per step (min_hits 2).  Every step: top-k ids bit-exact
-    with the oracle on the GPU's own x_l, hit/staged counts and the slot table
-    equal to an independent replay of the reference's policy, and the layer's
-    output within 1e-2 of the oracle.  At the end every resident expert's three
-    projections hold its bytes."""
+    each layer's 32 most popular experts, 12 decode steps with staging of the
+    pcie_frac share of the misses and one promotion per layer per step (min_hits 2);
+    the other misses run on the CPU (pcie_frac 0: all of them, the reference's
+    default).  Staged uploads complete through an event or the polled flag.  Every
+    step: top-k ids bit-exact with the oracle on the GPU's own x_l, hit / staged /
+    CPU counts and the slot table equal to an independent replay of the reference's
+    policy, and the layer's output within 1e-2 of the oracle.  At the end every
+    resident expert's three projections hold its bytes."""
     nm = gpu
     L, E, H, I, k, usable, rows, steps, min_hits = 2, 128, 2048, 768, 8, 32, 1, 12, 2
     dt = (O.Q4_K,) * 3
@@ -414,9 +438,12 @@ def test_cached_qwen3_shape_zipf(gpu):
         banks = nm.LayerBanks(usable + ring.length, H, I, dt, contiguous=True)
         layer = nm.policy.CachedLayer(router, banks, stacks, E, k, usable, ring, copy.handle,
                                       mode=O.ROUTE_SOFTMAX_TOPK_RENORM, router_bias=bias_d)
-        # the 32 most popular experts (largest bias) first
-        popular = [int(e) for e in np.argsort(-bias, kind="stable")[:usable]]
-        assert layer.seed(popular) == usable
+        layer.set_upload_sync(nm.policy.UPLOAD_SYNC_POLL if sync == "poll" else nm.policy.UPLOAD_SYNC_EVENT)
+        # the 32 most popular experts (largest bias) first; at pcie_frac 0.5 only 12, so
+        # that steps miss several experts and split them between the ring and the CPU
+        seeded = usable if frac != 0.5 else 12
+        popular = [int(e) for e in np.argsort(-bias, kind="stable")[:seeded]]
+        assert layer.seed(popular) == seeded
         model = PromotingSlotModel(usable, E)
         for e in popular:
             model.admit(e)
@@ -429,22 +456,27 @@ def test_cached_qwen3_shape_zipf(gpu):
     x = S.activations_bf16(2200, rows, H)
     xd = nm.DeviceBuffer.from_array(x)
     out = nm.DeviceBuffer(rows * H * 4)
-    tot = {"staged": 0, "promoted": 0}
+    tot = {"staged": 0, "promoted": 0, "cpu": 0}
+    both_in_one_step = False
     for step in range(steps):
         for l, (layer, banks, stacks) in enumerate(layers):
-            print(f"[cached qwen3 step {step} layer {l}]", flush=True)
-            info = layer.forward(xd, rows, out, pcie_frac=1.0, promote_cap=1, min_hits=min_hits,
+            print(f"[cached qwen3 {sync} frac={frac} step {step} layer {l}]", flush=True)
+            info = layer.forward(xd, rows, out, pcie_frac=frac, promote_cap=1, min_hits=min_hits,
                                  stream=stream.handle)
             stream.sync()
             ids, w = layer.routing(rows)
             want_ids, want_w, want = oracle_step(hosts[l], x, E, k, H)
             assert np.array_equal(ids, want_ids), (step, l, ids, want_ids)
             assert np.allclose(w, want_w, rtol=1e-5, atol=1e-7)
-            flat = ids.reshape(-1).tolist()
+            flat, flat_w = ids.reshape(-1).tolist(), w.reshape(-1).tolist()
             model = models[l]
-            staged = sorted(set(e for e in flat if not model.resident(e)))
+            chosen = streamed(flat, flat_w, model.resident, frac, ring.length)
+            staged = sorted(chosen)
+            n_staged = sum(1 for e in flat if e in chosen and not model.resident(e))
+            n_cpu = sum(1 for e in flat if not model.resident(e) and e not in chosen)
             hits = model.route(flat)
             assert info["hits"] == hits and info["staged_experts"] == len(staged), (step, l, info)
+            assert info["staged"] == n_staged and info["cpu"] == n_cpu, (step, l, info)
             promoted = model.promote(staged, 1, min_hits)
             assert info["promoted"] == len(promoted), (step, l, info, promoted)
             table = layer.cache.slot_table()
@@ -460,13 +492,19 @@ def test_cached_qwen3_shape_zipf(gpu):
             assert err < TOL, (step, l, err)
             tot["staged"] += info["staged_experts"]
             tot["promoted"] += info["promoted"]
+            tot["cpu"] += info["cpu"]
+            both_in_one_step |= info["staged_experts"] > 0 and info["cpu"] > 0
             x = O.to_bf16(O.from_bf16(x).astype(np.float32) + y)
             xd = nm.DeviceBuffer.from_array(x)
         # the next step starts from a fresh token
         x = S.activations_bf16(2201 + step, rows, H)
         xd = nm.DeviceBuffer.from_array(x)
-    assert tot["staged"] > 0 and tot["promoted"] > 0, tot
+    assert (tot["staged"] > 0 and tot["promoted"] > 0) == (frac > 0), tot
+    assert (tot["cpu"] > 0) == (frac < 1), tot
+    if frac == 0.5:
+        assert both_in_one_step, "no step split its misses between the ring and the CPU"
     for layer, banks, stacks in layers:
+        assert layer.upload_timeouts() == 0
         check_resident_bytes(layer, banks, stacks)
 
 
@@ -494,7 +532,7 @@ def test_cached_stack_forward_matches_the_layer_calls(gpu, swaps):
                 info, ahead = nm.policy.CachedLayer.stack_forward(layers, x, rows, y, lookahead_swaps=swaps,
                                                                   stream=stream.handle)
             else:
-                info = {"hits": 0, "staged": 0, "staged_experts": 0, "promoted": 0, "pcie_bytes": 0,
+                info = {"hits": 0, "staged": 0, "staged_experts": 0, "promoted": 0, "pcie_bytes": 0, "cpu": 0,
                         "preload_waits": 0}
                 ahead = {"predicted": 0, "resident": 0, "loads": 0, "swaps": 0, "pcie_bytes": 0}
                 for l, layer in enumerate(layers):
@@ -518,3 +556,76 @@ def test_cached_stack_forward_matches_the_layer_calls(gpu, swaps):
     assert sa == sb
     assert np.array_equal(xa, xb)
     assert any(r[0]["staged"] for r in ra)   # the run stages misses
+
+
+def _policy_state(layer, ring):
+    c = layer.cache
+    return (c.tick, c.hit_counts().tolist(), [c.slot_state(s) for s in range(c.slots)], ring.acquire(0))
+
+
+def test_cpu_misses_off_refuses_the_step_before_any_state_changes(gpu):
+    """With the CPU path switched off, a step whose misses the ring does not take
+    (pcie_frac 0) is refused with NAIWA_E_UNSUPPORTED, and the tick, the hit counts,
+    every slot's state and the ring cursor are as before.  Switched on again, the same
+    step runs its misses on the CPU and matches the oracle."""
+    nm = gpu
+    E, H, I, k, usable, rows = 16, 256, 256, 4, 4, 2
+    copy, stream = nm.Stream(), nm.Stream()
+    ring = nm.policy.StagingRing()
+    layer, banks, stacks, host = make_layer(nm, 2600, E, H, I, k, usable, ring, copy)
+    for e in range(usable):
+        assert layer.fill(e) == e
+    x = S.activations_bf16(2601, rows, H)
+    xd = nm.DeviceBuffer.from_array(x)
+    out = nm.DeviceBuffer(rows * H * 4)
+    layer.set_cpu_misses(False)
+    before = _policy_state(layer, ring)
+    with pytest.raises(nm.NaiwaError) as e:
+        layer.forward(xd, rows, out, pcie_frac=0.0, stream=stream.handle)
+    assert e.value.rc == nm.E_UNSUPPORTED
+    assert _policy_state(layer, ring) == before
+    layer.set_cpu_misses(True)
+    info = layer.forward(xd, rows, out, pcie_frac=0.0, stream=stream.handle)
+    stream.sync()
+    assert info["cpu"] > 0 and info["staged_experts"] == 0 and info["hits"] + info["cpu"] == rows * k
+    _, _, want = oracle_step(host, x, E, k, H)
+    assert S.max_rel_err(out.download(np.float32).reshape(rows, H), want) < TOL
+
+
+def test_poll_upload_wait_that_runs_out_is_reported_by_the_next_step(gpu):
+    """Poll mode with the device wait bound forced to 1 us from the host and the copy
+    stream kept busy, so the staged-upload wait of a step gives up: the wait counts it
+    in the layer's doorbell, and the layer's next forward returns NAIWA_E_TIMEOUT before
+    it changes any policy state.  With the bound restored the layer goes on and its
+    outputs match the oracle again."""
+    nm = gpu
+    L = nm.lib()
+    E, H, I, k, usable, rows = 16, 256, 256, 4, 2, 1
+    copy, stream = nm.Stream(), nm.Stream()
+    ring = nm.policy.StagingRing()
+    layer, banks, stacks, host = make_layer(nm, 2700, E, H, I, k, usable, ring, copy)
+    layer.set_upload_sync(nm.policy.UPLOAD_SYNC_POLL)
+    x = S.activations_bf16(2701, rows, H)
+    xd = nm.DeviceBuffer.from_array(x)
+    out = nm.DeviceBuffer(rows * H * 4)
+    big_src, big_dst = nm.DeviceBuffer(256 << 20), nm.DeviceBuffer(256 << 20)
+    assert L.naiwa_memcpy_d2d(big_dst.ptr, big_src.ptr, 256 << 20, copy.handle) == 0   # the copy stream is busy
+    L.naiwa_doorbell_set_wait_limit_us(1)
+    try:
+        info = layer.forward(xd, rows, out, pcie_frac=1.0, stream=stream.handle)   # nothing cached: all staged
+        stream.sync()
+    finally:
+        L.naiwa_doorbell_set_wait_limit_us(0)
+    copy.sync()
+    assert info["staged_experts"] > 0
+    assert layer.upload_timeouts() == 1
+    before = _policy_state(layer, ring)
+    with pytest.raises(nm.NaiwaError) as e:
+        layer.forward(xd, rows, out, pcie_frac=1.0, stream=stream.handle)
+    assert e.value.rc == nm.E_TIMEOUT
+    assert _policy_state(layer, ring) == before
+    info = layer.forward(xd, rows, out, pcie_frac=1.0, stream=stream.handle)
+    stream.sync()
+    _, _, want = oracle_step(host, x, E, k, H)
+    assert S.max_rel_err(out.download(np.float32).reshape(rows, H), want) < TOL
+    assert layer.upload_timeouts() == 1

@@ -150,3 +150,86 @@ def test_stale_seq_is_not_accepted(gpu):
         L.naiwa_doorbell_set_wait_limit_us(0)
     assert not dst.download(np.float32).any()
     m.free()
+
+
+# ---- the persistent-wave doorbell (doorbell_poll_serve / _wait / _signal) -----------------
+
+def _timeouts(L):
+    n = C.c_uint32(0)
+    assert L.naiwa_doorbell_timeouts(C.byref(n)) == 0
+    return n.value
+
+
+def test_poll_serve_answers_every_host_ring(gpu):
+    """One wave serves 200 host rings in a row: the host raises seq to i, the wave
+    release-stores i to ack, and the host sees it before ringing again -- the
+    round trip the reference's harness times with a stream sync per ring
+    (docs/worklogs/m0.md:43).  No wait runs out."""
+    nm = gpu
+    L = nm.lib()
+    m = Mapped(nm, 256)              # seq at 0, ack at 128 (own cache lines)
+    s = nm.Stream()
+    before = _timeouts(L)
+    L.naiwa_doorbell_set_wait_limit_us(2_000_000)
+    try:
+        assert L.doorbell_poll_serve(m.dev, m.dev + 128, 1, 200, s.handle) == 0
+        for i in range(1, 201):
+            L.naiwa_host_store_release_u32(m.host, i)
+            assert L.naiwa_host_wait_ge(m.host + 128, i, 2_000_000, 0) == 0, i
+        s.sync()
+    finally:
+        L.naiwa_doorbell_set_wait_limit_us(0)
+    assert L.naiwa_host_load_acquire_u32(m.host + 128) == 200
+    assert _timeouts(L) == before
+    m.free()
+
+
+def test_poll_signal_then_wait_orders_two_streams(gpu):
+    """doorbell_poll_signal on stream A after A's work, doorbell_poll_wait on stream B
+    before B's reader: B's copy sees what A wrote last, every epoch, although A starts
+    with a long copy and the host never synchronises between them."""
+    nm = gpu
+    L = nm.lib()
+    a, b = nm.Stream(), nm.Stream()
+    flag = nm.DeviceBuffer(256)
+    big_src, big_dst = nm.DeviceBuffer(64 << 20), nm.DeviceBuffer(64 << 20)
+    marker, seen = nm.DeviceBuffer(256), nm.DeviceBuffer(256 * 8)
+    assert L.naiwa_memset(flag.ptr, 0, 256, 0) == 0
+    assert L.naiwa_memset(seen.ptr, 0, 256 * 8, 0) == 0
+    nm.synchronize()
+    before = _timeouts(L)
+    for epoch in range(1, 9):
+        assert L.naiwa_memcpy_d2d(big_dst.ptr, big_src.ptr, 64 << 20, a.handle) == 0   # A is busy
+        assert L.naiwa_memset(marker.ptr, 0x10 + epoch, 4, a.handle) == 0             # A's last write
+        assert L.doorbell_poll_signal(flag.ptr, epoch, a.handle) == 0
+        assert L.doorbell_poll_wait(flag.ptr, epoch, b.handle) == 0
+        assert L.naiwa_memcpy_d2d(seen.ptr + 256 * (epoch - 1), marker.ptr, 4, b.handle) == 0
+    a.sync()
+    b.sync()
+    got = seen.download(np.uint8).reshape(8, 256)[:, :4]
+    for epoch in range(1, 9):
+        assert (got[epoch - 1] == 0x10 + epoch).all(), (epoch, got[epoch - 1])
+    assert _timeouts(L) == before
+
+
+def test_poll_wait_that_is_never_signalled_gives_up_on_its_bound(gpu):
+    """Must-fail arm: a flag nobody raises ends doorbell_poll_wait by its wall-clock
+    bound (here 2 ms), counts one timeout, and the stream goes on.  The persistent
+    server given a ring that never comes does the same."""
+    nm = gpu
+    L = nm.lib()
+    flag = nm.DeviceBuffer(256)
+    assert L.naiwa_memset(flag.ptr, 0, 256, 0) == 0
+    m = Mapped(nm, 256)
+    nm.synchronize()
+    before = _timeouts(L)
+    L.naiwa_doorbell_set_wait_limit_us(2_000)
+    try:
+        assert L.doorbell_poll_wait(flag.ptr, 1, 0) == 0
+        assert L.doorbell_poll_serve(m.dev, m.dev + 128, 1, 1, 0) == 0
+        nm.synchronize()
+    finally:
+        L.naiwa_doorbell_set_wait_limit_us(0)
+    assert _timeouts(L) == before + 2
+    assert L.naiwa_host_load_acquire_u32(m.host + 128) == 0   # no ack for a ring never rung
+    m.free()

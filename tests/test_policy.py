@@ -188,3 +188,52 @@ def test_stats_accumulate_and_reset():
     s = P.stats(reset=True)
     assert s["hits"] == 4 and s["staged"] == 2 and s["pcie_bytes"] == 100 and s["misses"] == 0
     assert P.stats()["hits"] == 0
+
+
+# ---- the step plan: route + stage without their side effects ------------------------------
+
+def _state(c, ring):
+    slots = [c.slot_state(s) for s in range(c.slots)]
+    return c.tick, c.hit_counts().tolist(), slots, ring.acquire(0)
+
+
+@pytest.mark.parametrize("frac", [0.0, 0.5, 1.0])
+def test_plan_predicts_route_and_stage_and_changes_nothing(frac):
+    """naiwa_cache_plan reports the hits, staged pairs, staged experts and CPU pairs that
+    naiwa_cache_route followed by naiwa_cache_stage then produce, over a run of random
+    Zipf-like steps, and leaves the tick, the hit counts, every slot's state and the ring
+    cursor exactly as they were (the partial-cache step refuses a step it cannot finish
+    with it, before anything moves)."""
+    rng = np.random.default_rng(7)
+    E, slots, k, rows = 64, 12, 6, 3
+    c = P.ExpertCache(E, slots)
+    for s in range(slots):
+        c.place(int(s * 5 % E), s)
+    ring = P.StagingRing(8)
+    pop = 1.0 / np.arange(1, E + 1) ** 1.1
+    pop /= pop.sum()
+    for step in range(30):
+        ids = np.stack([rng.choice(E, size=k, replace=False, p=pop) for _ in range(rows)]).astype(np.uint32)
+        w = rng.random((rows, k)).astype(np.float32)
+        w[0, 0] = 0.0  # a zero weight still counts as a pair of its kind
+        before = _state(c, ring)
+        plan = c.plan(ids, w, ring.length, frac)
+        assert _state(c, ring) == before, step
+        got = c.route(ids)
+        slots_io = np.array(got, dtype=np.int32).reshape(rows, k)
+        staged = ring.stage(ids, w, slots_io, frac)
+        hits = int((np.array(got) >= 0).sum())
+        in_ring = int((slots_io >= P.STAGING_RING_FIRST).sum())
+        cpu = int((slots_io < 0).sum())
+        assert plan == {"hits": hits, "staged": in_ring, "staged_experts": len(staged), "cpu": cpu}, (step, plan)
+        assert hits + in_ring + cpu == rows * k
+
+
+def test_plan_rejects_bad_ids_without_changing_state():
+    c = P.ExpertCache(8, 2)
+    ring = P.StagingRing(4)
+    before = _state(c, ring)
+    with pytest.raises(NaiwaError) as e:
+        c.plan(np.array([[1, 9]], dtype=np.uint32), np.ones((1, 2), np.float32), ring.length, 1.0)
+    assert e.value.rc == E_BAD_ID
+    assert _state(c, ring) == before
