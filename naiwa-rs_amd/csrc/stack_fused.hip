@@ -1533,13 +1533,76 @@ __global__ void roll_status(int* st) {
     }
 }
 
-struct FusedCache {
-    std::mutex mu;
-    LayerDev* dev_layers = nullptr;
-    size_t cap = 0;
-    std::vector<LayerDev> last;
+// Per device: the layer-descriptor sets uploaded so far, and the completion of the
+// last fused launch.  A set never changes once uploaded (a new descriptor list gets
+// its own set, copied on the launch stream), so a launch still queued on another
+// stream keeps reading what it was given; the least recently used of kMaxSets sets
+// is freed only after its last launch has completed.  Fused launches share the
+// device's exchange scratch and each occupies every CU, so each one waits for the
+// previous one, whatever stream either came from.
+struct DescSet {
+    std::vector<LayerDev> desc;
+    LayerDev* dev = nullptr;    // device copy
+    LayerDev* host = nullptr;   // pinned source of the upload (kept with the set)
+    hipEvent_t ready = nullptr; // after the upload
+    hipEvent_t used = nullptr;  // after the last launch that read it
+    uint64_t stamp = 0;
 };
-FusedCache g_fused;
+struct FusedDev {
+    std::mutex mu;
+    std::vector<DescSet> sets;
+    uint64_t clock = 0;
+    hipEvent_t done = nullptr;  // after the last fused launch
+    bool have_done = false;
+};
+constexpr size_t kMaxSets = 8;
+FusedDev g_fused[64]; // per device (the launch checks dev < 64)
+
+void free_set(DescSet& d) {
+    if (d.used) (void)hipEventSynchronize(d.used);
+    if (d.dev) (void)hipFree(d.dev);
+    if (d.host) (void)hipHostFree(d.host);
+    for (hipEvent_t ev : {d.ready, d.used})
+        if (ev) (void)hipEventDestroy(ev);
+    d = DescSet{};
+}
+
+// The set holding `desc` on this device (uploaded on `st` if new), ready on `st`.
+int desc_set(FusedDev& f, const std::vector<LayerDev>& desc, hipStream_t st, DescSet** out) {
+    const size_t bytes = desc.size() * sizeof(LayerDev);
+    for (DescSet& d : f.sets)
+        if (d.desc.size() == desc.size() && memcmp(d.desc.data(), desc.data(), bytes) == 0) {
+            d.stamp = ++f.clock;
+            *out = &d;
+            return naiwa_hip_rc(hipStreamWaitEvent(st, d.ready, 0));
+        }
+    if (f.sets.size() >= kMaxSets) {
+        auto lru = std::min_element(f.sets.begin(), f.sets.end(),
+                                    [](const DescSet& a, const DescSet& b) { return a.stamp < b.stamp; });
+        free_set(*lru);
+        f.sets.erase(lru);
+    }
+    DescSet d;
+    d.desc = desc;
+    int rc = 0;
+    if ((rc = naiwa_hip_rc(hipMalloc(&d.dev, bytes))) || (rc = naiwa_hip_rc(hipHostMalloc(&d.host, bytes, 0))) ||
+        (rc = naiwa_hip_rc(hipEventCreateWithFlags(&d.ready, hipEventDisableTiming))) ||
+        (rc = naiwa_hip_rc(hipEventCreateWithFlags(&d.used, hipEventDisableTiming)))) {
+        free_set(d);
+        return rc;
+    }
+    memcpy(d.host, desc.data(), bytes);
+    if ((rc = naiwa_hip_rc(hipMemcpyAsync(d.dev, d.host, bytes, hipMemcpyHostToDevice, st))) ||
+        (rc = naiwa_hip_rc(hipEventRecord(d.ready, st)))) {
+        (void)hipStreamSynchronize(st);
+        free_set(d);
+        return rc;
+    }
+    d.stamp = ++f.clock;
+    f.sets.push_back(std::move(d));
+    *out = &f.sets.back();
+    return NAIWA_OK;
+}
 
 template <int DG, int DD, int MR>
 int launch(const Params& prm, int blocks, size_t lds, hipStream_t st) {
@@ -1754,6 +1817,13 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     bool sync_fresh = false;
     uint8_t* sync = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK + 1, 4096, &rc, &sync_fresh);
     if (!sync) return rc;
+    // this launch's work on `st` (clearing the exchange words included) follows the previous
+    // fused launch on this device, whatever its stream; the lock is held until this
+    // launch's events are recorded
+    FusedDev& fdev = g_fused[dev];
+    std::lock_guard<std::mutex> flock(fdev.mu);
+    if (!fdev.done && (rc = naiwa_hip_rc(hipEventCreateWithFlags(&fdev.done, hipEventDisableTiming)))) return rc;
+    if (fdev.have_done && (rc = naiwa_hip_rc(hipStreamWaitEvent(st, fdev.done, 0)))) return rc;
     uint32_t seq = 0;
     {
         std::lock_guard<std::mutex> lock(g_seq_mu);
@@ -1778,29 +1848,9 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
                            (const uint8_t*)L.down.base, L.gate.slot_stride, L.up.slot_stride,
                            L.down.slot_stride, L.slot_of_expert, L.gate.slots, 0};
     }
-    LayerDev* dev_layers = nullptr;
-    {
-        std::lock_guard<std::mutex> lock(g_fused.mu);
-        const size_t bytes = desc.size() * sizeof(LayerDev);
-        if (g_fused.cap < bytes) {
-            if (g_fused.dev_layers) {
-                hipError_t e = hipDeviceSynchronize();
-                if (e != hipSuccess) return (int)e;
-                (void)hipFree(g_fused.dev_layers);
-            }
-            g_fused.dev_layers = nullptr;
-            g_fused.cap = 0;
-            g_fused.last.clear();
-            if (hipMalloc(&g_fused.dev_layers, bytes) != hipSuccess) return NAIWA_E_NOMEM;
-            g_fused.cap = bytes;
-        }
-        if (g_fused.last.size() != desc.size() || memcmp(g_fused.last.data(), desc.data(), bytes) != 0) {
-            hipError_t e = hipMemcpy(g_fused.dev_layers, desc.data(), bytes, hipMemcpyHostToDevice);
-            if (e != hipSuccess) return (int)e;
-            g_fused.last = desc;
-        }
-        dev_layers = g_fused.dev_layers;
-    }
+    DescSet* set = nullptr;
+    if ((rc = desc_set(fdev, desc, st, &set))) return rc;
+    LayerDev* dev_layers = set->dev;
 
     Params prm{};
     prm.layers = dev_layers;
@@ -1837,5 +1887,9 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     if (sync_fresh) zero_u32<<<1, 64, 0, st>>>((unsigned int*)(sync + kStatusOff), 64);
     roll_status<<<1, 64, 0, st>>>((int*)(sync + kStatusOff));
     const LaunchOp go{&prm, blocks, lds, st};
-    return rows == 1 ? with_kernel<1>(fg, fd, go) : with_kernel<kMaxRows>(fg, fd, go);
+    rc = rows == 1 ? with_kernel<1>(fg, fd, go) : with_kernel<kMaxRows>(fg, fd, go);
+    if (rc) return rc;
+    if ((rc = naiwa_hip_rc(hipEventRecord(fdev.done, st)))) return rc;
+    fdev.have_done = true;
+    return naiwa_hip_rc(hipEventRecord(set->used, st));
 }

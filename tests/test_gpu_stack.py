@@ -65,6 +65,13 @@ def run_and_check(nm, layers, host, x, rows, H, E, k, mode, fused, label):
     ids = ids_d.download(np.uint32).reshape(L, rows, k)
     w = w_d.download(np.float32).reshape(L, rows, k)
     ys = y_d.download(np.float32).reshape(L, rows, H)
+    errs = check_chain(host, x, ids, w, ys, xd.download(np.uint16).reshape(rows, H), rows, H, E, k, mode)
+    return errs, ids
+
+
+def check_chain(host, x, ids, w, ys, x_final, rows, H, E, k, mode):
+    """Teacher-forced check of one launch's outputs (see run_and_check)."""
+    L = len(host)
     x_l = x.copy()
     errs = []
     for l in range(L):
@@ -77,8 +84,8 @@ def run_and_check(nm, layers, host, x, rows, H, E, k, mode, fused, label):
         assert err < TOL, (l, err)
         x_l = O.to_bf16(O.from_bf16(x_l).astype(np.float32) + ys[l])
     # the kernel's stored x is the chain of its own y outputs, bit for bit
-    assert np.array_equal(xd.download(np.uint16).reshape(rows, H), x_l)
-    return errs, ids
+    assert np.array_equal(x_final, x_l)
+    return errs
 
 
 @pytest.mark.parametrize("fused", [True, False])
@@ -204,3 +211,36 @@ def test_layered_residual_in_the_combine_is_bit_identical(gpu, rows, E, k, dt):
         outs.append((ids_d.download(np.uint32), xd.download(np.uint16)))
     assert np.array_equal(outs[0][0], outs[1][0])
     assert np.array_equal(outs[0][1], outs[1][1])
+
+
+def test_fused_launches_on_two_streams_stay_ordered(gpu):
+    """Two different two-layer Qwen3-shaped stacks launched alternately on two streams,
+    eight launches with no host synchronisation between them: each launch uploads or
+    reuses its own descriptor set on its stream and waits for the previous fused launch
+    (they share the exchange words), so every launch's routing and outputs match the
+    oracle layer by layer and no wait of the kernel runs out."""
+    nm = gpu
+    rows, L, H, E, k, I = 1, 2, 2048, 128, 8, 768
+    dt = (O.Q4_K,) * 3
+    stacks = [build_stack(nm, L, H, E, I, dt, 1400), build_stack(nm, L, H, E, I, dt, 1410)]
+    streams = [nm.Stream(), nm.Stream()]
+    mode = O.ROUTE_SOFTMAX_TOPK_RENORM
+    runs = []
+    for i in range(4):
+        for j, (layers, host, keep) in enumerate(stacks):
+            x = S.activations_bf16(1420 + 2 * i + j, rows, H)
+            bufs = (nm.DeviceBuffer.from_array(x), nm.DeviceBuffer(L * rows * k * 4),
+                    nm.DeviceBuffer(L * rows * k * 4), nm.DeviceBuffer(L * rows * H * 4))
+            print(f"[two streams launch {i} stack {j}]", flush=True)
+            nm.stack_decode(layers, bufs[0], rows, H, E, k, mode=mode, ids_out=bufs[1], w_out=bufs[2], fused=True,
+                            y_out=bufs[3], stream=streams[j].handle)
+            runs.append((j, x, bufs))
+    for st in streams:
+        st.sync()
+    assert nm.stack_status() == (0, 0)
+    for j, x, (xd, ids_d, w_d, y_d) in runs:
+        host = stacks[j][1]
+        check_chain(host, x, ids_d.download(np.uint32).reshape(L, rows, k), w_d.download(np.float32).reshape(L, rows, k),
+                    y_d.download(np.float32).reshape(L, rows, H), xd.download(np.uint16).reshape(rows, H), rows, H,
+                    E, k, mode)
+
