@@ -197,10 +197,22 @@ int naiwa_moe_decode_ex(const naiwa_bank* gate, const naiwa_bank* up, const naiw
  * the scratch (segments, permutation, h) in a fixed device array of
  * NAIWA_DECODE_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends,
  * instead of the library's grow-only buffer.  No hipMalloc, hipFree or
- * allocating routine is called; nothing is cleared with a memset.  A call needs
- * 256 + 2 align256(4 n) + align256(4 (n + 1)) + 4 n I bytes (n = rows *
- * width pairs, I the intermediate size): NAIWA_E_TOO_LARGE when that exceeds
- * the array (8 MiB holds n <= 146 pairs at I = 14336, n <= 2719 at I = 768).
+ * allocating routine is called; nothing is cleared with a memset.  A call of
+ * n = rows * width pairs (H the hidden size, I the intermediate size, a(v) = v
+ * rounded up to a multiple of 256) needs
+ *   S = 256 + 2 a(4 n) + a(4 (n + 1)) + T  bytes, where
+ *   T = a(max(n D, a(2 rows H) + 2 n I)) + ceil(I / 2048) 4 n H
+ *       when n <= 512 and width <= 16 (h staged once in the down format, D =
+ *       its bytes per pair: 2 I + I / 4 for Q4_K, 2 I + I / 8 for Q8_0,
+ *       rounded up to a multiple of 16; plus the f32 dots of each 2048-wide
+ *       K part of down),
+ *   T = 4 n I otherwise (h as f32),
+ * which naiwa_moe_decode_scratch_bytes returns; the entry point returns
+ * NAIWA_E_TOO_LARGE, before any device call, when S exceeds the array.  The
+ * 8 MiB array holds 56 pairs (rows <= 28 at top-2) at H 4096, I 14336, Q4_K;
+ * 2712 pairs (rows <= 339 at top-8) at H 2048, I 768.  S is not monotone in n:
+ * the staged path's K-part dots cost more per pair than f32 h, so at H 5120,
+ * I 1536, top-6, rows 1-55 and 86-227 fit and rows 56-85 do not.
  * Every call on one GPU uses that GPU's one array: calls that overlap
  * on the device (other streams, other host threads) race and must be ordered
  * by the caller. */
@@ -208,6 +220,12 @@ int naiwa_moe_decode_ex(const naiwa_bank* gate, const naiwa_bank* up, const naiw
 int naiwa_moe_decode_noalloc(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down,
                              const void* x, int x_dtype, const uint32_t* slot_ids, const float* w,
                              int rows, int width, int act, float* out, int flags, int64_t stream);
+/* No counterpart in the reference.  The scratch bytes S (above) that a decode
+ * call of rows x width pairs needs at hidden size H, intermediate size I and
+ * down format down_dtype; the no-alloc entry point accepts the call when S <=
+ * NAIWA_DECODE_NOALLOC_SCRATCH_BYTES.  0 for an empty call, -1 for invalid
+ * sizes.  No device call. */
+int64_t naiwa_moe_decode_scratch_bytes(int rows, int width, int H, int I, int down_dtype);
 
 /* Router: logits = W . x with the chunked fixed-point accumulation (chunks of 8
  * features summed as an f32 fma chain, each rounded to int64 with 32

@@ -860,6 +860,13 @@ extern "C" int naiwa_moe_decode_noalloc(const naiwa_bank* gate, const naiwa_bank
                          (hipStream_t)stream);
 }
 
+extern "C" int64_t naiwa_moe_decode_scratch_bytes(int rows, int width, int H, int I, int down_dtype) {
+    if (rows < 0 || width < 0 || (int64_t)rows * width > 65536 || H <= 0 || I <= 0 || H % 32 || I % 32) return -1;
+    if (down_dtype != NAIWA_Q4_K && down_dtype != NAIWA_Q8_0) return -1;
+    if (rows == 0 || width == 0) return 0;
+    return (int64_t)DecodeScratch(rows, width, H, I, down_dtype).total;
+}
+
 int naiwa_moe_decode_residual(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, void* x,
                               const uint32_t* slot_ids, const float* w, int rows, int width, int act, float* y,
                               int keep_y, int64_t stream) {

@@ -165,6 +165,7 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_moe_decode": (i32, [_P(Bank), _P(Bank), _P(Bank), vp, i32, vp, vp, i32, i32, i32, vp, i64]),
     "naiwa_moe_decode_ex": (i32, [_P(Bank), _P(Bank), _P(Bank), vp, i32, vp, vp, i32, i32, i32, vp, i32, i64]),
     "naiwa_moe_decode_noalloc": (i32, [_P(Bank), _P(Bank), _P(Bank), vp, i32, vp, vp, i32, i32, i32, vp, i32, i64]),
+    "naiwa_moe_decode_scratch_bytes": (i64, [i32, i32, i32, i32, i32]),
     "naiwa_router_topk": (i32, [vp, i32, vp, i32, i32, i32, i32, i32, vp, vp, vp, i64]),
     "naiwa_router_topk_biased": (i32, [vp, i32, vp, vp, i32, i32, i32, i32, i32, vp, vp, vp, i64]),
     "naiwa_router_topk_ld": (i32, [vp, i32, vp, vp, i32, i32, i32, i32, i32, vp, vp, i32, vp, i64]),

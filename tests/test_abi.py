@@ -56,3 +56,39 @@ def test_argument_errors_need_no_device():
         == naiwa_moe._lib.E_INVALID
     assert L.naiwa_router_topk(None, 99, None, 1, 16, 8, 2, 0, None, None, None, 0) \
         == naiwa_moe._lib.E_UNSUPPORTED
+
+
+def _fake_bank(n, k, dtype, slots=8):
+    """A bank descriptor whose base is a made-up (aligned, never dereferenced) address."""
+    stride = (naiwa_moe.lib().naiwa_projection_bytes(dtype, n, k) + 255) & ~255
+    return _lib.Bank(0x7f0000000000, stride, slots, n, k, dtype)
+
+
+def test_noalloc_capacity_is_checked_before_any_device_call():
+    """naiwa_moe_decode_noalloc refuses a call one pair past its fixed array with
+    NAIWA_E_TOO_LARGE before it touches a device (none here: the made-up
+    pointers would fault if anything ran), and the size query names the limit:
+    56 pairs (28 rows of top-2) at H 4096 / I 14336 in Q4_K, 339 rows of top-8 at
+    H 2048 / I 768."""
+    L = naiwa_moe.lib()
+    cap = 8 << 20   # NAIWA_DECODE_NOALLOC_SCRATCH_BYTES
+    Q4K = naiwa_moe.Q4_K
+    fake = ctypes.c_void_p(0x7f0000100000)
+    for H, I, width, rows_max in ((4096, 14336, 2, 28), (2048, 768, 8, 339), (4096, 14336, 1, 55)):
+        assert 0 < L.naiwa_moe_decode_scratch_bytes(rows_max, width, H, I, Q4K) <= cap
+        assert L.naiwa_moe_decode_scratch_bytes(rows_max + 1, width, H, I, Q4K) > cap
+        g, u, d = _fake_bank(I, H, Q4K), _fake_bank(I, H, Q4K), _fake_bank(H, I, Q4K)
+        rc = L.naiwa_moe_decode_noalloc(ctypes.byref(g), ctypes.byref(u), ctypes.byref(d), fake, naiwa_moe.BF16,
+                                        fake, fake, rows_max + 1, width, naiwa_moe.ACT_SILU, fake, 0, 0)
+        assert rc == _lib.E_TOO_LARGE, (H, I, width, rc)
+    # the staged-h path (<= 512 pairs, <= 16 per row) carries K-part dots and
+    # costs more per pair than f32 h, so the limit is not monotone in the pairs
+    fits = [r for r in range(1, 260) if L.naiwa_moe_decode_scratch_bytes(r, 6, 5120, 1536, Q4K) <= cap]
+    assert fits == list(range(1, 56)) + list(range(86, 228))
+    # the K-part dots: one f32 per K part, pair and hidden feature, on top of h
+    s1 = L.naiwa_moe_decode_scratch_bytes(1, 1, 4096, 14336, Q4K)
+    s2 = L.naiwa_moe_decode_scratch_bytes(1, 2, 4096, 14336, Q4K)
+    assert s2 - s1 >= 7 * 4096 * 4
+    assert L.naiwa_moe_decode_scratch_bytes(0, 8, 2048, 768, Q4K) == 0
+    assert L.naiwa_moe_decode_scratch_bytes(1, 8, 2048, 770, Q4K) == -1
+    assert L.naiwa_moe_decode_scratch_bytes(1, 8, 2048, 768, 99) == -1
