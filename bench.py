@@ -109,6 +109,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--upload-sync", choices=["event", "poll"], default="poll",
                     help="cache25: staged uploads complete into the expert pass through an event the compute "
                          "stream waits for, or a device flag one wave polls")
+    ap.add_argument("--upload-path", choices=["kernel", "dma"], default="kernel",
+                    help="cache25: staged uploads as one copy kernel reading the mapped host stacks (the expert "
+                         "pass after it), or hipMemcpyAsync on the copy stream (the cache pairs during it)")
     ap.add_argument("--pcie-frac", type=float, default=1.0,
                     help="cache25: share of each step's missed experts staged over PCIe; the rest run on the "
                          "CPU (the reference's default is 0)")
@@ -515,6 +518,8 @@ def run_cache25(args) -> int:
                                       mode=nm.ROUTE_SOFTMAX_TOPK_RENORM, router_bias=bias_d)
         layer.set_upload_sync(nm.policy.UPLOAD_SYNC_POLL if args.upload_sync == "poll"
                               else nm.policy.UPLOAD_SYNC_EVENT)
+        layer.set_upload_path(nm.policy.UPLOAD_PATH_DMA if args.upload_path == "dma"
+                              else nm.policy.UPLOAD_PATH_KERNEL)
         ranking += [(l, int(e)) for e in np.argsort(ranks)]
         layers.append(layer)
         keep += [stacks, router, bias_d, banks]
@@ -570,7 +575,7 @@ def run_cache25(args) -> int:
     tok_s = rows * steps / (ms / 1e3)
     pairs = tot["hits"] + tot["staged"] + tot["cpu"]
     pcie_gbs = tot["pcie_bytes"] / (ms / 1e3) / 1e9
-    log(f"cache25 ({args.upload_sync}, pcie_frac {args.pcie_frac}): {ms / steps * 1e3:.1f} us/step, "
+    log(f"cache25 ({args.upload_sync}, {args.upload_path} uploads, pcie_frac {args.pcie_frac}): {ms / steps * 1e3:.1f} us/step, "
         f"{tok_s:.1f} tok/s, hit rate {tot['hits'] / pairs:.3f}, "
         f"{tot['staged_experts'] / (steps * L):.2f} staged experts/layer/token, "
         f"{tot['cpu'] / (steps * L):.2f} CPU pairs/layer/token, {tot['promoted']} promotions, "
@@ -587,7 +592,7 @@ def run_cache25(args) -> int:
                                "Zipf(1.1) routing bias, the pcie_frac share of misses staged over PCIe "
                                "(16-slot ring), the rest on the CPU",
                    "layers": L, "hidden": H, "experts": E, "top_k": K, "intermediate": I, "cached": usable,
-                   "ring": ring.length, "pcie_frac": args.pcie_frac, "upload_sync": args.upload_sync,
+                   "ring": ring.length, "pcie_frac": args.pcie_frac, "upload_sync": args.upload_sync, "upload_path": args.upload_path,
                    "promote_cap": 1,
                    "lookahead_swaps": swaps if swaps >= 0 else None, "parallelism": "none (1 GPU)"},
         "cache": {"hit_rate": round(tot["hits"] / pairs, 4),

@@ -120,8 +120,8 @@ int naiwa_cached_layer_seed(naiwa_cached_layer* L, const uint32_t* experts, int 
 
 /* One decode step: x bf16 [rows, H] -> out f32 [rows, H], all on `stream`.
  * Staged uploads are one kernel reading the host stacks through their device
- * mapping when they are mapped pinned memory, else DMA copies; the
- * environment variable NAIWA_UPLOAD_PATH=dma takes DMA copies always.
+ * mapping when they are mapped pinned memory, else DMA copies
+ * (naiwa_cached_layer_set_upload_path).
  * The routing comes back through a mapped doorbell (the reference's
  * TopkDoorbell, src/doorbell/d2h/topk.rs:20-125): the device writes the
  * top-k into fine-grained host memory and raises a sequence word, and the
@@ -155,6 +155,21 @@ int naiwa_cached_layer_forward(naiwa_cached_layer* L, const void* x, int rows, f
 #define NAIWA_UPLOAD_SYNC_POLL 1
 int naiwa_cached_layer_set_upload_sync(naiwa_cached_layer* L, int mode);
 int naiwa_cached_layer_upload_timeouts(const naiwa_cached_layer* L, uint32_t* count);
+
+/* How staged uploads travel (per layer; CopyStream::queue_async,
+ * src/copy_stream.rs:387-409):
+ *  NAIWA_UPLOAD_PATH_KERNEL (the default): when the host stacks are mapped
+ *    pinned memory, one batched copy kernel on the copy stream reads every
+ *    staged expert through the host mapping; the expert pass runs once, after
+ *    the uploads (a kernel beside the copy kernel ends with it);
+ *  NAIWA_UPLOAD_PATH_DMA: hipMemcpyAsync on the copy stream (the SDMA
+ *    engines), one range per expert when slots and stacks are expert-
+ *    contiguous; the cache-slot pairs run while the uploads land and the
+ *    staged pairs accumulate after them, the same bits either way.
+ * Pageable or unmapped stacks always take DMA copies. */
+#define NAIWA_UPLOAD_PATH_KERNEL 0
+#define NAIWA_UPLOAD_PATH_DMA 1
+int naiwa_cached_layer_set_upload_path(naiwa_cached_layer* L, int path);
 
 /* Misses the ring does not take go to the CPU (1, the default) or, with 0, a
  * step that would leave any miss unstaged is refused with NAIWA_E_UNSUPPORTED

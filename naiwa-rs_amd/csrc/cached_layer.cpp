@@ -219,7 +219,7 @@ struct naiwa_cached_layer {
     // one expert is one range (one DMA copy, or one range of the batched copy kernel)
     bool contiguous = false;
     size_t expert_bytes = 0;
-    bool dma_uploads = false;            // NAIWA_UPLOAD_PATH=dma: staged uploads as DMA copies
+    bool dma_uploads = false;            // staged uploads as DMA copies even from mapped stacks
     // lookahead: this layer's prediction (its router on the previous layer's
     // activation), the fence after the last step that read its cache slots,
     // and the claim a forward waits for before its expert kernel
@@ -768,8 +768,6 @@ int naiwa_cached_layer_create(const naiwa_cached_layer_desc* d, naiwa_ring* ring
                         (const uint8_t*)d->down.base == g + L->bytes[0] + L->bytes[1] &&
                         d->gate.slot_stride == d->up.slot_stride && d->gate.slot_stride == d->down.slot_stride &&
                         d->gate.slot_stride >= (int64_t)L->expert_bytes;
-        const char* v = getenv("NAIWA_UPLOAD_PATH");
-        L->dma_uploads = v && strcmp(v, "dma") == 0;
     }
     // staged uploads read the host stacks through their device mapping when all three
     // are mapped pinned memory and every expert range is 16-byte aligned
@@ -822,6 +820,12 @@ int naiwa_cached_layer_destroy(naiwa_cached_layer* L) {
 int naiwa_cached_layer_set_upload_sync(naiwa_cached_layer* L, int mode) {
     if (!L || (mode != NAIWA_UPLOAD_SYNC_EVENT && mode != NAIWA_UPLOAD_SYNC_POLL)) return NAIWA_E_INVALID;
     L->upload_sync = mode;
+    return NAIWA_OK;
+}
+
+int naiwa_cached_layer_set_upload_path(naiwa_cached_layer* L, int path) {
+    if (!L || (path != NAIWA_UPLOAD_PATH_KERNEL && path != NAIWA_UPLOAD_PATH_DMA)) return NAIWA_E_INVALID;
+    L->dma_uploads = path == NAIWA_UPLOAD_PATH_DMA;
     return NAIWA_OK;
 }
 

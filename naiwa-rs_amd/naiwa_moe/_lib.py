@@ -225,6 +225,7 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_cached_layer_prefetch": (i32, [vp, vp, i32, i32, i64, _P(LookaheadStep)]),
     "naiwa_cached_layer_predicted": (i32, [vp, vp, i32, _P(i32)]),
     "naiwa_cached_layer_set_upload_sync": (i32, [vp, i32]),
+    "naiwa_cached_layer_set_upload_path": (i32, [vp, i32]),
     "naiwa_cached_layer_set_cpu_misses": (i32, [vp, i32]),
     "naiwa_cached_layer_upload_timeouts": (i32, [vp, _P(C.c_uint32)]),
     "naiwa_cpu_moe_decode": (i32, [_P(HostExperts), vp, vp, vp, i32, i32, i32, vp]),

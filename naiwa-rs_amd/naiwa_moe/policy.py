@@ -268,6 +268,10 @@ class CachedLayer:
         complete into the expert pass."""
         check(lib().naiwa_cached_layer_set_upload_sync(self._h, mode), "cached_layer_set_upload_sync")
 
+    def set_upload_path(self, path: int) -> None:
+        """UPLOAD_PATH_KERNEL (0, the default) or UPLOAD_PATH_DMA (1): how staged uploads travel."""
+        check(lib().naiwa_cached_layer_set_upload_path(self._h, path), "cached_layer_set_upload_path")
+
     def set_cpu_misses(self, on: bool) -> None:
         """Misses the ring does not take run on the CPU (default), or such a step is refused."""
         check(lib().naiwa_cached_layer_set_cpu_misses(self._h, 1 if on else 0), "cached_layer_set_cpu_misses")
@@ -385,6 +389,8 @@ __all__ = ["ExpertCache", "StagingRing", "CachedLayer", "ExpertProfile", "STAGIN
 
 UPLOAD_SYNC_EVENT = 0
 UPLOAD_SYNC_POLL = 1
+UPLOAD_PATH_KERNEL = 0
+UPLOAD_PATH_DMA = 1
 
 
 def cpu_moe_decode(gate, up, down, dtypes, hidden: int, inter: int, xs, ids, w, act: int = 0) -> np.ndarray:

@@ -631,22 +631,24 @@ def test_poll_upload_wait_that_runs_out_is_reported_by_the_next_step(gpu):
     assert layer.upload_timeouts() == 1
 
 
-def test_poll_and_event_upload_waits_give_the_same_bits(gpu):
-    """Two identical layers, one waiting for its staged uploads through the polled
-    device flag and one through an event, run the same ten steps (pcie_frac 1 and 0.5
-    alternating, so some steps also run misses on the CPU): the outputs are identical
-    bit for bit, as are the per-step counts, and they match the oracle."""
+def test_upload_waits_and_paths_give_the_same_bits(gpu):
+    """Identical layers whose staged uploads travel as one copy kernel or as DMA
+    copies, and complete into the expert pass through the polled device flag or an
+    event, run the same ten steps (pcie_frac 1 and 0.5 alternating, so some steps also
+    run misses on the CPU): the outputs are identical bit for bit, as are the per-step
+    counts, and they match the oracle."""
     nm = gpu
     E, H, I, k, usable, rows = 16, 256, 256, 4, 4, 2
     outs = {}
-    for sync in ("event", "poll"):
+    for sync, path in (("event", "kernel"), ("poll", "kernel"), ("poll", "dma"), ("event", "dma")):
         copy, stream = nm.Stream(), nm.Stream()
         ring = nm.policy.StagingRing()
         layer, banks, stacks, host = make_layer(nm, 2800, E, H, I, k, usable, ring, copy)
         layer.set_upload_sync(nm.policy.UPLOAD_SYNC_POLL if sync == "poll" else nm.policy.UPLOAD_SYNC_EVENT)
+        layer.set_upload_path(nm.policy.UPLOAD_PATH_DMA if path == "dma" else nm.policy.UPLOAD_PATH_KERNEL)
         res = []
         for i in range(10):
-            print(f"[{sync} step {i}]", flush=True)
+            print(f"[{sync} {path} step {i}]", flush=True)
             x = S.activations_bf16(2810 + i, rows, H)
             out = nm.DeviceBuffer(rows * H * 4)
             info = layer.forward(nm.DeviceBuffer.from_array(x), rows, out, pcie_frac=1.0 if i % 2 == 0 else 0.5,
@@ -658,8 +660,10 @@ def test_poll_and_event_upload_waits_give_the_same_bits(gpu):
             res.append((y, info["hits"], info["staged_experts"], info["cpu"]))
         copy.sync()
         assert layer.upload_timeouts() == 0
-        outs[sync] = res
-    for (ye, *ce), (yp, *cp) in zip(outs["event"], outs["poll"]):
-        assert np.array_equal(ye.view(np.uint32), yp.view(np.uint32))
-        assert ce == cp
-    assert sum(r[3] for r in outs["poll"]) > 0 and sum(r[2] for r in outs["poll"]) > 0
+        outs[(sync, path)] = res
+    first = outs[("event", "kernel")]
+    for key, res in outs.items():
+        for (ye, *ce), (yp, *cp) in zip(first, res):
+            assert np.array_equal(ye.view(np.uint32), yp.view(np.uint32)), key
+            assert ce == cp, key
+    assert sum(r[3] for r in first) > 0 and sum(r[2] for r in first) > 0
