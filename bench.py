@@ -705,7 +705,7 @@ def run_prefill_stream(args) -> int:
         "metric": "MoE prefill tok/s with host-resident experts (DeepSeek-V2-Lite shape, layer stream)",
         "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f16 x Q4_K/Q8_0 (f32 accumulate)",
+        "dtype": "bf16 x Q4_K/Q8_0 (f32 accumulate)",
         "data": "synthetic (device-generated Q4_K/Q8_0 experts in pinned host stacks: gate/up N(0,0.02), "
                 f"down N(0,{DOWN_STD_DEEPSEEK}); N(0,1) bf16 tokens)",
         "config": {"workload": "DeepSeek-V2-Lite-shaped MoE prefill, 26 layers, 64 routed top-6 + 2 shared experts "
@@ -816,9 +816,8 @@ def run_mixtral(args) -> int:
     stream.sync()
     ms = e0.elapsed_ms(e1) / reps
     health = activation_health(x, T * H)
-    clamped = nm.prefill_status()
-    if health["nonfinite"] or clamped:
-        log(f"mixtral prefill: activations overflowed: {health}, {clamped} f16 clamps")
+    if health["nonfinite"]:
+        log(f"mixtral prefill: activations overflowed: {health}")
         return 1
     flop = 6.0 * H * I * K * T * L
     tflops = flop / (ms / 1e3) / 1e12
@@ -895,7 +894,7 @@ def run_mixtral(args) -> int:
         "metric": "MoE decode tok/s @bs1 (Mixtral-8x7B shape, Q4_K, all experts resident)",
         "value": d1["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": max(3, min(args.steps, 20)), "warmup": 2,
         "ms_per_step": d1["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16 x Q4_K (f32 accumulate); prefill f16 x Q4_K (f32 accumulate)",
+        "dtype": "bf16 x Q4_K (f32 accumulate)",
         "data": f"synthetic (device-generated Q4_K experts: gate/up N(0,0.02), down N(0,{DOWN_STD_MIXTRAL}); "
                 "N(0,1) bf16 tokens)",
         "config": {"workload": "Mixtral-8x7B-shaped MoE stack: decode bs 1/16/64 (all resident), 4096-token "
@@ -1036,7 +1035,6 @@ def run_prefill(args) -> int:
     for _ in range(warmup):
         step()
     stream.sync()
-    nm.prefill_status()
     if args.calibrate_copy:
         calibration_copy(nm, args.calibrate_copy, stream)
     e0, e1 = nm.Event(), nm.Event()
@@ -1047,9 +1045,8 @@ def run_prefill(args) -> int:
     stream.sync()
     ms = e0.elapsed_ms(e1) / steps
     health = activation_health(x, tokens * H)
-    clamped = nm.prefill_status()
-    if health["nonfinite"] or clamped:
-        log(f"prefill: activations overflowed: {health}, {clamped} f16 clamps")
+    if health["nonfinite"]:
+        log(f"prefill: activations overflowed: {health}")
         return 1
     flop = 6.0 * H * I * (K + S_) * tokens * L   # 2 flop/MAC x (gate + up + down)
     tflops = flop / (ms / 1e3) / 1e12
@@ -1088,7 +1085,7 @@ def run_prefill(args) -> int:
         "metric": "MoE prefill tok/s (DeepSeek-V2-Lite shape, 2048 tokens in 512-token chunks)",
         "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f16 x Q4_K/Q8_0 (f32 accumulate)",
+        "dtype": "bf16 x Q4_K/Q8_0 (f32 accumulate)",
         "data": f"synthetic (device-generated Q4_K/Q8_0 experts: gate/up N(0,0.02), down N(0,{DOWN_STD_DEEPSEEK}); "
                 "N(0,1) bf16 tokens)",
         "config": {"workload": "DeepSeek-V2-Lite-shaped MoE prefill, 26 layers, 64 routed top-6 + 2 shared "
@@ -1101,7 +1098,7 @@ def run_prefill(args) -> int:
                      "bytes_per_launch": call_bytes, "call_avg_us": round(call_ms * 1e3, 2),
                      "mfma_tflops": round(call_flop / (call_ms / 1e3) / 1e12, 2),
                      "mfma_frac": round(call_flop / (call_ms / 1e3) / 1e12 / 2500.0, 4)},
-        "activations_after_last_layer": health, "f16_clamped": clamped,
+        "activations_after_last_layer": health,
         "cpu_baseline": None,
     }
     print(json.dumps(result), flush=True)

@@ -261,8 +261,9 @@ int naiwa_moe_gather(const uint32_t* ids, int n, int E, uint32_t* perm_out, uint
  * grouped GEMMs on the matrix cores -- the counterpart of the fork's grouped
  * MoEExperts::forward (src/prefill_stream.rs:2080-2102).  Same banks, slot ids
  * and weights [T, k] as naiwa_moe_decode; x is bf16 [T, H]; out f32 [T, H].
- * Weights are dequantised to f16 in registers and multiplied with
- * v_mfma_f32_32x32x16_f16 (f32 accumulation); x and h are f16.  Needs
+ * Weights are dequantised in f32 in registers, rounded once to bf16 and
+ * multiplied with v_mfma_f32_32x32x16_bf16 (f32 accumulation); x and h are
+ * bf16.  Needs
  * H, I multiples of 128; gate/up Q4_K (H % 256 == 0) or Q8_0, down Q4_K (I %
  * 256 == 0) or Q8_0; T * k <= 65536; slots <= 4096.  Slot ids outside the
  * bank contribute nothing.  flags: NAIWA_PREFILL_ACCUMULATE adds to out
@@ -272,11 +273,8 @@ int naiwa_moe_gather(const uint32_t* ids, int n, int E, uint32_t* perm_out, uint
  * launch fewer than a separate residual add (the same bits); x must then be
  * writable and no other work may read it during the call. */
 #define NAIWA_PREFILL_RESIDUAL 2
-/* The matrix cores take x and h as f16: magnitudes past 65504 are clamped to
- * +-65504, and every clamped value is counted.  naiwa_moe_prefill_status
- * returns the count since its last call (resetting it) after synchronizing
- * the device; a nonzero count means those calls' outputs are not exact. */
-int naiwa_moe_prefill_status(uint64_t* clamped);
+/* The matrix cores take x, the dequantised weights and h as bf16 (f32
+ * accumulation): any finite activation is taken as it is, without clamping. */
 int naiwa_moe_prefill(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, const void* x,
                       const uint32_t* slot_ids, const float* w, int T, int k, int act, float* out, int flags,
                       int64_t stream);

@@ -1,5 +1,5 @@
 // The expert GEMMs of naiwa_moe_decode calls with several tokens per expert, on
-// the matrix cores (prefill.hip): x -> f16 in the 16x16x32 K order, gate/up per
+// the matrix cores (prefill.hip): x -> bf16 in the 16x16x32 K order, gate/up per
 // (64 features, slot segment), down per (64 rows, K part, slot segment) into
 // unweighted partial dots that the decode's ordered combine adds up.
 #pragma once
@@ -9,7 +9,7 @@
 // Whether the call's formats and shapes fit the matrix-core decode.
 bool naiwa_decode_mfma_ok(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, const void* x);
 
-// Scratch bytes of its f16 x [rows, H] and h [n, I].
+// Scratch bytes of its bf16 x [rows, H] and h [n, I].
 size_t naiwa_decode_mfma_bytes(int rows, int n, int H, int I);
 
 // The launches: ws holds naiwa_decode_mfma_bytes bytes; dpart receives K parts of

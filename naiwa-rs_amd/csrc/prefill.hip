@@ -4,13 +4,14 @@
 //
 //   1. gather:   (token, k) pairs sorted by slot (stable), offsets per slot;
 //   2. tiles:    the sorted pairs cut into tiles of 64 pairs of one slot;
-//   3. prep:     x (bf16) converted once to f16 and laid out in the K order of
-//                the gate/up weight format (below);
+//   3. prep:     x (bf16) laid out once in the K order of the gate/up weight
+//                format (below);
 //   4. gate/up:  per (tile, 128 intermediate features): 64 x rows times the
-//                slot's gate and up rows with v_mfma_f32_32x32x16_f16; every
-//                lane dequantises its own weight values to f16 in registers,
-//                straight into the MFMA B operand; the epilogue writes
-//                h = act(gate) * up as f16 in the K order of the down format;
+//                slot's gate and up rows with v_mfma_f32_32x32x16_bf16; every
+//                lane dequantises its own weight values in f32 and rounds them
+//                once to bf16, straight into the MFMA B operand; the epilogue
+//                writes h = act(gate) * up as bf16 in the K order of the down
+//                format;
 //   5. down:     per (tile, 128 output features): h rows times the down rows,
 //                scaled by the pair's routing weight into the pair's f32 row;
 //   6. combine:  out[t] = sum over j ascending of the pair rows (no atomics).
@@ -32,15 +33,19 @@
 //   Q8_0: step s = 4j + u reads block b = 2j + h, its values 8u + 0..7:
 //         run r = 4b + u, elements in order.
 // The activations (x for gate/up, h for down) are stored as groups g = 2s + h
-// of 8 f16 in that order, so the A operand of a step is one 16-byte read.
+// of 8 bf16 in that order, so the A operand of a step is one 16-byte read.
+// bf16 operands carry the f32 exponent range: any finite activation goes in
+// without clamping or scaling.
 #include "common.h"
 #include "decode_mfma.h"
 #include "workspace.h"
 
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float float2v __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -52,22 +57,15 @@ constexpr int kTNG = 128;      // gate/up features per block (waves 0-3 gate, 4-
 constexpr int kTND = 256;      // down output features per block
 constexpr int NAIWA_SCRATCH_PREFILL = 5;
 
-// f16 operands hold |v| <= 65504: activations (x, h) past that are clamped, and every
-// clamped value is counted here (naiwa_moe_prefill_status reads and resets the count).
-__device__ unsigned long long g_prefill_clamped = 0;
-
-// v clamped to the f16 range; n counts the values it changed (NaN included).
-__device__ __forceinline__ float clamp_f16(float v, int& n) {
-    n += !(fabsf(v) <= 65504.0f);
-    return fminf(fmaxf(v, -65504.0f), 65504.0f);
+// Two f32 values rounded to nearest-even bf16 (v_cvt_pk_bf16_f32), as one word.
+__device__ __forceinline__ uint32_t bf16x2_bits(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{a, b}, bf16x2));
 }
-// Add this thread's clamp count to the total: one atomic per wave, and only when
-// something was clamped.  Every lane of the wave calls it.
-__device__ __forceinline__ void count_clamped(int n) {
-    if (__ballot(n != 0) == 0) return;
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) n += __shfl_xor(n, m, 64);
-    if ((threadIdx.x & 63) == 0) atomicAdd(&g_prefill_clamped, (unsigned long long)n);
+// Eight f32 values as the bf16 MFMA operand.
+__device__ __forceinline__ bf16x8 to_bf16x8(const float (&f)[8]) {
+    const u32x4 w = {bf16x2_bits(f[0], f[1]), bf16x2_bits(f[2], f[3]), bf16x2_bits(f[4], f[5]),
+                     bf16x2_bits(f[6], f[7])};
+    return __builtin_bit_cast(bf16x8, w);
 }
 
 template <int DT> struct KBlock;
@@ -141,47 +139,37 @@ __global__ void __launch_bounds__(kThreads) tiles_kernel(const uint32_t* offsets
     }
 }
 
-__device__ __forceinline__ uint32_t f16x2_bits(float a, float b) {
-    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+// One word of two 16-bit values: element e0 (low half) and element e1 (high half)
+// of the 8 values held in w (two a word, low half first).
+__device__ __forceinline__ uint32_t pick16(const uint32_t (&w)[4], int e0, int e1) {
+    const uint32_t a = (w[e0 >> 1] >> (16 * (e0 & 1))) & 0xffffu;
+    const uint32_t b = (w[e1 >> 1] >> (16 * (e1 & 1))) & 0xffffu;
+    return a | (b << 16);
 }
 
-// x bf16 [T, H] -> xp f16 [T, H] in the K order of DT.  One thread per run of
-// 8 values.  bf16 values are exact in f16 inside its range; larger magnitudes
-// are clamped to +-65504 and counted (the expert inputs are normalised
-// activations, so a nonzero count flags a call whose results are not exact).
+// x bf16 [T, H] -> xp bf16 [T, H] in the K order of DT (the values unchanged, only
+// placed).  One thread per run of 8 values.
 template <int DT>
 __global__ void __launch_bounds__(kThreads) prep_kernel(const uint16_t* x, int T, int H, uint16_t* xp) {
     const int runs = H / 8;
     const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    const bool in = i < (int64_t)T * runs;
-    const int t = in ? (int)(i / runs) : 0, run = in ? (int)(i % runs) : 0;
-    uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    if (in) v = *reinterpret_cast<const uint4*>(x + (size_t)t * H + 8 * run);
+    if (i >= (int64_t)T * runs) return;
+    const int t = (int)(i / runs), run = (int)(i % runs);
+    const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)t * H + 8 * run);
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    float f[8];
-    int clamped = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        f[2 * j] = clamp_f16(__uint_as_float(w[j] << 16), clamped);
-        f[2 * j + 1] = clamp_f16(__uint_as_float(w[j] & 0xffff0000u), clamped);
-    }
-    count_clamped(clamped);
-    if (!in) return;
-    float g[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) g[e] = f[DT == NAIWA_Q4_K ? q4_elem(e) : e];
+    auto el = [](int e) { return DT == NAIWA_Q4_K ? q4_elem(e) : e; };
     const int dst = laid_pos<DT>(8 * run); // the run's group (its element 0 is byte 0)
     uint4 o;
-    o.x = f16x2_bits(g[0], g[1]);
-    o.y = f16x2_bits(g[2], g[3]);
-    o.z = f16x2_bits(g[4], g[5]);
-    o.w = f16x2_bits(g[6], g[7]);
+    o.x = pick16(w, el(0), el(1));
+    o.y = pick16(w, el(2), el(3));
+    o.z = pick16(w, el(4), el(5));
+    o.w = pick16(w, el(6), el(7));
     *reinterpret_cast<uint4*>(xp + (size_t)t * H + dst) = o;
 }
 
 // (d * scale, -dmin * min) of 32-value sub-block j of a Q4_K block whose first 16
-// bytes are hd (ggml's get_scale_min_k4), as f16.
-__device__ __forceinline__ void q4k_scale_min(const u32x4& hd, int j, _Float16& sc, _Float16& mn) {
+// bytes are hd (ggml's get_scale_min_k4), exact in f32 (an f16 times a 6-bit integer).
+__device__ __forceinline__ void q4k_scale_min(const u32x4& hd, int j, float& sc, float& mn) {
     const uint32_t s3[3] = {hd.y, hd.z, hd.w};
     auto sb = [&](int i) -> int { return (int)((s3[i >> 2] >> (8 * (i & 3))) & 0xFFu); };
     int s, m;
@@ -192,8 +180,8 @@ __device__ __forceinline__ void q4k_scale_min(const u32x4& hd, int j, _Float16& 
         s = (sb(j + 4) & 0xF) | ((sb(j - 4) >> 6) << 4);
         m = (sb(j + 4) >> 4) | ((sb(j) >> 6) << 4);
     }
-    sc = (_Float16)(naiwa_f16_to_f32(hd.x & 0xffffu) * (float)s);
-    mn = (_Float16)(-(naiwa_f16_to_f32(hd.x >> 16) * (float)m));
+    sc = naiwa_f16_to_f32(hd.x & 0xffffu) * (float)s;
+    mn = -(naiwa_f16_to_f32(hd.x >> 16) * (float)m);
 }
 
 // Nibble masks held in registers.  A nibble masked into the mantissa of an f16 magic
@@ -211,50 +199,42 @@ __device__ __forceinline__ NibMask nib_mask() {
     return n;
 }
 
-// The 8 f16 weights q * sc + mn of quant words da, db (bytes 0-7 of a run), the low
-// nibbles when hi = 0 and the high ones when hi = 1, in byte order 0 2 1 3 4 6 5 7.
-__device__ __forceinline__ half8 q4k_unpack(uint32_t da, uint32_t db, int hi, const NibMask& nm, _Float16 sc,
-                                            _Float16 mn) {
+// The 8 weights q * sc + mn of quant words da, db (bytes 0-7 of a run), the low
+// nibbles when hi = 0 and the high ones when hi = 1, in byte order 0 2 1 3 4 6 5 7,
+// rounded once to bf16.  Each pair of nibbles becomes two f16 magic + q (one
+// v_and_or_b32), and each weight one v_fma_mix_f32: (magic + q) * sc + (mn - magic
+// * sc) in f32.  The folded offset is rounded once in f32 (an error below 2^-14 sc,
+// far under the bf16 rounding of the weight).
+__device__ __forceinline__ bf16x8 q4k_unpack(uint32_t da, uint32_t db, int hi, const NibMask& nm, float sc,
+                                             float mn) {
     const uint32_t mk = nm.m[hi], magic = hi ? 0x54005400u : 0x64006400u;
-    const _Float16 b = hi ? (_Float16)-64.0f : (_Float16)-1024.0f;
-    const half2v scv = {sc, sc}, mnv = {mn, mn}, bias = {b, b};
-    half2v p[4];
-    p[0] = __builtin_bit_cast(half2v, (da & mk) | magic);
-    p[1] = __builtin_bit_cast(half2v, ((da >> 8) & mk) | magic);
-    p[2] = __builtin_bit_cast(half2v, (db & mk) | magic);
-    p[3] = __builtin_bit_cast(half2v, ((db >> 8) & mk) | magic);
-    half8 out;
+    const float m2 = __builtin_fmaf(hi ? -64.0f : -1024.0f, sc, mn);
+    const uint32_t p[4] = {(da & mk) | magic, ((da >> 8) & mk) | magic, (db & mk) | magic,
+                           ((db >> 8) & mk) | magic};
+    float f[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const half2v w = __builtin_elementwise_fma(p[i] + bias, scv, mnv);
-        out[2 * i] = w[0];
-        out[2 * i + 1] = w[1];
+        const half2v v = __builtin_bit_cast(half2v, p[i]);
+        f[2 * i] = __builtin_fmaf((float)v[0], sc, m2);
+        f[2 * i + 1] = __builtin_fmaf((float)v[1], sc, m2);
     }
-    return out;
+    return to_bf16x8(f);
 }
 
-// The 8 f16 weights d * q of the signed bytes of words d0, d1 (values in order).
-__device__ __forceinline__ half8 q8_unpack(uint32_t d0, uint32_t d1, _Float16 dv) {
-    const half2v d = {dv, dv};
-    const half2v k1152 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-    half2v p[4];
-    // (q0, q1) -> f16 1024 + (q ^ 0x80) = 1152 + q for the signed byte q
-    p[0] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(d0, d0, 0x0C010C00u) ^ 0x64806480u);
-    p[1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(d0, d0, 0x0C030C02u) ^ 0x64806480u);
-    p[2] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(d1, d1, 0x0C010C00u) ^ 0x64806480u);
-    p[3] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(d1, d1, 0x0C030C02u) ^ 0x64806480u);
-    half8 out;
+// The 8 weights d * q of the signed bytes of words d0, d1 (values in order): the
+// product is exact in f32 and rounded once to bf16.
+__device__ __forceinline__ bf16x8 q8_unpack(uint32_t d0, uint32_t d1, float d) {
+    float f[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const half2v v = (p[i] + k1152) * d;
-        out[2 * i] = v[0];
-        out[2 * i + 1] = v[1];
+    for (int k = 0; k < 4; ++k) {
+        f[k] = (float)(int8_t)(d0 >> (8 * k)) * d;
+        f[4 + k] = (float)(int8_t)(d1 >> (8 * k)) * d;
     }
-    return out;
+    return to_bf16x8(f);
 }
 
 // One lane's share of a weight row for one K-block: raw words, then unpacked
-// step by step into the MFMA B operand (8 f16).
+// step by step into the MFMA B operand (8 bf16).
 template <int DT> struct BRow;
 
 template <> struct BRow<NAIWA_Q4_K> {
@@ -267,12 +247,12 @@ template <> struct BRow<NAIWA_Q4_K> {
 #pragma unroll
         for (int c = 0; c < 4; ++c) q[c] = *reinterpret_cast<const u32x4*>(blk + 16 + 32 * c + 16 * h);
     }
-    __device__ __forceinline__ half8 step(int s, const NibMask& nm) const {
+    __device__ __forceinline__ bf16x8 step(int s) const {
         const int c = s / 4, t = s % 4;
         const uint32_t da = (t % 2) ? q[c].z : q[c].x, db = (t % 2) ? q[c].w : q[c].y;
-        _Float16 a, b;
+        float a, b;
         q4k_scale_min(hd, 2 * c + t / 2, a, b);
-        return q4k_unpack(da, db, t / 2, nm, a, b);
+        return q4k_unpack(da, db, t / 2, nib_mask(), a, b);
     }
 };
 
@@ -290,7 +270,7 @@ template <> struct BRow<NAIWA_Q8_0> {
             for (int i = 0; i < 9; ++i) w[j][i] = p[i];
         }
     }
-    __device__ __forceinline__ half8 step(int s) const {
+    __device__ __forceinline__ bf16x8 step(int s) const {
         const int j = s / 4, u = s % 4;
         // values 8u .. 8u + 7 are bytes sh + 2 + 8u .. of the window: words 2u + 1 and
         // 2u + 2 when the block starts at byte 2 of its first word, else shifted by 2
@@ -298,7 +278,7 @@ template <> struct BRow<NAIWA_Q8_0> {
         const uint32_t d1 =
             sh[j] ? w[j][2 * u + 2] : __builtin_amdgcn_alignbyte(w[j][2 * u + 2], w[j][2 * u + 1], 2);
         const uint32_t dbits = sh[j] ? (w[j][0] >> 16) : (w[j][0] & 0xffffu);
-        return q8_unpack(d0, d1, __builtin_bit_cast(_Float16, (uint16_t)dbits));
+        return q8_unpack(d0, d1, naiwa_f16_to_f32(dbits));
     }
 };
 
@@ -392,7 +372,7 @@ __device__ __forceinline__ void tile_k_loop(const uint16_t* abase, const int* ro
             const u32x4* ab = alane + (kb & 1) * kBuf;
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                _Float16 sc[2], mn[2];
+                float sc[2], mn[2];
                 q4k_scale_min(b.hd, 2 * c, sc[0], mn[0]);
                 q4k_scale_min(b.hd, 2 * c + 1, sc[1], mn[1]);
                 // the last chunk's scales are taken: the next header can replace this one
@@ -401,11 +381,11 @@ __device__ __forceinline__ void tile_k_loop(const uint16_t* abase, const int* ro
                 for (int t = 0; t < 4; ++t) {
                     const int s = 4 * c + t;
                     const uint32_t da = (t % 2) ? b.q[c].z : b.q[c].x, db = (t % 2) ? b.q[c].w : b.q[c].y;
-                    const half8 wv = q4k_unpack(da, db, t / 2, nm, sc[t / 2], mn[t / 2]);
+                    const bf16x8 wv = q4k_unpack(da, db, t / 2, nm, sc[t / 2], mn[t / 2]);
 #pragma unroll
                     for (int ms = 0; ms < 2; ++ms) {
-                        const half8 x8 = __builtin_bit_cast(half8, ab[2 * s * (kTM + 1) + 32 * ms]);
-                        acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x8, wv, acc[ms], 0, 0, 0);
+                        const bf16x8 x8 = __builtin_bit_cast(bf16x8, ab[2 * s * (kTM + 1) + 32 * ms]);
+                        acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x8, wv, acc[ms], 0, 0, 0);
                     }
                 }
                 b.q[c] = *reinterpret_cast<const u32x4*>(nblk + 16 + 32 * c + 16 * h);
@@ -433,11 +413,11 @@ __device__ __forceinline__ void tile_k_loop(const uint16_t* abase, const int* ro
             const ATile<DT>& a = as[kb & 1];
 #pragma unroll
             for (int s = 0; s < KBlock<DT>::kSteps; ++s) {
-                const half8 wv = bw.step(s);
+                const bf16x8 wv = bw.step(s);
 #pragma unroll
                 for (int ms = 0; ms < 2; ++ms) {
-                    const half8 x8 = __builtin_bit_cast(half8, a.at(2 * s + h, 32 * ms + (lane & 31)));
-                    acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x8, wv, acc[ms], 0, 0, 0);
+                    const bf16x8 x8 = __builtin_bit_cast(bf16x8, a.at(2 * s + h, 32 * ms + (lane & 31)));
+                    acc[ms] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x8, wv, acc[ms], 0, 0, 0);
                 }
             }
             st.store(as[(kb + 1) & 1], tid);
@@ -454,7 +434,7 @@ __device__ __forceinline__ void tile_k_loop(const uint16_t* abase, const int* ro
 
 // gate/up: one tile of <= 64 pairs x 128 intermediate features; waves 0-3 the
 // gate rows, waves 4-7 the up rows of the same 4 x 32 features.  xp: x in the K
-// order of DG; hp (out): h in the K order of DD, f16 [pairs, I].
+// order of DG; hp (out): h in the K order of DD, bf16 [pairs, I].
 template <int DG, int DD>
 __global__ void __launch_bounds__(kGemm, 4)
 gateup_kernel(Bank gate, Bank up, const uint16_t* xp, int H, int I, int k, const uint32_t* perm, Tiles tl,
@@ -476,7 +456,7 @@ gateup_kernel(Bank gate, Bank up, const uint16_t* xp, int H, int I, int k, const
     floatx16 acc[2] = {}; // [m subtile]
     tile_k_loop<DG>(xp, rows, wrow, nkb, as, tid, lane, h, acc);
     // epilogue: the gate waves hand act(g) to the up waves of the same strip through
-    // LDS (the A tiles are no longer read); h = act(g) * u as f16 at its laid-out
+    // LDS (the A tiles are no longer read); h = act(g) * u as bf16 at its laid-out
     // position for the down format
     float* xch = reinterpret_cast<float*>(&as[0]);
     const int xbase = (strip * 32) * 64 + lane;
@@ -489,7 +469,6 @@ gateup_kernel(Bank gate, Bank up, const uint16_t* xp, int H, int I, int k, const
     __syncthreads();
     if (is_up) {
         const int col = laid_pos<DD>(n);
-        int clamped = 0;
 #pragma unroll
         for (int ms = 0; ms < 2; ++ms)
 #pragma unroll
@@ -497,11 +476,9 @@ gateup_kernel(Bank gate, Bank up, const uint16_t* xp, int H, int I, int k, const
                 const int m = 32 * ms + 8 * (v / 4) + 4 * h + v % 4;
                 if (m < cnt) {
                     const float g = xch[xbase + (16 * ms + v) * 64];
-                    const _Float16 hv = (_Float16)clamp_f16(g * acc[ms][v], clamped);
-                    hp[(size_t)(start + m) * I + col] = __builtin_bit_cast(uint16_t, hv);
+                    hp[(size_t)(start + m) * I + col] = (uint16_t)bf16x2_bits(g * acc[ms][v], 0.0f);
                 }
             }
-        count_clamped(clamped);
     }
 }
 
@@ -591,7 +568,7 @@ combine_kernel(const float* ypair, const uint32_t* ids, int k, int H, int slots,
 // naiwa_moe_decode calls with several tokens per expert run their expert GEMMs
 // here.  A block of 4 waves takes one slot segment (the sorted pairs of one
 // slot) and 64 features; chunks of up to 16 of the segment's tokens are the A
-// operand of v_mfma_f32_16x16x32_f16 and each lane dequantises its own weight
+// operand of v_mfma_f32_16x16x32_bf16 and each lane dequantises its own weight
 // values once into the B operand, so a weight costs the same whatever the
 // token count.  Lane l = 16 g + m holds A[m][8 g + 0..7] (token m of the
 // chunk), B[8 g + 0..7][m] (feature m of the wave's 16) and D[4 g + i][m].
@@ -632,7 +609,7 @@ __host__ __device__ inline int laid16(int f) {
 
 // Per-K-block scale state of one lane (Q4_K: its two sub-blocks 2 g and 2 g + 1).
 struct Scl {
-    _Float16 sc[2], mn[2];
+    float sc[2], mn[2];
 };
 
 // One lane's weights of one K-block (row `row`, lane group g).
@@ -650,7 +627,7 @@ template <> struct W16<NAIWA_Q4_K> {
         q4k_scale_min(hd, 2 * g, c.sc[0], c.mn[0]);
         q4k_scale_min(hd, 2 * g + 1, c.sc[1], c.mn[1]);
     }
-    __device__ __forceinline__ half8 step(int s, const Scl& c, const NibMask& nm) const {
+    __device__ __forceinline__ bf16x8 step(int s, const Scl& c, const NibMask& nm) const {
         const int p = s >> 1, t = s & 1;
         const u32x4& q = p < 2 ? q0 : q1;
         const uint32_t da = (p & 1) ? q.z : q.x, db = (p & 1) ? q.w : q.y;
@@ -669,11 +646,11 @@ template <> struct W16<NAIWA_Q8_0> {
         for (int i = 0; i < 9; ++i) w[i] = p[i];
     }
     __device__ __forceinline__ void prep(int, Scl&) const {}
-    __device__ __forceinline__ half8 step(int s, const Scl&, const NibMask&) const {
+    __device__ __forceinline__ bf16x8 step(int s, const Scl&, const NibMask&) const {
         const uint32_t d0 = sh ? w[2 * s + 1] : __builtin_amdgcn_alignbyte(w[2 * s + 1], w[2 * s], 2);
         const uint32_t d1 = sh ? w[2 * s + 2] : __builtin_amdgcn_alignbyte(w[2 * s + 2], w[2 * s + 1], 2);
         const uint32_t dbits = sh ? (w[0] >> 16) : (w[0] & 0xffffu);
-        return q8_unpack(d0, d1, __builtin_bit_cast(_Float16, (uint16_t)dbits));
+        return q8_unpack(d0, d1, naiwa_f16_to_f32(dbits));
     }
 };
 
@@ -713,8 +690,8 @@ template <int DT, int MT> struct AStage16 {
     }
 };
 
-// x (bf16 or f32) [T, H] -> xl f16 [T, H] in the 16x16x32 K order of DT, one thread
-// per run of 8 values; values past the f16 range are clamped and counted.
+// x (bf16 or f32) [T, H] -> xl bf16 [T, H] in the 16x16x32 K order of DT, one thread
+// per run of 8 values (bf16 input unchanged, f32 rounded to nearest-even bf16).
 template <int DT>
 __global__ void __launch_bounds__(kThreads) dec_prep_kernel(const void* x, int x_bf16, int T, int H, uint16_t* xl) {
     const int runs = H / 8;
@@ -738,19 +715,15 @@ __global__ void __launch_bounds__(kThreads) dec_prep_kernel(const void* x, int x
             f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
         }
     }
-    int clamped = 0;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = clamp_f16(f[e], clamped);
-    count_clamped(clamped);
     if (!in) return;
     float g[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) g[e] = f[DT == NAIWA_Q4_K ? q4_elem(e) : e];
     uint4 o;
-    o.x = f16x2_bits(g[0], g[1]);
-    o.y = f16x2_bits(g[2], g[3]);
-    o.z = f16x2_bits(g[4], g[5]);
-    o.w = f16x2_bits(g[6], g[7]);
+    o.x = bf16x2_bits(g[0], g[1]);
+    o.y = bf16x2_bits(g[2], g[3]);
+    o.z = bf16x2_bits(g[4], g[5]);
+    o.w = bf16x2_bits(g[6], g[7]);
     *reinterpret_cast<uint4*>(xl + (size_t)t * H + laid16<DT>(8 * run)) = o;
 }
 
@@ -782,15 +755,15 @@ __device__ __forceinline__ void dec_chunk(const uint16_t* abase, const int* rows
         const ATile16<DT, MT>& a = as[j & 1];
 #pragma unroll
         for (int s = 0; s < K16<DT>::kSteps; ++s) {
-            half8 x8[MT];
+            bf16x8 x8[MT];
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) x8[mt] = __builtin_bit_cast(half8, a.at(4 * s + g, kDecM * mt + m));
+            for (int mt = 0; mt < MT; ++mt) x8[mt] = __builtin_bit_cast(bf16x8, a.at(4 * s + g, kDecM * mt + m));
 #pragma unroll
             for (int q = 0; q < NP; ++q) {
-                const half8 b = bw[q].step(s, c[q], nm);
+                const bf16x8 b = bw[q].step(s, c[q], nm);
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
-                    acc[q][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x8[mt], b, acc[q][mt], 0, 0, 0);
+                    acc[q][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x8[mt], b, acc[q][mt], 0, 0, 0);
             }
         }
         st.store(as[(j + 1) & 1], tid);
@@ -804,7 +777,7 @@ __device__ __forceinline__ void dec_chunk(const uint16_t* abase, const int* rows
     if (j < nkb) block(j, cur, nxt);
 }
 
-// gate/up: block (64 features, slot segment); h = act(gate) * up as f16 at the
+// gate/up: block (64 features, slot segment); h = act(gate) * up as bf16 at the
 // pair's sorted position, in the 16x16x32 K order of DD.
 template <int DG, int DD, int MT>
 __global__ void __launch_bounds__(kDecThreads, 2)
@@ -822,7 +795,6 @@ dec_gateup_kernel(Bank gate, Bank up, const uint16_t* xl, int H, int I, int widt
     const uint8_t* wrow[2] = {gate.base + (int64_t)slot * gate.stride + (int64_t)n * gate.row_bytes,
                               up.base + (int64_t)slot * up.stride + (int64_t)n * up.row_bytes};
     const int col = laid16<DD>(n);
-    int clamped = 0;
     for (int c0 = b; c0 < e; c0 += CM) {
         const int cnt = min(CM, e - c0);
         __syncthreads(); // the previous chunk is done with rows and the A tiles
@@ -835,13 +807,11 @@ dec_gateup_kernel(Bank gate, Bank up, const uint16_t* xl, int H, int I, int widt
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int mm = kDecM * mt + 4 * g + i;
-                if (mm < cnt) {
-                    const float hv = clamp_f16(naiwa_act(act, acc[0][mt][i]) * acc[1][mt][i], clamped);
-                    hl[(size_t)(c0 + mm) * I + col] = __builtin_bit_cast(uint16_t, (_Float16)hv);
-                }
+                if (mm < cnt)
+                    hl[(size_t)(c0 + mm) * I + col] =
+                        (uint16_t)bf16x2_bits(naiwa_act(act, acc[0][mt][i]) * acc[1][mt][i], 0.0f);
             }
     }
-    count_clamped(clamped);
 }
 
 // down: block (64 output rows, K part, slot segment); the unweighted partial dot of
@@ -961,18 +931,6 @@ int naiwa_decode_mfma_experts(const naiwa_bank* gate, const naiwa_bank* up, cons
     return naiwa_hip_rc(hipGetLastError());
 }
 
-extern "C" int naiwa_moe_prefill_status(uint64_t* clamped) {
-    if (!clamped) return NAIWA_E_INVALID;
-    hipError_t e = hipDeviceSynchronize();
-    if (e != hipSuccess) return (int)e;
-    unsigned long long v = 0;
-    if ((e = hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_prefill_clamped), sizeof(v), 0, hipMemcpyDeviceToHost)) != hipSuccess)
-        return (int)e;
-    *clamped = v;
-    v = 0;
-    return naiwa_hip_rc(hipMemcpyToSymbol(HIP_SYMBOL(g_prefill_clamped), &v, sizeof(v), 0, hipMemcpyHostToDevice));
-}
-
 extern "C" int naiwa_moe_prefill(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, const void* x,
                                  const uint32_t* slot_ids, const float* w, int T, int k, int act, float* out,
                                  int flags, int64_t stream) {
@@ -998,7 +956,7 @@ extern "C" int naiwa_moe_prefill(const naiwa_bank* gate, const naiwa_bank* up, c
     if ((gate->dtype == NAIWA_Q4_K && (rbg % 16)) || (down->dtype == NAIWA_Q4_K && (rbd % 16))) return NAIWA_E_INVALID;
     if ((gate->dtype == NAIWA_Q8_0 && (rbg % 4)) || (down->dtype == NAIWA_Q8_0 && (rbd % 4))) return NAIWA_E_INVALID;
 
-    // scratch: perm [n] | offsets [slots + 1] | bad | tiles 3 x max + n | xp f16 [T, H] | h f16 [n, I] |
+    // scratch: perm [n] | offsets [slots + 1] | bad | tiles 3 x max + n | xp bf16 [T, H] | h bf16 [n, I] |
     //          ypair f32 [n, H]
     const int64_t max_tiles = (n + kTM - 1) / kTM + slots;
     auto a256 = [](size_t b) { return (b + 255) & ~size_t(255); };

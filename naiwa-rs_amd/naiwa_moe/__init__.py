@@ -12,7 +12,7 @@ from .device import DeviceBuffer, Event, PinnedBuffer, Stream, device_count, dev
 from . import doorbells, gguf, policy, prefill
 from .ops import (HostExpertStacks, LayerBanks, SlotBank, copy_batch, expert_range, indexed_moe_fused_decode,
                   layer_desc, moe_gather, moe_prefill, router_topk, row_bytes, slot_stride, stack_decode, stack_status,
-                  prefill_status, synth, upload_expert)
+                  synth, upload_expert)
 
 __all__ = [
     "ACT_GELU_PYTORCH_TANH", "ACT_SILU", "BF16", "F16", "F32", "Q4_K", "Q8_0", "E_BAD_ID", "E_DEVICE",
@@ -21,6 +21,6 @@ __all__ = [
     "NaiwaError", "lib", "DeviceBuffer", "Event", "PinnedBuffer", "Stream", "device_count",
     "device_info", "mem_info", "synchronize", "LayerBanks", "SlotBank", "expert_range",
     "indexed_moe_fused_decode", "moe_gather", "moe_prefill", "router_topk", "row_bytes", "slot_stride",
-    "layer_desc", "stack_decode", "stack_status", "prefill_status", "synth", "policy", "doorbells", "gguf", "prefill", "HostExpertStacks", "upload_expert",
+    "layer_desc", "stack_decode", "stack_status", "synth", "policy", "doorbells", "gguf", "prefill", "HostExpertStacks", "upload_expert",
     "copy_batch",
 ]

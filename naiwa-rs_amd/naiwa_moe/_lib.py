@@ -169,7 +169,6 @@ SIGNATURES: dict[str, tuple] = {
     "naiwa_router_topk": (i32, [vp, i32, vp, i32, i32, i32, i32, i32, vp, vp, vp, i64]),
     "naiwa_router_topk_biased": (i32, [vp, i32, vp, vp, i32, i32, i32, i32, i32, vp, vp, vp, i64]),
     "naiwa_router_topk_ld": (i32, [vp, i32, vp, vp, i32, i32, i32, i32, i32, vp, vp, i32, vp, i64]),
-    "naiwa_moe_prefill_status": (i32, [_P(C.c_uint64)]),
     "naiwa_moe_prefill": (i32, [_P(Bank), _P(Bank), _P(Bank), vp, vp, vp, i32, i32, i32, vp, i32, i64]),
     "naiwa_moe_gather": (i32, [vp, i32, i32, vp, vp, vp, i64]),
     "naiwa_synth": (i32, [i32, u64, u64, i64, f32, f32, vp, i64]),

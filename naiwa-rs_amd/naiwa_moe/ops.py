@@ -198,13 +198,6 @@ def moe_prefill(banks: LayerBanks, x, slot_ids, weights, T: int, topk: int, out,
     check(rc, "naiwa_moe_prefill")
 
 
-def prefill_status() -> int:
-    """Activations clamped to the f16 range by prefill calls since the last read (synchronizes)."""
-    v = C.c_uint64()
-    check(lib().naiwa_moe_prefill_status(C.byref(v)), "naiwa_moe_prefill_status")
-    return v.value
-
-
 def router_topk(x, x_dtype: int, W, rows: int, H: int, E: int, k: int, ids_out, w_out,
                 mode: int = ROUTE_SOFTMAX_TOPK_RENORM, logits_out=None, stream: int = 0, ld: int = 0) -> None:
     """ld > 0: ids_out / w_out rows ld entries apart (the routed experts in columns 0..k-1)."""
@@ -258,5 +251,5 @@ def synth(dtype: int, seed: int, n: int, out, mean: float = 0.0, std: float = 1.
     check(lib().naiwa_synth(dtype, seed, offset, n, mean, std, _dev(out), stream), "naiwa_synth")
 
 
-__all__ = ["layer_desc", "stack_decode", "stack_status", "synth","SlotBank", "LayerBanks", "indexed_moe_fused_decode", "router_topk", "moe_gather", "prefill_status",
+__all__ = ["layer_desc", "stack_decode", "stack_status", "synth","SlotBank", "LayerBanks", "indexed_moe_fused_decode", "router_topk", "moe_gather",
            "row_bytes", "expert_range", "slot_stride", "BF16", "F32", "Q4_K", "Q8_0"]

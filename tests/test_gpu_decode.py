@@ -269,7 +269,7 @@ def test_k_parts_and_large_calls(gpu, dt, H, I, E, k, rows):
     ((O.Q8_0, O.Q8_0, O.Q4_K), 384, 2304, 5, 2, 7, False, 0),  # Q4_K down in two K parts
 ])
 def test_matrix_core_decode(gpu, dt, H, I, E, k, rows, x_f32, act):
-    """Calls of 4 or more rows run their expert GEMMs on the matrix cores (f16
+    """Calls of 4 or more rows run their expert GEMMs on the matrix cores (bf16
     operands, f32 accumulation): every format pairing, tokens past one 16-token
     tile, K parts of the down projection, f32 input and both activations."""
     nm = gpu
@@ -295,7 +295,32 @@ def test_matrix_core_decode(gpu, dt, H, I, E, k, rows, x_f32, act):
     err = S.max_rel_err(got, want)
     print(f"  max_rel_err={err:.3e}", flush=True)
     assert err < TOL
-    assert nm.prefill_status() == 0   # no activation left the f16 range
+
+
+@pytest.mark.parametrize("x_f32", [False, True])
+def test_matrix_core_decode_takes_activations_of_1e5(gpu, x_f32):
+    """The matrix-core decode (8 rows) with every other token's activations scaled
+    to ~1e5 (h then reaches ~1e9, far past the f16 range): bf16 operands keep the
+    exponent range, so both groups of rows land within the 1e-2 bar of the oracle,
+    each against its own scale."""
+    nm = gpu
+    dt, H, I, E, k, rows = (O.Q4_K, O.Q4_K, O.Q8_0), 512, 384, 6, 3, 8
+    g, u, d, r = S.layer(2600, E, H, I, dt)
+    x0 = S.activations_bf16(2601, rows, H)
+    ids, w = O.topk(O.router_logits(O.from_bf16(x0), r), k)
+    xs = O.from_bf16(x0).copy()
+    big = np.arange(rows) % 2 == 0
+    xs[big] *= np.float32(1.0e5)
+    x = O.to_bf16(xs)
+    print(f"[mfma decode 1e5 rows x_f32={x_f32}]", flush=True)
+    got = run_decode(nm, g, u, d, dt, H, I, x, ids, w, x_f32=x_f32)
+    want = oracle_decode(g, u, d, dt, H, I, x, ids, w)
+    assert np.isfinite(got).all()
+    assert np.abs(want[big]).max() > 1.0e8
+    for sel in (big, ~big):
+        err = S.max_rel_err(got[sel], want[sel])
+        print(f"  max_rel_err={err:.3e}", flush=True)
+        assert err < TOL
 
 
 def test_matrix_core_decode_accumulates(gpu):

@@ -27,7 +27,6 @@ def run_case(nm, seed, T, E, k, H, I, dt, mode=O.ROUTE_SOFTMAX_TOPK_RENORM, muta
     print(f"[prefill seed={seed} T={T} E={E} k={k} H={H} I={I} dt={dt}]", flush=True)
     nm.moe_prefill(banks, xd, idd, wd, T, k, out)
     nm.synchronize()
-    assert nm.prefill_status() == 0   # nothing was clamped to the f16 range
     got = out.download(np.float32).reshape(T, H)
     gs, us, ds = O.stack(g, dt[0], I, H), O.stack(u, dt[1], I, H), O.stack(d, dt[2], H, I)
     # a pair outside the bank contributes nothing: the same as a valid id with weight 0
@@ -187,27 +186,36 @@ def test_prefill_deepseek_chunk_with_shared_experts(gpu):
     assert err < TOL
 
 
-def test_prefill_counts_values_past_the_f16_range(gpu):
-    """x and h enter the matrix cores as f16: values past 65504 are clamped and
-    counted, so a caller can tell that a call's result is not exact."""
+def test_prefill_takes_activations_of_1e5_as_they_are(gpu):
+    """x and h enter the matrix cores as bf16, which keeps the f32 exponent range:
+    rows of activations around 1e5 (h then reaches ~1e9) land within the 1e-2 bar
+    of the oracle, and the unit-scale rows of the same call are as exact as in a
+    call of their own (each output row depends on its own token only)."""
     nm = gpu
-    T, E, k, H, I, dt = 16, 8, 2, 256, 256, (O.Q4_K,) * 3
+    T, E, k, H, I, dt = 32, 8, 2, 512, 256, (O.Q4_K, O.Q4_K, O.Q8_0)
     g, u, d, r = S.layer(1900, E, H, I, dt)
     banks = nm.LayerBanks(E, H, I, dt)
     for e in range(E):
         banks.load(e, g[e], u[e], d[e])
-    x = S.activations_bf16(1901, T, H)
-    ids, w = O.topk(O.router_logits(O.from_bf16(x), r), k, O.ROUTE_SOFTMAX_TOPK_RENORM)
+    xs = O.from_bf16(S.activations_bf16(1901, T, H)).copy()
+    big = np.arange(T) % 2 == 0
+    xs[big] *= np.float32(1.0e5)
+    x = O.to_bf16(xs)
+    xf = O.from_bf16(x)
+    assert np.abs(xf[big]).max() > 3.0e5 and np.abs(xf[~big]).max() < 10.0
+    ids, w = O.topk(O.router_logits(O.from_bf16(S.activations_bf16(1901, T, H)), r), k, O.ROUTE_SOFTMAX_TOPK_RENORM)
     idd = nm.DeviceBuffer.from_array(ids.astype(np.uint32))
     wd = nm.DeviceBuffer.from_array(w.astype(np.float32))
     out = nm.DeviceBuffer(T * H * 4)
-    nm.prefill_status()   # reset
-    xd = nm.DeviceBuffer.from_array(x)
-    nm.moe_prefill(banks, xd, idd, wd, T, k, out)
-    assert nm.prefill_status() == 0
-    big = O.from_bf16(x).copy()
-    big[3, :5] = 1.0e5       # exact in bf16, past the f16 range
-    xb = nm.DeviceBuffer.from_array(O.to_bf16(big))
-    nm.moe_prefill(banks, xb, idd, wd, T, k, out)
-    assert nm.prefill_status() >= 5
-    assert nm.prefill_status() == 0   # reading resets the count
+    print(f"[prefill 1e5 rows T={T} H={H} I={I}]", flush=True)
+    nm.moe_prefill(banks, nm.DeviceBuffer.from_array(x), idd, wd, T, k, out)
+    nm.synchronize()
+    got = out.download(np.float32).reshape(T, H)
+    gs, us, ds = O.stack(g, dt[0], I, H), O.stack(u, dt[1], I, H), O.stack(d, dt[2], H, I)
+    want = O.fused_moe_decode(gs, us, ds, xf, ids, w)
+    assert np.isfinite(got).all()
+    assert np.abs(want[big]).max() > 1.0e8     # h far past the f16 range
+    for rows in (big, ~big):
+        err = S.max_rel_err(got[rows], want[rows])
+        print(f"  rows of max |x| {np.abs(xf[rows]).max():.3g}: max_rel_err={err:.3e}", flush=True)
+        assert err < TOL
