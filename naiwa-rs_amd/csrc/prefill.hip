@@ -364,10 +364,10 @@ __device__ __forceinline__ void tile_k_loop(const uint16_t* abase, const int* ro
         for (int kb = 0; kb < nkb; ++kb) {
             const int kn = min(kb + 1, nkb - 1);
             const uint8_t* nblk = wrow + (size_t)kn * NAIWA_Q4_K_BYTES;
-            // the next A tile goes to the other buffer in two halves during this block (its
-            // last reads were before the previous barrier): half the staging registers
-            constexpr int kHalf = AStage<DT>::kPer / 2;
-            st.load(abase, rows, kn, tid, 0, kHalf);
+            // the next A tile's loads go out now and land in the other buffer (its last
+            // reads were before the previous barrier) after this block's last chunk: a
+            // whole K-block of MFMA work hides their latency
+            st.load(abase, rows, kn, tid);
             __builtin_amdgcn_sched_barrier(0); // keep the prefetches where they are issued
             const u32x4* ab = alane + (kb & 1) * kBuf;
 #pragma unroll
@@ -389,14 +389,8 @@ __device__ __forceinline__ void tile_k_loop(const uint16_t* abase, const int* ro
                     }
                 }
                 b.q[c] = *reinterpret_cast<const u32x4*>(nblk + 16 + 32 * c + 16 * h);
-                if (c == 0) {
-                    st.store(as[(kb + 1) & 1], tid, 0, kHalf);
-                    st.load(abase, rows, kn, tid, kHalf, AStage<DT>::kPer);
-                }
                 __builtin_amdgcn_sched_barrier(0);
-                if (c == 2) {
-                    st.store(as[(kb + 1) & 1], tid, kHalf, AStage<DT>::kPer);
-                }
+                if (c == 3) st.store(as[(kb + 1) & 1], tid);
             }
             lds_barrier();
         }
