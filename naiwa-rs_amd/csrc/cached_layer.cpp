@@ -209,8 +209,6 @@ struct naiwa_cached_layer {
     uint32_t* xpub_dev = nullptr;
     uint32_t xpub_seq = 0;
     float* cpu_out = nullptr;
-    std::vector<hipEvent_t> ring_fence;  // per ring position: recorded after the step that read it
-    std::vector<char> ring_fenced;
     hipEvent_t staged_done = nullptr;
     bool batch_uploads = false;          // staged uploads as one batched copy kernel, reading
     const void* host_dev[3] = {nullptr, nullptr, nullptr}; // the host stacks' device views
@@ -576,15 +574,17 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         }
     }
 
-    // uploads on the copy stream after the last step that read each ring slot: one kernel
-    // for all of them when the host stacks are mapped pinned memory (one range per expert
-    // when its projections are adjacent, else one per projection), else DMA copies (one per
-    // expert when adjacent, else one per projection)
+    // uploads on the copy stream: one kernel for all of them when the host stacks are
+    // mapped pinned memory (one range per expert when its projections are adjacent, else
+    // one per projection), else DMA copies (one per expert when adjacent, else one per
+    // projection).  They need no fence of their own: every earlier read of this layer's
+    // ring slots (expert passes, promotion copies) precedes the previous step's read_done,
+    // which precedes this step's routing on the device, and the host has seen that
+    // routing complete (its doorbell) before it queues these uploads.
     {
         naiwa_copy items[NAIWA_COPY_BATCH_MAX];
         int ni = 0;
         for (int i = 0; i < nc; ++i) {
-            const int64_t fence = L->ring_fenced[pos[i]] ? (int64_t)L->ring_fence[pos[i]] : 0;
             if (batch) {
                 void* dst[3];
                 L->slot_ptrs(d.usable + pos[i], dst);
@@ -596,8 +596,7 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
                         items[ni++] = naiwa_copy{dst[p],
                                                  (const uint8_t*)L->host_dev[p] + (size_t)chosen[i] * L->host_stride[p],
                                                  (uint64_t)L->bytes[p]};
-                if (fence && (rc = naiwa_hip_rc(hipStreamWaitEvent(L->copy, (hipEvent_t)fence, 0)))) return rc;
-            } else if ((rc = L->upload((int)chosen[i], d.usable + pos[i], fence))) {
+            } else if ((rc = L->upload((int)chosen[i], d.usable + pos[i], 0))) {
                 return rc;
             }
         }
@@ -687,12 +686,6 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         }
     }
 
-    // every read of this step's ring slots (the expert kernel's and the promotion copies')
-    // is before this point on `stream`: a later upload into one of them waits for its fence
-    for (int i = 0; i < nc; ++i) {
-        if ((rc = naiwa_hip_rc(hipEventRecord(L->ring_fence[pos[i]], st)))) return rc;
-        L->ring_fenced[pos[i]] = 1;
-    }
     // the CPU pairs' sum, added last: the device waits for the job's result doorbell,
     // copies it and adds it to the resident and staged sum (src/moe/decode.rs:371-381)
     if (cpu) {
@@ -786,10 +779,6 @@ int naiwa_cached_layer_create(const naiwa_cached_layer_desc* d, naiwa_ring* ring
         delete L;
         return rc;
     }
-    L->ring_fence.assign((size_t)ring_len, nullptr);
-    L->ring_fenced.assign((size_t)ring_len, 0);
-    for (auto& ev : L->ring_fence)
-        if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) rc = NAIWA_E_DEVICE;
     for (hipEvent_t* ev : {&L->staged_done, &L->read_done, &L->ahead_done})
         if (hipEventCreateWithFlags(ev, hipEventDisableTiming) != hipSuccess) rc = NAIWA_E_DEVICE;
     if (!rc && (hipMalloc(&L->upload_flag, 256) != hipSuccess || hipMemset(L->upload_flag, 0, 256) != hipSuccess))
@@ -807,8 +796,6 @@ int naiwa_cached_layer_destroy(naiwa_cached_layer* L) {
     if (!L) return NAIWA_OK;
     (void)hipDeviceSynchronize();
     L->release_buffers();
-    for (auto ev : L->ring_fence)
-        if (ev) (void)hipEventDestroy(ev);
     for (hipEvent_t ev : {L->staged_done, L->read_done, L->ahead_done})
         if (ev) (void)hipEventDestroy(ev);
     if (L->upload_flag) (void)hipFree(L->upload_flag);

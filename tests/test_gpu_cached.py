@@ -300,11 +300,12 @@ class PageableStacks:
 @pytest.mark.parametrize("host_mem", ["pinned", "pageable", "contiguous"])
 def test_cached_layer_alternating_streams(gpu, host_mem, sync):
     """Steps alternate between two compute streams with no host synchronisation of
-    their own: a staged upload into a ring slot must wait for every earlier read of
-    that slot -- the expert kernel's and the promotion copy's -- through the slot's
-    fence alone.  Every step's output matches the oracle and every resident
-    (promoted) expert's three projections hold its bytes.  With pageable host
-    stacks the uploads are per-projection DMA copies."""
+    their own: a staged upload into a ring slot must come after every earlier read of
+    that slot -- the expert kernel's and the promotion copy's -- which the step order
+    guarantees (a step's routing waits for the previous step's last read, and the
+    host queues the uploads only after that routing).  Every step's output matches
+    the oracle and every resident (promoted) expert's three projections hold its
+    bytes.  With pageable host stacks the uploads are per-projection DMA copies."""
     nm = gpu
     E, H, I, k, usable, rows = 16, 256, 256, 4, 4, 1
     copy = nm.Stream()
