@@ -228,6 +228,20 @@ struct naiwa_cached_layer {
     std::vector<uint32_t> predicted;
     hipEvent_t read_done = nullptr;
     bool read_recorded = false;
+    // read_done is recorded when something needs it (a step on another stream, a
+    // lookahead upload into this layer's slots): recording it on last_stream then covers
+    // every read queued there so far.  Once a lookahead targets the layer it is recorded
+    // at the end of every step, so that its uploads need not wait for later work.
+    bool read_pending = false;
+    bool lookahead_target = false;
+    int record_reads() {
+        if (!read_pending) return NAIWA_OK;
+        const int rc = naiwa_hip_rc(hipEventRecord(read_done, last_stream));
+        if (rc) return rc;
+        read_pending = false;
+        read_recorded = true;
+        return NAIWA_OK;
+    }
     hipEvent_t ahead_done = nullptr;
     bool ahead_claimed = false;
 
@@ -375,6 +389,8 @@ struct naiwa_cached_layer {
         for (uint32_t e : predicted)
             if (e < (uint32_t)d.num_experts && table[e] >= 0) ++a.resident;
         const int max_swaps = swaps_per_row * rows;
+        lookahead_target = true;
+        if ((rc = record_reads())) return rc;
         const int64_t fence = read_recorded ? (int64_t)read_done : 0;
         for (uint32_t e : predicted) {
             if (e >= (uint32_t)d.num_experts) continue;
@@ -438,12 +454,11 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
 
     // one layer's steps run in order whatever stream each is queued on: the routing
     // buffers, the step inputs and the ring slots of the previous step are then free
-    if (L->have_last_stream && L->last_stream != st && L->read_recorded &&
-        (rc = naiwa_hip_rc(hipStreamWaitEvent(st, L->read_done, 0))))
-        return rc;
-    if (next && next->have_last_stream && next->last_stream != st && next->read_recorded &&
-        (rc = naiwa_hip_rc(hipStreamWaitEvent(st, next->read_done, 0))))
-        return rc;
+    for (naiwa_cached_layer* o : {L, next}) {
+        if (!o || !o->have_last_stream || o->last_stream == st) continue;
+        if ((rc = o->record_reads())) return rc;
+        if (o->read_recorded && (rc = naiwa_hip_rc(hipStreamWaitEvent(st, o->read_done, 0)))) return rc;
+    }
 
     // route on the device, then read the top-k back through the mapped doorbell: the
     // router's results (and the lookahead's prediction) are published with seq + 1 and
@@ -695,9 +710,12 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         if ((rc = naiwa_hip_rc(hipGetLastError()))) return rc;
     }
     // every read of this layer's cache slots and of its publish page is before this
-    // point on `stream` (the CPU job has finished reading x once its result arrived)
-    if ((rc = naiwa_hip_rc(hipEventRecord(L->read_done, st)))) return rc;
-    L->read_recorded = true;
+    // point on `stream` (the CPU job has finished reading x once its result arrived):
+    // read_done is recorded here, or later on this stream when first needed
+    L->last_stream = st;
+    L->have_last_stream = true;
+    L->read_pending = true;
+    if (L->lookahead_target && (rc = L->record_reads())) return rc;
 
     naiwa_cache_stats s{};
     s.hits = (uint64_t)step.hits;
@@ -709,8 +727,6 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     s.sync_waits = (uint64_t)((nc ? 1 : 0) + step.preload_waits);
     naiwa_stats_add(&s);
     if (info) *info = step;
-    L->last_stream = st;
-    L->have_last_stream = true;
     if (next) return next->prefetch_apply(L->db_host + kDbHead + 2 * n, swaps_per_row, ahead);
     return NAIWA_OK;
 }
