@@ -125,33 +125,42 @@ __attribute__((target("avx2,fma"))) inline __m256 dot32_u8(__m256i q, const floa
     return a;
 }
 
-__attribute__((target("avx2,fma"))) float dot_q4k_avx2(const uint8_t* row, const float* x, const float* sums, int k) {
+// Q4_K: the 8-lane partial dots of each 32-value sub-block are scaled by d * scale
+// and kept in one vector accumulator (one horizontal sum per row); the min terms
+// (dmin * min * group sum) are summed apart and subtracted at the end.
+__attribute__((target("avx2,fma,f16c"))) float dot_q4k_avx2(const uint8_t* row, const float* x, const float* sums,
+                                                          int k) {
     const __m256i mask = _mm256_set1_epi8(0x0F);
-    float acc = 0.0f;
+    __m256 acc = _mm256_setzero_ps();
+    float macc = 0.0f;
     for (int b = 0; b < k / 256; ++b) {
         const uint8_t* blk = row + 144 * b;
-        const float d = f16_to_f32(ld16(blk)), dmin = f16_to_f32(ld16(blk + 2));
+        const float d = _cvtsh_ss(ld16(blk)), dmin = _cvtsh_ss(ld16(blk + 2));
         const uint8_t* sc = blk + 4;
         const float* xb = x + 256 * b;
+        int s[8], m[8];
+        float ms = 0.0f;
+        for (int j = 0; j < 8; ++j) {
+            q4k_scale_min(sc, j, &s[j], &m[j]);
+            ms += (float)m[j] * sums[8 * b + j];
+        }
+        macc += dmin * ms;
         for (int c = 0; c < 4; ++c) {
             const __m256i q = _mm256_loadu_si256((const __m256i*)(blk + 16 + 32 * c));
-            const float lo = hsum8(dot32_u8(_mm256_and_si256(q, mask), xb + 64 * c));
-            const float hi = hsum8(dot32_u8(_mm256_and_si256(_mm256_srli_epi16(q, 4), mask), xb + 64 * c + 32));
-            int s0, m0, s1, m1;
-            q4k_scale_min(sc, 2 * c, &s0, &m0);
-            q4k_scale_min(sc, 2 * c + 1, &s1, &m1);
-            acc += d * ((float)s0 * lo + (float)s1 * hi) -
-                   dmin * ((float)m0 * sums[8 * b + 2 * c] + (float)m1 * sums[8 * b + 2 * c + 1]);
+            const __m256 lo = dot32_u8(_mm256_and_si256(q, mask), xb + 64 * c);
+            const __m256 hi = dot32_u8(_mm256_and_si256(_mm256_srli_epi16(q, 4), mask), xb + 64 * c + 32);
+            acc = _mm256_fmadd_ps(lo, _mm256_set1_ps(d * (float)s[2 * c]), acc);
+            acc = _mm256_fmadd_ps(hi, _mm256_set1_ps(d * (float)s[2 * c + 1]), acc);
         }
     }
-    return acc;
+    return hsum8(acc) - macc;
 }
 
-__attribute__((target("avx2,fma"))) float dot_q8_0_avx2(const uint8_t* row, const float* x, int k) {
+__attribute__((target("avx2,fma,f16c"))) float dot_q8_0_avx2(const uint8_t* row, const float* x, int k) {
     __m256 acc = _mm256_setzero_ps();
     for (int b = 0; b < k / 32; ++b) {
         const uint8_t* blk = row + 34 * b;
-        const __m256 d = _mm256_set1_ps(f16_to_f32(ld16(blk)));
+        const __m256 d = _mm256_set1_ps(_cvtsh_ss(ld16(blk)));
         const __m128i q0 = _mm_loadu_si128((const __m128i*)(blk + 2)), q1 = _mm_loadu_si128((const __m128i*)(blk + 18));
         __m256 s = _mm256_mul_ps(_mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(q0)), _mm256_loadu_ps(x + 32 * b));
         s = _mm256_fmadd_ps(_mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(_mm_srli_si128(q0, 8))), _mm256_loadu_ps(x + 32 * b + 8), s);
@@ -163,7 +172,8 @@ __attribute__((target("avx2,fma"))) float dot_q8_0_avx2(const uint8_t* row, cons
 }
 
 bool have_avx2() {
-    static const bool v = __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
+    static const bool v =
+        __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma") && __builtin_cpu_supports("f16c");
     return v;
 }
 #endif
