@@ -668,3 +668,27 @@ def test_upload_waits_and_paths_give_the_same_bits(gpu):
             assert np.array_equal(ye.view(np.uint32), yp.view(np.uint32)), key
             assert ce == cp, key
     assert sum(r[3] for r in first) > 0 and sum(r[2] for r in first) > 0
+
+
+def test_lookahead_into_a_layer_of_another_top_k_is_refused(gpu):
+    """forward_ahead publishes the next layer's prediction in this layer's top_k
+    columns, so a next layer with another top_k is refused with NAIWA_E_INVALID
+    before any state changes; the same layer still runs a plain forward after it."""
+    nm = gpu
+    E, H, I, usable, rows = 16, 256, 256, 4, 1
+    copy, stream = nm.Stream(), nm.Stream()
+    ring0, ring1 = nm.policy.StagingRing(), nm.policy.StagingRing()
+    l0, banks0, stacks0, host0 = make_layer(nm, 2900, E, H, I, 4, usable, ring0, copy)
+    l1, banks1, stacks1, host1 = make_layer(nm, 2910, E, H, I, 2, usable, ring1, copy)
+    x = S.activations_bf16(2901, rows, H)
+    xd = nm.DeviceBuffer.from_array(x)
+    out = nm.DeviceBuffer(rows * H * 4)
+    before = _policy_state(l0, ring0)
+    with pytest.raises(nm.NaiwaError) as e:
+        l0.forward_ahead(l1, xd, rows, out, lookahead_swaps=2, stream=stream.handle)
+    assert e.value.rc == nm.E_INVALID
+    assert _policy_state(l0, ring0) == before
+    l0.forward(xd, rows, out, pcie_frac=1.0, stream=stream.handle)
+    stream.sync()
+    _, _, want = oracle_step(host0, x, E, 4, H)
+    assert S.max_rel_err(out.download(np.float32).reshape(rows, H), want) < TOL

@@ -237,3 +237,26 @@ def test_plan_rejects_bad_ids_without_changing_state():
         c.plan(np.array([[1, 9]], dtype=np.uint32), np.ones((1, 2), np.float32), ring.length, 1.0)
     assert e.value.rc == E_BAD_ID
     assert _state(c, ring) == before
+
+
+def test_cached_layer_rejects_overlapping_host_stacks():
+    """naiwa_cached_layer_create refuses a negative host_expert_stride, or a positive
+    one shorter than a projection (the experts would overlap in the host stacks), with
+    NAIWA_E_INVALID before it touches a device: every pointer here is made up."""
+    import ctypes as C
+    from naiwa_moe import Q4_K
+    from naiwa_moe._lib import Bank, CachedLayerDesc, E_INVALID, lib
+    L = lib()
+    E, H, I, usable = 8, 256, 256, 2
+    ring = P.StagingRing()
+    proj = L.naiwa_projection_bytes(Q4_K, I, H)                  # 36,864 B a projection here
+    stride = (proj + 255) // 256 * 256
+    fake = 0x7f0000000000
+    bank = lambda n, k: Bank(fake, stride, usable + ring.length, n, k, Q4_K)
+    for host_stride in (-1, proj - 16, 1):
+        d = CachedLayerDesc(fake, None, bank(I, H), bank(I, H), bank(H, I), fake, fake, fake, E, 2, H, I, usable,
+                            0, 0, host_stride)
+        h = C.c_void_p()
+        rc = L.naiwa_cached_layer_create(C.byref(d), ring._h, ring.length, 0, C.byref(h))
+        assert rc == E_INVALID, (host_stride, rc)
+        assert not h.value
