@@ -1052,7 +1052,7 @@ def run_prefill(args) -> int:
     tflops = flop / (ms / 1e3) / 1e12
     tok_s = tokens / (ms / 1e3)
     log(f"prefill: {ms:.2f} ms per {tokens}-token prefill, {tok_s:.0f} tok/s, {tflops:.1f} TFLOP/s "
-        f"({tflops / 2500 * 100:.1f}% of 2.5 PFLOP/s f16 dense)")
+        f"({tflops / 2500 * 100:.1f}% of 2.5 PFLOP/s bf16 dense)")
     # The grouped call's roofline: a 512-token chunk's 3072 routed + 1024 shared pairs touch
     # every expert of the layer (66 x 6,307,840 B of weights) for 70.9 GFLOP, 170 flop/B,
     # below the ridge of 2.5 PFLOP/s / 8 TB/s = 312 flop/B: the call is HBM-bound.  Each
