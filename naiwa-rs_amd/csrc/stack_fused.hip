@@ -21,7 +21,7 @@
 //              done word, reads all h once, dots every (feature, pair), adds the
 //              pairs of each token in ascending slot order (no atomics),
 //              applies the residual, publishes its x chunk and its int64 partial
-//              sums of the next layer's router logits; 32 leader workgroups add
+//              sums of the next layer's router logits; 16 leader workgroups add
 //              every chunk's partials for their experts and publish the logits.
 //
 // There is no grid barrier.  Every value one workgroup hands to another (x,
@@ -63,7 +63,7 @@ constexpr int kMaxRows = 8;               // tokens per step served by this kern
 constexpr int kMaxK = 8;                  // routed experts per token
 constexpr int kMaxPairs = kMaxRows * kMaxK;
 constexpr int kMaxE = 256;
-constexpr int kLeaders = 32;              // workgroups that add the router partials
+constexpr int kLeaders = 16;              // workgroups that add the router partials
 constexpr int kChunk = NAIWA_ROUTER_CHUNK; // output features per phase-C chunk
 constexpr int kMaxChunks = 4;             // chunks per workgroup
 constexpr int kCPairs = 32;               // h vectors staged per phase-C pass, at most
