@@ -34,26 +34,31 @@ bool bank_ok(const naiwa_bank& b, int n, int k, int min_slots) {
 }
 
 // Doorbell layout of a layer's routing read-back (fine-grained mapped host memory):
-// [seq u32][15 pad words][ids n][weights n][predicted ids n].
+// [16 u32 header words: word 1 counts the staged-upload waits that ran out]
+// [tagged u64 words: ids n | weights n | predicted ids n].  Each payload word is
+// tag << 32 | value with the step's tag: the host waits until every word it needs
+// carries the tag, so the words need no ordering among themselves and the device
+// publishes them without a system-scope fence (which writes back the L2 and cost
+// ~2.5 us a publish).
 constexpr int kDbHead = 16;
+// Device words of the one-token routing kernel: tagged logits of two routers, then
+// its arrival counter.
+constexpr int kRouteWords = 2 * NAIWA_ROUTER_MAX_E;
 
-// The routing of one step into the mapped doorbell, then seq + 1 behind a system-scope
-// fence: the host spins on seq instead of synchronising the stream (the reference's
-// TopkDoorbell publish, src/doorbell/d2h/topk.rs:20-125).
-__global__ void __launch_bounds__(256)
-routing_publish_kernel(uint32_t* db, const uint32_t* ids, const float* w, int n, const uint32_t* pred, int npred) {
-    volatile uint32_t* out = db + kDbHead;
+typedef __attribute__((address_space(1))) uint64_t gu64;
+
+// The routing of one step (several tokens) into the mapped doorbell as tagged words
+// (the reference's TopkDoorbell publish, src/doorbell/d2h/topk.rs:20-125).
+__global__ void __launch_bounds__(256) routing_publish_kernel(uint64_t* pay, uint32_t tag, const uint32_t* ids,
+                                                              const float* w, int n, const uint32_t* pred, int npred) {
+    const uint64_t t = (uint64_t)tag << 32;
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        out[i] = ids[i];
-        out[n + i] = __float_as_uint(w[i]);
+        __hip_atomic_store((gu64*)(pay + i), t | ids[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store((gu64*)(pay + n + i), t | __float_as_uint(w[i]), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
     }
-    for (int i = threadIdx.x; i < npred; i += blockDim.x) out[2 * n + i] = pred[i];
-    __threadfence_system();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t cur = __hip_atomic_load(db, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        __hip_atomic_store(db, cur + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
+    for (int i = threadIdx.x; i < npred; i += blockDim.x)
+        __hip_atomic_store((gu64*)(pay + 2 * n + i), t | pred[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // The step's inputs (slot ids and split weights, nwords words) from mapped host memory
@@ -71,7 +76,9 @@ __global__ void __launch_bounds__(64)
 staged_wait_kernel(const uint32_t* flag, uint32_t target, uint64_t limit_ticks, uint32_t* fail) {
     if (threadIdx.x != 0) return;
     const uint64_t t0 = wall_clock64();
-    while (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) < target) {
+    // relaxed spin loads (an acquire load invalidates the L2 on every try); the kernels
+    // queued behind this one acquire at their start
+    while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) < target) {
         if (wall_clock64() - t0 > limit_ticks) {
             const uint32_t n = __hip_atomic_load(fail, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             __hip_atomic_store(fail, n + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -140,15 +147,22 @@ constexpr int64_t kRouteWaitUs = 10 * 1000 * 1000;
 // a sleep costs the OS timer slack, ~50 us or more, on every layer of every token.
 constexpr int64_t kRouteSpinUs = 2000;
 
-// *word >= target: spin (pause) for up to kRouteSpinUs, then sleep-poll every 20 us,
-// until kRouteWaitUs have passed (NAIWA_E_TIMEOUT).
-int wait_routing(const uint32_t* word, uint32_t target) {
+// Every one of the nw tagged words carries tag: spin (pause) for up to kRouteSpinUs,
+// then sleep-poll every 20 us, until kRouteWaitUs have passed (NAIWA_E_TIMEOUT).  The
+// words' values (low halves) then go to out.
+int wait_routing(const uint64_t* words, int nw, uint32_t tag, uint32_t* out) {
     using clock = std::chrono::steady_clock;
     const auto t0 = clock::now();
     const auto spin_end = t0 + std::chrono::microseconds(kRouteSpinUs);
     const auto deadline = t0 + std::chrono::microseconds(kRouteWaitUs);
+    int have = 0; // words[0..have) carry the tag
     for (uint32_t i = 0;; ++i) {
-        if (naiwa_host_load_acquire_u32(word) >= target) return NAIWA_OK;
+        while (have < nw) {
+            const uint64_t v = __atomic_load_n(words + have, __ATOMIC_ACQUIRE);
+            if ((uint32_t)(v >> 32) != tag) break;
+            out[have++] = (uint32_t)v;
+        }
+        if (have == nw) return NAIWA_OK;
         if ((i & 63) == 0) {
             const auto now = clock::now();
             if (now >= deadline) return NAIWA_E_TIMEOUT;
@@ -188,10 +202,14 @@ struct naiwa_cached_layer {
     float* wsplit_h = nullptr;     // host view: weights of the cache pairs | of the staged pairs
     float* wsplit_dev = nullptr;
     int last_rows = 0;
-    // routing read-back doorbell: host view, device view, publishes so far
+    // routing read-back doorbell: host view, device view, publishes so far (the tag of
+    // the latest); the values read back (ids | weights | predicted ids); the one-token
+    // routing kernel's tagged logits and arrival counter
     uint32_t* db_host = nullptr;
     uint32_t* db_dev = nullptr;
     uint32_t db_seq = 0;
+    std::vector<uint32_t> route_h;
+    uint64_t* rwords_dev = nullptr;
     // the stream of the previous step: a step on another stream waits for read_done first
     hipStream_t last_stream = nullptr;
     bool have_last_stream = false;
@@ -247,6 +265,8 @@ struct naiwa_cached_layer {
 
     void release_buffers() {
         if (route_dev_base) (void)hipFree(route_dev_base);
+        if (rwords_dev) (void)hipFree(rwords_dev);
+        rwords_dev = nullptr;
         if (in_dev_base) (void)hipFree(in_dev_base);
         in_map_base = nullptr;
         if (db_host) (void)doorbell_free_host(db_host);
@@ -255,6 +275,7 @@ struct naiwa_cached_layer {
         if (in_h_base) (void)doorbell_free_host(in_h_base);
         if (slots_h) (void)hipHostFree(slots_h);
         route_dev_base = in_dev_base = in_h_base = nullptr;
+        route_h.clear();
         views(0);
         if (pred_ids_dev) (void)hipFree(pred_ids_dev);
         if (pred_w_dev) (void)hipFree(pred_w_dev);
@@ -284,7 +305,9 @@ struct naiwa_cached_layer {
         void* xp = nullptr;
         const size_t xn = (size_t)rows * d.hidden;
         if (hipMalloc(&route_dev_base, 2 * n * 4) != hipSuccess || hipMalloc(&in_dev_base, 3 * n * 4) != hipSuccess ||
-            doorbell_alloc_mapped(&db, (kDbHead + 3 * n) * 4) != NAIWA_OK ||
+            hipMalloc(&rwords_dev, (kRouteWords + 1) * 8) != hipSuccess ||
+            hipMemset(rwords_dev, 0, (kRouteWords + 1) * 8) != hipSuccess ||
+            doorbell_alloc_mapped(&db, kDbHead * 4 + 3 * n * 8) != NAIWA_OK ||
             doorbell_alloc_mapped(&in, 3 * n * 4) != NAIWA_OK || hipHostMalloc(&slots_h, n * 4, 0) != hipSuccess ||
             hipMalloc(&pred_ids_dev, n * 4) != hipSuccess || hipMalloc(&pred_w_dev, n * 4) != hipSuccess ||
             hipHostMalloc(&pred_ids_h, n * 4, 0) != hipSuccess ||
@@ -314,6 +337,7 @@ struct naiwa_cached_layer {
         db_seq = 0;
         upload_fail_seen = 0;
         xpub_seq = 0;
+        route_h.assign(3 * n, 0u);
         cap_rows = rows;
         return NAIWA_OK;
     }
@@ -322,8 +346,8 @@ struct naiwa_cached_layer {
     void views(int n) {
         ids_dev = route_dev_base;
         w_dev = route_dev_base ? (float*)(route_dev_base + n) : nullptr;
-        ids_h = db_host ? db_host + kDbHead : nullptr;
-        w_h = db_host ? (float*)(db_host + kDbHead + n) : nullptr;
+        ids_h = route_h.empty() ? nullptr : route_h.data();
+        w_h = route_h.empty() ? nullptr : (float*)(route_h.data() + n);
         slots_dev = in_dev_base;
         wsplit_dev = in_dev_base ? (float*)(in_dev_base + n) : nullptr;
         slots_up = in_h_base;
@@ -461,32 +485,35 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     }
 
     // route on the device, then read the top-k back through the mapped doorbell: the
-    // router's results (and the lookahead's prediction) are published with seq + 1 and
-    // the host spins on seq, with no stream synchronisation (the routing round trip)
-    if (rows == 1 && !next) {
-        // one token and no prediction to publish: the top-k block publishes itself
-        rc = naiwa_router_topk_publish(x, NAIWA_BF16, d.router, d.router_bias, d.hidden, d.num_experts, k, d.mode,
-                                       L->ids_dev, L->w_dev, L->db_dev, L->db_dev + kDbHead, stream);
+    // router's results (and the lookahead's prediction) are published as words tagged
+    // with the step's sequence number and the host spins on the tags, with no stream
+    // synchronisation (the routing round trip)
+    const uint32_t tag = ++L->db_seq;
+    uint64_t* pay_dev = reinterpret_cast<uint64_t*>(L->db_dev + kDbHead);
+    const int nwords = 2 * n + (next ? n : 0);
+    if (rows == 1 && (!next || next->d.top_k == k)) {
+        // one token: both routers' logits (the layer's, and the next layer's for the
+        // prediction), the top ks and the publish in one launch
+        rc = naiwa_route_one_publish(x, NAIWA_BF16, d.hidden, d.router, d.router_bias, d.num_experts, k, d.mode,
+                                     L->ids_dev, L->w_dev, next ? next->d.router : nullptr,
+                                     next ? next->d.router_bias : nullptr, next ? next->d.num_experts : 0, k,
+                                     NAIWA_ROUTE_TOPK_SOFTMAX, next ? next->pred_ids_dev : nullptr,
+                                     next ? next->pred_w_dev : nullptr, tag, L->rwords_dev,
+                                     reinterpret_cast<unsigned*>(L->rwords_dev + kRouteWords), pay_dev,
+                                     naiwa_doorbell_wait_limit_ticks(), stream);
         if (rc) return rc;
-    } else if (rows == 1 && next->d.top_k == k) {
-        // one token with the prediction: both routers' logits in one launch, both
-        // top-ks and the publish in another (five launches as separate calls)
-        rc = naiwa_router_topk_pair_publish(x, NAIWA_BF16, d.hidden, d.router, d.router_bias, d.num_experts, k,
-                                            d.mode, L->ids_dev, L->w_dev, next->d.router, next->d.router_bias,
-                                            next->d.num_experts, k, NAIWA_ROUTE_TOPK_SOFTMAX, next->pred_ids_dev,
-                                            next->pred_w_dev, L->db_dev, L->db_dev + kDbHead, stream);
-        if (rc) return rc;
-        next->pred_rows = rows;
+        if (next) next->pred_rows = rows;
     } else {
         rc = naiwa_router_topk_biased(x, NAIWA_BF16, d.router, d.router_bias, rows, d.hidden, d.num_experts, k,
                                       d.mode, L->ids_dev, L->w_dev, nullptr, stream);
         if (!rc && next) rc = next->predict_launch(x, rows, stream);
         if (rc) return rc;
-        routing_publish_kernel<<<1, 256, 0, st>>>(L->db_dev, L->ids_dev, L->w_dev, n,
+        routing_publish_kernel<<<1, 256, 0, st>>>(pay_dev, tag, L->ids_dev, L->w_dev, n,
                                                   next ? next->pred_ids_dev : nullptr, next ? n : 0);
         if ((rc = naiwa_hip_rc(hipGetLastError()))) return rc;
     }
-    if ((rc = wait_routing(L->db_host, ++L->db_seq))) return rc;
+    if ((rc = wait_routing(reinterpret_cast<const uint64_t*>(L->db_host + kDbHead), nwords, tag, L->route_h.data())))
+        return rc;
     L->last_rows = rows;
 
     // the previous step's staged-upload wait ran out (poll mode; its kernels ran before
@@ -727,7 +754,7 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
     s.sync_waits = (uint64_t)((nc ? 1 : 0) + step.preload_waits);
     naiwa_stats_add(&s);
     if (info) *info = step;
-    if (next) return next->prefetch_apply(L->db_host + kDbHead + 2 * n, swaps_per_row, ahead);
+    if (next) return next->prefetch_apply(L->route_h.data() + 2 * n, swaps_per_row, ahead);
     return NAIWA_OK;
 }
 

@@ -52,6 +52,13 @@ __device__ __forceinline__ void store_release_sys(uint32_t* p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+// Spin loads are relaxed (an acquire load invalidates the L2 on every try); the
+// wait ends with one acquire fence.
+__device__ __forceinline__ uint32_t load_relaxed_sys(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void acquire_sys() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, ""); }
+
 // Every thread fences its own payload stores at system scope before the
 // block barrier, then one thread bumps the counter with a release store.
 __device__ __forceinline__ void publish_bump(uint32_t* d_seq) {
@@ -87,7 +94,7 @@ doorbell_wait_copy_f32_kernel(const uint32_t* d_seq, uint32_t target, const vola
     if (threadIdx.x == 0) {
         const uint64_t t0 = wall_clock64();
         int reached = 1;
-        while (load_acquire_sys(d_seq) < target) {
+        while (load_relaxed_sys(d_seq) < target) {
             if (wall_clock64() - t0 > limit_ticks) {
                 reached = 0;
                 break;
@@ -108,9 +115,10 @@ doorbell_wait_copy_f32_kernel(const uint32_t* d_seq, uint32_t target, const vola
 }
 
 // The persistent-wave doorbell: one wave answers `count` host rings in a row.
-// For ring i it waits (bounded) until *d_seq >= first + i, then release-stores
-// first + i to *d_ack.  A wait that runs past its limit counts a timeout and
-// ends the kernel, so the wave always exits.
+// For ring i it waits (bounded) until *d_seq >= first + i, then stores first + i
+// to *d_ack (system scope; the wave writes nothing else, so the store needs no
+// release fence, which would write back the L2 on every ring).  A wait that runs
+// past its limit counts a timeout and ends the kernel, so the wave always exits.
 __global__ void __launch_bounds__(64)
 doorbell_poll_serve_kernel(const uint32_t* d_seq, uint32_t* d_ack, uint32_t first, uint32_t count,
                            uint64_t limit_ticks) {
@@ -118,13 +126,14 @@ doorbell_poll_serve_kernel(const uint32_t* d_seq, uint32_t* d_ack, uint32_t firs
     for (uint32_t i = 0; i < count; ++i) {
         const uint32_t target = first + i;
         const uint64_t t0 = wall_clock64();
-        while (load_acquire_sys(d_seq) < target) {
+        while (load_relaxed_sys(d_seq) < target) {
             if (wall_clock64() - t0 > limit_ticks) {
                 atomicAdd(&g_doorbell_timeouts, 1u);
                 return;
             }
         }
-        store_release_sys(d_ack, target);
+        acquire_sys();
+        __hip_atomic_store(d_ack, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 
@@ -135,20 +144,23 @@ __global__ void __launch_bounds__(64)
 doorbell_poll_wait_kernel(const uint32_t* d_flag, uint32_t target, uint64_t limit_ticks) {
     if (threadIdx.x != 0) return;
     const uint64_t t0 = wall_clock64();
-    while (load_acquire_sys(d_flag) < target) {
+    while (load_relaxed_sys(d_flag) < target) {
         if (wall_clock64() - t0 > limit_ticks) {
             atomicAdd(&g_doorbell_timeouts, 1u);
             return;
         }
         __builtin_amdgcn_s_sleep(1);
     }
+    acquire_sys();
 }
 
 // Raise *d_flag to value once the work queued before it on the stream is done.
+// Stream order starts this kernel after that work has completed, and each kernel's
+// writes are released when it ends, so the store needs no fence of its own (a
+// system-scope fence writes back the L2: ~2.5 us).
 __global__ void __launch_bounds__(64) doorbell_poll_signal_kernel(uint32_t* d_flag, uint32_t value) {
     if (threadIdx.x != 0) return;
-    __threadfence_system();
-    store_release_sys(d_flag, value);
+    __hip_atomic_store(d_flag, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 } // namespace

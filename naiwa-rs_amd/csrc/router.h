@@ -172,18 +172,14 @@ __device__ inline void naiwa_wave_topk(const float* l, int E, int k, int mode, u
     }
 }
 
-// naiwa_router_topk_biased for one row, publishing the routing read-back from the
-// top-k block: ids and weights to pay[0..k) and pay[k..2k) of mapped host memory,
-// then *db_seq + 1 with a system-scope release (the host spins on db_seq).
-int naiwa_router_topk_publish(const void* x, int x_dtype, const float* W, const float* bias, int H, int E, int k,
-                              int mode, uint32_t* ids_out, float* w_out, uint32_t* db_seq, uint32_t* pay,
-                              int64_t stream);
-
-// One row under two routers in two launches (both logits, then both top-ks and one
-// publish): the layer's routing (ids1, w1 at pay[0..k1) and pay[k1..2k1)) and the
-// lookahead's prediction of the next layer (ids2 at pay[2k1..2k1+k2)), then *db_seq + 1
-// with a system-scope release.
-int naiwa_router_topk_pair_publish(const void* x, int x_dtype, int H, const float* W1, const float* b1, int E1,
-                                   int k1, int mode1, uint32_t* ids1, float* w1, const float* W2, const float* b2,
-                                   int E2, int k2, int mode2, uint32_t* ids2, float* w2, uint32_t* db_seq,
-                                   uint32_t* pay, int64_t stream);
+// One token's routing read-back in one launch: the logits of router 1 (and of router 2
+// when W2 is given: the next layer's, for the lookahead's prediction), the top k of
+// each into ids/w on the device, and tagged words (tag << 32 | value) in mapped host
+// memory: ids1 at pay[0..k1), weights1 at pay[k1..2 k1), ids2 at pay[2 k1..2 k1 + k2).
+// words: E1 + E2 device words for the tagged logits; counter: a device word that
+// starts at 0 and is back at 0 after each launch.  Launches that share words or
+// counter must not overlap, and tag must differ from the previous launch's.
+int naiwa_route_one_publish(const void* x, int x_dtype, int H, const float* W1, const float* b1, int E1, int k1,
+                            int mode1, uint32_t* ids1, float* w1, const float* W2, const float* b2, int E2, int k2,
+                            int mode2, uint32_t* ids2, float* w2, uint32_t tag, uint64_t* words, unsigned* counter,
+                            uint64_t* pay, uint64_t limit_ticks, int64_t stream);

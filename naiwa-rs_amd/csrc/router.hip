@@ -73,9 +73,10 @@ router_logits_rows_kernel(const void* x, int x_bf16, const float* W, const float
 // 8-feature chunks i, i + 256, ..., issuing up to kLogitPer chunks' loads at once;
 // the waves' sums meet in LDS.  The chunk values are int64 fixed point, so their
 // sum is the same in any order.
-// logit[t, e] by the whole block (part: kLogitThreads / 64 words of LDS).
-__device__ inline void logit_block(const void* x, int x_bf16, const float* W, const float* bias, int H, int E, int e,
-                                   int t, float* logits, long long* part) {
+// logit[t, e] by the whole block, returned in thread 0 (part: kLogitThreads / 64
+// words of LDS).
+__device__ inline float logit_value(const void* x, int x_bf16, const float* W, const float* bias, int H, int e, int t,
+                                    long long* part) {
     const int tid = threadIdx.x;
     const int nchunks = H / NAIWA_ROUTER_CHUNK;
     const float* wr = W + (int64_t)e * H;
@@ -96,37 +97,29 @@ __device__ inline void logit_block(const void* x, int x_bf16, const float* W, co
     acc = naiwa_wave_sum_i64(acc);
     if ((tid & 63) == 0) part[tid >> 6] = acc;
     __syncthreads();
+    float v = 0.0f;
     if (tid == 0) {
         long long sum = 0;
 #pragma unroll
         for (int i = 0; i < kLogitThreads / 64; ++i) sum += part[i];
-        logits[(int64_t)t * E + e] = naiwa_router_fix_to_f32(sum) + (bias ? bias[e] : 0.0f);
+        v = naiwa_router_fix_to_f32(sum) + (bias ? bias[e] : 0.0f);
     }
     __syncthreads(); // part is reused by the next call
+    return v;
 }
 
 __global__ void __launch_bounds__(kLogitThreads)
 router_logits_kernel(const void* x, int x_bf16, const float* W, const float* bias, int rows, int H, int E,
                      float* logits) {
     __shared__ long long part[kLogitThreads / 64];
-    for (int t = blockIdx.y; t < rows; t += gridDim.y)
-        logit_block(x, x_bf16, W, bias, H, E, blockIdx.x, t, logits, part);
-}
-
-// One row under two routers (a layer's, and the next layer's for the lookahead's
-// prediction): blocks [0, E1) take W1's experts, blocks [E1, E1 + E2) W2's.
-__global__ void __launch_bounds__(kLogitThreads)
-router_logits_pair_kernel(const void* x, int x_bf16, int H, const float* W1, const float* b1, int E1, float* l1,
-                          const float* W2, const float* b2, int E2, float* l2) {
-    __shared__ long long part[kLogitThreads / 64];
-    const int b = blockIdx.x;
-    if (b < E1)
-        logit_block(x, x_bf16, W1, b1, H, E1, b, 0, l1, part);
-    else
-        logit_block(x, x_bf16, W2, b2, H, E2, b - E1, 0, l2, part);
+    for (int t = blockIdx.y; t < rows; t += gridDim.y) {
+        const float v = logit_value(x, x_bf16, W, bias, H, blockIdx.x, t, part);
+        if (threadIdx.x == 0) logits[(int64_t)t * E + blockIdx.x] = v;
+    }
 }
 
 constexpr int kTopkThreads = 256;
+static_assert(kTopkThreads == kLogitThreads, "the one-token routing kernel computes a logit per block");
 
 __global__ void __launch_bounds__(kTopkThreads)
 router_topk_kernel(const float* logits, int E, int k, int mode, uint32_t* ids, float* w, int ld) {
@@ -145,120 +138,132 @@ router_topk_kernel(const float* logits, int E, int k, int mode, uint32_t* ids, f
     }
 }
 
-// router_topk_kernel for one row with the routing read-back published from the same
-// block: ids and weights also go to the mapped payload (ids at pay[0..k), weights at
-// pay[k..2k)), then the sequence word goes up by one with a system-scope release --
-// the reference's TopkDoorbell publish (src/doorbell/d2h/topk.rs:20-125) without a
-// launch of its own.
-__global__ void __launch_bounds__(kTopkThreads)
-router_topk_publish_kernel(const float* logits, int E, int k, int mode, uint32_t* ids, float* w, uint32_t* db_seq,
-                           uint32_t* pay) {
-    __shared__ float l[NAIWA_ROUTER_MAX_E];
-    __shared__ int rank_tmp[NAIWA_ROUTER_MAX_E];
-    __shared__ float ex_tmp[NAIWA_ROUTER_MAX_E];
-    __shared__ uint32_t ids_s[NAIWA_ROUTER_MAX_K];
-    __shared__ float w_s[NAIWA_ROUTER_MAX_K];
-    for (int e = threadIdx.x; e < E; e += kTopkThreads) l[e] = logits[e];
-    __syncthreads();
-    naiwa_block_topk<kTopkThreads>(l, E, k, mode, ids_s, w_s, rank_tmp, ex_tmp);
-    if (threadIdx.x < k) {
-        const uint32_t id = ids_s[threadIdx.x];
-        const float wv = w_s[threadIdx.x];
-        ids[threadIdx.x] = id;
-        w[threadIdx.x] = wv;
-        volatile uint32_t* out = pay;
-        out[threadIdx.x] = id;
-        out[k + threadIdx.x] = __float_as_uint(wv);
-    }
-    __threadfence_system();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t cur = __hip_atomic_load(db_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        __hip_atomic_store(db_seq, cur + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
-}
+typedef __attribute__((address_space(1))) uint64_t gu64;
+__device__ __forceinline__ uint64_t tagged_word(uint32_t tag, uint32_t v) { return ((uint64_t)tag << 32) | v; }
 
-// The top k of both rows of router_logits_pair_kernel in one block, then one publish
-// of the routing read-back: ids1 at pay[0..k1), weights1 at pay[k1..2k1), ids2 at
-// pay[2k1..2k1+k2), and the sequence word up by one with a system-scope release.
-__global__ void __launch_bounds__(kTopkThreads)
-router_topk_pair_publish_kernel(const float* l1, int E1, int k1, int mode1, uint32_t* ids1, float* w1,
-                                const float* l2, int E2, int k2, int mode2, uint32_t* ids2, float* w2,
-                                uint32_t* db_seq, uint32_t* pay) {
-    __shared__ float l[NAIWA_ROUTER_MAX_E];
+// One token's routing in one launch, under one router or two (a layer's, and the next
+// layer's for the lookahead's prediction), published to the host without a fence.
+// Block b computes logit b of the routers' concatenated experts and stores it as a
+// tagged word (tag << 32 | f32 bits) in words[b]; the block that arrives last on the
+// wrapping counter (atomicInc, back to 0 after the last arrival) loads every logit,
+// waiting (bounded) until each carries the tag, and ranks them.  The results go to
+// the device outputs and, as tagged words, to the mapped payload: ids at pay[0..k0),
+// weights at pay[k0..2 k0), the prediction's ids at pay[2 k0..2 k0 + k1).  Every
+// word carries its own tag, so the host needs no ordering between them: it waits
+// until all of them carry the step's tag.  A wait that runs out publishes nothing
+// (the host's own bounded wait then reports the step).
+struct RouteOne {
+    const void* x;
+    int x_bf16, H, nr;
+    const float* W[2];
+    const float* bias[2];
+    int E[2], k[2], mode[2];
+    uint32_t* ids[2];
+    float* w[2];
+    uint32_t tag;
+    uint64_t* words;
+    unsigned* counter;
+    uint64_t* pay;
+    uint64_t limit_ticks;
+};
+
+__global__ void __launch_bounds__(kTopkThreads) router_route_one_kernel(RouteOne a) {
+    __shared__ long long part[kLogitThreads / 64];
+    __shared__ float l[2 * NAIWA_ROUTER_MAX_E];
     __shared__ int rank_tmp[NAIWA_ROUTER_MAX_E];
     __shared__ float ex_tmp[NAIWA_ROUTER_MAX_E];
     __shared__ uint32_t ids_s[NAIWA_ROUTER_MAX_K];
     __shared__ float w_s[NAIWA_ROUTER_MAX_K];
-    volatile uint32_t* out = pay;
-    for (int e = threadIdx.x; e < E1; e += kTopkThreads) l[e] = l1[e];
-    __syncthreads();
-    naiwa_block_topk<kTopkThreads>(l, E1, k1, mode1, ids_s, w_s, rank_tmp, ex_tmp);
-    if (threadIdx.x < k1) {
-        ids1[threadIdx.x] = ids_s[threadIdx.x];
-        w1[threadIdx.x] = w_s[threadIdx.x];
-        out[threadIdx.x] = ids_s[threadIdx.x];
-        out[k1 + threadIdx.x] = __float_as_uint(w_s[threadIdx.x]);
+    __shared__ int last, ok;
+    const int b = blockIdx.x, tid = threadIdx.x, nb = (int)gridDim.x;
+    const int r = b < a.E[0] ? 0 : 1, e = b - (r ? a.E[0] : 0);
+    const float v = logit_value(a.x, a.x_bf16, a.W[r], a.bias[r], a.H, e, 0, part);
+    if (tid == 0) {
+        __hip_atomic_store((gu64*)(a.words + b), tagged_word(a.tag, __float_as_uint(v)), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        last = atomicInc(a.counter, (unsigned)(nb - 1)) == (unsigned)(nb - 1);
+        ok = 1;
     }
-    __syncthreads(); // l, ids_s and w_s are reused
-    for (int e = threadIdx.x; e < E2; e += kTopkThreads) l[e] = l2[e];
     __syncthreads();
-    naiwa_block_topk<kTopkThreads>(l, E2, k2, mode2, ids_s, w_s, rank_tmp, ex_tmp);
-    if (threadIdx.x < k2) {
-        ids2[threadIdx.x] = ids_s[threadIdx.x];
-        w2[threadIdx.x] = w_s[threadIdx.x];
-        out[2 * k1 + threadIdx.x] = ids_s[threadIdx.x];
+    if (!last) return;
+    const uint64_t t0 = wall_clock64();
+    for (int i = tid; i < nb; i += kTopkThreads) {
+        uint64_t wd;
+        while ((uint32_t)((wd = __hip_atomic_load((gu64*)(a.words + i), __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT)) >> 32) != a.tag) {
+            if (wall_clock64() - t0 > a.limit_ticks) {
+                ok = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        l[i] = __uint_as_float((uint32_t)wd);
     }
-    __threadfence_system();
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t cur = __hip_atomic_load(db_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        __hip_atomic_store(db_seq, cur + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (!ok) return;
+    for (int q = 0; q < a.nr; ++q) {
+        naiwa_block_topk<kTopkThreads>(l + (q ? a.E[0] : 0), a.E[q], a.k[q], a.mode[q], ids_s, w_s, rank_tmp, ex_tmp);
+        if (tid < a.k[q]) {
+            const uint32_t id = ids_s[tid];
+            const float wv = w_s[tid];
+            a.ids[q][tid] = id;
+            a.w[q][tid] = wv;
+            if (q == 0) {
+                __hip_atomic_store((gu64*)(a.pay + tid), tagged_word(a.tag, id), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store((gu64*)(a.pay + a.k[0] + tid), tagged_word(a.tag, __float_as_uint(wv)),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            } else {
+                __hip_atomic_store((gu64*)(a.pay + 2 * a.k[0] + tid), tagged_word(a.tag, id), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+        }
+        __syncthreads(); // ids_s, w_s and the ranking scratch are reused
     }
 }
 
 } // namespace
 
-int naiwa_router_topk_publish(const void* x, int x_dtype, const float* W, const float* bias, int H, int E, int k,
-                              int mode, uint32_t* ids_out, float* w_out, uint32_t* db_seq, uint32_t* pay,
-                              int64_t stream) {
+int naiwa_route_one_publish(const void* x, int x_dtype, int H, const float* W1, const float* b1, int E1, int k1,
+                            int mode1, uint32_t* ids1, float* w1, const float* W2, const float* b2, int E2, int k2,
+                            int mode2, uint32_t* ids2, float* w2, uint32_t tag, uint64_t* words, unsigned* counter,
+                            uint64_t* pay, uint64_t limit_ticks, int64_t stream) {
     if (x_dtype != NAIWA_BF16 && x_dtype != NAIWA_F32) return NAIWA_E_UNSUPPORTED;
-    if (mode < NAIWA_ROUTE_SOFTMAX_TOPK_RENORM || mode > NAIWA_ROUTE_SOFTMAX_TOPK)
-        return NAIWA_E_UNSUPPORTED;
-    if (H <= 0 || H % NAIWA_ROUTER_CHUNK || E <= 0 || E > NAIWA_ROUTER_MAX_E || k <= 0 || k > E ||
-        k > NAIWA_ROUTER_MAX_K)
+    const int nr = W2 ? 2 : 1;
+    const int mode[2] = {mode1, mode2}, E[2] = {E1, E2}, k[2] = {k1, k2};
+    for (int q = 0; q < nr; ++q) {
+        if (mode[q] < NAIWA_ROUTE_SOFTMAX_TOPK_RENORM || mode[q] > NAIWA_ROUTE_SOFTMAX_TOPK)
+            return NAIWA_E_UNSUPPORTED;
+        if (E[q] <= 0 || E[q] > NAIWA_ROUTER_MAX_E || k[q] <= 0 || k[q] > E[q] || k[q] > NAIWA_ROUTER_MAX_K)
+            return NAIWA_E_INVALID;
+    }
+    if (H <= 0 || H % NAIWA_ROUTER_CHUNK || !x || !W1 || !ids1 || !w1 || !words || !counter || !pay)
         return NAIWA_E_INVALID;
-    if (!x || !W || !ids_out || !w_out || !db_seq || !pay) return NAIWA_E_INVALID;
-    hipStream_t st = (hipStream_t)stream;
-    int rc = 0;
-    float* logits = (float*)naiwa_scratch(NAIWA_SCRATCH_ROUTER, (size_t)E * 4, &rc);
-    if (!logits) return rc;
-    router_logits_kernel<<<dim3((unsigned)E, 1u), kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, W, bias, 1, H, E,
-                                                                         logits);
-    router_topk_publish_kernel<<<1, kTopkThreads, 0, st>>>(logits, E, k, mode, ids_out, w_out, db_seq, pay);
-    return naiwa_hip_rc(hipGetLastError());
-}
-
-int naiwa_router_topk_pair_publish(const void* x, int x_dtype, int H, const float* W1, const float* b1, int E1,
-                                   int k1, int mode1, uint32_t* ids1, float* w1, const float* W2, const float* b2,
-                                   int E2, int k2, int mode2, uint32_t* ids2, float* w2, uint32_t* db_seq,
-                                   uint32_t* pay, int64_t stream) {
-    if (x_dtype != NAIWA_BF16 && x_dtype != NAIWA_F32) return NAIWA_E_UNSUPPORTED;
-    for (int m : {mode1, mode2})
-        if (m < NAIWA_ROUTE_SOFTMAX_TOPK_RENORM || m > NAIWA_ROUTE_SOFTMAX_TOPK) return NAIWA_E_UNSUPPORTED;
-    if (H <= 0 || H % NAIWA_ROUTER_CHUNK || E1 <= 0 || E1 > NAIWA_ROUTER_MAX_E || k1 <= 0 || k1 > E1 ||
-        k1 > NAIWA_ROUTER_MAX_K || E2 <= 0 || E2 > NAIWA_ROUTER_MAX_E || k2 <= 0 || k2 > E2 ||
-        k2 > NAIWA_ROUTER_MAX_K)
-        return NAIWA_E_INVALID;
-    if (!x || !W1 || !W2 || !ids1 || !w1 || !ids2 || !w2 || !db_seq || !pay) return NAIWA_E_INVALID;
-    hipStream_t st = (hipStream_t)stream;
-    int rc = 0;
-    float* logits = (float*)naiwa_scratch(NAIWA_SCRATCH_ROUTER, (size_t)(E1 + E2) * 4, &rc);
-    if (!logits) return rc;
-    router_logits_pair_kernel<<<(unsigned)(E1 + E2), kLogitThreads, 0, st>>>(x, x_dtype == NAIWA_BF16, H, W1, b1, E1,
-                                                                           logits, W2, b2, E2, logits + E1);
-    router_topk_pair_publish_kernel<<<1, kTopkThreads, 0, st>>>(logits, E1, k1, mode1, ids1, w1, logits + E1, E2, k2,
-                                                                mode2, ids2, w2, db_seq, pay);
+    if (nr == 2 && (!ids2 || !w2)) return NAIWA_E_INVALID;
+    RouteOne a{};
+    a.x = x;
+    a.x_bf16 = x_dtype == NAIWA_BF16;
+    a.H = H;
+    a.nr = nr;
+    a.W[0] = W1;
+    a.W[1] = W2;
+    a.bias[0] = b1;
+    a.bias[1] = b2;
+    a.ids[0] = ids1;
+    a.ids[1] = ids2;
+    a.w[0] = w1;
+    a.w[1] = w2;
+    for (int q = 0; q < 2; ++q) {
+        a.E[q] = q < nr ? E[q] : 0;
+        a.k[q] = q < nr ? k[q] : 0;
+        a.mode[q] = q < nr ? mode[q] : 0;
+    }
+    a.tag = tag;
+    a.words = words;
+    a.counter = counter;
+    a.pay = pay;
+    a.limit_ticks = limit_ticks;
+    router_route_one_kernel<<<(unsigned)(a.E[0] + a.E[1]), kTopkThreads, 0, (hipStream_t)stream>>>(a);
     return naiwa_hip_rc(hipGetLastError());
 }
 
