@@ -555,6 +555,108 @@ down_combine_one_kernel(const float* dpart, int kparts, int n, int H, const int*
     if (out) out[r] = acc;
 }
 
+// The down projection and the ordered combine of a one-token call in one launch
+// (rows == 1, I in one K part, at most kOneMaxPos positions, a row's units in one
+// round of down_split_kernel<DD, 1>): no partial dots go through global memory and
+// no combine launch follows.  Block: kOneRows output rows x kOneHalves position
+// groups, one 16-lane group each; a group dots its row against its positions
+// (half, half + kOneHalves, ...) with down_split_kernel's unit assignment and
+// summation order, and one thread per row then adds w * dot over the positions in
+// ascending order from 0 or from out, as down_combine_one_kernel does: the same
+// bits as the three-launch path.  The weight loads of a group's first positions go
+// out before the h vectors are staged.
+constexpr int kOneRows = 8;
+constexpr int kOneHalves = kDownThreads / NAIWA_GROUP / kOneRows;
+constexpr int kOneMaxPos = kCombineWidth;
+constexpr int kOneChunk = 4; // positions whose weight loads a lane issues together
+
+template <int DD>
+__global__ void __launch_bounds__(kDownThreads)
+down_one_kernel(BankArg down, int H, int I, int n, const int* seg_count, const uint32_t* seg_key,
+                const uint32_t* seg_begin, const uint32_t* perm, const uint8_t* hst, int hst_stride, const float* w,
+                int accumulate, float* out, uint16_t* res) {
+    constexpr int UM = DD == NAIWA_Q4_K ? 2 : Umax<DD>::v; // as down_split_kernel<DD, 1>
+    extern __shared__ __align__(16) uint8_t smem[];        // the positions' h vectors
+    __shared__ uint32_t p_slot[kOneMaxPos], p_perm[kOneMaxPos];
+    __shared__ float p_w[kOneMaxPos];
+    __shared__ float vls[kOneMaxPos][kOneRows];
+    __shared__ int s_npos;
+    const int tid = threadIdx.x, grp = tid / NAIWA_GROUP, lr = tid % NAIWA_GROUP;
+    const int row = grp % kOneRows, half = grp / kOneRows;
+    const int r = blockIdx.x * kOneRows + row;
+    // wave 0: every segment's slot over its positions, the permutation and the position
+    // count, from one round of loads
+    if (tid < 64) {
+        const int sc = *seg_count;
+        const bool in = tid < n;
+        const uint32_t key = in ? seg_key[tid] : 0u, b0 = in ? seg_begin[tid] : 0u, b1 = in ? seg_begin[tid + 1] : 0u;
+        const uint32_t pm = in ? perm[tid] : 0u;
+        const int npos = sc > 0 ? __builtin_amdgcn_readlane((int)b1, sc - 1) : 0;
+        if (tid < sc)
+            for (uint32_t q = b0; q < b1; ++q) p_slot[q] = key;
+        if (tid < npos) p_perm[tid] = pm;
+        if (tid == 0) s_npos = npos;
+    }
+    __syncthreads();
+    const int npos = s_npos;
+    const int nus = Fmt<DD>::units(I);
+    typename Fmt<DD>::Frag f[kOneChunk][UM];
+    auto load_chunk = [&](int j0) {
+#pragma unroll
+        for (int c = 0; c < kOneChunk; ++c) {
+            const int pos = half + kOneHalves * (j0 + c);
+            if (pos >= npos || r >= H) continue;
+            const uint8_t* drow = down.base + (int64_t)p_slot[pos] * down.stride + (int64_t)r * down.row_bytes;
+#pragma unroll
+            for (int q = 0; q < UM; ++q) {
+                const int u = lr + NAIWA_GROUP * q;
+                if (u < nus) f[c][q] = Fmt<DD>::load(drow, u);
+            }
+        }
+    };
+    load_chunk(0);
+    // the h vectors of every position (and the routing weights) while the rows land
+    {
+        const int nv = hst_stride / 16;
+        for (int i = tid; i < npos * nv; i += kDownThreads) {
+            const int pos = i / nv, j = i % nv;
+            reinterpret_cast<uint4*>(smem + (size_t)pos * hst_stride)[j] =
+                reinterpret_cast<const uint4*>(hst + (size_t)p_perm[pos] * hst_stride)[j];
+        }
+        if (tid < npos) p_w[tid] = w[p_perm[tid]];
+    }
+    __syncthreads();
+    for (int j0 = 0; half + kOneHalves * j0 < npos; j0 += kOneChunk) {
+        if (j0 > 0) load_chunk(j0);
+#pragma unroll
+        for (int c = 0; c < kOneChunk; ++c) {
+            const int pos = half + kOneHalves * (j0 + c);
+            if (pos >= npos) break;
+            const uint32_t* words = reinterpret_cast<const uint32_t*>(smem + (size_t)pos * hst_stride);
+            const float* sums = reinterpret_cast<const float*>(smem + (size_t)pos * hst_stride + (size_t)I * 2);
+            float a = 0.0f;
+#pragma unroll
+            for (int q = 0; q < UM; ++q) {
+                const int u = lr + NAIWA_GROUP * q;
+                if (u < nus && r < H) a += Fmt<DD>::dot(f[c][q], u, words, sums);
+            }
+            const float v = naiwa_group_sum<NAIWA_GROUP>(a);
+            if (lr == 0) vls[pos][row] = v;
+        }
+    }
+    __syncthreads();
+    if (tid < kOneRows) {
+        const int ro = blockIdx.x * kOneRows + tid;
+        if (ro < H) {
+            const float x0 = res ? naiwa_bf16_to_f32(res[ro]) : 0.0f;
+            float acc = accumulate ? out[ro] : 0.0f;
+            for (int q = 0; q < npos; ++q) acc = __builtin_fmaf(p_w[q], vls[q][tid], acc);
+            if (res) res[ro] = (uint16_t)naiwa_f32_to_bf16(x0 + acc);
+            if (out) out[ro] = acc;
+        }
+    }
+}
+
 bool bank_ok(const naiwa_bank* b) {
     if (!b || !b->base || b->slots <= 0 || b->n <= 0 || b->k <= 0) return false;
     if (b->dtype != NAIWA_Q4_K && b->dtype != NAIWA_Q8_0) return false;
@@ -674,6 +776,15 @@ int staged_kernels(BankArg g, BankArg u, BankArg d, const void* x, int xb, int H
     int rpg = 1;
     while (rpg < 8 && (int64_t)((H + groups * rpg * 2 - 1) / (groups * rpg * 2)) * kparts * segs >= 1024) rpg *= 2;
     const int stage_d = naiwa_stage_bytes(DD, ks);
+    // one token whose down rows take one K part and one round of units: down and the
+    // ordered combine in one launch
+    constexpr int UM1 = DD == NAIWA_Q4_K ? 2 : Umax<DD>::v;
+    if (rows == 1 && n <= kOneMaxPos && kparts == 1 && Fmt<DD>::units(I) <= NAIWA_GROUP * UM1 &&
+        (size_t)n * hst_stride <= 64 * 1024) {
+        down_one_kernel<DD><<<(H + kOneRows - 1) / kOneRows, kDownThreads, (size_t)n * hst_stride, st>>>(
+            d, H, I, n, seg_count, seg_key, seg_begin, perm, hst, hst_stride, w, accumulate, out, res);
+        return naiwa_hip_rc(hipGetLastError());
+    }
     const int tok_d = std::max(1, std::min({kTokD, rows, (64 * 1024) / stage_d}));
     const dim3 dgrid((H + groups * rpg - 1) / (groups * rpg), kparts, segs);
     if (tok_d == 1)

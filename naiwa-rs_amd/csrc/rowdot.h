@@ -17,7 +17,7 @@ template <> struct Fmt<NAIWA_Q4_K> {
     struct Frag {
         uint4 q, hd;
     };
-    __device__ static int units(int k) { return (k / NAIWA_QK_K) * 8; }
+    __host__ __device__ static int units(int k) { return (k / NAIWA_QK_K) * 8; }
     template <int AS = 0>
     __device__ __forceinline__ static Frag load(const uint8_t* row, int u) {
         const uint8_t* blk = row + (u >> 3) * NAIWA_Q4_K_BYTES;
@@ -49,7 +49,7 @@ template <> struct Fmt<NAIWA_Q8_0> {
     struct Frag {
         uint32_t d[17];
     };
-    __device__ static int units(int k) { return k / (2 * NAIWA_QK8_0); }
+    __host__ __device__ static int units(int k) { return k / (2 * NAIWA_QK8_0); }
     template <int AS = 0>
     __device__ __forceinline__ static Frag load(const uint8_t* row, int u) {
         const uint8_t* p = row + 68 * u;
@@ -82,7 +82,7 @@ template <> struct Fmt<NAIWA_Q8_0_ODD> {
         uint32_t d;
         uint32_t q[8];
     };
-    __device__ static int units(int k) { return k / NAIWA_QK8_0; }
+    __host__ __device__ static int units(int k) { return k / NAIWA_QK8_0; }
     template <int AS = 0>
     __device__ __forceinline__ static Frag load(const uint8_t* row, int u) {
         const uint8_t* p = row + NAIWA_Q8_0_BYTES * u;

@@ -210,11 +210,14 @@ def test_split_by_slot_with_accumulate_is_bit_identical(gpu):
     ((O.Q4_K,) * 3, 2048, 768, 16, 8),              # one K part, 8 pairs
     ((O.Q4_K,) * 3, 1024, 4352, 8, 2),              # three K parts: 2048 + 2048 + 256
     ((O.Q4_K, O.Q4_K, O.Q8_0), 512, 2304, 6, 4),    # Q8_0 down in two K parts
+    ((O.Q4_K, O.Q4_K, O.Q8_0), 1024, 1408, 12, 6),  # Q8_0 down in one K part (one launch for down + combine)
+    ((O.Q8_0,) * 3, 512, 1376, 20, 16),             # odd Q8_0 block count, 16 pairs (one launch)
 ])
 def test_one_token_combine_matches_the_general_combine(gpu, dt, H, I, E, k):
-    """A one-token call (its combine issues every load up front) gives row 0 of a
-    two-token call over the same pairs (the general combine) bit for bit, plain and
-    accumulating into an output that already holds values."""
+    """A one-token call (its combine issues every load up front, or down and combine run
+    as one launch when the down rows fit one K part) gives row 0 of a two-token call
+    over the same pairs (the general combine) bit for bit, plain and accumulating into
+    an output that already holds values."""
     nm = gpu
     g, u, d, r = S.layer(2200 + H, E, H, I, dt)
     banks = nm.LayerBanks(E, H, I, dt)
