@@ -236,32 +236,48 @@ int split_parts(int I) { return (I + split_ks(I) - 1) / split_ks(I); }
 // occupancy.  With TG <= 4 a Q4_K lane also loads 2 units of each row per round
 // instead of 4; at 136-152 VGPRs a SIMD then keeps 3 waves instead of 2 (Mixtral
 // bs1 367 -> 445 tok/s).
+// one_row: the call has one token, whose activations are staged once, before the
+// segments are known (by the waves other than wave 0 while it segments the pairs).
 template <int DG, int DD, int TG>
 __global__ void __launch_bounds__(512, TG == 1 || (TG <= 4 && DG != NAIWA_Q8_0) ? 3 : 1)
 gate_up_staged_kernel(BankArg gate, BankArg up, const void* x, int x_bf16, int H, int I, int width, int tok_max,
                       const int* seg_count, const uint32_t* seg_key, const uint32_t* seg_begin,
-                      const uint32_t* perm, int act, uint8_t* hst, int hst_stride, SegIn seg_in) {
+                      const uint32_t* perm, int act, uint8_t* hst, int hst_stride, SegIn seg_in, int one_row) {
     constexpr int SPAN = Fmt<DD>::kSumSpan;   // rows per block (one group of 16 lanes each)
     constexpr int GPG = SPAN / 4;             // 4-row groups per sum
+    constexpr int NT = SPAN * NAIWA_GROUP;    // threads per block
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float hloc[TG][SPAN];
     __shared__ uint32_t l_perm[kSmallSeg], l_key[kSmallSeg], l_begin[kSmallSeg + 1];
-    __shared__ int l_count;
+    __shared__ int l_count, l_bad;
+    const int wave = threadIdx.x >> 6;
     if (seg_in.slot_ids) {
-        // the call's few pairs segmented by this block (wave 0) into LDS; block (0, 0)'s
-        // wave 1 also writes the global copy the down launches read
-        const int wave = threadIdx.x >> 6;
+        // the call's few pairs segmented by this block (wave 0) into LDS, meanwhile the one
+        // token's activations staged by the other waves; block (0, 0)'s wave 1 then writes
+        // the global copy of the segments the down launches read
         if (wave == 0)
             naiwa_segment_small(seg_in.slot_ids, seg_in.w, seg_in.n, seg_in.nslots, l_perm, &l_count, l_key, l_begin,
-                                nullptr);
-        else if (wave == 1 && blockIdx.x == 0 && blockIdx.y == 0)
-            naiwa_segment_small(seg_in.slot_ids, seg_in.w, seg_in.n, seg_in.nslots, (uint32_t*)perm, (int*)seg_count,
-                                (uint32_t*)seg_key, (uint32_t*)seg_begin, seg_in.bad);
+                                &l_bad);
+        else if (one_row)
+            naiwa_stage<DG>(x, x_bf16 != 0, H, (uint32_t*)smem, (float*)((uint32_t*)smem + H / 2), threadIdx.x - 64,
+                            NT - 64);
         __syncthreads();
+        if (wave == 1 && blockIdx.x == 0 && blockIdx.y == 0) {
+            const int lane = threadIdx.x & 63, c = l_count;
+            if (lane < seg_in.n) ((uint32_t*)perm)[lane] = l_perm[lane];
+            if (lane < c) ((uint32_t*)seg_key)[lane] = l_key[lane];
+            if (lane <= c) ((uint32_t*)seg_begin)[lane] = l_begin[lane];
+            if (lane == 0) {
+                *(int*)seg_count = c;
+                *seg_in.bad = l_bad;
+            }
+        }
         seg_count = &l_count;
         seg_key = l_key;
         seg_begin = l_begin;
         perm = l_perm;
+    } else if (one_row) {
+        naiwa_stage<DG>(x, x_bf16 != 0, H, (uint32_t*)smem, (float*)((uint32_t*)smem + H / 2), threadIdx.x, NT);
     }
     const int s = blockIdx.x;
     if (s >= *seg_count) return;
@@ -277,12 +293,12 @@ gate_up_staged_kernel(BankArg gate, BankArg up, const void* x, int x_bf16, int H
     for (int c0 = b; c0 < e; c0 += tok_max) {
         const int nt = min(tok_max, e - c0);
         __syncthreads();
-        for (int tt = 0; tt < nt; ++tt) {
+        for (int tt = 0; tt < nt && !one_row; ++tt) {
             const int t = (int)perm[c0 + tt] / width;
             const void* src = x_bf16 ? (const void*)((const uint16_t*)x + (int64_t)t * H)
                                      : (const void*)((const float*)x + (int64_t)t * H);
             uint32_t* words = (uint32_t*)(smem + tt * stage);
-            naiwa_stage<DG>(src, x_bf16 != 0, H, words, (float*)(words + H / 2), tid, SPAN * NAIWA_GROUP);
+            naiwa_stage<DG>(src, x_bf16 != 0, H, words, (float*)(words + H / 2), tid, NT);
         }
         __syncthreads();
         float ag[TG], au[TG];
@@ -306,7 +322,7 @@ gate_up_staged_kernel(BankArg gate, BankArg up, const void* x, int x_bf16, int H
 #pragma unroll
                     for (int tt = 0; tt < TG; ++tt) {
                         if (tt >= nt) break;
-                        const uint32_t* words = (const uint32_t*)(smem + tt * stage);
+                        const uint32_t* words = (const uint32_t*)(smem + (one_row ? 0 : tt) * stage);
                         const float* sums = (const float*)(words + H / 2);
                         ag[tt] += Fmt<DG>::dot(fg[i], u, words, sums);
                         au[tt] += Fmt<DG>::dot(fu[i], u, words, sums);
@@ -762,13 +778,13 @@ int staged_kernels(BankArg g, BankArg u, BankArg d, const void* x, int xb, int H
     const dim3 ggrid(std::max(1, std::min(n, slots)), I / SPAN);
     if (tok == 1)
         gate_up_staged_kernel<DG, DD, 1><<<ggrid, SPAN * NAIWA_GROUP, (size_t)stage_g, st>>>(
-            g, u, x, xb, H, I, width, 1, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride, seg_in);
+            g, u, x, xb, H, I, width, 1, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride, seg_in, rows == 1);
     else if (tok <= 4)
         gate_up_staged_kernel<DG, DD, 4><<<ggrid, SPAN * NAIWA_GROUP, (size_t)tok * stage_g, st>>>(
-            g, u, x, xb, H, I, width, tok, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride, seg_in);
+            g, u, x, xb, H, I, width, tok, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride, seg_in, rows == 1);
     else
         gate_up_staged_kernel<DG, DD, kTokG><<<ggrid, SPAN * NAIWA_GROUP, (size_t)tok * stage_g, st>>>(
-            g, u, x, xb, H, I, width, tok, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride, seg_in);
+            g, u, x, xb, H, I, width, tok, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride, seg_in, rows == 1);
     // down: rows per group doubled while the grid keeps at least 1024 blocks
     const int ks = split_ks(I), kparts = split_parts(I);
     const int segs = std::max(1, std::min(n, slots));
