@@ -664,15 +664,19 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
         ++step.preload_waits;
     }
     if (!split) {
-        if (nc && (rc = wait_staged())) return rc;
+        // poll mode: the wait rides in the expert kernels (a one-token call's gate/up
+        // blocks segment the pairs and stage x while the uploads land, then wait)
+        const naiwa_decode_wait wt{L->upload_flag, L->upload_epoch, naiwa_doorbell_wait_limit_ticks(), L->db_dev + 1};
+        const naiwa_decode_wait* wp = nc && poll ? &wt : nullptr;
+        if (nc && !poll && (rc = wait_staged())) return rc;
         if (res_x && !cpu) {
             // out keeps the layer's output; the residual rides in the ordered combine
             if ((rc = naiwa_moe_decode_residual(&d.gate, &d.up, &d.down, res_x, slot_ids, w_one, rows, k,
-                                                d.act, out, 1, stream)))
+                                                d.act, out, 1, stream, wp)))
                 return rc;
             if (folded) *folded = true;
-        } else if ((rc = naiwa_moe_decode(&d.gate, &d.up, &d.down, x, NAIWA_BF16, slot_ids, w_one, rows, k,
-                                          d.act, out, stream))) {
+        } else if ((rc = naiwa_moe_decode_wait(&d.gate, &d.up, &d.down, x, NAIWA_BF16, slot_ids, w_one, rows, k,
+                                               d.act, out, stream, wp))) {
             return rc;
         }
     } else {

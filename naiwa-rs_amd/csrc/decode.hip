@@ -208,6 +208,34 @@ struct SegIn {
     int n, nslots;
     int* bad;
 };
+// The folded wait of a call (flag null: none).  count: this waiter adds to *fail when
+// it runs out (one waiter per call counts).
+struct WaitArg {
+    const uint32_t* flag;
+    uint32_t target;
+    uint64_t limit;
+    uint32_t* fail;
+};
+__device__ inline void wait_flag(const WaitArg& a, bool count) {
+    const uint64_t t0 = wall_clock64();
+    // relaxed spin loads (an acquire load invalidates the L2 on every try), one acquire
+    // after: the rows the other stream wrote are read only behind it
+    while (__hip_atomic_load(a.flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) < a.target) {
+        if (wall_clock64() - t0 > a.limit) {
+            if (count) {
+                const uint32_t n = __hip_atomic_load(a.fail, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(a.fail, n + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+__global__ void __launch_bounds__(64) decode_wait_kernel(WaitArg a) {
+    if (threadIdx.x == 0) wait_flag(a, true);
+}
+
 constexpr int kTokG = 8;
 constexpr int kTokD = 8;
 constexpr int kDownThreads = 256;
@@ -242,7 +270,8 @@ template <int DG, int DD, int TG>
 __global__ void __launch_bounds__(512, TG == 1 || (TG <= 4 && DG != NAIWA_Q8_0) ? 3 : 1)
 gate_up_staged_kernel(BankArg gate, BankArg up, const void* x, int x_bf16, int H, int I, int width, int tok_max,
                       const int* seg_count, const uint32_t* seg_key, const uint32_t* seg_begin,
-                      const uint32_t* perm, int act, uint8_t* hst, int hst_stride, SegIn seg_in, int one_row) {
+                      const uint32_t* perm, int act, uint8_t* hst, int hst_stride, SegIn seg_in, int one_row,
+                      WaitArg wt) {
     constexpr int SPAN = Fmt<DD>::kSumSpan;   // rows per block (one group of 16 lanes each)
     constexpr int GPG = SPAN / 4;             // 4-row groups per sum
     constexpr int NT = SPAN * NAIWA_GROUP;    // threads per block
@@ -281,6 +310,11 @@ gate_up_staged_kernel(BankArg gate, BankArg up, const void* x, int x_bf16, int H
     }
     const int s = blockIdx.x;
     if (s >= *seg_count) return;
+    // the folded wait: every block's thread 0 waits (block (0, 0)'s counts a timeout)
+    if (wt.flag) {
+        if (threadIdx.x == 0) wait_flag(wt, blockIdx.x == 0 && blockIdx.y == 0);
+        __syncthreads();
+    }
     const int tid = threadIdx.x, grp = tid / NAIWA_GROUP, lr = tid % NAIWA_GROUP;
     const int r0 = blockIdx.y * SPAN, r = r0 + grp;
     const uint32_t slot = seg_key[s];
@@ -765,7 +799,7 @@ template <int DG, int DD>
 int staged_kernels(BankArg g, BankArg u, BankArg d, const void* x, int xb, int H, int I, int rows, int width,
                    int act, const float* w, float* out, int accumulate, int n, int slots, const int* seg_count,
                    const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm, uint8_t* hst,
-                   float* dpart, SegIn seg_in, hipStream_t st, uint16_t* res) {
+                   float* dpart, SegIn seg_in, hipStream_t st, uint16_t* res, WaitArg wt) {
     constexpr int SPAN = Fmt<DD>::kSumSpan;
     const int stage_g = naiwa_stage_bytes(DG, H);
     // tokens staged per chunk: a segment holds at most `rows` tokens unless a token repeats
@@ -778,13 +812,13 @@ int staged_kernels(BankArg g, BankArg u, BankArg d, const void* x, int xb, int H
     const dim3 ggrid(std::max(1, std::min(n, slots)), I / SPAN);
     if (tok == 1)
         gate_up_staged_kernel<DG, DD, 1><<<ggrid, SPAN * NAIWA_GROUP, (size_t)stage_g, st>>>(
-            g, u, x, xb, H, I, width, 1, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride, seg_in, rows == 1);
+            g, u, x, xb, H, I, width, 1, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride, seg_in, rows == 1, wt);
     else if (tok <= 4)
         gate_up_staged_kernel<DG, DD, 4><<<ggrid, SPAN * NAIWA_GROUP, (size_t)tok * stage_g, st>>>(
-            g, u, x, xb, H, I, width, tok, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride, seg_in, rows == 1);
+            g, u, x, xb, H, I, width, tok, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride, seg_in, rows == 1, wt);
     else
         gate_up_staged_kernel<DG, DD, kTokG><<<ggrid, SPAN * NAIWA_GROUP, (size_t)tok * stage_g, st>>>(
-            g, u, x, xb, H, I, width, tok, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride, seg_in, rows == 1);
+            g, u, x, xb, H, I, width, tok, seg_count, seg_key, seg_begin, perm, act, hst, hst_stride, seg_in, rows == 1, wt);
     // down: rows per group doubled while the grid keeps at least 1024 blocks
     const int ks = split_ks(I), kparts = split_parts(I);
     const int segs = std::max(1, std::min(n, slots));
@@ -819,13 +853,13 @@ int staged_kernels(BankArg g, BankArg u, BankArg d, const void* x, int xb, int H
 int staged_launch(BankArg g, BankArg u, BankArg d, int gdt, int ddt, const void* x, int x_dtype, int H, int I,
                   int rows, int width, int act, const float* w, float* out, int accumulate, int n, int slots,
                   const int* seg_count, const uint32_t* seg_key, const uint32_t* seg_begin, const uint32_t* perm,
-                  uint8_t* hst, float* dpart, SegIn seg_in, hipStream_t st, uint16_t* res) {
+                  uint8_t* hst, float* dpart, SegIn seg_in, hipStream_t st, uint16_t* res, WaitArg wt) {
     const int xb = x_dtype == NAIWA_BF16;
     const int fg = naiwa_kernel_fmt(gdt, H), fd = naiwa_kernel_fmt(ddt, I);
 #define NAIWA_STAGED(FG, FD)                                                                                       \
     if (fg == FG && fd == FD)                                                                                      \
         return staged_kernels<FG, FD>(g, u, d, x, xb, H, I, rows, width, act, w, out, accumulate, n, slots,         \
-                                      seg_count, seg_key, seg_begin, perm, hst, dpart, seg_in, st, res);
+                                      seg_count, seg_key, seg_begin, perm, hst, dpart, seg_in, st, res, wt);
     NAIWA_STAGED(NAIWA_Q4_K, NAIWA_Q4_K)
     NAIWA_STAGED(NAIWA_Q4_K, NAIWA_Q8_0)
     NAIWA_STAGED(NAIWA_Q4_K, NAIWA_Q8_0_ODD)
@@ -844,7 +878,9 @@ int staged_launch(BankArg g, BankArg u, BankArg d, int gdt, int ddt, const void*
 // place, x = bf16(x + y); out may then be null.
 int decode_launch(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, const void* x, int x_dtype,
                   const uint32_t* slot_ids, const float* w, int rows, int width, int act, float* out, int flags,
-                  uint8_t* ws, hipStream_t st, uint16_t* res = nullptr) {
+                  uint8_t* ws, hipStream_t st, uint16_t* res = nullptr, const naiwa_decode_wait* wait = nullptr) {
+    WaitArg wt{nullptr, 0u, 0ull, nullptr};
+    if (wait) wt = WaitArg{wait->flag, wait->target, wait->limit_ticks, wait->fail};
     const int accumulate = (flags & NAIWA_DECODE_ACCUMULATE) ? 1 : 0;
     const int H = gate->k, I = gate->n;
     if (width == 0) {
@@ -874,9 +910,14 @@ int decode_launch(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank
     // a staged call of few pairs is segmented by its gate/up blocks; every other call
     // by one segments launch first
     SegIn seg_in{nullptr, nullptr, 0, 0, nullptr};
-    if (staged && !mfma && n <= kSmallSeg)
+    if (staged && !mfma && n <= kSmallSeg) {
         seg_in = SegIn{slot_ids, w, n, gate->slots, bad};
-    else
+    } else if (wt.flag) {
+        // the wait is not folded into gate/up blocks here: one wave waits first
+        decode_wait_kernel<<<1, 64, 0, st>>>(wt);
+        wt.flag = nullptr;
+    }
+    if (!seg_in.slot_ids)
         segments_kernel<<<1, NAIWA_SEG_THREADS, 0, st>>>(slot_ids, w, n, gate->slots, perm, seg_count, seg_key,
                                                          seg_begin, bad);
     if (staged) {
@@ -891,7 +932,7 @@ int decode_launch(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank
         }
         return staged_launch(g, u, d, gate->dtype, down->dtype, x, x_dtype, H, I, rows, width, act, w, out,
                              accumulate, n, gate->slots, seg_count, seg_key, seg_begin, perm, (uint8_t*)hbuf, dpart,
-                             seg_in, st, res);
+                             seg_in, st, res, wt);
     }
     const dim3 ggrid(n, (I + kRowsPerBlock - 1) / kRowsPerBlock);
     const size_t lds_g = (size_t)tok_g * naiwa_stage_bytes(gate->dtype, H);
@@ -996,19 +1037,41 @@ extern "C" int64_t naiwa_moe_decode_scratch_bytes(int rows, int width, int H, in
 
 int naiwa_moe_decode_residual(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, void* x,
                               const uint32_t* slot_ids, const float* w, int rows, int width, int act, float* y,
-                              int keep_y, int64_t stream) {
+                              int keep_y, int64_t stream, const naiwa_decode_wait* wait) {
     int rc = check_args(gate, up, down, x, NAIWA_BF16, slot_ids, w, rows, width, act, y, 0);
     if (rc || rows == 0 || width == 0) return rc;
+    if (wait && (!wait->flag || !wait->fail)) return NAIWA_E_INVALID;
     const DecodeScratch L(rows, width, gate->k, gate->n, down->dtype);
     uint8_t* ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_DECODE, L.total, &rc);
     if (!ws) return rc;
     if (split_path(rows * width, width))
         return decode_launch(gate, up, down, x, NAIWA_BF16, slot_ids, w, rows, width, act, keep_y ? y : nullptr, 0,
-                             ws, (hipStream_t)stream, (uint16_t*)x);
+                             ws, (hipStream_t)stream, (uint16_t*)x, wait);
     if ((rc = decode_launch(gate, up, down, x, NAIWA_BF16, slot_ids, w, rows, width, act, y, 0, ws,
-                            (hipStream_t)stream)))
+                            (hipStream_t)stream, nullptr, wait)))
         return rc;
     return naiwa_residual_add_bf16(x, y, (int64_t)rows * gate->k, stream);
+}
+
+int naiwa_moe_decode_wait(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down, const void* x,
+                          int x_dtype, const uint32_t* slot_ids, const float* w, int rows, int width, int act,
+                          float* out, int64_t stream, const naiwa_decode_wait* wait) {
+    int rc = check_args(gate, up, down, x, x_dtype, slot_ids, w, rows, width, act, out, 0);
+    if (rc || rows == 0) return rc;
+    if (wait && (!wait->flag || !wait->fail)) return NAIWA_E_INVALID;
+    uint8_t* ws = nullptr;
+    if (width > 0) {
+        const DecodeScratch L(rows, width, gate->k, gate->n, down->dtype);
+        ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_DECODE, L.total, &rc);
+        if (!ws) return rc;
+    } else if (wait) {
+        // nothing to compute: the wait still orders the stream
+        decode_wait_kernel<<<1, 64, 0, (hipStream_t)stream>>>(
+            WaitArg{wait->flag, wait->target, wait->limit_ticks, wait->fail});
+        if ((rc = naiwa_hip_rc(hipGetLastError()))) return rc;
+    }
+    return decode_launch(gate, up, down, x, x_dtype, slot_ids, w, rows, width, act, out, 0, ws, (hipStream_t)stream,
+                         nullptr, width > 0 ? wait : nullptr);
 }
 
 extern "C" int naiwa_moe_decode(const naiwa_bank* gate, const naiwa_bank* up, const naiwa_bank* down,
