@@ -615,7 +615,7 @@ down_combine_one_kernel(const float* dpart, int kparts, int n, int H, const int*
 // ascending order from 0 or from out, as down_combine_one_kernel does: the same
 // bits as the three-launch path.  The weight loads of a group's first positions go
 // out before the h vectors are staged.
-constexpr int kOneRows = 8;
+constexpr int kOneRows = 4;
 constexpr int kOneHalves = kDownThreads / NAIWA_GROUP / kOneRows;
 constexpr int kOneMaxPos = kCombineWidth;
 constexpr int kOneChunk = 4; // positions whose weight loads a lane issues together
