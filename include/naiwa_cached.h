@@ -122,11 +122,12 @@ int naiwa_cached_layer_seed(naiwa_cached_layer* L, const uint32_t* experts, int 
  * Staged uploads are one kernel reading the host stacks through their device
  * mapping when they are mapped pinned memory, else DMA copies
  * (naiwa_cached_layer_set_upload_path).
- * The routing comes back through a mapped doorbell (the reference's
- * TopkDoorbell, src/doorbell/d2h/topk.rs:20-125): the device writes the
- * top-k into fine-grained host memory and raises a sequence word, and the
- * host spins on that word (at most 10 s, else NAIWA_E_TIMEOUT) instead of
- * synchronising the stream.  Steps of one layer are ordered even when each
+ * The routing comes back through a mapped doorbell (the role of the
+ * reference's TopkDoorbell, src/doorbell/d2h/topk.rs:20-125): the device
+ * writes the top-k into fine-grained host memory as 64-bit words tagged with
+ * the step's sequence number, and the host spins until every word carries the
+ * tag (at most 10 s, else NAIWA_E_TIMEOUT) instead of synchronising the
+ * stream.  Steps of one layer are ordered even when each
  * is queued on another stream (a step waits for the previous step's last
  * read of the layer's buffers).  Staged uploads complete into the staged
  * expert pass as naiwa_cached_layer_set_upload_sync chooses.  Misses left
