@@ -632,14 +632,16 @@ def test_poll_upload_wait_that_runs_out_is_reported_by_the_next_step(gpu):
     assert layer.upload_timeouts() == 1
 
 
-def test_upload_waits_and_paths_give_the_same_bits(gpu):
+@pytest.mark.parametrize("rows", [2, 5])
+def test_upload_waits_and_paths_give_the_same_bits(gpu, rows):
     """Identical layers whose staged uploads travel as one copy kernel or as DMA
     copies, and complete into the expert pass through the polled device flag or an
     event, run the same ten steps (pcie_frac 1 and 0.5 alternating, so some steps also
     run misses on the CPU): the outputs are identical bit for bit, as are the per-step
-    counts, and they match the oracle."""
+    counts, and they match the oracle.  At 2 rows the poll wait rides in the gate/up
+    blocks; at 5 rows (the matrix-core pass) one wave waits before the pass."""
     nm = gpu
-    E, H, I, k, usable, rows = 16, 256, 256, 4, 4, 2
+    E, H, I, k, usable = 16, 256, 256, 4, 4
     outs = {}
     for sync, path in (("event", "kernel"), ("poll", "kernel"), ("poll", "dma"), ("event", "dma")):
         copy, stream = nm.Stream(), nm.Stream()
@@ -649,7 +651,7 @@ def test_upload_waits_and_paths_give_the_same_bits(gpu):
         layer.set_upload_path(nm.policy.UPLOAD_PATH_DMA if path == "dma" else nm.policy.UPLOAD_PATH_KERNEL)
         res = []
         for i in range(10):
-            print(f"[{sync} {path} step {i}]", flush=True)
+            print(f"[{sync} {path} rows {rows} step {i}]", flush=True)
             x = S.activations_bf16(2810 + i, rows, H)
             out = nm.DeviceBuffer(rows * H * 4)
             info = layer.forward(nm.DeviceBuffer.from_array(x), rows, out, pcie_frac=1.0 if i % 2 == 0 else 0.5,
