@@ -118,6 +118,45 @@ def test_fused_matches_layered_bit_for_bit_routing(gpu, rows):
         run_and_check(nm, layers, host, x, rows, H, E, k, O.ROUTE_SOFTMAX_TOPK_RENORM, fused, "chain")
 
 
+def test_fused_status_counts_add_up_across_launches(gpu):
+    """Pairs routed to an expert that has no slot are counted as missing (and left out of
+    the output).  Each launch starts its own counts from zero and folds its predecessor's
+    into the running totals, so launches in a row add up to the sum of their counts, a
+    status read returns them and clears them, and no wait times out."""
+    nm = gpu
+    L, H, E, I, k, rows, gone = 2, 256, 16, 256, 4, 2, 5
+    dt = (O.Q4_K,) * 3
+    layers, keep = [], []
+    for l in range(L):
+        g, u, d, r = S.layer(3100 + l, E, H, I, dt)
+        r = r.copy()
+        r[gone] *= 3.0  # larger logits either way: expert `gone` is often in the top k
+        banks = nm.LayerBanks(E, H, I, dt)
+        slot_of = np.arange(E, dtype=np.int32)
+        slot_of[gone] = -1
+        for e in range(E):
+            if e != gone:
+                banks.load(e, g[e], u[e], d[e])
+        rd, table = nm.DeviceBuffer.from_array(r), nm.DeviceBuffer.from_array(slot_of)
+        layers.append(nm.layer_desc(rd, banks, table))
+        keep += [banks, rd, table]
+    nm.stack_status()  # earlier tests' counts
+    counts = []
+    for launch in range(4):
+        x = S.activations_bf16(3110 + launch, rows, H)
+        xd = nm.DeviceBuffer.from_array(x)
+        ids_d, w_d = nm.DeviceBuffer(L * rows * k * 4), nm.DeviceBuffer(L * rows * k * 4)
+        print(f"[status launch {launch}]", flush=True)
+        nm.stack_decode(layers, xd, rows, H, E, k, ids_out=ids_d, w_out=w_d, fused=True)
+        nm.synchronize()
+        counts.append(int((ids_d.download(np.uint32) == gone).sum()))
+        if launch == 2:
+            assert nm.stack_status() == (0, sum(counts))
+    assert nm.stack_status() == (0, counts[3])
+    assert nm.stack_status() == (0, 0)
+    assert sum(counts) > 0
+
+
 def test_fused_last_slot_of_exact_bank(gpu):
     """Routing forced onto the last slot of a bank sized exactly to its experts (no
     slot stride padding past the last slot): the fused kernel's LDS prefetch of the
