@@ -129,13 +129,16 @@ void doorbell_wait_copy_f32(void* d_seq, uint32_t target, void* d_payload, int64
 /* The persistent-wave variant of the device-side doorbell waits (the
  * reference launches one spinning kernel per wait, doorbell.cu:105-149):
  *  - doorbell_poll_serve: one wave answers `count` host rings in a row: for
- *    i = 0 .. count-1 it waits until *d_seq >= first + i, then release-stores
- *    first + i to *d_ack (the host's round trip is ring -> observe ack);
+ *    i = 0 .. count-1 it waits until *d_seq >= first + i, then stores first + i
+ *    to *d_ack at system scope (the host's round trip is ring -> observe ack;
+ *    the wave publishes nothing else, so no release fence goes with it);
  *  - doorbell_poll_wait: a stream-ordered wait for *d_flag >= target, polled by
- *    one wave (e.g. an "upload done" flag another stream raises): work queued
- *    after it on `stream` starts when it exits;
- *  - doorbell_poll_signal: release-store `value` to *d_flag once the work
- *    queued before it on `stream` is done.
+ *    one wave (e.g. an "upload done" flag another stream raises) with relaxed
+ *    loads and one acquire at the end: work queued after it on `stream` starts
+ *    when it exits;
+ *  - doorbell_poll_signal: store `value` to *d_flag (system scope) once the
+ *    work queued before it on `stream` is done: that work has completed and its
+ *    writes were released when it ended, so the store needs no fence.
  * Flags are u32 words in device memory or mapped memory (device pointers).
  * Every wait is bounded like doorbell_wait_copy_f32's; an expired wait counts a
  * timeout (naiwa_doorbell_timeouts) and the wave exits. */
