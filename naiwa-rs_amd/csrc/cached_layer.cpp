@@ -41,8 +41,7 @@ bool bank_ok(const naiwa_bank& b, int n, int k, int min_slots) {
 // publishes them without a system-scope fence (which writes back the L2 and cost
 // ~2.5 us a publish).
 constexpr int kDbHead = 16;
-// Device words of the one-token routing kernel: tagged logits of two routers, then
-// its arrival counter.
+// Device words of the one-token routing kernel: tagged logits of two routers.
 constexpr int kRouteWords = 2 * NAIWA_ROUTER_MAX_E;
 
 typedef __attribute__((address_space(1))) uint64_t gu64;
@@ -305,8 +304,8 @@ struct naiwa_cached_layer {
         void* xp = nullptr;
         const size_t xn = (size_t)rows * d.hidden;
         if (hipMalloc(&route_dev_base, 2 * n * 4) != hipSuccess || hipMalloc(&in_dev_base, 3 * n * 4) != hipSuccess ||
-            hipMalloc(&rwords_dev, (kRouteWords + 1) * 8) != hipSuccess ||
-            hipMemset(rwords_dev, 0, (kRouteWords + 1) * 8) != hipSuccess ||
+            hipMalloc(&rwords_dev, kRouteWords * 8) != hipSuccess ||
+            hipMemset(rwords_dev, 0, kRouteWords * 8) != hipSuccess ||
             doorbell_alloc_mapped(&db, kDbHead * 4 + 3 * n * 8) != NAIWA_OK ||
             doorbell_alloc_mapped(&in, 3 * n * 4) != NAIWA_OK || hipHostMalloc(&slots_h, n * 4, 0) != hipSuccess ||
             hipMalloc(&pred_ids_dev, n * 4) != hipSuccess || hipMalloc(&pred_w_dev, n * 4) != hipSuccess ||
@@ -498,9 +497,8 @@ int forward_impl(naiwa_cached_layer* L, naiwa_cached_layer* next, int swaps_per_
                                      L->ids_dev, L->w_dev, next ? next->d.router : nullptr,
                                      next ? next->d.router_bias : nullptr, next ? next->d.num_experts : 0, k,
                                      NAIWA_ROUTE_TOPK_SOFTMAX, next ? next->pred_ids_dev : nullptr,
-                                     next ? next->pred_w_dev : nullptr, tag, L->rwords_dev,
-                                     reinterpret_cast<unsigned*>(L->rwords_dev + kRouteWords), pay_dev,
-                                     naiwa_doorbell_wait_limit_ticks(), stream);
+                                     next ? next->pred_w_dev : nullptr, tag, L->rwords_dev, pay_dev,
+                                     naiwa_wall_ticks_ms(2000), stream);
         if (rc) return rc;
         if (next) next->pred_rows = rows;
     } else {

@@ -255,3 +255,6 @@ __device__ __forceinline__ float naiwa_q8_0_pair(const uint32_t* D, const uint32
 // The bound of the device-side doorbell waits in wall-clock ticks (doorbell.hip;
 // naiwa_doorbell_set_wait_limit_us sets it).
 uint64_t naiwa_doorbell_wait_limit_ticks();
+// Wall-clock ticks (s_memrealtime) in `ms` milliseconds on the current device, for
+// bounds on waits between the workgroups of one launch (not the doorbell bound).
+uint64_t naiwa_wall_ticks_ms(uint64_t ms);

@@ -44,10 +44,6 @@ uint64_t wait_limit_ticks() {
     return us * (uint64_t)wall_clock_khz_current() / 1000ull;
 }
 
-__device__ __forceinline__ uint32_t load_acquire_sys(const uint32_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-
 __device__ __forceinline__ void store_release_sys(uint32_t* p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
@@ -168,6 +164,7 @@ __global__ void __launch_bounds__(64) doorbell_poll_signal_kernel(uint32_t* d_fl
 // The bound of the device-side doorbell waits, in wall-clock ticks (for other
 // kernels of the library that wait on a doorbell word).
 uint64_t naiwa_doorbell_wait_limit_ticks() { return wait_limit_ticks(); }
+uint64_t naiwa_wall_ticks_ms(uint64_t ms) { return ms * (uint64_t)wall_clock_khz_current(); }
 
 extern "C" {
 

@@ -176,10 +176,10 @@ __device__ inline void naiwa_wave_topk(const float* l, int E, int k, int mode, u
 // when W2 is given: the next layer's, for the lookahead's prediction), the top k of
 // each into ids/w on the device, and tagged words (tag << 32 | value) in mapped host
 // memory: ids1 at pay[0..k1), weights1 at pay[k1..2 k1), ids2 at pay[2 k1..2 k1 + k2).
-// words: E1 + E2 device words for the tagged logits; counter: a device word that
-// starts at 0 and is back at 0 after each launch.  Launches that share words or
-// counter must not overlap, and tag must differ from the previous launch's.
+// words: E1 + E2 device words for the tagged logits.  Launches that share words must
+// not overlap, and tag must differ from the previous launch's.  limit_ticks bounds
+// block 0's wait for the other blocks' logits.
 int naiwa_route_one_publish(const void* x, int x_dtype, int H, const float* W1, const float* b1, int E1, int k1,
                             int mode1, uint32_t* ids1, float* w1, const float* W2, const float* b2, int E2, int k2,
-                            int mode2, uint32_t* ids2, float* w2, uint32_t tag, uint64_t* words, unsigned* counter,
-                            uint64_t* pay, uint64_t limit_ticks, int64_t stream);
+                            int mode2, uint32_t* ids2, float* w2, uint32_t tag, uint64_t* words, uint64_t* pay,
+                            uint64_t limit_ticks, int64_t stream);

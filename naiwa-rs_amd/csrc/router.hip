@@ -144,9 +144,9 @@ __device__ __forceinline__ uint64_t tagged_word(uint32_t tag, uint32_t v) { retu
 // One token's routing in one launch, under one router or two (a layer's, and the next
 // layer's for the lookahead's prediction), published to the host without a fence.
 // Block b computes logit b of the routers' concatenated experts and stores it as a
-// tagged word (tag << 32 | f32 bits) in words[b]; the block that arrives last on the
-// wrapping counter (atomicInc, back to 0 after the last arrival) loads every logit,
-// waiting (bounded) until each carries the tag, and ranks them.  The results go to
+// tagged word (tag << 32 | f32 bits) in words[b]; block 0 then loads every logit,
+// waiting (bounded) until each carries the tag, and ranks them (no arrival counter:
+// 128 atomics on one word serialise at the L2).  The results go to
 // the device outputs and, as tagged words, to the mapped payload: ids at pay[0..k0),
 // weights at pay[k0..2 k0), the prediction's ids at pay[2 k0..2 k0 + k1).  Every
 // word carries its own tag, so the host needs no ordering between them: it waits
@@ -162,7 +162,6 @@ struct RouteOne {
     float* w[2];
     uint32_t tag;
     uint64_t* words;
-    unsigned* counter;
     uint64_t* pay;
     uint64_t limit_ticks;
 };
@@ -174,18 +173,17 @@ __global__ void __launch_bounds__(kTopkThreads) router_route_one_kernel(RouteOne
     __shared__ float ex_tmp[NAIWA_ROUTER_MAX_E];
     __shared__ uint32_t ids_s[NAIWA_ROUTER_MAX_K];
     __shared__ float w_s[NAIWA_ROUTER_MAX_K];
-    __shared__ int last, ok;
+    __shared__ int ok;
     const int b = blockIdx.x, tid = threadIdx.x, nb = (int)gridDim.x;
     const int r = b < a.E[0] ? 0 : 1, e = b - (r ? a.E[0] : 0);
     const float v = logit_value(a.x, a.x_bf16, a.W[r], a.bias[r], a.H, e, 0, part);
     if (tid == 0) {
         __hip_atomic_store((gu64*)(a.words + b), tagged_word(a.tag, __float_as_uint(v)), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
-        last = atomicInc(a.counter, (unsigned)(nb - 1)) == (unsigned)(nb - 1);
         ok = 1;
     }
+    if (b != 0) return;
     __syncthreads();
-    if (!last) return;
     const uint64_t t0 = wall_clock64();
     for (int i = tid; i < nb; i += kTopkThreads) {
         uint64_t wd;
@@ -226,8 +224,8 @@ __global__ void __launch_bounds__(kTopkThreads) router_route_one_kernel(RouteOne
 
 int naiwa_route_one_publish(const void* x, int x_dtype, int H, const float* W1, const float* b1, int E1, int k1,
                             int mode1, uint32_t* ids1, float* w1, const float* W2, const float* b2, int E2, int k2,
-                            int mode2, uint32_t* ids2, float* w2, uint32_t tag, uint64_t* words, unsigned* counter,
-                            uint64_t* pay, uint64_t limit_ticks, int64_t stream) {
+                            int mode2, uint32_t* ids2, float* w2, uint32_t tag, uint64_t* words, uint64_t* pay,
+                            uint64_t limit_ticks, int64_t stream) {
     if (x_dtype != NAIWA_BF16 && x_dtype != NAIWA_F32) return NAIWA_E_UNSUPPORTED;
     const int nr = W2 ? 2 : 1;
     const int mode[2] = {mode1, mode2}, E[2] = {E1, E2}, k[2] = {k1, k2};
@@ -237,7 +235,7 @@ int naiwa_route_one_publish(const void* x, int x_dtype, int H, const float* W1, 
         if (E[q] <= 0 || E[q] > NAIWA_ROUTER_MAX_E || k[q] <= 0 || k[q] > E[q] || k[q] > NAIWA_ROUTER_MAX_K)
             return NAIWA_E_INVALID;
     }
-    if (H <= 0 || H % NAIWA_ROUTER_CHUNK || !x || !W1 || !ids1 || !w1 || !words || !counter || !pay)
+    if (H <= 0 || H % NAIWA_ROUTER_CHUNK || !x || !W1 || !ids1 || !w1 || !words || !pay)
         return NAIWA_E_INVALID;
     if (nr == 2 && (!ids2 || !w2)) return NAIWA_E_INVALID;
     RouteOne a{};
@@ -260,7 +258,6 @@ int naiwa_route_one_publish(const void* x, int x_dtype, int H, const float* W1, 
     }
     a.tag = tag;
     a.words = words;
-    a.counter = counter;
     a.pay = pay;
     a.limit_ticks = limit_ticks;
     router_route_one_kernel<<<(unsigned)(a.E[0] + a.E[1]), kTopkThreads, 0, (hipStream_t)stream>>>(a);
