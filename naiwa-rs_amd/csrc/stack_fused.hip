@@ -925,6 +925,12 @@ __device__ inline void stage_h_wave(const Params& p, int v, uint32_t* hw, float*
     }
 }
 
+// Model shapes with an instantiation of their own (the launch checks the sizes).
+template <int SH> struct FixedShape;
+template <> struct FixedShape<1> { // Qwen3-30B-A3B: hidden 2048, 128 experts, top-8, intermediate 768
+    static constexpr int H = 2048, I = 768, E = 128, k = 8;
+};
+
 // The pointer, as a value the compiler cannot see through: address math on it
 // is then redone inside the layer loop instead of being hoisted out and kept
 // live in registers across all layers.
@@ -935,10 +941,25 @@ __device__ __forceinline__ T* opaque(T* ptr) {
 }
 
 // MR: the largest rows (tokens per step) this instantiation serves, 1 or kMaxRows;
-// it sizes the per-thread (token, expert) item arrays.
-template <int DG, int DD, int MR>
+// it sizes the per-thread (token, expert) item arrays.  SH: 0 for any shape, or a
+// FixedShape whose routing sizes the kernel then knows at compile time: the routing
+// loops unroll and their bounds and addresses fold to constants, so fewer scalar
+// values are live across the layer loop.  The scalar registers overflow into vector
+// lanes in this kernel, and every reload of a spilled value is a v_readlane; at the
+// Qwen3-30B-A3B shape this took the bs1 token from 786-805 to 769-773 us.  TR: false
+// compiles the phase marks out (the trace buffer is then never written): 755-770 ->
+// 745-748 us, for the same reason.
+template <int DG, int DD, int MR, int SH, bool TR>
 __global__ void __launch_bounds__(kThreads)
 stack_kernel(Params p) {
+    if constexpr (MR == 1) p.rows = 1;
+    if constexpr (!TR) p.trace = nullptr;
+    if constexpr (SH != 0) {
+        // only the expert count and top k: with the hidden and intermediate sizes fixed
+        // too, the unrolled loops spill vector registers to scratch
+        p.E = FixedShape<SH>::E;
+        p.k = FixedShape<SH>::k;
+    }
     constexpr int PPT = (MR * kMaxE + kThreads - 1) / kThreads; // router items per thread
     constexpr int XG = MR == 1 ? 2 : kXG;                       // activation groups per thread per round
     extern __shared__ __align__(16) uint8_t dyn[];
@@ -1613,9 +1634,9 @@ int desc_set(FusedDev& f, const std::vector<LayerDev>& desc, hipStream_t st, Des
     return NAIWA_OK;
 }
 
-template <int DG, int DD, int MR>
+template <int DG, int DD, int MR, int SH, bool TR>
 int launch(const Params& prm, int blocks, size_t lds, hipStream_t st) {
-    auto fn = stack_kernel<DG, DD, MR>;
+    auto fn = stack_kernel<DG, DD, MR, SH, TR>;
     Params copy = prm;
     void* args[] = {&copy};
     hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -1629,28 +1650,35 @@ int launch(const Params& prm, int blocks, size_t lds, hipStream_t st) {
     return naiwa_hip_rc(e);
 }
 
-template <int DG, int DD, int MR>
+template <int DG, int DD, int MR, int SH, bool TR>
 int occupancy(size_t lds, int* per_cu) {
-    return naiwa_hip_rc(hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, stack_kernel<DG, DD, MR>,
+    return naiwa_hip_rc(hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, stack_kernel<DG, DD, MR, SH, TR>,
                                                                      kThreads, lds));
 }
 
 // The instantiation for (gate/up format, down format, rows class): op(fn) on it.
+// sh: the FixedShape the sizes match (0: none); trace: the phase marks are wanted.
+// The fixed-shape kernel has a traced and an untraced instantiation; the others
+// test for a trace buffer at run time.
 template <int MR, class Op>
-int with_kernel(int fg, int fd, const Op& op) {
-    if (fg == NAIWA_Q4_K && fd == NAIWA_Q4_K) return op.template run<NAIWA_Q4_K, NAIWA_Q4_K, MR>();
-    if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0) return op.template run<NAIWA_Q4_K, NAIWA_Q8_0, MR>();
-    if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0_ODD) return op.template run<NAIWA_Q4_K, NAIWA_Q8_0_ODD, MR>();
-    if (fg == NAIWA_Q8_0 && fd == NAIWA_Q8_0) return op.template run<NAIWA_Q8_0, NAIWA_Q8_0, MR>();
-    if (fg == NAIWA_Q8_0 && fd == NAIWA_Q8_0_ODD) return op.template run<NAIWA_Q8_0, NAIWA_Q8_0_ODD, MR>();
+int with_kernel(int fg, int fd, int sh, bool trace, const Op& op) {
+    if constexpr (MR == 1)
+        if (sh == 1 && fg == NAIWA_Q4_K && fd == NAIWA_Q4_K)
+            return trace ? op.template run<NAIWA_Q4_K, NAIWA_Q4_K, 1, 1, true>()
+                         : op.template run<NAIWA_Q4_K, NAIWA_Q4_K, 1, 1, false>();
+    if (fg == NAIWA_Q4_K && fd == NAIWA_Q4_K) return op.template run<NAIWA_Q4_K, NAIWA_Q4_K, MR, 0, true>();
+    if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0) return op.template run<NAIWA_Q4_K, NAIWA_Q8_0, MR, 0, true>();
+    if (fg == NAIWA_Q4_K && fd == NAIWA_Q8_0_ODD) return op.template run<NAIWA_Q4_K, NAIWA_Q8_0_ODD, MR, 0, true>();
+    if (fg == NAIWA_Q8_0 && fd == NAIWA_Q8_0) return op.template run<NAIWA_Q8_0, NAIWA_Q8_0, MR, 0, true>();
+    if (fg == NAIWA_Q8_0 && fd == NAIWA_Q8_0_ODD) return op.template run<NAIWA_Q8_0, NAIWA_Q8_0_ODD, MR, 0, true>();
     return NAIWA_E_UNSUPPORTED;
 }
 
 struct OccupancyOp {
     size_t lds;
     int* per_cu;
-    template <int DG, int DD, int MR>
-    int run() const { return occupancy<DG, DD, MR>(lds, per_cu); }
+    template <int DG, int DD, int MR, int SH, bool TR>
+    int run() const { return occupancy<DG, DD, MR, SH, TR>(lds, per_cu); }
 };
 
 struct LaunchOp {
@@ -1658,8 +1686,8 @@ struct LaunchOp {
     int blocks;
     size_t lds;
     hipStream_t st;
-    template <int DG, int DD, int MR>
-    int run() const { return launch<DG, DD, MR>(*prm, blocks, lds, st); }
+    template <int DG, int DD, int MR, int SH, bool TR>
+    int run() const { return launch<DG, DD, MR, SH, TR>(*prm, blocks, lds, st); }
 };
 
 } // namespace
@@ -1799,7 +1827,9 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     if ((rc = naiwa_hip_rc(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev)))) return rc;
     int per_cu = 0;
     const OccupancyOp occ{lds, &per_cu};
-    rc = rows == 1 ? with_kernel<1>(fg, fd, occ) : with_kernel<kMaxRows>(fg, fd, occ);
+    const int sh = H == FixedShape<1>::H && I == FixedShape<1>::I && E == FixedShape<1>::E && k == FixedShape<1>::k;
+    const bool tr = g_trace_enabled;
+    rc = rows == 1 ? with_kernel<1>(fg, fd, sh, tr, occ) : with_kernel<kMaxRows>(fg, fd, sh, tr, occ);
     if (rc) return rc;
     const int bpc = per_cu < g_fused_blocks_per_cu ? per_cu : g_fused_blocks_per_cu;
     if (bpc < 1) return NAIWA_E_UNSUPPORTED;
@@ -1896,7 +1926,7 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     if (sync_fresh) zero_u32<<<1, 64, 0, st>>>((unsigned int*)(sync + kStatusOff), 64);
     roll_status<<<1, 64, 0, st>>>((int*)(sync + kStatusOff));
     const LaunchOp go{&prm, blocks, lds, st};
-    rc = rows == 1 ? with_kernel<1>(fg, fd, go) : with_kernel<kMaxRows>(fg, fd, go);
+    rc = rows == 1 ? with_kernel<1>(fg, fd, sh, tr, go) : with_kernel<kMaxRows>(fg, fd, sh, tr, go);
     if (rc) return rc;
     if ((rc = naiwa_hip_rc(hipEventRecord(fdev.done, st)))) return rc;
     fdev.have_done = true;

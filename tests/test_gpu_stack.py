@@ -91,6 +91,7 @@ def check_chain(host, x, ids, w, ys, x_final, rows, H, E, k, mode):
 @pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("rows,L,H,E,k,I,dt,mode,perm", [
     (1, 4, 2048, 128, 8, 768, (O.Q4_K,) * 3, O.ROUTE_SOFTMAX_TOPK_RENORM, False),  # Qwen3 shape
+    (1, 2, 2048, 64, 4, 768, (O.Q4_K,) * 3, O.ROUTE_SOFTMAX_TOPK_RENORM, True),    # any shape, Q4_K
     (8, 3, 2048, 128, 8, 768, (O.Q4_K,) * 3, O.ROUTE_SOFTMAX_TOPK_RENORM, True),   # Qwen3 shape, bs8
     (1, 2, 1024, 8, 2, 2048, (O.Q8_0,) * 3, O.ROUTE_TOPK_SOFTMAX, True),
     (1, 2, 2048, 64, 6, 1408, (O.Q4_K, O.Q4_K, O.Q8_0), O.ROUTE_SOFTMAX_TOPK, True),
@@ -116,6 +117,48 @@ def test_fused_matches_layered_bit_for_bit_routing(gpu, rows):
     x = S.activations_bf16(951, rows, H)
     for fused in (True, False):
         run_and_check(nm, layers, host, x, rows, H, E, k, O.ROUTE_SOFTMAX_TOPK_RENORM, fused, "chain")
+
+
+def test_fused_trace_records_phases_and_leaves_the_bits_unchanged(gpu):
+    """The phase trace (a separate instantiation at the Qwen3 shape, with its marks
+    compiled in) records every workgroup's timestamps, in order within each layer's
+    first phases, and the traced launch gives the same ids, weights and x bits as the
+    untraced one."""
+    import ctypes as C
+    nm = gpu
+    lib = nm.lib()
+    rows, L, H, E, k, I = 1, 2, 2048, 128, 8, 768
+    layers, host, keep = build_stack(nm, L, H, E, I, (O.Q4_K,) * 3, 990)
+    x = S.activations_bf16(991, rows, H)
+    outs = []
+    for trace in (0, 1, 0):
+        xd = nm.DeviceBuffer.from_array(x)
+        ids_d, w_d = nm.DeviceBuffer(L * rows * k * 4), nm.DeviceBuffer(L * rows * k * 4)
+        print(f"[trace={trace}]", flush=True)
+        assert lib.naiwa_stack_trace_enable(trace) == 0
+        try:
+            nm.stack_decode(layers, xd, rows, H, E, k, ids_out=ids_d, w_out=w_d, fused=True)
+            nm.synchronize()
+        finally:
+            lib.naiwa_stack_trace_enable(0)
+        assert nm.stack_status() == (0, 0)
+        outs.append((ids_d.download(np.uint32), w_d.download(np.uint32), xd.download(np.uint16)))
+        if trace:
+            slots = 24
+            cap = 4096 * (L + 1) * slots
+            buf = (C.c_uint64 * cap)()
+            nl, nb = C.c_int(0), C.c_int(0)
+            assert lib.naiwa_stack_trace_read(buf, cap, C.byref(nl), C.byref(nb)) == 0
+            assert nl.value == L and nb.value >= 16
+            t = np.frombuffer(buf, dtype=np.uint64)[: nb.value * (L + 1) * slots].reshape(nb.value, L + 1, slots)
+            # every workgroup: x received (0) <= ranked (1) <= routed (2) <= gate/up rows landed (3)
+            for l in range(L):
+                m = t[:, l, :4].astype(np.int64)
+                assert (m > 0).all(), l
+                assert (np.diff(m, axis=1) >= 0).all(), l
+    for o in outs[1:]:
+        for a_, b_ in zip(outs[0], o):
+            assert np.array_equal(a_, b_)
 
 
 def test_fused_status_counts_add_up_across_launches(gpu):
