@@ -165,7 +165,8 @@ def test_fused_status_counts_add_up_across_launches(gpu):
     """Pairs routed to an expert that has no slot are counted as missing (and left out of
     the output).  Each launch starts its own counts from zero and folds its predecessor's
     into the running totals, so launches in a row add up to the sum of their counts, a
-    status read returns them and clears them, and no wait times out."""
+    status read returns them and clears them, and no wait times out -- also over 1,100
+    launches in a row without a status read."""
     nm = gpu
     L, H, E, I, k, rows, gone = 2, 256, 16, 256, 4, 2, 5
     dt = (O.Q4_K,) * 3
@@ -198,6 +199,25 @@ def test_fused_status_counts_add_up_across_launches(gpu):
     assert nm.stack_status() == (0, counts[3])
     assert nm.stack_status() == (0, 0)
     assert sum(counts) > 0
+    # past the ring: the same token again and again, its count known from the first launch
+    x = S.activations_bf16(3110, rows, H)
+    xd = nm.DeviceBuffer.from_array(x)
+    ids_d, w_d = nm.DeviceBuffer(L * rows * k * 4), nm.DeviceBuffer(L * rows * k * 4)
+    n = 1100
+    print(f"[status over {n} launches]", flush=True)
+    total = 0
+    for launch in range(n):
+        xd.upload(x)
+        nm.stack_decode(layers, xd, rows, H, E, k, ids_out=ids_d, w_out=w_d, fused=True)
+        if launch % 100 == 0:
+            nm.synchronize()
+        if launch == 0:
+            nm.synchronize()
+            per = int((ids_d.download(np.uint32) == gone).sum())
+            assert per == counts[0]
+        total += per
+    nm.synchronize()
+    assert nm.stack_status() == (0, total)
 
 
 def test_fused_last_slot_of_exact_bank(gpu):
