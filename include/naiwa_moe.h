@@ -349,8 +349,8 @@ int naiwa_upload_expert(void* const dst[3], const void* const src[3], const size
 /* pinned host memory mapped for the device (naiwa_host_alloc), every dst   */
 /* in device memory; src, dst and bytes 16-byte aligned.  Sources are        */
 /* checked before the launch: NAIWA_E_UNSUPPORTED (nothing queued) when one  */
-/* is not mapped pinned memory or not aligned, and the caller copies those   */
-/* another way.  The ranges must not overlap.                                */
+/* is not mapped pinned memory or not aligned, or a range exceeds 16 GiB,   */
+/* and the caller copies those another way.  The ranges must not overlap.    */
 #define NAIWA_COPY_BATCH_MAX 64
 typedef struct naiwa_copy {
     void* dst;

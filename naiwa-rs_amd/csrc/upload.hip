@@ -14,6 +14,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kCopyThreads = 256;
 constexpr int kCopyUnroll = 4;     // 16-byte loads in flight per thread
 constexpr int kBlocksPerRange = 16; // more loads in flight measured slower over PCIe
+constexpr uint64_t kMaxRangeBytes = uint64_t(1) << 34; // 16 GiB: unit indices stay far below 2^32
 
 // The ranges travel as kernel arguments, sized to the batch: a launch's host cost grows
 // with its argument bytes (~3.1 us with a few, ~4.4 us with all 64 ranges' 1.5 KB).
@@ -30,9 +31,12 @@ __global__ void __launch_bounds__(kCopyThreads) copy_batch_kernel(CopyArgs<CAP> 
     if (r >= a.n) return;
     const u32x4* src = reinterpret_cast<const u32x4*>(a.c[r].src);
     u32x4* dst = reinterpret_cast<u32x4*>(a.c[r].dst);
-    const int64_t n16 = (int64_t)(a.c[r].bytes / 16);
-    const int64_t step = (int64_t)gridDim.x * kCopyThreads;
-    for (int64_t i0 = (int64_t)blockIdx.x * kCopyThreads + threadIdx.x; i0 < n16; i0 += step * kCopyUnroll) {
+    // 32-bit unit indices (ranges are at most kMaxRangeBytes): 26 VGPRs instead of 36, so
+    // that a wave fits on a SIMD beside three waves of the staged gate/up kernels that
+    // wait for this copy (up to 160 VGPRs each)
+    const uint32_t n16 = (uint32_t)(a.c[r].bytes / 16);
+    const uint32_t step = gridDim.x * kCopyThreads;
+    for (uint32_t i0 = blockIdx.x * kCopyThreads + threadIdx.x; i0 < n16; i0 += step * kCopyUnroll) {
         u32x4 v[kCopyUnroll];
 #pragma unroll
         for (int u = 0; u < kCopyUnroll; ++u)
@@ -90,6 +94,7 @@ int naiwa_copy_batch_mapped(const naiwa_copy* items, int n, int64_t stream) {
         if (!it.bytes) continue;
         if (!it.dst || !it.src) return NAIWA_E_INVALID;
         if (((uintptr_t)it.dst | (uintptr_t)it.src | (uintptr_t)it.bytes) & 15) return NAIWA_E_UNSUPPORTED;
+        if ((uint64_t)it.bytes > kMaxRangeBytes) return NAIWA_E_UNSUPPORTED;
         c[m++] = it;
     }
     if (!m) return NAIWA_OK;

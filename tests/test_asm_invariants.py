@@ -56,3 +56,41 @@ def test_no_instruction_reads_m0_implicitly(fused_asm):
                           r"buffer_load\S*\s.*\blds\b|ds_append|ds_consume)")
     hits = [l for l in fused_asm if implicit.match(l)]
     assert not hits, hits[:5]
+
+
+def _kernel_vgprs(src: str, tmp_path) -> dict:
+    """VGPRs of every kernel in csrc/<src>, from the code object metadata of its gfx950
+    assembly, by mangled name."""
+    b = _build_module()
+    if not os.path.exists(b.HIPCC):
+        pytest.skip("hipcc is not installed")
+    out = tmp_path / (src + ".s")
+    flags = [f for f in b.CFLAGS if f != "-fPIC"]
+    r = subprocess.run([b.HIPCC, *flags, "-I", b.CSRC, "--cuda-device-only", "-S", os.path.join(b.CSRC, src),
+                        "-o", str(out)], capture_output=True, text=True, timeout=900)
+    assert r.returncode == 0, r.stderr[-2000:]
+    text = out.read_text()
+    meta = text[text.index("amdhsa.kernels"):]
+    vgprs = {}
+    for entry in meta.split("\n  - ")[1:]:
+        name = re.search(r"\.name:\s+(\S+)", entry)
+        count = re.search(r"\.vgpr_count:\s+(\d+)", entry)
+        if name and count:
+            vgprs[name.group(1)] = int(count.group(1))
+    return vgprs
+
+
+def test_staged_gate_up_leaves_registers_for_the_copy_kernel(tmp_path):
+    """Staged gate/up blocks of small calls wait for the upload flag while the copy kernel
+    on the other stream has still to run, so however many of them a SIMD holds, the copy
+    kernel's wave must still fit beside them (512 VGPRs a SIMD lane, allocated 8 at a
+    time; the LDS can only lower the count).  A build where they filled every register
+    made every wait run out."""
+    gate_up = {n: v for n, v in _kernel_vgprs("decode.hip", tmp_path).items() if "gate_up_staged_kernel" in n}
+    copies = {n: v for n, v in _kernel_vgprs("upload.hip", tmp_path).items() if "copy_batch_kernel" in n}
+    assert gate_up and copies
+    alloc = lambda v: (v + 7) // 8 * 8
+    copy_need = max(alloc(v) for v in copies.values())
+    for name, v in gate_up.items():
+        waves = min(8, 512 // alloc(v))
+        assert waves * alloc(v) + copy_need <= 512, (name, v, waves, copy_need)
