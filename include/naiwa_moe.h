@@ -322,9 +322,11 @@ int naiwa_stack_set_blocks_per_cu(int n);
 int naiwa_stack_status(int* barrier_timeouts, int* missing_experts);
 
 /* Diagnostic phase timestamps of the fused kernel: when enabled, every block
- * records s_memrealtime ticks at each phase boundary.  naiwa_stack_trace_read
- * copies [blocks][n_layers + 1][24] ticks of the last launch (row n_layers is
- * the prologue) and synchronizes the device. */
+ * records s_memrealtime ticks at each phase boundary (at the Qwen3-30B-A3B
+ * routing sizes a separate traced instantiation runs; the untraced one has no
+ * marks compiled in).  naiwa_stack_trace_read copies
+ * [blocks][n_layers + 1][24] ticks of the last launch (row n_layers is the
+ * prologue) and synchronizes the device. */
 int naiwa_stack_trace_enable(int on);
 int naiwa_stack_trace_read(uint64_t* out, int capacity, int* n_layers, int* blocks);
 
