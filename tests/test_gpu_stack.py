@@ -93,6 +93,7 @@ def check_chain(host, x, ids, w, ys, x_final, rows, H, E, k, mode):
     (1, 4, 2048, 128, 8, 768, (O.Q4_K,) * 3, O.ROUTE_SOFTMAX_TOPK_RENORM, False),  # Qwen3 shape
     (1, 2, 2048, 64, 4, 768, (O.Q4_K,) * 3, O.ROUTE_SOFTMAX_TOPK_RENORM, True),    # any shape, Q4_K
     (8, 3, 2048, 128, 8, 768, (O.Q4_K,) * 3, O.ROUTE_SOFTMAX_TOPK_RENORM, True),   # Qwen3 shape, bs8
+    (2, 3, 2048, 128, 8, 768, (O.Q4_K,) * 3, O.ROUTE_SOFTMAX_TOPK_RENORM, True),   # Qwen3 shape, bs2
     (1, 2, 1024, 8, 2, 2048, (O.Q8_0,) * 3, O.ROUTE_TOPK_SOFTMAX, True),
     (1, 2, 2048, 64, 6, 1408, (O.Q4_K, O.Q4_K, O.Q8_0), O.ROUTE_SOFTMAX_TOPK, True),
     (1, 2, 512, 256, 8, 256, (O.Q8_0,) * 3, O.ROUTE_SOFTMAX_TOPK_RENORM, True),   # 256 experts
