@@ -55,7 +55,6 @@ constexpr int kGemm = 512;     // GEMM blocks: 8 waves, one 32-feature weight st
 constexpr int kTM = 64;        // pairs per tile: two 32-row MFMA subtiles
 constexpr int kTNG = 128;      // gate/up features per block (waves 0-3 gate, 4-7 up)
 constexpr int kTND = 256;      // down output features per block
-constexpr int NAIWA_SCRATCH_PREFILL = 5;
 
 // Two f32 values rounded to nearest-even bf16 (v_cvt_pk_bf16_f32), as one word.
 __device__ __forceinline__ uint32_t bf16x2_bits(float a, float b) {

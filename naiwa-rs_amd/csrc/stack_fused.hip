@@ -1725,7 +1725,7 @@ extern "C" int naiwa_stack_trace_read(uint64_t* out, int capacity, int* n_layers
     if (!g_trace_layers) return NAIWA_E_NOT_FOUND;
     const size_t n = (size_t)g_trace_blocks * (g_trace_layers + 1) * kTraceSlots;
     if (!out || capacity < 0 || (size_t)capacity < n) return NAIWA_E_INVALID;
-    void* t = naiwa_scratch(NAIWA_SCRATCH_STACK + 2, n * 8, &rc);
+    void* t = naiwa_scratch(NAIWA_SCRATCH_FUSED_TRACE, n * 8, &rc);
     if (!t) return rc;
     if (n_layers) *n_layers = g_trace_layers;
     if (blocks) *blocks = g_trace_blocks;
@@ -1755,7 +1755,7 @@ std::mutex g_seq_mu;
 extern "C" int naiwa_stack_status(int* barrier_timeouts, int* missing_experts) {
     int rc = 0;
     bool fresh = false;
-    uint8_t* sync = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK + 1, 4096, &rc, &fresh);
+    uint8_t* sync = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_FUSED_STATUS, 4096, &rc, &fresh);
     if (!sync) return rc;
     hipError_t e = hipDeviceSynchronize();
     if (e != hipSuccess) return (int)e;
@@ -1870,16 +1870,16 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     const size_t done_bytes = a256((size_t)blocks * 8);
     const size_t tag_bytes = h_bytes + part_bytes + lg_bytes + xt_bytes + done_bytes;
     bool fresh = false;
-    uint8_t* ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK, tag_bytes, &rc, &fresh);
+    uint8_t* ws = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_FUSED, tag_bytes, &rc, &fresh);
     if (!ws) return rc;
     bool sync_fresh = false;
-    uint8_t* sync = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK + 1, 4096, &rc, &sync_fresh);
+    uint8_t* sync = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_FUSED_STATUS, 4096, &rc, &sync_fresh);
     if (!sync) return rc;
     // per-launch outputs of a two-launch step: ids, weights [2][layers][k], y [2][layers][H]
     const size_t tok_rk = (size_t)n_layers * k, tok_y = y_out ? (size_t)n_layers * H : 0;
     uint8_t* tout = nullptr;
     if (launches == 2 && (ids_out || y_out)) {
-        tout = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_STACK + 3, 2 * (2 * tok_rk + tok_y) * 4, &rc);
+        tout = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_FUSED_TOKENS, 2 * (2 * tok_rk + tok_y) * 4, &rc);
         if (!tout) return rc;
     }
     uint32_t* const tids = (uint32_t*)tout;
@@ -1947,7 +1947,7 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
     prm.dpre = dpre;
     prm.hwb_bytes = (int)hwb;
     prm.trace = g_trace_enabled ? (unsigned long long*)naiwa_scratch(
-                                      NAIWA_SCRATCH_STACK + 2, (size_t)blocks * (n_layers + 1) * kTraceSlots * 8, &rc)
+                                      NAIWA_SCRATCH_FUSED_TRACE, (size_t)blocks * (n_layers + 1) * kTraceSlots * 8, &rc)
                                 : nullptr;
     if (g_trace_enabled && !prm.trace) return rc;
     g_trace_layers = n_layers;

@@ -24,4 +24,17 @@ void* naiwa_scratch(int tag, size_t bytes, int* rc);
 // contents are then undefined.
 void* naiwa_scratch(int tag, size_t bytes, int* rc, bool* fresh);
 
-enum { NAIWA_SCRATCH_DECODE = 0, NAIWA_SCRATCH_ROUTER = 1, NAIWA_SCRATCH_STACK = 2, NAIWA_SCRATCH_TAGS = 6 };
+// One buffer per user: a buffer shared by two entry points would let one overwrite what
+// the other keeps there between calls (the fused kernel's tagged exchange words are only
+// cleared when they are known to be dirty).
+enum {
+    NAIWA_SCRATCH_DECODE = 0,
+    NAIWA_SCRATCH_ROUTER = 1,
+    NAIWA_SCRATCH_STACK = 2,        // layered stack: per-layer routing and outputs
+    NAIWA_SCRATCH_FUSED = 3,        // fused stack: tagged exchange words
+    NAIWA_SCRATCH_FUSED_STATUS = 4, // fused stack: status counters
+    NAIWA_SCRATCH_FUSED_TRACE = 5,  // fused stack: phase timestamps
+    NAIWA_SCRATCH_FUSED_TOKENS = 6, // fused stack: per-launch outputs of two-launch steps
+    NAIWA_SCRATCH_PREFILL = 7,
+    NAIWA_SCRATCH_TAGS = 8
+};
