@@ -7,7 +7,12 @@
  * caller-owned.  `stream` is a hipStream_t passed as int64_t (0 = the null
  * stream), as in the reference's doorbell FFI.  Launches are asynchronous and
  * stream-ordered.  One thread submits GPU work per device; the upload entry
- * points may be called from one other thread.
+ * points may be called from one other thread.  The decode, prefill, router
+ * (when it keeps its logits internally) and layered-stack entry points reuse
+ * one grow-only scratch buffer per device and entry point from call to call:
+ * two such calls on different streams must be ordered by the caller (an event
+ * between them).  The fused stack orders its launches itself, whatever their
+ * streams.
  *
  * Reference interfaces each group replaces (naiwa-rs paths):
  *   doorbell_*            src/doorbell/mod.rs:31-69, src/doorbell/doorbell.cu:15-149
