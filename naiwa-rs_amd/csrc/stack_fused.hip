@@ -1882,9 +1882,9 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
         tout = (uint8_t*)naiwa_scratch(NAIWA_SCRATCH_FUSED_TOKENS, 2 * (2 * tok_rk + tok_y) * 4, &rc);
         if (!tout) return rc;
     }
-    uint32_t* const tids = (uint32_t*)tout;
-    float* const tw = (float*)tout + 2 * tok_rk;
-    float* const ty = (float*)tout + 4 * tok_rk;
+    uint32_t* const tids = tout ? (uint32_t*)tout : nullptr;
+    float* const tw = tout ? (float*)tout + 2 * tok_rk : nullptr;
+    float* const ty = tout ? (float*)tout + 4 * tok_rk : nullptr;
     // this launch's work on `st` (clearing the exchange words included) follows the previous
     // fused launch on this device, whatever its stream; the lock is held until this
     // launch's events are recorded
@@ -1964,7 +1964,11 @@ int naiwa_stack_fused(const naiwa_layer* layers, int n_layers, void* x, int rows
         }
         roll_status<<<1, 64, 0, st>>>((int*)(sync + kStatusOff));
         rc = krows == 1 ? with_kernel<1>(fg, fd, sh, tr, go) : with_kernel<kMaxRows>(fg, fd, sh, tr, go);
-        if (rc) return rc;
+        if (rc) {
+            // an earlier launch of this step is queued: later fused launches still follow it
+            if (t > 0 && hipEventRecord(fdev.done, st) == hipSuccess) fdev.have_done = true;
+            return rc;
+        }
     }
     if (tout) {
         interleave_tokens<<<dim3((unsigned)n_layers, 2), 256, 0, st>>>(tids, tw, ty, n_layers, k, H, ids_out, w_out,
