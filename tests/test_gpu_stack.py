@@ -162,6 +162,32 @@ def test_fused_trace_records_phases_and_leaves_the_bits_unchanged(gpu):
             assert np.array_equal(a_, b_)
 
 
+def test_two_token_steps_give_the_same_bits_with_and_without_outputs(gpu):
+    """Two tokens at the Qwen3 shape (two one-token launches whose outputs are
+    interleaved afterwards): the updated x, ids and weights are bit-identical whether
+    the call asks for the per-layer outputs, for ids and weights only, or for nothing."""
+    nm = gpu
+    rows, L, H, E, k, I = 2, 3, 2048, 128, 8, 768
+    layers, host, keep = build_stack(nm, L, H, E, I, (O.Q4_K,) * 3, 1010)
+    x = S.activations_bf16(1011, rows, H)
+    res = []
+    for mode in ("all", "ids", "none"):
+        xd = nm.DeviceBuffer.from_array(x)
+        ids_d, w_d = nm.DeviceBuffer(L * rows * k * 4), nm.DeviceBuffer(L * rows * k * 4)
+        y_d = nm.DeviceBuffer(L * rows * H * 4) if mode == "all" else None
+        print(f"[two tokens, outputs={mode}]", flush=True)
+        nm.stack_decode(layers, xd, rows, H, E, k, ids_out=None if mode == "none" else ids_d,
+                        w_out=None if mode == "none" else w_d, fused=True, y_out=y_d)
+        nm.synchronize()
+        assert nm.stack_status() == (0, 0)
+        res.append((xd.download(np.uint16), ids_d.download(np.uint32), w_d.download(np.uint32)))
+    assert np.array_equal(res[0][0], res[1][0]) and np.array_equal(res[0][0], res[2][0])
+    assert np.array_equal(res[0][1], res[1][1]) and np.array_equal(res[0][2], res[1][2])
+    # each token's row of the routing is its own: the two tokens route differently
+    ids = res[0][1].reshape(L, rows, k)
+    assert any(not np.array_equal(np.sort(ids[l, 0]), np.sort(ids[l, 1])) for l in range(L))
+
+
 def test_fused_status_counts_add_up_across_launches(gpu):
     """Pairs routed to an expert that has no slot are counted as missing (and left out of
     the output).  Each launch starts its own counts from zero and folds its predecessor's
