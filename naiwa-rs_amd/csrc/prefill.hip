@@ -130,7 +130,7 @@ __device__ __forceinline__ bool tile_col(int b, int ntiles, int ncol, int xcd, i
 }
 
 // Cut the sorted pairs into tiles of <= kTM pairs of one slot.  One block.
-__global__ void __launch_bounds__(kThreads) tiles_kernel(const uint32_t* offsets, int slots, Tiles t) {
+__device__ inline void tiles_block(const uint32_t* offsets, int slots, Tiles t) {
     __shared__ int part[kThreads + 1];
     const int tid = threadIdx.x;
     const int per = (slots + kThreads - 1) / kThreads;
@@ -172,9 +172,9 @@ __device__ __forceinline__ uint32_t pick16(const uint32_t (&w)[4], int e0, int e
 // x bf16 [T, H] -> xp bf16 [T, H] in the K order of DT (the values unchanged, only
 // placed).  One thread per run of 8 values.
 template <int DT>
-__global__ void __launch_bounds__(kThreads) prep_kernel(const uint16_t* x, int T, int H, uint16_t* xp) {
+__device__ inline void prep_block(const uint16_t* x, int T, int H, uint16_t* xp, int block) {
     const int runs = H / 8;
-    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t i = (int64_t)block * kThreads + threadIdx.x;
     if (i >= (int64_t)T * runs) return;
     const int t = (int)(i / runs), run = (int)(i % runs);
     const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)t * H + 8 * run);
@@ -187,6 +187,17 @@ __global__ void __launch_bounds__(kThreads) prep_kernel(const uint16_t* x, int T
     o.z = pick16(w, el(4), el(5));
     o.w = pick16(w, el(6), el(7));
     *reinterpret_cast<uint4*>(xp + (size_t)t * H + dst) = o;
+}
+
+// The placed activations (every block but the last) and the tile list (the last block)
+// in one launch: the two do not depend on each other.
+template <int DT>
+__global__ void __launch_bounds__(kThreads) prep_tiles_kernel(const uint16_t* x, int T, int H, uint16_t* xp,
+                                                              const uint32_t* offsets, int slots, Tiles t) {
+    if (blockIdx.x == gridDim.x - 1)
+        tiles_block(offsets, slots, t);
+    else
+        prep_block<DT>(x, T, H, xp, blockIdx.x);
 }
 
 // (d * scale, -dmin * min) of 32-value sub-block j of a Q4_K block whose first 16
@@ -996,12 +1007,13 @@ extern "C" int naiwa_moe_prefill(const naiwa_bank* gate, const naiwa_bank* up, c
     hipStream_t st = (hipStream_t)stream;
 
     if ((rc = naiwa_moe_gather(slot_ids, (int)n, slots, perm, offsets, (int*)(ws + o_bad), stream))) return rc;
-    tiles_kernel<<<1, kThreads, 0, st>>>(offsets, slots, tl);
     const unsigned prep_blocks = (unsigned)(((int64_t)T * (H / 8) + kThreads - 1) / kThreads);
     if (gate->dtype == NAIWA_Q4_K)
-        prep_kernel<NAIWA_Q4_K><<<prep_blocks, kThreads, 0, st>>>((const uint16_t*)x, T, H, xp);
+        prep_tiles_kernel<NAIWA_Q4_K><<<prep_blocks + 1, kThreads, 0, st>>>((const uint16_t*)x, T, H, xp, offsets,
+                                                                            slots, tl);
     else
-        prep_kernel<NAIWA_Q8_0><<<prep_blocks, kThreads, 0, st>>>((const uint16_t*)x, T, H, xp);
+        prep_tiles_kernel<NAIWA_Q8_0><<<prep_blocks + 1, kThreads, 0, st>>>((const uint16_t*)x, T, H, xp, offsets,
+                                                                            slots, tl);
     const Bank bg{(const uint8_t*)gate->base, gate->slot_stride, rbg}, bu{(const uint8_t*)up->base, up->slot_stride, rbg};
     const Bank bd{(const uint8_t*)down->base, down->slot_stride, rbd};
     const unsigned tiles8 = (unsigned)((max_tiles + 7) / 8 * 8);
